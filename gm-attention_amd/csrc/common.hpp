@@ -1,0 +1,134 @@
+// Shared device and host helpers of libgmhip.so (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+#include "gm_hip.h"
+
+namespace gm {
+
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = 4;  // 256-thread workgroups: one node per wavefront
+
+// ---- error reporting (runtime.hip) ----
+void set_error(const std::string& message);
+int fail(int code, const std::string& message);  // set_error + return code
+int check_launch(const char* what);               // hipGetLastError after a launch
+
+#define GM_REQUIRE(cond, message)                                   \
+  do {                                                              \
+    if (!(cond)) return ::gm::fail(GM_ERR_ARGUMENT, (message));     \
+  } while (0)
+
+// ---- device helpers ----
+
+template <typename T>
+__device__ __forceinline__ T neg_inf() {
+  return -static_cast<T>(INFINITY);
+}
+
+// Blocks are dispatched round-robin over the eight XCDs, each with its own L2.
+// Remap so XCD x runs a contiguous range of logical blocks: neighbouring nodes
+// (which share most of their neighbours' rows) then share one L2.
+__device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
+  const int64_t q = nb >> 3, r = nb & 7, x = b & 7;
+  return x * q + (x < r ? x : r) + (b >> 3);
+}
+
+// Four consecutive elements (16 B for float, 32 B for double), aligned.
+template <typename T>
+struct Quad {
+  T v[4];
+};
+
+__device__ __forceinline__ Quad<float> ld4(const float* p) {
+  const float4 x = *reinterpret_cast<const float4*>(p);
+  return {{x.x, x.y, x.z, x.w}};
+}
+__device__ __forceinline__ Quad<double> ld4(const double* p) {
+  const double2 x = reinterpret_cast<const double2*>(p)[0];
+  const double2 y = reinterpret_cast<const double2*>(p)[1];
+  return {{x.x, x.y, y.x, y.y}};
+}
+__device__ __forceinline__ void st4(float* p, const float* v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st4(double* p, const double* v) {
+  reinterpret_cast<double2*>(p)[0] = make_double2(v[0], v[1]);
+  reinterpret_cast<double2*>(p)[1] = make_double2(v[2], v[3]);
+}
+
+__device__ __forceinline__ float gm_exp(float x) { return expf(x); }
+__device__ __forceinline__ double gm_exp(double x) { return exp(x); }
+
+// Sum over the lanes of one group g = lane % G (G a power of two dividing 64):
+// a butterfly over the lane bits above log2(G); every lane gets its group's total.
+template <typename T>
+__device__ __forceinline__ T group_sum_pow2(T v, int G) {
+  for (int off = G; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Sum over lanes h, h + G, ..., h + (S - 1) G for any G (S = 64 / G, floor):
+// a tree into slot 0, then broadcast from lane h.  Lanes at or past S * G
+// contribute nothing and receive their group's total all the same.
+template <typename T>
+__device__ __forceinline__ T group_sum(T v, int lane, int G, int S) {
+  const int s = lane / G, h = lane % G;
+  if (s >= S) v = T(0);
+  for (int step = 1; step < S; step <<= 1) {
+    const int from = lane + step * G;
+    const T o = __shfl(v, from < kWave ? from : lane, kWave);
+    if ((s % (2 * step)) == 0 && s + step < S) v += o;
+  }
+  return __shfl(v, h, kWave);
+}
+
+// Online softmax state (running maximum m and sum l of exp(x - m)).
+template <typename T>
+__device__ __forceinline__ void online_add(T& m, T& l, T x) {
+  if (x == neg_inf<T>()) return;
+  if (x > m) {
+    l = (m == neg_inf<T>() ? T(0) : l * gm_exp(m - x)) + T(1);
+    m = x;
+  } else {
+    l += gm_exp(x - m);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void online_merge(T& m, T& l, T mo, T lo) {
+  const T mn = m > mo ? m : mo;
+  if (mn == neg_inf<T>()) return;
+  const T a = (m == neg_inf<T>()) ? T(0) : l * gm_exp(m - mn);
+  const T b = (mo == neg_inf<T>()) ? T(0) : lo * gm_exp(mo - mn);
+  m = mn;
+  l = a + b;
+}
+
+// Merge the online states of lanes h, h + G, ... (any G, S = 64 / G).
+template <typename T>
+__device__ __forceinline__ void group_online(T& m, T& l, int lane, int G, int S) {
+  const int s = lane / G, h = lane % G;
+  if (s >= S) {
+    m = neg_inf<T>();
+    l = T(0);
+  }
+  for (int step = 1; step < S; step <<= 1) {
+    const int from = lane + step * G;
+    const T mo = __shfl(m, from < kWave ? from : lane, kWave);
+    const T lo = __shfl(l, from < kWave ? from : lane, kWave);
+    if ((s % (2 * step)) == 0 && s + step < S) online_merge(m, l, mo, lo);
+  }
+  m = __shfl(m, h, kWave);
+  l = __shfl(l, h, kWave);
+}
+
+inline bool aligned(const void* p, size_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+inline int64_t blocks_for(int64_t items) { return (items + kWavesPerBlock - 1) / kWavesPerBlock; }
+
+}  // namespace gm

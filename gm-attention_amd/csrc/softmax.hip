@@ -1,0 +1,516 @@
+// Scores and neighbourhood softmax over CSR neighbour lists, forward and
+// backward, for CDNA4 (gfx950).
+//
+// Per edge e = (i <- j) and head h:
+//   s[e,h]  = scale * sum_n Re< q_i,n,h , tau_n(e) k_j,n,h > + bias[e]
+//   alpha   = softmax of s over i's edges with inside[e] != 0 (others 0)
+// and, from d alpha, ds = scale * alpha * (d alpha - sum_e alpha d alpha),
+// dq_i = sum_e ds tau k_j, dk_j = sum_{e: source j} ds conj(tau) q_i.
+// (The math contract of the reference's fused/attention.h:4-39, 145-165,
+// 236-247, 295-348.)
+//
+// Mapping: one wavefront per target node; its 64 lanes are (edge slot s,
+// head h) with S = 64 / H slots, so a lane scores its head on every S-th edge
+// of the neighbourhood, holding its head's query columns in registers, and
+// the 8 lanes of one edge read that edge's key row as contiguous 16-byte
+// pieces.  The softmax is online per lane (running max and sum) and merged
+// across the slots of a head with lane shuffles; the raw scores park in alpha
+// and are normalised by a second walk over the same lines (L2 hits).
+// The backward is two passes: per target (the adjoint's per-head total, ds,
+// and dq) and per source over the edges grouped by source (dk), so no atomics
+// are used and the result is deterministic.
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "layout.hpp"
+
+namespace gm {
+namespace {
+
+template <typename T>
+struct SmArgs {
+  const T* q;
+  const T* k;
+  const T* transport;  // (n_edges, orders, 2)
+  const T* bias;
+  const uint8_t* inside;
+  const int64_t* row_ptr;
+  const int64_t* source;
+  const T* alpha_in;  // backward: the forward's alpha
+  const T* dalpha;
+  T* alpha;
+  T* ds;  // (n_edges, H) workspace
+  T* dq;
+  T* dk;
+  const int64_t* src_ptr;
+  const int64_t* src_order;
+  const int64_t* target;
+  int64_t n_nodes;
+  int D, orders, H, S, hshift;  // hshift = log2(H) on the fast path
+  T scale;
+  AttnLayout L;
+  Chunks C;
+};
+
+// ---------------------------------------------------------------- fast path
+// Every head segment is whole chunks of four reals; H in {1, 2, 4, 8}.
+
+template <typename T>
+__device__ __forceinline__ T chunk_dot(const T* q4, const Quad<T>& k, int n, const T* tr) {
+  if (n == 0) return q4[0] * k.v[0] + q4[1] * k.v[1] + q4[2] * k.v[2] + q4[3] * k.v[3];
+  const T c = tr[2 * n], s = tr[2 * n + 1];
+  // tau k = (c k0 - s k1, c k1 + s k0) per pair, dotted with q's pair.
+  T acc = q4[0] * (c * k.v[0] - s * k.v[1]) + q4[1] * (c * k.v[1] + s * k.v[0]);
+  acc += q4[2] * (c * k.v[2] - s * k.v[3]) + q4[3] * (c * k.v[3] + s * k.v[2]);
+  return acc;
+}
+
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int lane = threadIdx.x & 63;
+  const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
+  if (i >= a.n_nodes) return;
+  const int H = a.H, S = a.S;
+  const int h = lane & (H - 1), s = lane >> a.hshift;
+  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+
+  T q[NCH * 4];
+  const T* qi = a.q + i * a.D;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const Quad<T> x = ld4(qi + a.C.base[c] + h * a.C.stride[c]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[4 * c + u] = x.v[u];
+  }
+
+  T m = neg_inf<T>(), l = T(0);
+  for (int64_t e = e0 + s; e < e1; e += S) {
+    const int64_t j = a.source[e];
+    const T* kj = a.k + j * a.D;
+    const T* tr = a.transport + e * a.orders * 2;
+    T acc = T(0);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) acc += chunk_dot(&q[4 * c], ld4(kj + a.C.base[c] + h * a.C.stride[c]), a.C.order[c], tr);
+    T lw = a.scale * acc + a.bias[e];
+    if (!a.inside[e]) lw = neg_inf<T>();  // outside the window: excluded from the max and the sum
+    a.alpha[e * H + h] = lw;
+    online_add(m, l, lw);
+  }
+  for (int off = H; off < kWave; off <<= 1) {
+    const T mo = __shfl_xor(m, off, kWave), lo = __shfl_xor(l, off, kWave);
+    online_merge(m, l, mo, lo);
+  }
+  for (int64_t e = e0 + s; e < e1; e += S) {
+    const T lw = a.alpha[e * H + h];
+    a.alpha[e * H + h] = gm_exp(lw - m) / l;  // an excluded edge is exp(-inf) = 0
+  }
+}
+
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a) {
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int lane = threadIdx.x & 63;
+  const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
+  if (i >= a.n_nodes) return;
+  const int H = a.H, S = a.S;
+  const int h = lane & (H - 1), s = lane >> a.hshift;
+  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+
+  T total = T(0);
+  for (int64_t e = e0 + s; e < e1; e += S) total += a.alpha_in[e * H + h] * a.dalpha[e * H + h];
+  total = group_sum_pow2(total, H);
+
+  T acc[NCH * 4];
+#pragma unroll
+  for (int u = 0; u < NCH * 4; ++u) acc[u] = T(0);
+  for (int64_t e = e0 + s; e < e1; e += S) {
+    const T ds = a.scale * a.alpha_in[e * H + h] * (a.dalpha[e * H + h] - total);
+    a.ds[e * H + h] = ds;
+    const int64_t j = a.source[e];
+    const T* kj = a.k + j * a.D;
+    const T* tr = a.transport + e * a.orders * 2;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const Quad<T> k = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
+      const int n = a.C.order[c];
+      if (n == 0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[4 * c + u] += ds * k.v[u];
+      } else {
+        const T cr = tr[2 * n], ci = tr[2 * n + 1];
+        acc[4 * c + 0] += ds * (cr * k.v[0] - ci * k.v[1]);
+        acc[4 * c + 1] += ds * (cr * k.v[1] + ci * k.v[0]);
+        acc[4 * c + 2] += ds * (cr * k.v[2] - ci * k.v[3]);
+        acc[4 * c + 3] += ds * (cr * k.v[3] + ci * k.v[2]);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NCH * 4; ++u) acc[u] = group_sum_pow2(acc[u], H);
+  if (s == 0) {
+    T* dqi = a.dq + i * a.D;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) st4(dqi + a.C.base[c] + h * a.C.stride[c], &acc[4 * c]);
+  }
+}
+
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a) {
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int lane = threadIdx.x & 63;
+  const int64_t j = blk * kWavesPerBlock + (threadIdx.x >> 6);
+  if (j >= a.n_nodes) return;
+  const int H = a.H, S = a.S;
+  const int h = lane & (H - 1), s = lane >> a.hshift;
+  const int64_t g0 = a.src_ptr[j], g1 = a.src_ptr[j + 1];
+
+  T acc[NCH * 4];
+#pragma unroll
+  for (int u = 0; u < NCH * 4; ++u) acc[u] = T(0);
+  for (int64_t g = g0 + s; g < g1; g += S) {
+    const int64_t e = a.src_order[g];
+    const int64_t t = a.target[e];
+    const T ds = a.ds[e * H + h];
+    const T* qt = a.q + t * a.D;
+    const T* tr = a.transport + e * a.orders * 2;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const Quad<T> qq = ld4(qt + a.C.base[c] + h * a.C.stride[c]);
+      const int n = a.C.order[c];
+      if (n == 0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[4 * c + u] += ds * qq.v[u];
+      } else {
+        const T cr = tr[2 * n], ci = tr[2 * n + 1];
+        // conj(tau) q = (c q0 + s q1, c q1 - s q0)
+        acc[4 * c + 0] += ds * (cr * qq.v[0] + ci * qq.v[1]);
+        acc[4 * c + 1] += ds * (cr * qq.v[1] - ci * qq.v[0]);
+        acc[4 * c + 2] += ds * (cr * qq.v[2] + ci * qq.v[3]);
+        acc[4 * c + 3] += ds * (cr * qq.v[3] - ci * qq.v[2]);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NCH * 4; ++u) acc[u] = group_sum_pow2(acc[u], H);
+  if (s == 0) {
+    T* dkj = a.dk + j * a.D;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) st4(dkj + a.C.base[c] + h * a.C.stride[c], &acc[4 * c]);
+  }
+}
+
+// ------------------------------------------------------------- generic path
+// Any descriptor within the bounds: lanes (slot, head) for the scores, lanes
+// over flat columns with a serial edge walk for dq and dk.
+
+template <typename T>
+__device__ T generic_score(const SmArgs<T>& a, const T* qi, const T* kj, const T* tr, int h) {
+  T acc = T(0);
+  for (int f = 0; f < a.L.F; ++f) {
+    const int n = a.L.n[f], an = a.L.a[f], off = a.L.off[f];
+    if (n == 0) {
+      const int base = off + h * an;
+      for (int u = 0; u < an; ++u) acc += qi[base + u] * kj[base + u];
+    } else {
+      const T c = tr[2 * n], s = tr[2 * n + 1];
+      const int base = off + 2 * h * an;
+      for (int u = 0; u < an; ++u) {
+        const T k0 = kj[base + 2 * u], k1 = kj[base + 2 * u + 1];
+        acc += qi[base + 2 * u] * (c * k0 - s * k1) + qi[base + 2 * u + 1] * (c * k1 + s * k0);
+      }
+    }
+  }
+  return acc;
+}
+
+// Where flat column c sits: its frequency, head and pair part (-1 when no row holds it).
+struct Col {
+  int n, h, part, pair;  // pair: the column of the pair's real part
+};
+
+template <typename T>
+__device__ Col locate(const SmArgs<T>& a, int c) {
+  for (int f = 0; f < a.L.F; ++f) {
+    const int dim = a.L.dim[f], width = a.H * a.L.a[f] * dim, off = a.L.off[f];
+    if (c >= off && c < off + width) {
+      const int local = c - off, copy = local / dim;
+      return {a.L.n[f], copy / a.L.a[f], local % dim, c - local % dim};
+    }
+  }
+  return {0, -1, 0, c};
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_forward_generic(SmArgs<T> a) {
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int lane = threadIdx.x & 63;
+  const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
+  if (i >= a.n_nodes) return;
+  const int H = a.H, S = a.S;
+  const int h = lane % H, s = lane / H;
+  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+  const T* qi = a.q + i * a.D;
+  T m = neg_inf<T>(), l = T(0);
+  if (s < S) {
+    for (int64_t e = e0 + s; e < e1; e += S) {
+      const T* tr = a.transport + e * a.orders * 2;
+      T lw = a.scale * generic_score(a, qi, a.k + a.source[e] * a.D, tr, h) + a.bias[e];
+      if (!a.inside[e]) lw = neg_inf<T>();
+      a.alpha[e * H + h] = lw;
+      online_add(m, l, lw);
+    }
+  }
+  group_online(m, l, lane, H, S);
+  if (s < S) {
+    for (int64_t e = e0 + s; e < e1; e += S) a.alpha[e * H + h] = gm_exp(a.alpha[e * H + h] - m) / l;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_backward_target_generic(SmArgs<T> a) {
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int lane = threadIdx.x & 63;
+  const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
+  if (i >= a.n_nodes) return;
+  const int H = a.H, S = a.S;
+  const int h = lane % H, s = lane / H;
+  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+  T total = T(0);
+  if (s < S)
+    for (int64_t e = e0 + s; e < e1; e += S) total += a.alpha_in[e * H + h] * a.dalpha[e * H + h];
+  total = group_sum(total, lane, H, S);
+  T totals[GM_ATTN_MAX_H];
+#pragma unroll
+  for (int hh = 0; hh < GM_ATTN_MAX_H; ++hh) totals[hh] = __shfl(total, hh < H ? hh : 0, kWave);
+  if (s < S)
+    for (int64_t e = e0 + s; e < e1; e += S)
+      a.ds[e * H + h] = a.scale * a.alpha_in[e * H + h] * (a.dalpha[e * H + h] - total);
+  const T* qi = a.q + i * a.D;
+  (void)qi;
+  for (int c = lane; c < a.D; c += kWave) {
+    const Col col = locate(a, c);
+    T acc = T(0);
+    if (col.h >= 0) {
+      const T tot = totals[col.h];
+      for (int64_t e = e0; e < e1; ++e) {
+        const T ds = a.scale * a.alpha_in[e * H + col.h] * (a.dalpha[e * H + col.h] - tot);
+        const T* kj = a.k + a.source[e] * a.D;
+        if (col.n == 0) {
+          acc += ds * kj[c];
+        } else {
+          const T* tr = a.transport + e * a.orders * 2;
+          const T cr = tr[2 * col.n], ci = tr[2 * col.n + 1];
+          const T k0 = kj[col.pair], k1 = kj[col.pair + 1];
+          acc += ds * (col.part == 0 ? cr * k0 - ci * k1 : cr * k1 + ci * k0);
+        }
+      }
+    }
+    a.dq[i * a.D + c] = acc;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_backward_source_generic(SmArgs<T> a) {
+  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int lane = threadIdx.x & 63;
+  const int64_t j = blk * kWavesPerBlock + (threadIdx.x >> 6);
+  if (j >= a.n_nodes) return;
+  const int H = a.H;
+  const int64_t g0 = a.src_ptr[j], g1 = a.src_ptr[j + 1];
+  for (int c = lane; c < a.D; c += kWave) {
+    const Col col = locate(a, c);
+    T acc = T(0);
+    if (col.h >= 0) {
+      for (int64_t g = g0; g < g1; ++g) {
+        const int64_t e = a.src_order[g];
+        const T ds = a.ds[e * H + col.h];
+        const T* qt = a.q + a.target[e] * a.D;
+        if (col.n == 0) {
+          acc += ds * qt[c];
+        } else {
+          const T* tr = a.transport + e * a.orders * 2;
+          const T cr = tr[2 * col.n], ci = tr[2 * col.n + 1];
+          const T q0 = qt[col.pair], q1 = qt[col.pair + 1];
+          acc += ds * (col.part == 0 ? cr * q0 + ci * q1 : cr * q1 - ci * q0);
+        }
+      }
+    }
+    a.dk[j * a.D + c] = acc;
+  }
+}
+
+// ------------------------------------------------------------------ launch
+
+#define GM_FAST_CASES(X) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15) X(16)
+
+enum class Kind { Forward, BackwardTarget, BackwardSource };
+
+template <typename T, int NCH>
+void launch_fast_n(Kind kind, const SmArgs<T>& a, dim3 grid, hipStream_t stream) {
+  switch (kind) {
+    case Kind::Forward:
+      hipLaunchKernelGGL((softmax_forward_fast<T, NCH>), grid, dim3(256), 0, stream, a);
+      break;
+    case Kind::BackwardTarget:
+      hipLaunchKernelGGL((softmax_backward_target_fast<T, NCH>), grid, dim3(256), 0, stream, a);
+      break;
+    case Kind::BackwardSource:
+      hipLaunchKernelGGL((softmax_backward_source_fast<T, NCH>), grid, dim3(256), 0, stream, a);
+      break;
+  }
+}
+
+template <typename T>
+void launch(Kind kind, bool fast, const SmArgs<T>& a, hipStream_t stream) {
+  const dim3 grid((unsigned)blocks_for(a.n_nodes));
+  if (fast) {
+    switch (a.C.count) {
+#define GM_CASE(n) \
+  case n:          \
+    launch_fast_n<T, n>(kind, a, grid, stream); \
+    return;
+      GM_FAST_CASES(GM_CASE)
+#undef GM_CASE
+      default:
+        break;
+    }
+  }
+  switch (kind) {
+    case Kind::Forward:
+      hipLaunchKernelGGL(softmax_forward_generic<T>, grid, dim3(256), 0, stream, a);
+      break;
+    case Kind::BackwardTarget:
+      hipLaunchKernelGGL(softmax_backward_target_generic<T>, grid, dim3(256), 0, stream, a);
+      break;
+    case Kind::BackwardSource:
+      hipLaunchKernelGGL(softmax_backward_source_generic<T>, grid, dim3(256), 0, stream, a);
+      break;
+  }
+}
+
+template <typename T>
+int prepare(SmArgs<T>& a, bool& fast, const T* q, const T* k, const T* transport, const T* bias,
+            const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr, const int64_t* source,
+            int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H, double scale) {
+  GM_REQUIRE(n_nodes >= 0 && n_edges >= 0, "sizes must be non-negative");
+  GM_REQUIRE(n_nodes < (int64_t(1) << 31) * kWavesPerBlock, "too many nodes for one launch");
+  a = SmArgs<T>{};
+  const int rc = parse_attention_layout(desc, F, H, D, orders, a.L);
+  if (rc != GM_OK) return rc;
+  if (n_nodes > 0) GM_REQUIRE(q && k && row_ptr, "q, k and row_ptr must be device pointers");
+  if (n_edges > 0) GM_REQUIRE(transport && bias && inside && source, "the per-edge tables must be device pointers");
+  a.q = q;
+  a.k = k;
+  a.transport = transport;
+  a.bias = bias;
+  a.inside = inside;
+  a.row_ptr = row_ptr;
+  a.source = source;
+  a.n_nodes = n_nodes;
+  a.D = (int)D;
+  a.orders = (int)orders;
+  a.H = (int)H;
+  a.S = gm::kWave / (int)H;
+  a.scale = (T)scale;
+  const bool pow2 = (H == 1 || H == 2 || H == 4 || H == 8);
+  a.hshift = H == 1 ? 0 : H == 2 ? 1 : H == 4 ? 2 : 3;
+  fast = pow2 && make_chunks(a.L, a.C) && aligned(q, 4 * sizeof(T)) && aligned(k, 4 * sizeof(T));
+  return GM_OK;
+}
+
+template <typename T>
+int softmax_forward(const T* q, const T* k, const T* transport, const T* bias, const uint8_t* inside,
+                    const int64_t* desc, const int64_t* row_ptr, const int64_t* source, int64_t n_nodes,
+                    int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H, double scale, T* alpha,
+                    hipStream_t stream) {
+  SmArgs<T> a;
+  bool fast = false;
+  const int rc = prepare(a, fast, q, k, transport, bias, inside, desc, row_ptr, source, n_nodes, n_edges, D, orders,
+                         F, H, scale);
+  if (rc != GM_OK) return rc;
+  if (n_nodes == 0 || n_edges == 0) return GM_OK;
+  GM_REQUIRE(alpha, "alpha must be a device pointer");
+  a.alpha = alpha;
+  launch(Kind::Forward, fast, a, stream);
+  return check_launch("softmax_forward");
+}
+
+template <typename T>
+int softmax_backward(const T* dalpha, const T* q, const T* k, const T* transport, const T* bias, const uint8_t* inside,
+                     const int64_t* desc, const int64_t* row_ptr, const int64_t* source, const T* alpha,
+                     int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H, double scale,
+                     const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, T* ds, T* dq, T* dk,
+                     hipStream_t stream) {
+  SmArgs<T> a;
+  bool fast = false;
+  const int rc = prepare(a, fast, q, k, transport, bias, inside, desc, row_ptr, source, n_nodes, n_edges, D, orders,
+                         F, H, scale);
+  if (rc != GM_OK) return rc;
+  if (n_nodes == 0) return GM_OK;
+  GM_REQUIRE(dq && dk && src_ptr, "dq, dk and src_ptr must be device pointers");
+  if (n_edges > 0) GM_REQUIRE(dalpha && alpha && src_order && target && ds, "dalpha, alpha, src_order, target and ds must be device pointers");
+  fast = fast && aligned(dq, 4 * sizeof(T)) && aligned(dk, 4 * sizeof(T));
+  a.alpha_in = alpha;
+  a.dalpha = dalpha;
+  a.ds = ds;
+  a.dq = dq;
+  a.dk = dk;
+  a.src_ptr = src_ptr;
+  a.src_order = src_order;
+  a.target = target;
+  launch(Kind::BackwardTarget, fast, a, stream);
+  int status = check_launch("softmax_backward (per target)");
+  if (status != GM_OK) return status;
+  launch(Kind::BackwardSource, fast, a, stream);
+  return check_launch("softmax_backward (per source)");
+}
+
+}  // namespace
+}  // namespace gm
+
+extern "C" int gm_softmax_forward_f32(const float* q, const float* k, const float* transport, const float* bias,
+                                      const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr,
+                                      const int64_t* source, int64_t n_nodes, int64_t n_edges, int64_t D,
+                                      int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
+                                      float* alpha, void* stream) {
+  (void)deg_max;
+  return gm::softmax_forward<float>(q, k, transport, bias, inside, desc, row_ptr, source, n_nodes, n_edges, D, orders,
+                                    F, H, scale, alpha, (hipStream_t)stream);
+}
+
+extern "C" int gm_softmax_forward_f64(const double* q, const double* k, const double* transport, const double* bias,
+                                      const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr,
+                                      const int64_t* source, int64_t n_nodes, int64_t n_edges, int64_t D,
+                                      int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
+                                      double* alpha, void* stream) {
+  (void)deg_max;
+  return gm::softmax_forward<double>(q, k, transport, bias, inside, desc, row_ptr, source, n_nodes, n_edges, D,
+                                     orders, F, H, scale, alpha, (hipStream_t)stream);
+}
+
+extern "C" int gm_softmax_backward_f32(const float* dalpha, const float* q, const float* k, const float* transport,
+                                       const float* bias, const uint8_t* inside, const int64_t* desc,
+                                       const int64_t* row_ptr, const int64_t* source, const float* alpha,
+                                       int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F,
+                                       int64_t H, double scale, int64_t deg_max, const int64_t* src_ptr,
+                                       const int64_t* src_order, const int64_t* target, float* ds, float* dq,
+                                       float* dk, void* stream) {
+  (void)deg_max;
+  return gm::softmax_backward<float>(dalpha, q, k, transport, bias, inside, desc, row_ptr, source, alpha, n_nodes,
+                                     n_edges, D, orders, F, H, scale, src_ptr, src_order, target, ds, dq, dk,
+                                     (hipStream_t)stream);
+}
+
+extern "C" int gm_softmax_backward_f64(const double* dalpha, const double* q, const double* k,
+                                       const double* transport, const double* bias, const uint8_t* inside,
+                                       const int64_t* desc, const int64_t* row_ptr, const int64_t* source,
+                                       const double* alpha, int64_t n_nodes, int64_t n_edges, int64_t D,
+                                       int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
+                                       const int64_t* src_ptr, const int64_t* src_order, const int64_t* target,
+                                       double* ds, double* dq, double* dk, void* stream) {
+  (void)deg_max;
+  return gm::softmax_backward<double>(dalpha, q, k, transport, bias, inside, desc, row_ptr, source, alpha, n_nodes,
+                                      n_edges, D, orders, F, H, scale, src_ptr, src_order, target, ds, dq, dk,
+                                      (hipStream_t)stream);
+}

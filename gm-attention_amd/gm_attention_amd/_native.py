@@ -1,0 +1,286 @@
+"""The HIP library behind the fused ops: loading, signatures, and the
+extension objects whose entry points carry the reference's names and
+argument orders.
+
+``attention()`` stands where the reference's ``gm_fused_attention`` pybind
+module stands (``nn/fused/attention_cpu.cpp:256-261``): ``softmax_forward``,
+``softmax_backward``, ``conv_forward``, ``conv_backward``.  Tensors are
+checked with the reference's messages (``attention_cpu.cpp:42-64, 149-171``),
+outputs are allocated here through torch's caching allocator, and the raw
+pointers go to ``libgmhip.so`` on the current HIP stream.  There is no CPU
+driver: a CPU tensor is an error, and a missing library is an error, never a
+silent fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import weakref
+from pathlib import Path
+from typing import Any
+
+import torch
+from torch import Tensor
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libgmhip.so"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int64
+_D = ctypes.c_double
+
+#: C signatures, in include/gm_hip.h order (the return type is int everywhere).
+SIGNATURES: dict[str, list[Any]] = {
+    "gm_softmax_forward": [_P] * 8 + [_I] * 6 + [_D, _I, _P, _P],
+    "gm_softmax_backward": [_P] * 10 + [_I] * 6 + [_D, _I] + [_P] * 7,
+    "gm_conv_forward": [_P] * 10 + [_I] * 7 + [_P, _P],
+    "gm_conv_backward": [_P] * 11 + [_I] * 7 + [_P] * 7,
+}
+
+
+class NativeLibraryError(RuntimeError):
+    """libgmhip.so is missing or cannot be loaded."""
+
+
+@functools.cache
+def library() -> ctypes.CDLL:
+    """Load libgmhip.so (after torch, so it binds to torch's HIP runtime)."""
+    if not LIB_PATH.exists():
+        raise NativeLibraryError(
+            f"{LIB_PATH} is not built: run `python gm-attention_amd/build.py` (hipcc --offload-arch=gfx950)"
+        )
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH))
+    except OSError as error:
+        raise NativeLibraryError(f"cannot load {LIB_PATH}: {error}") from error
+    lib.gm_last_error.restype = ctypes.c_char_p
+    lib.gm_last_error.argtypes = []
+    lib.gm_abi_version.restype = ctypes.c_int
+    for stem, args in SIGNATURES.items():
+        for suffix in ("_f32", "_f64"):
+            fn = getattr(lib, stem + suffix)
+            fn.restype = ctypes.c_int
+            fn.argtypes = args
+    return lib
+
+
+def _call(name: str, *args: Any) -> None:
+    status = getattr(library(), name)(*args)
+    if status != 0:
+        message = library().gm_last_error().decode()
+        raise RuntimeError(f"{name}: {message}")
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _suffix(dtype: torch.dtype) -> str:
+    if dtype == torch.float32:
+        return "_f32"
+    if dtype == torch.float64:
+        return "_f64"
+    raise RuntimeError(f"libgmhip supports float32 and float64, got {dtype}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError(message)
+
+
+def _require_device(*tensors: Tensor) -> None:
+    first = tensors[0]
+    if first.device.type != "cuda":
+        raise RuntimeError(
+            "libgmhip runs on the GPU only: the tensors are on the CPU (this build has no CPU driver)"
+        )
+    for t in tensors:
+        _check(t.is_contiguous(), "every tensor must be contiguous")
+        _check(t.device == first.device, "every tensor must live on the same device")
+
+
+_HOST_DESC: dict[tuple, tuple[Any, Tensor]] = {}
+
+
+def host_desc(desc: Tensor) -> Tensor:
+    """A CPU int64 copy of a descriptor table, cached per device tensor (its
+    identity and version), so a layer's descriptor is copied to the host once."""
+    if desc.device.type == "cpu":
+        return desc.contiguous()
+    key = (id(desc), desc.data_ptr(), desc._version)
+    held = _HOST_DESC.get(key)
+    if held is not None and held[0]() is desc:
+        return held[1]
+    copy = desc.detach().to("cpu").contiguous()
+    for stale in [k for k, (ref, _) in _HOST_DESC.items() if ref() is None]:
+        del _HOST_DESC[stale]
+    _HOST_DESC[key] = (weakref.ref(desc), copy)
+    return copy
+
+
+# ---------------------------------------------------------------- source groups
+
+_GROUPS: dict[tuple, tuple[Any, tuple[Tensor, Tensor, Tensor]]] = {}
+
+
+def source_major(source: Tensor, row_ptr: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """``(src_ptr, src_order, target)``: every node's run of edges in the
+    edges sorted (stably) by source, and each edge's target.  The transposed
+    CSR the backward passes walk instead of adding atomically; built on the
+    device once per edge set and cached against the ``source`` tensor."""
+    n_nodes = row_ptr.shape[0] - 1
+    key = (id(source), source.data_ptr(), source.numel(), source._version, row_ptr.data_ptr(), n_nodes)
+    held = _GROUPS.get(key)
+    if held is not None and held[0]() is source:
+        return held[1]
+    device = source.device
+    if source.numel() == 0:
+        result = (torch.zeros(n_nodes + 1, dtype=torch.int64, device=device),
+                  torch.zeros(0, dtype=torch.int64, device=device), torch.zeros(0, dtype=torch.int64, device=device))
+    else:
+        order = torch.argsort(source, stable=True)
+        counts = torch.bincount(source, minlength=n_nodes)
+        src_ptr = torch.zeros(n_nodes + 1, dtype=torch.int64, device=device)
+        torch.cumsum(counts, dim=0, out=src_ptr[1:])
+        degrees = row_ptr[1:] - row_ptr[:-1]
+        target = torch.repeat_interleave(torch.arange(n_nodes, device=device), degrees)
+        result = (src_ptr.contiguous(), order.contiguous(), target.contiguous())
+    for stale in [k for k, (ref, _) in _GROUPS.items() if ref() is None]:
+        del _GROUPS[stale]
+    _GROUPS[key] = (weakref.ref(source), result)
+    return result
+
+
+# ---------------------------------------------------------------- attention
+
+
+class AttentionExtension:
+    """The reference's ``gm_fused_attention`` module surface on libgmhip."""
+
+    with_cuda = True  # the device path exists (HIP on ROCm); the attribute name is the reference's
+
+    # ---- scores and softmax (attention_cpu.cpp:149-252) ----
+
+    @staticmethod
+    def _check_softmax(q: Tensor, k: Tensor, transport: Tensor, bias: Tensor, inside: Tensor, desc: Tensor,
+                       row_ptr: Tensor, source: Tensor, H: int) -> None:
+        _check(q.dim() == 2, "q must be (n_nodes, D)")
+        _require_device(q, k, transport, bias, inside, row_ptr, source)
+        _check(desc.is_contiguous(), "every tensor must be contiguous")
+        n, e = q.shape[0], source.shape[0]
+        for t in (k, transport, bias):
+            _check(t.dtype == q.dtype, "q, k and the tables must share a dtype")
+        _check(k.shape == q.shape, "q and k must share a shape")
+        _check(1 <= H <= 8, "at most 8 heads")
+        _check(transport.dim() == 3 and transport.shape[0] == e and transport.shape[2] == 2,
+               "transport must be (n_edges, orders, 2)")
+        _check(bias.dim() == 1 and bias.shape[0] == e, "bias must be (n_edges,)")
+        _check(inside.dtype == torch.uint8 and inside.shape == bias.shape, "inside must be uint8 (n_edges,)")
+        _check(desc.dtype == torch.int64 and desc.dim() == 2 and desc.shape[1] == 5 and desc.shape[0] <= 8,
+               "desc must be int64 (F <= 8, 5)")
+        _check(row_ptr.dtype == torch.int64 and row_ptr.dim() == 1 and row_ptr.shape[0] == n + 1,
+               "row_ptr must be int64 (n_nodes + 1,)")
+        _check(source.dtype == torch.int64 and source.dim() == 1, "source must be int64 (n_edges,)")
+        _check(q.shape[1] >= 1, "D must be positive")
+
+    def softmax_forward(self, q: Tensor, k: Tensor, transport: Tensor, bias: Tensor, inside: Tensor, desc: Tensor,
+                        row_ptr: Tensor, source: Tensor, H: int, scale: float, deg_max: int) -> Tensor:
+        """alpha (n_edges, H): the heads' neighbourhood softmax of the transported scores."""
+        self._check_softmax(q, k, transport, bias, inside, desc, row_ptr, source, H)
+        alpha = torch.empty(source.shape[0], H, dtype=q.dtype, device=q.device)
+        if q.shape[0] == 0:
+            return alpha
+        hd = host_desc(desc)
+        _call("gm_softmax_forward" + _suffix(q.dtype), _ptr(q), _ptr(k), _ptr(transport), _ptr(bias), _ptr(inside),
+              hd.data_ptr(), _ptr(row_ptr), _ptr(source), q.shape[0], source.shape[0], q.shape[1], transport.shape[1],
+              hd.shape[0], H, float(scale), int(deg_max), _ptr(alpha), _stream(q.device))
+        return alpha
+
+    def softmax_backward(self, dalpha: Tensor, q: Tensor, k: Tensor, transport: Tensor, bias: Tensor, inside: Tensor,
+                         desc: Tensor, row_ptr: Tensor, source: Tensor, alpha: Tensor, H: int, scale: float,
+                         deg_max: int) -> list[Tensor]:
+        """[dq, dk] from d alpha and the saved alpha (dk gathered per source, no atomics)."""
+        self._check_softmax(q, k, transport, bias, inside, desc, row_ptr, source, H)
+        for t in (alpha, dalpha):
+            _check(t.is_contiguous() and t.dim() == 2 and t.shape[0] == source.shape[0] and t.shape[1] == H
+                   and t.dtype == q.dtype, "alpha and dalpha must be contiguous (n_edges, H) in q's dtype")
+        dq = torch.empty_like(q)
+        dk = torch.empty_like(q)
+        if q.shape[0] == 0:
+            return [dq, dk]
+        src_ptr, src_order, target = source_major(source, row_ptr)
+        ds = torch.empty(source.shape[0], H, dtype=q.dtype, device=q.device)
+        hd = host_desc(desc)
+        _call("gm_softmax_backward" + _suffix(q.dtype), _ptr(dalpha), _ptr(q), _ptr(k), _ptr(transport), _ptr(bias),
+              _ptr(inside), hd.data_ptr(), _ptr(row_ptr), _ptr(source), _ptr(alpha), q.shape[0], source.shape[0],
+              q.shape[1], transport.shape[1], hd.shape[0], H, float(scale), int(deg_max), _ptr(src_ptr),
+              _ptr(src_order), _ptr(target), _ptr(ds), _ptr(dq), _ptr(dk), _stream(q.device))
+        return [dq, dk]
+
+    # ---- depthwise convolution (attention_cpu.cpp:42-145) ----
+
+    @staticmethod
+    def _check_conv(v: Tensor, rc: Tensor, cc: Tensor, transport: Tensor, angular: Tensor, rho: Tensor,
+                    weights: Tensor, desc: Tensor, row_ptr: Tensor, source: Tensor, A0: int, W: int) -> None:
+        _check(v.dim() == 2, "v must be (n_nodes, D)")
+        _require_device(v, rc, cc, transport, angular, rho, weights, row_ptr, source)
+        _check(desc.is_contiguous(), "every tensor must be contiguous")
+        n, e = v.shape[0], source.shape[0]
+        for t in (rc, cc, transport, angular, rho, weights):
+            _check(t.dtype == v.dtype, "v, the coefficients, the weights and the tables must share a dtype")
+        _check(rc.numel() == e * A0, "rc must hold (1, n_edges, a_0) entries")
+        _check(cc.numel() == e * W, "cc must hold (1, n_edges, W) entries")
+        _check(transport.dim() == 3 and transport.shape[0] == e and transport.shape[2] == 2,
+               "transport must be (n_edges, orders, 2)")
+        _check(angular.shape == transport.shape, "angular must match transport's shape")
+        _check(rho.dim() == 1 and rho.shape[0] == e and weights.shape == rho.shape, "rho and weights must be (n_edges,)")
+        _check(desc.dtype == torch.int64 and desc.dim() == 2 and desc.shape[1] == 5 and desc.shape[0] <= 8,
+               "desc must be int64 (F <= 8, 5)")
+        _check(row_ptr.dtype == torch.int64 and row_ptr.dim() == 1 and row_ptr.shape[0] == n + 1,
+               "row_ptr must be int64 (n_nodes + 1,)")
+        _check(source.dtype == torch.int64 and source.dim() == 1, "source must be int64 (n_edges,)")
+        _check(v.shape[1] >= 1, "D must be positive")
+
+    def conv_forward(self, v: Tensor, rc: Tensor, cc: Tensor, transport: Tensor, angular: Tensor, rho: Tensor,
+                     weights: Tensor, desc: Tensor, row_ptr: Tensor, source: Tensor, A0: int, W: int) -> Tensor:
+        """out (n_nodes, D) = sum over each target's edges of weight * C_e(tau v_j)."""
+        self._check_conv(v, rc, cc, transport, angular, rho, weights, desc, row_ptr, source, A0, W)
+        out = torch.empty_like(v)
+        if v.shape[0] == 0:
+            return out
+        hd = host_desc(desc)
+        _call("gm_conv_forward" + _suffix(v.dtype), _ptr(v), _ptr(rc), _ptr(cc), _ptr(transport), _ptr(angular),
+              _ptr(rho), _ptr(weights), hd.data_ptr(), _ptr(row_ptr), _ptr(source), v.shape[0], source.shape[0],
+              v.shape[1], transport.shape[1], hd.shape[0], int(A0), int(W), _ptr(out), _stream(v.device))
+        return out
+
+    def conv_backward(self, g: Tensor, v: Tensor, rc: Tensor, cc: Tensor, transport: Tensor, angular: Tensor,
+                      rho: Tensor, weights: Tensor, desc: Tensor, row_ptr: Tensor, source: Tensor, A0: int,
+                      W: int) -> list[Tensor]:
+        """[dv, drc, dcc] from the output gradient (one pass per source node, no atomics)."""
+        self._check_conv(v, rc, cc, transport, angular, rho, weights, desc, row_ptr, source, A0, W)
+        _check(g.shape == v.shape and g.is_contiguous() and g.dtype == v.dtype,
+               "g must be contiguous, shaped and typed as v")
+        dv = torch.empty_like(v)
+        drc = torch.empty_like(rc)
+        dcc = torch.empty_like(cc)
+        if v.shape[0] == 0:
+            dv.zero_()
+            return [dv, drc, dcc]
+        src_ptr, src_order, target = source_major(source, row_ptr)
+        hd = host_desc(desc)
+        _call("gm_conv_backward" + _suffix(v.dtype), _ptr(g), _ptr(v), _ptr(rc), _ptr(cc), _ptr(transport),
+              _ptr(angular), _ptr(rho), _ptr(weights), hd.data_ptr(), _ptr(row_ptr), _ptr(source), v.shape[0],
+              source.shape[0], v.shape[1], transport.shape[1], hd.shape[0], int(A0), int(W), _ptr(src_ptr),
+              _ptr(src_order), _ptr(target), _ptr(dv), _ptr(drc), _ptr(dcc), _stream(v.device))
+        return [dv, drc, dcc]
+
+
+@functools.cache
+def attention() -> AttentionExtension:
+    library()  # raises when the library is absent
+    return AttentionExtension()

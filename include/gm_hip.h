@@ -1,0 +1,156 @@
+/* gm_hip.h -- the C ABI of libgmhip.so, the MI355X (gfx950) kernels of
+ * gm-attention's fused hot path.
+ *
+ * Every entry point takes raw device pointers, element counts and a
+ * hipStream_t (passed as void*), launches asynchronously on that stream and
+ * returns GM_OK (0) or an error code; gm_last_error() holds the message of the
+ * calling thread's last failure.  Nothing here allocates, frees or
+ * synchronises: outputs and workspaces are the caller's.  Tensors are
+ * contiguous, row-major, in the element type the suffix names (_f32: float,
+ * _f64: double); index arrays are int64.
+ *
+ * Descriptor tables (`desc`) are HOST memory: they are a few dozen integers
+ * fixed per layer, read at launch to pick the kernel specialisation.  All other
+ * pointers are device memory.
+ *
+ * Flat node layout (the reference's SO2FeatureField.to_flat on the heads'
+ * direct sum): frequency 0 first, then each frequency n >= 1 as (copies, 2)
+ * real/imaginary pairs; within a frequency the heads' copies are head-major.
+ *
+ * Reference interfaces each entry point replaces are cited per function
+ * (paths relative to masonfaldet/gm-attention's src/gm_attention/nn/).
+ */
+#ifndef GM_HIP_H
+#define GM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  GM_OK = 0,
+  GM_ERR_ARGUMENT = 1, /* a shape, bound or pointer check failed */
+  GM_ERR_LAUNCH = 2,   /* the HIP runtime rejected a launch */
+  GM_ERR_UNSUPPORTED = 3
+};
+
+/* Attention descriptor: one row per frequency, GM_ATTN_DESC int64 columns
+ * (n, a_n per head, flat offset, coefficient offset, dim) -- the layout of
+ * fused_attention.Plan.rows (fused_attention.py:74-114, fused/attention.h:57-63). */
+#define GM_ATTN_DESC 5
+#define GM_ATTN_MAX_F 8
+#define GM_ATTN_MAX_H 8
+#define GM_ATTN_MAX_D 512
+
+/* Factored descriptor: one row per coefficient block, GM_FACT_DESC int32 columns
+ * (kind, z_offset, b_m, angular, transport, power, out_offset, take_real) --
+ * fused_factored.Block.row (fused_factored.py:80-99, fused/factored.h:74-83). */
+#define GM_FACT_DESC 8
+#define GM_FACT_MAX_K 20
+#define GM_FACT_MAX_OUT 128
+#define GM_FACT_MAX_BM 32
+#define GM_FACT_MAX_C 320
+#define GM_FACT_MAX_BLOCKS 64
+
+/* The calling thread's last error message ("" when none). */
+const char* gm_last_error(void);
+
+/* ABI version of this library: bump when a signature changes. */
+int gm_abi_version(void);
+
+/* ---------------- scores and neighbourhood softmax ----------------
+ *
+ * alpha[e, h] = softmax over target i's edges e of
+ *   scale * sum_n Re<q_i,n,h , tau_n(e) k_j,n,h> + bias[e],
+ * restricted to the edges with inside[e] != 0 (others get 0).
+ *
+ * Replaces gm_fused_attention.softmax_forward(q, k, transport, bias, inside,
+ * desc, row_ptr, source, H, scale, deg_max) (fused/attention_cpu.cpp:197-219,
+ * bound at :258-260; called from fused_attention.py:383).
+ *   q, k       (n_nodes, D)          transport (n_edges, orders, 2)
+ *   bias       (n_edges,)            inside    (n_edges,) uint8
+ *   desc       HOST (F, 5) int64     row_ptr   (n_nodes + 1,)    source (n_edges,)
+ *   alpha      (n_edges, H) out
+ * deg_max is accepted for signature parity; the kernels need no bound on it. */
+int gm_softmax_forward_f32(const float* q, const float* k, const float* transport, const float* bias,
+                           const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr, const int64_t* source,
+                           int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H,
+                           double scale, int64_t deg_max, float* alpha, void* stream);
+int gm_softmax_forward_f64(const double* q, const double* k, const double* transport, const double* bias,
+                           const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr, const int64_t* source,
+                           int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H,
+                           double scale, int64_t deg_max, double* alpha, void* stream);
+
+/* The softmax adjoint and the scores' backward: dq (n_nodes, D) written, dk
+ * (n_nodes, D) written (every row, zero where a node is nobody's source).
+ *
+ * Replaces gm_fused_attention.softmax_backward(dalpha, q, k, transport, bias,
+ * inside, desc, row_ptr, source, alpha, H, scale, deg_max)
+ * (fused/attention_cpu.cpp:222-252; called from fused_attention.py:395).
+ * Unlike the reference (atomic adds on dk, attention_cuda.cu:20-28) the key
+ * gradient is gathered per source, so it is deterministic; that pass reads
+ * the edges grouped by source:
+ *   src_ptr   (n_nodes + 1,)  group offsets into src_order
+ *   src_order (n_edges,)      edge ids sorted by source (stable)
+ *   target    (n_edges,)      each edge's target node
+ *   ds        (n_edges, H)    workspace of the element type
+ * bias and inside are accepted for signature parity and not read. */
+int gm_softmax_backward_f32(const float* dalpha, const float* q, const float* k, const float* transport,
+                            const float* bias, const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr,
+                            const int64_t* source, const float* alpha, int64_t n_nodes, int64_t n_edges, int64_t D,
+                            int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
+                            const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, float* ds,
+                            float* dq, float* dk, void* stream);
+int gm_softmax_backward_f64(const double* dalpha, const double* q, const double* k, const double* transport,
+                            const double* bias, const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr,
+                            const int64_t* source, const double* alpha, int64_t n_nodes, int64_t n_edges, int64_t D,
+                            int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
+                            const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, double* ds,
+                            double* dq, double* dk, void* stream);
+
+/* ---------------- depthwise steerable convolution ----------------
+ *
+ * out_i = sum_e weights[e] C_e(tau v_j): per scalar copy a, rc[e, a] v_j,a;
+ * per complex copy of frequency n, A z + (r/c)^{2n} e^{2 i n phi} B conj(z)
+ * with z = tau_n(e) v_j and (A, B) read from cc[e, coff + 2a], cc[e, coff + 2a_n + 2a].
+ *
+ * Replaces gm_fused_attention.conv_forward(v, rc, cc, transport, angular, rho,
+ * weights, desc, row_ptr, source, A0, W) (fused/attention_cpu.cpp:94-115;
+ * called from fused_attention.py:339).
+ *   v (n_nodes, D); rc (n_edges, A0); cc (n_edges, W); transport, angular
+ *   (n_edges, orders, 2); rho, weights (n_edges,); out (n_nodes, D). */
+int gm_conv_forward_f32(const float* v, const float* rc, const float* cc, const float* transport, const float* angular,
+                        const float* rho, const float* weights, const int64_t* desc, const int64_t* row_ptr,
+                        const int64_t* source, int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F,
+                        int64_t A0, int64_t W, float* out, void* stream);
+int gm_conv_forward_f64(const double* v, const double* rc, const double* cc, const double* transport,
+                        const double* angular, const double* rho, const double* weights, const int64_t* desc,
+                        const int64_t* row_ptr, const int64_t* source, int64_t n_nodes, int64_t n_edges, int64_t D,
+                        int64_t orders, int64_t F, int64_t A0, int64_t W, double* out, void* stream);
+
+/* (dv, drc, dcc) from the output gradient g (n_nodes, D).
+ * Replaces gm_fused_attention.conv_backward(g, v, rc, cc, transport, angular,
+ * rho, weights, desc, row_ptr, source, A0, W) (fused/attention_cpu.cpp:118-145;
+ * called from fused_attention.py:351).  One pass per source node (no atomics:
+ * the reference adds dv atomically, attention_cuda.cu:157-170); src_ptr,
+ * src_order and target as for gm_softmax_backward_*.  dv, drc, dcc written whole. */
+int gm_conv_backward_f32(const float* g, const float* v, const float* rc, const float* cc, const float* transport,
+                         const float* angular, const float* rho, const float* weights, const int64_t* desc,
+                         const int64_t* row_ptr, const int64_t* source, int64_t n_nodes, int64_t n_edges, int64_t D,
+                         int64_t orders, int64_t F, int64_t A0, int64_t W, const int64_t* src_ptr,
+                         const int64_t* src_order, const int64_t* target, float* dv, float* drc, float* dcc,
+                         void* stream);
+int gm_conv_backward_f64(const double* g, const double* v, const double* rc, const double* cc,
+                         const double* transport, const double* angular, const double* rho, const double* weights,
+                         const int64_t* desc, const int64_t* row_ptr, const int64_t* source, int64_t n_nodes,
+                         int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t A0, int64_t W,
+                         const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, double* dv,
+                         double* drc, double* dcc, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GM_HIP_H */
