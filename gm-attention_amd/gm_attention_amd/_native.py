@@ -4,7 +4,9 @@ argument orders.
 
 ``attention()`` stands where the reference's ``gm_fused_attention`` pybind
 module stands (``nn/fused/attention_cpu.cpp:256-261``): ``softmax_forward``,
-``softmax_backward``, ``conv_forward``, ``conv_backward``.  Tensors are
+``softmax_backward``, ``conv_forward``, ``conv_backward``.  ``factored()``
+stands for ``gm_factored`` (``nn/fused/factored_cpu.cpp:223-234``):
+``forward``, ``aggregate``, ``backward``, ``backward_aggregated``.  Tensors are
 checked with the reference's messages (``attention_cpu.cpp:42-64, 149-171``),
 outputs are allocated here through torch's caching allocator, and the raw
 pointers go to ``libgmhip.so`` on the current HIP stream.  There is no CPU
@@ -35,6 +37,9 @@ SIGNATURES: dict[str, list[Any]] = {
     "gm_softmax_backward": [_P] * 10 + [_I] * 6 + [_D, _I] + [_P] * 7,
     "gm_conv_forward": [_P] * 10 + [_I] * 7 + [_P, _P],
     "gm_conv_backward": [_P] * 11 + [_I] * 7 + [_P] * 7,
+    "gm_factored_forward": [_P] * 10 + [_I] * 10 + [_P, _P],
+    "gm_factored_aggregate": [_P] * 3 + [_I] * 3 + [_P, _P],
+    "gm_factored_backward": [_P] * 14 + [_I] * 9 + [_P] * 5,
 }
 
 
@@ -284,3 +289,174 @@ class AttentionExtension:
 def attention() -> AttentionExtension:
     library()  # raises when the library is absent
     return AttentionExtension()
+
+
+# ---------------------------------------------------------------- factored kernel
+
+MAX_K, MAX_OUT, MAX_BM, MAX_C, FACT_DESC = 20, 128, 32, 320, 8
+
+
+def _fcheck(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError("gm_factored: " + message)
+
+
+_HOST_DESC32: dict[tuple, tuple[Any, Tensor]] = {}
+
+
+def host_desc32(desc: Tensor) -> Tensor:
+    """A CPU int32 copy of a factored descriptor table, cached per device tensor."""
+    if desc.device.type == "cpu":
+        return desc.contiguous()
+    key = (id(desc), desc.data_ptr(), desc._version)
+    held = _HOST_DESC32.get(key)
+    if held is not None and held[0]() is desc:
+        return held[1]
+    copy = desc.detach().to("cpu").contiguous()
+    for stale in [k for k, (ref, _) in _HOST_DESC32.items() if ref() is None]:
+        del _HOST_DESC32[stale]
+    _HOST_DESC32[key] = (weakref.ref(desc), copy)
+    return copy
+
+
+class FactoredExtension:
+    """The reference's ``gm_factored`` module surface on libgmhip."""
+
+    with_cuda = True
+
+    @staticmethod
+    def _check_common(h: Tensor, zc: Tensor, zr: Tensor, angular: Tensor, transport: Tensor, rho: Tensor,
+                      desc: Tensor, source: Tensor, d_out: int) -> None:
+        """The checks of factored_cpu.cpp:37-58, with the same messages."""
+        _fcheck(h.dim() == 2 and h.is_contiguous(), "h must be a contiguous (n_edges, k - 1) tensor")
+        _fcheck(zc.dim() == 4 and zc.shape[3] == 2 and zc.is_contiguous(),
+                "zc must be a contiguous (n_nodes, k, wc, 2) tensor")
+        _fcheck(zr.dim() == 3 and zr.is_contiguous(), "zr must be a contiguous (n_nodes, k, wr) tensor")
+        _fcheck(zc.shape[1] == h.shape[1] + 1 and zr.shape[1] == h.shape[1] + 1,
+                "zc and zr must have k = h's width + 1 (the constant feature)")
+        _fcheck(zc.shape[0] == zr.shape[0], "zc and zr must have the same node count")
+        _fcheck(angular.dim() == 3 and angular.shape[2] == 2 and angular.is_contiguous()
+                and angular.shape[0] == h.shape[0], "angular must be a contiguous (n_edges, n_f, 2) tensor")
+        _fcheck(transport.shape == angular.shape and transport.is_contiguous(), "transport must match angular")
+        _fcheck(rho.dim() == 1 and rho.is_contiguous() and rho.shape[0] == h.shape[0],
+                "rho must be a contiguous (n_edges,) tensor")
+        _fcheck(desc.dim() == 2 and desc.shape[1] == FACT_DESC and desc.dtype == torch.int32 and desc.is_contiguous(),
+                "desc must be a contiguous int32 (n_blocks, 8) tensor")
+        _fcheck(source.dim() == 1 and source.shape[0] == h.shape[0] and source.dtype == torch.int64
+                and source.is_contiguous(), "source must be a contiguous int64 (n_edges,) tensor")
+        _fcheck(h.shape[1] + 1 <= MAX_K, "k exceeds MAX_K")
+        _fcheck(1 <= d_out <= MAX_OUT, "d_out must be in [1, MAX_OUT]")
+        _fcheck(2 * zc.shape[2] + zr.shape[2] <= MAX_C, "2 wc + wr exceeds MAX_C")
+        for t in (zc, zr, angular, transport, rho):
+            _fcheck(t.dtype == h.dtype, "every floating tensor must share h's dtype")
+            _fcheck(t.device == h.device, "every tensor must be on h's device")
+        _fcheck(desc.device == h.device and source.device == h.device, "desc and source must be on h's device")
+        if h.device.type != "cuda":
+            raise RuntimeError("libgmhip runs on the GPU only: the tensors are on the CPU (this build has no CPU driver)")
+
+    @staticmethod
+    def _groups(order: Tensor, group_ptr: Tensor, group_source: Tensor, n_edges: int) -> None:
+        _fcheck(order.dtype == torch.int64 and order.dim() == 1 and order.shape[0] == n_edges and order.is_contiguous(),
+                "order must be a contiguous int64 (n_edges,) tensor")
+        _fcheck(group_source.dtype == torch.int64 and group_source.dim() == 1 and group_source.is_contiguous(),
+                "group_source must be a contiguous int64 (n_groups,) tensor")
+        _fcheck(group_ptr.dtype == torch.int64 and group_ptr.dim() == 1 and group_ptr.is_contiguous()
+                and group_ptr.shape[0] == group_source.shape[0] + 1,
+                "group_ptr must be a contiguous int64 (n_groups + 1,) tensor")
+        for t in (order, group_ptr, group_source):
+            _fcheck(t.device.type == "cuda", "order and the groups must be device tensors")
+
+    def forward(self, h: Tensor, zc: Tensor, zr: Tensor, angular: Tensor, transport: Tensor, rho: Tensor, desc: Tensor,
+                source: Tensor, order: Tensor, group_ptr: Tensor, group_source: Tensor, d_out: int,
+                max_bm: int) -> Tensor:
+        """The rows ``(n_edges, d_out)``: every edge's message in the flat output layout."""
+        self._check_common(h, zc, zr, angular, transport, rho, desc, source, d_out)
+        out = torch.empty(h.shape[0], d_out, dtype=h.dtype, device=h.device)
+        _fcheck(1 <= max_bm <= MAX_BM, "max_bm must be in [1, MAX_BM]")
+        if h.shape[0] == 0:
+            return out
+        self._groups(order, group_ptr, group_source, h.shape[0])
+        hd = host_desc32(desc)
+        _call("gm_factored_forward" + _suffix(h.dtype), _ptr(h), _ptr(zc), _ptr(zr), _ptr(angular), _ptr(transport),
+              _ptr(rho), hd.data_ptr(), _ptr(order), _ptr(group_ptr), _ptr(group_source), zc.shape[0], h.shape[0],
+              group_source.shape[0], h.shape[1] + 1, zc.shape[2], zr.shape[2], angular.shape[1], hd.shape[0],
+              int(d_out), int(max_bm), _ptr(out), _stream(h.device))
+        return out
+
+    def aggregate(self, rows: Tensor, weights: Tensor, row_ptr: Tensor) -> Tensor:
+        """``(n_targets, d_out)``: each target's weighted sum of its rows."""
+        _fcheck(rows.dim() == 2 and rows.is_contiguous() and 1 <= rows.shape[1] <= MAX_OUT,
+                "rows must be a contiguous (n_edges, d_out <= MAX_OUT) tensor")
+        _fcheck(weights.dim() == 1 and weights.is_contiguous() and weights.shape[0] == rows.shape[0]
+                and weights.dtype == rows.dtype, "weights must be a contiguous (n_edges,) tensor in the rows' dtype")
+        _fcheck(row_ptr.dim() == 1 and row_ptr.is_contiguous() and row_ptr.shape[0] >= 1 and row_ptr.dtype == torch.int64,
+                "row_ptr must be a contiguous int64 (n_targets + 1,) tensor")
+        _fcheck(weights.device == rows.device and row_ptr.device == rows.device,
+                "every tensor must be on the rows' device")
+        if rows.device.type != "cuda":
+            raise RuntimeError("libgmhip runs on the GPU only: the tensors are on the CPU (this build has no CPU driver)")
+        n_targets = row_ptr.shape[0] - 1
+        out = torch.empty(n_targets, rows.shape[1], dtype=rows.dtype, device=rows.device)
+        if n_targets == 0:
+            return out
+        _call("gm_factored_aggregate" + _suffix(rows.dtype), _ptr(rows), _ptr(weights), _ptr(row_ptr), n_targets,
+              rows.shape[0], rows.shape[1], _ptr(out), _stream(rows.device))
+        return out
+
+    def _backward(self, g: Tensor, target: Tensor | None, weights: Tensor | None, rows: Tensor | None, h: Tensor,
+                  zc: Tensor, zr: Tensor, angular: Tensor, transport: Tensor, rho: Tensor, desc: Tensor,
+                  source: Tensor, order: Tensor, group_ptr: Tensor, group_source: Tensor) -> list[Tensor]:
+        _fcheck(g.dim() == 2 and g.is_contiguous() and g.dtype == h.dtype and g.device == h.device,
+                "g must be a contiguous (rows, d_out) tensor in h's dtype")
+        self._check_common(h, zc, zr, angular, transport, rho, desc, source, g.shape[1])
+        aggregated = target is not None
+        if aggregated:
+            _fcheck(target.dim() == 1 and target.shape[0] == h.shape[0] and target.dtype == torch.int64
+                    and target.is_contiguous() and target.device == h.device,
+                    "target must be a contiguous int64 (n_edges,) tensor")
+            _fcheck(weights.dim() == 1 and weights.shape[0] == h.shape[0] and weights.is_contiguous()
+                    and weights.dtype == h.dtype and weights.device == h.device,
+                    "weights must be a contiguous (n_edges,) tensor in h's dtype")
+            _fcheck(rows.dim() == 2 and rows.shape[0] == h.shape[0] and rows.shape[1] == g.shape[1]
+                    and rows.is_contiguous() and rows.dtype == h.dtype and rows.device == h.device,
+                    "rows must be a contiguous (n_edges, d_out) tensor in h's dtype")
+        else:
+            _fcheck(g.shape[0] == h.shape[0], "g must have one row per edge")
+        dh = torch.empty_like(h)
+        dzc = torch.zeros_like(zc)
+        dzr = torch.zeros_like(zr)
+        dweights = torch.empty_like(weights) if aggregated else None
+        if h.shape[0] == 0:
+            return [dh, dzc, dzr] + ([dweights] if aggregated else [])
+        self._groups(order, group_ptr, group_source, h.shape[0])
+        hd = host_desc32(desc)
+        _call("gm_factored_backward" + _suffix(h.dtype), _ptr(g), _ptr(target) if aggregated else None,
+              _ptr(weights) if aggregated else None, _ptr(rows) if aggregated else None, _ptr(h), _ptr(zc), _ptr(zr),
+              _ptr(angular), _ptr(transport), _ptr(rho), hd.data_ptr(), _ptr(order), _ptr(group_ptr),
+              _ptr(group_source), zc.shape[0], h.shape[0], group_source.shape[0], h.shape[1] + 1, zc.shape[2],
+              zr.shape[2], angular.shape[1], hd.shape[0], g.shape[1], _ptr(dh), _ptr(dzc), _ptr(dzr),
+              _ptr(dweights) if aggregated else None, _stream(h.device))
+        return [dh, dzc, dzr] + ([dweights] if aggregated else [])
+
+    def backward(self, g: Tensor, h: Tensor, zc: Tensor, zr: Tensor, angular: Tensor, transport: Tensor, rho: Tensor,
+                 desc: Tensor, source: Tensor, order: Tensor, group_ptr: Tensor,
+                 group_source: Tensor) -> list[Tensor]:
+        """[dh, dzc, dzr] from the rows' gradient ``g (n_edges, d_out)``."""
+        return self._backward(g, None, None, None, h, zc, zr, angular, transport, rho, desc, source, order, group_ptr,
+                              group_source)
+
+    def backward_aggregated(self, g: Tensor, target: Tensor, weights: Tensor, rows: Tensor, h: Tensor, zc: Tensor,
+                            zr: Tensor, angular: Tensor, transport: Tensor, rho: Tensor, desc: Tensor,
+                            source: Tensor, order: Tensor, group_ptr: Tensor, group_source: Tensor) -> list[Tensor]:
+        """[dh, dzc, dzr, dweights] from the targets' gradient ``g (n_targets, d_out)``."""
+        if h.shape[0] == 0:
+            return [torch.empty_like(h), torch.zeros_like(zc), torch.zeros_like(zr), torch.empty_like(weights)]
+        _fcheck(target.numel() == h.shape[0], "target must list every edge")
+        return self._backward(g, target, weights, rows, h, zc, zr, angular, transport, rho, desc, source, order,
+                              group_ptr, group_source)
+
+
+@functools.cache
+def factored() -> FactoredExtension:
+    library()
+    return FactoredExtension()

@@ -149,6 +149,67 @@ int gm_conv_backward_f64(const double* g, const double* v, const double* rc, con
                          const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, double* dv,
                          double* drc, double* dcc, void* stream);
 
+/* ---------------- factored steerable kernel ----------------
+ *
+ * Per edge e = (i <- j) with h~ = (1, h(e)): every block b's combination
+ * u_b = sum_t h~_t Z_t,b(j) of the source's packed mixes, times the block's
+ * factor e^{i ang phi} e^{i tr gamma} (rho_e)^power, summed per output slot
+ * (rows onto frequency 0 take the real part) into the edge's row.
+ *   h (n_edges, K - 1); zc (n_nodes, K, wc, 2); zr (n_nodes, K, wr);
+ *   angular, transport (n_edges, n_f, 2); rho (n_edges,);
+ *   desc HOST (n_blocks, 8) int32 (GM_FACT_DESC columns);
+ *   order (n_edges,) the edges sorted stably by source; group_ptr (n_groups + 1,)
+ *   each source's run in that order; group_source (n_groups,) the sources.
+ * The blocks must pack zc contiguously, cover zr with one real block, and
+ * list the blocks of one output slot consecutively (fused_factored.plan's
+ * order).
+ *
+ * Replaces gm_factored.forward(h, zc, zr, angular, transport, rho, desc,
+ * source, order, group_ptr, group_source, d_out, max_bm)
+ * (fused/factored_cpu.cpp:77-109; called from fused_factored.py:260, 281).
+ * out (n_edges, d_out) written. */
+int gm_factored_forward_f32(const float* h, const float* zc, const float* zr, const float* angular,
+                            const float* transport, const float* rho, const int32_t* desc, const int64_t* order,
+                            const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges,
+                            int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks,
+                            int64_t d_out, int64_t max_bm, float* out, void* stream);
+int gm_factored_forward_f64(const double* h, const double* zc, const double* zr, const double* angular,
+                            const double* transport, const double* rho, const int32_t* desc, const int64_t* order,
+                            const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges,
+                            int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks,
+                            int64_t d_out, int64_t max_bm, double* out, void* stream);
+
+/* out (n_targets, d_out) = each target's weighted sum of its rows over
+ * [row_ptr[i], row_ptr[i + 1]).
+ * Replaces gm_factored.aggregate(rows, weights, row_ptr)
+ * (fused/factored_cpu.cpp:113-138; called from fused_factored.py:283). */
+int gm_factored_aggregate_f32(const float* rows, const float* weights, const int64_t* row_ptr, int64_t n_targets,
+                              int64_t n_edges, int64_t d_out, float* out, void* stream);
+int gm_factored_aggregate_f64(const double* rows, const double* weights, const int64_t* row_ptr, int64_t n_targets,
+                              int64_t n_edges, int64_t d_out, double* out, void* stream);
+
+/* The backward: dh (n_edges, K - 1) written; dzc, dzr written for every
+ * group source (the caller zeroes them first: a node without edges keeps 0).
+ * With target == NULL, g is the rows' gradient (n_edges, d_out) and weights,
+ * rows and dweights are ignored (gm_factored.backward, factored_cpu.cpp:198-207).
+ * With target (n_edges,), g is the targets' gradient (n_targets, d_out), the
+ * edge's gradient is weights[e] g[target[e]], and dweights[e] = <g[target[e]],
+ * rows[e]> is written (gm_factored.backward_aggregated, factored_cpu.cpp:210-219;
+ * called from fused_factored.py:268, 297).  No atomics: dZ(j) is summed per
+ * source group in a fixed order. */
+int gm_factored_backward_f32(const float* g, const int64_t* target, const float* weights, const float* rows,
+                             const float* h, const float* zc, const float* zr, const float* angular,
+                             const float* transport, const float* rho, const int32_t* desc, const int64_t* order,
+                             const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges,
+                             int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks,
+                             int64_t d_out, float* dh, float* dzc, float* dzr, float* dweights, void* stream);
+int gm_factored_backward_f64(const double* g, const int64_t* target, const double* weights, const double* rows,
+                             const double* h, const double* zc, const double* zr, const double* angular,
+                             const double* transport, const double* rho, const int32_t* desc, const int64_t* order,
+                             const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges,
+                             int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks,
+                             int64_t d_out, double* dh, double* dzc, double* dzr, double* dweights, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -93,3 +93,69 @@ def conv_op(v: Tensor, rc: Tensor, cc: Tensor, transport: Tensor, angular: Tenso
     messages (convolution.py:310-355 with the fused path's given weights)."""
     m = depthwise_messages(v, rc, cc, transport, angular, rho, rows, source)
     return torch.segment_reduce(weights.unsqueeze(-1) * m, "sum", offsets=row_ptr, axis=0)
+
+
+# ---------------------------------------------------------------- factored steerable kernel
+
+
+def _block_factor(angular: Tensor, transport: Tensor, rho: Tensor, ang: int, tr: int, power: int) -> Tensor:
+    """``e^{i ang phi} e^{i tr gamma} (r / c)^power`` per edge: the factor of one
+    phase-carrying block (kernels.py:615-643), the radial power by repeated
+    multiplication as ``_radial_powers`` tabulates it (kernels.py:734-750)."""
+    factor = torch.ones(rho.shape[0], dtype=torch.complex128 if rho.dtype == torch.float64 else torch.complex64)
+    if ang != 0:
+        factor = factor * _phase(angular, ang)
+    if tr != 0:
+        factor = factor * _phase(transport, tr)
+    scale = torch.ones_like(rho)
+    for _ in range(power):
+        scale = scale * rho
+    return factor * scale
+
+
+def factored_rows(h: Tensor, zc: Tensor, zr: Tensor, angular: Tensor, transport: Tensor, rho: Tensor, blocks,
+                  source: Tensor, d_out: int) -> Tensor:
+    """The messages ``(E, d_out)`` of ``SO2SteerableKernel.forward_factored``'s
+    eager branch (kernels.py:645-697) from the fused op's inputs: per output
+    frequency, every block's ``sum_t h~_t Z_t(j)`` (``h~ = (1, h)``; ``Z`` from
+    the packed ``zc (N, K, wc, 2)`` / ``zr (N, K, wr)`` of fused_factored.pack,
+    fused_factored.py:156-180) times the block's factor, the real part taken
+    for the rows onto frequency 0.  ``blocks`` are the descriptor rows
+    ``(kind, z_offset, b_m, angular, transport, power, out_offset, take_real)``
+    of fused_factored.plan (fused_factored.py:101-139)."""
+    E = h.shape[0]
+    ht = torch.cat([torch.ones(E, 1, dtype=h.dtype), h], dim=1)  # (E, K)
+    zcc = torch.view_as_complex(zc.contiguous()) if zc.shape[2] > 0 else None  # (N, K, wc)
+    groups: dict[int, list] = {}
+    for row in blocks:
+        groups.setdefault(int(row[6]), []).append(row)
+    out = torch.zeros(E, d_out, dtype=h.dtype)
+    pieces = []
+    for offset, rows in sorted(groups.items()):
+        scalar = rows[0][0] == 0 or rows[0][7] == 1
+        b_m = rows[0][2]
+        acc = torch.zeros(E, b_m, dtype=h.dtype if scalar else (zcc.dtype if zcc is not None else h.dtype))
+        for kind, zoff, bm, ang, tr, power, _ooff, take_real in rows:
+            if kind == 0:
+                mixed = zr.index_select(0, source)[:, :, zoff:zoff + bm]  # (E, K, b)
+                acc = acc + (ht.unsqueeze(-1) * mixed).sum(dim=1)
+                continue
+            mixed = zcc.index_select(0, source)[:, :, zoff:zoff + bm]  # (E, K, b) complex
+            combined = (ht.unsqueeze(-1) * mixed).sum(dim=1)
+            term = _block_factor(angular, transport, rho, ang, tr, power).unsqueeze(-1) * combined
+            acc = acc + (term.real if take_real else term)
+        flat = acc if scalar else torch.view_as_real(acc).reshape(E, 2 * b_m)
+        pieces.append((offset, flat))
+    cols = []
+    for offset, flat in pieces:
+        cols.append(flat)
+    result = torch.cat(cols, dim=1) if cols else out
+    if result.shape[1] != d_out:
+        raise ValueError("the blocks' output groups must tile the flat output row")
+    return result
+
+
+def factored_aggregate(rows: Tensor, weights: Tensor, row_ptr: Tensor) -> Tensor:
+    """``out_i = sum_{e -> i} w_e rows_e`` (kernels.py:715-725 with
+    _scatter.py:36-58's segment sum)."""
+    return torch.segment_reduce(weights.unsqueeze(-1) * rows, "sum", offsets=row_ptr, axis=0)

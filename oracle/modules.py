@@ -1,0 +1,209 @@
+"""Eager restatements of the reference's steerable-kernel evaluation, from a
+kernel's parameters.  TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+* :func:`readout_messages` -- ``SO2SteerableKernel._forward_general``
+  (reference nn/kernels.py:752-915): per edge, the radial trunk's readout of
+  every block's coefficient matrix, applied to the transported source field
+  under the block's harmonic and radial power.  The coefficient layout is
+  derived here from the field types (kernels.py:336-397), independently of
+  the product's bookkeeping.
+* :func:`node_products` -- the complex ``einsum("ja,bat->jtb")`` of
+  kernels.py:575-603 over ``_block_weights`` (kernels.py:506-536).
+* :func:`factored_messages` -- the eager factored branch (kernels.py:645-697):
+  the node products gathered to the edges, combined with ``h~ = (1, h)`` and
+  each block's factor.
+
+The readout and the factored branch are the same function regrouped by
+associativity (the reference's own check: tests/nn/test_fused_factored.py:
+126-208), so each pins the other.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+
+def _phase(table: Tensor, order: int) -> Tensor:
+    col = table[:, abs(order)]
+    return col.conj() if order < 0 else col
+
+
+def _trunk(kernel, distances: Tensor) -> Tensor:
+    """The Gaussian basis of ``(r / cutoff)^2`` then the ``Linear``/``SiLU`` trunk (kernels.py:191-231, 108-117)."""
+    rb = kernel.radial_basis
+    s = (distances / rb.cutoff) * (distances / rb.cutoff)
+    hidden = torch.exp(-0.5 * ((s.unsqueeze(-1) - rb.centers) / rb.width) ** 2)
+    for layer in kernel.radial_trunk:
+        if isinstance(layer, torch.nn.Linear):
+            hidden = hidden @ layer.weight.T + (layer.bias if layer.bias is not None else 0.0)
+        else:
+            hidden = torch.nn.functional.silu(hidden)
+    return hidden
+
+
+def layout(fin, fout) -> tuple[list[tuple[int, int, str, int, int]], int]:
+    """The complex head's ranges ``(n, m, role, start, power)`` in readout
+    order and the real head's width: every pair ``(n, m)`` but ``(0, 0)`` a
+    linear range of ``2 b_m a_n`` reals, ``n, m >= 1`` an antilinear one after it."""
+    ranges, offset, real = [], 0, 0
+    for n in fin.frequencies:
+        for m in fout.frequencies:
+            a, b = fin.multiplicity(n), fout.multiplicity(m)
+            if n == 0 and m == 0:
+                real = a * b
+                continue
+            ranges.append((n, m, "linear", offset, abs(m - n)))
+            offset += 2 * a * b
+            if n >= 1 and m >= 1:
+                ranges.append((n, m, "antilinear", offset, m + n))
+                offset += 2 * a * b
+    return ranges, real
+
+
+def readout_messages(kernel, x: dict[int, Tensor], source: Tensor, distances: Tensor, angular: Tensor,
+                     transport: Tensor) -> dict[int, Tensor]:
+    """Per-edge messages of the kernel on the node field ``x`` (frequency ->
+    ``(N, a_0)`` / ``(N, a_n, 2)``) gathered by ``source``; ``angular`` and
+    ``transport`` are complex ``(E, K + 1)`` phase tables."""
+    fin, fout = kernel.field_type_in, kernel.field_type_out
+    E = source.shape[0]
+    hidden = _trunk(kernel, distances)
+    ranges, _ = layout(fin, fout)
+    coeff = None
+    if kernel.complex_head is not None:
+        coeff = hidden @ kernel.complex_head.weight.T
+        if kernel.complex_head.bias is not None:
+            coeff = coeff + kernel.complex_head.bias
+    real = None
+    if kernel.real_head is not None:
+        real = hidden @ kernel.real_head.weight.T
+        if kernel.real_head.bias is not None:
+            real = real + kernel.real_head.bias
+    rho = distances / kernel.radial_basis.cutoff
+    xs = {}
+    for n in fin.frequencies:
+        v = x[n].index_select(0, source)
+        if n == 0:
+            xs[0] = v
+        else:
+            xs[n] = _phase(transport, n).unsqueeze(-1) * torch.view_as_complex(v.contiguous())  # transported
+
+    def power(p: int) -> Tensor:
+        s = torch.ones_like(rho)
+        for _ in range(p):
+            s = s * rho
+        return s.unsqueeze(-1)
+
+    def matrix(n: int, m: int, role: str) -> Tensor:
+        for nn, mm, rr, start, _p in ranges:
+            if (nn, mm, rr) == (n, m, role):
+                a, b = fin.multiplicity(n), fout.multiplicity(m)
+                block = coeff[:, start:start + 2 * a * b].reshape(E, b, a, 2)
+                return torch.view_as_complex(block.contiguous())
+        raise KeyError((n, m, role))
+
+    out: dict[int, Tensor] = {}
+    for m in fout.frequencies:
+        b = fout.multiplicity(m)
+        acc = torch.zeros(E, b, dtype=distances.dtype if m == 0 else angular.dtype)
+        for n in fin.frequencies:
+            a = fin.multiplicity(n)
+            if n == 0 and m == 0:
+                acc = acc + (real.reshape(E, b, a) * xs[0].unsqueeze(-2)).sum(-1)
+                continue
+            lin = matrix(n, m, "linear")
+            if n == 0:
+                term = _phase(angular, m).unsqueeze(-1) * (lin * xs[0].to(lin.dtype).unsqueeze(-2)).sum(-1)
+                acc = acc + term * power(abs(m - n))
+            elif m == 0:
+                rotated = _phase(angular, -n).unsqueeze(-1) * xs[n]
+                acc = acc + (lin * rotated.conj().unsqueeze(-2)).sum(-1).real * power(n)
+            else:
+                anti = matrix(n, m, "antilinear")
+                lterm = (lin * (_phase(angular, m - n).unsqueeze(-1) * xs[n]).unsqueeze(-2)).sum(-1)
+                aterm = (anti * (_phase(angular, m + n).unsqueeze(-1) * xs[n].conj()).unsqueeze(-2)).sum(-1)
+                acc = acc + lterm * power(abs(m - n)) + aterm * power(m + n)
+        out[m] = acc if m == 0 else torch.view_as_real(acc)
+    return out
+
+
+def block_weights(kernel, n: int, m: int, role: str) -> Tensor:
+    """``(W_0 = bias, W_1..W_T)`` of one block, ``(b_m, a_n, T + 1)`` (kernels.py:506-536)."""
+    fin, fout = kernel.field_type_in, kernel.field_type_out
+    a, b = fin.multiplicity(n), fout.multiplicity(m)
+    if role == "real":
+        w = kernel.real_head.weight.reshape(b, a, -1)
+        bias = kernel.real_head.bias.reshape(b, a) if kernel.real_head.bias is not None else w.new_zeros(b, a)
+        return torch.cat([bias.unsqueeze(-1), w], dim=-1)
+    ranges, _ = layout(fin, fout)
+    start = next(s for nn, mm, rr, s, _p in ranges if (nn, mm, rr) == (n, m, role))
+    rows = slice(start, start + 2 * a * b)
+    w = torch.view_as_complex(kernel.complex_head.weight[rows].reshape(b, a, 2, -1).permute(0, 1, 3, 2).contiguous())
+    if kernel.complex_head.bias is not None:
+        bias = torch.view_as_complex(kernel.complex_head.bias[rows].reshape(b, a, 2).contiguous())
+    else:
+        bias = w.new_zeros(b, a)
+    return torch.cat([bias.unsqueeze(-1), w], dim=-1)
+
+
+def blocks_of(kernel) -> list[tuple[int, int, str]]:
+    fin, fout = kernel.field_type_in, kernel.field_type_out
+    ranges, real = layout(fin, fout)
+    return ([(0, 0, "real")] if real else []) + [(n, m, r) for n, m, r, _s, _p in ranges]
+
+
+def node_products(kernel, x: dict[int, Tensor]) -> dict[tuple[int, int, str], Tensor]:
+    """``W_t v_j`` per block, ``(N, T + 1, b_m)``, by complex einsum (kernels.py:575-603)."""
+    out = {}
+    for n, m, role in blocks_of(kernel):
+        w = block_weights(kernel, n, m, role)
+        if role == "real":
+            v = x[0]
+        elif n == 0:
+            v = x[0].to(w.dtype)
+        else:
+            v = torch.view_as_complex(x[n].contiguous())
+            if m == 0 or role == "antilinear":
+                v = v.conj()
+        out[(n, m, role)] = torch.einsum("ja,bat->jtb", v, w.to(v.dtype))
+    return out
+
+
+def factored_messages(kernel, x: dict[int, Tensor], source: Tensor, distances: Tensor, angular: Tensor,
+                      transport: Tensor) -> dict[int, Tensor]:
+    """The eager factored branch (kernels.py:645-697)."""
+    fout = kernel.field_type_out
+    products = node_products(kernel, x)
+    hidden = _trunk(kernel, distances)
+    h = torch.cat([torch.ones(hidden.shape[0], 1, dtype=hidden.dtype), hidden], dim=-1)
+    rho = distances / kernel.radial_basis.cutoff
+    ranges, _ = layout(kernel.field_type_in, fout)
+    powers = {(n, m, r): p for n, m, r, _s, p in ranges}
+    out = {}
+    for m in fout.frequencies:
+        acc = None
+        for block in blocks_of(kernel):
+            n, mm, role = block
+            if mm != m:
+                continue
+            combined = (h.unsqueeze(-1) * products[block].index_select(0, source)).sum(dim=1)
+            if role == "real":
+                term = combined
+            else:
+                if n == 0:
+                    phase = _phase(angular, m)
+                elif m == 0:
+                    phase = _phase(angular, n) * _phase(transport, -n)
+                elif role == "linear":
+                    phase = _phase(angular, m - n) * _phase(transport, n)
+                else:
+                    phase = _phase(angular, m + n) * _phase(transport, -n)
+                s = torch.ones_like(rho)
+                for _ in range(powers[block]):
+                    s = s * rho
+                term = (phase * s).unsqueeze(-1) * combined
+                term = term.real if m == 0 else term
+            acc = term if acc is None else acc + term
+        out[m] = acc if m == 0 else torch.view_as_real(acc)
+    return out

@@ -73,3 +73,32 @@ def conv_backward(g, v, rc, cc, transport, angular, rho, weights, desc, row_ptr,
         _p(g), _p(v), _p(rc), _p(cc), _p(transport), _p(angular), _p(rho), _p(weights), _p(desc), _p(row_ptr),
         _p(source), *_i(N, E, D, transport.shape[1], desc.shape[0], A0, W), _p(dv), _p(drc), _p(dcc))
     return dv, drc, dcc
+
+
+def factored_forward(h, zc, zr, angular, transport, rho, desc, source, d_out) -> Tensor:
+    E = h.shape[0]
+    out = torch.zeros(E, d_out, dtype=h.dtype)
+    getattr(lib(), "ref_factored_forward_" + _sfx(h))(
+        _p(h), _p(zc), _p(zr), _p(angular), _p(transport), _p(rho), _p(desc), _p(source),
+        *_i(E, h.shape[1] + 1, zc.shape[2], zr.shape[2], angular.shape[1], desc.shape[0], d_out), _p(out))
+    return out
+
+
+def factored_aggregate(rows, weights, row_ptr) -> Tensor:
+    N = row_ptr.shape[0] - 1
+    out = torch.zeros(N, rows.shape[1], dtype=rows.dtype)
+    getattr(lib(), "ref_factored_aggregate_" + _sfx(rows))(_p(rows), _p(weights), _p(row_ptr), *_i(N, rows.shape[1]),
+                                                            _p(out))
+    return out
+
+
+def factored_backward(g, target, weights, rows, h, zc, zr, angular, transport, rho, desc, source):
+    """The aggregated backward: (dh, dzc, dzr, dweights)."""
+    E = h.shape[0]
+    dh, dzc, dzr = torch.zeros_like(h), torch.zeros_like(zc), torch.zeros_like(zr)
+    dweights = torch.zeros_like(weights)
+    getattr(lib(), "ref_factored_backward_" + _sfx(h))(
+        _p(g), _p(target), _p(weights), _p(rows), _p(h), _p(zc), _p(zr), _p(angular), _p(transport), _p(rho),
+        _p(desc), _p(source), *_i(zc.shape[0], E, h.shape[1] + 1, zc.shape[2], zr.shape[2], angular.shape[1],
+                                   desc.shape[0], rows.shape[1]), _p(dh), _p(dzc), _p(dzr), _p(dweights))
+    return dh, dzc, dzr, dweights
