@@ -1,0 +1,214 @@
+"""Gauge-equivariant neighbourhood attention on the sphere over the fused ops.
+
+Restates the reference's ``nn/attention.py`` layers with their parameters,
+signatures and call structure:
+
+* ``SO2Attention`` (:97-476): intertwiner query and key maps, a steerable
+  value kernel, ``s_ij = <q_i, rho(g_ij) k_j> / sqrt(dim rho_attn)``, the
+  window-and-quadrature-weighted softmax per target, ``y_i = sum_j alpha_ij
+  V(v_ij) rho(g_ij) x_j``, an optional pointwise self map; ``forward_chunked``
+  over target ranges (:344-402);
+* ``SO2MHSA`` (:477-650): the heads' split of the field type, head-major
+  concatenation, the output intertwiner, and the batched pass
+  ``_attend_batched`` (:858-909): the heads' stacked query and key maps
+  (:653-669), the scores and softmax of every head in one fused op, the value
+  kernels in the factored order with one shared source grouping
+  (``_aggregated_factored``, :801-822).
+
+Every score, softmax and value aggregation runs in the HIP ops
+(``fused_attention.Softmax``, ``fused_factored.FactoredAggregate``); the
+projections are per-frequency dense products.  A layer whose fused op is not
+enabled raises (the reference would fall back to its eager torch path; here
+that path is the test oracle).
+"""
+
+from __future__ import annotations
+
+import functools
+import math
+import os
+from collections.abc import Sequence
+from typing import cast
+
+import torch
+import torch.utils.checkpoint
+from torch import Tensor, nn
+
+from gm_attention_amd.discretization.discretization import SphericalDiscretization
+from gm_attention_amd.nn import fused_attention, fused_factored
+from gm_attention_amd.nn.kernels import SO2SteerableKernel
+from gm_attention_amd.nn.linear import SO2Linear, apply_linear
+from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
+
+REMATERIALIZE_CHUNKS = os.environ.get("GM_CHUNK_REMATERIALIZE", "1") != "0"
+
+
+def _resolve_edges(edges, cutoff: float):
+    return edges.edges_within(cutoff) if isinstance(edges, SphericalDiscretization) else edges
+
+
+def _validate_node_field(x: SO2FeatureField, field_type: SO2FieldType, edges) -> None:
+    if x.field_type != field_type:
+        raise ValueError(f"Expected a field of type {field_type!r}, got {x.field_type!r}.")
+    n_nodes = edges.row_ptr.shape[0] - 1
+    if tuple(x.batch_shape) != (n_nodes,):
+        raise ValueError(f"x.batch_shape must equal (n_nodes,) = ({n_nodes},), inferred from edges.row_ptr, "
+                         f"got {tuple(x.batch_shape)}.")
+
+
+def _checkpointed(module: nn.Module, compute):
+    if module.training and torch.is_grad_enabled() and REMATERIALIZE_CHUNKS:
+        return torch.utils.checkpoint.checkpoint(compute, use_reentrant=False)
+    return compute()
+
+
+def _concatenate_heads(fields: Sequence[SO2FeatureField], field_type: SO2FieldType) -> SO2FeatureField:
+    """Direct sum of equal-typed fields along each frequency's multiplicity axis (:456-474)."""
+    return SO2FeatureField(field_type, {
+        f: torch.cat([fld[f] for fld in fields], dim=-1 if f == 0 else -2) for f in field_type.frequencies})
+
+
+class SO2Attention(nn.Module):
+    def __init__(self, field_type_in: SO2FieldType, field_type_attn: SO2FieldType, field_type_out: SO2FieldType, *,
+                 cutoff: float, window: str = "hard", self_interaction: str = "none", n_radial_basis: int = 8,
+                 radial_hidden_features: Sequence[int] = (16,), radial_basis: str = "gaussian", bias: bool = True,
+                 value_kind: str = "steerable", dtype=None, device=None) -> None:
+        super().__init__()
+        if window not in ("hard", "quartic"):
+            raise ValueError(f"window must be 'hard' or 'quartic', got {window!r}.")
+        if self_interaction not in ("none", "linear"):
+            raise ValueError(f"self_interaction must be 'none' or 'linear', got {self_interaction!r}.")
+        if value_kind != "steerable":
+            raise ValueError(f"value_kind must be 'steerable', got {value_kind!r}.")
+        self.value_kind = value_kind
+        self.field_type_in = field_type_in
+        self.field_type_attn = field_type_attn
+        self.field_type_out = field_type_out
+        self.cutoff = float(cutoff)
+        self.window = window
+        self.self_interaction = self_interaction
+        self.query = SO2Linear(field_type_in, field_type_attn, bias=bias, dtype=dtype, device=device)
+        self.key = SO2Linear(field_type_in, field_type_attn, bias=bias, dtype=dtype, device=device)
+        self.value = SO2SteerableKernel(field_type_in, field_type_out, cutoff=cutoff, n_radial_basis=n_radial_basis,
+                                        radial_hidden_features=radial_hidden_features, radial_basis=radial_basis,
+                                        bias=bias, dtype=dtype, device=device)
+        self.self_linear = (SO2Linear(field_type_in, field_type_out, bias=False, dtype=dtype, device=device)
+                            if self_interaction == "linear" else None)
+        self._score_scale = 1.0 / math.sqrt(field_type_attn.dimension)
+
+    def forward(self, x: SO2FeatureField, edges) -> SO2FeatureField:
+        edges = _resolve_edges(edges, self.cutoff)
+        _validate_node_field(x, self.field_type_in, edges)
+        with torch.profiler.record_function("gm::attention/attend"):
+            attended = self._attend(x, edges)
+        return self._finish(x, attended)
+
+    def _attend(self, x: SO2FeatureField, edges, products=None, groups=None) -> dict[int, Tensor]:
+        q, k = self.query(x), self.key(x)
+        if not fused_attention.softmax_head_enabled(self, x, edges):
+            raise RuntimeError("the fused scores-and-softmax op is not enabled for this call "
+                               "(GM_FUSED_ATTENTION=1 and device tensors required)")
+        alpha = fused_attention.softmax_head(self, q.to_flat(), k.to_flat(), edges)
+        return self.value.forward_factored_aggregated(x, edges, alpha, products, groups).coefficients
+
+    def forward_chunked(self, x: SO2FeatureField, edges, *, chunk_size: int) -> SO2FeatureField:
+        """:meth:`forward` one range of target nodes at a time (:344-402)."""
+        if chunk_size < 1:
+            raise ValueError(f"chunk_size must be at least 1, got {chunk_size}.")
+        edges = _resolve_edges(edges, self.cutoff)
+        _validate_node_field(x, self.field_type_in, edges)
+        n_nodes = edges.row_ptr.shape[0] - 1
+        products = self.value.node_products(x)
+        totals: dict[int, Tensor] = {}
+        for start in range(0, n_nodes, chunk_size):
+            stop = min(start + chunk_size, n_nodes)
+            first, last = int(edges.row_ptr[start]), int(edges.row_ptr[stop])
+            if first == last:
+                continue
+            chunk = edges.select(torch.arange(first, last, device=edges.row_ptr.device))
+            fused_attention.register_chunk(chunk, edges, first, last)
+            groups = fused_factored.source_groups(chunk.source_index, fused_factored.group_key(edges, first, last),
+                                                  owner=edges.edge_index)
+            partial = _checkpointed(self, functools.partial(self._attend, x, chunk, products, groups))
+            for f, v in partial.items():
+                totals[f] = v if f not in totals else totals[f] + v
+        if not totals:
+            return self._finish(x, self._attend(x, edges))
+        return self._finish(x, totals)
+
+    def _finish(self, x: SO2FeatureField, outputs: dict[int, Tensor]) -> SO2FeatureField:
+        attended = SO2FeatureField(self.field_type_out, outputs)
+        if self.self_linear is None:
+            return attended
+        pointwise = self.self_linear(x)
+        return SO2FeatureField(self.field_type_out, {f: attended[f] + pointwise[f] for f in self.field_type_out.frequencies})
+
+
+class SO2MHSA(nn.Module):
+    def __init__(self, field_type_in: SO2FieldType, num_heads: int, *, cutoff: float, window: str = "hard",
+                 n_radial_basis: int = 8, radial_hidden_features: Sequence[int] = (16,), radial_basis: str = "gaussian",
+                 bias: bool = True, batched: bool = False, value_kind: str = "steerable", dtype=None,
+                 device=None) -> None:
+        super().__init__()
+        if num_heads < 1:
+            raise ValueError(f"num_heads must be at least 1, got {num_heads}.")
+        offending = {f: m for f, m in field_type_in.items() if m % num_heads != 0}
+        if offending:
+            raise ValueError(f"num_heads ({num_heads}) must divide the multiplicity of every present frequency; "
+                             f"offending frequencies (as frequency: multiplicity): {offending}.")
+        self.batched = bool(batched)
+        self.value_kind = value_kind
+        self.field_type_in = field_type_in
+        self.num_heads = num_heads
+        self.cutoff = float(cutoff)
+        self.field_type_attn = SO2FieldType({f: m // num_heads for f, m in field_type_in.items()})
+        self.heads = nn.ModuleList([
+            SO2Attention(field_type_in, self.field_type_attn, self.field_type_attn, cutoff=cutoff, window=window,
+                         n_radial_basis=n_radial_basis, radial_hidden_features=radial_hidden_features,
+                         radial_basis=radial_basis, bias=bias, value_kind=value_kind, dtype=dtype, device=device)
+            for _ in range(num_heads)])
+        self.output_projection = SO2Linear(field_type_in, field_type_in, bias=bias, dtype=dtype, device=device)
+
+    def forward(self, x: SO2FeatureField, edges) -> SO2FeatureField:
+        edges = _resolve_edges(edges, self.cutoff)
+        if self.batched:
+            _validate_node_field(x, self.field_type_in, edges)
+            return self.output_projection(SO2FeatureField(self.field_type_in, _attend_batched(self, x, edges)))
+        fused = _concatenate_heads([head(x, edges) for head in self.heads], self.field_type_in)
+        return self.output_projection(fused)
+
+    def forward_chunked(self, x: SO2FeatureField, edges, *, chunk_size: int) -> SO2FeatureField:
+        edges = _resolve_edges(edges, self.cutoff)
+        outs = [cast(SO2Attention, h).forward_chunked(x, edges, chunk_size=chunk_size) for h in self.heads]
+        return self.output_projection(_concatenate_heads(outs, self.field_type_in))
+
+
+def _stacked_projection(linears: Sequence[SO2Linear], x: SO2FeatureField) -> SO2FeatureField:
+    """The heads' intertwiners as one map onto their direct sum, head-major (:653-669)."""
+    weights = {str(f): torch.cat([lin.weight[str(f)] for lin in linears], dim=0) for f in x.field_type.frequencies}
+    bias = torch.cat([lin.bias for lin in linears]) if linears[0].has_bias else None
+    return apply_linear(x.field_type, x.field_type.frequencies, weights, bias, x)
+
+
+def _attend_batched(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> dict[int, Tensor]:
+    heads = [cast(SO2Attention, h) for h in mhsa.heads]
+    with torch.profiler.record_function("gm::attention/attend"):
+        queries = _stacked_projection([h.query for h in heads], x)
+        keys = _stacked_projection([h.key for h in heads], x)
+        if not fused_attention.softmax_enabled(mhsa, x, edges):
+            raise RuntimeError("the fused scores-and-softmax op is not enabled for this call "
+                               "(GM_FUSED_ATTENTION=1 and device tensors required)")
+        alpha = fused_attention.softmax(mhsa, queries.to_flat(), keys.to_flat(), edges)  # (n_edges, n_heads)
+        return _aggregated_factored(mhsa, x, edges, alpha)
+
+
+def _aggregated_factored(mhsa: SO2MHSA, x: SO2FeatureField, edges, alpha: Tensor) -> dict[int, Tensor]:
+    """Every head's value kernel, factored and aggregated under its attention
+    weights, with one source grouping for all heads (:801-822)."""
+    groups = fused_factored.groups_for(edges, edges.source_index)
+    fields = []
+    for head, weights in zip(mhsa.heads, alpha.unbind(1), strict=True):
+        kernel = cast(SO2SteerableKernel, head.value)
+        fields.append(kernel.forward_factored_aggregated(x, edges, weights.contiguous(), kernel.node_products(x),
+                                                         groups))
+    return _concatenate_heads(fields, mhsa.field_type_in).coefficients

@@ -33,7 +33,8 @@ from gm_attention_amd import _native
 
 MAX_H, MAX_F, MAX_D, DESC = 8, 8, 512, 5
 #: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` accepted (no CPU driver in this build).
-MODE = os.environ.get("GM_FUSED_ATTENTION", "0")
+#: The default is ``"1"``: this build's layers run only through the fused ops (``"0"`` makes them raise).
+MODE = os.environ.get("GM_FUSED_ATTENTION", "1")
 
 
 def extension(cuda: bool = True) -> Any:

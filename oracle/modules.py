@@ -207,3 +207,80 @@ def factored_messages(kernel, x: dict[int, Tensor], source: Tensor, distances: T
             acc = term if acc is None else acc + term
         out[m] = acc if m == 0 else torch.view_as_real(acc)
     return out
+
+
+# ---------------------------------------------------------------- attention layers
+
+
+def linear(lin, x: dict[int, Tensor], fout) -> dict[int, Tensor]:
+    """``SO2Linear.forward`` (reference nn/linear.py:130-190): real matmul at 0,
+    complex matmul above, bias on frequency 0."""
+    out = {}
+    batch = next(iter(x.values())).shape[0]
+    for f in fout.frequencies:
+        b = fout.multiplicity(f)
+        if str(f) not in lin.weight:
+            z = torch.zeros(batch, b, dtype=torch.float64) if f == 0 else torch.zeros(batch, b, 2, dtype=torch.float64)
+            out[f] = z + (lin.bias if (f == 0 and lin.bias is not None) else 0.0)
+            continue
+        w = lin.weight[str(f)]
+        if f == 0:
+            out[0] = x[0] @ w.T + (lin.bias if lin.bias is not None else 0.0)
+        else:
+            out[f] = torch.view_as_real(torch.view_as_complex(x[f].contiguous())
+                                        @ torch.view_as_complex(w.contiguous()).T)
+    return out
+
+
+def flat(x: dict[int, Tensor]) -> Tensor:
+    return torch.cat([x[f] if f == 0 else x[f].flatten(-2) for f in sorted(x)], dim=-1)
+
+
+def softmax_weights(q: dict[int, Tensor], k: dict[int, Tensor], edges, cutoff: float, window: str, n_heads: int,
+                    scale: float, tolerance: float | None = None) -> Tensor:
+    """``_softmax_weights`` (reference attention.py:825-855) straight from the
+    edges: gathered queries, gathered and transported keys, per-head scores,
+    ``log c + log w`` with the tiny clamp, the window's support masked to
+    ``-inf``, a detached per-target max, exp, per-target normalisation."""
+    target, source = edges.target_index, edges.source_index
+    E = source.shape[0]
+    score = torch.zeros(E, n_heads, dtype=next(iter(q.values())).dtype)
+    for f in sorted(q):
+        qe, ke = q[f].index_select(0, target), k[f].index_select(0, source)
+        if f != 0:
+            ke = torch.view_as_real(edges.transport_phases[:, f].unsqueeze(-1) * torch.view_as_complex(ke.contiguous()))
+        prod = (qe * ke).reshape(E, n_heads, -1)
+        score = score + prod.sum(-1)
+    score = score * scale
+    d = edges.distances
+    # the hard window's slack is the distances' dtype's (edge_geometry.py:403-428); a float64
+    # oracle of a float32 run passes the float32 slack explicitly
+    tol = tolerance if tolerance is not None else (1e-10 if d.dtype == torch.float64 else 1e-5)
+    win = (d <= cutoff + tol).to(d.dtype) if window == "hard" else torch.relu(1.0 - (d / cutoff) ** 2) ** 2
+    tiny = torch.finfo(score.dtype).tiny
+    lw = score + (torch.log(win.clamp_min(tiny)) + torch.log(edges.tangent_quadrature_weights.clamp_min(tiny))).unsqueeze(-1)
+    lw = lw.masked_fill(~(win > 0).unsqueeze(-1), float("-inf"))
+    mx = torch.segment_reduce(lw, "max", offsets=edges.row_ptr, axis=0).detach()
+    u = torch.exp(lw - mx.index_select(0, target))
+    return u / torch.segment_reduce(u, "sum", offsets=edges.row_ptr, axis=0).index_select(0, target)
+
+
+def mhsa_forward(mhsa, x: dict[int, Tensor], edges, tolerance: float | None = None) -> dict[int, Tensor]:
+    """``SO2MHSA.forward`` (reference attention.py:582-608), head by head
+    (the function the batched pass computes, attention.py:858-909): each
+    head's query and key maps, its softmax, its value kernel's per-edge
+    readout weighted and summed per target; heads concatenated head-major;
+    the output intertwiner."""
+    fin = mhsa.field_type_in
+    outs = []
+    for head in mhsa.heads:
+        q = linear(head.query, x, head.field_type_attn)
+        k = linear(head.key, x, head.field_type_attn)
+        alpha = softmax_weights(q, k, edges, head.cutoff, head.window, 1, head._score_scale, tolerance)[:, 0]
+        msgs = readout_messages(head.value, x, edges.source_index, edges.distances, edges.angular_phases,
+                                edges.transport_phases)
+        agg = {f: torch.segment_reduce(alpha.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum", offsets=edges.row_ptr,
+                                       axis=0) for f, m in msgs.items()}
+        outs.append(agg)
+    fused = {f: torch.cat([o[f] for o in outs], dim=-1 if f == 0 else -2) for f in fin.frequencies}
+    return linear(mhsa.output_projection, fused, fin)

@@ -1,0 +1,169 @@
+"""The attention layers (SO2MHSA batched and per head, SO2Attention chunked) on
+the HIP path against the oracle (oracle.modules.mhsa_forward: the
+reference's eager head-by-head attention in float64), with the input field's
+and every parameter's gradient; and gauge equivariance under random frame
+rotations (the reference's pattern: tests/nn/test_attention_batched.py:105).
+"""
+
+import math
+
+import pytest
+import torch
+
+import problems
+from gm_attention_amd.discretization.discretization import SphericalDiscretization
+from gm_attention_amd.discretization.frames import build_tangent_frames, rotate_tangent_frames
+from gm_attention_amd.discretization.grid import build_equiangular_grid
+from gm_attention_amd.nn.attention import SO2Attention, SO2MHSA
+from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
+from oracle import modules
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got, want, dtype, name, reduction=False):
+    """float64: 1e-10.  float32: |got - want| <= 1e-5 |want| + 1e-6 max|want|
+    elementwise; a parameter gradient (``reduction``, a sum over every edge or
+    node) instead within 1e-5 of its norm and 1e-5 of its largest entry."""
+    want, got = want.detach().double().cpu(), got.detach().double().cpu()
+    if dtype == torch.float32 and reduction:
+        err = (got - want).norm() / want.norm().clamp_min(1e-30)
+        peak = (got - want).abs().max() / want.abs().max().clamp_min(1e-30)
+        if want.abs().max() < 1e-6:  # an identically zero gradient (e.g. a key bias under the softmax)
+            assert got.abs().max() <= 1e-5, f"{name}: {got.abs().max():.3e} where the gradient vanishes"
+        else:
+            assert err <= 1e-5 and peak <= 1e-5, f"{name}: relative error {err:.3e}, peak {peak:.3e}"
+        return
+    if dtype == torch.float64:
+        torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10, msg=lambda m, name=name: f"{name}: {m}")
+    else:
+        scale = max(1.0, float(want.abs().max()))
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6 * scale, msg=lambda m, name=name: f"{name}: {m}")
+
+
+def build(field, heads, window, batch, nlat=10, nlon=20, seed=0):
+    disc = problems.discretization(nlat, nlon)
+    edges = disc.edge_geometry.tile(batch, n_sources=disc.n_nodes) if batch > 1 else disc.edge_geometry
+    torch.manual_seed(seed)
+    mhsa = SO2MHSA(SO2FieldType(field), heads, cutoff=disc.coverage_radius, window=window, dtype=torch.float64)
+    n = edges.row_ptr.shape[0] - 1
+    x = problems.normal((n, mhsa.field_type_in.dimension), seed + 1)
+    return mhsa, x, edges
+
+
+def run(module, flat, edges, probe, *, oracle=False, chunk=None, tolerance=None):
+    leaf_flat = flat.clone().requires_grad_(True)
+    x = SO2FeatureField.from_flat(module.field_type_in, leaf_flat)
+    leaf = x.coefficients
+    module.zero_grad(set_to_none=True)
+    if oracle:
+        out = modules.flat(modules.mhsa_forward(module, leaf, edges, tolerance))
+    elif chunk is not None:
+        out = module.forward_chunked(x, edges, chunk_size=chunk).to_flat()
+    else:
+        out = module(x, edges).to_flat()
+    (out * probe.to(out.device, out.dtype)).sum().backward()
+    return out.detach(), {"x": leaf_flat.grad}, {n: p.grad for n, p in module.named_parameters()
+                                                  if p.grad is not None}
+
+
+CASES = [({0: 8, 1: 8, 2: 8}, 4, "hard", 2), ({0: 4, 1: 4, 2: 4}, 2, "quartic", 1), ({0: 6, 1: 3}, 3, "hard", 1)]
+
+
+@pytest.mark.parametrize("batched", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("case", CASES)
+def test_mhsa_matches_the_oracle(case, dtype, batched, cuda):
+    field, heads, window, batch = case
+    print(f"mhsa {case} {dtype} batched={batched}", flush=True)
+    mhsa, x, edges = build(field, heads, window, batch)
+    mhsa.batched = batched
+    probe = problems.normal(x.shape, 7)
+    if dtype == torch.float32:  # the oracle sees the same rounded parameters, inputs and geometry
+        mhsa.load_state_dict({k: v.float().double() for k, v in mhsa.state_dict().items()})
+        x = x.float().double()
+        edges_o = edges.to(None, torch.float32).to(None, torch.float64)
+    else:
+        edges_o = edges
+    # the hard window admits an edge by the tested dtype's slack (1e-5 in float32), as the fused path does
+    want = run(mhsa, x, edges_o, probe, oracle=True, tolerance=1e-5 if dtype == torch.float32 else None)
+    gpu = SO2MHSA(mhsa.field_type_in, heads, cutoff=mhsa.cutoff, window=window, batched=batched, dtype=dtype,
+                  device=cuda)
+    gpu.load_state_dict({k: v.to(dtype) for k, v in mhsa.state_dict().items()})
+    got = run(gpu, x.to(cuda, dtype), edges.to(cuda, dtype), probe)
+    close(got[0], want[0], dtype, "out")
+    for f in want[1]:
+        close(got[1][f], want[1][f], dtype, f"dx[{f}]")
+    assert set(got[2]) == set(want[2])
+    for n in want[2]:
+        close(got[2][n], want[2][n], dtype, f"d{n}", reduction=True)
+
+
+def test_chunked_equals_whole(cuda):
+    mhsa, x, edges = build({0: 8, 1: 8, 2: 8}, 4, "hard", 2)
+    gpu = mhsa.to(cuda)
+    gpu.train()
+    e = edges.to(cuda, torch.float64)
+    probe = problems.normal(x.shape, 7)
+    whole = run(gpu, x.to(cuda), e, probe)
+    chunked = run(gpu, x.to(cuda), e, probe, chunk=37)
+    close(chunked[0], whole[0], torch.float64, "out")
+    for f in whole[1]:
+        close(chunked[1][f], whole[1][f], torch.float64, f"dx[{f}]")
+    for n in whole[2]:
+        close(chunked[2][n], whole[2][n], torch.float64, f"d{n}")
+
+
+@pytest.mark.parametrize("window", ["hard", "quartic"])
+def test_gauge_equivariance_under_random_frame_rotations(window, cuda):
+    """Rotating every node's frame by theta_i and transforming the input by
+    rho(r_{-theta}) transforms the output the same way."""
+    nlat, nlon = 10, 20
+    grid = build_equiangular_grid(nlat, nlon)
+    cutoff = 3.0 * math.pi / (nlat - 1)
+    frames = build_tangent_frames(grid.nodes)
+    theta = torch.rand(grid.n_nodes, dtype=torch.float64, generator=torch.Generator().manual_seed(4)) * 2 * math.pi
+    base = SphericalDiscretization.from_grid(grid, cutoff, frames=frames)
+    turned = SphericalDiscretization.from_grid(grid, cutoff, frames=rotate_tangent_frames(frames, theta))
+    assert torch.equal(base.edge_geometry.edge_index, turned.edge_geometry.edge_index)
+    torch.manual_seed(0)
+    field = SO2FieldType({0: 8, 1: 8, 2: 8})
+    mhsa = SO2MHSA(field, 4, cutoff=cutoff, window=window, batched=True, dtype=torch.float64, device=cuda)
+    x = SO2FeatureField.from_flat(field, problems.normal((grid.n_nodes, field.dimension), 1).to(cuda))
+    with torch.no_grad():
+        y = mhsa(x, base.edge_geometry.to(cuda, torch.float64))
+        y_turned = mhsa(x.gauge_transform(theta.to(cuda)), turned.edge_geometry.to(cuda, torch.float64))
+    expected = y.gauge_transform(theta.to(cuda))
+    torch.testing.assert_close(y_turned.to_flat(), expected.to_flat(), rtol=1e-9, atol=1e-9)
+    # and the output is not trivially invariant
+    assert float((y.to_flat() - expected.to_flat()).abs().max()) > 1e-3
+
+
+def test_single_head_attention_matches_the_oracle(cuda):
+    mhsa, x, edges = build({0: 4, 1: 4, 2: 4}, 1, "quartic", 1)
+    head = mhsa.heads[0]
+    probe = problems.normal((x.shape[0], head.field_type_out.dimension), 3)
+
+    def run_head(module, flat, eds, oracle):
+        xx = SO2FeatureField.from_flat(mhsa.field_type_in, flat.clone().requires_grad_(True))
+        module.zero_grad(set_to_none=True)
+        if oracle:
+            q = modules.linear(module.query, xx.coefficients, module.field_type_attn)
+            k = modules.linear(module.key, xx.coefficients, module.field_type_attn)
+            alpha = modules.softmax_weights(q, k, eds, module.cutoff, module.window, 1, module._score_scale)[:, 0]
+            msgs = modules.readout_messages(module.value, xx.coefficients, eds.source_index, eds.distances,
+                                            eds.angular_phases, eds.transport_phases)
+            out = torch.segment_reduce(alpha.unsqueeze(-1) * modules.flat(msgs), "sum", offsets=eds.row_ptr, axis=0)
+        else:
+            out = module(xx, eds).to_flat()
+        (out * probe.to(out.device)).sum().backward()
+        return out.detach(), {n: p.grad for n, p in module.named_parameters() if p.grad is not None}
+
+    want = run_head(head, x, edges, True)
+    gpu = SO2Attention(mhsa.field_type_in, head.field_type_attn, head.field_type_out, cutoff=head.cutoff,
+                       window="quartic", dtype=torch.float64, device=cuda)
+    gpu.load_state_dict(head.state_dict())
+    got = run_head(gpu, x.to(cuda), edges.to(cuda, torch.float64), False)
+    close(got[0], want[0], torch.float64, "out")
+    for n in want[1]:
+        close(got[1][n], want[1][n], torch.float64, f"d{n}")

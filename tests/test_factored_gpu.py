@@ -35,14 +35,24 @@ CONFIGS = [
 ]
 
 
-def close(got, want, dtype, name):
-    want = want.detach().double().cpu()
-    got = got.detach().double().cpu()
+def close(got, want, dtype, name, reduction=False):
+    """float64: 1e-10.  float32: |got - want| <= 1e-5 |want| + 1e-6 max|want|
+    elementwise; a parameter gradient (``reduction``, a sum over every edge or
+    node) instead within 1e-5 of its norm and 1e-5 of its largest entry."""
+    want, got = want.detach().double().cpu(), got.detach().double().cpu()
+    if dtype == torch.float32 and reduction:
+        err = (got - want).norm() / want.norm().clamp_min(1e-30)
+        peak = (got - want).abs().max() / want.abs().max().clamp_min(1e-30)
+        if want.abs().max() < 1e-6:  # an identically zero gradient (e.g. a key bias under the softmax)
+            assert got.abs().max() <= 1e-5, f"{name}: {got.abs().max():.3e} where the gradient vanishes"
+        else:
+            assert err <= 1e-5 and peak <= 1e-5, f"{name}: relative error {err:.3e}, peak {peak:.3e}"
+        return
     if dtype == torch.float64:
-        torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10, msg=name)
+        torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10, msg=lambda m, name=name: f"{name}: {m}")
     else:
         scale = max(1.0, float(want.abs().max())) if want.numel() else 1.0
-        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6 * scale, msg=name)
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6 * scale, msg=lambda m, name=name: f"{name}: {m}")
 
 
 def setup(fin, fout, bias, dtype, nlat=12, nlon=24, batch=1, seed=0):
@@ -137,5 +147,5 @@ def test_the_kernel_matches_the_readout(fin, fout, bias, dtype, cuda):
         close(got[1][f], want[1][f], dtype, f"dx[{f}]")
     assert set(got[2]) == set(want[2]) and got[2]
     for n in want[2]:
-        close(got[2][n], want[2][n], dtype, f"d{n}")
+        close(got[2][n], want[2][n], dtype, f"d{n}", reduction=True)
     close(got[3], want[3], dtype, "dweights")
