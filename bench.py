@@ -1,17 +1,24 @@
-"""Benchmark of the fused neighbourhood-attention hot path on one MI355X.
+"""Benchmark of gm-attention's fused hot path on one MI355X.
 
-Default workload (the north-star shape): the scores-and-softmax attention op
-(``fused_attention.Softmax``, forward + backward) on the equiangular 256x512
-grid, batch 4 (a 4-fold disjoint union: 524,288 query points, 62,963,712
-edges), field {0: 32, 1: 32, 2: 32} (160 reals per point), 8 heads, geodesic
-radius 3 row spacings, hard window.  Inputs q, k and the upstream gradient
-are N(0, 1), float32, resident in HBM before the timed region.
+Default workload (the north-star shape): one ``SO2MHSA(batched=True)`` layer,
+forward + backward (input and every parameter gradient), on the equiangular
+256x512 grid, batch 4 (a 4-fold disjoint union: 524,288 query points,
+62,963,712 edges), field {0: 32, 1: 32, 2: 32} (160 reals per point), 8
+heads, geodesic radius 3 row spacings, hard window, float32.  The layer runs
+the stacked query/key projections, the fused scores-and-softmax op, every
+head's node products, radial trunk and fused factored value aggregation,
+and the output projection.  Inputs and the upstream gradient are N(0, 1),
+resident in HBM before the timed region.
 
-Prints one JSON line: query points per second over the whole step, the
-achieved HBM bandwidth of the step from the algorithmic bytes (the op
-boundary's compulsory traffic) against the 8 TB/s peak, and the reference's
-own CPU arithmetic (oracle/_ref, serial) timed on a bounded sample on this
-host.
+``--workload softmax`` times the scores-and-softmax op alone (forward +
+backward) on the same shape.
+
+Prints one JSON line.  Each fused op is timed live with HIP events on the
+stream it launches on; the roofline entry is the op with the largest share of
+the step, its algorithmic bytes or FLOPs per launch (formulas below) over its
+average launch time.  The CPU baseline is the eager PyTorch restatement of
+the reference's path (oracle/, the factored order) on a bounded sample of the
+same workload on this host's cores, extrapolated per edge.
 """
 
 from __future__ import annotations
@@ -22,6 +29,7 @@ import math
 import os
 import sys
 import time
+from collections import defaultdict
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -30,6 +38,7 @@ for _p in (ROOT, ROOT / "gm-attention_amd"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
 NLAT, NLON, BATCH, HEADS = 256, 512, 4, 8
 FIELD = {0: 32, 1: 32, 2: 32}
 
@@ -38,151 +47,272 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def softmax_bytes(E: int, N: int, D: int, H: int) -> tuple[int, int]:
-    """Algorithmic bytes of one forward and one backward: each tensor crossing
-    the op boundary once (int64 indices, float32 values, transport orders 1..2)."""
-    fwd = E * (8 + 16 + 4 + 1 + 4 * H) + N * (8 * D + 8)
-    bwd = E * (8 + 16 + 8 * H) + N * (16 * D + 8)
-    return fwd, bwd
+# ---------------------------------------------------------------- algorithmic cost per launch
 
 
-def build_problem(device):
+def softmax_cost(E: int, N: int, D: int, H: int) -> dict[str, tuple[float, float]]:
+    """(bytes, flops) of one launch of each softmax entry point: every tensor
+    crossing the op boundary once (int64 indices, fp32 values, transport orders 0..2)."""
+    return {
+        "softmax_forward": (E * (8 + 24 + 4 + 1 + 4 * H) + N * (8 * D + 8), E * 2.0 * D),
+        "softmax_backward": (E * (8 + 24 + 8 * H) + N * (16 * D + 8), E * 4.0 * D),
+    }
+
+
+def factored_cost(E: int, N: int, K: int, C: int, wc: int, d_out: int, n_f: int) -> dict[str, tuple[float, float]]:
+    """(bytes, flops) of one launch per head: h, the phase tables, rho, the
+    source grouping and the rows cross once; Z(j) once per node.  FLOPs: the
+    2 K C combination per edge (one K-long dot per packed column), the block
+    factors, the dZ and dh products in the backward."""
+    per_edge_in = 4 * (K - 1) + 2 * 8 * n_f + 4 + 8 + 8  # h, angular + transport, rho, order, source
+    z = N * 4 * K * C
+    return {
+        "factored_forward": (E * (per_edge_in + 4 * d_out) + z, E * (2.0 * K * C + 8 * wc)),
+        "factored_aggregate": (E * (4 * d_out + 4) + N * (4 * d_out + 8), E * 2.0 * d_out),
+        "factored_backward_aggregated": (E * (per_edge_in + 4 * d_out + 4 + 4 + 8 + 4 * (K - 1)) + N * 4 * d_out + 2 * z,
+                                         E * (4.0 * K * C + 8 * wc + 2 * d_out)),
+    }
+
+
+# ---------------------------------------------------------------- live op timing
+
+
+class OpTimer:
+    """Wraps the native entry points with HIP events on the launching stream."""
+
+    def __init__(self):
+        self.events = defaultdict(list)
+        self.enabled = False
+
+    def wrap(self, obj, name, label):
+        import torch
+
+        inner = getattr(obj, name)
+
+        def timed(*args, **kwargs):
+            if not self.enabled:
+                return inner(*args, **kwargs)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            out = inner(*args, **kwargs)
+            end.record()
+            self.events[label].append((start, end))
+            return out
+
+        setattr(obj, name, timed)
+
+    def summary(self, steps: int) -> dict[str, dict[str, float]]:
+        out = {}
+        for label, pairs in self.events.items():
+            times = [s.elapsed_time(e) for s, e in pairs]
+            out[label] = {"launches_per_step": len(times) / steps, "avg_ms": sum(times) / len(times),
+                          "ms_per_step": sum(times) / steps}
+        return out
+
+
+# ---------------------------------------------------------------- problem
+
+
+def build_edges(device):
     import torch
 
     from gm_attention_amd.discretization.edge_geometry import compute_edge_geometry
     from gm_attention_amd.discretization.frames import build_tangent_frames
     from gm_attention_amd.discretization.grid import build_equiangular_grid
-    from gm_attention_amd.nn import fused_attention
-    from gm_attention_amd.nn.fused_attention import plan_of
-    from gm_attention_amd.representations.field_type import SO2FieldType
 
     t0 = time.time()
     cutoff = 3.0 * math.pi / (NLAT - 1)
     grid = build_equiangular_grid(NLAT, NLON)
     edges = compute_edge_geometry(grid, build_tangent_frames(grid.nodes), cutoff)
     log(f"geometry {NLAT}x{NLON}: {edges.n_edges} edges per sample in {time.time() - t0:.1f}s")
-    n_sample = grid.n_nodes
-    single = edges.to(device, torch.float32)
-    tiled = single.tile(BATCH, n_sources=n_sample)
-    g = fused_attention.geometry(tiled, cutoff, "hard", torch.float32)
-    full = SO2FieldType(FIELD)
-    head = SO2FieldType({n: m // HEADS for n, m in FIELD.items()})
-    p = plan_of(head, full, HEADS)
-    desc = torch.tensor([list(r) for r in p.rows], dtype=torch.int64, device=device)
-    scale = 1.0 / math.sqrt(head.dimension)
-    return edges, g, p, desc, scale
+    tiled = edges.to(device, torch.float32).tile(BATCH, n_sources=grid.n_nodes)
+    return edges, tiled, cutoff
 
 
-def cpu_baseline(edges, p, scale, budget_edges: int = 2_000_000):
-    """The reference's own CPU arithmetic (oracle/_ref: nn/fused/attention.h's
-    node_softmax_forward/backward, serial, float32) on a bounded sample of the
-    same workload: targets 0..n_s of one sample (the pole and near-pole rows),
-    n_s chosen so the sample holds about ``budget_edges`` edges; seconds per
-    edge extrapolated to the whole step's edges."""
+def cpu_baseline_attention(edges, cutoff, mhsa_gpu, budget_edges: int):
+    """The eager restatement (oracle.modules, factored order as under
+    GM_FACTORED_KERNEL=1) of one SO2MHSA forward + backward in float32 on the
+    host's cores (at most 16 threads, one GPU's share of the box), over the
+    targets of a mixed sample of one 256x512 sample: the first (pole) targets
+    and whole equator rows.  The node-side work (projections, node products)
+    always covers one sample's 131,072 nodes; the edge-side work scales with
+    the sampled edges.  Two sample sizes (``budget_edges / 4`` and
+    ``budget_edges``) give both costs, extrapolated to the step's nodes and edges."""
     import torch
 
-    from oracle import ref
+    from gm_attention_amd.nn.attention import SO2MHSA
+    from gm_attention_amd.representations.field_type import SO2FeatureField
+    from oracle import modules
 
-    if not ref.available():
-        return None
-    row_ptr = edges.row_ptr.contiguous()
-    n_s = int(torch.searchsorted(row_ptr, torch.tensor(budget_edges)).item())
-    n_s = max(1, min(n_s, row_ptr.shape[0] - 1))
-    e_s = int(row_ptr[n_s])
-    N, D, H = row_ptr.shape[0] - 1, p.width, HEADS
-    gen = torch.Generator().manual_seed(0)
-    q = torch.randn(N, D, generator=gen)
-    k = torch.randn(N, D, generator=gen)
-    transport = torch.view_as_real(edges.transport_phases[:, :3].contiguous()).float().contiguous()
-    bias = torch.log(edges.tangent_quadrature_weights.float().clamp_min(torch.finfo(torch.float32).tiny)).contiguous()
-    inside = torch.ones(edges.n_edges, dtype=torch.uint8)
-    desc = torch.tensor([list(r) for r in p.rows], dtype=torch.int64)
-    source = edges.source_index.contiguous()
-    dalpha = torch.randn(edges.n_edges, H, generator=gen)
-    t0 = time.perf_counter()
-    alpha = ref.softmax_forward(q, k, transport, bias, inside, desc, row_ptr, source, H, scale, 0, n_s)
-    t1 = time.perf_counter()
-    ref.softmax_backward(dalpha, q, k, transport, desc, row_ptr, source, alpha, H, scale, 0, n_s)
-    t2 = time.perf_counter()
-    return dict(sample_edges=e_s, sample_targets=n_s, fwd_s=t1 - t0, bwd_s=t2 - t1)
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    row_ptr = edges.row_ptr
+    n = row_ptr.shape[0] - 1
+    mhsa = SO2MHSA(mhsa_gpu.field_type_in, HEADS, cutoff=cutoff, window="hard", batched=True, dtype=torch.float32)
+    mhsa.load_state_dict({k: v.detach().cpu() for k, v in mhsa_gpu.state_dict().items()})
+    fin = mhsa.field_type_in
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(n, fin.dimension, generator=gen).requires_grad_(True)
+    g = torch.randn(n, fin.dimension, generator=gen)
+
+    def sample(budget):
+        pole_last = max(1, int(torch.searchsorted(row_ptr, torch.tensor(budget // 2)).item()))
+        eq_first = (NLAT // 2) * NLON
+        eq_last = eq_first + NLON
+        while int(row_ptr[eq_last] - row_ptr[eq_first]) < budget // 2 and eq_last + NLON <= n:
+            eq_last += NLON
+        sel = torch.cat([torch.arange(int(row_ptr[a]), int(row_ptr[b])) for a, b in ((0, pole_last), (eq_first, eq_last))])
+        return edges.select(sel, n_nodes=n).to(None, torch.float32)
+
+    def step(sub):
+        xs = SO2FeatureField.from_flat(fin, x).coefficients
+        heads = []
+        for head in mhsa.heads:
+            q = modules.linear(head.query, xs, head.field_type_attn)
+            k = modules.linear(head.key, xs, head.field_type_attn)
+            alpha = modules.softmax_weights(q, k, sub, head.cutoff, head.window, 1, head._score_scale)[:, 0]
+            msgs = modules.factored_messages(head.value, xs, sub.source_index, sub.distances, sub.angular_phases,
+                                             sub.transport_phases)
+            heads.append({f: torch.segment_reduce(alpha.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum",
+                                                  offsets=sub.row_ptr, axis=0) for f, m in msgs.items()})
+        fused = {f: torch.cat([o[f] for o in heads], dim=-1 if f == 0 else -2) for f in fin.frequencies}
+        out = modules.flat(modules.linear(mhsa.output_projection, fused, fin))
+        (out * g).sum().backward()
+        x.grad = None
+        mhsa.zero_grad(set_to_none=True)
+
+    points = []
+    for budget in (budget_edges // 4, budget_edges):
+        sub = sample(budget)
+        step(sub)  # warm-up
+        t0 = time.perf_counter()
+        step(sub)
+        points.append((sub.n_edges, time.perf_counter() - t0))
+    (e1, t1), (e2, t2) = points
+    per_edge = (t2 - t1) / (e2 - e1)
+    per_sample_nodes = max(0.0, t1 - per_edge * e1)
+    return dict(per_edge=per_edge, per_sample_nodes=per_sample_nodes, points=points, threads=threads, cpu_s=t1 + t2)
 
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", choices=("attention", "softmax"), default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget-edges", type=int, default=200_000)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the hot path runs on one MI355X; "
-                                   "run with --gpus 1 (multi-GPU sharding is a design note, not built)"}))
+        print(json.dumps({"error": "this build measures one GPU only: every run here has one MI355X; "
+                                   "run with --gpus 1 (the multi-GPU sharding is a design note, not built)"}))
         sys.exit(2)
 
     import torch
 
-    from gm_attention_amd.nn import fused_attention
+    from gm_attention_amd import _native
+    from gm_attention_amd.nn import fused_attention, fused_factored
+    from gm_attention_amd.nn.attention import SO2MHSA
+    from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
 
     device = torch.device("cuda:0")
-    edges, g, p, desc, scale = build_problem(device)
-    N = g.row_ptr.shape[0] - 1
-    E = g.source.shape[0]
-    D = p.width
+    timer = OpTimer()
+    att, fac = _native.attention(), _native.factored()
+    for name in ("softmax_forward", "softmax_backward"):
+        timer.wrap(att, name, name)
+    timer.wrap(fac, "forward", "factored_forward")
+    timer.wrap(fac, "aggregate", "factored_aggregate")
+    timer.wrap(fac, "backward_aggregated", "factored_backward_aggregated")
+
+    edges_cpu, edges, cutoff = build_edges(device)
+    N = edges.row_ptr.shape[0] - 1
+    E = edges.n_edges
+    field = SO2FieldType(FIELD)
+    D = field.dimension
+    torch.manual_seed(0)
+    mhsa = SO2MHSA(field, HEADS, cutoff=cutoff, window="hard", batched=True, dtype=torch.float32, device=device)
     gen = torch.Generator(device=device).manual_seed(1)
-    q = torch.randn(N, D, device=device, generator=gen).requires_grad_(True)
-    k = torch.randn(N, D, device=device, generator=gen).requires_grad_(True)
-    dalpha = torch.randn(E, HEADS, device=device, generator=gen)
-    transport = g.transport_to(2)
+    x_flat = torch.randn(N, D, device=device, generator=gen).requires_grad_(True)
+    upstream = torch.randn(N, D, device=device, generator=gen)
+    g = fused_attention.geometry(edges, cutoff, "hard", torch.float32)
     log(f"problem: N={N} E={E} D={D} H={HEADS} max_degree={g.max_degree}")
 
-    def step(events=None):
-        if events is not None:
-            events[0].record()
-        alpha = fused_attention.Softmax.apply(q, k, transport, g.bias, g.inside, desc, g.row_ptr, g.source, HEADS,
-                                              scale, g.max_degree)
-        if events is not None:
-            events[1].record()
-        dq, dk = torch.autograd.grad(alpha, (q, k), dalpha)
-        if events is not None:
-            events[2].record()
-        return dq, dk
+    if args.workload == "attention":
+        def step():
+            x = SO2FeatureField.from_flat(field, x_flat)
+            y = mhsa(x, edges).to_flat()
+            torch.autograd.backward(y, upstream)
+        workload = ("SO2MHSA(batched) fwd+bwd: stacked Q/K projections, fused scores+softmax, 8 heads of node "
+                    "products + radial trunk + fused factored value aggregation, output projection; input and "
+                    "every parameter gradient")
+    else:
+        p = fused_attention.plan(mhsa)
+        desc = fused_attention.descriptors(mhsa, p, device)
+        scale = float(mhsa.heads[0]._score_scale)
+        q = torch.randn(N, D, device=device, generator=gen).requires_grad_(True)
+        k = torch.randn(N, D, device=device, generator=gen).requires_grad_(True)
+        dalpha = torch.randn(E, HEADS, device=device, generator=gen)
+        transport = g.transport_to(2)
+
+        def step():
+            alpha = fused_attention.Softmax.apply(q, k, transport, g.bias, g.inside, desc, g.row_ptr, g.source, HEADS,
+                                                  scale, g.max_degree)
+            torch.autograd.backward(alpha, dalpha)
+        workload = "Softmax.apply fwd+bwd: neighbourhood scores + softmax over CSR (gauge-transported keys)"
 
     for _ in range(args.warmup):
         step()
+        mhsa.zero_grad(set_to_none=True)
+        x_flat.grad = None
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
+    timer.enabled = True
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(events[i])
+    for _ in range(args.steps):
+        step()
+        mhsa.zero_grad(set_to_none=True)
+        x_flat.grad = None
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    timer.enabled = False
     ms_per_step = 1e3 * elapsed / args.steps
-    log(f"step {ms_per_step:.3f} ms (forward {fwd_ms:.3f} ms, backward {bwd_ms:.3f} ms)")
+    ops = timer.summary(args.steps)
+    log(f"step {ms_per_step:.2f} ms; ops: " + ", ".join(f"{k} {v['ms_per_step']:.2f} ms" for k, v in ops.items()))
 
-    fwd_b, bwd_b = softmax_bytes(E, N, D, HEADS)
-    gpu_ms = fwd_ms + bwd_ms
-    achieved = (fwd_b + bwd_b) / (gpu_ms * 1e-3) / 1e9
-    traffic = None
-    traffic_file = ROOT / "profiles" / "softmax_ns_traffic.json"
-    if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get("bytes_per_step")
+    costs = softmax_cost(E, N, D, HEADS)
+    kern = mhsa.heads[0].value
+    fp = fused_factored.plan(kern)
+    K = kern.complex_head.in_features + 1
+    costs.update(factored_cost(E, N, K, 2 * fp.wc + fp.wr, fp.wc, fp.d_out, 5))
+    dominant = max(ops, key=lambda k: ops[k]["ms_per_step"])
+    nbytes, flops = costs[dominant]
+    avg_s = ops[dominant]["avg_ms"] * 1e-3
+    if dominant.startswith("softmax") or dominant == "factored_aggregate":
+        roof = {"bound": "hbm", "achieved": nbytes / avg_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    else:
+        roof = {"bound": "mfma", "achieved": flops / avg_s / 1e12, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    traffic_file = ROOT / "profiles" / f"{dominant}_ns_traffic.json"
+    roof["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch") if traffic_file.exists() else None
+    roof["kernel"] = dominant
+    roof["algorithmic_per_launch"] = {"bytes": nbytes, "flops": flops}
+    op_rates = {}
+    for name, v in ops.items():
+        b, f = costs[name]
+        op_rates[name] = {**{k: round(x, 4) for k, x in v.items()}, "GB/s": b / (v["avg_ms"] * 1e-3) / 1e9,
+                          "TFLOP/s": f / (v["avg_ms"] * 1e-3) / 1e12}
 
     baseline = None
-    if not args.no_cpu_baseline:
-        b = cpu_baseline(edges, p, scale)
-        if b is not None:
-            per_edge = (b["fwd_s"] + b["bwd_s"]) / b["sample_edges"]
-            cpu_step_s = per_edge * E
-            baseline = {
-                "value": N / cpu_step_s, "unit": "query-points/s", "cores": 1, "kind": "reference",
-                "sample": (f"reference nn/fused/attention.h node_softmax_forward+backward (serial, float32) over "
-                           f"targets 0..{b['sample_targets']} of one 256x512 sample ({b['sample_edges']} edges, "
-                           f"{b['fwd_s'] + b['bwd_s']:.2f}s), extrapolated per edge to {E} edges"),
-            }
-            log(f"cpu baseline: {baseline['value']:.0f} qp/s ({b['fwd_s']:.2f}s fwd + {b['bwd_s']:.2f}s bwd sample)")
+    if not args.no_cpu_baseline and args.workload == "attention":
+        b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges)
+        cpu_step = b["per_sample_nodes"] * BATCH + b["per_edge"] * E
+        (e1, t1), (e2, t2) = b["points"]
+        baseline = {"value": N / cpu_step, "unit": "query-points/s", "cores": b["threads"], "kind": "port",
+                    "sample": (f"oracle eager SO2MHSA fwd+bwd (factored order, float32, torch on {b['threads']} "
+                               f"threads) on one 256x512 sample's nodes with the edges of its first (pole) targets "
+                               f"and equator rows: {e1} edges in {t1:.2f}s, {e2} edges in {t2:.2f}s; the fit "
+                               f"{b['per_sample_nodes']:.2f}s per sample's nodes + {b['per_edge'] * 1e6:.1f}us per "
+                               f"edge, extrapolated to {BATCH} samples and {E} edges")}
+        log(f"cpu baseline: {baseline['value']:.1f} qp/s ({baseline['sample']})")
 
     line = {
         "metric": "attn fwd+bwd query-points/s at 256x512 B=4",
@@ -196,20 +326,12 @@ def main() -> None:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: N(0,1) q, k and upstream gradient on the equiangular grid geometry",
-        "config": {
-            "workload": "Softmax.apply fwd+bwd: neighbourhood scores + softmax over CSR (gauge-transported keys)",
-            "grid": f"{NLAT}x{NLON} equiangular", "batch": BATCH, "field": "{0:32,1:32,2:32}", "heads": HEADS,
-            "radius": "3 row spacings", "window": "hard", "query_points": N, "edges": E,
-            "max_degree": g.max_degree,
-        },
-        "roofline": {
-            "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-            "kernel": "softmax step: forward + backward (per-target and per-source passes)",
-            "algorithmic_bytes": fwd_b + bwd_b,
-        },
-        "kernels_ms": {"softmax_forward": fwd_ms, "softmax_backward": bwd_ms},
+        "data": "synthetic: N(0,1) input field and upstream gradient, random-init weights, equiangular grid geometry",
+        "config": {"workload": workload, "grid": f"{NLAT}x{NLON} equiangular", "batch": BATCH,
+                   "field": "{0:32,1:32,2:32}", "heads": HEADS, "radius": "3 row spacings", "window": "hard",
+                   "query_points": N, "edges": E, "max_degree": g.max_degree},
+        "roofline": roof,
+        "ops": op_rates,
         "cpu_baseline": baseline,
     }
     print(json.dumps(line))
