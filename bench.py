@@ -223,6 +223,10 @@ def main() -> None:
     timer.wrap(fac, "forward", "factored_forward")
     timer.wrap(fac, "aggregate", "factored_aggregate")
     timer.wrap(fac, "backward_aggregated", "factored_backward_aggregated")
+    timer.wrap(_native, "factored_forward_seg", "factored_forward")
+    timer.wrap(_native, "factored_backward_seg", "factored_backward_aggregated")
+    timer.wrap(_native, "radial_trunk_forward", "radial_trunk_forward")
+    timer.wrap(_native, "radial_trunk_backward", "radial_trunk_backward")
 
     edges_cpu, edges, cutoff = build_edges(device)
     N = edges.row_ptr.shape[0] - 1
@@ -283,10 +287,13 @@ def main() -> None:
     fp = fused_factored.plan(kern)
     K = kern.complex_head.in_features + 1
     costs.update(factored_cost(E, N, K, 2 * fp.wc + fp.wr, fp.wc, fp.d_out, 5))
+    # the radial trunk for all heads: rho in, h (H, E, T) out; 2 T B + ~20 T FLOPs per edge and head
+    costs["radial_trunk_forward"] = (E * (4 + HEADS * 4 * (K - 1)), E * HEADS * (2.0 * (K - 1) * 8 + 20 * (K - 1)))
+    costs["radial_trunk_backward"] = (E * (4 + HEADS * 4 * (K - 1)), E * HEADS * (4.0 * (K - 1) * 8 + 30 * (K - 1)))
     dominant = max(ops, key=lambda k: ops[k]["ms_per_step"])
     nbytes, flops = costs[dominant]
     avg_s = ops[dominant]["avg_ms"] * 1e-3
-    if dominant.startswith("softmax") or dominant == "factored_aggregate":
+    if dominant.startswith(("softmax", "radial")) or dominant == "factored_aggregate":
         roof = {"bound": "hbm", "achieved": nbytes / avg_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     else:
         roof = {"bound": "mfma", "achieved": flops / avg_s / 1e12, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s"}

@@ -31,14 +31,26 @@ namespace gm {
 namespace {
 
 struct Block {
-  int kind, zoff, bm, ang, tr, power, ooff, take_real;
+  int16_t kind, zoff, bm, ang, tr, power, ooff, take_real;
+};
+
+// One run of the packed mix columns [c0, c0 + width) of every node: column
+// c of node j at mix t sits at z[j * node_stride + t * t_stride + (c - c0)]
+// (and its gradient at the same place of dz).  The reference's zc
+// (n_nodes, K, wc, 2) and zr (n_nodes, K, wr) are the two-run case.
+template <typename T>
+struct ZSeg {
+  const T* z;
+  T* dz;
+  int64_t node_stride;
+  int t_stride, c0, width;
 };
 
 template <typename T>
 struct FactArgs {
   const T* h;          // (n_edges, K - 1)
-  const T* zc;         // (n_nodes, K, wc, 2)
-  const T* zr;         // (n_nodes, K, wr)
+  ZSeg<T> seg[GM_FACT_MAX_SEG];
+  int n_seg;
   const T* angular;    // (n_edges, n_f, 2)
   const T* transport;  // (n_edges, n_f, 2)
   const T* rho;        // (n_edges,)
@@ -52,13 +64,27 @@ struct FactArgs {
   const T* weights;       // aggregated form or null
   const T* rows;          // aggregated form or null
   T* dh;
-  T* dzc;
-  T* dzr;
   T* dweights;
   int64_t n_groups;
   int K, wc, wr, C, KP, CP, n_f, n_blocks, d_out;
   int tile;  // backward: edges per LDS tile (a power of two <= 64)
+  int real_ooff;  // the real block's output offset (when wr > 0)
   Block desc[GM_FACT_MAX_BLOCKS];
+  uint8_t cmap[GM_FACT_MAX_C / 2];  // complex column -> its block
+  // MFMA path tables (C <= 128): per packed column, block | g index of the
+  // real part << 8 | of the imaginary part (0xFF: none) << 16 | kind << 24
+  // (0 real block, 1 real part, 2 imaginary part); per output slot the
+  // V columns it sums, in descriptor order (optr offsets into olist).
+  uint32_t colinfo[128];
+  uint8_t optr[GM_FACT_MAX_OUT + 1];
+  uint8_t olist[128];
+  // source-grouped streams (row g is the edge order[g]): the phase pairs
+  // (angular orders 0..pa-1, then transport orders 0..pt-1, 16 floats a row),
+  // r / cutoff and the edge's target
+  const float* phase_g;
+  const float* rho_g;
+  const int64_t* target_g;
+  int pa, pt;
 };
 
 template <typename T>
@@ -85,17 +111,33 @@ __device__ __forceinline__ void block_factor(const FactArgs<T>& a, int64_t e, co
   fi *= s;
 }
 
+template <typename T>
+__device__ __forceinline__ int seg_of(const FactArgs<T>& a, int c) {
+  int s = 0;
+  while (s + 1 < a.n_seg && c >= a.seg[s + 1].c0) ++s;
+  return s;
+}
+
+// Z_t(j) at packed column c (zero past K or C).
+template <typename T>
+__device__ __forceinline__ T zget(const FactArgs<T>& a, int64_t j, int t, int c) {
+  if (t >= a.K || c >= a.C) return T(0);
+  const ZSeg<T>& g = a.seg[seg_of(a, c)];
+  return g.z[j * g.node_stride + (int64_t)t * g.t_stride + (c - g.c0)];
+}
+
+template <typename T>
+__device__ __forceinline__ void zput(const FactArgs<T>& a, int64_t j, int t, int c, T v) {
+  const ZSeg<T>& g = a.seg[seg_of(a, c)];
+  g.dz[j * g.node_stride + (int64_t)t * g.t_stride + (c - g.c0)] = v;
+}
+
 // Z(j) into LDS as Zt[c * KP + t] (t >= K padded with zeros).
 template <typename T>
 __device__ __forceinline__ void stage_mixes(const FactArgs<T>& a, int64_t j, T* Zt, int lane) {
-  const int wc2 = 2 * a.wc;
-  const T* zc = a.zc + j * (int64_t)a.K * wc2;
-  const T* zr = a.zr + j * (int64_t)a.K * a.wr;
   for (int idx = lane; idx < a.KP * a.C; idx += kWave) {
     const int t = idx / a.C, c = idx - t * a.C;
-    T v = T(0);
-    if (t < a.K) v = c < wc2 ? zc[t * wc2 + c] : zr[t * a.wr + (c - wc2)];
-    Zt[c * a.KP + t] = v;
+    Zt[c * a.KP + t] = zget(a, j, t, c);
   }
 }
 
@@ -202,6 +244,7 @@ struct AggArgs {
   const T* weights;
   const int64_t* row_ptr;
   T* out;
+  const int64_t* inv;  // null: edge e's row is rows[e]; else rows[inv[e]] (rows kept in another order)
   int64_t n_targets;
   int d_out, S;  // S edge slots of d_out lanes each (S = 1: lanes stride the columns)
 };
@@ -217,7 +260,7 @@ __global__ __launch_bounds__(256) void aggregate_kernel(AggArgs<T> a) {
   if (a.S == 1) {
     for (int c = lane; c < a.d_out; c += kWave) {
       T s = T(0);
-      for (int64_t e = e0; e < e1; ++e) s += a.weights[e] * a.rows[e * a.d_out + c];
+      for (int64_t e = e0; e < e1; ++e) s += a.weights[e] * a.rows[(a.inv ? a.inv[e] : e) * a.d_out + c];
       o[c] = s;
     }
     return;
@@ -225,7 +268,7 @@ __global__ __launch_bounds__(256) void aggregate_kernel(AggArgs<T> a) {
   const int c = lane % a.d_out, slot = lane / a.d_out;
   T s = T(0);
   if (slot < a.S)
-    for (int64_t e = e0 + slot; e < e1; e += a.S) s += a.weights[e] * a.rows[e * a.d_out + c];
+    for (int64_t e = e0 + slot; e < e1; e += a.S) s += a.weights[e] * a.rows[(a.inv ? a.inv[e] : e) * a.d_out + c];
   s = group_sum(s, lane, a.d_out, a.S);
   if (slot == 0) o[c] = s;
 }
@@ -317,28 +360,656 @@ __global__ __launch_bounds__(64) void factored_backward_kernel(FactArgs<T> a) {
     }
     __syncthreads();
   }
-  T* dzc = a.dzc + j * (int64_t)a.K * wc2;
-  T* dzr = a.dzr + j * (int64_t)a.K * a.wr;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int c = lane + kWave * q;
     if (c < a.C) {
 #pragma unroll
       for (int t = 0; t < KMAX; ++t)
-        if (t < a.K) {
-          if (c < wc2)
-            dzc[t * wc2 + c] = acc[q][t];
-          else
-            dzr[t * a.wr + (c - wc2)] = acc[q][t];
-        }
+        if (t < a.K) zput(a, j, t, c, acc[q][t]);
     }
+  }
+}
+
+// -------------------------------------------------------- MFMA (fp32, K <= 17)
+//
+// With h~ = (1, h) and T = K - 1 <= 16 trunk features, every source group's
+// products are 16-deep matrix products on v_mfma_f32_16x16x4f32 (lane l
+// supplies A[l % 16][l / 16] and B[l / 16][l % 16] and holds
+// D[4 (l / 16) + r][l % 16]), 16 edges at a time:
+//   forward   P^T (C x 16 edges) = Z_{1..16}^T (C x 16) H^T (16 x 16 edges), plus Z_0;
+//   backward  dh (16 edges x 16)  = W (16 edges x C) Z_{1..16}^T (C x 16),
+//             dZ_{1..16} (16 x C) += H^T (16 x 16 edges) W (16 edges x C),
+//             dZ_0 (C)           += the column sums of W.
+// The k index of the forward's product runs over the trunk features as
+// t - 1 = 4 (l / 16) + s, so a lane's slice of h(e) is one 16-byte load.
+// The source's Z(j) lives in registers for the whole group; the tile's edge
+// phases, factors, gradient rows and W go through LDS; every output slot sums
+// its blocks in descriptor order (host-built lists), so results do not
+// depend on scheduling.
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMT = 16;  // edges per MFMA tile
+
+// The MFMA kernels run one wave per workgroup, and a wave's LDS operations
+// execute in order, so handing LDS data between its lanes needs only a
+// compiler-level ordering point: a wavefront-scope release/acquire pair (no
+// wait on outstanding global loads or stores, which __syncthreads' workgroup
+// fences would add).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+
+
+// The tile's edge ids (zero past n) into eid, the edges' rho and phase rows
+// (angular then transport, 4 n_f floats) into LDS, and then every block's
+// factor F[e][b] from them.
+// Z(j) into LDS as Zs[t * ZP + c] for t < 17 (zero past K and past C).  Lane
+// l owns the elements l, l + 64, ... of the 17 x CV block: it issues every
+// load first (a fixed, unrolled count), so they are all in flight at once,
+// and then writes them; its run is a short uniform-bound search.
+template <int NT>
+__device__ __forceinline__ void stage_z(const FactArgs<float>& a, int64_t j, float* Zs, int lane) {
+  constexpr int CV = 16 * NT, ZP = CV + 4, PER = (17 * CV + kWave - 1) / kWave;
+  float v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int idx = lane + kWave * i;
+    const int t = idx / CV, c = idx - t * CV;
+    v[i] = 0.f;
+    if (t < a.K && c < a.C) {
+      int r = 0;
+#pragma unroll
+      for (int k = 1; k < GM_FACT_MAX_SEG; ++k)
+        if (k < a.n_seg && c >= a.seg[k].c0) r = k;
+      const ZSeg<float>& g = a.seg[r];
+      v[i] = g.z[j * g.node_stride + (int64_t)t * g.t_stride + (c - g.c0)];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int idx = lane + kWave * i;
+    const int t = idx / CV, c = idx - t * CV;
+    if (t < 17) Zs[t * ZP + c] = v[i];
+  }
+}
+
+// dZ(j) from LDS Ds[t * zp + c] to the runs' gradient arrays.
+__device__ __forceinline__ void store_dz(const FactArgs<float>& a, int64_t j, const float* Ds, int zp, int lane) {
+  for (int r = 0; r < a.n_seg; ++r) {
+    const ZSeg<float>& g = a.seg[r];
+    float* dst = g.dz + j * g.node_stride;
+    for (int t = 0; t < a.K; ++t)
+      for (int c = lane; c < g.width; c += kWave) dst[(int64_t)t * g.t_stride + c] = Ds[t * zp + g.c0 + c];
+  }
+}
+
+// The descriptor rows into LDS (a lane-indexed table; kernel arguments read
+// with a per-lane index would be fetched from memory each time).
+__device__ __forceinline__ void stage_desc(const FactArgs<float>& a, Block* Ds, int lane) {
+  for (int b = lane; b < a.n_blocks; b += kWave) Ds[b] = a.desc[b];
+}
+
+__device__ __forceinline__ void stage_edges(const FactArgs<float>& a, int64_t base, int n, int64_t* eid, int lane) {
+  if (lane < kMT) eid[lane] = lane < n ? a.order[base + lane] : 0;
+}
+
+__device__ __forceinline__ void stage_phases(const FactArgs<float>& a, const int64_t* eid, int n, float* Ph, float* Rh,
+                                             int m, int q) {
+  const int w = 4 * a.n_f, half = 2 * a.n_f;
+  for (int e = q; e < kMT; e += 4) {
+    const int64_t ee = eid[e];
+    for (int k = m; k < w; k += kMT) {
+      float v = 0.f;
+      if (e < n) v = k < half ? a.angular[ee * half + k] : a.transport[ee * half + (k - half)];
+      Ph[e * w + k] = v;
+    }
+  }
+  if (q == 0) Rh[m] = m < n ? a.rho[eid[m]] : 0.f;
+}
+
+__device__ __forceinline__ void stage_factors(const FactArgs<float>& a, const Block* Bd, const float* Ph,
+                                              const float* Rh, float* Ft, int lane) {
+  const int nb = a.n_blocks, w = 4 * a.n_f, half = 2 * a.n_f;
+  for (int idx = lane; idx < kMT * nb; idx += kWave) {
+    const int e = idx & (kMT - 1), b = idx >> 4;
+    const Block d = Bd[b];
+    const float* ph = Ph + e * w;
+    float fr = 1.f, fi = 0.f;
+    if (d.ang != 0) {
+      const int o = d.ang < 0 ? -d.ang : d.ang;
+      fr = ph[2 * o];
+      fi = d.ang < 0 ? -ph[2 * o + 1] : ph[2 * o + 1];
+    }
+    if (d.tr != 0) {
+      const int o = d.tr < 0 ? -d.tr : d.tr;
+      const float pr = ph[half + 2 * o], pi = d.tr < 0 ? -ph[half + 2 * o + 1] : ph[half + 2 * o + 1];
+      const float nr = fr * pr - fi * pi, ni = fr * pi + fi * pr;
+      fr = nr;
+      fi = ni;
+    }
+    float sc = 1.f;
+    for (int i = 0; i < d.power; ++i) sc *= Rh[e];
+    Ft[2 * (e * nb + b)] = fr * sc;
+    Ft[2 * (e * nb + b) + 1] = fi * sc;
+  }
+}
+
+template <int NT>
+__global__ __launch_bounds__(64) void factored_forward_mfma(FactArgs<float> a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb = a.n_blocks, CV = 16 * NT, VP = CV + 1, wc2 = 2 * a.wc, d_out = a.d_out;
+  constexpr int ZP = 16 * NT + 4;
+  int64_t* eid = reinterpret_cast<int64_t*>(smem);  // [kMT]
+  Block* Bd = reinterpret_cast<Block*>(eid + kMT);  // [nb]
+  float* Rh = reinterpret_cast<float*>(Bd + GM_FACT_MAX_BLOCKS);  // [kMT]
+  float* Ph = Rh + kMT;                             // [kMT][4 n_f]
+  float* Ft = Ph + kMT * 4 * a.n_f;                 // [kMT][nb][2]
+  float* Vt = Ft + kMT * nb * 2;                    // [kMT][VP]
+  float* Zs = Vt + kMT * VP;                        // [17][ZP]
+  uint8_t* optr = reinterpret_cast<uint8_t*>(Zs + 17 * ZP);  // [d_out + 1]
+  uint8_t* olist = optr + GM_FACT_MAX_OUT + 1;                // [optr[d_out]]
+  const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
+  for (int i = lane; i <= d_out; i += kWave) optr[i] = a.optr[i];
+  for (int i = lane; i < a.optr[d_out]; i += kWave) olist[i] = a.olist[i];
+  stage_desc(a, Bd, lane);
+  const int64_t gi = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t j = a.group_source[gi];
+  const int64_t g0 = a.group_ptr[gi], g1 = a.group_ptr[gi + 1];
+  stage_z<NT>(a, j, Zs, lane);
+  wave_sync();
+  float za[NT][4], z0[NT][4];
+  int vb[NT][2];  // the block of each complex column pair this lane holds (-1: real block or padding)
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      za[nt][s] = Zs[(1 + 4 * q + s) * ZP + 16 * nt + m];
+      z0[nt][s] = Zs[16 * nt + 4 * q + s];
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int c = 16 * nt + 4 * q + 2 * p;
+      vb[nt][p] = c < wc2 ? (int)a.cmap[c >> 1] : -1;
+    }
+  }
+  for (int64_t base = g0; base < g1; base += kMT) {
+    const int n = (int)((g1 - base) < kMT ? (g1 - base) : kMT);
+    stage_edges(a, base, n, eid, lane);
+    wave_sync();
+    floatx4 hv = floatx4{0.f, 0.f, 0.f, 0.f};  // h(e = m)[t - 1 = 4 q + s]
+    if (m < n) {
+      const float* he = a.h + eid[m] * (a.K - 1);
+      if (a.K == 17) {
+        hv = *reinterpret_cast<const floatx4*>(he + 4 * q);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) hv[s] = 4 * q + s + 1 < a.K ? he[4 * q + s] : 0.f;
+      }
+    }
+    stage_phases(a, eid, n, Ph, Rh, m, q);
+    floatx4 acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], hv[s], acc[nt]);
+    wave_sync();
+    stage_factors(a, Bd, Ph, Rh, Ft, lane);
+    wave_sync();
+    // V = F (P + Z_0) on the complex columns, P + Z_0 on the real block's
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int c = 16 * nt + 4 * q + 2 * p;
+        const float ur = acc[nt][2 * p] + z0[nt][2 * p], ui = acc[nt][2 * p + 1] + z0[nt][2 * p + 1];
+        float vr = ur, vi = ui;
+        if (vb[nt][p] >= 0) {
+          const float* f = Ft + 2 * (m * nb + vb[nt][p]);
+          vr = f[0] * ur - f[1] * ui;
+          vi = f[0] * ui + f[1] * ur;
+        }
+        Vt[m * VP + c] = vr;
+        Vt[m * VP + c + 1] = vi;
+      }
+    wave_sync();
+    for (int e = q; e < n; e += 4) {
+      const float* v = Vt + e * VP;
+      float* row = a.out + eid[e] * d_out;
+      for (int o = m; o < d_out; o += kMT) {
+        float sum = 0.f;
+        for (int k = optr[o]; k < optr[o + 1]; ++k) sum += v[olist[k]];
+        row[o] = sum;
+      }
+    }
+    wave_sync();
+  }
+}
+
+template <int NT>
+__global__ __launch_bounds__(64) void factored_backward_mfma(FactArgs<float> a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb = a.n_blocks, CV = 16 * NT, WP = CV + 1, wc2 = 2 * a.wc, d_out = a.d_out;
+  constexpr int ZP = 16 * NT + 4;
+  int64_t* eid = reinterpret_cast<int64_t*>(smem);  // [kMT]
+  Block* Bd = reinterpret_cast<Block*>(eid + kMT);  // [nb]
+  float* Rh = reinterpret_cast<float*>(Bd + GM_FACT_MAX_BLOCKS);  // [kMT]
+  float* St = Rh + kMT;                             // [kMT] the edges' weights
+  float* Ph = St + kMT;                             // [kMT][4 n_f]
+  float* Ft = Ph + kMT * 4 * a.n_f;                 // [kMT][nb][2]
+  float* Gt = Ft + kMT * nb * 2;                    // [kMT][d_out] the edges' output gradients (unscaled)
+  float* Wt = Gt + kMT * d_out;                     // [kMT][WP]
+  float* Ht = Wt + kMT * WP;                        // [kMT][16]
+  float* Zs = Ht + kMT * 16;                        // [17][ZP] Z(j), then dZ(j)
+  const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
+  stage_desc(a, Bd, lane);
+  const int64_t gi = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t j = a.group_source[gi];
+  const int64_t g0 = a.group_ptr[gi], g1 = a.group_ptr[gi + 1];
+  stage_z<NT>(a, j, Zs, lane);
+  wave_sync();
+  float zb[4 * NT];  // B operand of dh: Z[t = 1 + m][c = q + 4 s]
+#pragma unroll
+  for (int s = 0; s < 4 * NT; ++s) zb[s] = Zs[(1 + m) * ZP + q + 4 * s];
+  uint32_t ci[NT];  // this lane's columns c = 16 nt + m: block | gre << 8 | gim << 16 | kind << 24
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) ci[nt] = 16 * nt + m < a.C ? a.colinfo[16 * nt + m] : 0xFFFFFFFFu;
+  floatx4 dz[NT];
+  float dz0[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    dz[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    dz0[nt] = 0.f;
+  }
+  for (int64_t base = g0; base < g1; base += kMT) {
+    const int n = (int)((g1 - base) < kMT ? (g1 - base) : kMT);
+    stage_edges(a, base, n, eid, lane);
+    if (lane < kMT) St[lane] = (lane < n && a.weights) ? a.weights[a.order[base + lane]] : 1.f;
+    wave_sync();
+    for (int e = q; e < kMT; e += 4) {
+      const float* grow = e < n ? (a.target ? a.g + a.target[eid[e]] * d_out : a.g + eid[e] * d_out) : nullptr;
+      for (int o = m; o < d_out; o += kMT) Gt[e * d_out + o] = grow ? grow[o] : 0.f;
+    }
+    {
+      const int e = lane >> 2, part = lane & 3;  // one 16-byte slice of one edge's h
+      floatx4 hv = floatx4{0.f, 0.f, 0.f, 0.f};
+      if (e < n) {
+        const float* he = a.h + eid[e] * (a.K - 1);
+        if (a.K == 17) {
+          hv = *reinterpret_cast<const floatx4*>(he + 4 * part);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) hv[s] = 4 * part + s + 1 < a.K ? he[4 * part + s] : 0.f;
+        }
+      }
+      *reinterpret_cast<floatx4*>(Ht + e * 16 + 4 * part) = hv;
+    }
+    stage_phases(a, eid, n, Ph, Rh, m, q);
+    wave_sync();
+    stage_factors(a, Bd, Ph, Rh, Ft, lane);
+    wave_sync();
+    if (a.dweights && lane < n) {
+      const float* r = a.rows + eid[lane] * d_out;
+      const float* gr = Gt + lane * d_out;
+      float sum = 0.f;
+      for (int o = 0; o < d_out; ++o) sum += gr[o] * r[o];
+      a.dweights[eid[lane]] = sum;
+    }
+    // W[e = q + 4 i][c = 16 nt + m] = w_e G conj(F) (complex) or w_e G (real block)
+    float w[NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const uint32_t info = ci[nt];
+      const int b = info & 0xFF, gre = (info >> 8) & 0xFF, gim = (info >> 16) & 0xFF, kind = info >> 24;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = q + 4 * i;
+        float v = 0.f;
+        if (info != 0xFFFFFFFFu) {
+          const float* gr = Gt + e * d_out;
+          const float g_re = gr[gre], g_im = gim == 0xFF ? 0.f : gr[gim];
+          if (kind == 0) {
+            v = g_re;
+          } else {
+            const float* f = Ft + 2 * (e * nb + b);
+            v = kind == 1 ? g_re * f[0] + g_im * f[1] : g_im * f[0] - g_re * f[1];
+          }
+          v *= St[e];
+        }
+        w[nt][i] = v;
+        Wt[e * WP + 16 * nt + m] = v;
+      }
+    }
+    wave_sync();
+    // dh (16 edges x 16 t) = W Z^T: lane holds dh[e = 4 q + r][t = 1 + m]
+    floatx4 dh = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4 * NT; ++s) dh = mfma16(Wt[m * WP + q + 4 * s], zb[s], dh);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = 4 * q + r;
+      if (e < n && m + 1 < a.K) a.dh[eid[e] * (a.K - 1) + m] = dh[r];
+    }
+    // dZ_{1..16} += H^T W (W straight from this lane's registers); dZ_0 += column sums
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dz[nt] = mfma16(Ht[(q + 4 * i) * 16 + m], w[nt][i], dz[nt]);
+        dz0[nt] += w[nt][i];
+      }
+    wave_sync();
+  }
+  // dZ(j) through LDS (Zs is free again) to the runs' gradient arrays
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    dz0[nt] += __shfl_xor(dz0[nt], 16, kWave);
+    dz0[nt] += __shfl_xor(dz0[nt], 32, kWave);
+    const int c = 16 * nt + m;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Zs[(1 + 4 * q + r) * ZP + c] = dz[nt][r];
+    if (q == 0) Zs[c] = dz0[nt];
+  }
+  wave_sync();
+  store_dz(a, j, Zs, ZP, lane);
+}
+
+// ------------------------------------------------ MFMA over source-grouped streams
+//
+// The same products as above with every per-edge stream already in source
+// order (row g of h, the phases, rho, the rows, dh and dweights is the g-th
+// edge of the grouping): a tile's loads are contiguous and their addresses
+// are known before the tile starts, so the next tile's loads are issued
+// while the current one computes.  Only the backward's target gradient
+// rows are gathered (through target_g).
+
+constexpr int kPhaseRow = 16;  // floats per grouped phase row (8 pairs)
+
+__device__ __forceinline__ void factors_grouped(const FactArgs<float>& a, const Block* Bd, const float* Ph,
+                                                const float* Rh, float* Ft, int lane) {
+  const int nb = a.n_blocks;
+  for (int idx = lane; idx < kMT * nb; idx += kWave) {
+    const int e = idx & (kMT - 1), b = idx >> 4;
+    const Block d = Bd[b];
+    const float* ph = Ph + e * kPhaseRow;
+    float fr = 1.f, fi = 0.f;
+    if (d.ang != 0) {
+      const int o = d.ang < 0 ? -d.ang : d.ang;
+      fr = ph[2 * o];
+      fi = d.ang < 0 ? -ph[2 * o + 1] : ph[2 * o + 1];
+    }
+    if (d.tr != 0) {
+      const int o = a.pa + (d.tr < 0 ? -d.tr : d.tr);
+      const float pr = ph[2 * o], pi = d.tr < 0 ? -ph[2 * o + 1] : ph[2 * o + 1];
+      const float nr = fr * pr - fi * pi, ni = fr * pi + fi * pr;
+      fr = nr;
+      fi = ni;
+    }
+    float sc = 1.f;
+    for (int i = 0; i < d.power; ++i) sc *= Rh[e];
+    Ft[2 * (e * nb + b)] = fr * sc;
+    Ft[2 * (e * nb + b) + 1] = fi * sc;
+  }
+}
+
+struct TileIn {
+  floatx4 h;    // this lane's slice of h: forward h(g = base + m)[4 q .. 4 q + 3]; backward h(base + l / 4)[4 (l % 4) ..]
+  floatx4 ph;   // phase row of edge base + l / 4, floats 4 (l % 4) .. + 3
+  float rho;    // rho of edge base + l (l < 16)
+  float w;      // backward: the weight of edge base + l
+  int64_t tgt;  // backward: the target of edge base + l
+};
+
+template <bool BACKWARD>
+__device__ __forceinline__ TileIn load_tile(const FactArgs<float>& a, int64_t base, int n, int lane) {
+  const int m = lane & 15, q = lane >> 4, e4 = lane >> 2, part = lane & 3;
+  TileIn t;
+  t.h = floatx4{0.f, 0.f, 0.f, 0.f};
+  t.ph = floatx4{0.f, 0.f, 0.f, 0.f};
+  t.rho = 0.f;
+  t.w = 0.f;
+  t.tgt = 0;
+  if (!BACKWARD) {
+    if (m < n) t.h = *reinterpret_cast<const floatx4*>(a.h + (base + m) * 16 + 4 * q);
+  } else {
+    if (e4 < n) t.h = *reinterpret_cast<const floatx4*>(a.h + (base + e4) * 16 + 4 * part);
+  }
+  if (e4 < n) t.ph = *reinterpret_cast<const floatx4*>(a.phase_g + (base + e4) * kPhaseRow + 4 * part);
+  if (lane < n) {
+    t.rho = a.rho_g[base + lane];
+    if (BACKWARD) {
+      t.w = a.weights[base + lane];
+      t.tgt = a.target_g[base + lane];
+    }
+  }
+  return t;
+}
+
+template <int NT>
+__global__ __launch_bounds__(64) void factored_forward_grouped(FactArgs<float> a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb = a.n_blocks, CV = 16 * NT, VP = CV + 1, wc2 = 2 * a.wc, d_out = a.d_out;
+  Block* Bd = reinterpret_cast<Block*>(smem);                      // [nb]
+  float* Ph = reinterpret_cast<float*>(Bd + GM_FACT_MAX_BLOCKS);   // [kMT][kPhaseRow]
+  float* Rh = Ph + kMT * kPhaseRow;                                // [kMT]
+  float* Ft = Rh + kMT;                                            // [kMT][nb][2]
+  float* Vt = Ft + kMT * nb * 2;                                   // [kMT][VP]
+  uint8_t* optr = reinterpret_cast<uint8_t*>(Vt + kMT * VP);       // [d_out + 1]
+  uint8_t* olist = optr + GM_FACT_MAX_OUT + 1;
+  const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
+  for (int i = lane; i <= d_out; i += kWave) optr[i] = a.optr[i];
+  for (int i = lane; i < a.optr[d_out]; i += kWave) olist[i] = a.olist[i];
+  stage_desc(a, Bd, lane);
+  const int64_t gi = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t j = a.group_source[gi];
+  const int64_t g0 = a.group_ptr[gi], g1 = a.group_ptr[gi + 1];
+  float za[NT][4], z0[NT][4];
+  int vb[NT][2];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      za[nt][s] = zget(a, j, 1 + 4 * q + s, 16 * nt + m);
+      z0[nt][s] = zget(a, j, 0, 16 * nt + 4 * q + s);
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int c = 16 * nt + 4 * q + 2 * p;
+      vb[nt][p] = c < wc2 ? (int)a.cmap[c >> 1] : -1;
+    }
+  }
+  TileIn next = load_tile<false>(a, g0, (int)((g1 - g0) < kMT ? (g1 - g0) : kMT), lane);
+  for (int64_t base = g0; base < g1; base += kMT) {
+    const int n = (int)((g1 - base) < kMT ? (g1 - base) : kMT);
+    const TileIn cur = next;
+    if (base + kMT < g1) {
+      const int64_t nb2 = base + kMT;
+      next = load_tile<false>(a, nb2, (int)((g1 - nb2) < kMT ? (g1 - nb2) : kMT), lane);
+    }
+    *reinterpret_cast<floatx4*>(Ph + 4 * lane) = cur.ph;
+    if (lane < kMT) Rh[lane] = cur.rho;
+    floatx4 acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], cur.h[s], acc[nt]);
+    wave_sync();
+    factors_grouped(a, Bd, Ph, Rh, Ft, lane);
+    wave_sync();
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int c = 16 * nt + 4 * q + 2 * p;
+        const float ur = acc[nt][2 * p] + z0[nt][2 * p], ui = acc[nt][2 * p + 1] + z0[nt][2 * p + 1];
+        float vr = ur, vi = ui;
+        if (vb[nt][p] >= 0) {
+          const float* f = Ft + 2 * (m * nb + vb[nt][p]);
+          vr = f[0] * ur - f[1] * ui;
+          vi = f[0] * ui + f[1] * ur;
+        }
+        Vt[m * VP + c] = vr;
+        Vt[m * VP + c + 1] = vi;
+      }
+    wave_sync();
+    for (int e = q; e < n; e += 4) {
+      const float* v = Vt + e * VP;
+      float* row = a.out + (base + e) * d_out;
+      for (int o = m; o < d_out; o += kMT) {
+        float sum = 0.f;
+        for (int k = optr[o]; k < optr[o + 1]; ++k) sum += v[olist[k]];
+        row[o] = sum;
+      }
+    }
+    wave_sync();
+  }
+}
+
+template <int NT>
+__global__ __launch_bounds__(64) void factored_backward_grouped(FactArgs<float> a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nb = a.n_blocks, CV = 16 * NT, WP = CV + 1, wc2 = 2 * a.wc, d_out = a.d_out;
+  int64_t* Tg = reinterpret_cast<int64_t*>(smem);                  // [kMT] targets
+  Block* Bd = reinterpret_cast<Block*>(Tg + kMT);                  // [nb]
+  float* Ph = reinterpret_cast<float*>(Bd + GM_FACT_MAX_BLOCKS);   // [kMT][kPhaseRow]
+  float* Rh = Ph + kMT * kPhaseRow;                                // [kMT]
+  float* St = Rh + kMT;                                            // [kMT]
+  float* Ft = St + kMT;                                            // [kMT][nb][2]
+  float* Gt = Ft + kMT * nb * 2;                                   // [kMT][d_out]
+  float* Wt = Gt + kMT * d_out;                                    // [kMT][WP]
+  float* Ht = Wt + kMT * WP;                                       // [kMT][16]
+  const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
+  stage_desc(a, Bd, lane);
+  const int64_t gi = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t j = a.group_source[gi];
+  const int64_t g0 = a.group_ptr[gi], g1 = a.group_ptr[gi + 1];
+  float zb[4 * NT];
+#pragma unroll
+  for (int s = 0; s < 4 * NT; ++s) zb[s] = zget(a, j, 1 + m, q + 4 * s);
+  uint32_t ci[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) ci[nt] = 16 * nt + m < a.C ? a.colinfo[16 * nt + m] : 0xFFFFFFFFu;
+  floatx4 dz[NT];
+  float dz0[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    dz[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    dz0[nt] = 0.f;
+  }
+  TileIn next = load_tile<true>(a, g0, (int)((g1 - g0) < kMT ? (g1 - g0) : kMT), lane);
+  for (int64_t base = g0; base < g1; base += kMT) {
+    const int n = (int)((g1 - base) < kMT ? (g1 - base) : kMT);
+    const TileIn cur = next;
+    if (base + kMT < g1) {
+      const int64_t nb2 = base + kMT;
+      next = load_tile<true>(a, nb2, (int)((g1 - nb2) < kMT ? (g1 - nb2) : kMT), lane);
+    }
+    *reinterpret_cast<floatx4*>(Ph + 4 * lane) = cur.ph;
+    *reinterpret_cast<floatx4*>(Ht + 4 * lane) = cur.h;  // Ht[e = l / 4][4 (l % 4) ..]
+    if (lane < kMT) {
+      Rh[lane] = cur.rho;
+      St[lane] = cur.w;
+      Tg[lane] = cur.tgt;
+    }
+    wave_sync();
+    for (int e = q; e < kMT; e += 4) {
+      const float* grow = e < n ? a.g + Tg[e] * d_out : nullptr;
+      for (int o = m; o < d_out; o += kMT) Gt[e * d_out + o] = grow ? grow[o] : 0.f;
+    }
+    factors_grouped(a, Bd, Ph, Rh, Ft, lane);
+    wave_sync();
+    if (lane < n) {
+      const float* r = a.rows + (base + lane) * d_out;
+      const float* gr = Gt + lane * d_out;
+      float sum = 0.f;
+      for (int o = 0; o < d_out; ++o) sum += gr[o] * r[o];
+      a.dweights[base + lane] = sum;
+    }
+    float w[NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const uint32_t info = ci[nt];
+      const int b = info & 0xFF, gre = (info >> 8) & 0xFF, gim = (info >> 16) & 0xFF, kind = info >> 24;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = q + 4 * i;
+        float v = 0.f;
+        if (info != 0xFFFFFFFFu) {
+          const float* gr = Gt + e * d_out;
+          const float g_re = gr[gre], g_im = gim == 0xFF ? 0.f : gr[gim];
+          if (kind == 0) {
+            v = g_re;
+          } else {
+            const float* f = Ft + 2 * (e * nb + b);
+            v = kind == 1 ? g_re * f[0] + g_im * f[1] : g_im * f[0] - g_re * f[1];
+          }
+          v *= St[e];
+        }
+        w[nt][i] = v;
+        Wt[e * WP + 16 * nt + m] = v;
+      }
+    }
+    wave_sync();
+    floatx4 dh = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4 * NT; ++s) dh = mfma16(Wt[m * WP + q + 4 * s], zb[s], dh);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = 4 * q + r;
+      if (e < n && m + 1 < a.K) a.dh[(base + e) * 16 + m] = dh[r];
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dz[nt] = mfma16(Ht[(q + 4 * i) * 16 + m], w[nt][i], dz[nt]);
+        dz0[nt] += w[nt][i];
+      }
+    wave_sync();
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    dz0[nt] += __shfl_xor(dz0[nt], 16, kWave);
+    dz0[nt] += __shfl_xor(dz0[nt], 32, kWave);
+    const int c = 16 * nt + m;
+    if (c >= a.C) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 1 + 4 * q + r;
+      if (t < a.K) zput(a, j, t, c, dz[nt][r]);
+    }
+    if (q == 0) zput(a, j, 0, c, dz0[nt]);
   }
 }
 
 // ------------------------------------------------------------------- launch
 
+// The mix runs of a call: the caller's (pointer, node stride, mix stride,
+// width) runs, in packed-column order.
 template <typename T>
-int prepare(FactArgs<T>& a, const T* h, const T* zc, const T* zr, const T* angular, const T* transport, const T* rho,
+struct Runs {
+  const T* const* z;
+  T* const* dz;  // null in the forward
+  const int64_t* node_stride;
+  const int64_t* t_stride;
+  const int64_t* width;
+  int64_t n;
+};
+
+template <typename T>
+int prepare(FactArgs<T>& a, const T* h, const Runs<T>& runs, const T* angular, const T* transport, const T* rho,
             const int32_t* desc, const int64_t* order, const int64_t* group_ptr, const int64_t* group_source,
             int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f,
             int64_t n_blocks, int64_t d_out) {
@@ -367,10 +1038,13 @@ int prepare(FactArgs<T>& a, const T* h, const T* zc, const T* zr, const T* angul
   // an output slot are consecutive, alike in width and kind of output.
   int covered_c = 0, covered_r = 0, open = -1;
   bool seen_real = false;
+  bool taken[GM_FACT_MAX_C / 2] = {};
   std::string why;
   for (int b = 0; b < n_blocks; ++b) {
     const int32_t* r = desc + b * GM_FACT_DESC;
-    Block d{r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]};
+    for (int k = 0; k < GM_FACT_DESC; ++k) GM_REQUIRE(r[k] >= -32768 && r[k] <= 32767, "descriptor entries must fit 16 bits");
+    Block d{(int16_t)r[0], (int16_t)r[1], (int16_t)r[2], (int16_t)r[3], (int16_t)r[4], (int16_t)r[5], (int16_t)r[6],
+            (int16_t)r[7]};
     GM_REQUIRE(d.kind == 0 || d.kind == 1, "a block's kind must be 0 (real) or 1 (complex)");
     GM_REQUIRE(d.bm >= 1 && d.bm <= GM_FACT_MAX_BM, "a block's multiplicity must be in [1, 32]");
     GM_REQUIRE(d.power >= 0 && d.power <= 64, "a block's radial power must be in [0, 64]");
@@ -381,8 +1055,14 @@ int prepare(FactArgs<T>& a, const T* h, const T* zc, const T* zr, const T* angul
       GM_REQUIRE(!seen_real && d.zoff == 0 && d.bm == wr, "the real block must be one block covering zr");
       seen_real = true;
       covered_r = d.bm;
+      a.real_ooff = d.ooff;
     } else {
-      GM_REQUIRE(d.zoff == covered_c, "the complex blocks must pack zc contiguously in descriptor order");
+      GM_REQUIRE(d.zoff >= 0 && d.zoff + d.bm <= wc, "a complex block's columns run past wc");
+      for (int u = 0; u < d.bm; ++u) {
+        GM_REQUIRE(!taken[d.zoff + u], "two complex blocks share a packed column");
+        taken[d.zoff + u] = true;
+        a.cmap[d.zoff + u] = (uint8_t)b;
+      }
       covered_c += d.bm;
     }
     if (d.ooff != open) {
@@ -396,9 +1076,65 @@ int prepare(FactArgs<T>& a, const T* h, const T* zc, const T* zr, const T* angul
     a.desc[b] = d;
   }
   GM_REQUIRE(covered_c == wc && covered_r == wr, "the blocks must cover zc and zr exactly");
+  if (a.C <= 128) {
+    // the MFMA path's tables: what each packed column reads of an edge's
+    // output gradient, and which V columns each output slot sums
+    int real_block = -1;
+    for (int b = 0; b < n_blocks; ++b)
+      if (a.desc[b].kind == 0) real_block = b;
+    for (int c = 0; c < a.C; ++c) {
+      uint32_t blk, gre, gim = 0xFF, kind;
+      if (c < 2 * wc) {
+        blk = a.cmap[c >> 1];
+        const Block& d = a.desc[blk];
+        const int jj = (c >> 1) - d.zoff;
+        if (d.take_real) {
+          gre = d.ooff + jj;
+        } else {
+          gre = d.ooff + 2 * jj;
+          gim = d.ooff + 2 * jj + 1;
+        }
+        kind = (c & 1) ? 2 : 1;
+      } else {
+        blk = (uint32_t)real_block;
+        gre = a.real_ooff + (c - 2 * wc);
+        kind = 0;
+      }
+      a.colinfo[c] = blk | (gre << 8) | (gim << 16) | (kind << 24);
+    }
+    int count = 0;
+    for (int o = 0; o < d_out; ++o) {
+      a.optr[o] = (uint8_t)count;
+      for (int b = 0; b < n_blocks; ++b) {
+        const Block& d = a.desc[b];
+        const bool scalar = d.kind == 0 || d.take_real;
+        const int k = o - d.ooff;
+        if (k < 0 || k >= (scalar ? d.bm : 2 * d.bm)) continue;
+        const int col = d.kind == 0 ? 2 * wc + d.zoff + k : d.take_real ? 2 * (d.zoff + k) : 2 * (d.zoff + (k >> 1)) + (k & 1);
+        GM_REQUIRE(count < 128, "more than 128 output terms");
+        a.olist[count++] = (uint8_t)col;
+      }
+    }
+    a.optr[d_out] = (uint8_t)count;
+  }
+  // the mix runs: in packed-column order, tiling [0, C), none straddling the
+  // complex / real boundary at 2 wc
+  GM_REQUIRE(runs.n >= 1 && runs.n <= GM_FACT_MAX_SEG, "between 1 and 4 mix runs");
+  a.n_seg = (int)runs.n;
+  int c0 = 0;
+  for (int r = 0; r < a.n_seg; ++r) {
+    const int64_t w = runs.width[r];
+    GM_REQUIRE(w >= 1 && c0 + w <= a.C, "the mix runs must tile the packed columns");
+    GM_REQUIRE(!(c0 < 2 * wc && c0 + w > 2 * wc), "a mix run straddles the complex and real columns");
+    GM_REQUIRE(runs.node_stride[r] >= 0 && runs.t_stride[r] >= 0, "mix strides must be non-negative");
+    GM_REQUIRE(runs.t_stride[r] <= (int64_t(1) << 30), "mix stride too large");
+    a.seg[r] = ZSeg<T>{runs.z[r], runs.dz ? runs.dz[r] : nullptr, runs.node_stride[r], (int)runs.t_stride[r], c0,
+                       (int)w};
+    if (n_edges > 0) GM_REQUIRE(runs.z[r] != nullptr, "every mix run must be a device pointer");
+    c0 += (int)w;
+  }
+  GM_REQUIRE(c0 == a.C, "the mix runs must tile the packed columns");
   a.h = h;
-  a.zc = zc;
-  a.zr = zr;
   a.angular = angular;
   a.transport = transport;
   a.rho = rho;
@@ -408,7 +1144,6 @@ int prepare(FactArgs<T>& a, const T* h, const T* zc, const T* zr, const T* angul
   if (n_edges > 0) {
     GM_REQUIRE((K == 1 || h) && rho && angular && transport, "the per-edge tables must be device pointers");
     GM_REQUIRE(order && group_ptr && group_source, "order, group_ptr and group_source must be device pointers");
-    GM_REQUIRE((wc == 0 || zc) && (wr == 0 || zr), "zc and zr must be device pointers");
   }
   return GM_OK;
 }
@@ -424,6 +1159,57 @@ template <typename T>
 size_t lds_backward(const FactArgs<T>& a) {
   return sizeof(T) * ((size_t)a.C * a.KP + (size_t)a.tile * (a.CP + a.KP));
 }
+
+// The MFMA kernels serve fp32 plans with at most 16 trunk features and 128
+// packed columns (GM_FACTORED_MFMA=0 selects the vector kernels instead).
+bool mfma_eligible(const FactArgs<float>& a) {
+  static const bool off = [] {
+    const char* v = std::getenv("GM_FACTORED_MFMA");
+    return v != nullptr && v[0] == '0';
+  }();
+  return !off && a.K <= 17 && a.C <= 128 && aligned(a.h, 16);
+}
+template <typename T>
+bool mfma_eligible(const FactArgs<T>&) {
+  return false;
+}
+
+size_t lds_forward_mfma(const FactArgs<float>& a, int NT) {
+  return sizeof(int64_t) * kMT + sizeof(Block) * GM_FACT_MAX_BLOCKS +
+         sizeof(float) * (size_t)(kMT + kMT * 4 * a.n_f + kMT * a.n_blocks * 2 + kMT * (16 * NT + 1) +
+                                  17 * (16 * NT + 4)) +
+         (GM_FACT_MAX_OUT + 1) + 128;
+}
+
+size_t lds_backward_mfma(const FactArgs<float>& a, int NT) {
+  return sizeof(int64_t) * kMT + sizeof(Block) * GM_FACT_MAX_BLOCKS +
+         sizeof(float) * (size_t)(2 * kMT + kMT * 4 * a.n_f + kMT * a.n_blocks * 2 + kMT * a.d_out +
+                                  kMT * (16 * NT + 1) + kMT * 16 + 17 * (16 * NT + 4));
+}
+
+template <int NT>
+void launch_mfma_nt(bool forward, const FactArgs<float>& a, hipStream_t stream) {
+  const dim3 grid((unsigned)a.n_groups), block(64);
+  if (forward)
+    hipLaunchKernelGGL(factored_forward_mfma<NT>, grid, block, lds_forward_mfma(a, NT), stream, a);
+  else
+    hipLaunchKernelGGL(factored_backward_mfma<NT>, grid, block, lds_backward_mfma(a, NT), stream, a);
+}
+
+void launch_mfma(bool forward, const FactArgs<float>& a, hipStream_t stream) {
+  switch ((a.C + 15) / 16) {
+    case 1: launch_mfma_nt<1>(forward, a, stream); break;
+    case 2: launch_mfma_nt<2>(forward, a, stream); break;
+    case 3: launch_mfma_nt<3>(forward, a, stream); break;
+    case 4: launch_mfma_nt<4>(forward, a, stream); break;
+    case 5: launch_mfma_nt<5>(forward, a, stream); break;
+    case 6: launch_mfma_nt<6>(forward, a, stream); break;
+    case 7: launch_mfma_nt<7>(forward, a, stream); break;
+    default: launch_mfma_nt<8>(forward, a, stream); break;
+  }
+}
+template <typename T>
+void launch_mfma(bool, const FactArgs<T>&, hipStream_t) {}
 
 template <typename T, int KMAX>
 void launch_forward_k(const FactArgs<T>& a, int bm, hipStream_t stream) {
@@ -453,12 +1239,12 @@ void launch_backward_k(const FactArgs<T>& a, hipStream_t stream) {
 }
 
 template <typename T>
-int factored_forward(const T* h, const T* zc, const T* zr, const T* angular, const T* transport, const T* rho,
+int factored_forward(const T* h, const Runs<T>& runs, const T* angular, const T* transport, const T* rho,
                      const int32_t* desc, const int64_t* order, const int64_t* group_ptr, const int64_t* group_source,
                      int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr,
                      int64_t n_f, int64_t n_blocks, int64_t d_out, int64_t max_bm, T* out, hipStream_t stream) {
   FactArgs<T> a;
-  const int status = prepare(a, h, zc, zr, angular, transport, rho, desc, order, group_ptr, group_source, n_nodes,
+  const int status = prepare(a, h, runs, angular, transport, rho, desc, order, group_ptr, group_source, n_nodes,
                              n_edges, n_groups, K, wc, wr, n_f, n_blocks, d_out);
   if (status != GM_OK) return status;
   GM_REQUIRE(max_bm >= 1 && max_bm <= GM_FACT_MAX_BM, "max_bm must be in [1, 32]");
@@ -469,6 +1255,10 @@ int factored_forward(const T* h, const T* zc, const T* zr, const T* angular, con
   GM_REQUIRE(out, "out must be a device pointer");
   GM_REQUIRE(lds_forward(a) <= kLdsBudget, "the staged mixes exceed 64 KiB");
   a.out = out;
+  if (mfma_eligible(a)) {
+    launch_mfma(true, a, stream);
+    return check_launch("factored_forward (mfma)");
+  }
   if (a.K == 17)
     launch_forward_k<T, 17>(a, widest, stream);
   else
@@ -478,30 +1268,31 @@ int factored_forward(const T* h, const T* zc, const T* zr, const T* angular, con
 
 template <typename T>
 int factored_aggregate(const T* rows, const T* weights, const int64_t* row_ptr, int64_t n_targets, int64_t n_edges,
-                       int64_t d_out, T* out, hipStream_t stream) {
+                       int64_t d_out, T* out, hipStream_t stream, const int64_t* inv = nullptr) {
   GM_REQUIRE(n_targets >= 0 && n_edges >= 0, "sizes must be non-negative");
   GM_REQUIRE(d_out >= 1 && d_out <= GM_FACT_MAX_OUT, "d_out must be in [1, 128]");
   GM_REQUIRE(n_targets < (int64_t(1) << 31) * kWavesPerBlock, "too many targets for one launch");
   if (n_targets == 0) return GM_OK;
   GM_REQUIRE(row_ptr && out && (n_edges == 0 || (rows && weights)), "rows, weights, row_ptr and out must be device pointers");
-  AggArgs<T> a{rows, weights, row_ptr, out, n_targets, (int)d_out, d_out <= 32 ? (int)(kWave / d_out) : 1};
+  AggArgs<T> a{rows, weights, row_ptr, out, inv, n_targets, (int)d_out, d_out <= 32 ? (int)(kWave / d_out) : 1};
   hipLaunchKernelGGL(aggregate_kernel<T>, dim3((unsigned)blocks_for(n_targets)), dim3(256), 0, stream, a);
   return check_launch("factored_aggregate");
 }
 
 template <typename T>
-int factored_backward(const T* g, const int64_t* target, const T* weights, const T* rows, const T* h, const T* zc,
-                      const T* zr, const T* angular, const T* transport, const T* rho, const int32_t* desc,
+int factored_backward(const T* g, const int64_t* target, const T* weights, const T* rows, const T* h,
+                      const Runs<T>& runs, const T* angular, const T* transport, const T* rho, const int32_t* desc,
                       const int64_t* order, const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes,
                       int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f,
-                      int64_t n_blocks, int64_t d_out, T* dh, T* dzc, T* dzr, T* dweights, hipStream_t stream) {
+                      int64_t n_blocks, int64_t d_out, T* dh, T* dweights, hipStream_t stream) {
   FactArgs<T> a;
-  const int status = prepare(a, h, zc, zr, angular, transport, rho, desc, order, group_ptr, group_source, n_nodes,
+  const int status = prepare(a, h, runs, angular, transport, rho, desc, order, group_ptr, group_source, n_nodes,
                              n_edges, n_groups, K, wc, wr, n_f, n_blocks, d_out);
   if (status != GM_OK) return status;
   const bool aggregated = target != nullptr;
   if (n_edges == 0 || n_groups == 0) return GM_OK;
-  GM_REQUIRE(g && (K == 1 || dh) && (wc == 0 || dzc) && (wr == 0 || dzr), "g, dh, dzc and dzr must be device pointers");
+  GM_REQUIRE(g && (K == 1 || dh) && runs.dz, "g, dh and the mix gradients must be device pointers");
+  for (int r = 0; r < a.n_seg; ++r) GM_REQUIRE(a.seg[r].dz != nullptr, "every mix gradient run must be a device pointer");
   if (aggregated) GM_REQUIRE(weights && rows && dweights, "the aggregated form needs weights, rows and dweights");
   a.tile = kWave;
   while (a.tile > 1 && lds_backward(a) > kLdsBudget) a.tile >>= 1;
@@ -512,14 +1303,103 @@ int factored_backward(const T* g, const int64_t* target, const T* weights, const
   a.rows = aggregated ? rows : nullptr;
   a.dweights = aggregated ? dweights : nullptr;
   a.dh = dh;
-  a.dzc = dzc;
-  a.dzr = dzr;
+  if (mfma_eligible(a)) {
+    launch_mfma(false, a, stream);
+    return check_launch("factored_backward (mfma)");
+  }
   if (a.K == 17)
     launch_backward_k<T, 17>(a, stream);
   else
     launch_backward_k<T, GM_FACT_MAX_K>(a, stream);
   return check_launch("factored_backward");
 }
+
+}  // namespace
+}  // namespace gm
+
+namespace gm {
+namespace {
+
+size_t lds_forward_grouped(const FactArgs<float>& a, int NT) {
+  return sizeof(Block) * GM_FACT_MAX_BLOCKS +
+         sizeof(float) * (size_t)(kMT * kPhaseRow + kMT + kMT * a.n_blocks * 2 + kMT * (16 * NT + 1)) +
+         (GM_FACT_MAX_OUT + 1) + 128;
+}
+
+size_t lds_backward_grouped(const FactArgs<float>& a, int NT) {
+  return sizeof(int64_t) * kMT + sizeof(Block) * GM_FACT_MAX_BLOCKS +
+         sizeof(float) * (size_t)(kMT * kPhaseRow + 2 * kMT + kMT * a.n_blocks * 2 + kMT * a.d_out +
+                                  kMT * (16 * NT + 1) + kMT * 16);
+}
+
+template <int NT>
+void launch_grouped_nt(bool forward, const FactArgs<float>& a, hipStream_t stream) {
+  const dim3 grid((unsigned)a.n_groups), block(64);
+  if (forward)
+    hipLaunchKernelGGL(factored_forward_grouped<NT>, grid, block, lds_forward_grouped(a, NT), stream, a);
+  else
+    hipLaunchKernelGGL(factored_backward_grouped<NT>, grid, block, lds_backward_grouped(a, NT), stream, a);
+}
+
+void launch_grouped(bool forward, const FactArgs<float>& a, hipStream_t stream) {
+  switch ((a.C + 15) / 16) {
+    case 1: launch_grouped_nt<1>(forward, a, stream); break;
+    case 2: launch_grouped_nt<2>(forward, a, stream); break;
+    case 3: launch_grouped_nt<3>(forward, a, stream); break;
+    case 4: launch_grouped_nt<4>(forward, a, stream); break;
+    case 5: launch_grouped_nt<5>(forward, a, stream); break;
+    case 6: launch_grouped_nt<6>(forward, a, stream); break;
+    case 7: launch_grouped_nt<7>(forward, a, stream); break;
+    default: launch_grouped_nt<8>(forward, a, stream); break;
+  }
+}
+
+// The grouped path's extra checks: fp32, 16 trunk features, at most 128
+// packed columns, both phase tables within one 8-pair row, 16-byte rows.
+int prepare_grouped(FactArgs<float>& a, const float* h, const Runs<float>& runs, const float* phase_g,
+                    const float* rho_g, const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source,
+                    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa,
+                    int64_t pt, int64_t n_blocks, int64_t d_out) {
+  GM_REQUIRE(pa >= 1 && pt >= 1 && pa + pt <= kPhaseRow / 2, "the grouped phase rows hold at most 8 pairs");
+  const int status = prepare(a, h, runs, phase_g, phase_g, rho_g, desc, group_ptr /* order unused */, group_ptr,
+                             group_source, n_nodes, n_edges, n_groups, K, wc, wr, pa > pt ? pa : pt, n_blocks, d_out);
+  if (status != GM_OK) return status;
+  GM_REQUIRE(K == 17, "the grouped kernels take 16 trunk features (K = 17)");
+  GM_REQUIRE(a.C <= 128, "the grouped kernels take at most 128 packed columns");
+  for (int b = 0; b < a.n_blocks; ++b) {
+    const Block& d = a.desc[b];
+    GM_REQUIRE(std::abs(d.ang) < pa && std::abs(d.tr) < pt, "a block's harmonic order exceeds the grouped phase rows");
+  }
+  if (n_edges > 0) GM_REQUIRE(h && aligned(h, 16) && phase_g && aligned(phase_g, 16) && rho_g,
+                              "h and the phase rows must be 16-byte aligned device pointers");
+  a.phase_g = phase_g;
+  a.rho_g = rho_g;
+  a.pa = (int)pa;
+  a.pt = (int)pt;
+  return GM_OK;
+}
+
+// The reference's zc / zr as two mix runs (an empty one dropped).
+template <typename T>
+struct TwoRuns {
+  const T* z[2];
+  T* dz[2];
+  int64_t node_stride[2], t_stride[2], width[2];
+  int64_t n = 0;
+  TwoRuns(const T* zc, const T* zr, T* dzc, T* dzr, int64_t K, int64_t wc, int64_t wr) {
+    if (wc > 0) add(zc, dzc, K * 2 * wc, 2 * wc, 2 * wc);
+    if (wr > 0) add(zr, dzr, K * wr, wr, wr);
+  }
+  void add(const T* p, T* dp, int64_t ns, int64_t ts, int64_t w) {
+    z[n] = p;
+    dz[n] = dp;
+    node_stride[n] = ns;
+    t_stride[n] = ts;
+    width[n] = w;
+    ++n;
+  }
+  Runs<T> runs(bool backward) const { return Runs<T>{z, backward ? dz : nullptr, node_stride, t_stride, width, n}; }
+};
 
 }  // namespace
 }  // namespace gm
@@ -531,7 +1411,20 @@ int factored_backward(const T* g, const int64_t* target, const T* weights, const
                                          int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr,        \
                                          int64_t n_f, int64_t n_blocks, int64_t d_out, int64_t max_bm, T* out,        \
                                          void* stream) {                                                              \
-    return gm::factored_forward<T>(h, zc, zr, angular, transport, rho, desc, order, group_ptr, group_source, n_nodes, \
+    const gm::TwoRuns<T> two(zc, zr, nullptr, nullptr, K, wc, wr);                                                    \
+    return gm::factored_forward<T>(h, two.runs(false), angular, transport, rho, desc, order, group_ptr, group_source, \
+                                   n_nodes, n_edges, n_groups, K, wc, wr, n_f, n_blocks, d_out, max_bm, out,          \
+                                   (hipStream_t)stream);                                                              \
+  }                                                                                                                   \
+  extern "C" int gm_factored_forward_seg_##S(                                                                         \
+      const T* h, const T* const* z, const int64_t* node_stride, const int64_t* t_stride, const int64_t* width,       \
+      int64_t n_runs, const T* angular, const T* transport, const T* rho, const int32_t* desc, const int64_t* order,  \
+      const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges, int64_t n_groups,      \
+      int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks, int64_t d_out, int64_t max_bm, T* out,        \
+      void* stream) {                                                                                                 \
+    GM_REQUIRE(z && node_stride && t_stride && width, "the mix runs must be host arrays");                           \
+    const gm::Runs<T> runs{z, nullptr, node_stride, t_stride, width, n_runs};                                         \
+    return gm::factored_forward<T>(h, runs, angular, transport, rho, desc, order, group_ptr, group_source, n_nodes,   \
                                    n_edges, n_groups, K, wc, wr, n_f, n_blocks, d_out, max_bm, out,                   \
                                    (hipStream_t)stream);                                                              \
   }                                                                                                                   \
@@ -545,10 +1438,78 @@ int factored_backward(const T* g, const int64_t* target, const T* weights, const
       const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges, int64_t n_groups,      \
       int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks, int64_t d_out, T* dh, T* dzc, T* dzr,         \
       T* dweights, void* stream) {                                                                                    \
-    return gm::factored_backward<T>(g, target, weights, rows, h, zc, zr, angular, transport, rho, desc, order,        \
+    const gm::TwoRuns<T> two(zc, zr, dzc, dzr, K, wc, wr);                                                            \
+    return gm::factored_backward<T>(g, target, weights, rows, h, two.runs(true), angular, transport, rho, desc,       \
+                                    order, group_ptr, group_source, n_nodes, n_edges, n_groups, K, wc, wr, n_f,       \
+                                    n_blocks, d_out, dh, dweights, (hipStream_t)stream);                              \
+  }                                                                                                                   \
+  extern "C" int gm_factored_backward_seg_##S(                                                                        \
+      const T* g, const int64_t* target, const T* weights, const T* rows, const T* h, const T* const* z,             \
+      T* const* dz, const int64_t* node_stride, const int64_t* t_stride, const int64_t* width, int64_t n_runs,        \
+      const T* angular, const T* transport, const T* rho, const int32_t* desc, const int64_t* order,                  \
+      const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges, int64_t n_groups,      \
+      int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks, int64_t d_out, T* dh, T* dweights,            \
+      void* stream) {                                                                                                 \
+    GM_REQUIRE(z && dz && node_stride && t_stride && width, "the mix runs must be host arrays");                     \
+    const gm::Runs<T> runs{z, dz, node_stride, t_stride, width, n_runs};                                              \
+    return gm::factored_backward<T>(g, target, weights, rows, h, runs, angular, transport, rho, desc, order,          \
                                     group_ptr, group_source, n_nodes, n_edges, n_groups, K, wc, wr, n_f, n_blocks,    \
-                                    d_out, dh, dzc, dzr, dweights, (hipStream_t)stream);                              \
+                                    d_out, dh, dweights, (hipStream_t)stream);                                        \
   }
 
 GM_FACT_EXPORTS(float, f32)
 GM_FACT_EXPORTS(double, f64)
+
+extern "C" int gm_factored_forward_grouped_f32(
+    const float* h_g, const float* const* z, const int64_t* node_stride, const int64_t* t_stride,
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const int32_t* desc,
+    const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
+    int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks, int64_t d_out, float* rows_g,
+    void* stream) {
+  GM_REQUIRE(z && node_stride && t_stride && width, "the mix runs must be host arrays");
+  const gm::Runs<float> runs{z, nullptr, node_stride, t_stride, width, n_runs};
+  gm::FactArgs<float> a;
+  const int status = gm::prepare_grouped(a, h_g, runs, phase_g, rho_g, desc, group_ptr, group_source, n_nodes, n_edges,
+                                         n_groups, K, wc, wr, pa, pt, n_blocks, d_out);
+  if (status != GM_OK) return status;
+  if (n_edges == 0 || n_groups == 0) return GM_OK;
+  GM_REQUIRE(rows_g, "rows must be a device pointer");
+  a.out = rows_g;
+  gm::launch_grouped(true, a, (hipStream_t)stream);
+  return gm::check_launch("factored_forward_grouped");
+}
+
+extern "C" int gm_factored_backward_grouped_f32(
+    const float* g, const int64_t* target_g, const float* weights_g, const float* rows_g, const float* h_g,
+    const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const int32_t* desc,
+    const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
+    int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks, int64_t d_out, float* dh_g,
+    float* dweights_g, void* stream) {
+  GM_REQUIRE(z && dz && node_stride && t_stride && width, "the mix runs must be host arrays");
+  const gm::Runs<float> runs{z, dz, node_stride, t_stride, width, n_runs};
+  gm::FactArgs<float> a;
+  const int status = gm::prepare_grouped(a, h_g, runs, phase_g, rho_g, desc, group_ptr, group_source, n_nodes, n_edges,
+                                         n_groups, K, wc, wr, pa, pt, n_blocks, d_out);
+  if (status != GM_OK) return status;
+  if (n_edges == 0 || n_groups == 0) return GM_OK;
+  GM_REQUIRE(g && target_g && weights_g && rows_g && dh_g && dweights_g,
+             "g, target_g, weights_g, rows_g, dh_g and dweights_g must be device pointers");
+  for (int r = 0; r < a.n_seg; ++r) GM_REQUIRE(a.seg[r].dz != nullptr, "every mix gradient run must be a device pointer");
+  a.g = g;
+  a.target_g = target_g;
+  a.weights = weights_g;
+  a.rows = rows_g;
+  a.dh = dh_g;
+  a.dweights = dweights_g;
+  gm::launch_grouped(false, a, (hipStream_t)stream);
+  return gm::check_launch("factored_backward_grouped");
+}
+
+extern "C" int gm_factored_aggregate_gather_f32(const float* rows, const int64_t* inv, const float* weights,
+                                                const int64_t* row_ptr, int64_t n_targets, int64_t n_edges,
+                                                int64_t d_out, float* out, void* stream) {
+  GM_REQUIRE(n_edges == 0 || inv, "inv must be a device pointer");
+  return gm::factored_aggregate<float>(rows, weights, row_ptr, n_targets, n_edges, d_out, out, (hipStream_t)stream,
+                                       inv);
+}

@@ -40,6 +40,18 @@ SIGNATURES: dict[str, list[Any]] = {
     "gm_factored_forward": [_P] * 10 + [_I] * 10 + [_P, _P],
     "gm_factored_aggregate": [_P] * 3 + [_I] * 3 + [_P, _P],
     "gm_factored_backward": [_P] * 14 + [_I] * 9 + [_P] * 5,
+    "gm_factored_forward_seg": [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P, _P],
+    "gm_factored_backward_seg": [_P] * 10 + [_I] + [_P] * 7 + [_I] * 9 + [_P] * 3,
+}
+
+#: fp32-only entry points (name -> (restype, argtypes)).
+SIGNATURES_F32 = {
+    "gm_radial_trunk_forward_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_D, _P, _P]),
+    "gm_radial_trunk_backward_f32": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_D, _P, _P, _P]),
+    "gm_radial_trunk_partials": (ctypes.c_int64, [_I]),
+    "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 5 + [_I] * 10 + [_P, _P]),
+    "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 5 + [_I] * 10 + [_P] * 3),
+    "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
 }
 
 
@@ -66,6 +78,10 @@ def library() -> ctypes.CDLL:
             fn = getattr(lib, stem + suffix)
             fn.restype = ctypes.c_int
             fn.argtypes = args
+    for name, (res, args) in SIGNATURES_F32.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
     return lib
 
 
@@ -460,3 +476,130 @@ class FactoredExtension:
 def factored() -> FactoredExtension:
     library()
     return FactoredExtension()
+
+
+# ---------------------------------------------------------------- mix runs and the radial trunk
+
+
+class MixRuns:
+    """Host arrays describing up to four runs of packed mix columns: run r
+    covers ``width[r]`` columns, column c of node j at mix t at
+    ``z[r] + j * node_stride[r] + t * t_stride[r] + (c - c_r)`` (elements)."""
+
+    def __init__(self, runs: list[tuple[Tensor, int, int, int]], grads: list[Tensor] | None = None):
+        n = len(runs)
+        _fcheck(1 <= n <= 4, "between 1 and 4 mix runs")
+        self.keep = [t for t, *_ in runs] + (grads or [])
+        self.z = (ctypes.c_void_p * n)(*[t.data_ptr() for t, *_ in runs])
+        self.dz = (ctypes.c_void_p * n)(*[g.data_ptr() for g in grads]) if grads is not None else None
+        self.node_stride = (ctypes.c_int64 * n)(*[r[1] for r in runs])
+        self.t_stride = (ctypes.c_int64 * n)(*[r[2] for r in runs])
+        self.width = (ctypes.c_int64 * n)(*[r[3] for r in runs])
+        self.n = n
+
+
+def factored_forward_seg(h: Tensor, runs: MixRuns, n_nodes: int, angular: Tensor, transport: Tensor, rho: Tensor,
+                         desc: Tensor, order: Tensor, group_ptr: Tensor, group_source: Tensor, K: int, wc: int, wr: int,
+                         d_out: int, max_bm: int) -> Tensor:
+    """The rows ``(n_edges, d_out)`` with the mixes read from ``runs``."""
+    out = torch.empty(h.shape[0], d_out, dtype=h.dtype, device=h.device)
+    if h.shape[0] == 0:
+        return out
+    hd = host_desc32(desc)
+    _call("gm_factored_forward_seg" + _suffix(h.dtype), _ptr(h), ctypes.cast(runs.z, ctypes.c_void_p),
+          ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
+          ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(angular), _ptr(transport), _ptr(rho), hd.data_ptr(),
+          _ptr(order), _ptr(group_ptr), _ptr(group_source), n_nodes, h.shape[0], group_source.shape[0], K, wc, wr,
+          angular.shape[1], hd.shape[0], d_out, max_bm, _ptr(out), _stream(h.device))
+    return out
+
+
+def factored_backward_seg(g: Tensor, target: Tensor, weights: Tensor, rows: Tensor, h: Tensor, runs: MixRuns,
+                          n_nodes: int, angular: Tensor, transport: Tensor, rho: Tensor, desc: Tensor, order: Tensor,
+                          group_ptr: Tensor, group_source: Tensor, K: int, wc: int, wr: int,
+                          dh: Tensor) -> Tensor:
+    """dh written into ``dh``, the mix gradients into the runs' gradient
+    arrays (zeroed by the caller); returns dweights."""
+    dweights = torch.empty_like(weights)
+    if h.shape[0] == 0:
+        return dweights
+    hd = host_desc32(desc)
+    _call("gm_factored_backward_seg" + _suffix(h.dtype), _ptr(g), _ptr(target), _ptr(weights), _ptr(rows), _ptr(h),
+          ctypes.cast(runs.z, ctypes.c_void_p), ctypes.cast(runs.dz, ctypes.c_void_p),
+          ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
+          ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(angular), _ptr(transport), _ptr(rho),
+          hd.data_ptr(), _ptr(order), _ptr(group_ptr), _ptr(group_source), n_nodes, h.shape[0],
+          group_source.shape[0], K, wc, wr, angular.shape[1], hd.shape[0], g.shape[1], _ptr(dh), _ptr(dweights),
+          _stream(h.device))
+    return dweights
+
+
+def radial_trunk_forward(rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor, width: float) -> Tensor:
+    """``h (H, E, T)``: every head's SiLU(W b(rho) + c) over the Gaussian basis of rho^2."""
+    H, T, B = weight.shape
+    h = torch.empty(H, rho.shape[0], T, dtype=rho.dtype, device=rho.device)
+    if rho.shape[0] == 0:
+        return h
+    _call("gm_radial_trunk_forward_f32", _ptr(rho), _ptr(weight), _ptr(bias) if bias is not None else None,
+          _ptr(centers), rho.shape[0], H, T, B, float(width), _ptr(h), _stream(rho.device))
+    return h
+
+
+def radial_trunk_backward(dh: Tensor, rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor,
+                          width: float) -> tuple[Tensor, Tensor]:
+    """(dweight (H, T, B), dbias (H, T)) summed over the edges in a fixed order."""
+    H, T, B = weight.shape
+    P = T * B + T
+    lib = library()
+    blocks = int(lib.gm_radial_trunk_partials(rho.shape[0]))
+    partial = torch.empty(max(blocks, 1) * H * P, dtype=torch.float32, device=rho.device)
+    dparams = torch.empty(H, P, dtype=torch.float32, device=rho.device)
+    _call("gm_radial_trunk_backward_f32", _ptr(dh), _ptr(rho), _ptr(weight), _ptr(bias) if bias is not None else None,
+          _ptr(centers), rho.shape[0], H, T, B, float(width), _ptr(partial), _ptr(dparams), _stream(rho.device))
+    return dparams[:, : T * B].reshape(H, T, B), dparams[:, T * B:]
+
+
+def factored_forward_grouped(h_g: Tensor, runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor, pa: int,
+                             pt: int, desc: Tensor, group_ptr: Tensor, group_source: Tensor, K: int, wc: int, wr: int,
+                             d_out: int) -> Tensor:
+    """The rows in the grouping's order, every per-edge stream read in that order."""
+    out = torch.empty(h_g.shape[0], d_out, dtype=h_g.dtype, device=h_g.device)
+    if h_g.shape[0] == 0:
+        return out
+    hd = host_desc32(desc)
+    _call("gm_factored_forward_grouped_f32", _ptr(h_g), ctypes.cast(runs.z, ctypes.c_void_p),
+          ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
+          ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), hd.data_ptr(),
+          _ptr(group_ptr), _ptr(group_source), n_nodes, h_g.shape[0], group_source.shape[0], K, wc, wr, pa, pt,
+          hd.shape[0], d_out, _ptr(out), _stream(h_g.device))
+    return out
+
+
+def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, rows_g: Tensor, h_g: Tensor,
+                              runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor, pa: int, pt: int,
+                              desc: Tensor, group_ptr: Tensor, group_source: Tensor, K: int, wc: int, wr: int,
+                              dh_g: Tensor) -> Tensor:
+    """dh (grouping order) into ``dh_g``, the mix gradients into the runs'
+    gradient arrays; returns dweights in the grouping's order."""
+    dweights = torch.empty_like(weights_g)
+    if h_g.shape[0] == 0:
+        return dweights
+    hd = host_desc32(desc)
+    _call("gm_factored_backward_grouped_f32", _ptr(g), _ptr(target_g), _ptr(weights_g), _ptr(rows_g), _ptr(h_g),
+          ctypes.cast(runs.z, ctypes.c_void_p), ctypes.cast(runs.dz, ctypes.c_void_p),
+          ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
+          ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), hd.data_ptr(),
+          _ptr(group_ptr), _ptr(group_source), n_nodes, h_g.shape[0], group_source.shape[0], K, wc, wr, pa, pt,
+          hd.shape[0], g.shape[1], _ptr(dh_g), _ptr(dweights), _stream(h_g.device))
+    return dweights
+
+
+def aggregate_gather(rows_g: Tensor, inv: Tensor, weights: Tensor, row_ptr: Tensor) -> Tensor:
+    """``out_i = sum_e weights[e] rows_g[inv[e]]`` over each target's edges."""
+    n_targets = row_ptr.shape[0] - 1
+    out = torch.empty(n_targets, rows_g.shape[1], dtype=rows_g.dtype, device=rows_g.device)
+    if n_targets == 0:
+        return out
+    _call("gm_factored_aggregate_gather_f32", _ptr(rows_g), _ptr(inv), _ptr(weights), _ptr(row_ptr), n_targets,
+          rows_g.shape[0], rows_g.shape[1], _ptr(out), _stream(rows_g.device))
+    return out

@@ -35,7 +35,7 @@ import torch.utils.checkpoint
 from torch import Tensor, nn
 
 from gm_attention_amd.discretization.discretization import SphericalDiscretization
-from gm_attention_amd.nn import fused_attention, fused_factored
+from gm_attention_amd.nn import fused_attention, fused_factored, radial
 from gm_attention_amd.nn.kernels import SO2SteerableKernel
 from gm_attention_amd.nn.linear import SO2Linear, apply_linear
 from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
@@ -204,8 +204,24 @@ def _attend_batched(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> dict[int, Tenso
 
 def _aggregated_factored(mhsa: SO2MHSA, x: SO2FeatureField, edges, alpha: Tensor) -> dict[int, Tensor]:
     """Every head's value kernel, factored and aggregated under its attention
-    weights, with one source grouping for all heads (:801-822)."""
+    weights, with one source grouping for all heads (:801-822).
+
+    All heads go through one pass (``fused_factored.forward_aggregated_heads``):
+    the trunk features of every head from one HIP trunk pass (or the heads'
+    own trunks when that kernel does not serve them), every head's node
+    mixes from one matrix product per input frequency, then the fused factored
+    op per head on those mixes in place."""
     groups = fused_factored.groups_for(edges, edges.source_index)
+    kernels = [cast(SO2SteerableKernel, head.value) for head in mhsa.heads]
+    if fused_factored.enabled(kernels[0], x, edges):
+        if radial.eligible(kernels, x.dtype, x.device):
+            h, trunk = None, functools.partial(radial.trunk_hidden_heads, kernels)
+        else:
+            h, trunk = torch.stack([k._trunk_hidden(edges.distances) for k in kernels]), None
+        out = fused_factored.forward_aggregated_heads(kernels, x, edges, alpha, h, groups, trunk)  # (N, H, d_out)
+        attn = mhsa.field_type_attn
+        return _concatenate_heads([SO2FeatureField.from_flat(attn, o) for o in out.unbind(1)],
+                                  mhsa.field_type_in).coefficients
     fields = []
     for head, weights in zip(mhsa.heads, alpha.unbind(1), strict=True):
         kernel = cast(SO2SteerableKernel, head.value)

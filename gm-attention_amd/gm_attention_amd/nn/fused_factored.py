@@ -311,3 +311,324 @@ def forward_aggregated(kernel: Any, x: SO2FeatureField, edges: Any, weights: Ten
                                    i.desc, i.source, edges.target_index.contiguous(), edges.row_ptr.contiguous(),
                                    order, group_ptr, group_source, i.plan.d_out, i.plan.max_bm)
     return SO2FeatureField.from_flat(kernel.field_type_out, flat)
+
+
+# ---------------------------------------------------------------- every head at once
+
+
+@dataclass(frozen=True)
+class HeadsPlan:
+    """The heads' common plan with the complex blocks' mixes packed by input
+    frequency (their columns in ``zc`` grouped by the node vector's frequency
+    n, in descriptor order within a frequency), so one matrix product per
+    input frequency yields every head's mixes where the op reads them.
+
+    ``groups[n] = (blocks reading x_n in packed order, complex width, real width)``."""
+
+    plan: Plan
+    desc_rows: tuple[tuple[int, ...], ...]
+    groups: tuple[tuple[int, tuple[Block, ...], int, int], ...]  # (n, blocks, 2 * complex columns, real columns)
+
+
+def heads_plan(kernel: Any) -> HeadsPlan:
+    cached = kernel.__dict__.get("_fused_heads_plan")
+    if cached is not None:
+        return cached
+    base = plan(kernel)
+    by_n: dict[int, list[Block]] = {}
+    real: list[Block] = []
+    for b in base.blocks:
+        (real if b.kind == 0 else by_n.setdefault(b.block[0], [])).append(b)
+    offset = 0
+    zoff: dict[tuple[int, int, str], int] = {}
+    groups = []
+    for n in sorted(set(by_n) | ({0} if real else set())):
+        blocks = by_n.get(n, [])
+        for b in blocks:
+            zoff[b.block] = offset
+            offset += b.b_m
+        width = 2 * sum(b.b_m for b in blocks)
+        groups.append((n, tuple(blocks) + (tuple(real) if n == 0 else ()), width, base.wr if n == 0 else 0))
+    rows = []
+    for b in base.blocks:
+        row = b.row()
+        if b.kind == 1:
+            row[1] = zoff[b.block]
+        rows.append(tuple(row))
+    result = HeadsPlan(base, tuple(rows), tuple(groups))
+    kernel.__dict__["_fused_heads_plan"] = result
+    return result
+
+
+def heads_mixing(kernels: list[Any], hp: HeadsPlan) -> list[Tensor]:
+    """Per input frequency n, ``M_n`` of ``(reals of x_n, H * K * C_n)``: columns
+    ``(head, t, [complex pairs in packed order | the real block's columns])``,
+    so ``X_n M_n`` is every head's ``Z_t`` for the blocks reading x_n."""
+    from gm_attention_amd.nn.node_products import mixing_matrix
+
+    mats = []
+    for n, blocks, _cw, _rw in hp.groups:
+        per_head = []
+        for k in kernels:
+            pieces = []
+            for b in blocks:
+                w = k._block_weights(b.block)  # (b_m, a_n, K)
+                if b.kind == 0:
+                    m = mixing_matrix(w, "real")  # (a_0, K * b_0)
+                    pieces.append(m.reshape(m.shape[0], w.shape[-1], -1))
+                    continue
+                bn, bm, role = b.block
+                mode = "promote" if bn == 0 else ("conj" if (bm == 0 or role == "antilinear") else "plain")
+                m = mixing_matrix(w, mode)  # (w_n, K * b_m * 2)
+                pieces.append(m.reshape(m.shape[0], w.shape[-1], -1))
+            per_head.append(torch.cat(pieces, dim=-1))  # (w_n, K, C_n)
+        stacked = torch.stack(per_head, dim=1)  # (w_n, H, K, C_n)
+        mats.append(stacked.reshape(stacked.shape[0], -1))
+    return mats
+
+
+def node_vectors(x: SO2FeatureField, hp: HeadsPlan) -> list[Tensor]:
+    """The node field's reals each input frequency's product reads."""
+    n_nodes = x.batch_shape[0]
+    return [x[0] if n == 0 else x[n].reshape(n_nodes, -1) for n, *_ in hp.groups]
+
+
+class FactoredHeads(torch.autograd.Function):
+    """Every head's factored value aggregation on the mixes ``X_n M_n``.
+
+    Inputs: ``h (H, E, T)``, ``alpha (E, H)``, then one ``(N, H * K * C_n)`` mix
+    array per input frequency; out ``(N, H, d_out)``.  The backward returns
+    ``dh``, ``dalpha`` and the mix arrays' gradients (written in place by the
+    HIP backward), so autograd carries them through the products to the
+    node field and the heads' readout weights."""
+
+    @staticmethod
+    def forward(ctx: Any, h: Tensor, alpha: Tensor, meta: dict, *mixes: Tensor) -> Tensor:
+        H, E = h.shape[0], h.shape[1]
+        N = meta["n_nodes"]
+        ext = extension()
+        rows, outs = [], []
+        for head in range(H):
+            runs = _heads_runs(meta, mixes, head, None)
+            with torch.profiler.record_function("gm::kernel/pairs"):
+                r = _native.factored_forward_seg(h[head], runs, N, meta["angular"], meta["transport"], meta["rho"],
+                                                 meta["desc"], meta["order"], meta["group_ptr"], meta["group_source"],
+                                                 meta["K"], meta["wc"], meta["wr"], meta["d_out"], meta["max_bm"])
+            with torch.profiler.record_function("gm::kernel/aggregate"):
+                outs.append(ext.aggregate(r, alpha[:, head].contiguous(), meta["row_ptr"]))
+            rows.append(r)
+        ctx.meta = meta
+        ctx.save_for_backward(h, alpha, *rows, *mixes)
+        return torch.stack(outs, dim=1)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx: Any, grad: Tensor) -> tuple:
+        meta = ctx.meta
+        saved = ctx.saved_tensors
+        h, alpha = saved[0], saved[1]
+        H = h.shape[0]
+        rows, mixes = saved[2:2 + H], saved[2 + H:]
+        dmixes = [torch.zeros_like(m) for m in mixes]
+        dh = torch.empty_like(h)
+        dalpha = torch.empty_like(alpha)
+        for head in range(H):
+            runs = _heads_runs(meta, mixes, head, dmixes)
+            with torch.profiler.record_function("gm::kernel/pairs_backward"):
+                dw = _native.factored_backward_seg(grad[:, head].contiguous(), meta["target"],
+                                                   alpha[:, head].contiguous(), rows[head], h[head], runs,
+                                                   meta["n_nodes"], meta["angular"], meta["transport"], meta["rho"],
+                                                   meta["desc"], meta["order"], meta["group_ptr"],
+                                                   meta["group_source"], meta["K"], meta["wc"], meta["wr"], dh[head])
+            dalpha[:, head] = dw
+        return (dh, dalpha, None, *dmixes)
+
+
+def _heads_runs(meta: dict, mixes: tuple[Tensor, ...], head: int, grads: list[Tensor] | None) -> _native.MixRuns:
+    """Head ``head``'s mix runs in packed-column order: every input
+    frequency's complex columns, then the real block's."""
+    K, H = meta["K"], meta["heads"]
+    complex_runs, real_runs = [], []
+    for (n, _blocks, cw, rw), mix in zip(meta["groups"], mixes, strict=True):
+        C = cw + rw
+        base = head * K * C
+        if cw:
+            complex_runs.append((mix, base, H * K * C, C, cw))
+        if rw:
+            real_runs.append((mix, base + cw, H * K * C, C, rw))
+    runs = complex_runs + real_runs
+    views = [(m.view(-1)[off:], ns, ts, w) for m, off, ns, ts, w in runs]
+    grad_views = None
+    if grads is not None:
+        by_id = {id(m): g for m, g in zip(mixes, grads, strict=True)}
+        grad_views = [by_id[id(m)].view(-1)[off:] for m, off, *_ in runs]
+    return _native.MixRuns(views, grad_views)
+
+
+@dataclass
+class GroupedStreams:
+    """An edge set's per-edge streams in the order of its source grouping:
+    ``perm`` (= the grouping's order), its inverse ``inv``, ``rho_g``, the
+    phase rows ``phase_g (E, 8, 2)`` (angular orders ``0..pa-1`` then
+    transport orders ``0..pt-1``) and ``target_g``."""
+
+    perm: Tensor
+    inv: Tensor
+    rho_g: Tensor
+    phase_g: Tensor
+    target_g: Tensor
+    pa: int
+    pt: int
+
+
+_STREAMS: OrderedDict[tuple, tuple[Any, GroupedStreams]] = OrderedDict()
+
+
+def grouped_streams(edges: Any, order: Tensor, cutoff: float, pa: int, pt: int, dtype: torch.dtype) -> GroupedStreams:
+    """The grouped streams of ``edges`` under ``order``, cached while the edge set lives."""
+    key = (id(edges.edge_index), edges.edge_index.data_ptr(), int(edges.n_edges), order.data_ptr(), float(cutoff), pa,
+           pt, dtype)
+    hit = _STREAMS.get(key)
+    if hit is not None and hit[0]() is edges.edge_index:
+        return hit[1]
+    with torch.profiler.record_function("gm::kernel/group_streams"):
+        perm = order
+        inv = torch.empty_like(perm)
+        inv[perm] = torch.arange(perm.shape[0], device=perm.device)
+        rho_g = (edges.distances.index_select(0, perm) / cutoff).to(dtype).contiguous()
+        ang = torch.view_as_real(edges.angular_phases[:, :pa].index_select(0, perm))
+        tra = torch.view_as_real(edges.transport_phases[:, :pt].index_select(0, perm))
+        phase_g = torch.zeros(perm.shape[0], 8, 2, dtype=dtype, device=perm.device)
+        phase_g[:, :pa] = ang.to(dtype)
+        phase_g[:, pa:pa + pt] = tra.to(dtype)
+        streams = GroupedStreams(perm, inv, rho_g, phase_g.contiguous(),
+                                 edges.target_index.index_select(0, perm).contiguous(), pa, pt)
+    for stale in [k for k, (ref, _) in _STREAMS.items() if ref() is None]:
+        del _STREAMS[stale]
+    _STREAMS[key] = (weakref.ref(edges.edge_index), streams)
+    while len(_STREAMS) > 8:
+        _STREAMS.popitem(last=False)
+    return streams
+
+
+def grouped_eligible(hp: HeadsPlan, h_dtype: torch.dtype, K: int) -> tuple[bool, int, int]:
+    """Whether the heads take the grouped kernels (fp32, K = 17, <= 128 packed
+    columns, phase orders within one 8-pair row); with (pa, pt)."""
+    p = hp.plan
+    pa = max((abs(b.angular) for b in p.blocks), default=0) + 1
+    pt = max((abs(b.transport) for b in p.blocks), default=0) + 1
+    ok = (h_dtype == torch.float32 and K == 17 and 2 * p.wc + p.wr <= 128 and pa + pt <= 8
+          and os.environ.get("GM_FACTORED_GROUPED", "1") != "0")
+    return ok, pa, pt
+
+
+class FactoredHeadsGrouped(torch.autograd.Function):
+    """:class:`FactoredHeads` over the grouped streams: ``h_g (H, E, 16)`` in
+    the grouping's order, ``alpha (E, H)`` in edge order, the mix arrays;
+    out ``(N, H, d_out)``; gradients ``dh_g``, ``dalpha`` and the mixes'."""
+
+    @staticmethod
+    def forward(ctx: Any, h_g: Tensor, alpha: Tensor, meta: dict, *mixes: Tensor) -> Tensor:
+        H = h_g.shape[0]
+        st: GroupedStreams = meta["streams"]
+        rows, outs = [], []
+        for head in range(H):
+            runs = _heads_runs(meta, mixes, head, None)
+            with torch.profiler.record_function("gm::kernel/pairs"):
+                r = _native.factored_forward_grouped(h_g[head], runs, meta["n_nodes"], st.phase_g, st.rho_g, st.pa,
+                                                     st.pt, meta["desc"], meta["group_ptr"], meta["group_source"],
+                                                     meta["K"], meta["wc"], meta["wr"], meta["d_out"])
+            with torch.profiler.record_function("gm::kernel/aggregate"):
+                outs.append(_native.aggregate_gather(r, st.inv, alpha[:, head].contiguous(), meta["row_ptr"]))
+            rows.append(r)
+        ctx.meta = meta
+        ctx.save_for_backward(h_g, alpha, *rows, *mixes)
+        return torch.stack(outs, dim=1)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx: Any, grad: Tensor) -> tuple:
+        meta = ctx.meta
+        st: GroupedStreams = meta["streams"]
+        saved = ctx.saved_tensors
+        h_g, alpha = saved[0], saved[1]
+        H = h_g.shape[0]
+        rows, mixes = saved[2:2 + H], saved[2 + H:]
+        dmixes = [torch.zeros_like(m) for m in mixes]
+        dh_g = torch.empty_like(h_g)
+        alpha_g = alpha.index_select(0, st.perm)
+        dalpha_g = torch.empty_like(alpha_g)
+        for head in range(H):
+            runs = _heads_runs(meta, mixes, head, dmixes)
+            with torch.profiler.record_function("gm::kernel/pairs_backward"):
+                dalpha_g[:, head] = _native.factored_backward_grouped(
+                    grad[:, head].contiguous(), st.target_g, alpha_g[:, head].contiguous(), rows[head], h_g[head], runs,
+                    meta["n_nodes"], st.phase_g, st.rho_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
+                    meta["group_source"], meta["K"], meta["wc"], meta["wr"], dh_g[head])
+        dalpha = torch.empty_like(alpha)
+        dalpha.index_copy_(0, st.perm, dalpha_g)
+        return (dh_g, dalpha, None, *dmixes)
+
+
+def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any, alpha: Tensor, h: Tensor | None,
+                             groups: tuple[Tensor, Tensor, Tensor], trunk=None) -> Tensor:
+    """Every head's ``forward_factored_aggregated`` at once: ``(N, H, d_out)``.
+
+    ``h`` is every head's trunk features in edge order; alternatively
+    ``trunk(rho)`` computes them from ``rho = d / cutoff`` in whatever order
+    it is given, which lets the grouped kernels have them in the grouping's
+    order directly."""
+    hp = heads_plan(kernels[0])
+    K = (h.shape[2] if h is not None else kernels[0].complex_head.in_features) + 1
+    dtype = h.dtype if h is not None else x.dtype
+    ok, pa, pt = grouped_eligible(hp, dtype, K)
+    if ok:
+        p = hp.plan
+        mats = heads_mixing(kernels, hp)
+        vecs = node_vectors(x, hp)
+        with torch.profiler.record_function("gm::kernel/node_products"):
+            mixes = [v @ m.to(v.dtype) for v, m in zip(vecs, mats, strict=True)]
+        order, group_ptr, group_source = groups
+        st = grouped_streams(edges, order, kernels[0].radial_basis.cutoff, pa, pt, dtype)
+        h_g = trunk(st.rho_g) if trunk is not None else h.index_select(1, st.perm)
+        meta = dict(n_nodes=x.batch_shape[0], heads=len(kernels), K=K, wc=p.wc, wr=p.wr, d_out=p.d_out,
+                    groups=hp.groups, desc=_heads_desc(kernels[0], hp, x.device), group_ptr=group_ptr,
+                    group_source=group_source, row_ptr=edges.row_ptr.contiguous(), streams=st)
+        return FactoredHeadsGrouped.apply(h_g.contiguous(), alpha.to(dtype).contiguous(), meta, *mixes)
+    if h is None:
+        h = trunk((edges.distances / kernels[0].radial_basis.cutoff).to(dtype).contiguous())
+    return _forward_aggregated_heads_seg(kernels, x, edges, alpha, h, groups)
+
+
+def _heads_desc(kernel: Any, hp: HeadsPlan, device: torch.device) -> Tensor:
+    key = ("_fused_heads_desc", str(device))
+    desc = kernel.__dict__.get(key)
+    if desc is None:
+        desc = torch.tensor([list(r) for r in hp.desc_rows], dtype=torch.int32, device=device)
+        kernel.__dict__[key] = desc
+    return desc
+
+
+def _forward_aggregated_heads_seg(kernels: list[Any], x: SO2FeatureField, edges: Any, alpha: Tensor, h: Tensor,
+                                  groups: tuple[Tensor, Tensor, Tensor]) -> Tensor:
+    """Every head's ``forward_factored_aggregated`` at once: ``(N, H, d_out)``."""
+    hp = heads_plan(kernels[0])
+    p = hp.plan
+    mats = heads_mixing(kernels, hp)
+    vecs = node_vectors(x, hp)
+    with torch.profiler.record_function("gm::kernel/node_products"):
+        mixes = [v @ m.to(v.dtype) for v, m in zip(vecs, mats, strict=True)]
+    order, group_ptr, group_source = groups
+    angular = torch.view_as_real(edges.angular_phases.contiguous()).contiguous().to(h.dtype)
+    transport = torch.view_as_real(edges.transport_phases.contiguous()).contiguous().to(h.dtype)
+    needed = max((max(abs(b.angular), abs(b.transport)) for b in p.blocks), default=0)
+    if needed >= angular.shape[1]:
+        raise ValueError(f"the geometry's phase tables ({angular.shape[1]} orders) are narrower than the kernel's "
+                         f"blocks need (order {needed})")
+    desc = _heads_desc(kernels[0], hp, h.device)
+    meta = dict(n_nodes=x.batch_shape[0], heads=len(kernels), K=h.shape[2] + 1, wc=p.wc, wr=p.wr, d_out=p.d_out,
+                max_bm=p.max_bm, groups=hp.groups, angular=angular, transport=transport,
+                rho=(edges.distances / kernels[0].radial_basis.cutoff).to(h.dtype).contiguous(), desc=desc,
+                order=order, group_ptr=group_ptr, group_source=group_source,
+                target=edges.target_index.contiguous(), row_ptr=edges.row_ptr.contiguous())
+    return FactoredHeads.apply(h, alpha.to(h.dtype).contiguous(), meta, *mixes)

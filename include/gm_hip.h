@@ -53,6 +53,7 @@ enum {
 #define GM_FACT_MAX_BM 32
 #define GM_FACT_MAX_C 320
 #define GM_FACT_MAX_BLOCKS 64
+#define GM_FACT_MAX_SEG 4
 
 /* The calling thread's last error message ("" when none). */
 const char* gm_last_error(void);
@@ -209,6 +210,102 @@ int gm_factored_backward_f64(const double* g, const int64_t* target, const doubl
                              const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges,
                              int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks,
                              int64_t d_out, double* dh, double* dzc, double* dzr, double* dweights, void* stream);
+
+/* The same forward and backward with the node mixes as up to GM_FACT_MAX_SEG
+ * runs of packed columns: run r covers columns [c_r, c_r + width[r]) (runs in
+ * column order, tiling [0, 2 wc + wr), none straddling the boundary 2 wc), and
+ * column c of node j at mix t is z[r][j * node_stride[r] + t * t_stride[r] +
+ * (c - c_r)]; the backward writes dZ to dz[r] at the same places (the caller
+ * zeroes them first).  The arrays are HOST memory; the runs are device memory.
+ * With this layout the node mixes of every head and input frequency come from
+ * one matrix product per input frequency and are read where they were
+ * written, with no packing copy.  No counterpart in the reference: zc / zr
+ * of gm_factored.forward / backward_aggregated are the two-run case
+ * (fused_factored.py:247-299); its batched attention packs every head's
+ * node products with a concatenation instead (fused_factored.py:156-180). */
+int gm_factored_forward_seg_f32(const float* h, const float* const* z, const int64_t* node_stride,
+                                const int64_t* t_stride, const int64_t* width, int64_t n_runs, const float* angular,
+                                const float* transport, const float* rho, const int32_t* desc, const int64_t* order,
+                                const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes,
+                                int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f,
+                                int64_t n_blocks, int64_t d_out, int64_t max_bm, float* out, void* stream);
+int gm_factored_forward_seg_f64(const double* h, const double* const* z, const int64_t* node_stride,
+                                const int64_t* t_stride, const int64_t* width, int64_t n_runs, const double* angular,
+                                const double* transport, const double* rho, const int32_t* desc, const int64_t* order,
+                                const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes,
+                                int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f,
+                                int64_t n_blocks, int64_t d_out, int64_t max_bm, double* out, void* stream);
+int gm_factored_backward_seg_f32(const float* g, const int64_t* target, const float* weights, const float* rows,
+                                 const float* h, const float* const* z, float* const* dz, const int64_t* node_stride,
+                                 const int64_t* t_stride, const int64_t* width, int64_t n_runs, const float* angular,
+                                 const float* transport, const float* rho, const int32_t* desc, const int64_t* order,
+                                 const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes,
+                                 int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t n_f,
+                                 int64_t n_blocks, int64_t d_out, float* dh, float* dweights, void* stream);
+int gm_factored_backward_seg_f64(const double* g, const int64_t* target, const double* weights, const double* rows,
+                                 const double* h, const double* const* z, double* const* dz,
+                                 const int64_t* node_stride, const int64_t* t_stride, const int64_t* width,
+                                 int64_t n_runs, const double* angular, const double* transport, const double* rho,
+                                 const int32_t* desc, const int64_t* order, const int64_t* group_ptr,
+                                 const int64_t* group_source, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
+                                 int64_t K, int64_t wc, int64_t wr, int64_t n_f, int64_t n_blocks, int64_t d_out,
+                                 double* dh, double* dweights, void* stream);
+
+/* The same forward and backward (fp32, K = 17, at most 128 packed columns)
+ * with every per-edge stream in the order of the source grouping: row g of
+ * h_g (n_edges, 16), phase_g (n_edges, 8, 2) -- the angular orders 0..pa-1
+ * then the transport orders 0..pt-1 as re/im pairs, pa + pt <= 8 --, rho_g,
+ * target_g, weights_g, rows_g (n_edges, d_out), dh_g and dweights_g belongs to
+ * the g-th edge of the grouping (order[g] in the others' terms).  A tile's
+ * loads are then contiguous and issued before the previous tile finishes.
+ * The mixes come as runs (see gm_factored_forward_seg_*).  No counterpart in
+ * the reference, whose kernels index every per-edge table through the
+ * grouping (factored_cuda.cu:70-89, 133-248); the results equal those of
+ * gm_factored_forward_seg / backward_seg on the permuted streams. */
+int gm_factored_forward_grouped_f32(const float* h_g, const float* const* z, const int64_t* node_stride,
+                                    const int64_t* t_stride, const int64_t* width, int64_t n_runs,
+                                    const float* phase_g, const float* rho_g, const int32_t* desc,
+                                    const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes,
+                                    int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa,
+                                    int64_t pt, int64_t n_blocks, int64_t d_out, float* rows_g, void* stream);
+int gm_factored_backward_grouped_f32(const float* g, const int64_t* target_g, const float* weights_g,
+                                     const float* rows_g, const float* h_g, const float* const* z, float* const* dz,
+                                     const int64_t* node_stride, const int64_t* t_stride, const int64_t* width,
+                                     int64_t n_runs, const float* phase_g, const float* rho_g, const int32_t* desc,
+                                     const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes,
+                                     int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa,
+                                     int64_t pt, int64_t n_blocks, int64_t d_out, float* dh_g, float* dweights_g,
+                                     void* stream);
+
+/* gm_factored_aggregate with edge e's row at rows[inv[e]] (rows kept in the
+ * grouping's order; inv is the grouping's inverse permutation). */
+int gm_factored_aggregate_gather_f32(const float* rows, const int64_t* inv, const float* weights,
+                                     const int64_t* row_ptr, int64_t n_targets, int64_t n_edges, int64_t d_out,
+                                     float* out, void* stream);
+
+/* ---------------- radial trunk ----------------
+ *
+ * Every head's radial trunk over the edges in one pass: with r = rho[e] and
+ * s = r^2, the basis b_k = exp(-((s - centers[k]) / width)^2 / 2) (k < B) and
+ * h[head, e, t] = SiLU(sum_k weight[head, t, k] b_k + bias[head, t]) (t < T).
+ * T = 16 and B in {4, 6, 8} (the reference's default trunk (16,) over
+ * n_radial_basis functions); fp32; h (H, E, T) written.
+ * Replaces, for all H heads at once, SO2SteerableKernel._trunk_hidden
+ * (nn/kernels.py:605-607): _GaussianRadialBasis (:191-231) then
+ * apply_radial_trunk's Linear + SiLU (:108-117). */
+int gm_radial_trunk_forward_f32(const float* rho, const float* weight, const float* bias, const float* centers,
+                                int64_t n_edges, int64_t H, int64_t T, int64_t B, double width, float* h,
+                                void* stream);
+
+/* The trunk's parameter gradients from dh (H, E, T): dparams (H, T * B + T) =
+ * per head dweight (T, B) then dbias (T), summed over the edges in a fixed
+ * order through `partial`, a workspace of gm_radial_trunk_partials(n_edges)
+ * * H * (T * B + T) floats.  Replaces the weight and bias gradients of the
+ * reference's split_k_linear (nn/kernels.py:49-105) for the trunk layer. */
+int64_t gm_radial_trunk_partials(int64_t n_edges);
+int gm_radial_trunk_backward_f32(const float* dh, const float* rho, const float* weight, const float* bias,
+                                 const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B, double width,
+                                 float* partial, float* dparams, void* stream);
 
 #ifdef __cplusplus
 }

@@ -167,3 +167,10 @@ def test_single_head_attention_matches_the_oracle(cuda):
     close(got[0], want[0], torch.float64, "out")
     for n in want[1]:
         close(got[1][n], want[1][n], torch.float64, f"d{n}")
+
+
+def test_mhsa_float32_on_the_run_kernels_matches_the_oracle(cuda, monkeypatch):
+    """The batched layer with the grouped kernels switched off (every head on
+    the mix-run kernels), float32, against the oracle."""
+    monkeypatch.setenv("GM_FACTORED_GROUPED", "0")
+    test_mhsa_matches_the_oracle(CASES[0], torch.float32, True, cuda)
