@@ -225,6 +225,9 @@ def main() -> None:
     timer.wrap(fac, "backward_aggregated", "factored_backward_aggregated")
     timer.wrap(_native, "factored_forward_seg", "factored_forward")
     timer.wrap(_native, "factored_backward_seg", "factored_backward_aggregated")
+    timer.wrap(_native, "factored_forward_grouped", "factored_forward")
+    timer.wrap(_native, "factored_backward_grouped", "factored_backward_aggregated")
+    timer.wrap(_native, "aggregate_gather", "factored_aggregate")
     timer.wrap(_native, "radial_trunk_forward", "radial_trunk_forward")
     timer.wrap(_native, "radial_trunk_backward", "radial_trunk_backward")
 

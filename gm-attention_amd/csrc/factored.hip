@@ -84,6 +84,7 @@ struct FactArgs {
   const float* phase_g;
   const float* rho_g;
   const int64_t* target_g;
+  const int64_t* group_order;  // the groups in launch order (largest first), or null
   int pa, pt;
 };
 
@@ -810,7 +811,8 @@ __global__ __launch_bounds__(64) void factored_forward_grouped(FactArgs<float> a
   for (int i = lane; i <= d_out; i += kWave) optr[i] = a.optr[i];
   for (int i = lane; i < a.optr[d_out]; i += kWave) olist[i] = a.olist[i];
   stage_desc(a, Bd, lane);
-  const int64_t gi = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
+  if (gi < 0 || gi >= a.n_groups) return;  // a malformed order names no group
   const int64_t j = a.group_source[gi];
   const int64_t g0 = a.group_ptr[gi], g1 = a.group_ptr[gi + 1];
   float za[NT][4], z0[NT][4];
@@ -892,7 +894,8 @@ __global__ __launch_bounds__(64) void factored_backward_grouped(FactArgs<float> 
   float* Ht = Wt + kMT * WP;                                       // [kMT][16]
   const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
   stage_desc(a, Bd, lane);
-  const int64_t gi = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
+  if (gi < 0 || gi >= a.n_groups) return;  // a malformed order names no group
   const int64_t j = a.group_source[gi];
   const int64_t g0 = a.group_ptr[gi], g1 = a.group_ptr[gi + 1];
   float zb[4 * NT];
@@ -1463,8 +1466,9 @@ GM_FACT_EXPORTS(double, f64)
 extern "C" int gm_factored_forward_grouped_f32(
     const float* h_g, const float* const* z, const int64_t* node_stride, const int64_t* t_stride,
     const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const int32_t* desc,
-    const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
-    int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks, int64_t d_out, float* rows_g,
+    const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order, int64_t n_nodes,
+    int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
+    int64_t d_out, float* rows_g,
     void* stream) {
   GM_REQUIRE(z && node_stride && t_stride && width, "the mix runs must be host arrays");
   const gm::Runs<float> runs{z, nullptr, node_stride, t_stride, width, n_runs};
@@ -1475,6 +1479,7 @@ extern "C" int gm_factored_forward_grouped_f32(
   if (n_edges == 0 || n_groups == 0) return GM_OK;
   GM_REQUIRE(rows_g, "rows must be a device pointer");
   a.out = rows_g;
+  a.group_order = group_order;
   gm::launch_grouped(true, a, (hipStream_t)stream);
   return gm::check_launch("factored_forward_grouped");
 }
@@ -1483,8 +1488,9 @@ extern "C" int gm_factored_backward_grouped_f32(
     const float* g, const int64_t* target_g, const float* weights_g, const float* rows_g, const float* h_g,
     const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
     const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const int32_t* desc,
-    const int64_t* group_ptr, const int64_t* group_source, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
-    int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks, int64_t d_out, float* dh_g,
+    const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order, int64_t n_nodes,
+    int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
+    int64_t d_out, float* dh_g,
     float* dweights_g, void* stream) {
   GM_REQUIRE(z && dz && node_stride && t_stride && width, "the mix runs must be host arrays");
   const gm::Runs<float> runs{z, dz, node_stride, t_stride, width, n_runs};
@@ -1497,6 +1503,7 @@ extern "C" int gm_factored_backward_grouped_f32(
              "g, target_g, weights_g, rows_g, dh_g and dweights_g must be device pointers");
   for (int r = 0; r < a.n_seg; ++r) GM_REQUIRE(a.seg[r].dz != nullptr, "every mix gradient run must be a device pointer");
   a.g = g;
+  a.group_order = group_order;
   a.target_g = target_g;
   a.weights = weights_g;
   a.rows = rows_g;

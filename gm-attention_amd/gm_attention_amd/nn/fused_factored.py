@@ -479,6 +479,7 @@ class GroupedStreams:
     target_g: Tensor
     pa: int
     pt: int
+    group_order: Tensor | None = None
 
 
 _STREAMS: OrderedDict[tuple, tuple[Any, GroupedStreams]] = OrderedDict()
@@ -537,7 +538,8 @@ class FactoredHeadsGrouped(torch.autograd.Function):
             with torch.profiler.record_function("gm::kernel/pairs"):
                 r = _native.factored_forward_grouped(h_g[head], runs, meta["n_nodes"], st.phase_g, st.rho_g, st.pa,
                                                      st.pt, meta["desc"], meta["group_ptr"], meta["group_source"],
-                                                     meta["K"], meta["wc"], meta["wr"], meta["d_out"])
+                                                     meta["group_order"], meta["K"], meta["wc"], meta["wr"],
+                                                     meta["d_out"])
             with torch.profiler.record_function("gm::kernel/aggregate"):
                 outs.append(_native.aggregate_gather(r, st.inv, alpha[:, head].contiguous(), meta["row_ptr"]))
             rows.append(r)
@@ -564,7 +566,7 @@ class FactoredHeadsGrouped(torch.autograd.Function):
                 dalpha_g[:, head] = _native.factored_backward_grouped(
                     grad[:, head].contiguous(), st.target_g, alpha_g[:, head].contiguous(), rows[head], h_g[head], runs,
                     meta["n_nodes"], st.phase_g, st.rho_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
-                    meta["group_source"], meta["K"], meta["wc"], meta["wr"], dh_g[head])
+                    meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"], dh_g[head])
         dalpha = torch.empty_like(alpha)
         dalpha.index_copy_(0, st.perm, dalpha_g)
         return (dh_g, dalpha, None, *dmixes)
@@ -591,9 +593,13 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
         order, group_ptr, group_source = groups
         st = grouped_streams(edges, order, kernels[0].radial_basis.cutoff, pa, pt, dtype)
         h_g = trunk(st.rho_g) if trunk is not None else h.index_select(1, st.perm)
+        if st.group_order is None and os.environ.get("GM_FACTORED_LPT", "0") == "1":
+            # the groups largest first: the long pole groups start early instead of trailing the launch
+            st.group_order = torch.argsort(group_ptr[1:] - group_ptr[:-1], descending=True, stable=True).contiguous()
         meta = dict(n_nodes=x.batch_shape[0], heads=len(kernels), K=K, wc=p.wc, wr=p.wr, d_out=p.d_out,
                     groups=hp.groups, desc=_heads_desc(kernels[0], hp, x.device), group_ptr=group_ptr,
-                    group_source=group_source, row_ptr=edges.row_ptr.contiguous(), streams=st)
+                    group_source=group_source, row_ptr=edges.row_ptr.contiguous(), streams=st,
+                    group_order=st.group_order if os.environ.get("GM_FACTORED_LPT", "0") == "1" else None)
         return FactoredHeadsGrouped.apply(h_g.contiguous(), alpha.to(dtype).contiguous(), meta, *mixes)
     if h is None:
         h = trunk((edges.distances / kernels[0].radial_basis.cutoff).to(dtype).contiguous())

@@ -174,3 +174,10 @@ def test_mhsa_float32_on_the_run_kernels_matches_the_oracle(cuda, monkeypatch):
     the mix-run kernels), float32, against the oracle."""
     monkeypatch.setenv("GM_FACTORED_GROUPED", "0")
     test_mhsa_matches_the_oracle(CASES[0], torch.float32, True, cuda)
+
+
+def test_mhsa_float32_with_largest_first_groups_matches_the_oracle(cuda, monkeypatch):
+    """The grouped kernels launched in largest-first group order (an explicit
+    group_order permutation), float32, against the oracle."""
+    monkeypatch.setenv("GM_FACTORED_LPT", "1")
+    test_mhsa_matches_the_oracle(CASES[0], torch.float32, True, cuda)
