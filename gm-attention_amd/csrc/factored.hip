@@ -86,6 +86,14 @@ struct FactArgs {
   const int64_t* target_g;
   const int64_t* group_order;  // the groups in launch order (largest first), or null
   int pa, pt;
+  // lane-owned output kernels: per-slot words, slot column -> packed column
+  // (0xFF padding), the backward's live dh k-steps (bit 4 nt + r), the LDS
+  // stride of a G row
+  uint32_t slot[16];
+  uint8_t slotcol[128];
+  uint32_t colslot32[32];  // packed column -> slot column, four bytes a word
+  uint32_t kmask;
+  int n_slots, gstride;
 };
 
 template <typename T>
@@ -997,6 +1005,641 @@ __global__ __launch_bounds__(64) void factored_backward_grouped(FactArgs<float> 
   }
 }
 
+// ------------------------------------------------------------ lane-owned outputs
+//
+// Plans whose blocks come in multiplicities of four, with radial power equal
+// to the angular order (F_b = (r e^{i phi})^a e^{i s gamma}: every plan the
+// steerable kernel builds), run on kernels where the four lanes sharing an
+// edge split every block by copy: lane q owns the copies k = q (mod 4).
+// A lane's slots are its (block, copy) pairs, ordered so that the blocks
+// summed into one output follow each other; slot s sits in MFMA column tile
+// s / 2 at register pair s % 2.  The forward then sums its own slots into its
+// own outputs in registers (no LDS pass over the row), and the backward forms
+// W in the same slots, takes dh straight from them on MFMA and transposes W
+// once through LDS for dZ.  Per-slot words:
+//   bits 0-6 the output base (+ q for scalar outputs, + 2 q for complex),
+//   7 active, 8 the real block (factor 1), 9 scalar output, 10 last slot of
+//   its output, 11-13 the angular entry, 14 its conjugate, 15-17 the
+//   transport entry, 18 its conjugate.
+// The words are compile-time constants for the plans the steerable kernel
+// builds with four copies per frequency and head (then the phases stay in
+// registers and every slot's code is fixed), kernel arguments otherwise.
+//
+// Every per-edge stream of a group is read and written through a buffer
+// resource bounded to the group: the lanes past the group's last edge load
+// zeros and their stores are dropped, so the tile loop has no branches and
+// the wait for the prefetched tile never waits on the tile's own stores.
+// Z(j) comes in (and dZ(j) goes out) through LDS in slot-column order, run by
+// run, with coalesced row reads.
+constexpr int kMaxSlots = 16;
+constexpr int kPhStride = 18;  // floats per LDS phase row: 16 + 2 puts the 16 rows' 8-byte reads in distinct banks
+constexpr int kWtStride = 20;  // floats per LDS W column (16 edges + 4): 16-byte aligned four-edge reads
+
+enum : uint32_t {
+  kSlotActive = 1u << 7,
+  kSlotReal = 1u << 8,
+  kSlotScalar = 1u << 9,
+  kSlotFlush = 1u << 10,
+  kSlotAConj = 1u << 14,
+  kSlotTConj = 1u << 18,
+};
+
+__host__ __device__ constexpr int slot_ob(uint32_t w) { return (int)(w & 0x7F); }
+__host__ __device__ constexpr int slot_ai(uint32_t w) { return (int)((w >> 11) & 7); }
+__host__ __device__ constexpr int slot_ti(uint32_t w) { return (int)((w >> 15) & 7); }
+
+// Compile-time slot words: PA angular entries in the phase row, DOUT floats a row.
+template <int PA, int DOUT, uint32_t... W>
+struct StaticSlots {
+  static constexpr bool kStatic = true;
+  static constexpr int kSlots = (int)sizeof...(W);
+  static constexpr int kPa = PA;
+  static constexpr int kDout = DOUT;
+  __host__ __device__ static constexpr uint32_t word(int s) {
+    constexpr uint32_t w[] = {W..., 0u};
+    return s >= 0 && s < kSlots ? w[s] : 0u;
+  }
+};
+struct RuntimeSlots {
+  static constexpr bool kStatic = false;
+  static constexpr int kSlots = kMaxSlots;
+  static constexpr int kPa = 0;
+  static constexpr int kDout = 0;
+  __host__ __device__ static constexpr uint32_t word(int) { return 0u; }
+};
+// frequencies 0..2, four copies each: 13 slots (one real, two onto frequency
+// 0 taking the real part, five onto each of frequencies 1 and 2)
+using SlotsF2 = StaticSlots<5, 20, 0x28380u, 0x70a80u, 0x79680u, 0x28884u, 0x30084u, 0x71084u, 0x3c884u, 0x79c84u,
+                            0x2908cu, 0x3088cu, 0x7188cu, 0x3808cu, 0x7a48cu>;
+// frequencies 0..1, four copies each: 5 slots
+using SlotsF1 = StaticSlots<3, 12, 0x18380u, 0x60e80u, 0x18884u, 0x20084u, 0x61484u>;
+
+template <class P>
+__device__ __forceinline__ uint32_t slot_word(const FactArgs<float>& a, int s) {
+  if constexpr (P::kStatic)
+    return P::word(s);
+  else
+    return a.slot[s];
+}
+
+// The first slot of slot s's output (its G and row values are loaded there).
+template <class P>
+__device__ __forceinline__ constexpr int group_start(int s) {
+  int b = s;
+  while (b > 0 && !(P::word(b - 1) & kSlotFlush)) --b;
+  return b;
+}
+
+// A (byte-addressed) buffer resource over n_bytes from p: reads past the end
+// return zero, writes past it are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span(const void* p, int64_t n_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n_bytes, 0x00020000);
+}
+__device__ __forceinline__ float bload1(__amdgpu_buffer_rsrc_t r, int off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ float2 bload2(__amdgpu_buffer_rsrc_t r, int off) {
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  const u2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+__device__ __forceinline__ int64_t bload_i64(__amdgpu_buffer_rsrc_t r, int off) {
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  const u2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return (int64_t)(((uint64_t)v[1] << 32) | v[0]);
+}
+__device__ __forceinline__ floatx4 bload4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ void bstore1(float v, __amdgpu_buffer_rsrc_t r, int off) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+}
+__device__ __forceinline__ void bstore2(float x, float y, __amdgpu_buffer_rsrc_t r, int off) {
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(u2{__float_as_uint(x), __float_as_uint(y)}, r, off, 0, 0);
+}
+__device__ __forceinline__ void bstore4(floatx4 v, __amdgpu_buffer_rsrc_t r, int off) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, off, 0, 0);
+}
+constexpr int kDrop = 0x7FFFFFF0;  // a byte offset past every group's span: the access is dropped
+
+// Z(j) into LDS in slot-column order, Zs[t * ZS + sc] for t < 17, zero in the
+// padding columns: each mix run's 17 x width block is read in index order
+// (coalesced), twelve elements a lane in flight at once, and scattered to its
+// slot columns through colslot.
+template <int ZS>
+__device__ __forceinline__ void stage_z_slots(const FactArgs<float>& a, int64_t j, float* Zs, const uint8_t* colslot,
+                                              int lane) {
+  for (int i = lane; i < 17 * ZS / 4; i += kWave) reinterpret_cast<floatx4*>(Zs)[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  wave_sync();
+  for (int r = 0; r < a.n_seg; ++r) {
+    const ZSeg<float>& g = a.seg[r];
+    const float* base = g.z + j * g.node_stride;
+    const int w = g.width, total = 17 * w, ts = g.t_stride, c0 = g.c0;
+    const float inv = 1.f / (float)w;
+    for (int i0 = 0; i0 < total; i0 += 12 * kWave) {
+      float v[12];
+      int dst[12];
+#pragma unroll
+      for (int u = 0; u < 12; ++u) {
+        const int idx = i0 + u * kWave + lane;
+        int t = (int)((float)idx * inv);
+        t -= t * w > idx;
+        t += (t + 1) * w <= idx;
+        const int cc = idx - t * w;
+        dst[u] = -1;
+        v[u] = 0.f;
+        if (idx < total) {
+          v[u] = base[(int64_t)t * ts + cc];
+          dst[u] = t * ZS + colslot[c0 + cc];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 12; ++u)
+        if (dst[u] >= 0) Zs[dst[u]] = v[u];
+    }
+  }
+  wave_sync();
+}
+
+// dZ(j) out of LDS (slot-column order) into the runs' gradient arrays.
+template <int ZS>
+__device__ __forceinline__ void flush_dz_slots(const FactArgs<float>& a, int64_t j, const float* Zs,
+                                               const uint8_t* colslot, int lane) {
+  for (int r = 0; r < a.n_seg; ++r) {
+    const ZSeg<float>& g = a.seg[r];
+    float* base = g.dz + j * g.node_stride;
+    const int w = g.width, total = 17 * w, ts = g.t_stride, c0 = g.c0;
+    const float inv = 1.f / (float)w;
+    for (int i0 = 0; i0 < total; i0 += 12 * kWave) {
+      float v[12];
+      int64_t dst[12];
+#pragma unroll
+      for (int u = 0; u < 12; ++u) {
+        const int idx = i0 + u * kWave + lane;
+        int t = (int)((float)idx * inv);
+        t -= t * w > idx;
+        t += (t + 1) * w <= idx;
+        const int cc = idx - t * w;
+        dst[u] = -1;
+        v[u] = 0.f;
+        if (idx < total) {
+          v[u] = Zs[t * ZS + colslot[c0 + cc]];
+          dst[u] = (int64_t)t * ts + cc;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 12; ++u)
+        if (dst[u] >= 0) base[dst[u]] = v[u];
+    }
+  }
+}
+
+// The rows of packed column -> slot column, into LDS (128 bytes).
+__device__ __forceinline__ void stage_colslot(const FactArgs<float>& a, uint8_t* colslot, int lane) {
+  if (lane < 32) reinterpret_cast<uint32_t*>(colslot)[lane] = a.colslot32[lane];
+}
+
+// A tile's phase row entries o = 1 .. 7 of the lane's edge, the angular ones
+// (o < PA) scaled by rho^o: chunk k of the row (entries 2 k, 2 k + 1) in
+// ph[k].  Entry 0 and entry PA are e^{i 0} = 1 and are not read.
+template <class P>
+struct PhaseRegs {
+  floatx4 ph[4];
+  __device__ __forceinline__ float re(int o) const { return ph[o >> 1][2 * (o & 1)]; }
+  __device__ __forceinline__ float im(int o) const { return ph[o >> 1][2 * (o & 1) + 1]; }
+};
+
+template <class P>
+__device__ __forceinline__ constexpr bool chunk_needed(int k) {
+  for (int s = 0; s < P::kSlots; ++s) {
+    const uint32_t w = P::word(s);
+    if (w & kSlotReal) continue;
+    const int ai = slot_ai(w), ti = slot_ti(w);
+    if ((ai != 0 && (ai >> 1) == k) || (ti != P::kPa && (ti >> 1) == k)) return true;
+  }
+  return false;
+}
+
+template <class P>
+__device__ __forceinline__ void load_phases(PhaseRegs<P>& r, __amdgpu_buffer_rsrc_t ph_r, int edge_off) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    r.ph[k] = chunk_needed<P>(k) ? bload4(ph_r, (edge_off * kPhaseRow + 4 * k) * 4) : floatx4{0.f, 0.f, 0.f, 0.f};
+}
+
+// Slot s's factor from the phase registers (compile-time slot words).
+template <class P>
+__device__ __forceinline__ void static_factor(const PhaseRegs<P>& r, const float* rp, int s, float& fr, float& fi) {
+  constexpr int dummy = 0;
+  (void)dummy;
+  const uint32_t w = P::word(s);
+  const int ai = slot_ai(w), ti = slot_ti(w);
+  float ar = 1.f, aim = 0.f, tr = 1.f, tim = 0.f;
+  if (ai != 0) {
+    ar = rp[ai] * r.re(ai);
+    aim = rp[ai] * r.im(ai);
+    if (w & kSlotAConj) aim = -aim;
+  }
+  if (ti != P::kPa) {
+    tr = r.re(ti);
+    tim = r.im(ti);
+    if (w & kSlotTConj) tim = -tim;
+  }
+  if (ai == 0) {
+    fr = tr;
+    fi = tim;
+  } else if (ti == P::kPa) {
+    fr = ar;
+    fi = aim;
+  } else {
+    fr = ar * tr - aim * tim;
+    fi = ar * tim + aim * tr;
+  }
+}
+
+// Runtime slot words: the tile's phase rows in LDS (lane (m, q) writes chunk q
+// of edge m, the angular entries scaled by rho^o), then per-slot reads.
+__device__ __forceinline__ void stage_phases_lanes(const FactArgs<float>& a, float* Ph, floatx4 chunk, float rho,
+                                                   int m, int q) {
+  const int o = 2 * q;
+  const float r2 = rho * rho;
+  float p = 1.f;
+  for (int i = 0; i < q; ++i) p *= r2;
+  const float s0 = o < a.pa ? p : 1.f, s1 = o + 1 < a.pa ? p * rho : 1.f;
+  float* dst = Ph + m * kPhStride + 2 * o;
+  *reinterpret_cast<float2*>(dst) = make_float2(chunk[0] * s0, chunk[1] * s0);
+  *reinterpret_cast<float2*>(dst + 2) = make_float2(chunk[2] * s1, chunk[3] * s1);
+}
+
+__device__ __forceinline__ void runtime_factor(const float* prow, uint32_t w, float& fr, float& fi) {
+  const float2 A = *reinterpret_cast<const float2*>(prow + 2 * slot_ai(w));
+  const float2 T = *reinterpret_cast<const float2*>(prow + 2 * slot_ti(w));
+  const float ai = (w & kSlotAConj) ? -A.y : A.y, ti = (w & kSlotTConj) ? -T.y : T.y;
+  fr = A.x * T.x - ai * ti;
+  fi = A.x * ti + ai * T.x;
+}
+
+// Whether the dh k-step (nt, r) reads any real column (else it is skipped).
+template <class P>
+__device__ __forceinline__ bool kstep_live(const FactArgs<float>& a, int nt, int r) {
+  const int s = 2 * nt + (r >> 1);
+  const uint32_t w = slot_word<P>(a, s);
+  return (w & kSlotActive) && !((w & kSlotReal) && (r & 1));
+}
+
+template <class P>
+struct FwdTile {
+  floatx4 h;           // h(edge m)[4 q .. 4 q + 3]
+  PhaseRegs<P> ph;     // static slots: edge m's phase row chunks; runtime: chunk q in ph.ph[0]
+  float rho;           // rho of edge m
+};
+
+template <class P>
+__device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amdgpu_buffer_rsrc_t ph_r,
+                                               __amdgpu_buffer_rsrc_t rho_r, int tb, int m, int q) {
+  FwdTile<P> t;
+  const int e = tb + m;
+  t.h = bload4(h_r, (e * 16 + 4 * q) * 4);
+  if constexpr (P::kStatic) {
+    load_phases<P>(t.ph, ph_r, e);
+  } else {
+    t.ph.ph[0] = bload4(ph_r, (e * kPhaseRow + 4 * q) * 4);
+  }
+  t.rho = bload1(rho_r, e * 4);
+  return t;
+}
+
+// One forward tile: 16 edges from tb, the rows stored through out_r.
+template <int NT, class P>
+__device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const FwdTile<P>& cur, const float (&za)[NT][4],
+                                             const floatx4 (&z0)[NT], float* Ph, __amdgpu_buffer_rsrc_t out_r,
+                                             int d_out, int tb, int m, int q) {
+  // u(e) = Z0 + sum_t h_t Z_t: lane (m, q) ends with edge m's slot columns 16 nt + 4 q + r
+  floatx4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = z0[nt];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], cur.h[s], acc[nt]);
+  float rp[5];
+  if constexpr (P::kStatic) {
+    rp[0] = 1.f;
+    rp[1] = cur.rho;
+    rp[2] = cur.rho * cur.rho;
+    rp[3] = rp[2] * cur.rho;
+    rp[4] = rp[2] * rp[2];
+  } else {
+    stage_phases_lanes(a, Ph, cur.ph.ph[0], cur.rho, m, q);
+    wave_sync();
+  }
+  // V = F u per slot, summed over each output's slots and stored
+  const int row = (tb + m) * d_out;
+  float sr = 0.f, si = 0.f;
+#pragma unroll
+  for (int s = 0; s < 2 * NT; ++s) {
+    const uint32_t w = slot_word<P>(a, s);
+    const float ur = acc[s >> 1][2 * (s & 1)], ui = acc[s >> 1][2 * (s & 1) + 1];
+    if (P::kStatic && (w & kSlotReal)) {
+      sr += ur;
+    } else {
+      float fr, fi;
+      if constexpr (P::kStatic)
+        static_factor<P>(cur.ph, rp, s, fr, fi);
+      else
+        runtime_factor(Ph + m * kPhStride, w, fr, fi);
+      sr += fr * ur - fi * ui;
+      si += fr * ui + fi * ur;
+    }
+    if (w & kSlotFlush) {
+      if (w & kSlotScalar)
+        bstore1(sr, out_r, (row + slot_ob(w) + q) * 4);
+      else
+        bstore2(sr, si, out_r, (row + slot_ob(w) + 2 * q) * 4);
+      sr = 0.f;
+      si = 0.f;
+    }
+  }
+  if constexpr (!P::kStatic) wave_sync();
+}
+
+template <int NT, class P>
+__global__ __launch_bounds__(64) void factored_forward_lanes(FactArgs<float> a) {
+  constexpr int ZS = 16 * NT + 4;
+  __shared__ __align__(16) float Zs[17 * ZS];
+  __shared__ __align__(16) float Ph[P::kStatic ? 4 : kMT * kPhStride];
+  __shared__ __align__(16) uint8_t colslot[128];
+  const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
+  const int d_out = P::kStatic ? P::kDout : a.d_out;
+  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
+  if (gi < 0 || gi >= a.n_groups) return;  // a malformed order names no group
+  const int64_t j = a.group_source[gi];
+  const int64_t g0 = a.group_ptr[gi];
+  const int ng = (int)(a.group_ptr[gi + 1] - g0);
+  stage_colslot(a, colslot, lane);
+  wave_sync();
+  stage_z_slots<ZS>(a, j, Zs, colslot, lane);
+  float za[NT][4];
+  floatx4 z0[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) za[nt][s] = Zs[(1 + 4 * q + s) * ZS + 16 * nt + m];
+    z0[nt] = *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q);
+  }
+  const auto h_r = span(a.h + g0 * 16, (int64_t)ng * 64);
+  const auto ph_r = span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
+  const auto rho_r = span(a.rho_g + g0, (int64_t)ng * 4);
+  const auto out_r = span(a.out + g0 * d_out, (int64_t)ng * d_out * 4);
+  // two tiles in flight: each buffer is refilled right after its tile's
+  // stores, so waiting for a tile never waits for the previous tile's stores
+  FwdTile<P> ta = load_fwd<P>(h_r, ph_r, rho_r, 0, m, q);
+  FwdTile<P> tbf = load_fwd<P>(h_r, ph_r, rho_r, kMT, m, q);
+  for (int tb = 0;;) {
+    forward_tile<NT, P>(a, ta, za, z0, Ph, out_r, d_out, tb, m, q);
+    ta = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q);
+    tb += kMT;
+    if (tb >= ng) break;
+    forward_tile<NT, P>(a, tbf, za, z0, Ph, out_r, d_out, tb, m, q);
+    tbf = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q);
+    tb += kMT;
+    if (tb >= ng) break;
+  }
+}
+
+template <class P>
+struct BwdTile {
+  floatx4 h;        // h(edge 4 q + i)[m], i < 4
+  PhaseRegs<P> ph;  // as in the forward
+  float rho, w;     // edge m
+  int64_t tgt;      // runtime slots: the target of edge m
+};
+
+template <class P>
+__device__ __forceinline__ BwdTile<P> load_bwd(__amdgpu_buffer_rsrc_t h_r, __amdgpu_buffer_rsrc_t ph_r,
+                                               __amdgpu_buffer_rsrc_t rho_r, __amdgpu_buffer_rsrc_t w_r,
+                                               __amdgpu_buffer_rsrc_t t_r, int tb, int m, int q) {
+  BwdTile<P> t;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t.h[i] = bload1(h_r, ((tb + 4 * q + i) * 16 + m) * 4);
+  const int e = tb + m;
+  if constexpr (P::kStatic) {
+    load_phases<P>(t.ph, ph_r, e);
+    t.tgt = 0;
+  } else {
+    t.ph.ph[0] = bload4(ph_r, (e * kPhaseRow + 4 * q) * 4);
+    t.tgt = bload_i64(t_r, e * 8);
+  }
+  t.rho = bload1(rho_r, e * 4);
+  t.w = bload1(w_r, e * 4);
+  return t;
+}
+
+// Static slots: the target gradient's and the row's values of the lane's
+// outputs (per output group, loaded at its first slot) for edge m.
+template <int NT>
+struct OutVals {
+  float gr[2 * NT], gi[2 * NT], rr[2 * NT], ri[2 * NT];
+};
+
+template <int NT, class P>
+__device__ __forceinline__ void load_outs(OutVals<NT>& v, const float* g, int64_t tgt, __amdgpu_buffer_rsrc_t rows_r,
+                                          int row, int q) {
+#pragma unroll
+  for (int s = 0; s < 2 * NT; ++s) {
+    const uint32_t w = P::word(s);
+    if (!(w & kSlotActive) || group_start<P>(s) != s) continue;
+    if (w & kSlotScalar) {
+      const int o = slot_ob(w) + q;
+      v.gr[s] = g[tgt * P::kDout + o];
+      v.gi[s] = 0.f;
+      v.rr[s] = bload1(rows_r, (row + o) * 4);
+      v.ri[s] = 0.f;
+    } else {
+      const int o = slot_ob(w) + 2 * q;
+      const float2 gv = *reinterpret_cast<const float2*>(g + tgt * P::kDout + o);
+      const float2 rv = bload2(rows_r, (row + o) * 4);
+      v.gr[s] = gv.x;
+      v.gi[s] = gv.y;
+      v.rr[s] = rv.x;
+      v.ri[s] = rv.y;
+    }
+  }
+}
+
+struct BwdSpans {
+  __amdgpu_buffer_rsrc_t h, ph, rho, w, t, rows, dh, dw;
+};
+
+// One backward tile: 16 edges from tb; dh and dweights stored, dZ
+// accumulated in registers.
+template <int NT, class P, class O>
+__device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const BwdTile<P>& cur, const O& outs,
+                                              const floatx4 (&zb)[NT], floatx4 (&dz)[NT], float (&dz0)[NT], float* Sh,
+                                              float* Ph, float* Gt, int64_t* Tg, const BwdSpans& sp, int d_out,
+                                              int ng, int tb, int m, int q) {
+  const int row = (tb + m) * d_out;
+  float wv[NT][4];
+  float dwp = 0.f;  // this lane's share of dweights(edge m)
+  if constexpr (P::kStatic) {
+    float rp[5];
+    rp[0] = 1.f;
+    rp[1] = cur.rho;
+    rp[2] = cur.rho * cur.rho;
+    rp[3] = rp[2] * cur.rho;
+    rp[4] = rp[2] * rp[2];
+#pragma unroll
+    for (int s = 0; s < 2 * NT; ++s) {
+      const uint32_t w = P::word(s);
+      const int b = group_start<P>(s);
+      if ((w & kSlotActive) && b == s) dwp += outs.gr[s] * outs.rr[s] + outs.gi[s] * outs.ri[s];
+      float fr = 1.f, fi = 0.f;
+      if ((w & kSlotActive) && !(w & kSlotReal)) static_factor<P>(cur.ph, rp, s, fr, fi);
+      const float gr = (w & kSlotActive) ? outs.gr[b] : 0.f, gim = (w & kSlotActive) ? outs.gi[b] : 0.f;
+      wv[s >> 1][2 * (s & 1)] = cur.w * (fr * gr + fi * gim);
+      wv[s >> 1][2 * (s & 1) + 1] = cur.w * (fr * gim - fi * gr);
+    }
+  } else {
+    // the targets' gradient rows through LDS (zero for absent edges and past d_out)
+    const int GS = a.gstride;
+    stage_phases_lanes(a, Ph, cur.ph.ph[0], cur.rho, m, q);
+    if (q == 0) Tg[m] = cur.tgt;
+    wave_sync();
+    for (int e = q; e < kMT; e += 4) {
+      const float* grow = tb + e < ng ? a.g + Tg[e] * d_out : nullptr;
+      for (int o = m; o < GS; o += kMT) Gt[e * GS + o] = grow && o < d_out ? grow[o] : 0.f;
+    }
+    wave_sync();
+    for (int o = q; o < d_out; o += 4) dwp += Gt[m * GS + o] * bload1(sp.rows, (row + o) * 4);
+    const float* prow = Ph + m * kPhStride;
+    const float* gq1 = Gt + m * GS + q;
+    const float* gq2 = Gt + m * GS + 2 * q;
+#pragma unroll
+    for (int s = 0; s < 2 * NT; ++s) {
+      const uint32_t w = a.slot[s];
+      float fr, fi;
+      runtime_factor(prow, w, fr, fi);
+      const float* gp = ((w & kSlotScalar) ? gq1 : gq2) + slot_ob(w);
+      const float gr = gp[0], gim = (w & kSlotScalar) ? 0.f : gp[1];
+      wv[s >> 1][2 * (s & 1)] = cur.w * (fr * gr + fi * gim);
+      wv[s >> 1][2 * (s & 1) + 1] = cur.w * (fr * gim - fi * gr);
+    }
+  }
+  // dweights = <g(target), row>: the four lanes' shares of edge m
+  dwp += __shfl_xor(dwp, 16, kWave);
+  dwp += __shfl_xor(dwp, 32, kWave);
+  bstore1(dwp, sp.dw, q == 0 ? (tb + m) * 4 : kDrop);
+  // dh(e)_t = sum_c W(e)_c Z_t,c: lane (m, q) ends with edge m's features 4 q .. 4 q + 3
+  floatx4 dh = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (kstep_live<P>(a, nt, r)) dh = mfma16(zb[nt][r], wv[nt][r], dh);
+  bstore4(dh, sp.dh, ((tb + m) * 16 + 4 * q) * 4);
+  // W through LDS, column-major, for dZ's edge-major operand
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Sh[(16 * nt + 4 * q + r) * kWtStride + m] = wv[nt][r];
+  wave_sync();
+  // dZ_t,c += sum_e h_t(e) W(e)_c over edges 4 q' + i; the t = 0 column sums W
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const floatx4 wt = *reinterpret_cast<const floatx4*>(Sh + (16 * nt + m) * kWtStride + 4 * q);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dz[nt] = mfma16(cur.h[i], wt[i], dz[nt]);
+    dz0[nt] += (wt[0] + wt[1]) + (wt[2] + wt[3]);
+  }
+  wave_sync();
+}
+
+template <int NT, class P>
+__global__ __launch_bounds__(64) void factored_backward_lanes(FactArgs<float> a) {
+  constexpr int ZS = 16 * NT + 4;
+  constexpr int kZWords = 17 * ZS, kWWords = 16 * NT * kWtStride;
+  __shared__ __align__(16) float Sh[kZWords > kWWords ? kZWords : kWWords];  // Z in, then W's transpose, then dZ out
+  __shared__ __align__(16) float Ph[P::kStatic ? 4 : kMT * kPhStride];
+  __shared__ __align__(16) float Gt[P::kStatic ? 4 : kMT * (GM_FACT_MAX_OUT + 4)];
+  __shared__ __align__(16) uint8_t colslot[128];
+  __shared__ int64_t Tg[P::kStatic ? 1 : kMT];
+  const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
+  const int d_out = P::kStatic ? P::kDout : a.d_out;
+  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
+  if (gi < 0 || gi >= a.n_groups) return;  // a malformed order names no group
+  const int64_t j = a.group_source[gi];
+  const int64_t g0 = a.group_ptr[gi];
+  const int ng = (int)(a.group_ptr[gi + 1] - g0);
+  stage_colslot(a, colslot, lane);
+  wave_sync();
+  stage_z_slots<ZS>(a, j, Sh, colslot, lane);
+  // Z_t(j) for t = 1 + m at the lane's slot columns 16 nt + 4 q + r
+  floatx4 zb[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) zb[nt] = *reinterpret_cast<const floatx4*>(Sh + (1 + m) * ZS + 16 * nt + 4 * q);
+  wave_sync();
+  floatx4 dz[NT];
+  float dz0[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    dz[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    dz0[nt] = 0.f;
+  }
+  BwdSpans sp;
+  sp.h = span(a.h + g0 * 16, (int64_t)ng * 64);
+  sp.ph = span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
+  sp.rho = span(a.rho_g + g0, (int64_t)ng * 4);
+  sp.w = span(a.weights + g0, (int64_t)ng * 4);
+  sp.t = span(a.target_g + g0, (int64_t)ng * 8);
+  sp.rows = span(a.rows + g0 * d_out, (int64_t)ng * d_out * 4);
+  sp.dh = span(a.dh + g0 * 16, (int64_t)ng * 64);
+  sp.dw = span(a.dweights + g0, (int64_t)ng * 4);
+  // Two tiles in flight (buffers A and B, each refilled right after its
+  // tile's stores); with static slots the targets run three tiles ahead and
+  // the targets' gradient values and row values two, so no load is waited
+  // for within the tile after the one that issued it.
+  BwdTile<P> ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, 0, m, q);
+  BwdTile<P> tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, kMT, m, q);
+  OutVals<P::kStatic ? NT : 1> oa, ob;
+  int64_t tn = 0;  // static slots: the targets of the tile two ahead of the current one
+  if constexpr (P::kStatic) {
+    load_outs<NT, P>(oa, a.g, bload_i64(sp.t, m * 8), sp.rows, m * d_out, q);
+    load_outs<NT, P>(ob, a.g, bload_i64(sp.t, (kMT + m) * 8), sp.rows, (kMT + m) * d_out, q);
+    tn = bload_i64(sp.t, (2 * kMT + m) * 8);
+  }
+  for (int tb = 0;;) {
+    backward_tile<NT, P>(a, ta, oa, zb, dz, dz0, Sh, Ph, Gt, Tg, sp, d_out, ng, tb, m, q);
+    if constexpr (P::kStatic) {
+      load_outs<NT, P>(oa, a.g, tn, sp.rows, (tb + 2 * kMT + m) * d_out, q);
+      tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
+    }
+    ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q);
+    tb += kMT;
+    if (tb >= ng) break;
+    backward_tile<NT, P>(a, tbf, ob, zb, dz, dz0, Sh, Ph, Gt, Tg, sp, d_out, ng, tb, m, q);
+    if constexpr (P::kStatic) {
+      load_outs<NT, P>(ob, a.g, tn, sp.rows, (tb + 2 * kMT + m) * d_out, q);
+      tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
+    }
+    tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q);
+    tb += kMT;
+    if (tb >= ng) break;
+  }
+  // dZ(j) into LDS in slot-column order, then out by runs
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    dz0[nt] += __shfl_xor(dz0[nt], 16, kWave);
+    dz0[nt] += __shfl_xor(dz0[nt], 32, kWave);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Sh[(1 + 4 * q + i) * ZS + 16 * nt + m] = dz[nt][i];
+    if (q == 0) Sh[16 * nt + m] = dz0[nt];
+  }
+  wave_sync();
+  flush_dz_slots<ZS>(a, j, Sh, colslot, lane);
+}
+
 // ------------------------------------------------------------------- launch
 
 // The mix runs of a call: the caller's (pointer, node stride, mix stride,
@@ -1344,7 +1987,41 @@ void launch_grouped_nt(bool forward, const FactArgs<float>& a, hipStream_t strea
     hipLaunchKernelGGL(factored_backward_grouped<NT>, grid, block, lds_backward_grouped(a, NT), stream, a);
 }
 
+template <int NT, class P = RuntimeSlots>
+void launch_lanes_nt(bool forward, const FactArgs<float>& a, hipStream_t stream) {
+  const dim3 grid((unsigned)a.n_groups), block(64);
+  if (forward)
+    hipLaunchKernelGGL((factored_forward_lanes<NT, P>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((factored_backward_lanes<NT, P>), grid, block, 0, stream, a);
+}
+
+// Whether a plan's runtime slot words are P's compile-time ones.
+template <class P>
+bool matches(const FactArgs<float>& a) {
+  if (a.n_slots != P::kSlots || a.d_out != P::kDout || a.pa != P::kPa) return false;
+  for (int s = 0; s < a.n_slots; ++s)
+    if (a.slot[s] != P::word(s)) return false;
+  return true;
+}
+
 void launch_grouped(bool forward, const FactArgs<float>& a, hipStream_t stream) {
+  if (a.n_slots > 0) {
+    const char* env = std::getenv("GM_FACTORED_STATIC");
+    const bool fixed = env == nullptr || env[0] != '0';
+    if (fixed && matches<SlotsF2>(a)) return launch_lanes_nt<(SlotsF2::kSlots + 1) / 2, SlotsF2>(forward, a, stream);
+    if (fixed && matches<SlotsF1>(a)) return launch_lanes_nt<(SlotsF1::kSlots + 1) / 2, SlotsF1>(forward, a, stream);
+    switch ((a.n_slots + 1) / 2) {
+      case 1: launch_lanes_nt<1>(forward, a, stream); return;
+      case 2: launch_lanes_nt<2>(forward, a, stream); return;
+      case 3: launch_lanes_nt<3>(forward, a, stream); return;
+      case 4: launch_lanes_nt<4>(forward, a, stream); return;
+      case 5: launch_lanes_nt<5>(forward, a, stream); return;
+      case 6: launch_lanes_nt<6>(forward, a, stream); return;
+      case 7: launch_lanes_nt<7>(forward, a, stream); return;
+      default: launch_lanes_nt<8>(forward, a, stream); return;
+    }
+  }
   switch ((a.C + 15) / 16) {
     case 1: launch_grouped_nt<1>(forward, a, stream); break;
     case 2: launch_grouped_nt<2>(forward, a, stream); break;
@@ -1355,6 +2032,76 @@ void launch_grouped(bool forward, const FactArgs<float>& a, hipStream_t stream) 
     case 7: launch_grouped_nt<7>(forward, a, stream); break;
     default: launch_grouped_nt<8>(forward, a, stream); break;
   }
+}
+
+// The lane-owned slot tables of a grouped plan, or n_slots = 0 when the plan
+// does not fit them (GM_FACTORED_LANES=0 declines every plan): blocks in
+// multiplicities of four, radial power equal to the angular order, complex
+// outputs at even offsets of an even-width row, at most 16 slots.
+void prepare_lanes(FactArgs<float>& a) {
+  const char* env = std::getenv("GM_FACTORED_LANES");
+  const bool off = env != nullptr && env[0] == '0';
+  a.n_slots = 0;
+  if (off || a.K != 17 || a.d_out % 2 != 0 || a.pa + a.pt > 8) return;
+  uint32_t slot[kMaxSlots] = {};
+  uint8_t slotcol[128];
+  for (int i = 0; i < 128; ++i) slotcol[i] = 0xFF;
+  int n = 0;
+  for (int b = 0; b < a.n_blocks;) {
+    int e = b + 1;  // the output group: blocks b .. e - 1 share an output offset (consecutive, alike)
+    while (e < a.n_blocks && a.desc[e].ooff == a.desc[b].ooff) ++e;
+    const Block& d0 = a.desc[b];
+    const bool scalar = d0.kind == 0 || d0.take_real;
+    if (d0.bm % 4 != 0 || (!scalar && d0.ooff % 2 != 0)) return;
+    for (int u = 0; u < d0.bm / 4; ++u)
+      for (int k = b; k < e; ++k) {
+        const Block& d = a.desc[k];
+        if (n >= kMaxSlots) return;
+        uint32_t w = kSlotActive | (scalar ? kSlotScalar : 0u) | (uint32_t)(scalar ? d.ooff + 4 * u : d.ooff + 8 * u);
+        if (d.kind == 0) {
+          w |= kSlotReal | (uint32_t)a.pa << 15;  // angular entry 0 and transport entry pa: both e^{i 0} = 1
+        } else {
+          const int aa = std::abs(d.ang), ta = std::abs(d.tr);
+          if (d.power != aa) return;
+          w |= (uint32_t)aa << 11 | (d.ang < 0 ? kSlotAConj : 0u) | (uint32_t)(a.pa + ta) << 15 |
+               (d.tr < 0 ? kSlotTConj : 0u);
+        }
+        if (k == e - 1) w |= kSlotFlush;
+        slot[n] = w;
+        for (int q = 0; q < 4; ++q) {
+          const int sc = 16 * (n / 2) + 4 * q + 2 * (n % 2);
+          if (d.kind == 0) {
+            slotcol[sc] = (uint8_t)(2 * a.wc + d.zoff + 4 * u + q);
+          } else {
+            const int cc = d.zoff + 4 * u + q;
+            slotcol[sc] = (uint8_t)(2 * cc);
+            slotcol[sc + 1] = (uint8_t)(2 * cc + 1);
+          }
+        }
+        ++n;
+      }
+    b = e;
+  }
+  if (n == 0) return;
+  uint32_t kmask = 0;
+  for (int nt = 0; nt < (n + 1) / 2; ++nt)
+    for (int r = 0; r < 4; ++r)
+      for (int q = 0; q < 4; ++q)
+        if (slotcol[16 * nt + 4 * q + r] != 0xFF) kmask |= 1u << (4 * nt + r);
+  int gs = a.d_out + 1;
+  while (gs % 4 != 2) ++gs;  // G rows 2 (mod 4) floats apart: the 16 rows' reads fall in distinct banks
+  for (int i = 0; i < kMaxSlots; ++i) a.slot[i] = slot[i];
+  for (int i = 0; i < 128; ++i) a.slotcol[i] = slotcol[i];
+  a.kmask = kmask;
+  uint8_t colslot[128];
+  for (int i = 0; i < 128; ++i) colslot[i] = 0;
+  for (int sc = 0; sc < 128; ++sc)
+    if (slotcol[sc] != 0xFF) colslot[slotcol[sc]] = (uint8_t)sc;
+  for (int i = 0; i < 32; ++i)
+    a.colslot32[i] = (uint32_t)colslot[4 * i] | (uint32_t)colslot[4 * i + 1] << 8 | (uint32_t)colslot[4 * i + 2] << 16 |
+                     (uint32_t)colslot[4 * i + 3] << 24;
+  a.gstride = gs;
+  a.n_slots = n;
 }
 
 // The grouped path's extra checks: fp32, 16 trunk features, at most 128
@@ -1379,6 +2126,7 @@ int prepare_grouped(FactArgs<float>& a, const float* h, const Runs<float>& runs,
   a.rho_g = rho_g;
   a.pa = (int)pa;
   a.pt = (int)pt;
+  prepare_lanes(a);
   return GM_OK;
 }
 
@@ -1519,4 +2267,36 @@ extern "C" int gm_factored_aggregate_gather_f32(const float* rows, const int64_t
   GM_REQUIRE(n_edges == 0 || inv, "inv must be a device pointer");
   return gm::factored_aggregate<float>(rows, weights, row_ptr, n_targets, n_edges, d_out, out, (hipStream_t)stream,
                                        inv);
+}
+
+extern "C" int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out,
+                                       int64_t pa, int64_t pt, int32_t* n_slots, uint32_t* slot, uint8_t* slotcol) {
+  GM_REQUIRE(n_slots != nullptr, "n_slots must be a host pointer");
+  GM_REQUIRE(pa >= 1 && pt >= 1 && pa + pt <= gm::kPhaseRow / 2, "the grouped phase rows hold at most 8 pairs");
+  gm::FactArgs<float> a;
+  // the two runs of zc / zr (no memory behind them: nothing is read)
+  const float* z[2] = {nullptr, nullptr};
+  const int64_t zero[2] = {0, 0};
+  int64_t width[2] = {2 * wc, wr}, n_runs = 2;
+  if (wc == 0 || wr == 0) {
+    width[0] = 2 * wc + wr;
+    n_runs = 1;
+  }
+  const gm::Runs<float> runs{z, nullptr, zero, zero, width, n_runs};
+  const float* none = nullptr;
+  const int status = gm::prepare<float>(a, none, runs, none, none, none, desc, nullptr, nullptr, nullptr, 0, 0, 0, 17,
+                                        wc, wr, pa > pt ? pa : pt, n_blocks, d_out);
+  if (status != GM_OK) return status;
+  for (int b = 0; b < a.n_blocks; ++b)
+    GM_REQUIRE(std::abs(a.desc[b].ang) < pa && std::abs(a.desc[b].tr) < pt,
+               "a block's harmonic order exceeds the grouped phase rows");
+  a.pa = (int)pa;
+  a.pt = (int)pt;
+  gm::prepare_lanes(a);
+  *n_slots = a.n_slots;
+  if (slot)
+    for (int i = 0; i < gm::kMaxSlots; ++i) slot[i] = a.n_slots ? a.slot[i] : 0u;
+  if (slotcol)
+    for (int i = 0; i < 128; ++i) slotcol[i] = a.n_slots ? a.slotcol[i] : (uint8_t)0xFF;
+  return GM_OK;
 }

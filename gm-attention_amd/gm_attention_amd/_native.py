@@ -44,7 +44,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "gm_factored_backward_seg": [_P] * 10 + [_I] + [_P] * 7 + [_I] * 9 + [_P] * 3,
 }
 
-#: fp32-only entry points (name -> (restype, argtypes)).
+#: fp32-only and host-only entry points (name -> (restype, argtypes)).
 SIGNATURES_F32 = {
     "gm_radial_trunk_forward_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_D, _P, _P]),
     "gm_radial_trunk_backward_f32": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_D, _P, _P, _P]),
@@ -52,6 +52,7 @@ SIGNATURES_F32 = {
     "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 6 + [_I] * 10 + [_P, _P]),
     "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 6 + [_I] * 10 + [_P] * 3),
     "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
+    "gm_factored_lane_tables": (ctypes.c_int, [_P] + [_I] * 6 + [_P] * 3),
 }
 
 
@@ -602,6 +603,18 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
           _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, h_g.shape[0], group_source.shape[0], K,
           wc, wr, pa, pt, hd.shape[0], g.shape[1], _ptr(dh_g), _ptr(dweights), _stream(h_g.device))
     return dweights
+
+
+def lane_tables(desc: Tensor, wc: int, wr: int, d_out: int, pa: int, pt: int) -> tuple[int, list[int], list[int]]:
+    """The grouped kernels' lane-owned slot tables for a plan: (slot count,
+    per-slot words, slot column -> packed column with 255 for padding); a
+    count of 0 means the plan takes the generic grouped kernels."""
+    hd = host_desc32(desc)
+    n = ctypes.c_int32(0)
+    slot = (ctypes.c_uint32 * 16)()
+    slotcol = (ctypes.c_uint8 * 128)()
+    _call("gm_factored_lane_tables", hd.data_ptr(), hd.shape[0], wc, wr, d_out, pa, pt, ctypes.byref(n), slot, slotcol)
+    return n.value, list(slot), list(slotcol)
 
 
 def aggregate_gather(rows_g: Tensor, inv: Tensor, weights: Tensor, row_ptr: Tensor) -> Tensor:

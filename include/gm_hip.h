@@ -310,6 +310,22 @@ int gm_radial_trunk_backward_f32(const float* dh, const float* rho, const float*
                                  const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B, double width,
                                  float* partial, float* dparams, void* stream);
 
+/* The lane-owned output tables the grouped factored kernels use for a plan
+ * (host only; nothing runs on the GPU).  When every block comes in
+ * multiplicities of four with radial power equal to its angular order, lane
+ * q of an edge's four lanes owns the copies q (mod 4) of every block; its
+ * slots are its (block, copy) pairs, the blocks of one output consecutive.
+ * On return *n_slots is the slot count (0: the plan takes the generic grouped
+ * kernels), slot[16] the per-slot words (bits 0-6 output base, 7 active,
+ * 8 real block, 9 scalar output, 10 last slot of its output, 11-13 angular
+ * entry, 14 its conjugate, 15-17 transport entry, 18 its conjugate) and
+ * slotcol[128] the packed column of slot column 16 (s / 2) + 4 q + 2 (s % 2)
+ * + part (0xFF: padding).  desc as for gm_factored_forward_grouped_f32.  No
+ * counterpart in the reference: it exposes this build's kernel layout for
+ * tests and tools. */
+int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out, int64_t pa,
+                            int64_t pt, int32_t* n_slots, uint32_t* slot, uint8_t* slotcol);
+
 #ifdef __cplusplus
 }
 #endif

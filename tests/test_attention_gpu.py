@@ -181,3 +181,19 @@ def test_mhsa_float32_with_largest_first_groups_matches_the_oracle(cuda, monkeyp
     group_order permutation), float32, against the oracle."""
     monkeypatch.setenv("GM_FACTORED_LPT", "1")
     test_mhsa_matches_the_oracle(CASES[0], torch.float32, True, cuda)
+
+
+LANE_CASES = [({0: 8, 1: 8, 2: 8}, 2, "hard", 2), ({0: 16, 1: 8, 2: 8}, 2, "quartic", 1), ({0: 8, 1: 8}, 2, "hard", 1)]
+
+
+@pytest.mark.parametrize("form", ["fixed", "runtime", "generic"])
+@pytest.mark.parametrize("case", LANE_CASES)
+def test_mhsa_float32_on_the_lane_kernels_matches_the_oracle(case, form, cuda, monkeypatch):
+    """Heads with four (or eight) copies per frequency on the grouped kernels'
+    lane-owned output form: with compile-time slot words where the plan has
+    them ("fixed"), with the words as kernel arguments
+    (GM_FACTORED_STATIC=0), and on the generic grouped form
+    (GM_FACTORED_LANES=0); float32 batched, against the oracle."""
+    monkeypatch.setenv("GM_FACTORED_STATIC", "0" if form == "runtime" else "1")
+    monkeypatch.setenv("GM_FACTORED_LANES", "0" if form == "generic" else "1")
+    test_mhsa_matches_the_oracle(case, torch.float32, True, cuda)
