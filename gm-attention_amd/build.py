@@ -36,9 +36,14 @@ FLAGS = [
 ]
 
 
+#: Per-source extra flags.  The factored kernels keep their MFMA accumulators
+#: in VGPRs (the VALU reads every accumulator, so AGPRs would only add copies).
+EXTRA = {"factored.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(source: Path, verbose: bool) -> Path:
     obj = BUILD / (source.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(source), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(source.name, []), "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if verbose or result.returncode != 0:
         sys.stderr.write(" ".join(cmd) + "\n" + result.stdout + result.stderr)

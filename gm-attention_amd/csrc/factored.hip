@@ -1125,9 +1125,9 @@ __device__ __forceinline__ void bstore4(floatx4 v, __amdgpu_buffer_rsrc_t r, int
 constexpr int kDrop = 0x7FFFFFF0;  // a byte offset past every group's span: the access is dropped
 
 // Z(j) into LDS in slot-column order, Zs[t * ZS + sc] for t < 17, zero in the
-// padding columns: each mix run's 17 x width block is read in index order
-// (coalesced), twelve elements a lane in flight at once, and scattered to its
-// slot columns through colslot.
+// padding columns: per mix run, lane c reads column c's 17 mixes (17 loads in
+// flight, each row coalesced across the lanes) and writes them to its slot
+// column.
 template <int ZS>
 __device__ __forceinline__ void stage_z_slots(const FactArgs<float>& a, int64_t j, float* Zs, const uint8_t* colslot,
                                               int lane) {
@@ -1136,28 +1136,14 @@ __device__ __forceinline__ void stage_z_slots(const FactArgs<float>& a, int64_t 
   for (int r = 0; r < a.n_seg; ++r) {
     const ZSeg<float>& g = a.seg[r];
     const float* base = g.z + j * g.node_stride;
-    const int w = g.width, total = 17 * w, ts = g.t_stride, c0 = g.c0;
-    const float inv = 1.f / (float)w;
-    for (int i0 = 0; i0 < total; i0 += 12 * kWave) {
-      float v[12];
-      int dst[12];
+    const int64_t ts = g.t_stride;
+    for (int c = lane; c < g.width; c += kWave) {
+      const int sc = colslot[g.c0 + c];
+      float v[17];
 #pragma unroll
-      for (int u = 0; u < 12; ++u) {
-        const int idx = i0 + u * kWave + lane;
-        int t = (int)((float)idx * inv);
-        t -= t * w > idx;
-        t += (t + 1) * w <= idx;
-        const int cc = idx - t * w;
-        dst[u] = -1;
-        v[u] = 0.f;
-        if (idx < total) {
-          v[u] = base[(int64_t)t * ts + cc];
-          dst[u] = t * ZS + colslot[c0 + cc];
-        }
-      }
+      for (int t = 0; t < 17; ++t) v[t] = base[t * ts + c];
 #pragma unroll
-      for (int u = 0; u < 12; ++u)
-        if (dst[u] >= 0) Zs[dst[u]] = v[u];
+      for (int t = 0; t < 17; ++t) Zs[t * ZS + sc] = v[t];
     }
   }
   wave_sync();
@@ -1170,28 +1156,14 @@ __device__ __forceinline__ void flush_dz_slots(const FactArgs<float>& a, int64_t
   for (int r = 0; r < a.n_seg; ++r) {
     const ZSeg<float>& g = a.seg[r];
     float* base = g.dz + j * g.node_stride;
-    const int w = g.width, total = 17 * w, ts = g.t_stride, c0 = g.c0;
-    const float inv = 1.f / (float)w;
-    for (int i0 = 0; i0 < total; i0 += 12 * kWave) {
-      float v[12];
-      int64_t dst[12];
+    const int64_t ts = g.t_stride;
+    for (int c = lane; c < g.width; c += kWave) {
+      const int sc = colslot[g.c0 + c];
+      float v[17];
 #pragma unroll
-      for (int u = 0; u < 12; ++u) {
-        const int idx = i0 + u * kWave + lane;
-        int t = (int)((float)idx * inv);
-        t -= t * w > idx;
-        t += (t + 1) * w <= idx;
-        const int cc = idx - t * w;
-        dst[u] = -1;
-        v[u] = 0.f;
-        if (idx < total) {
-          v[u] = Zs[t * ZS + colslot[c0 + cc]];
-          dst[u] = (int64_t)t * ts + cc;
-        }
-      }
+      for (int t = 0; t < 17; ++t) v[t] = Zs[t * ZS + sc];
 #pragma unroll
-      for (int u = 0; u < 12; ++u)
-        if (dst[u] >= 0) base[dst[u]] = v[u];
+      for (int t = 0; t < 17; ++t) base[t * ts + c] = v[t];
     }
   }
 }
@@ -1366,7 +1338,8 @@ __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const Fwd
 }
 
 template <int NT, class P>
-__global__ __launch_bounds__(64) void factored_forward_lanes(FactArgs<float> a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? 4 : 1))) void factored_forward_lanes(
+    FactArgs<float> a) {
   constexpr int ZS = 16 * NT + 4;
   __shared__ __align__(16) float Zs[17 * ZS];
   __shared__ __align__(16) float Ph[P::kStatic ? 4 : kMT * kPhStride];
