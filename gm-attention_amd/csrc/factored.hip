@@ -85,6 +85,7 @@ struct FactArgs {
   const float* rho_g;
   const int64_t* target_g;
   const int64_t* group_order;  // the groups in launch order (largest first), or null
+  const float* zw_g;           // (n_edges, 4): r e^{i phi}, e^{i gamma} in grouping order, or null
   int pa, pt;
   // lane-owned output kernels: per-slot words, slot column -> packed column
   // (0xFF padding), the backward's live dh k-steps (bit 4 nt + r), the LDS
@@ -1059,6 +1060,19 @@ struct StaticSlots {
     constexpr uint32_t w[] = {W..., 0u};
     return s >= 0 && s < kSlots ? w[s] : 0u;
   }
+  // one past the highest angular and transport orders the slots use
+  __host__ __device__ static constexpr int angular_orders() {
+    int n = 1;
+    for (int s = 0; s < kSlots; ++s)
+      if (!(word(s) & kSlotReal) && slot_ai(word(s)) + 1 > n) n = slot_ai(word(s)) + 1;
+    return n;
+  }
+  __host__ __device__ static constexpr int transport_orders() {
+    int n = 1;
+    for (int s = 0; s < kSlots; ++s)
+      if (!(word(s) & kSlotReal) && slot_ti(word(s)) - PA + 1 > n) n = slot_ti(word(s)) - PA + 1;
+    return n;
+  }
 };
 struct RuntimeSlots {
   static constexpr bool kStatic = false;
@@ -1066,6 +1080,8 @@ struct RuntimeSlots {
   static constexpr int kPa = 0;
   static constexpr int kDout = 0;
   __host__ __device__ static constexpr uint32_t word(int) { return 0u; }
+  __host__ __device__ static constexpr int angular_orders() { return 1; }
+  __host__ __device__ static constexpr int transport_orders() { return 1; }
 };
 // frequencies 0..2, four copies each: 13 slots (one real, two onto frequency
 // 0 taking the real part, five onto each of frequencies 1 and 2)
@@ -1173,61 +1189,75 @@ __device__ __forceinline__ void stage_colslot(const FactArgs<float>& a, uint8_t*
   if (lane < 32) reinterpret_cast<uint32_t*>(colslot)[lane] = a.colslot32[lane];
 }
 
-// A tile's phase row entries o = 1 .. 7 of the lane's edge, the angular ones
-// (o < PA) scaled by rho^o: chunk k of the row (entries 2 k, 2 k + 1) in
-// ph[k].  Entry 0 and entry PA are e^{i 0} = 1 and are not read.
+// The lane's edge's phase registers.  Fixed slots: zw = (r e^{i phi},
+// e^{i gamma}), from which every factor is a product of powers; runtime
+// slots: chunk q of the edge's phase row (staged to LDS).
 template <class P>
 struct PhaseRegs {
-  floatx4 ph[4];
-  __device__ __forceinline__ float re(int o) const { return ph[o >> 1][2 * (o & 1)]; }
-  __device__ __forceinline__ float im(int o) const { return ph[o >> 1][2 * (o & 1) + 1]; }
+  floatx4 ph;
 };
 
+// Powers z^o (o < angular orders) of z = r e^{i phi} and w^o of w = e^{i gamma}
+// (o < transport orders), by squaring and one multiplication per odd power.
 template <class P>
-__device__ __forceinline__ constexpr bool chunk_needed(int k) {
-  for (int s = 0; s < P::kSlots; ++s) {
-    const uint32_t w = P::word(s);
-    if (w & kSlotReal) continue;
-    const int ai = slot_ai(w), ti = slot_ti(w);
-    if ((ai != 0 && (ai >> 1) == k) || (ti != P::kPa && (ti >> 1) == k)) return true;
-  }
-  return false;
+struct Powers {
+  static constexpr int NA = P::kStatic ? P::angular_orders() : 1;
+  static constexpr int NW = P::kStatic ? P::transport_orders() : 1;
+  float zr[NA], zi[NA], wr[NW], wi[NW];
+};
+
+__device__ __forceinline__ void cmul(float ar, float ai, float br, float bi, float& cr, float& ci) {
+  cr = ar * br - ai * bi;
+  ci = ar * bi + ai * br;
 }
 
 template <class P>
-__device__ __forceinline__ void load_phases(PhaseRegs<P>& r, __amdgpu_buffer_rsrc_t ph_r, int edge_off) {
+__device__ __forceinline__ Powers<P> powers(const floatx4& zw) {
+  Powers<P> p;
+  p.zr[0] = 1.f;
+  p.zi[0] = 0.f;
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
-    r.ph[k] = chunk_needed<P>(k) ? bload4(ph_r, (edge_off * kPhaseRow + 4 * k) * 4) : floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int o = 1; o < Powers<P>::NA; ++o) {
+    if (o == 1) {
+      p.zr[1] = zw[0];
+      p.zi[1] = zw[1];
+    } else if (o % 2 == 0) {
+      cmul(p.zr[o / 2], p.zi[o / 2], p.zr[o / 2], p.zi[o / 2], p.zr[o], p.zi[o]);
+    } else {
+      cmul(p.zr[o - 1], p.zi[o - 1], zw[0], zw[1], p.zr[o], p.zi[o]);
+    }
+  }
+  p.wr[0] = 1.f;
+  p.wi[0] = 0.f;
+#pragma unroll
+  for (int o = 1; o < Powers<P>::NW; ++o) {
+    if (o == 1) {
+      p.wr[1] = zw[2];
+      p.wi[1] = zw[3];
+    } else if (o % 2 == 0) {
+      cmul(p.wr[o / 2], p.wi[o / 2], p.wr[o / 2], p.wi[o / 2], p.wr[o], p.wi[o]);
+    } else {
+      cmul(p.wr[o - 1], p.wi[o - 1], zw[2], zw[3], p.wr[o], p.wi[o]);
+    }
+  }
+  return p;
 }
 
-// Slot s's factor from the phase registers (compile-time slot words).
+// Slot s's factor z^a w^t (conjugates as the word says) for compile-time slots.
 template <class P>
-__device__ __forceinline__ void static_factor(const PhaseRegs<P>& r, const float* rp, int s, float& fr, float& fi) {
-  constexpr int dummy = 0;
-  (void)dummy;
+__device__ __forceinline__ void static_factor(const Powers<P>& p, int s, float& fr, float& fi) {
   const uint32_t w = P::word(s);
-  const int ai = slot_ai(w), ti = slot_ti(w);
-  float ar = 1.f, aim = 0.f, tr = 1.f, tim = 0.f;
-  if (ai != 0) {
-    ar = rp[ai] * r.re(ai);
-    aim = rp[ai] * r.im(ai);
-    if (w & kSlotAConj) aim = -aim;
-  }
-  if (ti != P::kPa) {
-    tr = r.re(ti);
-    tim = r.im(ti);
-    if (w & kSlotTConj) tim = -tim;
-  }
+  const int ai = slot_ai(w), to = slot_ti(w) - P::kPa;
+  const float ar = p.zr[ai], aim = (w & kSlotAConj) ? -p.zi[ai] : p.zi[ai];
+  const float tr = p.wr[to], tim = (w & kSlotTConj) ? -p.wi[to] : p.wi[to];
   if (ai == 0) {
     fr = tr;
     fi = tim;
-  } else if (ti == P::kPa) {
+  } else if (to == 0) {
     fr = ar;
     fi = aim;
   } else {
-    fr = ar * tr - aim * tim;
-    fi = ar * tim + aim * tr;
+    cmul(ar, aim, tr, tim, fr, fi);
   }
 }
 
@@ -1263,11 +1293,12 @@ __device__ __forceinline__ bool kstep_live(const FactArgs<float>& a, int nt, int
 
 template <class P>
 struct FwdTile {
-  floatx4 h;           // h(edge m)[4 q .. 4 q + 3]
-  PhaseRegs<P> ph;     // static slots: edge m's phase row chunks; runtime: chunk q in ph.ph[0]
-  float rho;           // rho of edge m
+  floatx4 h;        // h(edge m)[4 q .. 4 q + 3]
+  PhaseRegs<P> ph;  // fixed slots: edge m's zw; runtime: chunk q of its phase row
+  float rho;        // runtime slots: rho of edge m
 };
 
+// ph_r spans the zw rows (fixed slots) or the phase rows (runtime slots).
 template <class P>
 __device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amdgpu_buffer_rsrc_t ph_r,
                                                __amdgpu_buffer_rsrc_t rho_r, int tb, int m, int q) {
@@ -1275,11 +1306,12 @@ __device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amd
   const int e = tb + m;
   t.h = bload4(h_r, (e * 16 + 4 * q) * 4);
   if constexpr (P::kStatic) {
-    load_phases<P>(t.ph, ph_r, e);
+    t.ph.ph = bload4(ph_r, e * 16);
+    t.rho = 0.f;
   } else {
-    t.ph.ph[0] = bload4(ph_r, (e * kPhaseRow + 4 * q) * 4);
+    t.ph.ph = bload4(ph_r, (e * kPhaseRow + 4 * q) * 4);
+    t.rho = bload1(rho_r, e * 4);
   }
-  t.rho = bload1(rho_r, e * 4);
   return t;
 }
 
@@ -1296,15 +1328,11 @@ __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const Fwd
   for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], cur.h[s], acc[nt]);
-  float rp[5];
+  Powers<P> pw;
   if constexpr (P::kStatic) {
-    rp[0] = 1.f;
-    rp[1] = cur.rho;
-    rp[2] = cur.rho * cur.rho;
-    rp[3] = rp[2] * cur.rho;
-    rp[4] = rp[2] * rp[2];
+    pw = powers<P>(cur.ph.ph);
   } else {
-    stage_phases_lanes(a, Ph, cur.ph.ph[0], cur.rho, m, q);
+    stage_phases_lanes(a, Ph, cur.ph.ph, cur.rho, m, q);
     wave_sync();
   }
   // V = F u per slot, summed over each output's slots and stored
@@ -1319,7 +1347,7 @@ __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const Fwd
     } else {
       float fr, fi;
       if constexpr (P::kStatic)
-        static_factor<P>(cur.ph, rp, s, fr, fi);
+        static_factor<P>(pw, s, fr, fi);
       else
         runtime_factor(Ph + m * kPhStride, w, fr, fi);
       sr += fr * ur - fi * ui;
@@ -1363,7 +1391,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ?
     z0[nt] = *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q);
   }
   const auto h_r = span(a.h + g0 * 16, (int64_t)ng * 64);
-  const auto ph_r = span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
+  const auto ph_r = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
+                               : span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
   const auto rho_r = span(a.rho_g + g0, (int64_t)ng * 4);
   const auto out_r = span(a.out + g0 * d_out, (int64_t)ng * d_out * 4);
   // two tiles in flight: each buffer is refilled right after its tile's
@@ -1386,7 +1415,7 @@ template <class P>
 struct BwdTile {
   floatx4 h;        // h(edge 4 q + i)[m], i < 4
   PhaseRegs<P> ph;  // as in the forward
-  float rho, w;     // edge m
+  float rho, w;     // edge m (rho: runtime slots)
   int64_t tgt;      // runtime slots: the target of edge m
 };
 
@@ -1399,13 +1428,14 @@ __device__ __forceinline__ BwdTile<P> load_bwd(__amdgpu_buffer_rsrc_t h_r, __amd
   for (int i = 0; i < 4; ++i) t.h[i] = bload1(h_r, ((tb + 4 * q + i) * 16 + m) * 4);
   const int e = tb + m;
   if constexpr (P::kStatic) {
-    load_phases<P>(t.ph, ph_r, e);
+    t.ph.ph = bload4(ph_r, e * 16);
     t.tgt = 0;
+    t.rho = 0.f;
   } else {
-    t.ph.ph[0] = bload4(ph_r, (e * kPhaseRow + 4 * q) * 4);
+    t.ph.ph = bload4(ph_r, (e * kPhaseRow + 4 * q) * 4);
     t.tgt = bload_i64(t_r, e * 8);
+    t.rho = bload1(rho_r, e * 4);
   }
-  t.rho = bload1(rho_r, e * 4);
   t.w = bload1(w_r, e * 4);
   return t;
 }
@@ -1457,19 +1487,14 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
   float wv[NT][4];
   float dwp = 0.f;  // this lane's share of dweights(edge m)
   if constexpr (P::kStatic) {
-    float rp[5];
-    rp[0] = 1.f;
-    rp[1] = cur.rho;
-    rp[2] = cur.rho * cur.rho;
-    rp[3] = rp[2] * cur.rho;
-    rp[4] = rp[2] * rp[2];
+    const Powers<P> pw = powers<P>(cur.ph.ph);
 #pragma unroll
     for (int s = 0; s < 2 * NT; ++s) {
       const uint32_t w = P::word(s);
       const int b = group_start<P>(s);
       if ((w & kSlotActive) && b == s) dwp += outs.gr[s] * outs.rr[s] + outs.gi[s] * outs.ri[s];
       float fr = 1.f, fi = 0.f;
-      if ((w & kSlotActive) && !(w & kSlotReal)) static_factor<P>(cur.ph, rp, s, fr, fi);
+      if ((w & kSlotActive) && !(w & kSlotReal)) static_factor<P>(pw, s, fr, fi);
       const float gr = (w & kSlotActive) ? outs.gr[b] : 0.f, gim = (w & kSlotActive) ? outs.gi[b] : 0.f;
       wv[s >> 1][2 * (s & 1)] = cur.w * (fr * gr + fi * gim);
       wv[s >> 1][2 * (s & 1) + 1] = cur.w * (fr * gim - fi * gr);
@@ -1477,7 +1502,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
   } else {
     // the targets' gradient rows through LDS (zero for absent edges and past d_out)
     const int GS = a.gstride;
-    stage_phases_lanes(a, Ph, cur.ph.ph[0], cur.rho, m, q);
+    stage_phases_lanes(a, Ph, cur.ph.ph, cur.rho, m, q);
     if (q == 0) Tg[m] = cur.tgt;
     wave_sync();
     for (int e = q; e < kMT; e += 4) {
@@ -1530,7 +1555,8 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
 }
 
 template <int NT, class P>
-__global__ __launch_bounds__(64) void factored_backward_lanes(FactArgs<float> a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? 2 : 1))) void factored_backward_lanes(
+    FactArgs<float> a) {
   constexpr int ZS = 16 * NT + 4;
   constexpr int kZWords = 17 * ZS, kWWords = 16 * NT * kWtStride;
   __shared__ __align__(16) float Sh[kZWords > kWWords ? kZWords : kWWords];  // Z in, then W's transpose, then dZ out
@@ -1562,7 +1588,8 @@ __global__ __launch_bounds__(64) void factored_backward_lanes(FactArgs<float> a)
   }
   BwdSpans sp;
   sp.h = span(a.h + g0 * 16, (int64_t)ng * 64);
-  sp.ph = span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
+  sp.ph = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
+                     : span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
   sp.rho = span(a.rho_g + g0, (int64_t)ng * 4);
   sp.w = span(a.weights + g0, (int64_t)ng * 4);
   sp.t = span(a.target_g + g0, (int64_t)ng * 8);
@@ -1981,7 +2008,7 @@ bool matches(const FactArgs<float>& a) {
 void launch_grouped(bool forward, const FactArgs<float>& a, hipStream_t stream) {
   if (a.n_slots > 0) {
     const char* env = std::getenv("GM_FACTORED_STATIC");
-    const bool fixed = env == nullptr || env[0] != '0';
+    const bool fixed = (env == nullptr || env[0] != '0') && a.zw_g != nullptr;
     if (fixed && matches<SlotsF2>(a)) return launch_lanes_nt<(SlotsF2::kSlots + 1) / 2, SlotsF2>(forward, a, stream);
     if (fixed && matches<SlotsF1>(a)) return launch_lanes_nt<(SlotsF1::kSlots + 1) / 2, SlotsF1>(forward, a, stream);
     switch ((a.n_slots + 1) / 2) {
@@ -2186,11 +2213,10 @@ GM_FACT_EXPORTS(double, f64)
 
 extern "C" int gm_factored_forward_grouped_f32(
     const float* h_g, const float* const* z, const int64_t* node_stride, const int64_t* t_stride,
-    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const int32_t* desc,
-    const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order, int64_t n_nodes,
-    int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
-    int64_t d_out, float* rows_g,
-    void* stream) {
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
+    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
+    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+    int64_t n_blocks, int64_t d_out, float* rows_g, void* stream) {
   GM_REQUIRE(z && node_stride && t_stride && width, "the mix runs must be host arrays");
   const gm::Runs<float> runs{z, nullptr, node_stride, t_stride, width, n_runs};
   gm::FactArgs<float> a;
@@ -2201,6 +2227,8 @@ extern "C" int gm_factored_forward_grouped_f32(
   GM_REQUIRE(rows_g, "rows must be a device pointer");
   a.out = rows_g;
   a.group_order = group_order;
+  GM_REQUIRE(zw_g == nullptr || gm::aligned(zw_g, 16), "zw_g must be a 16-byte aligned device pointer (or null)");
+  a.zw_g = zw_g;
   gm::launch_grouped(true, a, (hipStream_t)stream);
   return gm::check_launch("factored_forward_grouped");
 }
@@ -2208,11 +2236,10 @@ extern "C" int gm_factored_forward_grouped_f32(
 extern "C" int gm_factored_backward_grouped_f32(
     const float* g, const int64_t* target_g, const float* weights_g, const float* rows_g, const float* h_g,
     const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
-    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const int32_t* desc,
-    const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order, int64_t n_nodes,
-    int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
-    int64_t d_out, float* dh_g,
-    float* dweights_g, void* stream) {
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
+    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
+    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+    int64_t n_blocks, int64_t d_out, float* dh_g, float* dweights_g, void* stream) {
   GM_REQUIRE(z && dz && node_stride && t_stride && width, "the mix runs must be host arrays");
   const gm::Runs<float> runs{z, dz, node_stride, t_stride, width, n_runs};
   gm::FactArgs<float> a;
@@ -2225,6 +2252,8 @@ extern "C" int gm_factored_backward_grouped_f32(
   for (int r = 0; r < a.n_seg; ++r) GM_REQUIRE(a.seg[r].dz != nullptr, "every mix gradient run must be a device pointer");
   a.g = g;
   a.group_order = group_order;
+  GM_REQUIRE(zw_g == nullptr || gm::aligned(zw_g, 16), "zw_g must be a 16-byte aligned device pointer (or null)");
+  a.zw_g = zw_g;
   a.target_g = target_g;
   a.weights = weights_g;
   a.rows = rows_g;

@@ -49,8 +49,8 @@ SIGNATURES_F32 = {
     "gm_radial_trunk_forward_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_D, _P, _P]),
     "gm_radial_trunk_backward_f32": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_D, _P, _P, _P]),
     "gm_radial_trunk_partials": (ctypes.c_int64, [_I]),
-    "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 6 + [_I] * 10 + [_P, _P]),
-    "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 6 + [_I] * 10 + [_P] * 3),
+    "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P, _P]),
+    "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3),
     "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
     "gm_factored_lane_tables": (ctypes.c_int, [_P] + [_I] * 6 + [_P] * 3),
 }
@@ -568,9 +568,10 @@ def _check_order(group_order: Tensor | None, group_source: Tensor) -> None:
         raise ValueError("group_order must be a contiguous int64 permutation of the groups, on their device")
 
 
-def factored_forward_grouped(h_g: Tensor, runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor, pa: int,
-                             pt: int, desc: Tensor, group_ptr: Tensor, group_source: Tensor, group_order: Tensor | None,
-                             K: int, wc: int, wr: int, d_out: int) -> Tensor:
+def factored_forward_grouped(h_g: Tensor, runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor,
+                             zw_g: Tensor | None, pa: int, pt: int, desc: Tensor, group_ptr: Tensor,
+                             group_source: Tensor, group_order: Tensor | None, K: int, wc: int, wr: int,
+                             d_out: int) -> Tensor:
     """The rows in the grouping's order, every per-edge stream read in that order."""
     out = torch.empty(h_g.shape[0], d_out, dtype=h_g.dtype, device=h_g.device)
     if h_g.shape[0] == 0:
@@ -579,16 +580,16 @@ def factored_forward_grouped(h_g: Tensor, runs: MixRuns, n_nodes: int, phase_g: 
     hd = host_desc32(desc)
     _call("gm_factored_forward_grouped_f32", _ptr(h_g), ctypes.cast(runs.z, ctypes.c_void_p),
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
-          ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), hd.data_ptr(),
+          ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),
           _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, h_g.shape[0], group_source.shape[0], K, wc,
           wr, pa, pt, hd.shape[0], d_out, _ptr(out), _stream(h_g.device))
     return out
 
 
 def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, rows_g: Tensor, h_g: Tensor,
-                              runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor, pa: int, pt: int,
-                              desc: Tensor, group_ptr: Tensor, group_source: Tensor, group_order: Tensor | None,
-                              K: int, wc: int, wr: int, dh_g: Tensor) -> Tensor:
+                              runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor, zw_g: Tensor | None,
+                              pa: int, pt: int, desc: Tensor, group_ptr: Tensor, group_source: Tensor,
+                              group_order: Tensor | None, K: int, wc: int, wr: int, dh_g: Tensor) -> Tensor:
     """dh (grouping order) into ``dh_g``, the mix gradients into the runs'
     gradient arrays; returns dweights in the grouping's order."""
     dweights = torch.empty_like(weights_g)
@@ -599,7 +600,7 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
     _call("gm_factored_backward_grouped_f32", _ptr(g), _ptr(target_g), _ptr(weights_g), _ptr(rows_g), _ptr(h_g),
           ctypes.cast(runs.z, ctypes.c_void_p), ctypes.cast(runs.dz, ctypes.c_void_p),
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
-          ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), hd.data_ptr(),
+          ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),
           _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, h_g.shape[0], group_source.shape[0], K,
           wc, wr, pa, pt, hd.shape[0], g.shape[1], _ptr(dh_g), _ptr(dweights), _stream(h_g.device))
     return dweights

@@ -479,6 +479,7 @@ class GroupedStreams:
     target_g: Tensor
     pa: int
     pt: int
+    zw_g: Tensor | None = None  # (E, 4): r e^{i phi}, e^{i gamma} (order-1 phases) in grouping order
     group_order: Tensor | None = None
 
 
@@ -502,8 +503,13 @@ def grouped_streams(edges: Any, order: Tensor, cutoff: float, pa: int, pt: int, 
         phase_g = torch.zeros(perm.shape[0], 8, 2, dtype=dtype, device=perm.device)
         phase_g[:, :pa] = ang.to(dtype)
         phase_g[:, pa:pa + pt] = tra.to(dtype)
+        # r e^{i phi} and e^{i gamma}: every block factor is a product of their powers
+        r64 = edges.distances.index_select(0, perm).double() / cutoff
+        a1 = edges.angular_phases[:, 1].index_select(0, perm).to(torch.complex128) * r64
+        t1 = edges.transport_phases[:, 1].index_select(0, perm).to(torch.complex128)
+        zw_g = torch.stack([a1.real, a1.imag, t1.real, t1.imag], dim=1).to(dtype).contiguous()
         streams = GroupedStreams(perm, inv, rho_g, phase_g.contiguous(),
-                                 edges.target_index.index_select(0, perm).contiguous(), pa, pt)
+                                 edges.target_index.index_select(0, perm).contiguous(), pa, pt, zw_g)
     for stale in [k for k, (ref, _) in _STREAMS.items() if ref() is None]:
         del _STREAMS[stale]
     _STREAMS[key] = (weakref.ref(edges.edge_index), streams)
@@ -536,8 +542,9 @@ class FactoredHeadsGrouped(torch.autograd.Function):
         for head in range(H):
             runs = _heads_runs(meta, mixes, head, None)
             with torch.profiler.record_function("gm::kernel/pairs"):
-                r = _native.factored_forward_grouped(h_g[head], runs, meta["n_nodes"], st.phase_g, st.rho_g, st.pa,
-                                                     st.pt, meta["desc"], meta["group_ptr"], meta["group_source"],
+                r = _native.factored_forward_grouped(h_g[head], runs, meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g,
+                                                     st.pa, st.pt, meta["desc"], meta["group_ptr"],
+                                                     meta["group_source"],
                                                      meta["group_order"], meta["K"], meta["wc"], meta["wr"],
                                                      meta["d_out"])
             with torch.profiler.record_function("gm::kernel/aggregate"):
@@ -565,7 +572,7 @@ class FactoredHeadsGrouped(torch.autograd.Function):
             with torch.profiler.record_function("gm::kernel/pairs_backward"):
                 dalpha_g[:, head] = _native.factored_backward_grouped(
                     grad[:, head].contiguous(), st.target_g, alpha_g[:, head].contiguous(), rows[head], h_g[head], runs,
-                    meta["n_nodes"], st.phase_g, st.rho_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
+                    meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
                     meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"], dh_g[head])
         dalpha = torch.empty_like(alpha)
         dalpha.index_copy_(0, st.perm, dalpha_g)

@@ -258,7 +258,12 @@ int gm_factored_backward_seg_f64(const double* g, const int64_t* target, const d
  * target_g, weights_g, rows_g (n_edges, d_out), dh_g and dweights_g belongs to
  * the g-th edge of the grouping (order[g] in the others' terms).  A tile's
  * loads are then contiguous and issued before the previous tile finishes.
- * The mixes come as runs (see gm_factored_forward_seg_*).  group_order
+ * The mixes come as runs (see gm_factored_forward_seg_*).  zw_g
+ * (n_edges, 4), or NULL, holds per edge (in the same order) r e^{i phi} and
+ * e^{i gamma} (r = rho, phi and gamma the angular and transport angles, the
+ * order-1 entries of the phase tables); given it, plans with four copies per
+ * frequency and head form every block factor (r e^{i phi})^a (e^{i gamma})^s
+ * from it by products instead of reading phase_g.  group_order
  * (n_groups,), or NULL, lists the groups in launch order: largest first
  * keeps the long pole groups off the end of the launch.  No counterpart in
  * the reference, whose kernels index every per-edge table through the
@@ -266,16 +271,16 @@ int gm_factored_backward_seg_f64(const double* g, const int64_t* target, const d
  * gm_factored_forward_seg / backward_seg on the permuted streams. */
 int gm_factored_forward_grouped_f32(const float* h_g, const float* const* z, const int64_t* node_stride,
                                     const int64_t* t_stride, const int64_t* width, int64_t n_runs,
-                                    const float* phase_g, const float* rho_g, const int32_t* desc,
-                                    const int64_t* group_ptr, const int64_t* group_source,
+                                    const float* phase_g, const float* rho_g, const float* zw_g,
+                                    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source,
                                     const int64_t* group_order, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
                                     int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
                                     int64_t d_out, float* rows_g, void* stream);
 int gm_factored_backward_grouped_f32(const float* g, const int64_t* target_g, const float* weights_g,
                                      const float* rows_g, const float* h_g, const float* const* z, float* const* dz,
                                      const int64_t* node_stride, const int64_t* t_stride, const int64_t* width,
-                                     int64_t n_runs, const float* phase_g, const float* rho_g, const int32_t* desc,
-                                     const int64_t* group_ptr, const int64_t* group_source,
+                                     int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
+                                     const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source,
                                      const int64_t* group_order, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
                                      int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
                                      int64_t d_out, float* dh_g, float* dweights_g, void* stream);
