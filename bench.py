@@ -59,18 +59,22 @@ def softmax_cost(E: int, N: int, D: int, H: int) -> dict[str, tuple[float, float
     }
 
 
-def factored_cost(E: int, N: int, K: int, C: int, wc: int, d_out: int, n_f: int) -> dict[str, tuple[float, float]]:
-    """(bytes, flops) of one launch per head: h, the phase tables, rho, the
-    source grouping and the rows cross once; Z(j) once per node.  FLOPs: the
-    2 K C combination per edge (one K-long dot per packed column), the block
-    factors, the dZ and dh products in the backward."""
-    per_edge_in = 4 * (K - 1) + 2 * 8 * n_f + 4 + 8 + 8  # h, angular + transport, rho, order, source
+def factored_cost(E: int, N: int, K: int, C: int, wc: int, d_out: int, H: int) -> dict[str, tuple[float, float]]:
+    """(bytes, flops) of one launch of the grouped factored ops.  Forward (per
+    head): h (K - 1 floats), zw (4 floats) in and the row (d_out floats) out
+    per edge, Z(j) (K C floats) once per node.  Backward (per head): h, zw,
+    weight, target, the row and the target's gradient row in, dh and dweight
+    out per edge; Z(j) in and dZ(j) out per node.  Aggregate (all heads at
+    once): inv, alpha's row and every head's row per edge, the output row per
+    node.  FLOPs: 2 K C per edge forward (the K-long combination of each
+    packed column) plus the block factors, 4 K C backward (dh and dZ)."""
     z = N * 4 * K * C
+    fwd_edge = 4 * (K - 1) + 16 + 4 * d_out
+    bwd_edge = 4 * (K - 1) + 16 + 4 + 8 + 2 * 4 * d_out + 4 * (K - 1) + 4
     return {
-        "factored_forward": (E * (per_edge_in + 4 * d_out) + z, E * (2.0 * K * C + 8 * wc)),
-        "factored_aggregate": (E * (4 * d_out + 4) + N * (4 * d_out + 8), E * 2.0 * d_out),
-        "factored_backward_aggregated": (E * (per_edge_in + 4 * d_out + 4 + 4 + 8 + 4 * (K - 1)) + N * 4 * d_out + 2 * z,
-                                         E * (4.0 * K * C + 8 * wc + 2 * d_out)),
+        "factored_forward": (E * fwd_edge + z, E * (2.0 * K * C + 8 * wc)),
+        "factored_aggregate": (E * (8 + 4 * H + 4 * H * d_out) + N * 4 * H * d_out, E * 2.0 * H * d_out),
+        "factored_backward_aggregated": (E * bwd_edge + 2 * z, E * (4.0 * K * C + 8 * wc)),
     }
 
 
@@ -228,6 +232,7 @@ def main() -> None:
     timer.wrap(_native, "factored_forward_grouped", "factored_forward")
     timer.wrap(_native, "factored_backward_grouped", "factored_backward_aggregated")
     timer.wrap(_native, "aggregate_gather", "factored_aggregate")
+    timer.wrap(_native, "aggregate_heads", "factored_aggregate")
     timer.wrap(_native, "radial_trunk_forward", "radial_trunk_forward")
     timer.wrap(_native, "radial_trunk_backward", "radial_trunk_backward")
 
@@ -289,7 +294,7 @@ def main() -> None:
     kern = mhsa.heads[0].value
     fp = fused_factored.plan(kern)
     K = kern.complex_head.in_features + 1
-    costs.update(factored_cost(E, N, K, 2 * fp.wc + fp.wr, fp.wc, fp.d_out, 5))
+    costs.update(factored_cost(E, N, K, 2 * fp.wc + fp.wr, fp.wc, fp.d_out, HEADS))
     # the radial trunk for all heads: rho in, h (H, E, T) out; 2 T B + ~20 T FLOPs per edge and head
     costs["radial_trunk_forward"] = (E * (4 + HEADS * 4 * (K - 1)), E * HEADS * (2.0 * (K - 1) * 8 + 20 * (K - 1)))
     costs["radial_trunk_backward"] = (E * (4 + HEADS * 4 * (K - 1)), E * HEADS * (4.0 * (K - 1) * 8 + 30 * (K - 1)))

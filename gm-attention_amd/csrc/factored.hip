@@ -283,6 +283,78 @@ __global__ __launch_bounds__(256) void aggregate_kernel(AggArgs<T> a) {
   if (slot == 0) o[c] = s;
 }
 
+// Every head's aggregate in one pass: out[i, h, :] = sum_{e -> i} alpha[e, h]
+// rows[h, inv[e], :] (rows kept per head in the grouping's order).  One wave
+// per target; lane l owns the outputs l, l + 64, l + 128 of the target's
+// H d_out; the edges go in CSR order, four a step with their loads in
+// flight together, so every sum has a fixed order.
+struct AggHeadsArgs {
+  const float* rows;   // (H, n_rows, d_out)
+  const float* alpha;  // (n_edges, H)
+  const int64_t* inv;
+  const int64_t* row_ptr;
+  float* out;  // (n_targets, H, d_out)
+  int64_t n_targets, n_rows;
+  int H, d_out;
+};
+
+__global__ __launch_bounds__(256) void aggregate_heads_kernel(AggHeadsArgs a) {
+  const int64_t i = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= a.n_targets) return;
+  const int W = a.H * a.d_out;
+  int hh[3], cc[3];
+  bool live[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int o = lane + 64 * k;
+    live[k] = o < W;
+    hh[k] = live[k] ? o / a.d_out : 0;
+    cc[k] = live[k] ? o - hh[k] * a.d_out : 0;
+  }
+  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+  float s[3] = {0.f, 0.f, 0.f};
+  for (int64_t e = e0; e < e1; e += 4) {
+    float w[4][3], v[4][3];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool in = e + u < e1;
+      const int64_t r = in ? a.inv[e + u] : 0;
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        w[u][k] = in && live[k] ? a.alpha[(e + u) * a.H + hh[k]] : 0.f;
+        v[u][k] = in && live[k] ? a.rows[((int64_t)hh[k] * a.n_rows + r) * a.d_out + cc[k]] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) s[k] += w[u][k] * v[u][k];
+  }
+  float* o = a.out + i * W;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+    if (live[k]) o[lane + 64 * k] = s[k];
+}
+
+// dst_t[h, g] = src[perm[g], h] (a row gather and a transpose), and its
+// inverse dst[perm[g], h] = src_t[h, g]: one thread per row g.
+__global__ __launch_bounds__(256) void gather_transpose_kernel(const float* src, const int64_t* perm, int64_t n,
+                                                               int width, float* dst_t) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n) return;
+  const float* row = src + perm[g] * width;
+  for (int h = 0; h < width; ++h) dst_t[h * n + g] = row[h];
+}
+
+__global__ __launch_bounds__(256) void scatter_transpose_kernel(const float* src_t, const int64_t* perm, int64_t n,
+                                                                int width, float* dst) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n) return;
+  float* row = dst + perm[g] * width;
+  for (int h = 0; h < width; ++h) row[h] = src_t[h * n + g];
+}
+
 // ----------------------------------------------------------------- backward
 
 template <typename T, int KMAX, int NQ>
@@ -2301,4 +2373,41 @@ extern "C" int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, in
   if (slotcol)
     for (int i = 0; i < 128; ++i) slotcol[i] = a.n_slots ? a.slotcol[i] : (uint8_t)0xFF;
   return GM_OK;
+}
+
+extern "C" int gm_factored_aggregate_heads_f32(const float* rows, const int64_t* inv, const float* alpha,
+                                               const int64_t* row_ptr, int64_t n_targets, int64_t n_edges, int64_t H,
+                                               int64_t d_out, float* out, void* stream) {
+  GM_REQUIRE(n_targets >= 0 && n_edges >= 0, "sizes must be non-negative");
+  GM_REQUIRE(H >= 1 && d_out >= 1 && H * d_out <= 192, "H d_out must be in [1, 192]");
+  GM_REQUIRE(n_targets < (int64_t(1) << 31) * gm::kWavesPerBlock, "too many targets for one launch");
+  if (n_targets == 0) return GM_OK;
+  GM_REQUIRE(row_ptr && out && (n_edges == 0 || (rows && inv && alpha)),
+             "rows, inv, alpha, row_ptr and out must be device pointers");
+  const gm::AggHeadsArgs a{rows, alpha, inv, row_ptr, out, n_targets, n_edges, (int)H, (int)d_out};
+  hipLaunchKernelGGL(gm::aggregate_heads_kernel, dim3((unsigned)gm::blocks_for(n_targets)), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  return gm::check_launch("factored_aggregate_heads");
+}
+
+extern "C" int gm_gather_transpose_f32(const float* src, const int64_t* perm, int64_t n, int64_t width, float* dst_t,
+                                       void* stream) {
+  GM_REQUIRE(n >= 0 && width >= 1 && width <= 64, "n must be non-negative and width in [1, 64]");
+  if (n == 0) return GM_OK;
+  GM_REQUIRE(src && perm && dst_t, "src, perm and dst_t must be device pointers");
+  GM_REQUIRE(n < (int64_t(1) << 31) * 256, "too many rows for one launch");
+  hipLaunchKernelGGL(gm::gather_transpose_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     src, perm, n, (int)width, dst_t);
+  return gm::check_launch("gather_transpose");
+}
+
+extern "C" int gm_scatter_transpose_f32(const float* src_t, const int64_t* perm, int64_t n, int64_t width, float* dst,
+                                        void* stream) {
+  GM_REQUIRE(n >= 0 && width >= 1 && width <= 64, "n must be non-negative and width in [1, 64]");
+  if (n == 0) return GM_OK;
+  GM_REQUIRE(src_t && perm && dst, "src_t, perm and dst must be device pointers");
+  GM_REQUIRE(n < (int64_t(1) << 31) * 256, "too many rows for one launch");
+  hipLaunchKernelGGL(gm::scatter_transpose_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, src_t, perm, n, (int)width, dst);
+  return gm::check_launch("scatter_transpose");
 }

@@ -53,6 +53,9 @@ SIGNATURES_F32 = {
     "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3),
     "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
     "gm_factored_lane_tables": (ctypes.c_int, [_P] + [_I] * 6 + [_P] * 3),
+    "gm_factored_aggregate_heads_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_P, _P]),
+    "gm_gather_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
+    "gm_scatter_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
 }
 
 
@@ -571,9 +574,13 @@ def _check_order(group_order: Tensor | None, group_source: Tensor) -> None:
 def factored_forward_grouped(h_g: Tensor, runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor,
                              zw_g: Tensor | None, pa: int, pt: int, desc: Tensor, group_ptr: Tensor,
                              group_source: Tensor, group_order: Tensor | None, K: int, wc: int, wr: int,
-                             d_out: int) -> Tensor:
-    """The rows in the grouping's order, every per-edge stream read in that order."""
-    out = torch.empty(h_g.shape[0], d_out, dtype=h_g.dtype, device=h_g.device)
+                             d_out: int, out: Tensor | None = None) -> Tensor:
+    """The rows in the grouping's order, every per-edge stream read in that order
+    (into ``out`` (n_edges, d_out) when given)."""
+    if out is None:
+        out = torch.empty(h_g.shape[0], d_out, dtype=h_g.dtype, device=h_g.device)
+    elif out.shape != (h_g.shape[0], d_out) or not out.is_contiguous() or out.dtype != h_g.dtype:
+        raise ValueError("out must be a contiguous (n_edges, d_out) tensor in h's dtype")
     if h_g.shape[0] == 0:
         return out
     _check_order(group_order, group_source)
@@ -589,10 +596,15 @@ def factored_forward_grouped(h_g: Tensor, runs: MixRuns, n_nodes: int, phase_g: 
 def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, rows_g: Tensor, h_g: Tensor,
                               runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor, zw_g: Tensor | None,
                               pa: int, pt: int, desc: Tensor, group_ptr: Tensor, group_source: Tensor,
-                              group_order: Tensor | None, K: int, wc: int, wr: int, dh_g: Tensor) -> Tensor:
+                              group_order: Tensor | None, K: int, wc: int, wr: int, dh_g: Tensor,
+                              dweights: Tensor | None = None) -> Tensor:
     """dh (grouping order) into ``dh_g``, the mix gradients into the runs'
-    gradient arrays; returns dweights in the grouping's order."""
-    dweights = torch.empty_like(weights_g)
+    gradient arrays; returns dweights in the grouping's order (into
+    ``dweights`` when given)."""
+    if dweights is None:
+        dweights = torch.empty_like(weights_g)
+    elif dweights.shape != weights_g.shape or not dweights.is_contiguous() or dweights.dtype != weights_g.dtype:
+        raise ValueError("dweights must be a contiguous tensor shaped like weights_g")
     if h_g.shape[0] == 0:
         return dweights
     _check_order(group_order, group_source)
@@ -616,6 +628,43 @@ def lane_tables(desc: Tensor, wc: int, wr: int, d_out: int, pa: int, pt: int) ->
     slotcol = (ctypes.c_uint8 * 128)()
     _call("gm_factored_lane_tables", hd.data_ptr(), hd.shape[0], wc, wr, d_out, pa, pt, ctypes.byref(n), slot, slotcol)
     return n.value, list(slot), list(slotcol)
+
+
+def aggregate_heads(rows: Tensor, inv: Tensor, alpha: Tensor, row_ptr: Tensor) -> Tensor:
+    """``out[i, h] = sum_e alpha[e, h] rows[h, inv[e]]`` over each target's
+    edges: rows ``(H, E, d_out)``, alpha ``(E, H)``; ``(N, H, d_out)`` out."""
+    H, E, d_out = rows.shape
+    n_targets = row_ptr.shape[0] - 1
+    out = torch.empty(n_targets, H, d_out, dtype=rows.dtype, device=rows.device)
+    if rows.dtype != torch.float32 or alpha.dtype != torch.float32 or alpha.shape != (E, H):
+        raise ValueError("rows (H, E, d_out) and alpha (E, H) must be float32")
+    if not (rows.is_contiguous() and alpha.is_contiguous() and inv.is_contiguous() and row_ptr.is_contiguous()):
+        raise ValueError("rows, alpha, inv and row_ptr must be contiguous")
+    if n_targets == 0:
+        return out
+    _call("gm_factored_aggregate_heads_f32", _ptr(rows), _ptr(inv), _ptr(alpha), _ptr(row_ptr), n_targets, E, H,
+          d_out, _ptr(out), _stream(rows.device))
+    return out
+
+
+def gather_transpose(src: Tensor, perm: Tensor) -> Tensor:
+    """``dst_t[h, g] = src[perm[g], h]``: ``(n, width)`` in, ``(width, n)`` out."""
+    n, width = src.shape
+    if src.dtype != torch.float32 or not src.is_contiguous() or perm.shape != (n,) or not perm.is_contiguous():
+        raise ValueError("src must be a contiguous float32 (n, width) tensor and perm a contiguous (n,) index")
+    out = torch.empty(width, n, dtype=src.dtype, device=src.device)
+    _call("gm_gather_transpose_f32", _ptr(src), _ptr(perm), n, width, _ptr(out), _stream(src.device))
+    return out
+
+
+def scatter_transpose(src_t: Tensor, perm: Tensor) -> Tensor:
+    """``dst[perm[g], h] = src_t[h, g]``: ``(width, n)`` in, ``(n, width)`` out."""
+    width, n = src_t.shape
+    if src_t.dtype != torch.float32 or not src_t.is_contiguous() or perm.shape != (n,) or not perm.is_contiguous():
+        raise ValueError("src_t must be a contiguous float32 (width, n) tensor and perm a contiguous (n,) index")
+    out = torch.empty(n, width, dtype=src_t.dtype, device=src_t.device)
+    _call("gm_scatter_transpose_f32", _ptr(src_t), _ptr(perm), n, width, _ptr(out), _stream(src_t.device))
+    return out
 
 
 def aggregate_gather(rows_g: Tensor, inv: Tensor, weights: Tensor, row_ptr: Tensor) -> Tensor:

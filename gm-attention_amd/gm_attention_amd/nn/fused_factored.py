@@ -536,46 +536,45 @@ class FactoredHeadsGrouped(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx: Any, h_g: Tensor, alpha: Tensor, meta: dict, *mixes: Tensor) -> Tensor:
-        H = h_g.shape[0]
+        H, E = h_g.shape[0], h_g.shape[1]
         st: GroupedStreams = meta["streams"]
-        rows, outs = [], []
+        rows = torch.empty(H, E, meta["d_out"], dtype=h_g.dtype, device=h_g.device)
         for head in range(H):
             runs = _heads_runs(meta, mixes, head, None)
             with torch.profiler.record_function("gm::kernel/pairs"):
-                r = _native.factored_forward_grouped(h_g[head], runs, meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g,
-                                                     st.pa, st.pt, meta["desc"], meta["group_ptr"],
-                                                     meta["group_source"],
-                                                     meta["group_order"], meta["K"], meta["wc"], meta["wr"],
-                                                     meta["d_out"])
-            with torch.profiler.record_function("gm::kernel/aggregate"):
-                outs.append(_native.aggregate_gather(r, st.inv, alpha[:, head].contiguous(), meta["row_ptr"]))
-            rows.append(r)
+                _native.factored_forward_grouped(h_g[head], runs, meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g,
+                                                 st.pa, st.pt, meta["desc"], meta["group_ptr"], meta["group_source"],
+                                                 meta["group_order"], meta["K"], meta["wc"], meta["wr"],
+                                                 meta["d_out"], out=rows[head])
+        with torch.profiler.record_function("gm::kernel/aggregate"):
+            out = _native.aggregate_heads(rows, st.inv, alpha, meta["row_ptr"])
         ctx.meta = meta
-        ctx.save_for_backward(h_g, alpha, *rows, *mixes)
-        return torch.stack(outs, dim=1)
+        ctx.save_for_backward(h_g, alpha, rows, *mixes)
+        return out
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad: Tensor) -> tuple:
         meta = ctx.meta
         st: GroupedStreams = meta["streams"]
-        saved = ctx.saved_tensors
-        h_g, alpha = saved[0], saved[1]
+        h_g, alpha, rows, *mixes = ctx.saved_tensors
         H = h_g.shape[0]
-        rows, mixes = saved[2:2 + H], saved[2 + H:]
-        dmixes = [torch.zeros_like(m) for m in mixes]
+        # every source node has a group (and so every mix row is written) unless some node has no edge out
+        fill = torch.zeros_like if meta["group_source"].shape[0] < meta["n_nodes"] else torch.empty_like
+        dmixes = [fill(m) for m in mixes]
         dh_g = torch.empty_like(h_g)
-        alpha_g = alpha.index_select(0, st.perm)
-        dalpha_g = torch.empty_like(alpha_g)
+        alpha_gt = _native.gather_transpose(alpha, st.perm)  # (H, E) in the grouping's order
+        dalpha_gt = torch.empty_like(alpha_gt)
+        grad = grad.contiguous()
         for head in range(H):
             runs = _heads_runs(meta, mixes, head, dmixes)
             with torch.profiler.record_function("gm::kernel/pairs_backward"):
-                dalpha_g[:, head] = _native.factored_backward_grouped(
-                    grad[:, head].contiguous(), st.target_g, alpha_g[:, head].contiguous(), rows[head], h_g[head], runs,
+                _native.factored_backward_grouped(
+                    grad[:, head].contiguous(), st.target_g, alpha_gt[head], rows[head], h_g[head], runs,
                     meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
-                    meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"], dh_g[head])
-        dalpha = torch.empty_like(alpha)
-        dalpha.index_copy_(0, st.perm, dalpha_g)
+                    meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"], dh_g[head],
+                    dweights=dalpha_gt[head])
+        dalpha = _native.scatter_transpose(dalpha_gt, st.perm)
         return (dh_g, dalpha, None, *dmixes)
 
 

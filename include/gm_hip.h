@@ -315,6 +315,29 @@ int gm_radial_trunk_backward_f32(const float* dh, const float* rho, const float*
                                  const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B, double width,
                                  float* partial, float* dparams, void* stream);
 
+/* Every head's aggregate at once: out[i, h, :] = sum over target i's edges e
+ * (CSR order) of alpha[e, h] rows[h, inv[e], :].  rows (H, n_edges, d_out)
+ * holds each head's rows in the grouping's order (inv[e] = edge e's position
+ * there), alpha (n_edges, H) and out (n_targets, H, d_out); H d_out <= 192.
+ * Serves the heads of one layer at once where the reference aggregates each
+ * head on its own (fused/factored_cpu.cpp:110-130 `aggregate`, called from
+ * fused_factored.py:273-299 FactoredAggregate); the per-head sums are the
+ * same, in the same edge order. */
+int gm_factored_aggregate_heads_f32(const float* rows, const int64_t* inv, const float* alpha, const int64_t* row_ptr,
+                                    int64_t n_targets, int64_t n_edges, int64_t H, int64_t d_out, float* out,
+                                    void* stream);
+
+/* A row gather fused with a transpose, and its inverse:
+ *   gm_gather_transpose_f32:  dst_t[h, g] = src[perm[g], h]   src (n, width), dst_t (width, n)
+ *   gm_scatter_transpose_f32: dst[perm[g], h] = src_t[h, g]   src_t (width, n), dst (n, width)
+ * perm a permutation of 0..n-1, width <= 64.  Moves per-edge, per-head
+ * tables (attention weights and their gradients) between edge order and the
+ * grouping's order; no counterpart in the reference. */
+int gm_gather_transpose_f32(const float* src, const int64_t* perm, int64_t n, int64_t width, float* dst_t,
+                            void* stream);
+int gm_scatter_transpose_f32(const float* src_t, const int64_t* perm, int64_t n, int64_t width, float* dst,
+                             void* stream);
+
 /* The lane-owned output tables the grouped factored kernels use for a plan
  * (host only; nothing runs on the GPU).  When every block comes in
  * multiplicities of four with radial power equal to its angular order, lane
