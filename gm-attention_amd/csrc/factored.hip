@@ -285,9 +285,10 @@ __global__ __launch_bounds__(256) void aggregate_kernel(AggArgs<T> a) {
 
 // Every head's aggregate in one pass: out[i, h, :] = sum_{e -> i} alpha[e, h]
 // rows[h, inv[e], :] (rows kept per head in the grouping's order).  One wave
-// per target; lane l owns the outputs l, l + 64, l + 128 of the target's
-// H d_out; the edges go in CSR order, four a step with their loads in
-// flight together, so every sum has a fixed order.
+// per target: with d_out a multiple of four, lane l < H d_out / 4 owns the
+// four outputs 4 l .. 4 l + 3 (one 16-byte row piece a load), else lane l
+// owns the outputs l, l + 64, l + 128.  The edges go in CSR order, eight a
+// step with their loads in flight together, so every sum has a fixed order.
 struct AggHeadsArgs {
   const float* rows;   // (H, n_rows, d_out)
   const float* alpha;  // (n_edges, H)
@@ -297,6 +298,34 @@ struct AggHeadsArgs {
   int64_t n_targets, n_rows;
   int H, d_out;
 };
+
+constexpr int kAggStep = 8;
+
+__global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a) {
+  const int64_t i = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= a.n_targets) return;
+  const int q4 = a.d_out / 4, W4 = a.H * q4;
+  const bool live = lane < W4;
+  const int hh = live ? lane / q4 : 0, c4 = live ? lane - hh * q4 : 0;
+  const float* base = a.rows + (int64_t)hh * a.n_rows * a.d_out + 4 * c4;
+  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+  floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t e = e0; e < e1; e += kAggStep) {
+    float w[kAggStep];
+    floatx4 v[kAggStep];
+#pragma unroll
+    for (int u = 0; u < kAggStep; ++u) {
+      const bool in = live && e + u < e1;
+      const int64_t r = e + u < e1 ? a.inv[e + u] : 0;
+      w[u] = in ? a.alpha[(e + u) * a.H + hh] : 0.f;
+      v[u] = in ? *reinterpret_cast<const floatx4*>(base + r * a.d_out) : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < kAggStep; ++u) s += w[u] * v[u];
+  }
+  if (live) *reinterpret_cast<floatx4*>(a.out + i * (int64_t)a.H * a.d_out + 4 * lane) = s;
+}
 
 __global__ __launch_bounds__(256) void aggregate_heads_kernel(AggHeadsArgs a) {
   const int64_t i = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + (threadIdx.x >> 6);
@@ -2385,8 +2414,13 @@ extern "C" int gm_factored_aggregate_heads_f32(const float* rows, const int64_t*
   GM_REQUIRE(row_ptr && out && (n_edges == 0 || (rows && inv && alpha)),
              "rows, inv, alpha, row_ptr and out must be device pointers");
   const gm::AggHeadsArgs a{rows, alpha, inv, row_ptr, out, n_targets, n_edges, (int)H, (int)d_out};
-  hipLaunchKernelGGL(gm::aggregate_heads_kernel, dim3((unsigned)gm::blocks_for(n_targets)), dim3(256), 0,
-                     (hipStream_t)stream, a);
+  const bool vec = d_out % 4 == 0 && H * d_out <= 256 && gm::aligned(rows, 16) && gm::aligned(out, 16);
+  if (vec)
+    hipLaunchKernelGGL(gm::aggregate_heads_vec_kernel, dim3((unsigned)gm::blocks_for(n_targets)), dim3(256), 0,
+                       (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(gm::aggregate_heads_kernel, dim3((unsigned)gm::blocks_for(n_targets)), dim3(256), 0,
+                       (hipStream_t)stream, a);
   return gm::check_launch("factored_aggregate_heads");
 }
 

@@ -12,7 +12,7 @@
 // apply_radial_trunk, :605-607 _trunk_hidden; one Linear + SiLU layer).
 //
 // Forward: one thread per edge for every head, the basis computed once from
-// rho, the heads' parameters in LDS.  Backward: a fixed grid whose threads
+// rho, the heads' parameters as uniform operands.  Backward: a fixed grid whose threads
 // stride over the edges, per head accumulating their (T x B + T) gradient
 // terms in registers (recomputing the basis and pre-activation), then one
 // fixed-order reduction per workgroup into a partial row; a second kernel
@@ -40,40 +40,48 @@ struct TrunkArgs {
   float inv_width;      // 1 / sigma
 };
 
-__device__ __forceinline__ float silu_of(float x) { return x / (1.f + expf(-x)); }
+// exp(x) as 2^(x log2 e) on the hardware exponential, and 1 / x on the
+// hardware reciprocal (each within about an ulp of the rounded result; the
+// trunk's features and gradients then stay within a few 1e-7 relative of
+// the precise ones).
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sigmoid_of(float x) { return fast_rcp(1.f + fast_exp(-x)); }
 
-template <int T, int B>
-__device__ __forceinline__ void basis_of(float r, const float* centers, float inv_width, float* b) {
+// The heads' parameters and the basis centres are read-only for the whole
+// launch: read through the constant address space, they become uniform
+// (scalar) loads and SGPR operands.
+typedef const __attribute__((address_space(4))) float* ConstPtr;
+__device__ __forceinline__ ConstPtr as_const(const float* p) { return (ConstPtr)p; }
+
+template <int B>
+__device__ __forceinline__ void basis_of(float r, ConstPtr centers, float inv_width, float* b) {
   const float s = r * r;
 #pragma unroll
   for (int k = 0; k < B; ++k) {
     const float z = (s - centers[k]) * inv_width;
-    b[k] = expf(-0.5f * z * z);
+    b[k] = fast_exp(-0.5f * z * z);
   }
 }
 
+// One thread per edge for every head: the basis once, then each head's
+// Linear + SiLU with its parameters read as uniform (scalar) operands.
 template <int T, int B>
 __global__ __launch_bounds__(kTrunkThreads) void trunk_forward_kernel(TrunkArgs a) {
-  __shared__ float w[8][T * B + T];
-  __shared__ float cen[B];
-  for (int i = threadIdx.x; i < a.H * (T * B + T); i += blockDim.x) {
-    const int hh = i / (T * B + T), k = i % (T * B + T);
-    w[hh][k] = k < T * B ? a.weight[hh * T * B + k] : (a.bias ? a.bias[hh * T + (k - T * B)] : 0.f);
-  }
-  if (threadIdx.x < B) cen[threadIdx.x] = a.centers[threadIdx.x];
-  __syncthreads();
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= a.n_edges) return;
+  const ConstPtr weight = as_const(a.weight), bias = as_const(a.bias);
   float b[B];
-  basis_of<T, B>(a.rho[e], cen, a.inv_width, b);
+  basis_of<B>(a.rho[e], as_const(a.centers), a.inv_width, b);
   for (int hh = 0; hh < a.H; ++hh) {
+    const ConstPtr W = weight + hh * T * B;
     float out[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      float p = w[hh][T * B + t];
+      float p = bias ? bias[hh * T + t] : 0.f;
 #pragma unroll
-      for (int k = 0; k < B; ++k) p += w[hh][t * B + k] * b[k];
-      out[t] = silu_of(p);
+      for (int k = 0; k < B; ++k) p = fmaf(W[t * B + k], b[k], p);
+      out[t] = p * sigmoid_of(p);
     }
     float* dst = a.h + ((int64_t)hh * a.n_edges + e) * T;
 #pragma unroll
@@ -81,59 +89,78 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_forward_kernel(TrunkArgs 
   }
 }
 
+// A fixed grid whose threads stride over the edges; per head and per half of
+// its features, each thread accumulates its gradient terms in registers
+// (recomputing the basis and pre-activation, the next edge's loads issued
+// before this edge's arithmetic), then one fixed-order reduction per
+// workgroup into a partial row.
 template <int T, int B>
 __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_kernel(TrunkArgs a) {
-  constexpr int P = T * B + T;
-  __shared__ float w[8][P];
-  __shared__ float cen[B];
-  __shared__ float red[kTrunkThreads / 64][P];  // per-wave sums
-  for (int i = threadIdx.x; i < a.H * P; i += blockDim.x) {
-    const int hh = i / P, k = i % P;
-    w[hh][k] = k < T * B ? a.weight[hh * T * B + k] : (a.bias ? a.bias[hh * T + (k - T * B)] : 0.f);
-  }
-  if (threadIdx.x < B) cen[threadIdx.x] = a.centers[threadIdx.x];
-  __syncthreads();
+  constexpr int P = T * B + T, TH = T / 2, PH = TH * B + TH;
+  __shared__ float red[kTrunkThreads / 64][PH];  // per-wave sums
+  const ConstPtr weight = as_const(a.weight), bias = as_const(a.bias), centers = as_const(a.centers);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int hh = 0; hh < a.H; ++hh) {
-    float acc[P];
+  const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int pass = 0; pass < 2 * a.H; ++pass) {
+    const int hh = pass >> 1, t0 = (pass & 1) * TH;
+    const ConstPtr W = weight + hh * T * B;
+    float acc[PH];
 #pragma unroll
-    for (int i = 0; i < P; ++i) acc[i] = 0.f;
-    // each thread's edges e = tid, tid + stride, ... in order
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < a.n_edges; e += stride) {
+    for (int i = 0; i < PH; ++i) acc[i] = 0.f;
+    const float* dh = a.dh + (int64_t)hh * a.n_edges * T + t0;
+    float4 g[TH / 4];
+    float r = 0.f;
+    if (first < a.n_edges) {
+      r = a.rho[first];
+#pragma unroll
+      for (int u = 0; u < TH / 4; ++u) g[u] = *reinterpret_cast<const float4*>(dh + first * T + 4 * u);
+    }
+    // each thread's edges e = first, first + stride, ... in order
+    for (int64_t e = first; e < a.n_edges; e += stride) {
+      const float rc = r;
+      float gv[TH];
+#pragma unroll
+      for (int u = 0; u < TH / 4; ++u) {
+        gv[4 * u] = g[u].x;
+        gv[4 * u + 1] = g[u].y;
+        gv[4 * u + 2] = g[u].z;
+        gv[4 * u + 3] = g[u].w;
+      }
+      const int64_t en = e + stride;
+      if (en < a.n_edges) {
+        r = a.rho[en];
+#pragma unroll
+        for (int u = 0; u < TH / 4; ++u) g[u] = *reinterpret_cast<const float4*>(dh + en * T + 4 * u);
+      }
       float b[B];
-      basis_of<T, B>(a.rho[e], cen, a.inv_width, b);
-      const float* g = a.dh + ((int64_t)hh * a.n_edges + e) * T;
+      basis_of<B>(rc, centers, a.inv_width, b);
 #pragma unroll
-      for (int t4 = 0; t4 < T; t4 += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(g + t4);
-        const float gv[4] = {v.x, v.y, v.z, v.w};
+      for (int t = 0; t < TH; ++t) {
+        float p = bias ? bias[hh * T + t0 + t] : 0.f;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int t = t4 + u;
-          float p = w[hh][T * B + t];
+        for (int k = 0; k < B; ++k) p = fmaf(W[(t0 + t) * B + k], b[k], p);
+        const float sg = sigmoid_of(p);
+        const float dp = gv[t] * sg * (1.f + p * (1.f - sg));  // dh * d silu / d pre
 #pragma unroll
-          for (int k = 0; k < B; ++k) p += w[hh][t * B + k] * b[k];
-          const float sg = 1.f / (1.f + expf(-p));
-          const float dp = gv[u] * sg * (1.f + p * (1.f - sg));  // dh * d silu / d pre
-#pragma unroll
-          for (int k = 0; k < B; ++k) acc[t * B + k] += dp * b[k];
-          acc[T * B + t] += dp;
-        }
+        for (int k = 0; k < B; ++k) acc[t * B + k] = fmaf(dp, b[k], acc[t * B + k]);
+        acc[TH * B + t] += dp;
       }
     }
     // the block's sum in a fixed order: a butterfly per wave, then the waves in order
 #pragma unroll
-    for (int i = 0; i < P; ++i) {
+    for (int i = 0; i < PH; ++i) {
       float v = acc[i];
       for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
       if (lane == 0) red[wave][i] = v;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < P; i += blockDim.x) {
+    for (int i = threadIdx.x; i < PH; i += blockDim.x) {
       float sum = 0.f;
       for (int wv = 0; wv < kTrunkThreads / 64; ++wv) sum += red[wv][i];
-      a.partial[((int64_t)blockIdx.x * a.H + hh) * P + i] = sum;
+      // weights of features t0 .. t0 + TH - 1, then their biases
+      const int slot = i < TH * B ? t0 * B + i : T * B + t0 + (i - TH * B);
+      a.partial[((int64_t)blockIdx.x * a.H + hh) * P + slot] = sum;
     }
     __syncthreads();
   }
