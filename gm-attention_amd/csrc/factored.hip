@@ -30,6 +30,8 @@
 namespace gm {
 namespace {
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 struct Block {
   int16_t kind, zoff, bm, ang, tr, power, ooff, take_real;
 };
@@ -499,7 +501,6 @@ __global__ __launch_bounds__(64) void factored_backward_kernel(FactArgs<T> a) {
 // its blocks in descriptor order (host-built lists), so results do not
 // depend on scheduling.
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMT = 16;  // edges per MFMA tile
 
