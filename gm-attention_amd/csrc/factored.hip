@@ -369,21 +369,43 @@ __global__ __launch_bounds__(256) void aggregate_heads_kernel(AggHeadsArgs a) {
 }
 
 // dst_t[h, g] = src[perm[g], h] (a row gather and a transpose), and its
-// inverse dst[perm[g], h] = src_t[h, g]: one thread per row g.
+// inverse dst[perm[g], h] = src_t[h, g]: one thread per row g, whole rows
+// moved as 16-byte pieces where the width allows (W4 = width / 4 pieces).
+template <int W4>
 __global__ __launch_bounds__(256) void gather_transpose_kernel(const float* src, const int64_t* perm, int64_t n,
                                                                int width, float* dst_t) {
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= n) return;
   const float* row = src + perm[g] * width;
-  for (int h = 0; h < width; ++h) dst_t[h * n + g] = row[h];
+  if constexpr (W4 > 0) {
+#pragma unroll
+    for (int u = 0; u < W4; ++u) {
+      const floatx4 v = *reinterpret_cast<const floatx4*>(row + 4 * u);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dst_t[(4 * u + k) * n + g] = v[k];
+    }
+  } else {
+    for (int h = 0; h < width; ++h) dst_t[h * n + g] = row[h];
+  }
 }
 
+template <int W4>
 __global__ __launch_bounds__(256) void scatter_transpose_kernel(const float* src_t, const int64_t* perm, int64_t n,
                                                                 int width, float* dst) {
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= n) return;
   float* row = dst + perm[g] * width;
-  for (int h = 0; h < width; ++h) row[h] = src_t[h * n + g];
+  if constexpr (W4 > 0) {
+#pragma unroll
+    for (int u = 0; u < W4; ++u) {
+      floatx4 v;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = src_t[(4 * u + k) * n + g];
+      *reinterpret_cast<floatx4*>(row + 4 * u) = v;
+    }
+  } else {
+    for (int h = 0; h < width; ++h) row[h] = src_t[h * n + g];
+  }
 }
 
 // ----------------------------------------------------------------- backward
@@ -2431,8 +2453,17 @@ extern "C" int gm_gather_transpose_f32(const float* src, const int64_t* perm, in
   if (n == 0) return GM_OK;
   GM_REQUIRE(src && perm && dst_t, "src, perm and dst_t must be device pointers");
   GM_REQUIRE(n < (int64_t(1) << 31) * 256, "too many rows for one launch");
-  hipLaunchKernelGGL(gm::gather_transpose_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     src, perm, n, (int)width, dst_t);
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  const bool vec = gm::aligned(src, 16);
+  if (vec && width == 8)
+    hipLaunchKernelGGL(gm::gather_transpose_kernel<2>, grid, block, 0, (hipStream_t)stream, src, perm, n, (int)width,
+                       dst_t);
+  else if (vec && width == 4)
+    hipLaunchKernelGGL(gm::gather_transpose_kernel<1>, grid, block, 0, (hipStream_t)stream, src, perm, n, (int)width,
+                       dst_t);
+  else
+    hipLaunchKernelGGL(gm::gather_transpose_kernel<0>, grid, block, 0, (hipStream_t)stream, src, perm, n, (int)width,
+                       dst_t);
   return gm::check_launch("gather_transpose");
 }
 
@@ -2442,7 +2473,16 @@ extern "C" int gm_scatter_transpose_f32(const float* src_t, const int64_t* perm,
   if (n == 0) return GM_OK;
   GM_REQUIRE(src_t && perm && dst, "src_t, perm and dst must be device pointers");
   GM_REQUIRE(n < (int64_t(1) << 31) * 256, "too many rows for one launch");
-  hipLaunchKernelGGL(gm::scatter_transpose_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, src_t, perm, n, (int)width, dst);
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  const bool vec = gm::aligned(dst, 16);
+  if (vec && width == 8)
+    hipLaunchKernelGGL(gm::scatter_transpose_kernel<2>, grid, block, 0, (hipStream_t)stream, src_t, perm, n,
+                       (int)width, dst);
+  else if (vec && width == 4)
+    hipLaunchKernelGGL(gm::scatter_transpose_kernel<1>, grid, block, 0, (hipStream_t)stream, src_t, perm, n,
+                       (int)width, dst);
+  else
+    hipLaunchKernelGGL(gm::scatter_transpose_kernel<0>, grid, block, 0, (hipStream_t)stream, src_t, perm, n,
+                       (int)width, dst);
   return gm::check_launch("scatter_transpose");
 }

@@ -35,7 +35,7 @@ def test_aggregate_heads_matches_a_csr_sum(H, d_out, cuda):
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5 * float(want.abs().max()))
 
 
-@pytest.mark.parametrize("width", [1, 8, 13])
+@pytest.mark.parametrize("width", [1, 4, 8, 13])
 def test_gather_and_scatter_transposes_are_exact(width, cuda):
     g = torch.Generator().manual_seed(width)
     n = 1000
