@@ -206,7 +206,21 @@ def main() -> None:
     ap.add_argument("--workload", choices=("attention", "softmax"), default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-edges", type=int, default=200_000)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB between two device buffers three times (the reference reading for the "
+                         "HBM traffic counters) and exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 3}))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: every run here has one MI355X; "
                                    "run with --gpus 1 (the multi-GPU sharding is a design note, not built)"}))
