@@ -1275,13 +1275,15 @@ __device__ __forceinline__ void stage_z_slots(const FactArgs<float>& a, int64_t 
   wave_sync();
   for (int r = 0; r < a.n_seg; ++r) {
     const ZSeg<float>& g = a.seg[r];
-    const float* base = g.z + j * g.node_stride;
-    const int64_t ts = g.t_stride;
+    // the node's 17 mix rows of this run through one buffer: row t at byte t * ts * 4 (a scalar offset)
+    const int ts = g.t_stride;
+    const auto zr = span(g.z + j * g.node_stride, ((int64_t)16 * ts + g.width) * 4);
     for (int c = lane; c < g.width; c += kWave) {
       const int sc = colslot[g.c0 + c];
       float v[17];
 #pragma unroll
-      for (int t = 0; t < 17; ++t) v[t] = base[t * ts + c];
+      for (int t = 0; t < 17; ++t)
+        v[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(zr, c * 4, t * ts * 4, 0));
 #pragma unroll
       for (int t = 0; t < 17; ++t) Zs[t * ZS + sc] = v[t];
     }
@@ -1295,15 +1297,16 @@ __device__ __forceinline__ void flush_dz_slots(const FactArgs<float>& a, int64_t
                                                const uint8_t* colslot, int lane) {
   for (int r = 0; r < a.n_seg; ++r) {
     const ZSeg<float>& g = a.seg[r];
-    float* base = g.dz + j * g.node_stride;
-    const int64_t ts = g.t_stride;
+    const int ts = g.t_stride;
+    const auto dzr = span(g.dz + j * g.node_stride, ((int64_t)16 * ts + g.width) * 4);
     for (int c = lane; c < g.width; c += kWave) {
       const int sc = colslot[g.c0 + c];
       float v[17];
 #pragma unroll
       for (int t = 0; t < 17; ++t) v[t] = Zs[t * ZS + sc];
 #pragma unroll
-      for (int t = 0; t < 17; ++t) base[t * ts + c] = v[t];
+      for (int t = 0; t < 17; ++t)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[t]), dzr, c * 4, t * ts * 4, 0);
     }
   }
 }
@@ -1612,16 +1615,34 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
   float dwp = 0.f;  // this lane's share of dweights(edge m)
   if constexpr (P::kStatic) {
     const Powers<P> pw = powers<P>(cur.ph.ph);
+    // the edge's weighted gradient values w G, once per output group
+    float wgr[2 * NT], wgi[2 * NT];
+#pragma unroll
+    for (int s = 0; s < 2 * NT; ++s) {
+      const uint32_t w = P::word(s);
+      if ((w & kSlotActive) && group_start<P>(s) == s) {
+        dwp += outs.gr[s] * outs.rr[s] + outs.gi[s] * outs.ri[s];
+        wgr[s] = cur.w * outs.gr[s];
+        wgi[s] = cur.w * outs.gi[s];
+      }
+    }
 #pragma unroll
     for (int s = 0; s < 2 * NT; ++s) {
       const uint32_t w = P::word(s);
       const int b = group_start<P>(s);
-      if ((w & kSlotActive) && b == s) dwp += outs.gr[s] * outs.rr[s] + outs.gi[s] * outs.ri[s];
-      float fr = 1.f, fi = 0.f;
-      if ((w & kSlotActive) && !(w & kSlotReal)) static_factor<P>(pw, s, fr, fi);
-      const float gr = (w & kSlotActive) ? outs.gr[b] : 0.f, gim = (w & kSlotActive) ? outs.gi[b] : 0.f;
-      wv[s >> 1][2 * (s & 1)] = cur.w * (fr * gr + fi * gim);
-      wv[s >> 1][2 * (s & 1) + 1] = cur.w * (fr * gim - fi * gr);
+      if (!(w & kSlotActive)) {
+        wv[s >> 1][2 * (s & 1)] = 0.f;
+        wv[s >> 1][2 * (s & 1) + 1] = 0.f;
+      } else if (w & kSlotReal) {
+        wv[s >> 1][2 * (s & 1)] = wgr[b];
+        wv[s >> 1][2 * (s & 1) + 1] = 0.f;
+      } else {
+        float fr, fi;
+        static_factor<P>(pw, s, fr, fi);
+        const float gr = wgr[b], gim = (w & kSlotScalar) ? 0.f : wgi[b];
+        wv[s >> 1][2 * (s & 1)] = fr * gr + fi * gim;
+        wv[s >> 1][2 * (s & 1) + 1] = fr * gim - fi * gr;
+      }
     }
   } else {
     // the targets' gradient rows through LDS (zero for absent edges and past d_out)
