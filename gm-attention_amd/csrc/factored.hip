@@ -1700,7 +1700,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
 }
 
 template <int NT, class P>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? 2 : 1))) void factored_backward_lanes(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? 3 : 1))) void factored_backward_lanes(
     FactArgs<float> a) {
   constexpr int ZS = 16 * NT + 4;
   constexpr int kZWords = 17 * ZS, kWWords = 16 * NT * kWtStride;
