@@ -65,6 +65,19 @@ __device__ __forceinline__ T chunk_dot(const T* q4, const Quad<T>& k, int n, con
   return acc;
 }
 
+// The edges of one lane go in steps of U: every index, key row piece and
+// transport pair of the step is loaded before any of them is used, so U
+// gathers are in flight at once.
+constexpr int kSmStep = 2;
+
+template <typename T>
+__device__ __forceinline__ T chunk_dot_pair(const T* q4, const Quad<T>& k, int n, T c, T s) {
+  if (n == 0) return q4[0] * k.v[0] + q4[1] * k.v[1] + q4[2] * k.v[2] + q4[3] * k.v[3];
+  T acc = q4[0] * (c * k.v[0] - s * k.v[1]) + q4[1] * (c * k.v[1] + s * k.v[0]);
+  acc += q4[2] * (c * k.v[2] - s * k.v[3]) + q4[3] * (c * k.v[3] + s * k.v[2]);
+  return acc;
+}
+
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
@@ -85,17 +98,40 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   }
 
   T m = neg_inf<T>(), l = T(0);
-  for (int64_t e = e0 + s; e < e1; e += S) {
-    const int64_t j = a.source[e];
-    const T* kj = a.k + j * a.D;
-    const T* tr = a.transport + e * a.orders * 2;
-    T acc = T(0);
+  for (int64_t e = e0 + s; e < e1; e += kSmStep * S) {
+    int64_t eu[kSmStep], ju[kSmStep];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) acc += chunk_dot(&q[4 * c], ld4(kj + a.C.base[c] + h * a.C.stride[c]), a.C.order[c], tr);
-    T lw = a.scale * acc + a.bias[e];
-    if (!a.inside[e]) lw = neg_inf<T>();  // outside the window: excluded from the max and the sum
-    a.alpha[e * H + h] = lw;
-    online_add(m, l, lw);
+    for (int u = 0; u < kSmStep; ++u) {
+      eu[u] = e + u * S < e1 ? e + u * S : e;  // a step past the row's end repeats its first edge (not stored)
+      ju[u] = a.source[eu[u]];
+    }
+    Quad<T> kv[kSmStep][NCH];
+    T tc[kSmStep][NCH], tsn[kSmStep][NCH], bias[kSmStep];
+    uint8_t in[kSmStep];
+#pragma unroll
+    for (int u = 0; u < kSmStep; ++u) {
+      const T* kj = a.k + ju[u] * a.D;
+      const T* tr = a.transport + eu[u] * a.orders * 2;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        kv[u][c] = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
+        tc[u][c] = tr[2 * a.C.order[c]];
+        tsn[u][c] = tr[2 * a.C.order[c] + 1];
+      }
+      bias[u] = a.bias[eu[u]];
+      in[u] = a.inside[eu[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < kSmStep; ++u) {
+      if (e + u * S >= e1) break;
+      T acc = T(0);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) acc += chunk_dot_pair(&q[4 * c], kv[u][c], a.C.order[c], tc[u][c], tsn[u][c]);
+      T lw = a.scale * acc + bias[u];
+      if (!in[u]) lw = neg_inf<T>();  // outside the window: excluded from the max and the sum
+      a.alpha[eu[u] * H + h] = lw;
+      online_add(m, l, lw);
+    }
   }
   for (int off = H; off < kWave; off <<= 1) {
     const T mo = __shfl_xor(m, off, kWave), lo = __shfl_xor(l, off, kWave);
@@ -124,25 +160,47 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
   T acc[NCH * 4];
 #pragma unroll
   for (int u = 0; u < NCH * 4; ++u) acc[u] = T(0);
-  for (int64_t e = e0 + s; e < e1; e += S) {
-    const T ds = a.scale * a.alpha_in[e * H + h] * (a.dalpha[e * H + h] - total);
-    a.ds[e * H + h] = ds;
-    const int64_t j = a.source[e];
-    const T* kj = a.k + j * a.D;
-    const T* tr = a.transport + e * a.orders * 2;
+  for (int64_t e = e0 + s; e < e1; e += kSmStep * S) {
+    int64_t eu[kSmStep], ju[kSmStep];
+    T al[kSmStep], da[kSmStep];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const Quad<T> k = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
-      const int n = a.C.order[c];
-      if (n == 0) {
+    for (int u = 0; u < kSmStep; ++u) {
+      eu[u] = e + u * S < e1 ? e + u * S : e;
+      ju[u] = a.source[eu[u]];
+      al[u] = a.alpha_in[eu[u] * H + h];
+      da[u] = a.dalpha[eu[u] * H + h];
+    }
+    Quad<T> kv[kSmStep][NCH];
+    T tc[kSmStep][NCH], tsn[kSmStep][NCH];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[4 * c + u] += ds * k.v[u];
-      } else {
-        const T cr = tr[2 * n], ci = tr[2 * n + 1];
-        acc[4 * c + 0] += ds * (cr * k.v[0] - ci * k.v[1]);
-        acc[4 * c + 1] += ds * (cr * k.v[1] + ci * k.v[0]);
-        acc[4 * c + 2] += ds * (cr * k.v[2] - ci * k.v[3]);
-        acc[4 * c + 3] += ds * (cr * k.v[3] + ci * k.v[2]);
+    for (int u = 0; u < kSmStep; ++u) {
+      const T* kj = a.k + ju[u] * a.D;
+      const T* tr = a.transport + eu[u] * a.orders * 2;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        kv[u][c] = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
+        tc[u][c] = tr[2 * a.C.order[c]];
+        tsn[u][c] = tr[2 * a.C.order[c] + 1];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSmStep; ++u) {
+      if (e + u * S >= e1) break;
+      const T ds = a.scale * al[u] * (da[u] - total);
+      a.ds[eu[u] * H + h] = ds;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const Quad<T>& k = kv[u][c];
+        if (a.C.order[c] == 0) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * k.v[v];
+        } else {
+          const T cr = tc[u][c], ci = tsn[u][c];
+          acc[4 * c + 0] += ds * (cr * k.v[0] - ci * k.v[1]);
+          acc[4 * c + 1] += ds * (cr * k.v[1] + ci * k.v[0]);
+          acc[4 * c + 2] += ds * (cr * k.v[2] - ci * k.v[3]);
+          acc[4 * c + 3] += ds * (cr * k.v[3] + ci * k.v[2]);
+        }
       }
     }
   }
@@ -168,26 +226,47 @@ __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a)
   T acc[NCH * 4];
 #pragma unroll
   for (int u = 0; u < NCH * 4; ++u) acc[u] = T(0);
-  for (int64_t g = g0 + s; g < g1; g += S) {
-    const int64_t e = a.src_order[g];
-    const int64_t t = a.target[e];
-    const T ds = a.ds[e * H + h];
-    const T* qt = a.q + t * a.D;
-    const T* tr = a.transport + e * a.orders * 2;
+  for (int64_t g = g0 + s; g < g1; g += kSmStep * S) {
+    int64_t eu[kSmStep], tu[kSmStep];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const Quad<T> qq = ld4(qt + a.C.base[c] + h * a.C.stride[c]);
-      const int n = a.C.order[c];
-      if (n == 0) {
+    for (int u = 0; u < kSmStep; ++u) eu[u] = a.src_order[g + u * S < g1 ? g + u * S : g];
+    T dsu[kSmStep];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[4 * c + u] += ds * qq.v[u];
-      } else {
-        const T cr = tr[2 * n], ci = tr[2 * n + 1];
-        // conj(tau) q = (c q0 + s q1, c q1 - s q0)
-        acc[4 * c + 0] += ds * (cr * qq.v[0] + ci * qq.v[1]);
-        acc[4 * c + 1] += ds * (cr * qq.v[1] - ci * qq.v[0]);
-        acc[4 * c + 2] += ds * (cr * qq.v[2] + ci * qq.v[3]);
-        acc[4 * c + 3] += ds * (cr * qq.v[3] - ci * qq.v[2]);
+    for (int u = 0; u < kSmStep; ++u) {
+      tu[u] = a.target[eu[u]];
+      dsu[u] = a.ds[eu[u] * H + h];
+    }
+    Quad<T> qv[kSmStep][NCH];
+    T tc[kSmStep][NCH], tsn[kSmStep][NCH];
+#pragma unroll
+    for (int u = 0; u < kSmStep; ++u) {
+      const T* qt = a.q + tu[u] * a.D;
+      const T* tr = a.transport + eu[u] * a.orders * 2;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        qv[u][c] = ld4(qt + a.C.base[c] + h * a.C.stride[c]);
+        tc[u][c] = tr[2 * a.C.order[c]];
+        tsn[u][c] = tr[2 * a.C.order[c] + 1];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSmStep; ++u) {
+      if (g + u * S >= g1) break;
+      const T ds = dsu[u];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const Quad<T>& qq = qv[u][c];
+        if (a.C.order[c] == 0) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * qq.v[v];
+        } else {
+          const T cr = tc[u][c], ci = tsn[u][c];
+          // conj(tau) q = (c q0 + s q1, c q1 - s q0)
+          acc[4 * c + 0] += ds * (cr * qq.v[0] + ci * qq.v[1]);
+          acc[4 * c + 1] += ds * (cr * qq.v[1] - ci * qq.v[0]);
+          acc[4 * c + 2] += ds * (cr * qq.v[2] + ci * qq.v[3]);
+          acc[4 * c + 3] += ds * (cr * qq.v[3] - ci * qq.v[2]);
+        }
       }
     }
   }
