@@ -21,6 +21,46 @@ from gm_attention_amd.representations import so2
 from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
 
 
+class RowsMatmul(torch.autograd.Function):
+    """``x @ w`` for many rows and few columns (``x (M, a)``, ``w (a, b)``):
+    the weight gradient ``x^T g`` sums blocks of rows through one batched
+    product instead of a single long reduction, which the GEMM libraries
+    run on a handful of workgroups.  The sum over blocks is in a fixed order."""
+
+    BLOCK = 8192
+
+    @staticmethod
+    def forward(ctx, x: Tensor, w: Tensor) -> Tensor:
+        ctx.save_for_backward(x, w)
+        return x @ w
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        x, w = ctx.saved_tensors
+        dx = g @ w.t() if ctx.needs_input_grad[0] else None
+        dw = blocked_gram(x, g, RowsMatmul.BLOCK) if ctx.needs_input_grad[1] else None
+        return dx, dw
+
+
+def blocked_gram(x: Tensor, g: Tensor, block: int) -> Tensor:
+    """``x^T g`` over the rows, summed as per-block partial products."""
+    rows = x.shape[0]
+    nb = rows // block
+    if nb < 2:
+        return x.t() @ g
+    head = nb * block
+    xs = x[:head].reshape(nb, block, x.shape[1]).transpose(1, 2)
+    gs = g[:head].reshape(nb, block, g.shape[1]).contiguous()
+    out = torch.bmm(xs, gs).sum(0)
+    if head < rows:
+        out = out + x[head:].t() @ g[head:]
+    return out
+
+
+def rows_matmul(x: Tensor, w: Tensor) -> Tensor:
+    return RowsMatmul.apply(x, w) if x.dim() == 2 else x @ w
+
+
 def complex_as_real(weight: Tensor) -> Tensor:
     """``(b, a, 2)`` complex weights as the real ``(2a, 2b)`` right factor acting
     on interleaved ``(a, 2)`` pairs: ``out = x_flat @ M`` with ``x_flat`` ``(..., 2a)``."""
@@ -81,9 +121,9 @@ def apply_linear(field_type_out: SO2FieldType, common: tuple[int, ...], weights:
             continue
         w = weights[str(f)]
         if f == 0:
-            out = x[0] @ w.T
+            out = rows_matmul(x[0].reshape(-1, x[0].shape[-1]), w.T).reshape(*batch, b)
             outputs[0] = out + bias if bias is not None else out
         else:
-            flat = x[f].reshape(*batch, -1) @ complex_as_real(w).to(x.dtype)
+            flat = rows_matmul(x[f].reshape(-1, 2 * x[f].shape[-2]), complex_as_real(w).to(x.dtype))
             outputs[f] = flat.reshape(*batch, b, 2)
     return SO2FeatureField(field_type_out, outputs)
