@@ -360,19 +360,17 @@ def heads_plan(kernel: Any) -> HeadsPlan:
     return result
 
 
-def heads_mixing(kernels: list[Any], hp: HeadsPlan) -> list[Tensor]:
-    """Per input frequency n, ``M_n`` of ``(reals of x_n, H * K * C_n)``: columns
-    ``(head, t, [complex pairs in packed order | the real block's columns])``,
-    so ``X_n M_n`` is every head's ``Z_t`` for the blocks reading x_n."""
+def _heads_mixing_from(kernels: list[Any], hp: HeadsPlan, params: list[list[Tensor | None]]) -> list[Tensor]:
+    """``heads_mixing`` from stand-in readout parameters (one list per head)."""
     from gm_attention_amd.nn.node_products import mixing_matrix
 
     mats = []
     for n, blocks, _cw, _rw in hp.groups:
         per_head = []
-        for k in kernels:
+        for k, pk in zip(kernels, params, strict=True):
             pieces = []
             for b in blocks:
-                w = k._block_weights(b.block)  # (b_m, a_n, K)
+                w = k._block_weights(b.block, pk)  # (b_m, a_n, K)
                 if b.kind == 0:
                     m = mixing_matrix(w, "real")  # (a_0, K * b_0)
                     pieces.append(m.reshape(m.shape[0], w.shape[-1], -1))
@@ -385,6 +383,53 @@ def heads_mixing(kernels: list[Any], hp: HeadsPlan) -> list[Tensor]:
         stacked = torch.stack(per_head, dim=1)  # (w_n, H, K, C_n)
         mats.append(stacked.reshape(stacked.shape[0], -1))
     return mats
+
+
+_MIXING_MAPS: OrderedDict = OrderedDict()
+
+
+def _mixing_maps(kernels: list[Any], hp: HeadsPlan) -> list[tuple[Tensor, Tensor]]:
+    """Per input frequency, (index, sign) with ``M_n = sign * flat[index]``,
+    ``flat`` the heads' readout parameters concatenated (``readout_parameters``
+    order, head by head): found once by running the construction on the
+    parameters' positions (+1) as float64 values, which it only moves and
+    negates."""
+    shapes = tuple(tuple(None if p is None else tuple(p.shape) for p in k.readout_parameters()) for k in kernels)
+    key = (tuple(id(k) for k in kernels), shapes)
+    hit = _MIXING_MAPS.get(key)
+    if hit is not None:
+        return hit
+    device = kernels[0].complex_head.weight.device
+    offset, ids = 1, []
+    for k in kernels:
+        per = []
+        for p in k.readout_parameters():
+            if p is None:
+                per.append(None)
+                continue
+            per.append(torch.arange(offset, offset + p.numel(), dtype=torch.float64).reshape(p.shape))
+            offset += p.numel()
+        ids.append(per)
+    maps = []
+    for m in _heads_mixing_from(kernels, hp, ids):
+        index = (m.abs().round().long() - 1).clamp_min(0)
+        maps.append((index.to(device), torch.sign(m).to(device)))
+    _MIXING_MAPS[key] = maps
+    while len(_MIXING_MAPS) > 16:
+        _MIXING_MAPS.popitem(last=False)
+    return maps
+
+
+def heads_mixing(kernels: list[Any], hp: HeadsPlan) -> list[Tensor]:
+    """Per input frequency n, ``M_n`` of ``(reals of x_n, H * K * C_n)``: columns
+    ``(head, t, [complex pairs in packed order | the real block's columns])``,
+    so ``X_n M_n`` is every head's ``Z_t`` for the blocks reading x_n.  Every
+    entry is one readout parameter, possibly negated, or zero: the matrices
+    are one gather from the heads' concatenated parameters (a handful of
+    kernels, differentiable) rather than a per-head, per-block build."""
+    maps = _mixing_maps(kernels, hp)
+    flat = torch.cat([p.reshape(-1) for k in kernels for p in k.readout_parameters() if p is not None])
+    return [flat[index] * sign.to(flat.dtype) for index, sign in maps]
 
 
 def node_vectors(x: SO2FeatureField, hp: HeadsPlan) -> list[Tensor]:

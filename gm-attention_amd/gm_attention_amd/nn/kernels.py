@@ -116,22 +116,29 @@ class SO2SteerableKernel(nn.Module):
         """Every coefficient block, the real ``(0, 0)`` block first (kernels.py:496-504)."""
         return ([(0, 0, "real")] if self.real_head is not None else []) + list(self._coefficient_order)
 
-    def _block_weights(self, block: tuple[int, int, str]) -> Tensor:
+    def readout_parameters(self) -> list[Tensor | None]:
+        """The readout heads' parameters in a fixed order: the real head's
+        weight and bias, then the complex head's (a bias may be None)."""
+        real = self.real_head
+        return [real.weight if real is not None else None, real.bias if real is not None else None,
+                self.complex_head.weight, self.complex_head.bias]
+
+    def _block_weights(self, block: tuple[int, int, str], params: list[Tensor | None] | None = None) -> Tensor:
         """``(W_0 = bias, W_1..W_T)`` of one block as ``(b_m, a_n, T + 1)``
-        (kernels.py:506-536): complex for the phase-carrying blocks."""
+        (kernels.py:506-536): complex for the phase-carrying blocks.  ``params``
+        stands in for the readout parameters (``readout_parameters`` order)."""
         n, m, role = block
+        real_w, real_b, cw, cb = self.readout_parameters() if params is None else params
         a_n, b_m = self.field_type_in.multiplicity(n), self.field_type_out.multiplicity(m)
         if role == "real":
-            head = self.real_head
-            columns = head.weight.reshape(b_m, a_n, -1)
-            bias = head.bias.reshape(b_m, a_n) if head.bias is not None else columns.new_zeros(b_m, a_n)
+            columns = real_w.reshape(b_m, a_n, -1)
+            bias = real_b.reshape(b_m, a_n) if real_b is not None else columns.new_zeros(b_m, a_n)
             return torch.cat([bias.unsqueeze(-1), columns], dim=-1)
-        head = self.complex_head
         rows = self._pair_ranges[block]
-        weight = head.weight[rows]
+        weight = cw[rows]
         columns = so2.as_complex(weight.reshape(b_m, a_n, 2, -1).permute(0, 1, 3, 2).contiguous())
-        if head.bias is not None:
-            bias = so2.as_complex(head.bias[rows].reshape(b_m, a_n, 2).contiguous())
+        if cb is not None:
+            bias = so2.as_complex(cb[rows].reshape(b_m, a_n, 2).contiguous())
         else:
             bias = columns.new_zeros(b_m, a_n)
         return torch.cat([bias.unsqueeze(-1), columns], dim=-1)
