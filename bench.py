@@ -11,7 +11,10 @@ and the output projection.  Inputs and the upstream gradient are N(0, 1),
 resident in HBM before the timed region.
 
 ``--workload softmax`` times the scores-and-softmax op alone (forward +
-backward) on the same shape.
+backward) on the same shape.  ``--workload conv`` times the depthwise steerable
+convolution layer (``SO2Convolution(depthwise=True, n_radial_basis=4)``,
+forward + backward with every parameter gradient) on the same grid, batch
+and field: the C3 configuration.
 
 Prints one JSON line.  Each fused op is timed live with HIP events on the
 stream it launches on; the roofline entry is the op with the largest share of
@@ -56,6 +59,21 @@ def softmax_cost(E: int, N: int, D: int, H: int) -> dict[str, tuple[float, float
     return {
         "softmax_forward": (E * (8 + 24 + 4 + 1 + 4 * H) + N * (8 * D + 8), E * 2.0 * D),
         "softmax_backward": (E * (8 + 24 + 8 * H) + N * (16 * D + 8), E * 4.0 * D),
+    }
+
+
+def conv_cost(E: int, N: int, D: int, A0: int, W: int) -> dict[str, tuple[float, float]]:
+    """(bytes, flops) of one launch of the depthwise walk at the reference's
+    boundary: per edge the source index, the coefficient rows (A0 + W floats),
+    the transport and angular tables (48 B) and rho and the weight; per node
+    the value row in and the output row out.  The backward also reads the
+    transposed CSR (source order, target) and writes the coefficient
+    gradients; per node it reads the value and upstream rows and writes dv."""
+    return {
+        "conv_forward": (E * (8 + 4 * A0 + 4 * W + 48 + 8) + N * (8 * D + 8), E * 12.0 * D),
+        "conv_backward": (E * (16 + 8 * (A0 + W) + 48 + 8) + N * (12 * D + 16), E * 24.0 * D),
+        "conv_radial_forward": (E * (8 + 48 + 8) + N * (8 * D + 8), E * (2.0 * 17 * (A0 + W) + 12 * D)),
+        "conv_radial_backward": (E * (16 + 48 + 8) + N * (12 * D + 16), E * (6.0 * 17 * (A0 + W) + 24 * D)),
     }
 
 
@@ -198,12 +216,56 @@ def cpu_baseline_attention(edges, cutoff, mhsa_gpu, budget_edges: int):
     return dict(per_edge=per_edge, per_sample_nodes=per_sample_nodes, points=points, threads=threads, cpu_s=t1 + t2)
 
 
+def cpu_baseline_conv(edges, cutoff, conv_gpu, budget_edges: int):
+    """The eager restatement (oracle.modules.conv_forward) of the depthwise
+    layer's forward + backward in float32 on the host's cores (at most 16
+    threads) over the targets of a mixed sample (the first, pole, targets
+    and whole equator rows) of one 256x512 sample; the layer has no node-side
+    work beyond the gather, so the time per edge is extrapolated to the step."""
+    import torch
+
+    from gm_attention_amd.nn.convolution import SO2Convolution
+    from gm_attention_amd.representations.field_type import SO2FeatureField
+    from oracle import modules
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    row_ptr = edges.row_ptr
+    n = row_ptr.shape[0] - 1
+    conv = SO2Convolution(conv_gpu.field_type_in, conv_gpu.field_type_out, cutoff=cutoff, depthwise=True,
+                          n_radial_basis=conv_gpu.kernel.radial_basis.n_basis, dtype=torch.float32)
+    conv.load_state_dict({k: v.detach().cpu() for k, v in conv_gpu.state_dict().items()})
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(n, conv.field_type_in.dimension, generator=gen).requires_grad_(True)
+    g = torch.randn(n, conv.field_type_in.dimension, generator=gen)
+    pole_last = max(1, int(torch.searchsorted(row_ptr, torch.tensor(budget_edges // 2)).item()))
+    eq_first = (NLAT // 2) * NLON
+    eq_last = eq_first + NLON
+    while int(row_ptr[eq_last] - row_ptr[eq_first]) < budget_edges // 2 and eq_last + NLON <= n:
+        eq_last += NLON
+    sel = torch.cat([torch.arange(int(row_ptr[a]), int(row_ptr[b])) for a, b in ((0, pole_last), (eq_first, eq_last))])
+    sub = edges.select(sel, n_nodes=n).to(None, torch.float32)
+
+    def step():
+        xs = SO2FeatureField.from_flat(conv.field_type_in, x).coefficients
+        out = modules.flat(modules.conv_forward(conv, xs, sub))
+        (out * g).sum().backward()
+        x.grad = None
+        conv.zero_grad(set_to_none=True)
+
+    step()
+    t0 = time.perf_counter()
+    step()
+    dt = time.perf_counter() - t0
+    return dict(per_edge=dt / sub.n_edges, edges=sub.n_edges, seconds=dt, threads=threads)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=("attention", "softmax"), default="attention")
+    ap.add_argument("--workload", choices=("attention", "softmax", "conv"), default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-edges", type=int, default=200_000)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -249,6 +311,11 @@ def main() -> None:
     timer.wrap(_native, "aggregate_heads", "factored_aggregate")
     timer.wrap(_native, "radial_trunk_forward", "radial_trunk_forward")
     timer.wrap(_native, "radial_trunk_backward", "radial_trunk_backward")
+    timer.wrap(att, "conv_forward", "conv_forward")
+    timer.wrap(att, "conv_backward", "conv_backward")
+    if hasattr(_native, "conv_radial_forward"):
+        timer.wrap(_native, "conv_radial_forward", "conv_radial_forward")
+        timer.wrap(_native, "conv_radial_backward", "conv_radial_backward")
 
     edges_cpu, edges, cutoff = build_edges(device)
     N = edges.row_ptr.shape[0] - 1
@@ -262,6 +329,7 @@ def main() -> None:
     upstream = torch.randn(N, D, device=device, generator=gen)
     g = fused_attention.geometry(edges, cutoff, "hard", torch.float32)
     log(f"problem: N={N} E={E} D={D} H={HEADS} max_degree={g.max_degree}")
+    module = mhsa  # the module whose parameter gradients the loop clears
 
     if args.workload == "attention":
         def step():
@@ -270,6 +338,21 @@ def main() -> None:
             torch.autograd.backward(y, upstream)
         workload = ("SO2MHSA(batched) fwd+bwd: stacked Q/K projections, fused scores+softmax, 8 heads of node "
                     "products + radial trunk + fused factored value aggregation, output projection; input and "
+                    "every parameter gradient")
+    elif args.workload == "conv":
+        from gm_attention_amd.nn.convolution import SO2Convolution
+
+        torch.manual_seed(0)
+        conv = SO2Convolution(field, field, cutoff=cutoff, window="hard", depthwise=True, n_radial_basis=4,
+                              dtype=torch.float32, device=device)
+        module = conv
+
+        def step():
+            x = SO2FeatureField.from_flat(field, x_flat)
+            y = conv(x, edges).to_flat()
+            torch.autograd.backward(y, upstream)
+        workload = ("SO2Convolution(depthwise=True, n_radial_basis=4) fwd+bwd: radial trunk and readout heads, "
+                    "fused depthwise walk (transport, coefficient products, weighting, segment sum); input and "
                     "every parameter gradient")
     else:
         p = fused_attention.plan(mhsa)
@@ -288,14 +371,14 @@ def main() -> None:
 
     for _ in range(args.warmup):
         step()
-        mhsa.zero_grad(set_to_none=True)
+        module.zero_grad(set_to_none=True)
         x_flat.grad = None
     torch.cuda.synchronize()
     timer.enabled = True
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
-        mhsa.zero_grad(set_to_none=True)
+        module.zero_grad(set_to_none=True)
         x_flat.grad = None
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -312,10 +395,12 @@ def main() -> None:
     # the radial trunk for all heads: rho in, h (H, E, T) out; 2 T B + ~20 T FLOPs per edge and head
     costs["radial_trunk_forward"] = (E * (4 + HEADS * 4 * (K - 1)), E * HEADS * (2.0 * (K - 1) * 8 + 20 * (K - 1)))
     costs["radial_trunk_backward"] = (E * (4 + HEADS * 4 * (K - 1)), E * HEADS * (4.0 * (K - 1) * 8 + 30 * (K - 1)))
+    a0 = field.multiplicity(0)
+    costs.update(conv_cost(E, N, D, a0, 4 * (D - a0) // 2))
     dominant = max(ops, key=lambda k: ops[k]["ms_per_step"])
     nbytes, flops = costs[dominant]
     avg_s = ops[dominant]["avg_ms"] * 1e-3
-    if dominant.startswith(("softmax", "radial")) or dominant == "factored_aggregate":
+    if dominant.startswith(("softmax", "radial", "conv_forward", "conv_backward")) or dominant == "factored_aggregate":
         roof = {"bound": "hbm", "achieved": nbytes / avg_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     else:
         roof = {"bound": "mfma", "achieved": flops / avg_s / 1e12, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s"}
@@ -342,9 +427,19 @@ def main() -> None:
                                f"{b['per_sample_nodes']:.2f}s per sample's nodes + {b['per_edge'] * 1e6:.1f}us per "
                                f"edge, extrapolated to {BATCH} samples and {E} edges")}
         log(f"cpu baseline: {baseline['value']:.1f} qp/s ({baseline['sample']})")
+    elif not args.no_cpu_baseline and args.workload == "conv":
+        b = cpu_baseline_conv(edges_cpu, cutoff, conv, args.cpu_budget_edges)
+        baseline = {"value": N / (b["per_edge"] * E), "unit": "query-points/s", "cores": b["threads"], "kind": "port",
+                    "sample": (f"oracle eager SO2Convolution(depthwise) fwd+bwd (float32, torch on {b['threads']} "
+                               f"threads) over the edges of one 256x512 sample's first (pole) targets and equator "
+                               f"rows: {b['edges']} edges in {b['seconds']:.2f}s, {b['per_edge'] * 1e6:.2f}us per "
+                               f"edge, extrapolated to {E} edges")}
+        log(f"cpu baseline: {baseline['value']:.1f} qp/s ({baseline['sample']})")
 
     line = {
-        "metric": "attn fwd+bwd query-points/s at 256x512 B=4",
+        "metric": {"attention": "attn fwd+bwd query-points/s at 256x512 B=4",
+                   "softmax": "attn scores+softmax fwd+bwd query-points/s at 256x512 B=4",
+                   "conv": "depthwise conv fwd+bwd query-points/s at 256x512 B=4"}[args.workload],
         "value": N / (ms_per_step * 1e-3),
         "unit": "query-points/s",
         "n_gpus": 1,

@@ -1,0 +1,126 @@
+"""The depthwise (per-copy) steerable kernel whose aggregation runs on the HIP path.
+
+Restates the reference's ``nn/depthwise.py``:
+
+* ``SO2DepthwiseKernel`` (:44-193): one steerable kernel per irrep copy of
+  ``field_type``; per copy ``a`` of frequency ``n`` the message is
+  ``C_a(r) x_a`` at ``n = 0`` and ``A_a(r) z + (r/c)^{2n} B_a(r) e^{2 i n phi}
+  conj(z)`` above it (``z`` the transported copy).  The radial functions are
+  heads over one shared trunk: a real head of ``a_0`` outputs and a complex
+  head of ``sum_n 4 a_n`` outputs laid out per frequency as ``(2, a_n, 2)``
+  = (A | B, copy, re/im) (:106-127, 175-191);
+* ``stacked_coefficients`` (:206-238): every kernel's ``(rc, cc)`` readouts of
+  one radial embedding, stacked on a leading kernel axis.
+
+The per-edge message form (``SO2DepthwiseKernel.forward`` on edge-shaped
+fields, :147-193) is the eager path; here it is the parity oracle and lives
+with the tests.  The layer (``convolution.SO2Convolution``) evaluates the
+kernel through the fused depthwise op.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from typing import cast
+
+import torch
+from torch import Tensor, nn
+
+from gm_attention_amd.discretization.edge_geometry import cutoff_tolerance
+from gm_attention_amd.nn.kernels import SO2SteerableKernel
+from gm_attention_amd.representations.field_type import SO2FieldType
+
+
+class SO2DepthwiseKernel(nn.Module):
+    """One steerable kernel per irrep copy, ``field_type -> field_type`` (:44-145)."""
+
+    def __init__(self, field_type: SO2FieldType, *, cutoff: float, n_radial_basis: int = 8,
+                 radial_hidden_features: Sequence[int] = (16,), radial_basis: str = "gaussian", bias: bool = True,
+                 dtype: torch.dtype | None = None, device: torch.device | str | None = None) -> None:
+        super().__init__()
+        if not isinstance(field_type, SO2FieldType):
+            raise TypeError(f"field_type must be an SO2FieldType, got {type(field_type).__name__}.")
+        self.field_type = field_type
+        self.field_type_in = field_type
+        self.field_type_out = field_type
+        # the radial embedding and trunk of a scalar 1 -> 1 steerable kernel: identical construction
+        template = SO2SteerableKernel(SO2FieldType({0: 1}), SO2FieldType({0: 1}), cutoff=cutoff,
+                                      n_radial_basis=n_radial_basis, radial_hidden_features=radial_hidden_features,
+                                      radial_basis=radial_basis, bias=bias, dtype=dtype, device=device)
+        self.radial_basis = template.radial_basis
+        self.radial_trunk = template.radial_trunk
+        trunk_width = [n_radial_basis, *radial_hidden_features][-1]
+        scalar_width = field_type.multiplicity(0) if 0 in field_type else 0
+        self._complex_frequencies = [f for f in field_type.frequencies if f != 0]
+        self._complex_widths = [4 * field_type.multiplicity(f) for f in self._complex_frequencies]
+        complex_width = sum(self._complex_widths)
+        self.real_head = (nn.Linear(trunk_width, scalar_width, bias=bias, dtype=dtype, device=device)
+                          if scalar_width > 0 else None)
+        self.complex_head = (nn.Linear(trunk_width, complex_width, bias=bias, dtype=dtype, device=device)
+                             if complex_width > 0 else None)
+        self._validated_edge_geometry_ids: set[int] = set()
+
+    @property
+    def cutoff(self) -> float:
+        return float(self.radial_basis.cutoff)
+
+    def validate_edges(self, edges) -> None:
+        """Harmonics tabulated to twice the top frequency; no edge beyond the
+        cutoff (checked once per edge set) (:129-145)."""
+        required = 2 * self.field_type.max_frequency
+        if edges.max_frequency < required:
+            raise ValueError(f"edges tabulates harmonics up to order {edges.max_frequency}, but a depthwise kernel "
+                             f"at frequency {self.field_type.max_frequency} needs order {required}.")
+        if edges.distances.numel() > 0 and id(edges) not in self._validated_edge_geometry_ids:
+            maximum = float(edges.distances.max())
+            if maximum > self.cutoff + cutoff_tolerance(edges.distances.dtype):
+                raise ValueError(f"edges contains a distance ({maximum:.6g}) beyond this kernel's cutoff "
+                                 f"({self.cutoff:.6g}).")
+            self._validated_edge_geometry_ids.add(id(edges))
+
+    def trunk_linears(self) -> list[nn.Linear]:
+        return [m for m in self.radial_trunk if isinstance(m, nn.Linear)]
+
+    def forward(self, x, edges):
+        raise RuntimeError("the per-edge depthwise messages are the eager path (the test oracle); the layer "
+                           "evaluates this kernel through the fused depthwise op (SO2Convolution)")
+
+    def extra_repr(self) -> str:
+        return f"field_type={self.field_type!r}, cutoff={self.cutoff:.6g}"
+
+
+def _stacked(parameters: Sequence[Tensor | None]) -> Tensor | None:
+    if parameters[0] is None:
+        return None
+    return torch.stack([cast(Tensor, p) for p in parameters])
+
+
+def _linear(hidden: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+    """``hidden (K, E, in) -> (K, E, out)`` under stacked ``weight (K, out, in)`` and ``bias (K, out)``."""
+    out = torch.bmm(hidden, weight.transpose(1, 2).contiguous())
+    return out if bias is None else out + bias.unsqueeze(1)
+
+
+def stacked_coefficients(kernels: Sequence[SO2DepthwiseKernel], edges) -> tuple[Tensor | None, Tensor | None]:
+    """Every kernel's ``rc (K, E, a_0)`` and ``cc (K, E, sum 4 a_n)`` on the
+    edges, through one radial embedding and the kernels' stacked trunks
+    (:206-238); ``None`` for a head the type does not have."""
+    first = kernels[0]
+    first.validate_edges(edges)
+    with torch.profiler.record_function("gm::kernel/radial"):
+        embedding = first.radial_basis(edges.distances)
+        hidden = embedding.unsqueeze(0).expand(len(kernels), -1, -1).contiguous()
+        trunks = [k.trunk_linears() for k in kernels]
+        for layer in range(len(trunks[0])):
+            weight = torch.stack([t[layer].weight for t in trunks])
+            bias = _stacked([t[layer].bias for t in trunks])
+            hidden = torch.nn.functional.silu(_linear(hidden, weight, bias))
+
+    def readout(heads: Sequence[nn.Linear | None]) -> Tensor | None:
+        if heads[0] is None:
+            return None
+        weight = torch.stack([cast(nn.Linear, h).weight for h in heads])
+        bias = _stacked([cast(nn.Linear, h).bias for h in heads])
+        return _linear(hidden, weight, bias)
+
+    return readout([k.real_head for k in kernels]), readout([k.complex_head for k in kernels])

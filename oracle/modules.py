@@ -284,3 +284,72 @@ def mhsa_forward(mhsa, x: dict[int, Tensor], edges, tolerance: float | None = No
         outs.append(agg)
     fused = {f: torch.cat([o[f] for o in outs], dim=-1 if f == 0 else -2) for f in fin.frequencies}
     return linear(mhsa.output_projection, fused, fin)
+
+
+# ---------------------------------------------------------------- convolution layers
+
+
+def depthwise_layer_messages(kernel, x: dict[int, Tensor], edges) -> dict[int, Tensor]:
+    """``SO2DepthwiseKernel.forward`` on the gathered source field (reference
+    nn/depthwise.py:147-193): the shared trunk, the real head ``C`` per scalar
+    copy, the complex head per frequency ``n`` as ``(2, a_n, 2)`` = (A | B,
+    copy, re/im); ``m = C x`` at 0, ``A z + (r/c)^{2n} e^{2 i n phi} B conj(z)``
+    above, ``z`` the transported copy; the radial power by repeated products."""
+    ft = kernel.field_type
+    source = edges.source_index
+    E = source.shape[0]
+    hidden = _trunk(kernel, edges.distances)
+    out: dict[int, Tensor] = {}
+    if kernel.real_head is not None:
+        c = hidden @ kernel.real_head.weight.T + (kernel.real_head.bias if kernel.real_head.bias is not None else 0.0)
+        out[0] = c * x[0].index_select(0, source)
+    if kernel.complex_head is not None:
+        cc = hidden @ kernel.complex_head.weight.T
+        if kernel.complex_head.bias is not None:
+            cc = cc + kernel.complex_head.bias
+        rho = edges.distances / kernel.radial_basis.cutoff
+        start = 0
+        for n in ft.frequencies:
+            if n == 0:
+                continue
+            a = ft.multiplicity(n)
+            block = cc[:, start:start + 4 * a].reshape(E, 2, a, 2)
+            start += 4 * a
+            A = torch.view_as_complex(block[:, 0].contiguous())
+            B = torch.view_as_complex(block[:, 1].contiguous())
+            z = edges.transport_phases[:, n].unsqueeze(-1) * torch.view_as_complex(
+                x[n].index_select(0, source).contiguous())
+            scale = torch.ones_like(rho)
+            for _ in range(2 * n):
+                scale = scale * rho
+            w = (scale * edges.angular_phases[:, 2 * n]).unsqueeze(-1)
+            out[n] = torch.view_as_real(A * z + w * B * z.conj())
+    return out
+
+
+def conv_forward(conv, x: dict[int, Tensor], edges, tolerance: float | None = None) -> dict[int, Tensor]:
+    """``SO2Convolution.forward`` eagerly (reference nn/convolution.py:271-355):
+    per-edge messages (the depthwise kernel's, or the general kernel's
+    per-edge readout), each weighted by the window times the quadrature
+    weight, summed per target, divided by the window mass under
+    ``normalize``, plus the self-intertwiner."""
+    if conv.depthwise:
+        msgs = depthwise_layer_messages(conv.kernel, x, edges)
+    else:
+        msgs = readout_messages(conv.kernel, x, edges.source_index, edges.distances, edges.angular_phases,
+                                edges.transport_phases)
+    d = edges.distances
+    tol = tolerance if tolerance is not None else (1e-10 if d.dtype == torch.float64 else 1e-5)
+    win = (d <= conv.cutoff + tol).to(d.dtype) if conv.window == "hard" else torch.relu(1.0 - (d / conv.cutoff) ** 2) ** 2
+    weight = win * edges.tangent_quadrature_weights
+    out = {}
+    for f, m in msgs.items():
+        s = torch.segment_reduce(weight.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum", offsets=edges.row_ptr, axis=0)
+        if conv.normalize:
+            mass = torch.segment_reduce(weight, "sum", offsets=edges.row_ptr, axis=0).clamp_min(conv.eps)
+            s = s / mass.reshape(-1, *([1] * (s.ndim - 1)))
+        out[f] = s
+    if conv.self_linear is not None:
+        pointwise = linear(conv.self_linear, x, conv.field_type_out)
+        out = {f: out[f] + pointwise[f] for f in out}
+    return out

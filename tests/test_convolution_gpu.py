@@ -1,0 +1,123 @@
+"""The convolution layer (SO2Convolution, depthwise and general kernels) on the
+HIP path against the oracle (oracle.modules.conv_forward: the reference's
+eager layer in float64), with the input's and every parameter's gradient;
+chunked evaluation equal to the whole; gauge equivariance under random frame
+rotations.  Tolerances as test_attention_gpu.close."""
+
+import math
+
+import pytest
+import torch
+
+import problems
+from gm_attention_amd.discretization.discretization import SphericalDiscretization
+from gm_attention_amd.discretization.frames import build_tangent_frames, rotate_tangent_frames
+from gm_attention_amd.discretization.grid import build_equiangular_grid
+from gm_attention_amd.nn.convolution import SO2Convolution
+from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
+from oracle import modules
+from test_attention_gpu import close
+
+pytestmark = pytest.mark.gpu
+
+
+def build(field, depthwise, window, normalize, self_interaction, batch, n_basis=4, seed=0, nlat=10, nlon=20):
+    disc = problems.discretization(nlat, nlon)
+    edges = disc.edge_geometry.tile(batch, n_sources=disc.n_nodes) if batch > 1 else disc.edge_geometry
+    torch.manual_seed(seed)
+    ft = SO2FieldType(field)
+    conv = SO2Convolution(ft, ft, cutoff=disc.coverage_radius, window=window, depthwise=depthwise,
+                          normalize=normalize, self_interaction=self_interaction, n_radial_basis=n_basis,
+                          dtype=torch.float64)
+    with torch.no_grad():  # nonzero biases everywhere
+        for p in conv.parameters():
+            p.add_(0.1 * torch.randn_like(p))
+    n = edges.row_ptr.shape[0] - 1
+    return conv, problems.normal((n, ft.dimension), seed + 1), edges
+
+
+def run(module, flat, edges, probe, *, oracle=False, chunk=None, tolerance=None):
+    leaf_flat = flat.clone().requires_grad_(True)
+    x = SO2FeatureField.from_flat(module.field_type_in, leaf_flat)
+    module.zero_grad(set_to_none=True)
+    if oracle:
+        out = modules.flat(modules.conv_forward(module, x.coefficients, edges, tolerance))
+    elif chunk is not None:
+        out = module.forward_chunked(x, edges, chunk_size=chunk).to_flat()
+    else:
+        out = module(x, edges).to_flat()
+    (out * probe.to(out.device, out.dtype)).sum().backward()
+    return out.detach(), leaf_flat.grad, {n: p.grad for n, p in module.named_parameters() if p.grad is not None}
+
+
+CASES = [
+    ({0: 32, 1: 32, 2: 32}, True, "hard", False, "none", 2),
+    ({0: 3, 1: 2}, True, "quartic", True, "linear", 1),
+    ({1: 2, 2: 3}, True, "hard", False, "none", 1),
+    ({0: 70, 1: 30, 2: 20}, True, "quartic", False, "none", 1),
+    ({0: 8, 1: 8, 2: 8}, False, "hard", False, "none", 2),
+    ({0: 4, 1: 3, 2: 2}, False, "quartic", True, "linear", 1),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("case", CASES)
+def test_convolution_matches_the_oracle(case, dtype, cuda):
+    field, depthwise, window, normalize, self_interaction, batch = case
+    print(f"conv {case} {dtype}", flush=True)
+    conv, x, edges = build(field, depthwise, window, normalize, self_interaction, batch)
+    probe = problems.normal(x.shape, 7)
+    if dtype == torch.float32:  # the oracle sees the same rounded parameters, inputs and geometry
+        conv.load_state_dict({k: v.float().double() for k, v in conv.state_dict().items()})
+        x = x.float().double()
+        edges_o = edges.to(None, torch.float32).to(None, torch.float64)
+    else:
+        edges_o = edges
+    want = run(conv, x, edges_o, probe, oracle=True, tolerance=1e-5 if dtype == torch.float32 else None)
+    gpu = SO2Convolution(conv.field_type_in, conv.field_type_out, cutoff=conv.cutoff, window=window,
+                         depthwise=depthwise, normalize=normalize, self_interaction=self_interaction,
+                         n_radial_basis=conv.kernel.radial_basis.n_basis, dtype=dtype, device=cuda)
+    gpu.load_state_dict({k: v.to(dtype) for k, v in conv.state_dict().items()})
+    got = run(gpu, x.to(cuda, dtype), edges.to(cuda, dtype), probe)
+    close(got[0], want[0], dtype, "out")
+    close(got[1], want[1], dtype, "dx")
+    assert set(got[2]) == set(want[2])
+    for n in want[2]:
+        close(got[2][n], want[2][n], dtype, f"d{n}", reduction=True)
+
+
+@pytest.mark.parametrize("depthwise", [True, False])
+def test_chunked_equals_whole(depthwise, cuda):
+    conv, x, edges = build({0: 8, 1: 8, 2: 8}, depthwise, "quartic", True, "none", 2)
+    gpu = conv.to(cuda)
+    gpu.train()
+    e = edges.to(cuda, torch.float64)
+    probe = problems.normal(x.shape, 7)
+    whole = run(gpu, x.to(cuda), e, probe)
+    chunked = run(gpu, x.to(cuda), e, probe, chunk=37)
+    close(chunked[0], whole[0], torch.float64, "out")
+    close(chunked[1], whole[1], torch.float64, "dx")
+    for n in whole[2]:
+        close(chunked[2][n], whole[2][n], torch.float64, f"d{n}")
+
+
+@pytest.mark.parametrize("depthwise", [True, False])
+def test_gauge_equivariance_under_random_frame_rotations(depthwise, cuda):
+    nlat, nlon = 10, 20
+    grid = build_equiangular_grid(nlat, nlon)
+    cutoff = 3.0 * math.pi / (nlat - 1)
+    frames = build_tangent_frames(grid.nodes)
+    theta = torch.rand(grid.n_nodes, dtype=torch.float64, generator=torch.Generator().manual_seed(4)) * 2 * math.pi
+    base = SphericalDiscretization.from_grid(grid, cutoff, frames=frames)
+    turned = SphericalDiscretization.from_grid(grid, cutoff, frames=rotate_tangent_frames(frames, theta))
+    torch.manual_seed(0)
+    field = SO2FieldType({0: 4, 1: 4, 2: 4})
+    conv = SO2Convolution(field, field, cutoff=cutoff, depthwise=depthwise, n_radial_basis=4, dtype=torch.float64,
+                          device=cuda)
+    x = SO2FeatureField.from_flat(field, problems.normal((grid.n_nodes, field.dimension), 1).to(cuda))
+    with torch.no_grad():
+        y = conv(x, base.edge_geometry.to(cuda, torch.float64))
+        y_turned = conv(x.gauge_transform(theta.to(cuda)), turned.edge_geometry.to(cuda, torch.float64))
+    expected = y.gauge_transform(theta.to(cuda))
+    torch.testing.assert_close(y_turned.to_flat(), expected.to_flat(), rtol=1e-9, atol=1e-9)
+    assert float((y.to_flat() - expected.to_flat()).abs().max()) > 1e-3
