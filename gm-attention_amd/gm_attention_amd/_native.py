@@ -6,7 +6,9 @@ argument orders.
 module stands (``nn/fused/attention_cpu.cpp:256-261``): ``softmax_forward``,
 ``softmax_backward``, ``conv_forward``, ``conv_backward``.  ``factored()``
 stands for ``gm_factored`` (``nn/fused/factored_cpu.cpp:223-234``):
-``forward``, ``aggregate``, ``backward``, ``backward_aggregated``.  Tensors are
+``forward``, ``aggregate``, ``backward``, ``backward_aggregated``.  ``pairs()``
+stands for the ``gm_pairs`` modules (``nn/fused/pairs_cpu.cpp:138-148``):
+``forward``, ``backward`` of one pair term.  Tensors are
 checked with the reference's messages (``attention_cpu.cpp:42-64, 149-171``),
 outputs are allocated here through torch's caching allocator, and the raw
 pointers go to ``libgmhip.so`` on the current HIP stream.  There is no CPU
@@ -42,6 +44,8 @@ SIGNATURES: dict[str, list[Any]] = {
     "gm_factored_backward": [_P] * 14 + [_I] * 9 + [_P] * 5,
     "gm_factored_forward_seg": [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P, _P],
     "gm_factored_backward_seg": [_P] * 10 + [_I] + [_P] * 7 + [_I] * 9 + [_P] * 3,
+    "gm_pairs_forward": [_P] * 8 + [_I] * 5 + [_P],
+    "gm_pairs_backward": [_P] * 11 + [_I] * 6 + [_P],
 }
 
 #: fp32-only and host-only entry points (name -> (restype, argtypes)).
@@ -676,3 +680,93 @@ def aggregate_gather(rows_g: Tensor, inv: Tensor, weights: Tensor, row_ptr: Tens
     _call("gm_factored_aggregate_gather_f32", _ptr(rows_g), _ptr(inv), _ptr(weights), _ptr(row_ptr), n_targets,
           rows_g.shape[0], rows_g.shape[1], _ptr(out), _stream(rows_g.device))
     return out
+
+
+# ---------------------------------------------------------------- pair terms of the general kernel
+
+PAIRS_MATRIX_COMPLEX, PAIRS_U_REAL, PAIRS_CONJ_U, PAIRS_OUT_REAL = 1, 2, 4, 8
+PAIRS_MAX_MULT, PAIRS_MAX_TRUNK = 16, 16
+
+
+def _pcheck(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError("gm_pairs: " + message)
+
+
+def _real_view(t: Tensor) -> Tensor:
+    return torch.view_as_real(t) if t.is_complex() else t
+
+
+class PairsExtension:
+    """``gm_pairs``' entry points (reference nn/fused/pairs_cpu.cpp:88-148):
+    one pair term per call, accumulating into caller-allocated outputs.  An
+    empty tensor stands for an absent ``bias``, ``pre``, ``post`` or ``scale``."""
+
+    with_cuda = True
+
+    @staticmethod
+    def _check(hidden: Tensor, weight: Tensor, u: Tensor, out: Tensor, a: int, b: int, flags: int) -> int:
+        trunk = hidden.shape[1]
+        _pcheck(1 <= a <= PAIRS_MAX_MULT and 1 <= b <= PAIRS_MAX_MULT, "block dimensions must be in 1..16")
+        _pcheck(1 <= trunk <= PAIRS_MAX_TRUNK, "trunk width must be in 1..16")
+        _pcheck(hidden.is_contiguous() and weight.is_contiguous() and u.is_contiguous() and out.is_contiguous(),
+                "hidden, weight, u and out must be contiguous")
+        width = (2 if flags & PAIRS_MATRIX_COMPLEX else 1) * a * b
+        _pcheck(weight.dim() == 2 and weight.shape[0] == width and weight.shape[1] == trunk,
+                "weight must be (width, trunk)")
+        _pcheck(u.dim() == 2 and out.dim() == 2 and u.shape[1] == a and out.shape[1] == b,
+                "u must be (n_edges, a) and out (n_edges, b)")
+        _pcheck(u.shape[0] == hidden.shape[0] and out.shape[0] == hidden.shape[0], "n_edges mismatch")
+        _pcheck(bool(flags & PAIRS_U_REAL) == (not u.is_complex()), "u must be real iff U_REAL")
+        _pcheck(bool(flags & PAIRS_OUT_REAL) == (not out.is_complex()), "out must be real iff OUT_REAL")
+        _pcheck(_real_view(u).dtype == hidden.dtype and weight.dtype == hidden.dtype
+                and _real_view(out).dtype == hidden.dtype, "every tensor must share the hidden dtype")
+        if hidden.device.type != "cuda":
+            raise RuntimeError("libgmhip runs on the GPU only: the tensors are on the CPU (this build has no CPU driver)")
+        return trunk
+
+    @staticmethod
+    def _optional(t: Tensor, n: int, complex_: bool, dtype: torch.dtype, what: str) -> int | None:
+        if t is None or t.numel() == 0:
+            return None
+        _pcheck(t.is_contiguous() and t.shape[0] == n and t.is_complex() == complex_
+                and _real_view(t).dtype == dtype, f"{what} must be a contiguous (n_edges,) tensor")
+        return t.data_ptr()
+
+    def forward(self, hidden: Tensor, weight: Tensor, bias: Tensor, u: Tensor, pre: Tensor, post: Tensor,
+                scale: Tensor, out: Tensor, a: int, b: int, flags: int) -> None:
+        trunk = self._check(hidden, weight, u, out, a, b, flags)
+        n = hidden.shape[0]
+        if n == 0:
+            return
+        _call("gm_pairs_forward" + _suffix(hidden.dtype), hidden.data_ptr(), weight.data_ptr(),
+              self._optional(bias, weight.shape[0], False, hidden.dtype, "bias"), u.data_ptr(),
+              self._optional(pre, n, True, hidden.dtype, "pre"), self._optional(post, n, True, hidden.dtype, "post"),
+              self._optional(scale, n, False, hidden.dtype, "scale"), out.data_ptr(), n, int(a), int(b), trunk,
+              int(flags), _stream(hidden.device))
+
+    def backward(self, hidden: Tensor, weight: Tensor, bias: Tensor, u: Tensor, pre: Tensor, post: Tensor,
+                 scale: Tensor, grad_out: Tensor, grad_u: Tensor, grad_hidden: Tensor, grad_k: Tensor, a: int, b: int,
+                 flags: int) -> None:
+        trunk = self._check(hidden, weight, u, grad_out, a, b, flags)
+        n = hidden.shape[0]
+        _pcheck(grad_u.is_contiguous() and grad_hidden.is_contiguous(), "grad_u and grad_hidden must be contiguous")
+        _pcheck(grad_u.shape == u.shape and grad_u.dtype == u.dtype and grad_hidden.shape == hidden.shape
+                and grad_hidden.dtype == hidden.dtype, "grad_u and grad_hidden must match u and hidden")
+        _pcheck(grad_k.dim() == 2 and grad_k.shape[1] == n and grad_k.shape[0] == weight.shape[0]
+                and grad_k.stride(1) == 1 and grad_k.stride(0) >= n and grad_k.dtype == hidden.dtype,
+                "grad_k must be (width, n_edges) with unit column stride")
+        if n == 0:
+            return
+        _call("gm_pairs_backward" + _suffix(hidden.dtype), hidden.data_ptr(), weight.data_ptr(),
+              self._optional(bias, weight.shape[0], False, hidden.dtype, "bias"), u.data_ptr(),
+              self._optional(pre, n, True, hidden.dtype, "pre"), self._optional(post, n, True, hidden.dtype, "post"),
+              self._optional(scale, n, False, hidden.dtype, "scale"), grad_out.data_ptr(), grad_u.data_ptr(),
+              grad_hidden.data_ptr(), grad_k.data_ptr(), grad_k.stride(0), n, int(a), int(b), trunk, int(flags),
+              _stream(hidden.device))
+
+
+@functools.cache
+def pairs() -> PairsExtension:
+    library()  # raises when the library is absent
+    return PairsExtension()

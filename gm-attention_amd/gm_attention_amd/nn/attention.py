@@ -16,8 +16,10 @@ signatures and call structure:
   (``_aggregated_factored``, :801-822).
 
 Every score, softmax and value aggregation runs in the HIP ops
-(``fused_attention.Softmax``, ``fused_factored.FactoredAggregate``); the
-projections are per-frequency dense products.  A layer whose fused op is not
+(``fused_attention.Softmax``, ``fused_factored.FactoredAggregate``; under
+``GM_FACTORED_KERNEL=0`` the value kernels' per-edge readout runs in the fused
+pair terms, ``fused_pairs``, and the weighted messages are summed per target);
+the projections are per-frequency dense products.  A layer whose fused op is not
 enabled raises (the reference would fall back to its eager torch path; here
 that path is the test oracle).
 """
@@ -35,7 +37,7 @@ import torch.utils.checkpoint
 from torch import Tensor, nn
 
 from gm_attention_amd.discretization.discretization import SphericalDiscretization
-from gm_attention_amd.nn import fused_attention, fused_factored, radial
+from gm_attention_amd.nn import fused_attention, fused_factored, kernels, radial
 from gm_attention_amd.nn.kernels import SO2SteerableKernel
 from gm_attention_amd.nn.linear import SO2Linear, apply_linear
 from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
@@ -54,6 +56,18 @@ def _validate_node_field(x: SO2FeatureField, field_type: SO2FieldType, edges) ->
     if tuple(x.batch_shape) != (n_nodes,):
         raise ValueError(f"x.batch_shape must equal (n_nodes,) = ({n_nodes},), inferred from edges.row_ptr, "
                          f"got {tuple(x.batch_shape)}.")
+
+
+def gather_to_edges(x: SO2FeatureField, index: Tensor) -> SO2FeatureField:
+    """Every frequency's rows at ``index`` (reference nn/_scatter.py:17-33)."""
+    return SO2FeatureField(x.field_type, {f: x[f].index_select(0, index) for f in x.field_type.frequencies})
+
+
+def weighted_segment_sum(weight: Tensor, messages: dict[int, Tensor], row_ptr: Tensor) -> dict[int, Tensor]:
+    """``sum_e w_e m_e`` over each target's CSR segment, per frequency
+    (reference nn/_scatter.py:36-58 on the weighted messages)."""
+    return {f: torch.segment_reduce(weight.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum", offsets=row_ptr, axis=0)
+            for f, m in messages.items()}
 
 
 def _checkpointed(module: nn.Module, compute):
@@ -109,6 +123,9 @@ class SO2Attention(nn.Module):
             raise RuntimeError("the fused scores-and-softmax op is not enabled for this call "
                                "(GM_FUSED_ATTENTION=1 and device tensors required)")
         alpha = fused_attention.softmax_head(self, q.to_flat(), k.to_flat(), edges)
+        if not kernels.factored_enabled():  # the per-edge readout through the fused pair terms
+            messages = self.value(gather_to_edges(x, edges.source_index), edges)
+            return weighted_segment_sum(alpha, messages.coefficients, edges.row_ptr)
         return self.value.forward_factored_aggregated(x, edges, alpha, products, groups).coefficients
 
     def forward_chunked(self, x: SO2FeatureField, edges, *, chunk_size: int) -> SO2FeatureField:
@@ -118,7 +135,7 @@ class SO2Attention(nn.Module):
         edges = _resolve_edges(edges, self.cutoff)
         _validate_node_field(x, self.field_type_in, edges)
         n_nodes = edges.row_ptr.shape[0] - 1
-        products = self.value.node_products(x)
+        products = self.value.node_products(x) if kernels.factored_enabled() else None
         totals: dict[int, Tensor] = {}
         for start in range(0, n_nodes, chunk_size):
             stop = min(start + chunk_size, n_nodes)
@@ -211,14 +228,22 @@ def _aggregated_factored(mhsa: SO2MHSA, x: SO2FeatureField, edges, alpha: Tensor
     own trunks when that kernel does not serve them), every head's node
     mixes from one matrix product per input frequency, then the fused factored
     op per head on those mixes in place."""
+    if not kernels.factored_enabled():  # per-edge readouts through the fused pair terms, head by head
+        source = gather_to_edges(x, edges.source_index)
+        fields = []
+        for head, weights in zip(mhsa.heads, alpha.unbind(1), strict=True):
+            messages = cast(SO2SteerableKernel, head.value)(source, edges)
+            fields.append(SO2FeatureField(mhsa.field_type_attn,
+                                          weighted_segment_sum(weights, messages.coefficients, edges.row_ptr)))
+        return _concatenate_heads(fields, mhsa.field_type_in).coefficients
     groups = fused_factored.groups_for(edges, edges.source_index)
-    kernels = [cast(SO2SteerableKernel, head.value) for head in mhsa.heads]
-    if fused_factored.enabled(kernels[0], x, edges):
-        if radial.eligible(kernels, x.dtype, x.device):
-            h, trunk = None, functools.partial(radial.trunk_hidden_heads, kernels)
+    values = [cast(SO2SteerableKernel, head.value) for head in mhsa.heads]
+    if fused_factored.enabled(values[0], x, edges):
+        if radial.eligible(values, x.dtype, x.device):
+            h, trunk = None, functools.partial(radial.trunk_hidden_heads, values)
         else:
-            h, trunk = torch.stack([k._trunk_hidden(edges.distances) for k in kernels]), None
-        out = fused_factored.forward_aggregated_heads(kernels, x, edges, alpha, h, groups, trunk)  # (N, H, d_out)
+            h, trunk = torch.stack([k._trunk_hidden(edges.distances) for k in values]), None
+        out = fused_factored.forward_aggregated_heads(values, x, edges, alpha, h, groups, trunk)  # (N, H, d_out)
         attn = mhsa.field_type_attn
         return _concatenate_heads([SO2FeatureField.from_flat(attn, o) for o in out.unbind(1)],
                                   mhsa.field_type_in).coefficients

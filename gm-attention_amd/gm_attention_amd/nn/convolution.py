@@ -27,7 +27,8 @@ import torch.utils.checkpoint
 from torch import Tensor, nn
 
 from gm_attention_amd.discretization.discretization import SphericalDiscretization
-from gm_attention_amd.nn import fused_attention, fused_factored
+from gm_attention_amd.nn import fused_attention, fused_factored, kernels
+from gm_attention_amd.nn.attention import gather_to_edges, weighted_segment_sum
 from gm_attention_amd.nn.depthwise import SO2DepthwiseKernel, stacked_coefficients
 from gm_attention_amd.nn.kernels import SO2SteerableKernel
 from gm_attention_amd.nn.linear import SO2Linear
@@ -106,6 +107,9 @@ class SO2Convolution(nn.Module):
         assert isinstance(kernel, SO2SteerableKernel)
         g = fused_attention.geometry(edges, self.cutoff, self.window, x.dtype)
         weights = g.aggregation_weights(self.normalize, self.eps)
+        if not kernels.factored_enabled():  # the per-edge readout through the fused pair terms
+            messages = kernel(gather_to_edges(x, edges.source_index), edges)
+            return weighted_segment_sum(weights, messages.coefficients, edges.row_ptr)
         return kernel.forward_factored_aggregated(x, edges, weights, products, groups).coefficients
 
     def _aggregate_fused(self, x: SO2FeatureField, edges) -> dict[int, Tensor]:
@@ -123,7 +127,7 @@ class SO2Convolution(nn.Module):
             raise ValueError(f"chunk_size must be at least 1, got {chunk_size}.")
         edges = self._check(x, edges)
         n_nodes = edges.row_ptr.shape[0] - 1
-        factored = isinstance(self.kernel, SO2SteerableKernel)
+        factored = isinstance(self.kernel, SO2SteerableKernel) and kernels.factored_enabled()
         products = self.kernel.node_products(x) if factored else None
         totals: dict[int, Tensor] = {}
         for start in range(0, n_nodes, chunk_size):

@@ -15,11 +15,14 @@ Restates the parts of the reference's ``nn/kernels.py`` the fused path needs:
   ``t = 0..T`` (the bias on ``t = 0``), the blocks that read one node vector
   as one product;
 * ``forward_factored`` / ``forward_factored_aggregated`` (:645-732) through the
-  fused factored op (``fused_factored.forward`` / ``forward_aggregated``).
+  fused factored op (``fused_factored.forward`` / ``forward_aggregated``);
+* ``forward`` / ``validate_call`` (:421-476) on an edge-shaped field: the
+  per-edge readout ``_forward_general`` (:752-915) through the fused pair
+  terms (``fused_pairs.forward_general``).
 
-The eager per-edge readout (``_forward_general``) and the eager factored
-branch are the parity oracle of this path and live with the tests, not here:
-a kernel whose fused op is not enabled raises instead of falling back.
+The eager per-edge readout and the eager factored branch are the parity
+oracle of this path and live with the tests, not here: a kernel whose fused
+op is not enabled raises instead of falling back.
 """
 
 from __future__ import annotations
@@ -109,6 +112,32 @@ class SO2SteerableKernel(nn.Module):
                 offset += width
         self.complex_head = nn.Linear(trunk_width, offset, bias=bias, dtype=dtype, device=device) if offset else None
         self.real_head = nn.Linear(trunk_width, real_width, bias=bias, dtype=dtype, device=device) if real_width else None
+
+    def validate_call(self, x: SO2FeatureField, edges) -> None:
+        """The checks of :meth:`forward` (:444-476): the input type, one
+        gathered feature per edge, harmonics tabulated to the top frequency pair."""
+        if x.field_type != self.field_type_in:
+            raise ValueError(f"Expected a field of type {self.field_type_in!r}, got {x.field_type!r}.")
+        if tuple(x.batch_shape) != (edges.n_edges,):
+            raise ValueError(f"x.batch_shape must equal (edges.n_edges,) = ({edges.n_edges},), got "
+                             f"{tuple(x.batch_shape)}. Gather node features to edge shape (e.g. via "
+                             "edges.source_index) before calling this kernel.")
+        required = self.field_type_in.max_frequency + self.field_type_out.max_frequency
+        if edges.max_frequency < required:
+            raise ValueError(f"edges tabulates harmonics up to order {edges.max_frequency}, but connecting frequency "
+                             f"{self.field_type_in.max_frequency} to {self.field_type_out.max_frequency} needs "
+                             f"order {required}.")
+
+    def forward(self, x: SO2FeatureField, edges) -> SO2FeatureField:
+        """One message per edge from the source features gathered to edge
+        shape (:421-442): the per-edge readout through the fused pair terms."""
+        from gm_attention_amd.nn import fused_pairs
+
+        self.validate_call(x, edges)
+        if not fused_pairs.enabled(self, x, edges):
+            raise RuntimeError("the fused pair terms are not enabled for this call (GM_FUSED_PAIRS=1, device "
+                               "tensors, float32/64, blocks and trunk within 16 required)")
+        return fused_pairs.forward_general(self, x, edges)
 
     # ---- the factored evaluation's pieces
 

@@ -354,6 +354,50 @@ int gm_scatter_transpose_f32(const float* src_t, const int64_t* perm, int64_t n,
 int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out, int64_t pa,
                             int64_t pt, int32_t* n_slots, uint32_t* slot, uint8_t* slotcol);
 
+/* ---------------- steerable kernel pair terms (per-edge readout) ----------------
+ *
+ * One (n, m, role) term of the general kernel's per-edge readout:
+ *   out(e) += post(e) s(e) f( sum_a M_ba(e) uu_a(e) ),  uu = pre(e) u~(e),
+ *   M_ba(e) = sum_t W[(b a) row, t] hidden(e, t) + bias[(b a) row],
+ * f = Re under GM_PAIRS_OUT_REAL (then out(e) += s(e) Re(...), post unused),
+ * u~ = conj(u) under GM_PAIRS_CONJ_U, a real u promoted under GM_PAIRS_U_REAL;
+ * under GM_PAIRS_MATRIX_COMPLEX entry idx = b * a + a' is the row pair
+ * (2 idx, 2 idx + 1) = (re, im), else the single real row idx.
+ *
+ * Replaces gm_pairs.forward(hidden, weight, bias, u, pre, post, scale, out,
+ * a, b, flags) (fused/pairs_cpu.cpp:88-111, the per-term launch of
+ * fused_pairs.py:176-185).
+ *   hidden (n_edges, trunk)     weight (width, trunk)   bias (width) or NULL
+ *   u      (n_edges, a[, 2])    pre, post (n_edges, 2) or NULL   scale (n_edges) or NULL
+ *   out    (n_edges, b[, 2])    accumulated
+ * width = (MATRIX_COMPLEX ? 2 : 1) a b;  1 <= a, b, trunk <= 16.
+ *
+ * gm_pairs_backward replaces gm_pairs.backward(hidden, weight, bias, u, pre,
+ * post, scale, grad_out, grad_u, grad_hidden, grad_k, a, b, flags)
+ * (fused/pairs_cpu.cpp:113-136; fused_pairs.py:209-218): accumulates
+ * grad_u (n_edges, a[, 2]) and grad_hidden (n_edges, trunk), and writes this
+ * term's coefficient gradient row r of edge e at grad_k[r * grad_k_stride + e]
+ * (grad_k_stride >= n_edges).  Terms launched in stream order accumulate
+ * without races (each lane owns its edge's rows). */
+#define GM_PAIRS_MATRIX_COMPLEX 1
+#define GM_PAIRS_U_REAL 2
+#define GM_PAIRS_CONJ_U 4
+#define GM_PAIRS_OUT_REAL 8
+int gm_pairs_forward_f32(const float* hidden, const float* weight, const float* bias, const float* u,
+                         const float* pre, const float* post, const float* scale, float* out, int64_t n_edges,
+                         int64_t a, int64_t b, int64_t trunk, int64_t flags, void* stream);
+int gm_pairs_forward_f64(const double* hidden, const double* weight, const double* bias, const double* u,
+                         const double* pre, const double* post, const double* scale, double* out, int64_t n_edges,
+                         int64_t a, int64_t b, int64_t trunk, int64_t flags, void* stream);
+int gm_pairs_backward_f32(const float* hidden, const float* weight, const float* bias, const float* u,
+                          const float* pre, const float* post, const float* scale, const float* grad_out,
+                          float* grad_u, float* grad_hidden, float* grad_k, int64_t grad_k_stride, int64_t n_edges,
+                          int64_t a, int64_t b, int64_t trunk, int64_t flags, void* stream);
+int gm_pairs_backward_f64(const double* hidden, const double* weight, const double* bias, const double* u,
+                          const double* pre, const double* post, const double* scale, const double* grad_out,
+                          double* grad_u, double* grad_hidden, double* grad_k, int64_t grad_k_stride,
+                          int64_t n_edges, int64_t a, int64_t b, int64_t trunk, int64_t flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

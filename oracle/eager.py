@@ -159,3 +159,27 @@ def factored_aggregate(rows: Tensor, weights: Tensor, row_ptr: Tensor) -> Tensor
     """``out_i = sum_{e -> i} w_e rows_e`` (kernels.py:715-725 with
     _scatter.py:36-58's segment sum)."""
     return torch.segment_reduce(weights.unsqueeze(-1) * rows, "sum", offsets=row_ptr, axis=0)
+
+
+def pair_term(hidden: Tensor, weight: Tensor, bias: Tensor | None, u: Tensor, pre: Tensor | None, post: Tensor | None,
+              scale: Tensor | None, a: int, b: int, flags: int) -> Tensor:
+    """One fused pair term's contribution (E, b) (reference nn/fused/pairs.h:1-22
+    and forward_edge :286-309): M(e) = W h(e) + bias as a (b, a) block, complex
+    from (re, im) row pairs under MATRIX_COMPLEX (1); uu = pre * u~ with u~ =
+    conj(u) under CONJ_U (4) or a real u promoted under U_REAL (2); q = M uu;
+    Re(q) * scale under OUT_REAL (8), else post * scale * q."""
+    E = hidden.shape[0]
+    m = hidden @ weight.T + (bias if bias is not None else 0.0)
+    if flags & 1:
+        M = torch.complex(m[:, 0::2], m[:, 1::2]).reshape(E, b, a)
+    else:
+        M = m.reshape(E, b, a).to(torch.complex128 if hidden.dtype == torch.float64 else torch.complex64)
+    uu = u.to(M.dtype) if flags & 2 else (u.conj() if flags & 4 else u)
+    if pre is not None:
+        uu = pre.unsqueeze(-1) * uu
+    q = (M * uu.unsqueeze(-2)).sum(-1)
+    s = scale if scale is not None else torch.ones(E, dtype=hidden.dtype)
+    if flags & 8:
+        return q.real * s.unsqueeze(-1)
+    p = (post if post is not None else torch.ones(E, dtype=M.dtype)) * s
+    return p.unsqueeze(-1) * q
