@@ -1,0 +1,552 @@
+// The depthwise steerable convolution with its radial heads evaluated inside
+// the walk (CDNA4, gfx950): no per-edge coefficient tensor in either direction.
+//
+// Per edge e = (i <- j) with r = rho_e = d_e / cutoff, s = r^2:
+//   b_k(e)   = exp(-((s - mu_k) / sigma)^2 / 2)                 k < NB  (Gaussian basis)
+//   pre_t(e) = sum_k W1[t, k] b_k(e) + b1[t],  h_t = SiLU(pre_t)   t < 16  (the shared trunk)
+//   C(e)     = R (h_0..h_15, 1)^T                                  (the readout heads, bias as column 16)
+// and per copy of the field, with z = e^{i n gamma_e} v_j (transport),
+//   scalar copy a:       m = C_a v_j,a
+//   complex copy of n:   m = A z + r^{2n} e^{2 i n phi_e} B conj(z),   (A, B) = C's rows (Ar, Ai, Br, Bi)
+//   out_i = sum_e w_e m_e.
+// (The reference: nn/depthwise.py:147-193 and :206-238 -- the readout
+// materialised per edge by torch products, then fused/attention.h:167-232 on
+// it.)  R's rows are ordered in 16-row tiles: scalar tiles first (row a =
+// copy a), then complex tiles of four copies, copy q of a tile owning rows
+// 4q..4q+3 = (Ar, Ai, Br, Bi); every complex tile holds one frequency.
+//
+// MFMA mapping (v_mfma_f32_16x16x4f32: lane l supplies A[l%16][l/16],
+// B[l/16][l%16] and holds D[4(l/16)+r][l%16]): lane (q = l/16, c = l%16)
+// works on edge c of a 16-edge tile and computes trunk features 4q..4q+3 of
+// it; the coefficient product D_m = R_m (w H~) over k-steps s = 0..4 (k =
+// 4q + s, then the bias row) leaves the lane rows 4q..4q+3 of tile m for its
+// edge: four scalar copies or one complex copy, whose message it forms at
+// once.  Forward: one wave per target node, lanes accumulate their edge
+// column's messages, a 16-lane butterfly per target.  Backward: persistent
+// waves over SOURCE nodes (the transposed CSR): per edge tile the same
+// coefficients, then dC (the coefficients' gradient) and dv in registers,
+// dh~ = R^T dC on MFMA (D layout = the lane's own trunk features), and
+// dR += dC h~^T on MFMA with dC and h~ transposed through the wave's LDS;
+// per wave the parameter gradients end in a partial row, and a second kernel
+// sums the rows in a fixed order (deterministic, no atomics).
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+
+namespace gm {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRNS = 2;            // scalar tiles: up to 32 scalar copies
+constexpr int kRNC = 16;           // complex tiles: up to 64 complex copies
+constexpr int kRNT = kRNS + kRNC;  // coefficient tiles
+constexpr int kRWaves = 4;         // waves per workgroup
+constexpr int kRThreads = kRWaves * kWave;
+constexpr int kRMaxBasis = 8;
+// per-wave partial row of the backward: dR in lane layout, the bias column, W1 and b1
+constexpr int kRPartDR = kRNT * 256;
+constexpr int kRPartDB = kRNT * 16;
+constexpr int kRPartW1 = 16 * kRMaxBasis + 16;
+constexpr int kRPart = kRPartDR + kRPartDB + kRPartW1;
+
+struct RadialConvArgs {
+  const float* v;          // (N, D)
+  const float* rf;         // (kRNT, 5, 64): A operand of the coefficient product
+  const float* rb;         // (kRNT, 4, 64): A operand of dh~ = R^T dC
+  const float* w1;         // (16, NB)
+  const float* b1;         // (16,) or null
+  const float* transport;  // (E, orders, 2)
+  const float* angular;    // (E, orders, 2)
+  const float* rho;        // (E,)
+  const float* weights;    // (E,)
+  const int64_t* row_ptr;  // (N + 1,)
+  const int64_t* source;   // (E,)
+  const float* g;          // (N, D) backward
+  const int64_t* src_ptr;  // (N + 1,) backward: edges grouped by source
+  const int64_t* src_order;
+  const int64_t* target;
+  float* out;      // (N, D)
+  float* dv;       // (N, D)
+  float* partial;  // (n_waves, kRPart)
+  int64_t n_nodes;
+  int D, orders, ns, nc, a0;
+  float inv_width;
+  float centers[kRMaxBasis];
+  int tile_n[kRNC];    // frequency of complex tile m
+  int tile_col[kRNC];  // flat column of its copy 0 (copy q at + 2q)
+};
+
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// A wave's LDS operations run in order; handing data between its lanes
+// needs only a compiler ordering point at wavefront scope.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f); }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+__device__ __forceinline__ float2 ld2(const float* p) { return *reinterpret_cast<const float2*>(p); }
+
+// One edge as a lane sees it: the source (or target), weight, transport
+// phases of orders 1 and 2 and the angular factors r^{2n} e^{2 i n phi}.
+struct EdgeView {
+  int64_t node;
+  float w, r;
+  float2 t1, t2, p1, p2;
+};
+
+__device__ __forceinline__ EdgeView edge_view(const RadialConvArgs& a, int64_t e, int64_t node, bool live) {
+  EdgeView v;
+  v.node = node;
+  v.w = live ? a.weights[e] : 0.f;
+  v.r = a.rho[e];
+  const float* tr = a.transport + e * a.orders * 2;
+  const float* an = a.angular + e * a.orders * 2;
+  v.t1 = ld2(tr + 2);
+  v.t2 = ld2(tr + 4);
+  const float r2 = v.r * v.r, r4 = r2 * r2;
+  const float2 a2 = ld2(an + 4), a4 = ld2(an + 8);
+  v.p1 = make_float2(r2 * a2.x, r2 * a2.y);
+  v.p2 = make_float2(r4 * a4.x, r4 * a4.y);
+  return v;
+}
+
+// The lane's trunk features k = 4q + s (s < 4) of its edge: pre-activations,
+// SiLU outputs and (for the backward) the basis.
+template <int NB>
+__device__ __forceinline__ void trunk_of(const RadialConvArgs& a, const float* w1s, float r, int q, float (&bas)[NB],
+                                         float (&pre)[4], float (&h)[4]) {
+  const float s = r * r;
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const float z = (s - a.centers[k]) * a.inv_width;
+    bas[k] = fexp(-0.5f * z * z);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = 4 * q + u;
+    float p = w1s[16 * kRMaxBasis + t];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) p = fmaf(w1s[t * kRMaxBasis + k], bas[k], p);
+    pre[u] = p;
+    h[u] = p * frcp(1.f + fexp(-p));
+  }
+}
+
+__device__ __forceinline__ void load_tables(const RadialConvArgs& a, float* rf_s, float* rb_s, float* w1s, int nb) {
+  for (int i = threadIdx.x; i < kRNT * 5 * 64; i += kRThreads) rf_s[i] = a.rf[i];
+  if (rb_s)
+    for (int i = threadIdx.x; i < kRNT * 4 * 64; i += kRThreads) rb_s[i] = a.rb[i];
+  for (int i = threadIdx.x; i < 16 * kRMaxBasis; i += kRThreads) {
+    const int t = i / kRMaxBasis, k = i % kRMaxBasis;
+    w1s[i] = k < nb ? a.w1[t * nb + k] : 0.f;
+  }
+  if (threadIdx.x < 16) w1s[16 * kRMaxBasis + threadIdx.x] = a.b1 ? a.b1[threadIdx.x] : 0.f;
+}
+
+template <int NB>
+__global__ __launch_bounds__(kRThreads) void conv_radial_forward_kernel(RadialConvArgs a) {
+  __shared__ float rf_s[kRNT * 5 * 64];
+  __shared__ float w1s[16 * kRMaxBasis + 16];
+  load_tables(a, rf_s, nullptr, w1s, NB);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
+  const int64_t i = xcd_block(blockIdx.x, gridDim.x) * kRWaves + (threadIdx.x >> 6);
+  if (i >= a.n_nodes) return;
+  float accs[kRNS][4], accc[kRNC][2];
+#pragma unroll
+  for (int m = 0; m < kRNS; ++m) accs[m][0] = accs[m][1] = accs[m][2] = accs[m][3] = 0.f;
+#pragma unroll
+  for (int m = 0; m < kRNC; ++m) accc[m][0] = accc[m][1] = 0.f;
+  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+  for (int64_t base = e0; base < e1; base += 16) {
+    const bool live = base + c < e1;
+    const int64_t e = live ? base + c : e0;
+    const EdgeView ev = edge_view(a, e, a.source[e], live);
+    float bas[NB], pre[4], h[4];
+    trunk_of<NB>(a, w1s, ev.r, q, bas, pre, h);
+    float bv[5];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) bv[u] = ev.w * h[u];
+    bv[4] = q == 0 ? ev.w : 0.f;
+    const float* vj = a.v + ev.node * a.D;
+#pragma unroll
+    for (int m = 0; m < kRNS; ++m) {
+      if (m < a.ns) {
+      floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 5; ++s) d = mfma16(rf_s[(m * 5 + s) * 64 + lane], bv[s], d);
+      const int col = 16 * m + 4 * q;
+      if (col < a.a0) {
+        const float4 x = *reinterpret_cast<const float4*>(vj + col);
+        accs[m][0] = fmaf(d[0], x.x, accs[m][0]);
+        accs[m][1] = fmaf(d[1], x.y, accs[m][1]);
+        accs[m][2] = fmaf(d[2], x.z, accs[m][2]);
+        accs[m][3] = fmaf(d[3], x.w, accs[m][3]);
+      }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < kRNC; ++m) {
+      if (m < a.nc) {
+      floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 5; ++s) d = mfma16(rf_s[((kRNS + m) * 5 + s) * 64 + lane], bv[s], d);
+      const bool one = a.tile_n[m] == 1;
+      const float2 x = ld2(vj + a.tile_col[m] + 2 * q);
+      const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
+      const float pr = one ? ev.p1.x : ev.p2.x, pi = one ? ev.p1.y : ev.p2.y;
+      const float zr = tc * x.x - ts * x.y, zi = tc * x.y + ts * x.x;
+      const float bzr = d[2] * zr + d[3] * zi, bzi = d[3] * zr - d[2] * zi;  // B conj(z)
+      accc[m][0] += (d[0] * zr - d[1] * zi) + (pr * bzr - pi * bzi);
+      accc[m][1] += (d[0] * zi + d[1] * zr) + (pr * bzi + pi * bzr);
+      }
+    }
+  }
+  // sum each copy over the 16 edge lanes of its row, then lane c = 0 stores
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {
+#pragma unroll
+    for (int m = 0; m < kRNS; ++m)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) accs[m][u] += __shfl_xor(accs[m][u], off, kWave);
+#pragma unroll
+    for (int m = 0; m < kRNC; ++m) {
+      accc[m][0] += __shfl_xor(accc[m][0], off, kWave);
+      accc[m][1] += __shfl_xor(accc[m][1], off, kWave);
+    }
+  }
+  if (c != 0) return;
+  float* oi = a.out + i * a.D;
+#pragma unroll
+  for (int m = 0; m < kRNS; ++m) {
+    const int col = 16 * m + 4 * q;
+    if (m < a.ns && col < a.a0)
+      *reinterpret_cast<float4*>(oi + col) = make_float4(accs[m][0], accs[m][1], accs[m][2], accs[m][3]);
+  }
+#pragma unroll
+  for (int m = 0; m < kRNC; ++m)
+    if (m < a.nc) *reinterpret_cast<float2*>(oi + a.tile_col[m] + 2 * q) = make_float2(accc[m][0], accc[m][1]);
+}
+
+// dC's rows for the lane's edge (D layout) through the wave's LDS tile into
+// the A-operand layout dC[row c][edge 4s + q], then the bias column sums and
+// dR += dC h~^T; and dh~ += R^T dC straight from the D layout.
+__device__ __forceinline__ void tile_gradients(const float* rb_s, float* T, int m, int lane, int c, int q,
+                                               const float (&dc)[4], const float (&ht)[4], floatx4& dh,
+                                               floatx4& dr, float& db) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) dh = mfma16(rb_s[(m * 4 + r) * 64 + lane], dc[r], dh);
+  wave_sync();
+  *reinterpret_cast<float4*>(T + c * 16 + 4 * q) = make_float4(dc[0], dc[1], dc[2], dc[3]);
+  wave_sync();
+  float at[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) at[s] = T[(4 * s + q) * 16 + c];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    db += at[s];
+    dr = mfma16(at[s], ht[s], dr);
+  }
+}
+
+template <int NB>
+__global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialConvArgs a) {
+  __shared__ float rf_s[kRNT * 5 * 64];
+  __shared__ float rb_s[kRNT * 4 * 64];
+  __shared__ float w1s[16 * kRMaxBasis + 16];
+  __shared__ __attribute__((aligned(16))) float tr_s[kRWaves][256];
+  load_tables(a, rf_s, rb_s, w1s, NB);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4, wave = threadIdx.x >> 6;
+  float* T = tr_s[wave];
+  const int64_t gw = (int64_t)blockIdx.x * kRWaves + wave, nw = (int64_t)gridDim.x * kRWaves;
+  floatx4 dr[kRNT];
+  float db[kRNT];
+#pragma unroll
+  for (int m = 0; m < kRNT; ++m) {
+    dr[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+    db[m] = 0.f;
+  }
+  float dw1[4][NB], db1[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    db1[u] = 0.f;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) dw1[u][k] = 0.f;
+  }
+  for (int64_t j = gw; j < a.n_nodes; j += nw) {
+    float dvs[kRNS][4], dvc[kRNC][2];
+#pragma unroll
+    for (int m = 0; m < kRNS; ++m) dvs[m][0] = dvs[m][1] = dvs[m][2] = dvs[m][3] = 0.f;
+#pragma unroll
+    for (int m = 0; m < kRNC; ++m) dvc[m][0] = dvc[m][1] = 0.f;
+    const float* vj = a.v + j * a.D;
+    const int64_t g0 = a.src_ptr[j], g1 = a.src_ptr[j + 1];
+    for (int64_t base = g0; base < g1; base += 16) {
+      const bool live = base + c < g1;
+      const int64_t e = a.src_order[live ? base + c : g0];
+      const EdgeView ev = edge_view(a, e, a.target[e], live);
+      float bas[NB], pre[4], h[4];
+      trunk_of<NB>(a, w1s, ev.r, q, bas, pre, h);
+      float bv[5];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bv[u] = ev.w * h[u];
+      bv[4] = q == 0 ? ev.w : 0.f;
+      // h~^T for dR's B operand: ht[s] = h_c(edge 4s + q)
+      wave_sync();
+      *reinterpret_cast<float4*>(T + c * 16 + 4 * q) = make_float4(h[0], h[1], h[2], h[3]);
+      wave_sync();
+      float ht[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ht[s] = T[(4 * s + q) * 16 + c];
+      const float* gt = a.g + ev.node * a.D;
+      floatx4 dh[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int m = 0; m < kRNS; ++m) {
+        if (m < a.ns) {
+        floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 5; ++s) d = mfma16(rf_s[(m * 5 + s) * 64 + lane], bv[s], d);
+        const int col = 16 * m + 4 * q;
+        float dc[4] = {0.f, 0.f, 0.f, 0.f};
+        if (col < a.a0) {
+          const float4 x = *reinterpret_cast<const float4*>(vj + col);
+          const float4 gv = *reinterpret_cast<const float4*>(gt + col);
+          dvs[m][0] = fmaf(d[0], gv.x, dvs[m][0]);
+          dvs[m][1] = fmaf(d[1], gv.y, dvs[m][1]);
+          dvs[m][2] = fmaf(d[2], gv.z, dvs[m][2]);
+          dvs[m][3] = fmaf(d[3], gv.w, dvs[m][3]);
+          dc[0] = ev.w * gv.x * x.x;
+          dc[1] = ev.w * gv.y * x.y;
+          dc[2] = ev.w * gv.z * x.z;
+          dc[3] = ev.w * gv.w * x.w;
+        }
+        tile_gradients(rb_s, T, m, lane, c, q, dc, ht, dh[m & 1], dr[m], db[m]);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < kRNC; ++m) {
+        if (m < a.nc) {
+        floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 5; ++s) d = mfma16(rf_s[((kRNS + m) * 5 + s) * 64 + lane], bv[s], d);
+        const bool one = a.tile_n[m] == 1;
+        const int col = a.tile_col[m] + 2 * q;
+        const float2 x = ld2(vj + col), gv = ld2(gt + col);
+        const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
+        const float pr = one ? ev.p1.x : ev.p2.x, pi = one ? ev.p1.y : ev.p2.y;
+        const float zr = tc * x.x - ts * x.y, zi = tc * x.y + ts * x.x;
+        // dz = conj(wA) g + p (wB) conj(g);  dv += conj(tau) dz
+        const float bgr = d[2] * gv.x + d[3] * gv.y, bgi = d[3] * gv.x - d[2] * gv.y;
+        const float dzr = (d[0] * gv.x + d[1] * gv.y) + (pr * bgr - pi * bgi);
+        const float dzi = (d[0] * gv.y - d[1] * gv.x) + (pr * bgi + pi * bgr);
+        dvc[m][0] += tc * dzr + ts * dzi;
+        dvc[m][1] += tc * dzi - ts * dzr;
+        // dA = w g conj(z);  dB = w (g conj(p)) z
+        const float xr = gv.x * pr + gv.y * pi, xi = gv.y * pr - gv.x * pi;
+        float dc[4];
+        dc[0] = ev.w * (gv.x * zr + gv.y * zi);
+        dc[1] = ev.w * (gv.y * zr - gv.x * zi);
+        dc[2] = ev.w * (xr * zr - xi * zi);
+        dc[3] = ev.w * (xr * zi + xi * zr);
+        tile_gradients(rb_s, T, kRNS + m, lane, c, q, dc, ht, dh[m & 1], dr[kRNS + m], db[kRNS + m]);
+        }
+      }
+      // the trunk's backward for the lane's features 4q + u of its edge
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float sg = frcp(1.f + fexp(-pre[u]));
+        const float dp = (dh[0][u] + dh[1][u]) * sg * (1.f + pre[u] * (1.f - sg));
+        db1[u] += dp;
+#pragma unroll
+        for (int k = 0; k < NB; ++k) dw1[u][k] = fmaf(dp, bas[k], dw1[u][k]);
+      }
+    }
+    // dv_j: each copy summed over the 16 edge lanes of its row
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+#pragma unroll
+      for (int m = 0; m < kRNS; ++m)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dvs[m][u] += __shfl_xor(dvs[m][u], off, kWave);
+#pragma unroll
+      for (int m = 0; m < kRNC; ++m) {
+        dvc[m][0] += __shfl_xor(dvc[m][0], off, kWave);
+        dvc[m][1] += __shfl_xor(dvc[m][1], off, kWave);
+      }
+    }
+    if (c == 0) {
+      float* dvj = a.dv + j * a.D;
+#pragma unroll
+      for (int m = 0; m < kRNS; ++m) {
+        const int col = 16 * m + 4 * q;
+        if (m < a.ns && col < a.a0)
+          *reinterpret_cast<float4*>(dvj + col) = make_float4(dvs[m][0], dvs[m][1], dvs[m][2], dvs[m][3]);
+      }
+#pragma unroll
+      for (int m = 0; m < kRNC; ++m)
+        if (m < a.nc) *reinterpret_cast<float2*>(dvj + a.tile_col[m] + 2 * q) = make_float2(dvc[m][0], dvc[m][1]);
+    }
+  }
+  // this wave's partial row: dR in lane layout, the bias column, W1 and b1
+  float* part = a.partial + gw * kRPart;
+#pragma unroll
+  for (int m = 0; m < kRNT; ++m)
+    *reinterpret_cast<float4*>(part + m * 256 + lane * 4) = make_float4(dr[m][0], dr[m][1], dr[m][2], dr[m][3]);
+#pragma unroll
+  for (int m = 0; m < kRNT; ++m) {
+    float v = db[m];
+    v += __shfl_xor(v, 16, kWave);
+    v += __shfl_xor(v, 32, kWave);
+    if (q == 0) part[kRPartDR + m * 16 + c] = v;
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float b = db1[u];
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) b += __shfl_xor(b, off, kWave);
+    if (c == 0) part[kRPartDR + kRPartDB + 16 * kRMaxBasis + 4 * q + u] = b;
+#pragma unroll
+    for (int k = 0; k < kRMaxBasis; ++k) {
+      float w = k < NB ? dw1[u][k < NB ? k : 0] : 0.f;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) w += __shfl_xor(w, off, kWave);
+      if (c == 0) part[kRPartDR + kRPartDB + (4 * q + u) * kRMaxBasis + k] = w;
+    }
+  }
+}
+
+// grad[p] = sum over waves w (in order) of partial[w][p].
+__global__ __launch_bounds__(256) void conv_radial_reduce_kernel(const float* partial, int64_t n_waves, float* grad) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= kRPart) return;
+  float s = 0.f;
+  for (int64_t w = 0; w < n_waves; ++w) s += partial[w * kRPart + p];
+  grad[p] = s;
+}
+
+int prepare(RadialConvArgs& a, const float* v, const float* rf, const float* rb, const float* w1, const float* b1,
+            const float* centers_host, int64_t nb, double width, const float* transport, const float* angular,
+            const float* rho, const float* weights, const int64_t* row_ptr, const int64_t* source, int64_t n_nodes,
+            int64_t n_edges, int64_t D, int64_t orders, int64_t a0, int64_t ns, int64_t nc, const int32_t* tile_n,
+            const int32_t* tile_col) {
+  a = RadialConvArgs{};
+  GM_REQUIRE(n_nodes >= 0 && n_edges >= 0, "sizes must be non-negative");
+  GM_REQUIRE(n_nodes < (int64_t(1) << 31) * kRWaves, "too many nodes for one launch");
+  GM_REQUIRE(nb == 4 || nb == 6 || nb == 8, "the radial basis must have 4, 6 or 8 functions");
+  GM_REQUIRE(width > 0, "the basis width must be positive");
+  GM_REQUIRE(ns >= 0 && ns <= kRNS && nc >= 0 && nc <= kRNC, "at most 32 scalar and 64 complex copies");
+  GM_REQUIRE(a0 >= 0 && a0 % 4 == 0 && a0 <= 16 * ns && a0 > 16 * (ns - 1), "a_0 must be a multiple of 4 filling ns tiles");
+  GM_REQUIRE(orders >= 5, "the phase tables must hold orders 0..4");
+  GM_REQUIRE(D % 4 == 0, "D must be a multiple of 4");
+  int covered = (int)a0;
+  for (int m = 0; m < nc; ++m) {
+    GM_REQUIRE(tile_n[m] == 1 || tile_n[m] == 2, "complex tiles hold frequency 1 or 2");
+    GM_REQUIRE(tile_col[m] >= a0 && tile_col[m] % 2 == 0 && tile_col[m] + 8 <= D, "a complex tile's columns lie in the field");
+    covered += 8;
+  }
+  GM_REQUIRE(covered == D, "the tiles must cover the flat width D exactly");
+  if (n_nodes > 0) GM_REQUIRE(v && rf && w1 && row_ptr, "v, the tables and row_ptr must be device pointers");
+  if (n_edges > 0) GM_REQUIRE(transport && angular && rho && weights && source, "the per-edge tables must be device pointers");
+  a.v = v;
+  a.rf = rf;
+  a.rb = rb;
+  a.w1 = w1;
+  a.b1 = b1;
+  a.transport = transport;
+  a.angular = angular;
+  a.rho = rho;
+  a.weights = weights;
+  a.row_ptr = row_ptr;
+  a.source = source;
+  a.n_nodes = n_nodes;
+  a.D = (int)D;
+  a.orders = (int)orders;
+  a.ns = (int)ns;
+  a.nc = (int)nc;
+  a.a0 = (int)a0;
+  a.inv_width = (float)(1.0 / width);
+  for (int k = 0; k < kRMaxBasis; ++k) a.centers[k] = k < nb ? centers_host[k] : 0.f;
+  for (int m = 0; m < kRNC; ++m) {
+    a.tile_n[m] = m < nc ? tile_n[m] : 0;
+    a.tile_col[m] = m < nc ? tile_col[m] : 0;
+  }
+  return GM_OK;
+}
+
+}  // namespace
+}  // namespace gm
+
+extern "C" int64_t gm_conv_radial_partial_row(void) { return gm::kRPart; }
+
+extern "C" int gm_conv_radial_forward_f32(const float* v, const float* rf, const float* w1, const float* b1,
+                                          const float* centers, int64_t nb, double width, const float* transport,
+                                          const float* angular, const float* rho, const float* weights,
+                                          const int64_t* row_ptr, const int64_t* source, int64_t n_nodes,
+                                          int64_t n_edges, int64_t D, int64_t orders, int64_t a0, int64_t ns,
+                                          int64_t nc, const int32_t* tile_n, const int32_t* tile_col, float* out,
+                                          void* stream) {
+  gm::RadialConvArgs a;
+  const int status = gm::prepare(a, v, rf, nullptr, w1, b1, centers, nb, width, transport, angular, rho, weights,
+                                 row_ptr, source, n_nodes, n_edges, D, orders, a0, ns, nc, tile_n, tile_col);
+  if (status != GM_OK) return status;
+  if (n_nodes == 0) return GM_OK;
+  GM_REQUIRE(out, "out must be a device pointer");
+  a.out = out;
+  const dim3 grid((unsigned)((n_nodes + gm::kRWaves - 1) / gm::kRWaves));
+  hipStream_t s = (hipStream_t)stream;
+  if (nb == 4)
+    hipLaunchKernelGGL(gm::conv_radial_forward_kernel<4>, grid, dim3(gm::kRThreads), 0, s, a);
+  else if (nb == 6)
+    hipLaunchKernelGGL(gm::conv_radial_forward_kernel<6>, grid, dim3(gm::kRThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(gm::conv_radial_forward_kernel<8>, grid, dim3(gm::kRThreads), 0, s, a);
+  return gm::check_launch("conv_radial_forward");
+}
+
+extern "C" int gm_conv_radial_backward_f32(const float* g, const float* v, const float* rf, const float* rb,
+                                           const float* w1, const float* b1, const float* centers, int64_t nb,
+                                           double width, const float* transport, const float* angular,
+                                           const float* rho, const float* weights, const int64_t* src_ptr,
+                                           const int64_t* src_order, const int64_t* target, int64_t n_nodes,
+                                           int64_t n_edges, int64_t D, int64_t orders, int64_t a0, int64_t ns,
+                                           int64_t nc, const int32_t* tile_n, const int32_t* tile_col,
+                                           int64_t n_blocks, float* partial, float* dv, float* grad, void* stream) {
+  gm::RadialConvArgs a;
+  const int status = gm::prepare(a, v, rf, rb, w1, b1, centers, nb, width, transport, angular, rho, weights, src_ptr,
+                                 src_order, n_nodes, n_edges, D, orders, a0, ns, nc, tile_n, tile_col);
+  if (status != GM_OK) return status;
+  GM_REQUIRE(n_blocks >= 1 && n_blocks <= 65536, "n_blocks must be in 1..65536");
+  GM_REQUIRE(grad && partial, "grad and partial must be device pointers");
+  if (n_nodes > 0) GM_REQUIRE(g && dv && rb && src_ptr, "g, dv, rb and src_ptr must be device pointers");
+  if (n_edges > 0) GM_REQUIRE(src_order && target, "src_order and target must be device pointers");
+  a.g = g;
+  a.dv = dv;
+  a.src_ptr = src_ptr;
+  a.src_order = src_order;
+  a.target = target;
+  a.partial = partial;
+  a.row_ptr = nullptr;
+  a.source = nullptr;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)n_blocks);
+  if (nb == 4)
+    hipLaunchKernelGGL(gm::conv_radial_backward_kernel<4>, grid, dim3(gm::kRThreads), 0, s, a);
+  else if (nb == 6)
+    hipLaunchKernelGGL(gm::conv_radial_backward_kernel<6>, grid, dim3(gm::kRThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(gm::conv_radial_backward_kernel<8>, grid, dim3(gm::kRThreads), 0, s, a);
+  int st = gm::check_launch("conv_radial_backward");
+  if (st != GM_OK) return st;
+  hipLaunchKernelGGL(gm::conv_radial_reduce_kernel, dim3((gm::kRPart + 255) / 256), dim3(256), 0, s, partial,
+                     n_blocks * (int64_t)gm::kRWaves, grad);
+  return gm::check_launch("conv_radial_reduce");
+}

@@ -8,7 +8,9 @@ Restates the reference's ``nn/convolution.py``:
   (``normalize``), an optional pointwise self-intertwiner added after the sum,
   and ``forward_chunked`` over target ranges holding whole neighbourhoods.
   ``depthwise=True`` takes :class:`~gm_attention_amd.nn.depthwise.SO2DepthwiseKernel`
-  through the fused depthwise op (reference ``_aggregate_fused``, :432-441);
+  through the fused depthwise op (reference ``_aggregate_fused``, :432-441),
+  with the radial heads evaluated inside the walk where the kernel allows
+  (``depthwise_radial``);
   the general kernel runs in the factored order through the fused factored
   aggregate (:310-330), with the window weights as the aggregation weights.
 
@@ -27,7 +29,7 @@ import torch.utils.checkpoint
 from torch import Tensor, nn
 
 from gm_attention_amd.discretization.discretization import SphericalDiscretization
-from gm_attention_amd.nn import fused_attention, fused_factored, kernels
+from gm_attention_amd.nn import depthwise_radial, fused_attention, fused_factored, kernels
 from gm_attention_amd.nn.attention import gather_to_edges, weighted_segment_sum
 from gm_attention_amd.nn.depthwise import SO2DepthwiseKernel, stacked_coefficients
 from gm_attention_amd.nn.kernels import SO2SteerableKernel
@@ -113,10 +115,16 @@ class SO2Convolution(nn.Module):
         return kernel.forward_factored_aggregated(x, edges, weights, products, groups).coefficients
 
     def _aggregate_fused(self, x: SO2FeatureField, edges) -> dict[int, Tensor]:
-        """The depthwise aggregation as one fused op per direction, on the
-        coefficients the radial heads give per edge (torch products)."""
+        """The depthwise aggregation as one fused op per direction: the radial
+        heads evaluated inside the walk where the kernel is eligible
+        (``depthwise_radial``), else on the coefficients the heads give per
+        edge by torch products (the reference's split)."""
         kernel = self.kernel
         assert isinstance(kernel, SO2DepthwiseKernel)
+        kernel.validate_edges(edges)
+        if depthwise_radial.eligible(kernel, x, edges):
+            flat = depthwise_radial.forward(self, x.to_flat(), edges)
+            return SO2FeatureField.from_flat(self.field_type_out, flat).coefficients
         rc, cc = stacked_coefficients([kernel], edges)
         flat = fused_attention.forward_depthwise(self, x.to_flat(), rc, cc, edges)
         return SO2FeatureField.from_flat(self.field_type_out, flat).coefficients

@@ -121,3 +121,48 @@ def test_gauge_equivariance_under_random_frame_rotations(depthwise, cuda):
     expected = y.gauge_transform(theta.to(cuda))
     torch.testing.assert_close(y_turned.to_flat(), expected.to_flat(), rtol=1e-9, atol=1e-9)
     assert float((y.to_flat() - expected.to_flat()).abs().max()) > 1e-3
+
+
+RADIAL_CASES = [
+    ({0: 32, 1: 32, 2: 32}, "hard", False, "none", 2, 4),
+    ({0: 4, 1: 4, 2: 4}, "quartic", True, "linear", 1, 8),
+    ({0: 8, 2: 4}, "hard", False, "none", 1, 6),
+    ({1: 8}, "quartic", False, "none", 1, 4),
+    ({0: 20, 1: 12, 2: 28}, "hard", True, "none", 1, 8),
+]
+
+
+@pytest.mark.parametrize("case", RADIAL_CASES)
+def test_radial_walk_matches_the_oracle(case, cuda):
+    """The depthwise layer with its radial heads evaluated in the walk
+    (depthwise_radial), float32, against the oracle, every gradient."""
+    from gm_attention_amd.nn import depthwise_radial
+
+    field, window, normalize, self_interaction, batch, n_basis = case
+    print(f"radial conv {case}", flush=True)
+    conv, x, edges = build(field, True, window, normalize, self_interaction, batch, n_basis=n_basis)
+    probe = problems.normal(x.shape, 7)
+    conv.load_state_dict({k: v.float().double() for k, v in conv.state_dict().items()})
+    x = x.float().double()
+    edges_o = edges.to(None, torch.float32).to(None, torch.float64)
+    want = run(conv, x, edges_o, probe, oracle=True, tolerance=1e-5)
+    gpu = SO2Convolution(conv.field_type_in, conv.field_type_out, cutoff=conv.cutoff, window=window, depthwise=True,
+                         normalize=normalize, self_interaction=self_interaction, n_radial_basis=n_basis,
+                         dtype=torch.float32, device=cuda)
+    gpu.load_state_dict({k: v.float() for k, v in conv.state_dict().items()})
+    e = edges.to(cuda, torch.float32)
+    assert depthwise_radial.eligible(gpu.kernel, SO2FeatureField.from_flat(gpu.field_type_in, x.to(cuda).float()), e)
+    got = run(gpu, x.to(cuda, torch.float32), e, probe)
+    close(got[0], want[0], torch.float32, "out")
+    close(got[1], want[1], torch.float32, "dx")
+    assert set(got[2]) == set(want[2])
+    for n in want[2]:
+        close(got[2][n], want[2][n], torch.float32, f"d{n}", reduction=True)
+
+
+def test_split_depthwise_path_matches_the_oracle(cuda, monkeypatch):
+    """The reference's split (torch readout, then the walk) with the in-walk radial heads switched off."""
+    from gm_attention_amd.nn import depthwise_radial
+
+    monkeypatch.setattr(depthwise_radial, "ENABLED", False)
+    test_convolution_matches_the_oracle(CASES[0], torch.float32, cuda)
