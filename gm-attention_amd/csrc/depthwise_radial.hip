@@ -52,7 +52,8 @@ constexpr int kRPart = kRPartDR + kRPartDB + kRPartW1;
 
 struct RadialConvArgs {
   const float* v;          // (N, D)
-  const float* rf;         // (kRNT, 5, 64): A operand of the coefficient product
+  const float* rf;         // (kRNT, 4, 64): A operand of the coefficient product
+  const float* rbias;      // (kRNT * 16,): the readout's bias column
   const float* rb;         // (kRNT, 4, 64): A operand of dh~ = R^T dC
   const float* w1;         // (16, NB)
   const float* b1;         // (16,) or null
@@ -68,7 +69,6 @@ struct RadialConvArgs {
   const int64_t* target;
   float* out;      // (N, D)
   float* dv;       // (N, D)
-  float* partial;  // (n_waves, kRPart)
   int64_t n_nodes;
   int D, orders, ns, nc, a0;
   float inv_width;
@@ -140,8 +140,10 @@ __device__ __forceinline__ void trunk_of(const RadialConvArgs& a, const float* w
   }
 }
 
-__device__ __forceinline__ void load_tables(const RadialConvArgs& a, float* rf_s, float* rb_s, float* w1s, int nb) {
-  for (int i = threadIdx.x; i < kRNT * 5 * 64; i += kRThreads) rf_s[i] = a.rf[i];
+__device__ __forceinline__ void load_tables(const RadialConvArgs& a, float* rf_s, float* rb_s, float* bias_s, float* w1s,
+                                            int nb) {
+  for (int i = threadIdx.x; i < kRNT * 4 * 64; i += kRThreads) rf_s[i] = a.rf[i];
+  for (int i = threadIdx.x; i < kRNT * 16; i += kRThreads) bias_s[i] = a.rbias[i];
   if (rb_s)
     for (int i = threadIdx.x; i < kRNT * 4 * 64; i += kRThreads) rb_s[i] = a.rb[i];
   for (int i = threadIdx.x; i < 16 * kRMaxBasis; i += kRThreads) {
@@ -151,11 +153,23 @@ __device__ __forceinline__ void load_tables(const RadialConvArgs& a, float* rf_s
   if (threadIdx.x < 16) w1s[16 * kRMaxBasis + threadIdx.x] = a.b1 ? a.b1[threadIdx.x] : 0.f;
 }
 
+// The lane's rows 4q..4q+3 of coefficient tile m for its edge, times the
+// edge's weight: w (R_m h~) = w bias + R_m (w h) over the four k-steps k = 4q + s.
+__device__ __forceinline__ floatx4 coefficients(const float* rf_s, const float* bias_s, int m, int lane, int q, float w,
+                                                const float (&bv)[4]) {
+  const float4 b = *reinterpret_cast<const float4*>(bias_s + m * 16 + 4 * q);
+  floatx4 d = floatx4{w * b.x, w * b.y, w * b.z, w * b.w};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) d = mfma16(rf_s[(m * 4 + s) * 64 + lane], bv[s], d);
+  return d;
+}
+
 template <int NB>
 __global__ __launch_bounds__(kRThreads) void conv_radial_forward_kernel(RadialConvArgs a) {
-  __shared__ float rf_s[kRNT * 5 * 64];
+  __shared__ float rf_s[kRNT * 4 * 64];
+  __shared__ __attribute__((aligned(16))) float bias_s[kRNT * 16];
   __shared__ float w1s[16 * kRMaxBasis + 16];
-  load_tables(a, rf_s, nullptr, w1s, NB);
+  load_tables(a, rf_s, nullptr, bias_s, w1s, NB);
   __syncthreads();
   const int lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4;
   const int64_t i = xcd_block(blockIdx.x, gridDim.x) * kRWaves + (threadIdx.x >> 6);
@@ -172,17 +186,14 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_forward_kernel(RadialCo
     const EdgeView ev = edge_view(a, e, a.source[e], live);
     float bas[NB], pre[4], h[4];
     trunk_of<NB>(a, w1s, ev.r, q, bas, pre, h);
-    float bv[5];
+    float bv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) bv[u] = ev.w * h[u];
-    bv[4] = q == 0 ? ev.w : 0.f;
     const float* vj = a.v + ev.node * a.D;
 #pragma unroll
     for (int m = 0; m < kRNS; ++m) {
       if (m < a.ns) {
-      floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 5; ++s) d = mfma16(rf_s[(m * 5 + s) * 64 + lane], bv[s], d);
+      const floatx4 d = coefficients(rf_s, bias_s, m, lane, q, ev.w, bv);
       const int col = 16 * m + 4 * q;
       if (col < a.a0) {
         const float4 x = *reinterpret_cast<const float4*>(vj + col);
@@ -196,9 +207,7 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_forward_kernel(RadialCo
 #pragma unroll
     for (int m = 0; m < kRNC; ++m) {
       if (m < a.nc) {
-      floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 5; ++s) d = mfma16(rf_s[((kRNS + m) * 5 + s) * 64 + lane], bv[s], d);
+      const floatx4 d = coefficients(rf_s, bias_s, kRNS + m, lane, q, ev.w, bv);
       const bool one = a.tile_n[m] == 1;
       const float2 x = ld2(vj + a.tile_col[m] + 2 * q);
       const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
@@ -257,23 +266,30 @@ __device__ __forceinline__ void tile_gradients(const float* rb_s, float* T, int 
   }
 }
 
-template <int NB>
-__global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialConvArgs a) {
-  __shared__ float rf_s[kRNT * 5 * 64];
+// The backward over the coefficient tiles [T0, T1) (slots: scalar tiles
+// 0..kRNS-1, then the complex tiles).  Each group of tiles is one launch with
+// its own accumulators, so a wave holds dR, the bias column and dv for its
+// tiles only; the per-edge work (loads, trunk, h~ transpose) is repeated per
+// group, and the trunk's gradient, linear in dh~, is each group's share.
+template <int NB, int T0, int T1>
+__global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialConvArgs a, float* partial) {
+  constexpr int G = T1 - T0;
+  __shared__ float rf_s[kRNT * 4 * 64];
   __shared__ float rb_s[kRNT * 4 * 64];
+  __shared__ __attribute__((aligned(16))) float bias_s[kRNT * 16];
   __shared__ float w1s[16 * kRMaxBasis + 16];
   __shared__ __attribute__((aligned(16))) float tr_s[kRWaves][256];
-  load_tables(a, rf_s, rb_s, w1s, NB);
+  load_tables(a, rf_s, rb_s, bias_s, w1s, NB);
   __syncthreads();
   const int lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4, wave = threadIdx.x >> 6;
   float* T = tr_s[wave];
   const int64_t gw = (int64_t)blockIdx.x * kRWaves + wave, nw = (int64_t)gridDim.x * kRWaves;
-  floatx4 dr[kRNT];
-  float db[kRNT];
+  floatx4 dr[G];
+  float db[G];
 #pragma unroll
-  for (int m = 0; m < kRNT; ++m) {
-    dr[m] = floatx4{0.f, 0.f, 0.f, 0.f};
-    db[m] = 0.f;
+  for (int i = 0; i < G; ++i) {
+    dr[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    db[i] = 0.f;
   }
   float dw1[4][NB], db1[4];
 #pragma unroll
@@ -283,11 +299,9 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
     for (int k = 0; k < NB; ++k) dw1[u][k] = 0.f;
   }
   for (int64_t j = gw; j < a.n_nodes; j += nw) {
-    float dvs[kRNS][4], dvc[kRNC][2];
+    float dvx[G][4];  // scalar tiles use four, complex tiles two
 #pragma unroll
-    for (int m = 0; m < kRNS; ++m) dvs[m][0] = dvs[m][1] = dvs[m][2] = dvs[m][3] = 0.f;
-#pragma unroll
-    for (int m = 0; m < kRNC; ++m) dvc[m][0] = dvc[m][1] = 0.f;
+    for (int i = 0; i < G; ++i) dvx[i][0] = dvx[i][1] = dvx[i][2] = dvx[i][3] = 0.f;
     const float* vj = a.v + j * a.D;
     const int64_t g0 = a.src_ptr[j], g1 = a.src_ptr[j + 1];
     for (int64_t base = g0; base < g1; base += 16) {
@@ -296,10 +310,9 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
       const EdgeView ev = edge_view(a, e, a.target[e], live);
       float bas[NB], pre[4], h[4];
       trunk_of<NB>(a, w1s, ev.r, q, bas, pre, h);
-      float bv[5];
+      float bv[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) bv[u] = ev.w * h[u];
-      bv[4] = q == 0 ? ev.w : 0.f;
       // h~^T for dR's B operand: ht[s] = h_c(edge 4s + q)
       wave_sync();
       *reinterpret_cast<float4*>(T + c * 16 + 4 * q) = make_float4(h[0], h[1], h[2], h[3]);
@@ -310,57 +323,53 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
       const float* gt = a.g + ev.node * a.D;
       floatx4 dh[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int m = 0; m < kRNS; ++m) {
-        if (m < a.ns) {
-        floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 5; ++s) d = mfma16(rf_s[(m * 5 + s) * 64 + lane], bv[s], d);
-        const int col = 16 * m + 4 * q;
-        float dc[4] = {0.f, 0.f, 0.f, 0.f};
-        if (col < a.a0) {
-          const float4 x = *reinterpret_cast<const float4*>(vj + col);
-          const float4 gv = *reinterpret_cast<const float4*>(gt + col);
-          dvs[m][0] = fmaf(d[0], gv.x, dvs[m][0]);
-          dvs[m][1] = fmaf(d[1], gv.y, dvs[m][1]);
-          dvs[m][2] = fmaf(d[2], gv.z, dvs[m][2]);
-          dvs[m][3] = fmaf(d[3], gv.w, dvs[m][3]);
-          dc[0] = ev.w * gv.x * x.x;
-          dc[1] = ev.w * gv.y * x.y;
-          dc[2] = ev.w * gv.z * x.z;
-          dc[3] = ev.w * gv.w * x.w;
-        }
-        tile_gradients(rb_s, T, m, lane, c, q, dc, ht, dh[m & 1], dr[m], db[m]);
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < kRNC; ++m) {
-        if (m < a.nc) {
-        floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 5; ++s) d = mfma16(rf_s[((kRNS + m) * 5 + s) * 64 + lane], bv[s], d);
-        const bool one = a.tile_n[m] == 1;
-        const int col = a.tile_col[m] + 2 * q;
-        const float2 x = ld2(vj + col), gv = ld2(gt + col);
-        const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
-        const float pr = one ? ev.p1.x : ev.p2.x, pi = one ? ev.p1.y : ev.p2.y;
-        const float zr = tc * x.x - ts * x.y, zi = tc * x.y + ts * x.x;
-        // dz = conj(wA) g + p (wB) conj(g);  dv += conj(tau) dz
-        const float bgr = d[2] * gv.x + d[3] * gv.y, bgi = d[3] * gv.x - d[2] * gv.y;
-        const float dzr = (d[0] * gv.x + d[1] * gv.y) + (pr * bgr - pi * bgi);
-        const float dzi = (d[0] * gv.y - d[1] * gv.x) + (pr * bgi + pi * bgr);
-        dvc[m][0] += tc * dzr + ts * dzi;
-        dvc[m][1] += tc * dzi - ts * dzr;
-        // dA = w g conj(z);  dB = w (g conj(p)) z
-        const float xr = gv.x * pr + gv.y * pi, xi = gv.y * pr - gv.x * pi;
-        float dc[4];
-        dc[0] = ev.w * (gv.x * zr + gv.y * zi);
-        dc[1] = ev.w * (gv.y * zr - gv.x * zi);
-        dc[2] = ev.w * (xr * zr - xi * zi);
-        dc[3] = ev.w * (xr * zi + xi * zr);
-        tile_gradients(rb_s, T, kRNS + m, lane, c, q, dc, ht, dh[m & 1], dr[kRNS + m], db[kRNS + m]);
+      for (int i = 0; i < G; ++i) {
+        const int m = T0 + i;
+        if (m < kRNS) {
+          if (m < a.ns) {
+            const floatx4 d = coefficients(rf_s, bias_s, m, lane, q, ev.w, bv);
+            const int col = 16 * m + 4 * q;
+            float dc[4] = {0.f, 0.f, 0.f, 0.f};
+            if (col < a.a0) {
+              const float4 x = *reinterpret_cast<const float4*>(vj + col);
+              const float4 gv = *reinterpret_cast<const float4*>(gt + col);
+              dvx[i][0] = fmaf(d[0], gv.x, dvx[i][0]);
+              dvx[i][1] = fmaf(d[1], gv.y, dvx[i][1]);
+              dvx[i][2] = fmaf(d[2], gv.z, dvx[i][2]);
+              dvx[i][3] = fmaf(d[3], gv.w, dvx[i][3]);
+              dc[0] = ev.w * gv.x * x.x;
+              dc[1] = ev.w * gv.y * x.y;
+              dc[2] = ev.w * gv.z * x.z;
+              dc[3] = ev.w * gv.w * x.w;
+            }
+            tile_gradients(rb_s, T, m, lane, c, q, dc, ht, dh[i & 1], dr[i], db[i]);
+          }
+        } else if (m - kRNS < a.nc) {
+          const int mc = m - kRNS;
+          const floatx4 d = coefficients(rf_s, bias_s, m, lane, q, ev.w, bv);
+          const bool one = a.tile_n[mc] == 1;
+          const int col = a.tile_col[mc] + 2 * q;
+          const float2 x = ld2(vj + col), gv = ld2(gt + col);
+          const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
+          const float pr = one ? ev.p1.x : ev.p2.x, pi = one ? ev.p1.y : ev.p2.y;
+          const float zr = tc * x.x - ts * x.y, zi = tc * x.y + ts * x.x;
+          // dz = conj(wA) g + p (wB) conj(g);  dv += conj(tau) dz
+          const float bgr = d[2] * gv.x + d[3] * gv.y, bgi = d[3] * gv.x - d[2] * gv.y;
+          const float dzr = (d[0] * gv.x + d[1] * gv.y) + (pr * bgr - pi * bgi);
+          const float dzi = (d[0] * gv.y - d[1] * gv.x) + (pr * bgi + pi * bgr);
+          dvx[i][0] += tc * dzr + ts * dzi;
+          dvx[i][1] += tc * dzi - ts * dzr;
+          // dA = w g conj(z);  dB = w (g conj(p)) z
+          const float xr = gv.x * pr + gv.y * pi, xi = gv.y * pr - gv.x * pi;
+          float dc[4];
+          dc[0] = ev.w * (gv.x * zr + gv.y * zi);
+          dc[1] = ev.w * (gv.y * zr - gv.x * zi);
+          dc[2] = ev.w * (xr * zr - xi * zi);
+          dc[3] = ev.w * (xr * zi + xi * zr);
+          tile_gradients(rb_s, T, m, lane, c, q, dc, ht, dh[i & 1], dr[i], db[i]);
         }
       }
-      // the trunk's backward for the lane's features 4q + u of its edge
+      // the trunk's backward for the lane's features 4q + u of its edge (this group's share of dh~)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float sg = frcp(1.f + fexp(-pre[u]));
@@ -370,43 +379,45 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
         for (int k = 0; k < NB; ++k) dw1[u][k] = fmaf(dp, bas[k], dw1[u][k]);
       }
     }
-    // dv_j: each copy summed over the 16 edge lanes of its row
+    // dv_j for this group's copies: each summed over the 16 edge lanes of its row
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
+    for (int off = 1; off < 16; off <<= 1)
 #pragma unroll
-      for (int m = 0; m < kRNS; ++m)
+      for (int i = 0; i < G; ++i)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) dvs[m][u] += __shfl_xor(dvs[m][u], off, kWave);
-#pragma unroll
-      for (int m = 0; m < kRNC; ++m) {
-        dvc[m][0] += __shfl_xor(dvc[m][0], off, kWave);
-        dvc[m][1] += __shfl_xor(dvc[m][1], off, kWave);
-      }
-    }
+        for (int u = 0; u < ((T0 + i) < kRNS ? 4 : 2); ++u) dvx[i][u] += __shfl_xor(dvx[i][u], off, kWave);
     if (c == 0) {
       float* dvj = a.dv + j * a.D;
 #pragma unroll
-      for (int m = 0; m < kRNS; ++m) {
-        const int col = 16 * m + 4 * q;
-        if (m < a.ns && col < a.a0)
-          *reinterpret_cast<float4*>(dvj + col) = make_float4(dvs[m][0], dvs[m][1], dvs[m][2], dvs[m][3]);
+      for (int i = 0; i < G; ++i) {
+        const int m = T0 + i;
+        if (m < kRNS) {
+          const int col = 16 * m + 4 * q;
+          if (m < a.ns && col < a.a0)
+            *reinterpret_cast<float4*>(dvj + col) = make_float4(dvx[i][0], dvx[i][1], dvx[i][2], dvx[i][3]);
+        } else if (m - kRNS < a.nc) {
+          *reinterpret_cast<float2*>(dvj + a.tile_col[m - kRNS] + 2 * q) = make_float2(dvx[i][0], dvx[i][1]);
+        }
       }
-#pragma unroll
-      for (int m = 0; m < kRNC; ++m)
-        if (m < a.nc) *reinterpret_cast<float2*>(dvj + a.tile_col[m] + 2 * q) = make_float2(dvc[m][0], dvc[m][1]);
     }
   }
-  // this wave's partial row: dR in lane layout, the bias column, W1 and b1
-  float* part = a.partial + gw * kRPart;
-#pragma unroll
-  for (int m = 0; m < kRNT; ++m)
-    *reinterpret_cast<float4*>(part + m * 256 + lane * 4) = make_float4(dr[m][0], dr[m][1], dr[m][2], dr[m][3]);
+  // this wave's partial row: dR in lane layout and the bias column for its tiles (zero for
+  // the other groups' tiles), its share of W1 and b1
+  float* part = partial + gw * kRPart;
 #pragma unroll
   for (int m = 0; m < kRNT; ++m) {
-    float v = db[m];
-    v += __shfl_xor(v, 16, kWave);
-    v += __shfl_xor(v, 32, kWave);
-    if (q == 0) part[kRPartDR + m * 16 + c] = v;
+    floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+    float b = 0.f;
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+      if (T0 + i == m) {
+        v = dr[i];
+        b = db[i];
+      }
+    *reinterpret_cast<float4*>(part + m * 256 + lane * 4) = make_float4(v[0], v[1], v[2], v[3]);
+    b += __shfl_xor(b, 16, kWave);
+    b += __shfl_xor(b, 32, kWave);
+    if (q == 0) part[kRPartDR + m * 16 + c] = b;
   }
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -433,7 +444,17 @@ __global__ __launch_bounds__(256) void conv_radial_reduce_kernel(const float* pa
   grad[p] = s;
 }
 
-int prepare(RadialConvArgs& a, const float* v, const float* rf, const float* rb, const float* w1, const float* b1,
+template <int NB>
+void launch_backward_groups(const RadialConvArgs& a, float* partial, int64_t rows, bool second, dim3 grid,
+                            hipStream_t s) {
+  hipLaunchKernelGGL((conv_radial_backward_kernel<NB, 0, 9>), grid, dim3(kRThreads), 0, s, a, partial);
+  if (second)
+    hipLaunchKernelGGL((conv_radial_backward_kernel<NB, 9, kRNT>), grid, dim3(kRThreads), 0, s, a,
+                       partial + rows * kRPart);
+}
+
+int prepare(RadialConvArgs& a, const float* v, const float* rf, const float* rbias, const float* rb, const float* w1,
+            const float* b1,
             const float* centers_host, int64_t nb, double width, const float* transport, const float* angular,
             const float* rho, const float* weights, const int64_t* row_ptr, const int64_t* source, int64_t n_nodes,
             int64_t n_edges, int64_t D, int64_t orders, int64_t a0, int64_t ns, int64_t nc, const int32_t* tile_n,
@@ -454,10 +475,11 @@ int prepare(RadialConvArgs& a, const float* v, const float* rf, const float* rb,
     covered += 8;
   }
   GM_REQUIRE(covered == D, "the tiles must cover the flat width D exactly");
-  if (n_nodes > 0) GM_REQUIRE(v && rf && w1 && row_ptr, "v, the tables and row_ptr must be device pointers");
+  if (n_nodes > 0) GM_REQUIRE(v && rf && rbias && w1 && row_ptr, "v, the tables and row_ptr must be device pointers");
   if (n_edges > 0) GM_REQUIRE(transport && angular && rho && weights && source, "the per-edge tables must be device pointers");
   a.v = v;
   a.rf = rf;
+  a.rbias = rbias;
   a.rb = rb;
   a.w1 = w1;
   a.b1 = b1;
@@ -487,7 +509,8 @@ int prepare(RadialConvArgs& a, const float* v, const float* rf, const float* rb,
 
 extern "C" int64_t gm_conv_radial_partial_row(void) { return gm::kRPart; }
 
-extern "C" int gm_conv_radial_forward_f32(const float* v, const float* rf, const float* w1, const float* b1,
+extern "C" int gm_conv_radial_forward_f32(const float* v, const float* rf, const float* rbias, const float* w1,
+                                          const float* b1,
                                           const float* centers, int64_t nb, double width, const float* transport,
                                           const float* angular, const float* rho, const float* weights,
                                           const int64_t* row_ptr, const int64_t* source, int64_t n_nodes,
@@ -495,7 +518,7 @@ extern "C" int gm_conv_radial_forward_f32(const float* v, const float* rf, const
                                           int64_t nc, const int32_t* tile_n, const int32_t* tile_col, float* out,
                                           void* stream) {
   gm::RadialConvArgs a;
-  const int status = gm::prepare(a, v, rf, nullptr, w1, b1, centers, nb, width, transport, angular, rho, weights,
+  const int status = gm::prepare(a, v, rf, rbias, nullptr, w1, b1, centers, nb, width, transport, angular, rho, weights,
                                  row_ptr, source, n_nodes, n_edges, D, orders, a0, ns, nc, tile_n, tile_col);
   if (status != GM_OK) return status;
   if (n_nodes == 0) return GM_OK;
@@ -512,7 +535,8 @@ extern "C" int gm_conv_radial_forward_f32(const float* v, const float* rf, const
   return gm::check_launch("conv_radial_forward");
 }
 
-extern "C" int gm_conv_radial_backward_f32(const float* g, const float* v, const float* rf, const float* rb,
+extern "C" int gm_conv_radial_backward_f32(const float* g, const float* v, const float* rf, const float* rbias,
+                                           const float* rb,
                                            const float* w1, const float* b1, const float* centers, int64_t nb,
                                            double width, const float* transport, const float* angular,
                                            const float* rho, const float* weights, const int64_t* src_ptr,
@@ -521,7 +545,7 @@ extern "C" int gm_conv_radial_backward_f32(const float* g, const float* v, const
                                            int64_t nc, const int32_t* tile_n, const int32_t* tile_col,
                                            int64_t n_blocks, float* partial, float* dv, float* grad, void* stream) {
   gm::RadialConvArgs a;
-  const int status = gm::prepare(a, v, rf, rb, w1, b1, centers, nb, width, transport, angular, rho, weights, src_ptr,
+  const int status = gm::prepare(a, v, rf, rbias, rb, w1, b1, centers, nb, width, transport, angular, rho, weights, src_ptr,
                                  src_order, n_nodes, n_edges, D, orders, a0, ns, nc, tile_n, tile_col);
   if (status != GM_OK) return status;
   GM_REQUIRE(n_blocks >= 1 && n_blocks <= 65536, "n_blocks must be in 1..65536");
@@ -533,20 +557,23 @@ extern "C" int gm_conv_radial_backward_f32(const float* g, const float* v, const
   a.src_ptr = src_ptr;
   a.src_order = src_order;
   a.target = target;
-  a.partial = partial;
   a.row_ptr = nullptr;
   a.source = nullptr;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)n_blocks);
-  if (nb == 4)
-    hipLaunchKernelGGL(gm::conv_radial_backward_kernel<4>, grid, dim3(gm::kRThreads), 0, s, a);
-  else if (nb == 6)
-    hipLaunchKernelGGL(gm::conv_radial_backward_kernel<6>, grid, dim3(gm::kRThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(gm::conv_radial_backward_kernel<8>, grid, dim3(gm::kRThreads), 0, s, a);
+  // two groups of nine tiles: the scalar tiles and complex tiles 0..6, then complex tiles 7..15
+  const int64_t rows = n_blocks * (int64_t)gm::kRWaves;
+  const bool second = nc > 7;
+  if (nb == 4) {
+    gm::launch_backward_groups<4>(a, partial, rows, second, grid, s);
+  } else if (nb == 6) {
+    gm::launch_backward_groups<6>(a, partial, rows, second, grid, s);
+  } else {
+    gm::launch_backward_groups<8>(a, partial, rows, second, grid, s);
+  }
   int st = gm::check_launch("conv_radial_backward");
   if (st != GM_OK) return st;
   hipLaunchKernelGGL(gm::conv_radial_reduce_kernel, dim3((gm::kRPart + 255) / 256), dim3(256), 0, s, partial,
-                     n_blocks * (int64_t)gm::kRWaves, grad);
+                     rows * (second ? 2 : 1), grad);
   return gm::check_launch("conv_radial_reduce");
 }

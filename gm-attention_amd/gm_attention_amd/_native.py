@@ -61,8 +61,8 @@ SIGNATURES_F32 = {
     "gm_gather_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
     "gm_scatter_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
     "gm_conv_radial_partial_row": (ctypes.c_int64, []),
-    "gm_conv_radial_forward_f32": (ctypes.c_int, [_P] * 5 + [_I, _D] + [_P] * 6 + [_I] * 7 + [_P] * 4),
-    "gm_conv_radial_backward_f32": (ctypes.c_int, [_P] * 7 + [_I, _D] + [_P] * 7 + [_I] * 7 + [_P, _P, _I] + [_P] * 4),
+    "gm_conv_radial_forward_f32": (ctypes.c_int, [_P] * 6 + [_I, _D] + [_P] * 6 + [_I] * 7 + [_P] * 4),
+    "gm_conv_radial_backward_f32": (ctypes.c_int, [_P] * 8 + [_I, _D] + [_P] * 7 + [_I] * 7 + [_P, _P, _I] + [_P] * 4),
 }
 
 
@@ -780,34 +780,34 @@ def pairs() -> PairsExtension:
 RADIAL_TILES_SCALAR, RADIAL_TILES_COMPLEX = 2, 16
 
 
-def conv_radial_forward(v: Tensor, rf: Tensor, w1: Tensor, b1: Tensor | None, centers: list[float], width: float,
+def conv_radial_forward(v: Tensor, rf: Tensor, rbias: Tensor, w1: Tensor, b1: Tensor | None, centers: list[float], width: float,
                         transport: Tensor, angular: Tensor, rho: Tensor, weights: Tensor, row_ptr: Tensor,
                         source: Tensor, a0: int, ns: int, tiles: Tensor) -> Tensor:
     """``out (N, D)``: the depthwise walk with the radial heads evaluated per
     edge from ``rho`` (``gm_conv_radial_forward_f32``).  ``rf`` is the packed
     readout in the kernel's A-operand layout, ``tiles`` a host int32 (2, nc)
     table of the complex tiles' frequencies and first columns."""
-    _require_device(v, rf, w1, transport, angular, rho, weights, row_ptr, source)
+    _require_device(v, rf, rbias, w1, transport, angular, rho, weights, row_ptr, source)
     _check(v.dtype == torch.float32 and v.data_ptr() % 16 == 0, "v must be 16-byte aligned float32")
     out = torch.empty_like(v)
     if v.shape[0] == 0:
         return out
     cen = (ctypes.c_float * 8)(*centers)
-    _call("gm_conv_radial_forward_f32", _ptr(v), _ptr(rf), _ptr(w1), _ptr(b1), ctypes.addressof(cen), len(centers),
+    _call("gm_conv_radial_forward_f32", _ptr(v), _ptr(rf), _ptr(rbias), _ptr(w1), _ptr(b1), ctypes.addressof(cen), len(centers),
           float(width), _ptr(transport), _ptr(angular), _ptr(rho), _ptr(weights), _ptr(row_ptr), _ptr(source),
           v.shape[0], source.shape[0], v.shape[1], transport.shape[1], int(a0), int(ns), tiles.shape[1],
           tiles[0].data_ptr(), tiles[1].data_ptr(), _ptr(out), _stream(v.device))
     return out
 
 
-def conv_radial_backward(g: Tensor, v: Tensor, rf: Tensor, rb: Tensor, w1: Tensor, b1: Tensor | None,
+def conv_radial_backward(g: Tensor, v: Tensor, rf: Tensor, rbias: Tensor, rb: Tensor, w1: Tensor, b1: Tensor | None,
                          centers: list[float], width: float, transport: Tensor, angular: Tensor, rho: Tensor,
                          weights: Tensor, source: Tensor, row_ptr: Tensor, a0: int, ns: int,
                          tiles: Tensor) -> tuple[Tensor, Tensor]:
     """``(dv, grad)``: the input gradient and the parameter-gradient row
     (``gm_conv_radial_partial_row()`` floats: dR in lane layout, its bias
     column, W1, b1), summed over per-wave partial rows in a fixed order."""
-    _require_device(g, v, rf, rb, w1, transport, angular, rho, weights, row_ptr, source)
+    _require_device(g, v, rf, rbias, rb, w1, transport, angular, rho, weights, row_ptr, source)
     _check(g.shape == v.shape and g.dtype == v.dtype and g.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0,
            "g must be shaped and typed as v, both 16-byte aligned")
     src_ptr, src_order, target = source_major(source, row_ptr)
@@ -815,10 +815,11 @@ def conv_radial_backward(g: Tensor, v: Tensor, rf: Tensor, rb: Tensor, w1: Tenso
     dv = torch.empty_like(v)
     row = int(library().gm_conv_radial_partial_row())
     n_blocks = max(1, min(1024, (n + 3) // 4))
-    partial = torch.empty(n_blocks * 4, row, dtype=torch.float32, device=v.device)
+    groups = 2 if tiles.shape[1] > 7 else 1  # the backward's launches over groups of coefficient tiles
+    partial = torch.empty(groups * n_blocks * 4, row, dtype=torch.float32, device=v.device)
     grad = torch.empty(row, dtype=torch.float32, device=v.device)
     cen = (ctypes.c_float * 8)(*centers)
-    _call("gm_conv_radial_backward_f32", _ptr(g), _ptr(v), _ptr(rf), _ptr(rb), _ptr(w1), _ptr(b1),
+    _call("gm_conv_radial_backward_f32", _ptr(g), _ptr(v), _ptr(rf), _ptr(rbias), _ptr(rb), _ptr(w1), _ptr(b1),
           ctypes.addressof(cen), len(centers), float(width), _ptr(transport), _ptr(angular), _ptr(rho),
           _ptr(weights), _ptr(src_ptr), _ptr(src_order), _ptr(target), n, source.shape[0], v.shape[1],
           transport.shape[1], int(a0), int(ns), tiles.shape[1], tiles[0].data_ptr(), tiles[1].data_ptr(), n_blocks,

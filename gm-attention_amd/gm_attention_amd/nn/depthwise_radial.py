@@ -93,14 +93,13 @@ class Packing:
         self.ns = (a0 + 15) // 16
         self.rowmap = torch.tensor(rowmap, dtype=torch.int64, device=device)
         self.tiles = torch.tensor([tile_n, tile_col], dtype=torch.int32).reshape(2, len(tile_n)).contiguous()
-        # the A operands' gathers: rf[m, s, l] = R~[16 m + l % 16, k(s, l // 16)], rb[m, r, l] = R[16 m + 4 (l // 16) + r, l % 16]
+        # the A operands' gathers: rf[m, s, l] = R[16 m + l % 16, 4 (l // 16) + s], rb[m, r, l] = R[16 m + 4 (l // 16) + r, l % 16]
         lanes = torch.arange(64)
         m = torch.arange(NT).view(NT, 1, 1)
-        s = torch.arange(5).view(1, 5, 1)
+        s = torch.arange(4).view(1, 4, 1)
         qq = (lanes // 16).view(1, 1, 64)
-        k = torch.where(s < 4, 4 * qq + s, torch.where(qq == 0, torch.full_like(qq, 16), torch.full_like(qq, 17)))
-        self.rf_rows = (16 * m + (lanes % 16).view(1, 1, 64)).expand(NT, 5, 64).reshape(-1).to(device)
-        self.rf_cols = k.expand(NT, 5, 64).reshape(-1).to(device)
+        self.rf_rows = (16 * m + (lanes % 16).view(1, 1, 64)).expand(NT, 4, 64).reshape(-1).to(device)
+        self.rf_cols = (4 * qq + s).expand(NT, 4, 64).reshape(-1).to(device)
         r = torch.arange(4).view(1, 4, 1)
         self.rb_rows = (16 * m + 4 * qq + r).expand(NT, 4, 64).reshape(-1).to(device)
         self.rb_cols = (lanes % 16).view(1, 1, 64).expand(NT, 4, 64).reshape(-1).to(device)
@@ -141,14 +140,14 @@ class ConvRadial(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, v: Tensor, R: Tensor, w1: Tensor, b1: Tensor | None, meta: dict) -> Tensor:
         p: Packing = meta["packing"]
-        Rx = torch.cat([R, R.new_zeros(R.shape[0], 1)], dim=1)
-        rf = Rx[p.rf_rows, p.rf_cols].contiguous()
+        rf = R[p.rf_rows, p.rf_cols].contiguous()
+        rbias = R[:, 16].contiguous()
         g = meta["geometry"]
         with torch.profiler.record_function("gm::conv/radial_fused"):
-            out = _native.conv_radial_forward(v, rf, w1.contiguous(), None if b1 is None else b1.contiguous(),
+            out = _native.conv_radial_forward(v, rf, rbias, w1.contiguous(), None if b1 is None else b1.contiguous(),
                                               meta["centers"], meta["width"], g.transport, g.angular, g.rho,
                                               meta["weights"], g.row_ptr, g.source, p.a0, p.ns, p.tiles)
-        ctx.save_for_backward(v, R, w1, b1 if b1 is not None else torch.empty(0, device=v.device), rf)
+        ctx.save_for_backward(v, R, w1, b1 if b1 is not None else torch.empty(0, device=v.device), rf, rbias)
         ctx.meta = meta
         ctx.has_b1 = b1 is not None
         return out
@@ -156,13 +155,13 @@ class ConvRadial(torch.autograd.Function):
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad: Tensor) -> tuple:
-        v, R, w1, b1, rf = ctx.saved_tensors
+        v, R, w1, b1, rf, rbias = ctx.saved_tensors
         meta = ctx.meta
         p: Packing = meta["packing"]
         g = meta["geometry"]
         rb = R[p.rb_rows, p.rb_cols].contiguous()
         with torch.profiler.record_function("gm::conv/radial_fused_backward"):
-            dv, flat = _native.conv_radial_backward(grad.contiguous(), v, rf, rb, w1.contiguous(),
+            dv, flat = _native.conv_radial_backward(grad.contiguous(), v, rf, rbias, rb, w1.contiguous(),
                                                     b1.contiguous() if ctx.has_b1 else None, meta["centers"],
                                                     meta["width"], g.transport, g.angular, g.rho, meta["weights"],
                                                     g.source, g.row_ptr, p.a0, p.ns, p.tiles)
