@@ -44,6 +44,7 @@ constexpr int kRNT = kRNS + kRNC;  // coefficient tiles
 constexpr int kRWaves = 4;         // waves per workgroup
 constexpr int kRThreads = kRWaves * kWave;
 constexpr int kRMaxBasis = 8;
+constexpr int kRChunk = 1;         // backward: coefficient tiles per LDS hand-over
 // per-wave partial row of the backward: dR in lane layout, the bias column, W1 and b1
 constexpr int kRPartDR = kRNT * 256;
 constexpr int kRPartDB = kRNT * 16;
@@ -180,10 +181,19 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_forward_kernel(RadialCo
 #pragma unroll
   for (int m = 0; m < kRNC; ++m) accc[m][0] = accc[m][1] = 0.f;
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+  // the next tile's edge rows and sources are requested while this tile computes
+  EdgeView nxt;
+  if (e0 < e1) {
+    const int64_t e = e0 + c < e1 ? e0 + c : e0;
+    nxt = edge_view(a, e, a.source[e], e0 + c < e1);
+  }
   for (int64_t base = e0; base < e1; base += 16) {
-    const bool live = base + c < e1;
-    const int64_t e = live ? base + c : e0;
-    const EdgeView ev = edge_view(a, e, a.source[e], live);
+    const EdgeView ev = nxt;
+    if (base + 16 < e1) {
+      const bool live = base + 16 + c < e1;
+      const int64_t e = live ? base + 16 + c : e0;
+      nxt = edge_view(a, e, a.source[e], live);
+    }
     float bas[NB], pre[4], h[4];
     trunk_of<NB>(a, w1s, ev.r, q, bas, pre, h);
     float bv[4];
@@ -245,25 +255,54 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_forward_kernel(RadialCo
     if (m < a.nc) *reinterpret_cast<float2*>(oi + a.tile_col[m] + 2 * q) = make_float2(accc[m][0], accc[m][1]);
 }
 
-// dC's rows for the lane's edge (D layout) through the wave's LDS tile into
-// the A-operand layout dC[row c][edge 4s + q], then the bias column sums and
-// dR += dC h~^T; and dh~ += R^T dC straight from the D layout.
-__device__ __forceinline__ void tile_gradients(const float* rb_s, float* T, int m, int lane, int c, int q,
-                                               const float (&dc)[4], const float (&ht)[4], floatx4& dh,
-                                               floatx4& dr, float& db) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) dh = mfma16(rb_s[(m * 4 + r) * 64 + lane], dc[r], dh);
-  wave_sync();
-  *reinterpret_cast<float4*>(T + c * 16 + 4 * q) = make_float4(dc[0], dc[1], dc[2], dc[3]);
-  wave_sync();
-  float at[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) at[s] = T[(4 * s + q) * 16 + c];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    db += at[s];
-    dr = mfma16(at[s], ht[s], dr);
+// Whether coefficient tile slot m holds copies (uniform).
+__device__ __forceinline__ bool tile_live(const RadialConvArgs& a, int m) {
+  return m < kRNS ? m < a.ns : m - kRNS < a.nc;
+}
+
+// The backward of one coefficient tile for the lane's edge: the coefficients
+// again (times w), the copy's value gradient into dv, and the coefficients'
+// gradient dC (rows 4q..4q+3, D layout).
+__device__ __forceinline__ void tile_dc(const RadialConvArgs& a, const float* rf_s, const float* bias_s, int m,
+                                        int lane, int q, const EdgeView& ev, const float (&bv)[4], const float* vj,
+                                        const float* gt, float (&dv)[4], float (&dc)[4]) {
+  const floatx4 d = coefficients(rf_s, bias_s, m, lane, q, ev.w, bv);
+  if (m < kRNS) {
+    const int col = 16 * m + 4 * q;
+    dc[0] = dc[1] = dc[2] = dc[3] = 0.f;
+    if (col < a.a0) {
+      const float4 x = *reinterpret_cast<const float4*>(vj + col);
+      const float4 gv = *reinterpret_cast<const float4*>(gt + col);
+      dv[0] = fmaf(d[0], gv.x, dv[0]);
+      dv[1] = fmaf(d[1], gv.y, dv[1]);
+      dv[2] = fmaf(d[2], gv.z, dv[2]);
+      dv[3] = fmaf(d[3], gv.w, dv[3]);
+      dc[0] = ev.w * gv.x * x.x;
+      dc[1] = ev.w * gv.y * x.y;
+      dc[2] = ev.w * gv.z * x.z;
+      dc[3] = ev.w * gv.w * x.w;
+    }
+    return;
   }
+  const int mc = m - kRNS;
+  const bool one = a.tile_n[mc] == 1;
+  const int col = a.tile_col[mc] + 2 * q;
+  const float2 x = ld2(vj + col), gv = ld2(gt + col);
+  const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
+  const float pr = one ? ev.p1.x : ev.p2.x, pi = one ? ev.p1.y : ev.p2.y;
+  const float zr = tc * x.x - ts * x.y, zi = tc * x.y + ts * x.x;
+  // dz = conj(wA) g + p (wB) conj(g);  dv += conj(tau) dz
+  const float bgr = d[2] * gv.x + d[3] * gv.y, bgi = d[3] * gv.x - d[2] * gv.y;
+  const float dzr = (d[0] * gv.x + d[1] * gv.y) + (pr * bgr - pi * bgi);
+  const float dzi = (d[0] * gv.y - d[1] * gv.x) + (pr * bgi + pi * bgr);
+  dv[0] += tc * dzr + ts * dzi;
+  dv[1] += tc * dzi - ts * dzr;
+  // dA = w g conj(z);  dB = w (g conj(p)) z
+  const float xr = gv.x * pr + gv.y * pi, xi = gv.y * pr - gv.x * pi;
+  dc[0] = ev.w * (gv.x * zr + gv.y * zi);
+  dc[1] = ev.w * (gv.y * zr - gv.x * zi);
+  dc[2] = ev.w * (xr * zr - xi * zi);
+  dc[3] = ev.w * (xr * zi + xi * zr);
 }
 
 // The backward over the coefficient tiles [T0, T1) (slots: scalar tiles
@@ -278,12 +317,17 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
   __shared__ float rb_s[kRNT * 4 * 64];
   __shared__ __attribute__((aligned(16))) float bias_s[kRNT * 16];
   __shared__ float w1s[16 * kRMaxBasis + 16];
-  __shared__ __attribute__((aligned(16))) float tr_s[kRWaves][256];
+  __shared__ __attribute__((aligned(16))) float tr_s[kRWaves][kRChunk * 256];
   load_tables(a, rf_s, rb_s, bias_s, w1s, NB);
   __syncthreads();
   const int lane = threadIdx.x & 63, c = lane & 15, q = lane >> 4, wave = threadIdx.x >> 6;
   float* T = tr_s[wave];
-  const int64_t gw = (int64_t)blockIdx.x * kRWaves + wave, nw = (int64_t)gridDim.x * kRWaves;
+  const int64_t gw = (int64_t)blockIdx.x * kRWaves + wave;
+  // Workgroups go round-robin to the eight XCDs (gridDim.x is a multiple of 8): XCD x
+  // walks the x-th eighth of the sources, so its waves' targets (rows of g) share its L2.
+  const int64_t xcd = blockIdx.x & 7, nwx = (int64_t)(gridDim.x >> 3) * kRWaves;
+  const int64_t lw = (int64_t)(blockIdx.x >> 3) * kRWaves + wave;
+  const int64_t j_lo = a.n_nodes * xcd / 8, j_hi = a.n_nodes * (xcd + 1) / 8;
   floatx4 dr[G];
   float db[G];
 #pragma unroll
@@ -298,7 +342,7 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
 #pragma unroll
     for (int k = 0; k < NB; ++k) dw1[u][k] = 0.f;
   }
-  for (int64_t j = gw; j < a.n_nodes; j += nw) {
+  for (int64_t j = j_lo + lw; j < j_hi; j += nwx) {
     float dvx[G][4];  // scalar tiles use four, complex tiles two
 #pragma unroll
     for (int i = 0; i < G; ++i) dvx[i][0] = dvx[i][1] = dvx[i][2] = dvx[i][3] = 0.f;
@@ -322,51 +366,43 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
       for (int s = 0; s < 4; ++s) ht[s] = T[(4 * s + q) * 16 + c];
       const float* gt = a.g + ev.node * a.D;
       floatx4 dh[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+      // kRChunk tiles at a time: dC and dh~ += R^T dC from the D layout, then dC through the
+      // wave's LDS into the A-operand layout dC[row c][edge 4s + q] (one hand-over per
+      // chunk), the bias column sums and dR += dC h~^T
 #pragma unroll
-      for (int i = 0; i < G; ++i) {
-        const int m = T0 + i;
-        if (m < kRNS) {
-          if (m < a.ns) {
-            const floatx4 d = coefficients(rf_s, bias_s, m, lane, q, ev.w, bv);
-            const int col = 16 * m + 4 * q;
-            float dc[4] = {0.f, 0.f, 0.f, 0.f};
-            if (col < a.a0) {
-              const float4 x = *reinterpret_cast<const float4*>(vj + col);
-              const float4 gv = *reinterpret_cast<const float4*>(gt + col);
-              dvx[i][0] = fmaf(d[0], gv.x, dvx[i][0]);
-              dvx[i][1] = fmaf(d[1], gv.y, dvx[i][1]);
-              dvx[i][2] = fmaf(d[2], gv.z, dvx[i][2]);
-              dvx[i][3] = fmaf(d[3], gv.w, dvx[i][3]);
-              dc[0] = ev.w * gv.x * x.x;
-              dc[1] = ev.w * gv.y * x.y;
-              dc[2] = ev.w * gv.z * x.z;
-              dc[3] = ev.w * gv.w * x.w;
-            }
-            tile_gradients(rb_s, T, m, lane, c, q, dc, ht, dh[i & 1], dr[i], db[i]);
+      for (int i0 = 0; i0 < G; i0 += kRChunk) {
+        float dcs[kRChunk][4];
+#pragma unroll
+        for (int p = 0; p < kRChunk; ++p) {
+          const int i = i0 + p, m = T0 + i;
+          if (i < G && tile_live(a, m)) {
+            tile_dc(a, rf_s, bias_s, m, lane, q, ev, bv, vj, gt, dvx[i], dcs[p]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dh[i & 1] = mfma16(rb_s[(m * 4 + r) * 64 + lane], dcs[p][r], dh[i & 1]);
           }
-        } else if (m - kRNS < a.nc) {
-          const int mc = m - kRNS;
-          const floatx4 d = coefficients(rf_s, bias_s, m, lane, q, ev.w, bv);
-          const bool one = a.tile_n[mc] == 1;
-          const int col = a.tile_col[mc] + 2 * q;
-          const float2 x = ld2(vj + col), gv = ld2(gt + col);
-          const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
-          const float pr = one ? ev.p1.x : ev.p2.x, pi = one ? ev.p1.y : ev.p2.y;
-          const float zr = tc * x.x - ts * x.y, zi = tc * x.y + ts * x.x;
-          // dz = conj(wA) g + p (wB) conj(g);  dv += conj(tau) dz
-          const float bgr = d[2] * gv.x + d[3] * gv.y, bgi = d[3] * gv.x - d[2] * gv.y;
-          const float dzr = (d[0] * gv.x + d[1] * gv.y) + (pr * bgr - pi * bgi);
-          const float dzi = (d[0] * gv.y - d[1] * gv.x) + (pr * bgi + pi * bgr);
-          dvx[i][0] += tc * dzr + ts * dzi;
-          dvx[i][1] += tc * dzi - ts * dzr;
-          // dA = w g conj(z);  dB = w (g conj(p)) z
-          const float xr = gv.x * pr + gv.y * pi, xi = gv.y * pr - gv.x * pi;
-          float dc[4];
-          dc[0] = ev.w * (gv.x * zr + gv.y * zi);
-          dc[1] = ev.w * (gv.y * zr - gv.x * zi);
-          dc[2] = ev.w * (xr * zr - xi * zi);
-          dc[3] = ev.w * (xr * zi + xi * zr);
-          tile_gradients(rb_s, T, m, lane, c, q, dc, ht, dh[i & 1], dr[i], db[i]);
+        }
+        wave_sync();
+#pragma unroll
+        for (int p = 0; p < kRChunk; ++p) {
+          const int i = i0 + p;
+          if (i < G && tile_live(a, T0 + i))
+            *reinterpret_cast<float4*>(T + p * 256 + c * 16 + 4 * q) =
+                make_float4(dcs[p][0], dcs[p][1], dcs[p][2], dcs[p][3]);
+        }
+        wave_sync();
+#pragma unroll
+        for (int p = 0; p < kRChunk; ++p) {
+          const int i = i0 + p;
+          if (i < G && tile_live(a, T0 + i)) {
+            float at[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) at[s] = T[p * 256 + (4 * s + q) * 16 + c];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              db[i] += at[s];
+              dr[i] = mfma16(at[s], ht[s], dr[i]);
+            }
+          }
         }
       }
       // the trunk's backward for the lane's features 4q + u of its edge (this group's share of dh~)
@@ -444,12 +480,23 @@ __global__ __launch_bounds__(256) void conv_radial_reduce_kernel(const float* pa
   grad[p] = s;
 }
 
+// The backward's tile groups: kRGroup consecutive slots each; a group runs
+// only when it holds a live tile.
+constexpr int kRGroup = 9;
+constexpr int kRGroups = (kRNT + kRGroup - 1) / kRGroup;
+
+int live_groups(int nc) {
+  const int slots = kRNS + nc;
+  return (slots + kRGroup - 1) / kRGroup;
+}
+
 template <int NB>
-void launch_backward_groups(const RadialConvArgs& a, float* partial, int64_t rows, bool second, dim3 grid,
+void launch_backward_groups(const RadialConvArgs& a, float* partial, int64_t rows, int groups, dim3 grid,
                             hipStream_t s) {
-  hipLaunchKernelGGL((conv_radial_backward_kernel<NB, 0, 9>), grid, dim3(kRThreads), 0, s, a, partial);
-  if (second)
-    hipLaunchKernelGGL((conv_radial_backward_kernel<NB, 9, kRNT>), grid, dim3(kRThreads), 0, s, a,
+  static_assert(kRGroups == 2, "two tile groups");
+  hipLaunchKernelGGL((conv_radial_backward_kernel<NB, 0, kRGroup>), grid, dim3(kRThreads), 0, s, a, partial);
+  if (groups > 1)
+    hipLaunchKernelGGL((conv_radial_backward_kernel<NB, kRGroup, kRNT>), grid, dim3(kRThreads), 0, s, a,
                        partial + rows * kRPart);
 }
 
@@ -509,6 +556,8 @@ int prepare(RadialConvArgs& a, const float* v, const float* rf, const float* rbi
 
 extern "C" int64_t gm_conv_radial_partial_row(void) { return gm::kRPart; }
 
+extern "C" int64_t gm_conv_radial_backward_groups(int64_t nc) { return gm::live_groups((int)nc); }
+
 extern "C" int gm_conv_radial_forward_f32(const float* v, const float* rf, const float* rbias, const float* w1,
                                           const float* b1,
                                           const float* centers, int64_t nb, double width, const float* transport,
@@ -548,7 +597,7 @@ extern "C" int gm_conv_radial_backward_f32(const float* g, const float* v, const
   const int status = gm::prepare(a, v, rf, rbias, rb, w1, b1, centers, nb, width, transport, angular, rho, weights, src_ptr,
                                  src_order, n_nodes, n_edges, D, orders, a0, ns, nc, tile_n, tile_col);
   if (status != GM_OK) return status;
-  GM_REQUIRE(n_blocks >= 1 && n_blocks <= 65536, "n_blocks must be in 1..65536");
+  GM_REQUIRE(n_blocks >= 8 && n_blocks <= 65536 && n_blocks % 8 == 0, "n_blocks must be a multiple of 8 in 8..65536");
   GM_REQUIRE(grad && partial, "grad and partial must be device pointers");
   if (n_nodes > 0) GM_REQUIRE(g && dv && rb && src_ptr, "g, dv, rb and src_ptr must be device pointers");
   if (n_edges > 0) GM_REQUIRE(src_order && target, "src_order and target must be device pointers");
@@ -561,19 +610,18 @@ extern "C" int gm_conv_radial_backward_f32(const float* g, const float* v, const
   a.source = nullptr;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)n_blocks);
-  // two groups of nine tiles: the scalar tiles and complex tiles 0..6, then complex tiles 7..15
   const int64_t rows = n_blocks * (int64_t)gm::kRWaves;
-  const bool second = nc > 7;
+  const int groups = gm::live_groups((int)nc);
   if (nb == 4) {
-    gm::launch_backward_groups<4>(a, partial, rows, second, grid, s);
+    gm::launch_backward_groups<4>(a, partial, rows, groups, grid, s);
   } else if (nb == 6) {
-    gm::launch_backward_groups<6>(a, partial, rows, second, grid, s);
+    gm::launch_backward_groups<6>(a, partial, rows, groups, grid, s);
   } else {
-    gm::launch_backward_groups<8>(a, partial, rows, second, grid, s);
+    gm::launch_backward_groups<8>(a, partial, rows, groups, grid, s);
   }
   int st = gm::check_launch("conv_radial_backward");
   if (st != GM_OK) return st;
   hipLaunchKernelGGL(gm::conv_radial_reduce_kernel, dim3((gm::kRPart + 255) / 256), dim3(256), 0, s, partial,
-                     rows * (second ? 2 : 1), grad);
+                     rows * groups, grad);
   return gm::check_launch("conv_radial_reduce");
 }
