@@ -471,13 +471,28 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
   }
 }
 
-// grad[p] = sum over waves w (in order) of partial[w][p].
-__global__ __launch_bounds__(256) void conv_radial_reduce_kernel(const float* partial, int64_t n_waves, float* grad) {
+// grad[p] = sum over the partial rows w (in order) of partial[w][p], in two
+// passes: kRSlices slices of the rows summed in parallel (consecutive threads,
+// consecutive columns), then the slices in order.  Deterministic.
+constexpr int kRSlices = 32;
+
+__global__ __launch_bounds__(256) void conv_radial_reduce_slices(const float* partial, int64_t n_rows, float* slices) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  const int sl = blockIdx.y;
+  if (p >= kRPart) return;
+  const int64_t w0 = n_rows * sl / kRSlices, w1 = n_rows * (sl + 1) / kRSlices;
+  float acc = 0.f;
+  for (int64_t w = w0; w < w1; ++w) acc += partial[w * kRPart + p];
+  slices[(int64_t)sl * kRPart + p] = acc;
+}
+
+__global__ __launch_bounds__(256) void conv_radial_reduce_kernel(const float* slices, float* grad) {
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= kRPart) return;
-  float s = 0.f;
-  for (int64_t w = 0; w < n_waves; ++w) s += partial[w * kRPart + p];
-  grad[p] = s;
+  float acc = 0.f;
+#pragma unroll 8
+  for (int sl = 0; sl < kRSlices; ++sl) acc += slices[(int64_t)sl * kRPart + p];
+  grad[p] = acc;
 }
 
 // The backward's tile groups: kRGroup consecutive slots each; a group runs
@@ -558,6 +573,12 @@ extern "C" int64_t gm_conv_radial_partial_row(void) { return gm::kRPart; }
 
 extern "C" int64_t gm_conv_radial_backward_groups(int64_t nc) { return gm::live_groups((int)nc); }
 
+// Rows of the backward's workspace for n_blocks workgroups: the partial rows of every
+// tile group, then the reduction's slices.
+extern "C" int64_t gm_conv_radial_workspace_rows(int64_t n_blocks) {
+  return n_blocks * gm::kRWaves * gm::kRGroups + gm::kRSlices;
+}
+
 extern "C" int gm_conv_radial_forward_f32(const float* v, const float* rf, const float* rbias, const float* w1,
                                           const float* b1,
                                           const float* centers, int64_t nb, double width, const float* transport,
@@ -621,7 +642,10 @@ extern "C" int gm_conv_radial_backward_f32(const float* g, const float* v, const
   }
   int st = gm::check_launch("conv_radial_backward");
   if (st != GM_OK) return st;
-  hipLaunchKernelGGL(gm::conv_radial_reduce_kernel, dim3((gm::kRPart + 255) / 256), dim3(256), 0, s, partial,
-                     rows * groups, grad);
+  // the slices' sums go to the rows past the partial rows (the caller sizes partial for them)
+  float* slices = partial + rows * gm::kRGroups * gm::kRPart;
+  hipLaunchKernelGGL(gm::conv_radial_reduce_slices, dim3((gm::kRPart + 255) / 256, gm::kRSlices), dim3(256), 0, s,
+                     partial, rows * groups, slices);
+  hipLaunchKernelGGL(gm::conv_radial_reduce_kernel, dim3((gm::kRPart + 255) / 256), dim3(256), 0, s, slices, grad);
   return gm::check_launch("conv_radial_reduce");
 }

@@ -62,6 +62,7 @@ SIGNATURES_F32 = {
     "gm_scatter_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
     "gm_conv_radial_partial_row": (ctypes.c_int64, []),
     "gm_conv_radial_backward_groups": (ctypes.c_int64, [_I]),
+    "gm_conv_radial_workspace_rows": (ctypes.c_int64, [_I]),
     "gm_conv_radial_forward_f32": (ctypes.c_int, [_P] * 6 + [_I, _D] + [_P] * 6 + [_I] * 7 + [_P] * 4),
     "gm_conv_radial_backward_f32": (ctypes.c_int, [_P] * 8 + [_I, _D] + [_P] * 7 + [_I] * 7 + [_P, _P, _I] + [_P] * 4),
 }
@@ -815,9 +816,11 @@ def conv_radial_backward(g: Tensor, v: Tensor, rf: Tensor, rbias: Tensor, rb: Te
     n = v.shape[0]
     dv = torch.empty_like(v)
     row = int(library().gm_conv_radial_partial_row())
-    n_blocks = max(8, min(1024, (n + 3) // 4 // 8 * 8))  # a multiple of 8: one share of the sources per XCD
-    groups = int(library().gm_conv_radial_backward_groups(tiles.shape[1]))  # launches over groups of coefficient tiles
-    partial = torch.empty(groups * n_blocks * 4, row, dtype=torch.float32, device=v.device)
+    # one resident round (two 4-wave workgroups per CU at the kernels' register use), a
+    # multiple of 8: one share of the sources per XCD
+    n_blocks = max(8, min(512, (n + 3) // 4 // 8 * 8))
+    rows = int(library().gm_conv_radial_workspace_rows(n_blocks))  # partial rows of every tile group + slices
+    partial = torch.empty(rows, row, dtype=torch.float32, device=v.device)
     grad = torch.empty(row, dtype=torch.float32, device=v.device)
     cen = (ctypes.c_float * 8)(*centers)
     _call("gm_conv_radial_backward_f32", _ptr(g), _ptr(v), _ptr(rf), _ptr(rbias), _ptr(rb), _ptr(w1), _ptr(b1),
