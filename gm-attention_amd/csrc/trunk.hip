@@ -100,10 +100,14 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_kernel(TrunkArgs
   __shared__ float red[kTrunkThreads / 64][PH];  // per-wave sums
   const ConstPtr weight = as_const(a.weight), bias = as_const(a.bias), centers = as_const(a.centers);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (int pass = 0; pass < 2 * a.H; ++pass) {
-    const int hh = pass >> 1, t0 = (pass & 1) * TH;
+  // Waves 0-1 take features 0..TH-1 and waves 2-3 features TH..T-1 of the same edges in the
+  // same pass, so the second half of each dh row is read while its line is still in L2
+  // (one pass per head; the features' half is wave-uniform, so the weights stay scalar operands).
+  constexpr int kEdgeThreads = kTrunkThreads / 2;
+  const int t0 = (wave >> 1) * TH;
+  const int64_t stride = (int64_t)gridDim.x * kEdgeThreads;
+  const int64_t first = (int64_t)blockIdx.x * kEdgeThreads + (threadIdx.x & (kEdgeThreads - 1));
+  for (int hh = 0; hh < a.H; ++hh) {
     const ConstPtr W = weight + hh * T * B;
     float acc[PH];
 #pragma unroll
@@ -147,7 +151,7 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_kernel(TrunkArgs
         acc[TH * B + t] += dp;
       }
     }
-    // the block's sum in a fixed order: a butterfly per wave, then the waves in order
+    // the block's sum in a fixed order: a butterfly per wave, then the half's two waves in order
 #pragma unroll
     for (int i = 0; i < PH; ++i) {
       float v = acc[i];
@@ -155,11 +159,11 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_kernel(TrunkArgs
       if (lane == 0) red[wave][i] = v;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < PH; i += blockDim.x) {
-      float sum = 0.f;
-      for (int wv = 0; wv < kTrunkThreads / 64; ++wv) sum += red[wv][i];
-      // weights of features t0 .. t0 + TH - 1, then their biases
-      const int slot = i < TH * B ? t0 * B + i : T * B + t0 + (i - TH * B);
+    for (int i = threadIdx.x; i < 2 * PH; i += blockDim.x) {
+      const int half = i / PH, j = i % PH;
+      const float sum = red[2 * half][j] + red[2 * half + 1][j];
+      // weights of features half * TH .. half * TH + TH - 1, then their biases
+      const int slot = j < TH * B ? half * TH * B + j : T * B + half * TH + (j - TH * B);
       a.partial[((int64_t)blockIdx.x * a.H + hh) * P + slot] = sum;
     }
     __syncthreads();
@@ -198,7 +202,7 @@ int prepare(TrunkArgs& a, const float* rho, const float* weight, const float* bi
 constexpr int64_t kTrunkBackwardBlocks = 2048;  // the backward's fixed grid (threads stride over the edges)
 
 int64_t backward_blocks(int64_t n_edges) {
-  const int64_t need = (n_edges + kTrunkThreads - 1) / kTrunkThreads;
+  const int64_t need = (n_edges + kTrunkThreads / 2 - 1) / (kTrunkThreads / 2);  // 128 edges per block pass
   return need < kTrunkBackwardBlocks ? (need > 0 ? need : 1) : kTrunkBackwardBlocks;
 }
 
