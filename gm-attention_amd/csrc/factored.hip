@@ -97,6 +97,14 @@ struct FactArgs {
   uint32_t colslot32[32];  // packed column -> slot column, four bytes a word
   uint32_t kmask;
   int n_slots, gstride;
+  // the value kernel's radial trunk evaluated in the lane kernels from rho_g
+  // (h_t = SiLU(W1 b + b1) over the Gaussian basis b_k = exp(-((rho^2 - c_k)
+  // inv_width)^2 / 2)) instead of reading h; trunk_w null: h is read
+  const float* trunk_w;  // (16, trunk_nb)
+  const float* trunk_b;  // (16,) or null
+  float trunk_c[8];
+  float trunk_inv_width;
+  int trunk_nb;
 };
 
 template <typename T>
@@ -525,6 +533,7 @@ __global__ __launch_bounds__(64) void factored_backward_kernel(FactArgs<T> a) {
 
 
 constexpr int kMT = 16;  // edges per MFMA tile
+constexpr int kHsStride = 16;  // floats per edge row of the fused trunk's LDS tile
 
 // The MFMA kernels run one wave per workgroup, and a wave's LDS operations
 // execute in order, so handing LDS data between its lanes needs only a
@@ -1418,23 +1427,69 @@ __device__ __forceinline__ bool kstep_live(const FactArgs<float>& a, int nt, int
   return (w & kSlotActive) && !((w & kSlotReal) && (r & 1));
 }
 
+// The fused trunk as one 16 x 16 matrix product per tile: pre (16 features x
+// 16 edges) = b1 + W1 (16 x 8) B (8 basis functions x 16 edges) in two
+// k-steps, so lane (m, q) supplies W1[m][4 s + q] and the basis function
+// 4 s + q of edge m (two exponentials) and holds the pre-activations of
+// features 4 q .. 4 q + 3 of edge m -- the layout the kernels use for h.
+struct TrunkLane {
+  float wa[2];   // W1[m][4 s + q], s = 0, 1 (zero past the basis)
+  floatx4 b1;    // b1[4 q .. 4 q + 3]
+};
+
+__device__ __forceinline__ TrunkLane trunk_lane(const FactArgs<float>& a, int m, int q) {
+  TrunkLane t;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int k = 4 * s + q;
+    t.wa[s] = k < a.trunk_nb ? a.trunk_w[m * a.trunk_nb + k] : 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) t.b1[r] = a.trunk_b ? a.trunk_b[4 * q + r] : 0.f;
+  return t;
+}
+
+// h of features 4 q .. 4 q + 3 of edge m (rho its distance / cutoff); the
+// pre-activations into pre.  Basis exp(-((rho^2 - c_k) / width)^2 / 2) and
+// SiLU on the hardware exponential and reciprocal, as the trunk kernel.
+__device__ __forceinline__ floatx4 trunk_features(const FactArgs<float>& a, const TrunkLane& t, int q, float rho,
+                                                  floatx4& pre) {
+  const float s2 = rho * rho;
+  pre = t.b1;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int k = 4 * s + q;
+    const float z = (s2 - (k < 8 ? a.trunk_c[k] : 0.f)) * a.trunk_inv_width;
+    const float b = k < a.trunk_nb ? __builtin_amdgcn_exp2f(-0.5f * z * z * 1.44269504088896340736f) : 0.f;
+    pre = mfma16(t.wa[s], b, pre);
+  }
+  floatx4 h;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) h[r] = pre[r] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-pre[r] * 1.44269504088896340736f));
+  return h;
+}
+
 template <class P>
 struct FwdTile {
   floatx4 h;        // h(edge m)[4 q .. 4 q + 3]
   PhaseRegs<P> ph;  // fixed slots: edge m's zw; runtime: chunk q of its phase row
-  float rho;        // runtime slots: rho of edge m
+  float rho;        // runtime slots or the fused trunk: rho of edge m
 };
 
 // ph_r spans the zw rows (fixed slots) or the phase rows (runtime slots).
 template <class P>
 __device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amdgpu_buffer_rsrc_t ph_r,
-                                               __amdgpu_buffer_rsrc_t rho_r, int tb, int m, int q) {
+                                               __amdgpu_buffer_rsrc_t rho_r, int tb, int m, int q, bool fused) {
   FwdTile<P> t;
   const int e = tb + m;
-  t.h = bload4(h_r, (e * 16 + 4 * q) * 4);
+  if (fused) {
+    t.h = floatx4{0.f, 0.f, 0.f, 0.f};
+  } else {
+    t.h = bload4(h_r, (e * 16 + 4 * q) * 4);
+  }
   if constexpr (P::kStatic) {
     t.ph.ph = bload4(ph_r, e * 16);
-    t.rho = 0.f;
+    t.rho = fused ? bload1(rho_r, e * 4) : 0.f;
   } else {
     t.ph.ph = bload4(ph_r, (e * kPhaseRow + 4 * q) * 4);
     t.rho = bload1(rho_r, e * 4);
@@ -1446,7 +1501,10 @@ __device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amd
 template <int NT, class P>
 __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const FwdTile<P>& cur, const float (&za)[NT][4],
                                              const floatx4 (&z0)[NT], float* Ph, __amdgpu_buffer_rsrc_t out_r,
-                                             int d_out, int tb, int m, int q) {
+                                             int d_out, int tb, int m, int q, const TrunkLane& tl, bool fused) {
+  // h(edge m)[4 q .. 4 q + 3]: read, or the trunk's features evaluated here
+  floatx4 pre;
+  const floatx4 h = fused ? trunk_features(a, tl, q, cur.rho, pre) : cur.h;
   // u(e) = Z0 + sum_t h_t Z_t: lane (m, q) ends with edge m's slot columns 16 nt + 4 q + r
   floatx4 acc[NT];
 #pragma unroll
@@ -1454,7 +1512,7 @@ __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const Fwd
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], cur.h[s], acc[nt]);
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], h[s], acc[nt]);
   Powers<P> pw;
   if constexpr (P::kStatic) {
     pw = powers<P>(cur.ph.ph);
@@ -1492,9 +1550,9 @@ __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const Fwd
   if constexpr (!P::kStatic) wave_sync();
 }
 
-template <int NT, class P>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? 4 : 1))) void factored_forward_lanes(
-    FactArgs<float> a) {
+template <int NT, class P, bool FUSED>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED ? 3 : 4) : 1))) void
+factored_forward_lanes(FactArgs<float> a) {
   constexpr int ZS = 16 * NT + 4;
   __shared__ __align__(16) float Zs[17 * ZS];
   __shared__ __align__(16) float Ph[P::kStatic ? 4 : kMT * kPhStride];
@@ -1517,22 +1575,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ?
     for (int s = 0; s < 4; ++s) za[nt][s] = Zs[(1 + 4 * q + s) * ZS + 16 * nt + m];
     z0[nt] = *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q);
   }
-  const auto h_r = span(a.h + g0 * 16, (int64_t)ng * 64);
+  constexpr bool fused = FUSED;
+  TrunkLane tl{};
+  if (fused) tl = trunk_lane(a, m, q);
+  const auto h_r = span(fused ? nullptr : a.h + g0 * 16, fused ? 0 : (int64_t)ng * 64);
   const auto ph_r = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
                                : span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
   const auto rho_r = span(a.rho_g + g0, (int64_t)ng * 4);
   const auto out_r = span(a.out + g0 * d_out, (int64_t)ng * d_out * 4);
   // two tiles in flight: each buffer is refilled right after its tile's
   // stores, so waiting for a tile never waits for the previous tile's stores
-  FwdTile<P> ta = load_fwd<P>(h_r, ph_r, rho_r, 0, m, q);
-  FwdTile<P> tbf = load_fwd<P>(h_r, ph_r, rho_r, kMT, m, q);
+  FwdTile<P> ta = load_fwd<P>(h_r, ph_r, rho_r, 0, m, q, fused);
+  FwdTile<P> tbf = load_fwd<P>(h_r, ph_r, rho_r, kMT, m, q, fused);
   for (int tb = 0;;) {
-    forward_tile<NT, P>(a, ta, za, z0, Ph, out_r, d_out, tb, m, q);
-    ta = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q);
+    forward_tile<NT, P>(a, ta, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
+    ta = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
     tb += kMT;
     if (tb >= ng) break;
-    forward_tile<NT, P>(a, tbf, za, z0, Ph, out_r, d_out, tb, m, q);
-    tbf = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q);
+    forward_tile<NT, P>(a, tbf, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
+    tbf = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
     tb += kMT;
     if (tb >= ng) break;
   }
@@ -1540,24 +1601,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ?
 
 template <class P>
 struct BwdTile {
-  floatx4 h;        // h(edge 4 q + i)[m], i < 4
+  floatx4 h;        // h(edge 4 q + i)[m], i < 4 (read; zero under the fused trunk)
   PhaseRegs<P> ph;  // as in the forward
-  float rho, w;     // edge m (rho: runtime slots)
+  float rho, w;     // edge m (rho: runtime slots or the fused trunk)
   int64_t tgt;      // runtime slots: the target of edge m
 };
 
 template <class P>
 __device__ __forceinline__ BwdTile<P> load_bwd(__amdgpu_buffer_rsrc_t h_r, __amdgpu_buffer_rsrc_t ph_r,
                                                __amdgpu_buffer_rsrc_t rho_r, __amdgpu_buffer_rsrc_t w_r,
-                                               __amdgpu_buffer_rsrc_t t_r, int tb, int m, int q) {
+                                               __amdgpu_buffer_rsrc_t t_r, int tb, int m, int q, bool fused) {
   BwdTile<P> t;
+  if (fused) {
+    t.h = floatx4{0.f, 0.f, 0.f, 0.f};
+  } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) t.h[i] = bload1(h_r, ((tb + 4 * q + i) * 16 + m) * 4);
+    for (int i = 0; i < 4; ++i) t.h[i] = bload1(h_r, ((tb + 4 * q + i) * 16 + m) * 4);
+  }
   const int e = tb + m;
   if constexpr (P::kStatic) {
     t.ph.ph = bload4(ph_r, e * 16);
     t.tgt = 0;
-    t.rho = 0.f;
+    t.rho = fused ? bload1(rho_r, e * 4) : 0.f;
   } else {
     t.ph.ph = bload4(ph_r, (e * kPhaseRow + 4 * q) * 4);
     t.tgt = bload_i64(t_r, e * 8);
@@ -1608,9 +1673,17 @@ struct BwdSpans {
 template <int NT, class P, class O>
 __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const BwdTile<P>& cur, const O& outs,
                                               const floatx4 (&zb)[NT], floatx4 (&dz)[NT], float (&dz0)[NT], float* Sh,
-                                              float* Ph, float* Gt, int64_t* Tg, const BwdSpans& sp, int d_out,
-                                              int ng, int tb, int m, int q) {
+                                              float* Ph, float* Gt, int64_t* Tg, float* Hs, const BwdSpans& sp,
+                                              int d_out, int ng, int tb, int m, int q, const TrunkLane& tl,
+                                              bool fused) {
   const int row = (tb + m) * d_out;
+  // the fused trunk: edge m's features 4 q .. 4 q + 3 here, handed to the dZ operand's
+  // layout (feature m of edges 4 q + i) through Hs with the W transpose below
+  floatx4 pre;
+  if (fused) {
+    const floatx4 hf = trunk_features(a, tl, q, cur.rho, pre);
+    *reinterpret_cast<floatx4*>(Hs + m * kHsStride + 4 * q) = hf;
+  }
   float wv[NT][4];
   float dwp = 0.f;  // this lane's share of dweights(edge m)
   if constexpr (P::kStatic) {
@@ -1688,20 +1761,25 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
 #pragma unroll
     for (int r = 0; r < 4; ++r) Sh[(16 * nt + 4 * q + r) * kWtStride + m] = wv[nt][r];
   wave_sync();
+  floatx4 hb = cur.h;
+  if (fused) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hb[i] = Hs[(4 * q + i) * kHsStride + m];
+  }
   // dZ_t,c += sum_e h_t(e) W(e)_c over edges 4 q' + i; the t = 0 column sums W
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const floatx4 wt = *reinterpret_cast<const floatx4*>(Sh + (16 * nt + m) * kWtStride + 4 * q);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dz[nt] = mfma16(cur.h[i], wt[i], dz[nt]);
+    for (int i = 0; i < 4; ++i) dz[nt] = mfma16(hb[i], wt[i], dz[nt]);
     dz0[nt] += (wt[0] + wt[1]) + (wt[2] + wt[3]);
   }
   wave_sync();
 }
 
-template <int NT, class P>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? 3 : 1))) void factored_backward_lanes(
-    FactArgs<float> a) {
+template <int NT, class P, bool FUSED>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED ? 2 : 3) : 1))) void
+factored_backward_lanes(FactArgs<float> a) {
   constexpr int ZS = 16 * NT + 4;
   constexpr int kZWords = 17 * ZS, kWWords = 16 * NT * kWtStride;
   __shared__ __align__(16) float Sh[kZWords > kWWords ? kZWords : kWWords];  // Z in, then W's transpose, then dZ out
@@ -1709,6 +1787,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ?
   __shared__ __align__(16) float Gt[P::kStatic ? 4 : kMT * (GM_FACT_MAX_OUT + 4)];
   __shared__ __align__(16) uint8_t colslot[128];
   __shared__ int64_t Tg[P::kStatic ? 1 : kMT];
+  __shared__ __align__(16) float Hs[kMT * kHsStride];  // the fused trunk's features, edge-major
   const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
   const int d_out = P::kStatic ? P::kDout : a.d_out;
   const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
@@ -1731,8 +1810,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ?
     dz[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     dz0[nt] = 0.f;
   }
+  constexpr bool fused = FUSED;
+  TrunkLane tl{};
+  if (fused) tl = trunk_lane(a, m, q);
   BwdSpans sp;
-  sp.h = span(a.h + g0 * 16, (int64_t)ng * 64);
+  sp.h = span(fused ? nullptr : a.h + g0 * 16, fused ? 0 : (int64_t)ng * 64);
   sp.ph = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
                      : span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
   sp.rho = span(a.rho_g + g0, (int64_t)ng * 4);
@@ -1745,8 +1827,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ?
   // tile's stores); with static slots the targets run three tiles ahead and
   // the targets' gradient values and row values two, so no load is waited
   // for within the tile after the one that issued it.
-  BwdTile<P> ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, 0, m, q);
-  BwdTile<P> tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, kMT, m, q);
+  BwdTile<P> ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, 0, m, q, fused);
+  BwdTile<P> tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, kMT, m, q, fused);
   OutVals<P::kStatic ? NT : 1> oa, ob;
   int64_t tn = 0;  // static slots: the targets of the tile two ahead of the current one
   if constexpr (P::kStatic) {
@@ -1755,20 +1837,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ?
     tn = bload_i64(sp.t, (2 * kMT + m) * 8);
   }
   for (int tb = 0;;) {
-    backward_tile<NT, P>(a, ta, oa, zb, dz, dz0, Sh, Ph, Gt, Tg, sp, d_out, ng, tb, m, q);
+    backward_tile<NT, P>(a, ta, oa, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl, fused);
     if constexpr (P::kStatic) {
       load_outs<NT, P>(oa, a.g, tn, sp.rows, (tb + 2 * kMT + m) * d_out, q);
       tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
     }
-    ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q);
+    ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused);
     tb += kMT;
     if (tb >= ng) break;
-    backward_tile<NT, P>(a, tbf, ob, zb, dz, dz0, Sh, Ph, Gt, Tg, sp, d_out, ng, tb, m, q);
+    backward_tile<NT, P>(a, tbf, ob, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl, fused);
     if constexpr (P::kStatic) {
       load_outs<NT, P>(ob, a.g, tn, sp.rows, (tb + 2 * kMT + m) * d_out, q);
       tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
     }
-    tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q);
+    tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused);
     tb += kMT;
     if (tb >= ng) break;
   }
@@ -2135,10 +2217,18 @@ void launch_grouped_nt(bool forward, const FactArgs<float>& a, hipStream_t strea
 template <int NT, class P = RuntimeSlots>
 void launch_lanes_nt(bool forward, const FactArgs<float>& a, hipStream_t stream) {
   const dim3 grid((unsigned)a.n_groups), block(64);
-  if (forward)
-    hipLaunchKernelGGL((factored_forward_lanes<NT, P>), grid, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL((factored_backward_lanes<NT, P>), grid, block, 0, stream, a);
+  const bool fused = a.trunk_w != nullptr;  // the trunk evaluated in the kernels: their own instantiation
+  if (forward) {
+    if (fused)
+      hipLaunchKernelGGL((factored_forward_lanes<NT, P, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((factored_forward_lanes<NT, P, false>), grid, block, 0, stream, a);
+  } else {
+    if (fused)
+      hipLaunchKernelGGL((factored_backward_lanes<NT, P, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((factored_backward_lanes<NT, P, false>), grid, block, 0, stream, a);
+  }
 }
 
 // Whether a plan's runtime slot words are P's compile-time ones.
@@ -2251,27 +2341,57 @@ void prepare_lanes(FactArgs<float>& a) {
 
 // The grouped path's extra checks: fp32, 16 trunk features, at most 128
 // packed columns, both phase tables within one 8-pair row, 16-byte rows.
+// The fused trunk's parameters: W1 (16, nb) and b1 (16) device pointers, the
+// basis centres (host, nb) and width; trunk_w null leaves h to be read.
+struct TrunkParams {
+  const float* w;
+  const float* b;
+  const float* centers;
+  int64_t nb;
+  double width;
+};
+
 int prepare_grouped(FactArgs<float>& a, const float* h, const Runs<float>& runs, const float* phase_g,
                     const float* rho_g, const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source,
                     int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa,
-                    int64_t pt, int64_t n_blocks, int64_t d_out) {
+                    int64_t pt, int64_t n_blocks, int64_t d_out, const TrunkParams& trunk) {
   GM_REQUIRE(pa >= 1 && pt >= 1 && pa + pt <= kPhaseRow / 2, "the grouped phase rows hold at most 8 pairs");
-  const int status = prepare(a, h, runs, phase_g, phase_g, rho_g, desc, group_ptr /* order unused */, group_ptr,
-                             group_source, n_nodes, n_edges, n_groups, K, wc, wr, pa > pt ? pa : pt, n_blocks, d_out);
+  const bool fused = trunk.w != nullptr;
+  // under the fused trunk h is never read: rho_g stands in for prepare's pointer check
+  const int status = prepare(a, fused ? rho_g : h, runs, phase_g, phase_g, rho_g, desc, group_ptr /* order unused */,
+                             group_ptr, group_source, n_nodes, n_edges, n_groups, K, wc, wr, pa > pt ? pa : pt,
+                             n_blocks, d_out);
   if (status != GM_OK) return status;
+  a.trunk_w = nullptr;
+  a.trunk_b = nullptr;
+  a.trunk_nb = 0;
+  if (fused) {
+    a.h = nullptr;
+    GM_REQUIRE(trunk.nb >= 1 && trunk.nb <= 8, "the fused trunk takes 1 to 8 basis functions");
+    GM_REQUIRE(trunk.width > 0.0 && trunk.centers != nullptr, "the fused trunk needs its basis centres and width");
+    a.trunk_w = trunk.w;
+    a.trunk_b = trunk.b;
+    a.trunk_nb = (int)trunk.nb;
+    a.trunk_inv_width = (float)(1.0 / trunk.width);
+    for (int k = 0; k < 8; ++k) a.trunk_c[k] = k < trunk.nb ? trunk.centers[k] : 0.f;
+  }
   GM_REQUIRE(K == 17, "the grouped kernels take 16 trunk features (K = 17)");
   GM_REQUIRE(a.C <= 128, "the grouped kernels take at most 128 packed columns");
   for (int b = 0; b < a.n_blocks; ++b) {
     const Block& d = a.desc[b];
     GM_REQUIRE(std::abs(d.ang) < pa && std::abs(d.tr) < pt, "a block's harmonic order exceeds the grouped phase rows");
   }
-  if (n_edges > 0) GM_REQUIRE(h && aligned(h, 16) && phase_g && aligned(phase_g, 16) && rho_g,
+  if (n_edges > 0) GM_REQUIRE((fused || (h && aligned(h, 16))) && phase_g && aligned(phase_g, 16) && rho_g,
                               "h and the phase rows must be 16-byte aligned device pointers");
   a.phase_g = phase_g;
   a.rho_g = rho_g;
   a.pa = (int)pa;
   a.pt = (int)pt;
   prepare_lanes(a);
+  if (fused && n_edges > 0) {
+    GM_REQUIRE(a.n_slots > 0, "the fused trunk runs in the lane-owned kernels only; this plan takes the generic ones");
+    GM_REQUIRE(trunk.w != nullptr, "trunk_w must be a device pointer");
+  }
   return GM_OK;
 }
 
@@ -2361,12 +2481,14 @@ extern "C" int gm_factored_forward_grouped_f32(
     const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
     const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
     int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
-    int64_t n_blocks, int64_t d_out, float* rows_g, void* stream) {
+    int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
+    int64_t trunk_nb, double trunk_width, float* rows_g, void* stream) {
   GM_REQUIRE(z && node_stride && t_stride && width, "the mix runs must be host arrays");
   const gm::Runs<float> runs{z, nullptr, node_stride, t_stride, width, n_runs};
   gm::FactArgs<float> a;
+  const gm::TrunkParams trunk{trunk_w, trunk_b, trunk_centers, trunk_nb, trunk_width};
   const int status = gm::prepare_grouped(a, h_g, runs, phase_g, rho_g, desc, group_ptr, group_source, n_nodes, n_edges,
-                                         n_groups, K, wc, wr, pa, pt, n_blocks, d_out);
+                                         n_groups, K, wc, wr, pa, pt, n_blocks, d_out, trunk);
   if (status != GM_OK) return status;
   if (n_edges == 0 || n_groups == 0) return GM_OK;
   GM_REQUIRE(rows_g, "rows must be a device pointer");
@@ -2384,12 +2506,14 @@ extern "C" int gm_factored_backward_grouped_f32(
     const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
     const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
     int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
-    int64_t n_blocks, int64_t d_out, float* dh_g, float* dweights_g, void* stream) {
+    int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
+    int64_t trunk_nb, double trunk_width, float* dh_g, float* dweights_g, void* stream) {
   GM_REQUIRE(z && dz && node_stride && t_stride && width, "the mix runs must be host arrays");
   const gm::Runs<float> runs{z, dz, node_stride, t_stride, width, n_runs};
   gm::FactArgs<float> a;
+  const gm::TrunkParams trunk{trunk_w, trunk_b, trunk_centers, trunk_nb, trunk_width};
   const int status = gm::prepare_grouped(a, h_g, runs, phase_g, rho_g, desc, group_ptr, group_source, n_nodes, n_edges,
-                                         n_groups, K, wc, wr, pa, pt, n_blocks, d_out);
+                                         n_groups, K, wc, wr, pa, pt, n_blocks, d_out, trunk);
   if (status != GM_OK) return status;
   if (n_edges == 0 || n_groups == 0) return GM_OK;
   GM_REQUIRE(g && target_g && weights_g && rows_g && dh_g && dweights_g,

@@ -53,8 +53,10 @@ SIGNATURES_F32 = {
     "gm_radial_trunk_forward_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_D, _P, _P]),
     "gm_radial_trunk_backward_f32": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_D, _P, _P, _P]),
     "gm_radial_trunk_partials": (ctypes.c_int64, [_I]),
-    "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P, _P]),
-    "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3),
+    "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
+                                        + [_P, _P]),
+    "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
+                                         + [_P] * 3),
     "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
     "gm_factored_lane_tables": (ctypes.c_int, [_P] + [_I] * 6 + [_P] * 3),
     "gm_factored_aggregate_heads_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_P, _P]),
@@ -580,41 +582,72 @@ def _check_order(group_order: Tensor | None, group_source: Tensor) -> None:
         raise ValueError("group_order must be a contiguous int64 permutation of the groups, on their device")
 
 
-def factored_forward_grouped(h_g: Tensor, runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor,
+class FusedTrunk:
+    """A head's radial trunk for the lane-owned grouped kernels to evaluate from
+    ``rho_g`` themselves: ``w (16, nb)`` and ``b (16,)`` (or None) on the
+    device, the basis centres (host floats) and width."""
+
+    def __init__(self, w: Tensor, b: Tensor | None, centers: list[float], width: float):
+        _check(w.dim() == 2 and w.shape[0] == 16 and 1 <= w.shape[1] <= 8 and w.is_contiguous()
+               and w.dtype == torch.float32, "the fused trunk's weight must be a contiguous float32 (16, nb <= 8)")
+        _check(b is None or (b.shape == (16,) and b.is_contiguous() and b.dtype == torch.float32),
+               "the fused trunk's bias must be a contiguous float32 (16,)")
+        _check(len(centers) == w.shape[1], "one basis centre per basis function")
+        self.w, self.b, self.width = w, b, float(width)
+        self.centers = (ctypes.c_float * 8)(*centers)
+        self.nb = w.shape[1]
+
+    def args(self) -> list:
+        return [_ptr(self.w), _ptr(self.b), ctypes.addressof(self.centers), self.nb, self.width]
+
+
+_NO_TRUNK = [None, None, None, 0, 0.0]
+
+
+def factored_forward_grouped(h_g: Tensor | None, runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor,
                              zw_g: Tensor | None, pa: int, pt: int, desc: Tensor, group_ptr: Tensor,
                              group_source: Tensor, group_order: Tensor | None, K: int, wc: int, wr: int,
-                             d_out: int, out: Tensor | None = None) -> Tensor:
+                             d_out: int, out: Tensor | None = None, trunk: FusedTrunk | None = None) -> Tensor:
     """The rows in the grouping's order, every per-edge stream read in that order
-    (into ``out`` (n_edges, d_out) when given)."""
+    (into ``out`` (n_edges, d_out) when given).  With ``trunk`` the kernels
+    evaluate h from ``rho_g`` and ``h_g`` may be None."""
+    n_edges = rho_g.shape[0]
+    if h_g is None and trunk is None:
+        raise ValueError("h_g is required without a fused trunk")
     if out is None:
-        out = torch.empty(h_g.shape[0], d_out, dtype=h_g.dtype, device=h_g.device)
-    elif out.shape != (h_g.shape[0], d_out) or not out.is_contiguous() or out.dtype != h_g.dtype:
-        raise ValueError("out must be a contiguous (n_edges, d_out) tensor in h's dtype")
-    if h_g.shape[0] == 0:
+        out = torch.empty(n_edges, d_out, dtype=rho_g.dtype, device=rho_g.device)
+    elif out.shape != (n_edges, d_out) or not out.is_contiguous() or out.dtype != rho_g.dtype:
+        raise ValueError("out must be a contiguous (n_edges, d_out) tensor in rho's dtype")
+    if n_edges == 0:
         return out
     _check_order(group_order, group_source)
     hd = host_desc32(desc)
     _call("gm_factored_forward_grouped_f32", _ptr(h_g), ctypes.cast(runs.z, ctypes.c_void_p),
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
           ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),
-          _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, h_g.shape[0], group_source.shape[0], K, wc,
-          wr, pa, pt, hd.shape[0], d_out, _ptr(out), _stream(h_g.device))
+          _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, n_edges, group_source.shape[0], K, wc,
+          wr, pa, pt, hd.shape[0], d_out, *(trunk.args() if trunk is not None else _NO_TRUNK), _ptr(out),
+          _stream(rho_g.device))
     return out
 
 
-def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, rows_g: Tensor, h_g: Tensor,
+def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, rows_g: Tensor, h_g: Tensor | None,
                               runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor, zw_g: Tensor | None,
                               pa: int, pt: int, desc: Tensor, group_ptr: Tensor, group_source: Tensor,
                               group_order: Tensor | None, K: int, wc: int, wr: int, dh_g: Tensor,
-                              dweights: Tensor | None = None) -> Tensor:
+                              dweights: Tensor | None = None, trunk: FusedTrunk | None = None) -> Tensor:
     """dh (grouping order) into ``dh_g``, the mix gradients into the runs'
     gradient arrays; returns dweights in the grouping's order (into
-    ``dweights`` when given)."""
+    ``dweights`` when given).  With ``trunk`` the kernels evaluate h from
+    ``rho_g`` and ``h_g`` may be None."""
+    if h_g is None and trunk is None:
+        raise ValueError("h_g is required without a fused trunk")
     if dweights is None:
         dweights = torch.empty_like(weights_g)
     elif dweights.shape != weights_g.shape or not dweights.is_contiguous() or dweights.dtype != weights_g.dtype:
         raise ValueError("dweights must be a contiguous tensor shaped like weights_g")
-    if h_g.shape[0] == 0:
+    n_edges = rho_g.shape[0]
+    if n_edges == 0:
         return dweights
     _check_order(group_order, group_source)
     hd = host_desc32(desc)
@@ -622,8 +655,9 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
           ctypes.cast(runs.z, ctypes.c_void_p), ctypes.cast(runs.dz, ctypes.c_void_p),
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
           ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),
-          _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, h_g.shape[0], group_source.shape[0], K,
-          wc, wr, pa, pt, hd.shape[0], g.shape[1], _ptr(dh_g), _ptr(dweights), _stream(h_g.device))
+          _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, n_edges, group_source.shape[0], K,
+          wc, wr, pa, pt, hd.shape[0], g.shape[1], *(trunk.args() if trunk is not None else _NO_TRUNK), _ptr(dh_g),
+          _ptr(dweights), _stream(rho_g.device))
     return dweights
 
 

@@ -623,6 +623,86 @@ class FactoredHeadsGrouped(torch.autograd.Function):
         return (dh_g, dalpha, None, *dmixes)
 
 
+class FactoredHeadsTrunk(torch.autograd.Function):
+    """:class:`FactoredHeadsGrouped` with each head's radial trunk evaluated
+    inside the lane-owned kernels from ``rho_g`` (no ``h (H, E, 16)`` tensor):
+    in ``trunk_w (H, 16, B)``, ``trunk_b (H, 16)`` or None, ``alpha (E, H)``
+    and the mix arrays; out ``(N, H, d_out)``; gradients for the trunk's
+    parameters (the trunk kernel's backward on the ``dh`` the factored
+    backward writes), ``alpha`` and the mixes."""
+
+    @staticmethod
+    def forward(ctx: Any, trunk_w: Tensor, trunk_b: Tensor | None, alpha: Tensor, meta: dict,
+                *mixes: Tensor) -> Tensor:
+        st: GroupedStreams = meta["streams"]
+        H, E = trunk_w.shape[0], st.rho_g.shape[0]
+        trunks = [_native.FusedTrunk(trunk_w[hh].contiguous(), None if trunk_b is None else trunk_b[hh].contiguous(),
+                                     meta["centers"], meta["width"]) for hh in range(H)]
+        rows = torch.empty(H, E, meta["d_out"], dtype=alpha.dtype, device=alpha.device)
+        for head in range(H):
+            runs = _heads_runs(meta, mixes, head, None)
+            with torch.profiler.record_function("gm::kernel/pairs"):
+                _native.factored_forward_grouped(None, runs, meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g, st.pa,
+                                                 st.pt, meta["desc"], meta["group_ptr"], meta["group_source"],
+                                                 meta["group_order"], meta["K"], meta["wc"], meta["wr"],
+                                                 meta["d_out"], out=rows[head], trunk=trunks[head])
+        with torch.profiler.record_function("gm::kernel/aggregate"):
+            out = _native.aggregate_heads(rows, st.inv, alpha, meta["row_ptr"])
+        ctx.meta = meta
+        ctx.trunks = trunks
+        ctx.has_bias = trunk_b is not None
+        ctx.save_for_backward(trunk_w, trunk_b if trunk_b is not None else alpha.new_empty(0), alpha, rows, *mixes)
+        return out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx: Any, grad: Tensor) -> tuple:
+        meta = ctx.meta
+        st: GroupedStreams = meta["streams"]
+        trunk_w, trunk_b, alpha, rows, *mixes = ctx.saved_tensors
+        H, E = trunk_w.shape[0], st.rho_g.shape[0]
+        fill = torch.zeros_like if meta["group_source"].shape[0] < meta["n_nodes"] else torch.empty_like
+        dmixes = [fill(m) for m in mixes]
+        dh_g = torch.empty(H, E, 16, dtype=alpha.dtype, device=alpha.device)
+        alpha_gt = _native.gather_transpose(alpha, st.perm)
+        dalpha_gt = torch.empty_like(alpha_gt)
+        grad = grad.contiguous()
+        for head in range(H):
+            runs = _heads_runs(meta, mixes, head, dmixes)
+            with torch.profiler.record_function("gm::kernel/pairs_backward"):
+                _native.factored_backward_grouped(
+                    grad[:, head].contiguous(), st.target_g, alpha_gt[head], rows[head], None, runs, meta["n_nodes"],
+                    st.phase_g, st.rho_g, st.zw_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
+                    meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"], dh_g[head],
+                    dweights=dalpha_gt[head], trunk=ctx.trunks[head])
+        dalpha = _native.scatter_transpose(dalpha_gt, st.perm)
+        with torch.profiler.record_function("gm::kernel/radial_backward"):
+            dw, db = _native.radial_trunk_backward(dh_g, st.rho_g, trunk_w.contiguous(),
+                                                   trunk_b.contiguous() if ctx.has_bias else None,
+                                                   meta["centers_t"], meta["width"])
+        return (dw, db if ctx.has_bias else None, dalpha, None, *dmixes)
+
+
+#: ``GM_FACTORED_TRUNK=1`` evaluates each head's radial trunk inside the lane-owned
+#: kernels instead of a pass of its own: no ``h (H, E, 16)`` or ``dh`` tensor (64 GB at
+#: 256x512, B = 4, 8 heads), at the cost of time -- the lane kernels are issue-bound, so
+#: the recomputation costs more than the round trip it saves (168 vs 155 ms a step there).
+FUSED_TRUNK = os.environ.get("GM_FACTORED_TRUNK", "0") == "1"
+
+
+def _lanes_apply(kernel: Any, hp: HeadsPlan, pa: int, pt: int) -> bool:
+    """Whether the grouped kernels take the lane-owned form for this plan."""
+    key = ("_lanes_apply", pa, pt, os.environ.get("GM_FACTORED_LANES", "1"))
+    hit = kernel.__dict__.get(key)
+    if hit is None:
+        p = hp.plan
+        n_slots, _, _ = _native.lane_tables(torch.tensor([list(r) for r in hp.desc_rows], dtype=torch.int32), p.wc,
+                                            p.wr, p.d_out, pa, pt)
+        hit = n_slots > 0
+        kernel.__dict__[key] = hit
+    return hit
+
+
 def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any, alpha: Tensor, h: Tensor | None,
                              groups: tuple[Tensor, Tensor, Tensor], trunk=None) -> Tensor:
     """Every head's ``forward_factored_aggregated`` at once: ``(N, H, d_out)``.
@@ -643,7 +723,8 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
             mixes = [v @ m.to(v.dtype) for v, m in zip(vecs, mats, strict=True)]
         order, group_ptr, group_source = groups
         st = grouped_streams(edges, order, kernels[0].radial_basis.cutoff, pa, pt, dtype)
-        h_g = trunk(st.rho_g) if trunk is not None else h.index_select(1, st.perm)
+        fused = FUSED_TRUNK and trunk is not None and _lanes_apply(kernels[0], hp, pa, pt)
+        h_g = None if fused else (trunk(st.rho_g) if trunk is not None else h.index_select(1, st.perm))
         if st.group_order is None and os.environ.get("GM_FACTORED_LPT", "0") == "1":
             # the groups largest first: the long pole groups start early instead of trailing the launch
             st.group_order = torch.argsort(group_ptr[1:] - group_ptr[:-1], descending=True, stable=True).contiguous()
@@ -651,6 +732,16 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
                     groups=hp.groups, desc=_heads_desc(kernels[0], hp, x.device), group_ptr=group_ptr,
                     group_source=group_source, row_ptr=edges.row_ptr.contiguous(), streams=st,
                     group_order=st.group_order if os.environ.get("GM_FACTORED_LPT", "0") == "1" else None)
+        if fused:
+            from gm_attention_amd.nn import radial
+
+            w, b, rb = radial.stacked_trunk(kernels)
+            centers = kernels[0].__dict__.get("_centers_host")
+            if centers is None:  # the basis centres are a fixed buffer: one host copy per kernel
+                centers = [float(c) for c in rb.centers.detach().cpu().tolist()]
+                kernels[0].__dict__["_centers_host"] = centers
+            meta.update(centers=centers, centers_t=rb.centers.contiguous(), width=float(rb.width))
+            return FactoredHeadsTrunk.apply(w, b, alpha.to(dtype).contiguous(), meta, *mixes)
         return FactoredHeadsGrouped.apply(h_g.contiguous(), alpha.to(dtype).contiguous(), meta, *mixes)
     if h is None:
         h = trunk((edges.distances / kernels[0].radial_basis.cutoff).to(dtype).contiguous())

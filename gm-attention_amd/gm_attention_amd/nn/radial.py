@@ -61,6 +61,13 @@ class RadialTrunk(torch.autograd.Function):
         return None, dw, db if ctx.has_bias else None, None, None
 
 
+def stacked_trunk(kernels: list[Any]) -> tuple[Tensor, Tensor | None, Any]:
+    """The heads' trunk parameters stacked, ``(W (H, 16, B), b (H, 16) or None)``, and the shared basis."""
+    weight = torch.stack([list(k.radial_trunk)[0].weight for k in kernels])
+    biases = [list(k.radial_trunk)[0].bias for k in kernels]
+    return weight, None if biases[0] is None else torch.stack(biases), kernels[0].radial_basis
+
+
 def trunk_hidden_heads(kernels: list[Any], rho: Tensor) -> Tensor:
     """The stacked heads' trunk features ``(H, E, 16)`` on ``rho = d / cutoff``."""
     weight = torch.stack([list(k.radial_trunk)[0].weight for k in kernels])

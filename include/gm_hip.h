@@ -268,14 +268,25 @@ int gm_factored_backward_seg_f64(const double* g, const int64_t* target, const d
  * keeps the long pole groups off the end of the launch.  No counterpart in
  * the reference, whose kernels index every per-edge table through the
  * grouping (factored_cuda.cu:70-89, 133-248); the results equal those of
- * gm_factored_forward_seg / backward_seg on the permuted streams. */
+ * gm_factored_forward_seg / backward_seg on the permuted streams.
+ *
+ * The fused trunk: with trunk_w (16, trunk_nb) non-NULL, the lane-owned
+ * kernels evaluate h from rho_g themselves -- h_t = SiLU(sum_k W1[t, k] b_k +
+ * b1[t]) over the Gaussian basis b_k = exp(-((rho^2 - c_k) / width)^2 / 2),
+ * trunk_centers (HOST, trunk_nb <= 8) the c_k, trunk_b (16) or NULL -- and h_g
+ * may be NULL (the reference's separate trunk, nn/kernels.py:191-231,
+ * 605-607, then never writes h).  Plans that take the generic grouped kernels
+ * are rejected under it (gm_factored_lane_tables reports which).  dh_g is
+ * still written by the backward. */
 int gm_factored_forward_grouped_f32(const float* h_g, const float* const* z, const int64_t* node_stride,
                                     const int64_t* t_stride, const int64_t* width, int64_t n_runs,
                                     const float* phase_g, const float* rho_g, const float* zw_g,
                                     const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source,
                                     const int64_t* group_order, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
                                     int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
-                                    int64_t d_out, float* rows_g, void* stream);
+                                    int64_t d_out, const float* trunk_w, const float* trunk_b,
+                                    const float* trunk_centers, int64_t trunk_nb, double trunk_width, float* rows_g,
+                                    void* stream);
 int gm_factored_backward_grouped_f32(const float* g, const int64_t* target_g, const float* weights_g,
                                      const float* rows_g, const float* h_g, const float* const* z, float* const* dz,
                                      const int64_t* node_stride, const int64_t* t_stride, const int64_t* width,
@@ -283,7 +294,9 @@ int gm_factored_backward_grouped_f32(const float* g, const int64_t* target_g, co
                                      const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source,
                                      const int64_t* group_order, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
                                      int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
-                                     int64_t d_out, float* dh_g, float* dweights_g, void* stream);
+                                     int64_t d_out, const float* trunk_w, const float* trunk_b,
+                                     const float* trunk_centers, int64_t trunk_nb, double trunk_width, float* dh_g,
+                                     float* dweights_g, void* stream);
 
 /* gm_factored_aggregate with edge e's row at rows[inv[e]] (rows kept in the
  * grouping's order; inv is the grouping's inverse permutation). */

@@ -197,3 +197,21 @@ def test_mhsa_float32_on_the_lane_kernels_matches_the_oracle(case, form, cuda, m
     monkeypatch.setenv("GM_FACTORED_STATIC", "0" if form == "runtime" else "1")
     monkeypatch.setenv("GM_FACTORED_LANES", "0" if form == "generic" else "1")
     test_mhsa_matches_the_oracle(case, torch.float32, True, cuda)
+
+
+@pytest.mark.parametrize("case", LANE_CASES)
+@pytest.mark.parametrize("form", ["fixed", "runtime"])
+def test_mhsa_float32_lanes_with_the_trunk_in_the_kernels_matches_the_oracle(case, form, cuda, monkeypatch):
+    """The lane-owned kernels evaluating each head's radial trunk themselves
+    (GM_FACTORED_TRUNK=1: no h tensor; the trunk's gradient from the dh they
+    write), float32 batched, against the oracle; the plans take the lane form."""
+    from gm_attention_amd.nn import fused_factored
+
+    monkeypatch.setattr(fused_factored, "FUSED_TRUNK", True)
+    monkeypatch.setenv("GM_FACTORED_STATIC", "0" if form == "runtime" else "1")
+    mhsa, _, _ = build(case[0], case[1], "hard", 1)
+    kernel = mhsa.heads[0].value
+    hp = fused_factored.heads_plan(kernel)
+    ok, pa, pt = fused_factored.grouped_eligible(hp, torch.float32, 17)
+    assert ok and fused_factored._lanes_apply(kernel, hp, pa, pt)
+    test_mhsa_matches_the_oracle(case, torch.float32, True, cuda)
