@@ -10,6 +10,11 @@ head's node products, radial trunk and fused factored value aggregation,
 and the output projection.  Inputs and the upstream gradient are N(0, 1),
 resident in HBM before the timed region.
 
+``--workload geometry`` times the GPU build of one 256x512 sample's
+neighbourhoods, CSR and per-edge geometry (float64 lattice membership, tables
+in float64) from the grid's nodes and frames resident on the device; its CPU
+baseline is the host builder (KD-tree + exact filter + torch arithmetic).
+
 ``--workload softmax`` times the scores-and-softmax op alone (forward +
 backward) on the same shape.  ``--workload conv`` times the depthwise steerable
 convolution layer (``SO2Convolution(depthwise=True, n_radial_basis=4)``,
@@ -260,12 +265,96 @@ def cpu_baseline_conv(edges, cutoff, conv_gpu, budget_edges: int):
     return dict(per_edge=dt / sub.n_edges, edges=sub.n_edges, seconds=dt, threads=threads)
 
 
+def run_geometry(args) -> None:
+    """One step = the whole edge-geometry build of one 256x512 sample: degree
+    walk, prefix sum, edge walk (gm_radius_*), then the per-edge tables
+    (gm_edge_tables_f64).  The step reads E back to size the edge list."""
+    import torch
+
+    from gm_attention_amd import _native
+    from gm_attention_amd.discretization import edge_geometry as eg
+    from gm_attention_amd.discretization.frames import build_tangent_frames
+    from gm_attention_amd.discretization.grid import build_equiangular_grid
+
+    device = torch.device("cuda:0")
+    cutoff = 3.0 * math.pi / (NLAT - 1)
+    grid = build_equiangular_grid(NLAT, NLON, device=device)
+    frames = build_tangent_frames(grid.nodes)
+    timer = OpTimer()
+    timer.wrap(_native, "radius_edges", "radius_edges")
+    timer.wrap(_native, "edge_tables", "edge_tables")
+    n_edges = 0
+    for _ in range(args.warmup):
+        n_edges = eg.compute_edge_geometry(grid, frames, cutoff).n_edges
+    torch.cuda.synchronize()
+    timer.enabled = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        n_edges = eg.compute_edge_geometry(grid, frames, cutoff).n_edges
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer.enabled = False
+    ms_per_step = 1e3 * elapsed / args.steps
+    ops = timer.summary(args.steps)
+    log(f"step {ms_per_step:.2f} ms; ops: " + ", ".join(f"{k} {v['ms_per_step']:.2f} ms" for k, v in ops.items()))
+    E, N, K = n_edges, grid.n_nodes, 4
+    # tables: edge_index in (16 B), log map, distance, polar, transport, quadrature and both phase tables out
+    table_bytes = E * (16 + 8 * (2 + 4) + 2 * 16 * (K + 1))
+    avg_s = ops["edge_tables"]["avg_ms"] * 1e-3
+    roof = {"bound": "hbm", "achieved": table_bytes / avg_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    traffic_file = ROOT / "profiles" / "edge_tables_ns_traffic.json"
+    roof["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch") if traffic_file.exists() else None
+    roof["kernel"] = "edge_tables"
+    roof["algorithmic_per_launch"] = {"bytes": table_bytes, "flops": None}
+    roof["note"] = ("radius_edges (the two box walks) is the larger share of the step; it is bound by float64 VALU "
+                    "issue and LDS latency, so neither the HBM nor the MFMA roofline applies to it")
+    baseline = None
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        torch.set_num_threads(threads)
+        host = build_equiangular_grid(NLAT, NLON)
+        hframes = build_tangent_frames(host.nodes)
+        t0 = time.perf_counter()
+        candidates = eg.radius_edges(host.exact_nodes, cutoff, exact=True, workers=threads)
+        keep = eg.geodesic_distances(host.exact_nodes, candidates) <= cutoff + eg.EXACT_SLACK
+        edges_cpu = eg.edge_geometry_from_index(host.nodes, hframes, host.quadrature_weights, candidates[:, keep],
+                                                N, K)
+        seconds = time.perf_counter() - t0
+        baseline = {"value": edges_cpu.n_edges / seconds, "unit": "edges/s", "cores": threads, "kind": "port",
+                    "sample": (f"the host builder on one whole 256x512 sample ({edges_cpu.n_edges} edges): scipy "
+                               f"cKDTree ball query ({threads} workers), float64 exact filter and torch per-edge "
+                               f"arithmetic ({threads} threads) in {seconds:.2f}s")}
+        log(f"cpu baseline: {baseline['value']:.3g} edges/s ({baseline['sample']})")
+    op_rates = {name: {k: round(x, 4) for k, x in v.items()} for name, v in ops.items()}
+    line = {
+        "metric": "edge-geometry build edges/s at 256x512 (one sample)",
+        "value": E / (ms_per_step * 1e-3),
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic: the equiangular grid's nodes, tangent frames and quadrature weights",
+        "config": {"workload": "neighbourhoods within 3 row spacings, CSR and per-edge geometry (max frequency 4)",
+                   "grid": f"{NLAT}x{NLON} equiangular", "nodes": N, "edges": E},
+        "roofline": roof,
+        "ops": op_rates,
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line))
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=("attention", "softmax", "conv"), default="attention")
+    ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry"), default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-edges", type=int, default=200_000)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -287,6 +376,10 @@ def main() -> None:
         print(json.dumps({"error": "this build measures one GPU only: every run here has one MI355X; "
                                    "run with --gpus 1 (the multi-GPU sharding is a design note, not built)"}))
         sys.exit(2)
+
+    if args.workload == "geometry":
+        run_geometry(args)
+        return
 
     import torch
 

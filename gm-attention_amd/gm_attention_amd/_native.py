@@ -67,6 +67,11 @@ SIGNATURES_F32 = {
     "gm_conv_radial_workspace_rows": (ctypes.c_int64, [_I]),
     "gm_conv_radial_forward_f32": (ctypes.c_int, [_P] * 6 + [_I, _D] + [_P] * 6 + [_I] * 7 + [_P] * 4),
     "gm_conv_radial_backward_f32": (ctypes.c_int, [_P] * 8 + [_I, _D] + [_P] * 7 + [_I] * 7 + [_P, _P, _I] + [_P] * 4),
+    "gm_radius_workspace_doubles": (ctypes.c_int64, [_I, _I]),
+    "gm_radius_row_ptr_f64": (ctypes.c_int, [_P, _I, _P, _I, _D, _P, _P, _P]),
+    "gm_radius_edges_f64": (ctypes.c_int, [_P, _I, _P, _I, _D, _P, _P, _I, _P, _P]),
+    "gm_geodesic_distances_f64": (ctypes.c_int, [_P] * 3 + [_I] * 3 + [_P, _P]),
+    "gm_edge_tables_f64": (ctypes.c_int, [_P] * 6 + [_I] * 4 + [_P] * 7 + [_P]),
 }
 
 
@@ -863,3 +868,77 @@ def conv_radial_backward(g: Tensor, v: Tensor, rf: Tensor, rbias: Tensor, rb: Te
           transport.shape[1], int(a0), int(ns), tiles.shape[1], tiles[0].data_ptr(), tiles[1].data_ptr(), n_blocks,
           _ptr(partial), _ptr(dv), _ptr(grad), _stream(v.device))
     return dv, grad
+
+
+# ---------------------------------------------------------------- neighbourhoods and edge geometry
+
+
+def _geo_nodes(x: Tensor, name: str) -> None:
+    _require_device(x)
+    _check(x.dtype == torch.float64 and x.dim() == 2 and x.shape[1] == 3 and x.shape[0] > 0,
+           f"{name} must be a non-empty (n, 3) float64 tensor")
+
+
+def radius_edges(targets: Tensor, sources: Tensor, limit: float) -> tuple[Tensor, Tensor]:
+    """``(edge_index (2, E), row_ptr (n_targets + 1))``: every pair with
+    ``atan2(|p x q|, clamp(<p, q>)) <= limit``, target-major, source-minor."""
+    _geo_nodes(targets, "targets")
+    _geo_nodes(sources, "sources")
+    _check(targets.device == sources.device, "targets and sources must live on the same device")
+    nt, ns = targets.shape[0], sources.shape[0]
+    device = targets.device
+    for x, name in ((targets, "targets"), (sources, "sources")):
+        drift = float(((x * x).sum(dim=1) - 1.0).abs().max())
+        _check(drift <= 1e-14, f"{name} must be unit vectors to 1e-14 (|p|^2 - 1 reaches {drift:.3g})")
+    workspace = torch.empty(int(library().gm_radius_workspace_doubles(nt, ns)), dtype=torch.float64, device=device)
+    row_ptr = torch.empty(nt + 1, dtype=torch.int64, device=device)
+    stream = _stream(device)
+    _call("gm_radius_row_ptr_f64", _ptr(targets), nt, _ptr(sources), ns, float(limit), _ptr(workspace),
+          _ptr(row_ptr), stream)
+    n_edges = int(row_ptr[-1])  # sizes the edge list (one host sync)
+    edge_index = torch.empty(2, n_edges, dtype=torch.int64, device=device)
+    _call("gm_radius_edges_f64", _ptr(targets), nt, _ptr(sources), ns, float(limit), _ptr(workspace), _ptr(row_ptr),
+          n_edges, _ptr(edge_index), stream)
+    return edge_index, row_ptr
+
+
+def geodesic_distances(targets: Tensor, sources: Tensor, edge_index: Tensor) -> Tensor:
+    """``atan2(|p x q|, clamp(<p, q>))`` per edge in float64 (the membership rule's distance)."""
+    _geo_nodes(targets, "targets")
+    _geo_nodes(sources, "sources")
+    _require_device(targets, sources, edge_index)
+    _check(edge_index.dtype == torch.int64 and edge_index.dim() == 2 and edge_index.shape[0] == 2,
+           "edge_index must be a (2, E) int64 tensor")
+    out = torch.empty(edge_index.shape[1], dtype=torch.float64, device=targets.device)
+    _call("gm_geodesic_distances_f64", _ptr(targets), _ptr(sources), _ptr(edge_index), edge_index.shape[1],
+          targets.shape[0], sources.shape[0], _ptr(out), _stream(targets.device))
+    return out
+
+
+def edge_tables(targets: Tensor, target_frames: Tensor, sources: Tensor, source_frames: Tensor,
+                source_quadrature: Tensor, edge_index: Tensor, max_frequency: int) -> dict[str, Tensor]:
+    """Per-edge geometry in float64: ``log_coordinates (E, 2)``, ``distances``,
+    ``polar_angles``, ``transport_angles``, ``tangent_quadrature_weights`` (E)
+    and the phase tables ``(E, K + 1, 2)`` (real, imaginary)."""
+    _geo_nodes(targets, "targets")
+    _geo_nodes(sources, "sources")
+    _require_device(targets, target_frames, sources, source_frames, source_quadrature, edge_index)
+    nt, ns = targets.shape[0], sources.shape[0]
+    _check(target_frames.dtype == torch.float64 and tuple(target_frames.shape) == (nt, 3, 2),
+           "target_frames must be (n_targets, 3, 2) float64")
+    _check(source_frames.dtype == torch.float64 and tuple(source_frames.shape) == (ns, 3, 2),
+           "source_frames must be (n_sources, 3, 2) float64")
+    _check(source_quadrature.dtype == torch.float64 and tuple(source_quadrature.shape) == (ns,),
+           "source_quadrature must be (n_sources,) float64")
+    _check(edge_index.dtype == torch.int64 and edge_index.dim() == 2 and edge_index.shape[0] == 2,
+           "edge_index must be a (2, E) int64 tensor")
+    E, K = edge_index.shape[1], int(max_frequency)
+    kw = dict(dtype=torch.float64, device=targets.device)
+    out = dict(log_coordinates=torch.empty(E, 2, **kw), distances=torch.empty(E, **kw),
+               polar_angles=torch.empty(E, **kw), transport_angles=torch.empty(E, **kw),
+               tangent_quadrature_weights=torch.empty(E, **kw), angular_phases=torch.empty(E, K + 1, 2, **kw),
+               transport_phases=torch.empty(E, K + 1, 2, **kw))
+    _call("gm_edge_tables_f64", _ptr(targets), _ptr(target_frames), _ptr(sources), _ptr(source_frames),
+          _ptr(source_quadrature), _ptr(edge_index), E, nt, ns, K, *(_ptr(t) for t in out.values()),
+          _stream(targets.device))
+    return out

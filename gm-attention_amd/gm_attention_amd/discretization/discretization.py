@@ -13,6 +13,7 @@ import math
 import torch
 from torch import Tensor
 
+from gm_attention_amd.discretization import hip_builder
 from gm_attention_amd.discretization.edge_geometry import (
     DEFAULT_MAX_FREQUENCY,
     EXACT_SLACK,
@@ -47,8 +48,11 @@ class SphericalDiscretization:
             frames = build_tangent_frames(grid.nodes)
         edges = compute_edge_geometry(grid, frames, coverage_radius, max_frequency=max_frequency)
         exact = None if CUTOFF_RULE == "legacy" else grid.exact_nodes
-        return cls(grid, frames, edges, coverage_radius,
-                   None if exact is None else geodesic_distances(exact, edges.edge_index.cpu()))
+        if exact is not None and hip_builder.applies(grid):
+            distances = hip_builder.exact_distances(grid, edges.edge_index)
+        else:
+            distances = None if exact is None else geodesic_distances(exact, edges.edge_index.cpu())
+        return cls(grid, frames, edges, coverage_radius, distances)
 
     @property
     def n_nodes(self) -> int:

@@ -16,6 +16,9 @@ Restates ``discretization/edge_geometry.py`` of the reference:
   ``w_j r / sin r`` (:588-591), ``phi = atan2`` of the log coordinates;
 * ``within_cutoff`` / ``cutoff_tolerance`` / ``GM_CUTOFF_RULE`` (:403-462).
 
+A grid whose nodes are on the GPU is built by ``hip_builder`` (the same edge
+list from the same float64 rule, tables in one HIP pass).
+
 The per-edge arithmetic runs in slices of edges to bound host memory at
 256x512 (elementwise per edge, so the values do not depend on the slicing).
 """
@@ -158,12 +161,14 @@ def geodesic_distances(nodes: Tensor, edge_index: Tensor) -> Tensor:
     return out
 
 
-def radius_edges(nodes: Tensor, coverage_radius: float, *, exact: bool = False) -> Tensor:
-    """Candidate pairs from a KD-tree ball query (float64 CPU), lexsorted
-    target-major, source-minor (reference :656-715)."""
+def radius_edges(nodes: Tensor, coverage_radius: float, *, exact: bool = False, workers: int = -1) -> Tensor:
+    """Candidate pairs from a KD-tree ball query (float64 CPU, ``workers``
+    threads, -1 for every core), lexsorted target-major, source-minor
+    (reference :656-715)."""
     cpu = nodes.detach().to("cpu", torch.float64).numpy()
     tree = cKDTree(cpu)
-    lists = tree.query_ball_point(cpu, r=_query_chord_radius(coverage_radius, nodes.dtype, exact=exact), workers=-1)
+    lists = tree.query_ball_point(cpu, r=_query_chord_radius(coverage_radius, nodes.dtype, exact=exact),
+                                  workers=workers)
     counts = np.fromiter((len(x) for x in lists), dtype=np.int64, count=len(lists))
     targets = np.repeat(np.arange(cpu.shape[0], dtype=np.int64), counts)
     sources = np.concatenate([np.asarray(x, dtype=np.int64) for x in lists]) if len(lists) else np.zeros(0, np.int64)
@@ -220,6 +225,10 @@ def compute_edge_geometry(grid, frames: Tensor, coverage_radius: float, *,
     coverage_radius = float(coverage_radius)
     if not (0.0 < coverage_radius < math.pi):
         raise ValueError(f"coverage_radius must lie in (0, pi), got {coverage_radius}.")
+    from gm_attention_amd.discretization import hip_builder
+
+    if hip_builder.applies(grid):
+        return hip_builder.compute_edge_geometry(grid, frames, coverage_radius, max_frequency=max_frequency)
     nodes = grid.nodes.contiguous()
     exact = None if CUTOFF_RULE == "legacy" else grid.exact_nodes
     edge_index = radius_edges(nodes if exact is None else exact, coverage_radius, exact=exact is not None)

@@ -150,6 +150,90 @@ int gm_conv_backward_f64(const double* g, const double* v, const double* rc, con
                          const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, double* dv,
                          double* drc, double* dcc, void* stream);
 
+/* ---------------- depthwise convolution with in-walk radial heads ----------------
+ *
+ * The depthwise layer's aggregation with its radial trunk and readout heads
+ * evaluated inside the walk from rho = d / cutoff: h = SiLU(W1 b(rho) + b1)
+ * over the Gaussian basis b_k = exp(-((rho^2 - c_k) / width)^2 / 2) (nb = 4, 6
+ * or 8 functions, centers HOST), then per 16-row tile of the packed readout R
+ * the coefficient rows R[:, :16] h + R[:, 16], fed to the same message as
+ * gm_conv_forward_*.  Replaces the reference's per-edge stacked_coefficients
+ * (nn/depthwise.py:206-238) followed by gm_fused_attention.conv_forward
+ * (fused/attention_cpu.cpp:94-115) as nn/convolution.py:432-441 chains them.
+ *   rf (18, 4, 64): R[:, :16] in MFMA A-operand order; rbias (18 * 16): R[:, 16];
+ *   w1 (16, nb), b1 (16) or NULL; ns scalar tiles (a0 = 4..16 ns, multiple of 4),
+ *   nc complex tiles of four copies each (tile_n[m] in {1, 2}, tile_col[m] its
+ *   first flat column; HOST int32 arrays); the tiles cover the flat width D. */
+int64_t gm_conv_radial_partial_row(void);
+int64_t gm_conv_radial_backward_groups(int64_t nc);
+/* Rows (of gm_conv_radial_partial_row() floats) of the backward's workspace. */
+int64_t gm_conv_radial_workspace_rows(int64_t n_blocks);
+int gm_conv_radial_forward_f32(const float* v, const float* rf, const float* rbias, const float* w1, const float* b1,
+                               const float* centers, int64_t nb, double width, const float* transport,
+                               const float* angular, const float* rho, const float* weights, const int64_t* row_ptr,
+                               const int64_t* source, int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders,
+                               int64_t a0, int64_t ns, int64_t nc, const int32_t* tile_n, const int32_t* tile_col,
+                               float* out, void* stream);
+/* dv (n_nodes, D) and grad = (dR in lane order (18 * 256), dR's bias column
+ * (18 * 16), dW1 (16 x 8, row-major, first nb columns live), db1 (16)),
+ * parameter gradients reduced over n_blocks (a multiple of 8 in 8..65536)
+ * persistent workgroups in a fixed order through `partial`
+ * (gm_conv_radial_workspace_rows(n_blocks) rows).  src_ptr, src_order, target
+ * as for gm_softmax_backward_*; rb (18, 4, 64): R[:, :16] in B-operand order.
+ * Replaces the readout and trunk gradients of the reference's torch autograd
+ * through stacked_coefficients plus gm_fused_attention.conv_backward
+ * (fused/attention_cpu.cpp:118-145). */
+int gm_conv_radial_backward_f32(const float* g, const float* v, const float* rf, const float* rbias, const float* rb,
+                                const float* w1, const float* b1, const float* centers, int64_t nb, double width,
+                                const float* transport, const float* angular, const float* rho, const float* weights,
+                                const int64_t* src_ptr, const int64_t* src_order, const int64_t* target,
+                                int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t a0, int64_t ns,
+                                int64_t nc, const int32_t* tile_n, const int32_t* tile_col, int64_t n_blocks,
+                                float* partial, float* dv, float* grad, void* stream);
+
+/* ---------------- neighbourhoods, CSR and per-edge geometry ----------------
+ *
+ * Paths in this section are relative to src/gm_attention/.
+ * targets (n_targets, 3) and sources (n_sources, 3) are float64 unit vectors,
+ * | |p|^2 - 1 | <= 1e-14 (the self graph passes one node set twice).  Target i and source j are
+ * neighbours iff atan2(|p_i x q_j|, clamp(<p_i, q_j>, -1, 1)) <= limit, each
+ * product rounded on its own (limit = r + 1e-10 under the whole-shell rule).
+ *
+ * Replaces _compute_radius_edges (discretization/edge_geometry.py:656-715: KD-tree ball
+ * query and lexsort), the exact filter of compute_edge_geometry (:381-387) and
+ * _build_row_ptr (:622-653): step one writes row_ptr (n_targets + 1); the
+ * caller reads E = row_ptr[n_targets], sizes edge_index (2, E) and calls step
+ * two, which writes targets in row 0 and sources in row 1, target-major,
+ * source-minor.  workspace: gm_radius_workspace_doubles(n_targets, n_sources)
+ * doubles, kept between the two steps. */
+int64_t gm_radius_workspace_doubles(int64_t n_targets, int64_t n_sources);
+int gm_radius_row_ptr_f64(const double* targets, int64_t n_targets, const double* sources, int64_t n_sources,
+                          double limit, double* workspace, int64_t* row_ptr, void* stream);
+int gm_radius_edges_f64(const double* targets, int64_t n_targets, const double* sources, int64_t n_sources,
+                        double limit, const double* workspace, const int64_t* row_ptr, int64_t n_edges,
+                        int64_t* edge_index, void* stream);
+
+/* The membership distance of each edge, float64 (_geodesic_distances,
+ * discretization/edge_geometry.py:492-503).  An index out of range yields NaN. */
+int gm_geodesic_distances_f64(const double* targets, const double* sources, const int64_t* edge_index,
+                              int64_t n_edges, int64_t n_targets, int64_t n_sources, double* distances, void* stream);
+
+/* The per-edge tables of edge_geometry_from_index
+ * (discretization/edge_geometry.py:506-619):
+ * log_coordinates (E, 2) = F_i^T (d / sin d)(q - <p, q> p); distances (E);
+ * polar_angles = atan2 of the log coordinates; transport_angles = atan2 of
+ * column 0 of F_i^T R F_j with R = I + K + K^2 / (1 + <q, p>), K = [q x p]_x
+ * (:718-771, :574-585); tangent_quadrature (E) = w_j d / sin d (:588-591);
+ * angular_phases and transport_phases (E, max_frequency + 1, 2) = (cos, sin)
+ * of k times the angle (phase_powers, representations/so2.py:167-213).
+ * Frames (n, 3, 2) hold e1, e2 as columns.  An index out of range yields a
+ * row of NaN. */
+int gm_edge_tables_f64(const double* targets, const double* target_frames, const double* sources,
+                       const double* source_frames, const double* source_quadrature, const int64_t* edge_index,
+                       int64_t n_edges, int64_t n_targets, int64_t n_sources, int64_t max_frequency,
+                       double* log_coordinates, double* distances, double* polar_angles, double* transport_angles,
+                       double* tangent_quadrature, double* angular_phases, double* transport_phases, void* stream);
+
 /* ---------------- factored steerable kernel ----------------
  *
  * Per edge e = (i <- j) with h~ = (1, h(e)): every block b's combination

@@ -16,21 +16,24 @@ def geodesic(p: np.ndarray, q: np.ndarray) -> np.ndarray:
     return np.arctan2(np.linalg.norm(np.cross(p, q), axis=-1), dot)
 
 
-def brute_force_edges(nodes: np.ndarray, radius: float, slack: float = 1e-10) -> np.ndarray:
-    """All pairs ``(i, j)`` with ``d(p_i, p_j) <= radius + slack`` from float64
+def brute_force_edges(nodes: np.ndarray, radius: float, slack: float = 1e-10,
+                      sources: np.ndarray | None = None) -> np.ndarray:
+    """All pairs ``(i, j)`` with ``d(p_i, q_j) <= radius + slack`` from float64
     coordinates, ordered target-major, source-minor: the membership rule of
     edge_geometry.py:381-387 decided with no tree (as the reference's
-    tests/discretization/test_neighborhoods.py:41-73 checks it)."""
+    tests/discretization/test_neighborhoods.py:41-73 checks it).  ``sources``
+    (default: the targets themselves) gives a bipartite neighbourhood."""
     n = nodes.shape[0]
-    targets, sources = [], []
+    src = nodes if sources is None else sources
+    targets, sources_out = [], []
     for lo in range(0, n, 256):
         hi = min(n, lo + 256)
-        d = geodesic(nodes[lo:hi, None, :], nodes[None, :, :])
+        d = geodesic(nodes[lo:hi, None, :], src[None, :, :])
         t, s = np.nonzero(d <= radius + slack)
         targets.append(t + lo)
-        sources.append(s)
+        sources_out.append(s)
     t = np.concatenate(targets)
-    s = np.concatenate(sources)
+    s = np.concatenate(sources_out)
     order = np.lexsort((s, t))
     return np.stack([t[order], s[order]])
 

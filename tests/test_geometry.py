@@ -92,3 +92,22 @@ def test_edge_geometry_closed_forms():
     assert float(d[loops].abs().max()) < 1e-15
     assert float(edges.log_coordinates[loops].abs().max()) < 1e-15
     assert float(edges.transport_angles[loops].abs().max()) < 1e-15
+
+
+def test_gpu_builder_routing_and_errors_on_the_host():
+    """Grids on the CPU keep the host builder; the GPU builder refuses the legacy
+    rule and host tensors with a message instead of computing anything."""
+    from gm_attention_amd import _native
+    from gm_attention_amd.discretization import hip_builder
+
+    grid = build_equiangular_grid(4, 6)
+    assert not hip_builder.applies(grid)
+    nodes = grid.exact_nodes
+    with pytest.raises(RuntimeError, match="GPU only"):
+        _native.radius_edges(nodes, nodes, 0.5)
+
+    class NoLattice:
+        exact_nodes = None
+
+    with pytest.raises(ValueError, match="float64 lattice"):
+        hip_builder._lattice(NoLattice(), torch.device("cpu"))

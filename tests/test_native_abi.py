@@ -31,6 +31,8 @@ def test_library_exports_every_declared_symbol():
     assert lib.gm_abi_version() == 1
     for stem in _native.SIGNATURES:
         assert stem + "_f32" in declared() and stem + "_f64" in declared()
+    undeclared = sorted(set(_native.SIGNATURES_F32) - declared())
+    assert not undeclared, undeclared
 
 
 def test_errors_are_reported_not_raised_through_the_abi():
