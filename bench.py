@@ -15,6 +15,13 @@ neighbourhoods, CSR and per-edge geometry (float64 lattice membership, tables
 in float64) from the grid's nodes and frames resident on the device; its CPU
 baseline is the host builder (KD-tree + exact filter + torch arithmetic).
 
+``--workload block`` runs the C4 configuration: one
+``SO2TransformerBlock(ffn_multiplier=4)`` (pre-norm: batched 8-head SO2MHSA,
+then the 160 -> 640 -> 160 gated feed-forward), forward + backward with every
+gradient, at 256x512, batch 2, with bfloat16 rows (residual stream, norms,
+gate, feed-forward GEMMs) and float32 parameters; the attention's kernels
+compute in float32.
+
 ``--workload softmax`` times the scores-and-softmax op alone (forward +
 backward) on the same shape.  ``--workload conv`` times the depthwise steerable
 convolution layer (``SO2Convolution(depthwise=True, n_radial_basis=4)``,
@@ -140,7 +147,7 @@ class OpTimer:
 # ---------------------------------------------------------------- problem
 
 
-def build_edges(device):
+def build_edges(device, batch: int = BATCH):
     import torch
 
     from gm_attention_amd.discretization.edge_geometry import compute_edge_geometry
@@ -152,7 +159,7 @@ def build_edges(device):
     grid = build_equiangular_grid(NLAT, NLON)
     edges = compute_edge_geometry(grid, build_tangent_frames(grid.nodes), cutoff)
     log(f"geometry {NLAT}x{NLON}: {edges.n_edges} edges per sample in {time.time() - t0:.1f}s")
-    tiled = edges.to(device, torch.float32).tile(BATCH, n_sources=grid.n_nodes)
+    tiled = edges.to(device, torch.float32).tile(batch, n_sources=grid.n_nodes)
     return edges, tiled, cutoff
 
 
@@ -219,6 +226,40 @@ def cpu_baseline_attention(edges, cutoff, mhsa_gpu, budget_edges: int):
     per_edge = (t2 - t1) / (e2 - e1)
     per_sample_nodes = max(0.0, t1 - per_edge * e1)
     return dict(per_edge=per_edge, per_sample_nodes=per_sample_nodes, points=points, threads=threads, cpu_s=t1 + t2)
+
+
+def cpu_baseline_ffn(block_gpu, n_nodes: int):
+    """The block's node-wise part (both layer norms, the two SO2Linear layers and
+    the gate, oracle.modules) forward + backward in float32 on the host's cores
+    (at most 16 threads) over one 256x512 sample's nodes: seconds per sample."""
+    import torch
+
+    from gm_attention_amd.nn.blocks import SO2TransformerBlock
+    from gm_attention_amd.representations.field_type import SO2FeatureField
+    from oracle import modules
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    ft = block_gpu.field_type
+    block = SO2TransformerBlock(ft, HEADS, ffn_multiplier=4, cutoff=1.0, attention_batched=True, dtype=torch.float32)
+    block.load_state_dict({k: v.detach().cpu() for k, v in block_gpu.state_dict().items()})
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(n_nodes, ft.dimension, generator=gen).requires_grad_(True)
+    g = torch.randn(n_nodes, ft.dimension, generator=gen)
+
+    def step():
+        xs = SO2FeatureField.from_flat(ft, x).coefficients
+        a = modules.layer_norm(block.norm1, xs)
+        h = modules.linear(block.linear1, modules.layer_norm(block.norm2, a), block.hidden_field_type)
+        out = modules.flat(modules.linear(block.linear2, modules.gated(block.activation, h), ft))
+        (out * g).sum().backward()
+        x.grad = None
+        block.zero_grad(set_to_none=True)
+
+    step()
+    t0 = time.perf_counter()
+    step()
+    return time.perf_counter() - t0, threads
 
 
 def cpu_baseline_conv(edges, cutoff, conv_gpu, budget_edges: int):
@@ -354,7 +395,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry"), default="attention")
+    ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry", "block"), default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-edges", type=int, default=200_000)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -410,7 +451,10 @@ def main() -> None:
         timer.wrap(_native, "conv_radial_forward", "conv_radial_forward")
         timer.wrap(_native, "conv_radial_backward", "conv_radial_backward")
 
-    edges_cpu, edges, cutoff = build_edges(device)
+    batch = 2 if args.workload == "block" else BATCH
+    for name in ("layer_norm_forward", "layer_norm_backward", "gate_forward", "gate_backward"):
+        timer.wrap(_native, name, name)
+    edges_cpu, edges, cutoff = build_edges(device, batch)
     N = edges.row_ptr.shape[0] - 1
     E = edges.n_edges
     field = SO2FieldType(FIELD)
@@ -424,7 +468,24 @@ def main() -> None:
     log(f"problem: N={N} E={E} D={D} H={HEADS} max_degree={g.max_degree}")
     module = mhsa  # the module whose parameter gradients the loop clears
 
-    if args.workload == "attention":
+    if args.workload == "block":
+        from gm_attention_amd.nn.blocks import SO2TransformerBlock
+
+        torch.manual_seed(0)
+        block = SO2TransformerBlock(field, HEADS, ffn_multiplier=4, cutoff=cutoff, window="hard",
+                                    attention_batched=True, dtype=torch.float32, device=device)
+        module = block
+        mhsa = block.attention
+        x_flat = x_flat.detach().to(torch.bfloat16).requires_grad_(True)
+        upstream = upstream.to(torch.bfloat16)
+
+        def step():
+            y = block.forward_flat(x_flat, edges)
+            torch.autograd.backward(y, upstream)
+        workload = ("SO2TransformerBlock(ffn_multiplier=4) fwd+bwd: layer norm, batched 8-head SO2MHSA (float32 "
+                    "kernels), residual, layer norm, SO2Linear 160->640 (bf16 GEMM), scalar gate (double sigmoid), "
+                    "SO2Linear 640->160, residual; bf16 rows, float32 parameters; input and every parameter gradient")
+    elif args.workload == "attention":
         def step():
             x = SO2FeatureField.from_flat(field, x_flat)
             y = mhsa(x, edges).to_flat()
@@ -498,10 +559,19 @@ def main() -> None:
     else:
         roof = {"bound": "mfma", "achieved": flops / avg_s / 1e12, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s"}
     roof["frac"] = roof["achieved"] / roof["peak"]
-    traffic_file = ROOT / "profiles" / f"{dominant}_ns_traffic.json"
+    traffic_file = ROOT / "profiles" / f"{dominant}_{'c4' if args.workload == 'block' else 'ns'}_traffic.json"
     roof["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch") if traffic_file.exists() else None
     roof["kernel"] = dominant
     roof["algorithmic_per_launch"] = {"bytes": nbytes, "flops": flops}
+    # pointwise block operators: bytes of the rows (and gate pre-activations) each reads and writes
+    rb = 2 if args.workload == "block" else 4
+    if args.workload == "block":
+        hd = block.hidden_field_type.dimension
+        G = sum(m for n, m in block.hidden_field_type.items() if n != 0)
+        costs["layer_norm_forward"] = (N * D * 2 * rb + 8 * N, 0.0)
+        costs["layer_norm_backward"] = (N * D * 3 * rb + 8 * N, 0.0)
+        costs["gate_forward"] = (N * (2 * hd + G) * rb, 0.0)
+        costs["gate_backward"] = (N * (3 * hd + 2 * G) * rb, 0.0)
     op_rates = {}
     for name, v in ops.items():
         b, f = costs[name]
@@ -511,14 +581,27 @@ def main() -> None:
     baseline = None
     if not args.no_cpu_baseline and args.workload == "attention":
         b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges)
-        cpu_step = b["per_sample_nodes"] * BATCH + b["per_edge"] * E
+        cpu_step = b["per_sample_nodes"] * batch + b["per_edge"] * E
         (e1, t1), (e2, t2) = b["points"]
         baseline = {"value": N / cpu_step, "unit": "query-points/s", "cores": b["threads"], "kind": "port",
                     "sample": (f"oracle eager SO2MHSA fwd+bwd (factored order, float32, torch on {b['threads']} "
                                f"threads) on one 256x512 sample's nodes with the edges of its first (pole) targets "
                                f"and equator rows: {e1} edges in {t1:.2f}s, {e2} edges in {t2:.2f}s; the fit "
                                f"{b['per_sample_nodes']:.2f}s per sample's nodes + {b['per_edge'] * 1e6:.1f}us per "
-                               f"edge, extrapolated to {BATCH} samples and {E} edges")}
+                               f"edge, extrapolated to {batch} samples and {E} edges")}
+        log(f"cpu baseline: {baseline['value']:.1f} qp/s ({baseline['sample']})")
+    elif not args.no_cpu_baseline and args.workload == "block":
+        b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges)
+        ffn_s, _ = cpu_baseline_ffn(block, N // batch)
+        cpu_step = (b["per_sample_nodes"] + ffn_s) * batch + b["per_edge"] * E
+        (e1, t1), (e2, t2) = b["points"]
+        baseline = {"value": N / cpu_step, "unit": "query-points/s", "cores": b["threads"], "kind": "port",
+                    "sample": (f"oracle eager block fwd+bwd in float32 (torch on {b['threads']} threads): the "
+                               f"SO2MHSA as in the attention workload ({e1} edges in {t1:.2f}s, {e2} edges in "
+                               f"{t2:.2f}s; {b['per_sample_nodes']:.2f}s per sample's nodes + "
+                               f"{b['per_edge'] * 1e6:.1f}us per edge) plus both layer norms, the feed-forward and "
+                               f"the gate over one sample's {N // batch} nodes in {ffn_s:.2f}s, extrapolated to "
+                               f"{batch} samples and {E} edges")}
         log(f"cpu baseline: {baseline['value']:.1f} qp/s ({baseline['sample']})")
     elif not args.no_cpu_baseline and args.workload == "conv":
         b = cpu_baseline_conv(edges_cpu, cutoff, conv, args.cpu_budget_edges)
@@ -532,7 +615,8 @@ def main() -> None:
     line = {
         "metric": {"attention": "attn fwd+bwd query-points/s at 256x512 B=4",
                    "softmax": "attn scores+softmax fwd+bwd query-points/s at 256x512 B=4",
-                   "conv": "depthwise conv fwd+bwd query-points/s at 256x512 B=4"}[args.workload],
+                   "conv": "depthwise conv fwd+bwd query-points/s at 256x512 B=4",
+                   "block": "transformer block fwd+bwd query-points/s at 256x512 B=2"}[args.workload],
         "value": N / (ms_per_step * 1e-3),
         "unit": "query-points/s",
         "n_gpus": 1,
@@ -542,9 +626,9 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16" if args.workload == "block" else "f32",
         "data": "synthetic: N(0,1) input field and upstream gradient, random-init weights, equiangular grid geometry",
-        "config": {"workload": workload, "grid": f"{NLAT}x{NLON} equiangular", "batch": BATCH,
+        "config": {"workload": workload, "grid": f"{NLAT}x{NLON} equiangular", "batch": batch,
                    "field": "{0:32,1:32,2:32}", "heads": HEADS, "radius": "3 row spacings", "window": "hard",
                    "query_points": N, "edges": E, "max_degree": g.max_degree},
         "roofline": roof,

@@ -72,6 +72,15 @@ SIGNATURES_F32 = {
     "gm_radius_edges_f64": (ctypes.c_int, [_P, _I, _P, _I, _D, _P, _P, _I, _P, _P]),
     "gm_geodesic_distances_f64": (ctypes.c_int, [_P] * 3 + [_I] * 3 + [_P, _P]),
     "gm_edge_tables_f64": (ctypes.c_int, [_P] * 6 + [_I] * 4 + [_P] * 7 + [_P]),
+    "gm_layer_norm_partial_rows": (ctypes.c_int64, [_I]),
+    **{f"gm_layer_norm_forward_{sfx}": (ctypes.c_int, [_P] * 3 + [_I] * 4 + [_P, _P, _D] + [_P] * 4)
+       for sfx in ("f32", "f64", "bf16")},
+    **{f"gm_layer_norm_backward_{sfx}": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_P] * 2 + [_P] * 4)
+       for sfx in ("f32", "f64", "bf16")},
+    **{f"gm_gate_forward_{sfx}": (ctypes.c_int, [_P] * 2 + [_I] * 4 + [_P, _P, _I, _P, _P])
+       for sfx in ("f32", "f64", "bf16")},
+    **{f"gm_gate_backward_{sfx}": (ctypes.c_int, [_P] * 3 + [_I] * 4 + [_P, _P, _I] + [_P] * 3)
+       for sfx in ("f32", "f64", "bf16")},
 }
 
 
@@ -942,3 +951,96 @@ def edge_tables(targets: Tensor, target_frames: Tensor, sources: Tensor, source_
           _ptr(source_quadrature), _ptr(edge_index), E, nt, ns, K, *(_ptr(t) for t in out.values()),
           _stream(targets.device))
     return out
+
+
+# ---------------------------------------------------------------- transformer block pointwise operators
+
+
+_PW_SUFFIX = {torch.float32: "f32", torch.float64: "f64", torch.bfloat16: "bf16"}
+
+
+class PointwiseLayout:
+    """A field type's flat layout as the pointwise entry points take it (host arrays)."""
+
+    def __init__(self, field_type: Any):
+        self.D = field_type.dimension
+        self.a0 = field_type.multiplicity(0) if 0 in field_type else 0
+        nonzero = [(n, field_type.multiplicity(n)) for n in field_type.frequencies if n != 0]
+        slices = field_type.slices()
+        self.nf = len(nonzero)
+        self.offsets = (ctypes.c_int64 * max(1, self.nf))(*[slices[n].start for n, _ in nonzero])
+        self.mults = (ctypes.c_int64 * max(1, self.nf))(*[m for _, m in nonzero])
+        self.G = sum(m for _, m in nonzero)
+
+    def args(self) -> tuple:
+        return (self.D, self.a0, self.nf, ctypes.cast(self.offsets, _P), ctypes.cast(self.mults, _P))
+
+
+def param_dtype(dtype: torch.dtype) -> torch.dtype:
+    """The parameter (and statistics) dtype of the pointwise entry points for rows of ``dtype``."""
+    return torch.float64 if dtype == torch.float64 else torch.float32
+
+
+def _pw_check(x: Tensor, layout: PointwiseLayout) -> str:
+    _require_device(x)
+    _check(x.dtype in _PW_SUFFIX, f"the pointwise operators take float32, float64 or bfloat16 rows, got {x.dtype}")
+    _check(x.dim() == 2 and x.shape[1] == layout.D, f"rows must be (n_nodes, {layout.D})")
+    return _PW_SUFFIX[x.dtype]
+
+
+def layer_norm_forward(x: Tensor, gamma: Tensor, beta: Tensor | None, layout: PointwiseLayout,
+                       eps: float) -> tuple[Tensor, Tensor, Tensor]:
+    """``(y, mean, inv_d)``: the merged equivariant layer normalization of the rows ``x``."""
+    sfx = _pw_check(x, layout)
+    pd = param_dtype(x.dtype)
+    _require_device(x, gamma, *(() if beta is None else (beta,)))
+    _check(gamma.dtype == pd and gamma.shape == (layout.D,), f"gamma must be ({layout.D},) {pd}")
+    _check(beta is None or (beta.dtype == pd and beta.shape == (layout.a0,)), f"beta must be ({layout.a0},) {pd}")
+    n = x.shape[0]
+    y = torch.empty_like(x)
+    mean = torch.empty(n, dtype=pd, device=x.device)
+    inv_d = torch.empty(n, dtype=pd, device=x.device)
+    _call(f"gm_layer_norm_forward_{sfx}", _ptr(x), _ptr(gamma), _ptr(beta), n, *layout.args(), float(eps), _ptr(y),
+          _ptr(mean), _ptr(inv_d), _stream(x.device))
+    return y, mean, inv_d
+
+
+def layer_norm_backward(gy: Tensor, x: Tensor, gamma: Tensor, mean: Tensor, inv_d: Tensor,
+                        layout: PointwiseLayout) -> tuple[Tensor, Tensor]:
+    """``(dx, dparams)`` with ``dparams = (dgamma (D), dbeta (a0))`` summed over the nodes in a fixed order."""
+    sfx = _pw_check(x, layout)
+    _require_device(gy, x, gamma, mean, inv_d)
+    _check(gy.dtype == x.dtype and gy.shape == x.shape, "gy must match x")
+    pd = param_dtype(x.dtype)
+    n = x.shape[0]
+    rows = int(library().gm_layer_norm_partial_rows(n))
+    partial = torch.empty(rows, layout.D + layout.a0, dtype=pd, device=x.device)
+    dparams = torch.empty(layout.D + layout.a0, dtype=pd, device=x.device)
+    dx = torch.empty_like(x)
+    _call(f"gm_layer_norm_backward_{sfx}", _ptr(gy), _ptr(x), _ptr(gamma), _ptr(mean), _ptr(inv_d), n, *layout.args(),
+          _ptr(dx), _ptr(partial), _ptr(dparams), _stream(x.device))
+    return dx, dparams
+
+
+def gate_forward(h: Tensor, pre: Tensor, layout: PointwiseLayout, double_sigmoid: bool) -> Tensor:
+    """SiLU on the scalar entries, every copy scaled by its gate ``act(pre)``."""
+    sfx = _pw_check(h, layout)
+    _require_device(h, pre)
+    _check(pre.dtype == h.dtype and tuple(pre.shape) == (h.shape[0], layout.G), f"pre must be (n_nodes, {layout.G})")
+    y = torch.empty_like(h)
+    _call(f"gm_gate_forward_{sfx}", _ptr(h), _ptr(pre), h.shape[0], *layout.args(), int(double_sigmoid), _ptr(y),
+          _stream(h.device))
+    return y
+
+
+def gate_backward(gy: Tensor, h: Tensor, pre: Tensor, layout: PointwiseLayout,
+                  double_sigmoid: bool) -> tuple[Tensor, Tensor]:
+    """``(dh, dpre)``: the gate's direct gradient and the pre-activations' gradient."""
+    sfx = _pw_check(h, layout)
+    _require_device(gy, h, pre)
+    _check(gy.dtype == h.dtype and gy.shape == h.shape, "gy must match h")
+    dh = torch.empty_like(h)
+    dpre = torch.empty_like(pre)
+    _call(f"gm_gate_backward_{sfx}", _ptr(gy), _ptr(h), _ptr(pre), h.shape[0], *layout.args(), int(double_sigmoid),
+          _ptr(dh), _ptr(dpre), _stream(h.device))
+    return dh, dpre

@@ -71,6 +71,54 @@ def complex_as_real(weight: Tensor) -> Tensor:
     return torch.stack([from_real, from_imag], dim=1).reshape(2 * a, 2 * b)
 
 
+class FlatLinear(torch.autograd.Function):
+    """``x @ M + bias`` on flat rows with ``M (D_in, D_out)`` the layer's
+    block-diagonal matrix: one GEMM (bias in its epilogue) straight between
+    the flat layouts.  ``M`` and the bias stay in the parameters' dtype and are
+    rounded to the rows' dtype for the product (bfloat16 rows: a bfloat16 GEMM
+    with float accumulation); their gradients come back in the parameters'
+    dtype: the blocked ``x^T g`` and the bias's column sums."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, m: Tensor, bias_flat: Tensor | None) -> Tensor:
+        ctx.save_for_backward(x, m)
+        ctx.has_bias = bias_flat is not None
+        mx = m.to(x.dtype)
+        return torch.addmm(bias_flat.to(x.dtype), x, mx) if bias_flat is not None else x @ mx
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        x, m = ctx.saved_tensors
+        g = g.contiguous()
+        dx = g @ m.t().to(g.dtype) if ctx.needs_input_grad[0] else None
+        dm = None
+        if ctx.needs_input_grad[1]:
+            dm = blocked_gram(x.to(m.dtype), g.to(m.dtype), RowsMatmul.BLOCK)
+        db = g.sum(0, dtype=m.dtype) if ctx.has_bias else None
+        return dx, dm, db
+
+
+def block_matrix(lin: "SO2Linear") -> Tensor:
+    """The layer as one ``(D_in, D_out)`` matrix acting on flat rows (zero off its frequency blocks)."""
+    fin, fout = lin.field_type_in, lin.field_type_out
+    sin, sout = fin.slices(), fout.slices()
+    ref = next(iter(lin.weight.values()))
+    m = ref.new_zeros(fin.dimension, fout.dimension)
+    for f in lin.common_frequencies:
+        w = lin.weight[str(f)]
+        m[sin[f], sout[f]] = w.T if f == 0 else complex_as_real(w)
+    return m
+
+
+def flat_forward(lin: "SO2Linear", flat: Tensor) -> Tensor:
+    """``lin`` on flat rows ``(N, D_in)`` -> ``(N, D_out)``."""
+    bias = None
+    if lin.has_bias:
+        b0 = lin.field_type_out.multiplicity(0)
+        bias = torch.cat([lin.bias, lin.bias.new_zeros(lin.field_type_out.dimension - b0)])
+    return FlatLinear.apply(flat, block_matrix(lin), bias)
+
+
 class SO2Linear(nn.Module):
     def __init__(self, field_type_in: SO2FieldType, field_type_out: SO2FieldType, *, bias: bool = True, dtype=None,
                  device=None) -> None:

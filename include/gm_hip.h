@@ -234,6 +234,71 @@ int gm_edge_tables_f64(const double* targets, const double* target_frames, const
                        double* log_coordinates, double* distances, double* polar_angles, double* transport_angles,
                        double* tangent_quadrature, double* angular_phases, double* transport_phases, void* stream);
 
+/* ---------------- transformer block pointwise operators ----------------
+ *
+ * Flat node rows of width D: frequency 0 in [0, a0), then the nf nonzero
+ * frequencies' copies as (re, im) pairs at [offsets[f], offsets[f] + 2 mults[f])
+ * (HOST arrays, contiguous after frequency 0, D <= 1024).  Suffixes: _f32
+ * (float rows, float parameters), _f64 (double, double), _bf16 (bfloat16 rows
+ * as uint16_t, float parameters and float arithmetic).
+ *
+ * Merged equivariant layer normalization; replaces SO2LayerNorm.forward
+ * (nn/normalization.py:150-190): mu = mean x0, v0 = mean (x0 - mu)^2,
+ * vn = mean_a |x_n,a|^2 / 2, d = sqrt(mean_present v + eps),
+ * y = gamma (x - mu [frequency 0]) / d + beta [frequency 0].  gamma (D) is
+ * per coordinate (a copy's gain repeated for re and im), beta (a0) or NULL.
+ * Writes y and per node mean and inv_d = 1 / d for the backward. */
+int gm_layer_norm_forward_f32(const float* x, const float* gamma, const float* beta, int64_t n_nodes, int64_t D,
+                              int64_t a0, int64_t nf, const int64_t* offsets, const int64_t* mults, double eps,
+                              float* y, float* mean, float* inv_d, void* stream);
+int gm_layer_norm_forward_f64(const double* x, const double* gamma, const double* beta, int64_t n_nodes, int64_t D,
+                              int64_t a0, int64_t nf, const int64_t* offsets, const int64_t* mults, double eps,
+                              double* y, double* mean, double* inv_d, void* stream);
+int gm_layer_norm_forward_bf16(const uint16_t* x, const float* gamma, const float* beta, int64_t n_nodes, int64_t D,
+                               int64_t a0, int64_t nf, const int64_t* offsets, const int64_t* mults, double eps,
+                               uint16_t* y, float* mean, float* inv_d, void* stream);
+/* dx (n_nodes, D) and dparams (D + a0) = (dgamma per coordinate, dbeta), the
+ * parameter gradients summed over the nodes in a fixed order through
+ * `partial` (gm_layer_norm_partial_rows(n_nodes) rows of D + a0). */
+int64_t gm_layer_norm_partial_rows(int64_t n_nodes);
+int gm_layer_norm_backward_f32(const float* gy, const float* x, const float* gamma, const float* mean,
+                               const float* inv_d, int64_t n_nodes, int64_t D, int64_t a0, int64_t nf,
+                               const int64_t* offsets, const int64_t* mults, float* dx, float* partial, float* dparams,
+                               void* stream);
+int gm_layer_norm_backward_f64(const double* gy, const double* x, const double* gamma, const double* mean,
+                               const double* inv_d, int64_t n_nodes, int64_t D, int64_t a0, int64_t nf,
+                               const int64_t* offsets, const int64_t* mults, double* dx, double* partial,
+                               double* dparams, void* stream);
+int gm_layer_norm_backward_bf16(const uint16_t* gy, const uint16_t* x, const float* gamma, const float* mean,
+                                const float* inv_d, int64_t n_nodes, int64_t D, int64_t a0, int64_t nf,
+                                const int64_t* offsets, const int64_t* mults, uint16_t* dx, float* partial,
+                                float* dparams, void* stream);
+
+/* Scalar-gated nonlinearity; replaces SO2ScalarGatedNonlinearity.forward after
+ * its gate Linear layers (nn/nonlinearities.py:140-166): y0 = SiLU(h0), and
+ * copy a of the f-th nonzero frequency times act(pre[node, g_f + a]) on both
+ * coordinates, act = SiLU or, with double_sigmoid, 2 sigmoid; pre (n_nodes, G)
+ * holds the gates' pre-activations, frequency-major (g_f = sum of the earlier
+ * multiplicities).  Backward: dh = the direct part (SiLU'(h0) gy0, act gy_n)
+ * and dpre = act'(pre) <gy_n, h_n>; the gate Linear's own gradient is the
+ * caller's. */
+int gm_gate_forward_f32(const float* h, const float* pre, int64_t n_nodes, int64_t D, int64_t a0, int64_t nf,
+                        const int64_t* offsets, const int64_t* mults, int64_t double_sigmoid, float* y, void* stream);
+int gm_gate_forward_f64(const double* h, const double* pre, int64_t n_nodes, int64_t D, int64_t a0, int64_t nf,
+                        const int64_t* offsets, const int64_t* mults, int64_t double_sigmoid, double* y, void* stream);
+int gm_gate_forward_bf16(const uint16_t* h, const uint16_t* pre, int64_t n_nodes, int64_t D, int64_t a0, int64_t nf,
+                         const int64_t* offsets, const int64_t* mults, int64_t double_sigmoid, uint16_t* y,
+                         void* stream);
+int gm_gate_backward_f32(const float* gy, const float* h, const float* pre, int64_t n_nodes, int64_t D, int64_t a0,
+                         int64_t nf, const int64_t* offsets, const int64_t* mults, int64_t double_sigmoid, float* dh,
+                         float* dpre, void* stream);
+int gm_gate_backward_f64(const double* gy, const double* h, const double* pre, int64_t n_nodes, int64_t D, int64_t a0,
+                         int64_t nf, const int64_t* offsets, const int64_t* mults, int64_t double_sigmoid, double* dh,
+                         double* dpre, void* stream);
+int gm_gate_backward_bf16(const uint16_t* gy, const uint16_t* h, const uint16_t* pre, int64_t n_nodes, int64_t D,
+                          int64_t a0, int64_t nf, const int64_t* offsets, const int64_t* mults, int64_t double_sigmoid,
+                          uint16_t* dh, uint16_t* dpre, void* stream);
+
 /* ---------------- factored steerable kernel ----------------
  *
  * Per edge e = (i <- j) with h~ = (1, h(e)): every block b's combination

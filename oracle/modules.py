@@ -16,6 +16,12 @@ kernel's parameters.  TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 The readout and the factored branch are the same function regrouped by
 associativity (the reference's own check: tests/nn/test_fused_factored.py:
 126-208), so each pins the other.
+
+The transformer block's pieces (:func:`layer_norm`, :func:`gated`,
+:func:`block_forward`) restate nn/normalization.py, nn/nonlinearities.py and
+nn/blocks.py of the reference; tests/test_oracle_block.py pins them (torch's
+LayerNorm and RMSNorm on one-frequency fields, the pooled denominator, the
+identity gate, gauge equivariance).
 """
 
 from __future__ import annotations
@@ -353,3 +359,59 @@ def conv_forward(conv, x: dict[int, Tensor], edges, tolerance: float | None = No
         pointwise = linear(conv.self_linear, x, conv.field_type_out)
         out = {f: out[f] + pointwise[f] for f in out}
     return out
+
+
+# ---------------------------------------------------------------- transformer block
+
+
+def layer_norm(norm, x: dict[int, Tensor]) -> dict[int, Tensor]:
+    """``SO2LayerNorm.forward`` (reference nn/normalization.py:150-190): only
+    frequency 0 centred; v_0 = mean (x_0 - mu)^2, v_n = mean_a |x_n,a|^2 / 2;
+    one denominator sqrt(mean_n v_n + eps); a gain per copy, a bias on
+    frequency 0."""
+    stats = []
+    out = {}
+    if 0 in x:
+        c0 = x[0] - x[0].mean(dim=-1, keepdim=True)
+        stats.append((c0 * c0).mean(dim=-1))
+    for f in sorted(x):
+        if f != 0:
+            stats.append((x[f] * x[f]).sum(dim=-1).mean(dim=-1) / 2)
+    d = torch.sqrt(sum(stats) / len(stats) + norm.eps)
+    for f in sorted(x):
+        g = norm.gamma[str(f)]
+        if f == 0:
+            out[0] = g * c0 / d.unsqueeze(-1) + (norm.beta if norm.beta is not None else 0.0)
+        else:
+            out[f] = g.unsqueeze(-1) * x[f] / d.unsqueeze(-1).unsqueeze(-1)
+    return out
+
+
+def gated(act, x: dict[int, Tensor]) -> dict[int, Tensor]:
+    """``SO2ScalarGatedNonlinearity.forward`` (reference
+    nn/nonlinearities.py:140-166): SiLU on the scalars; each copy of frequency n
+    times act(A_n x_0 + b_n), act = SiLU or 2 sigmoid, from the raw scalars."""
+    s = x[0]
+    out = {0: s * torch.sigmoid(s)}
+    for f in sorted(x):
+        if f == 0:
+            continue
+        lin = act.gates[str(f)]
+        pre = s @ lin.weight.T + (lin.bias if lin.bias is not None else 0.0)
+        g = 2 * torch.sigmoid(pre) if act.gate == "double_sigmoid" else pre * torch.sigmoid(pre)
+        out[f] = x[f] * g.unsqueeze(-1)
+    return out
+
+
+def block_forward(block, x: dict[int, Tensor], edges, tolerance: float | None = None) -> dict[int, Tensor]:
+    """``SO2TransformerBlock._run`` (reference nn/blocks.py:326-349) with
+    dropout off: x + Mixer(LN1 x), then + W2 act(W1 LN2 x)."""
+    normed = layer_norm(block.norm1, x)
+    if block.mixer == "attention":
+        mixed = mhsa_forward(block.attention, normed, edges, tolerance)
+    else:
+        mixed = conv_forward(block.attention, normed, edges, tolerance)
+    x = {f: x[f] + mixed[f] for f in x}
+    hidden = linear(block.linear1, layer_norm(block.norm2, x), block.hidden_field_type)
+    hidden = linear(block.linear2, gated(block.activation, hidden), block.field_type)
+    return {f: x[f] + hidden[f] for f in x}

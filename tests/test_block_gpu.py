@@ -1,0 +1,216 @@
+"""The transformer block on the HIP path against the oracle (float64 eager
+restatement of the reference's block, oracle.modules.block_forward):
+
+* the layer norm (gm_layer_norm_*) and the gated nonlinearity (gm_gate_*) in
+  float32 (1e-5 relative), float64 (1e-10) and bfloat16 rows against the
+  float64 oracle on the same rounded inputs (2e-2 relative to the largest
+  entry), with the input's and every parameter's gradient, over field types
+  with and without scalars, uneven multiplicities and a 640-wide row;
+* the whole block (both mixers, batched and per-head attention) in float32 and
+  float64, every gradient; in bfloat16 rows with float32 parameters (the C4
+  configuration) within 2e-2 of the float64 block;
+* gauge equivariance under random frame rotations; chunked equals whole."""
+
+import math
+
+import pytest
+import torch
+
+import problems
+from gm_attention_amd.discretization.discretization import SphericalDiscretization
+from gm_attention_amd.discretization.frames import build_tangent_frames, rotate_tangent_frames
+from gm_attention_amd.discretization.grid import build_equiangular_grid
+from gm_attention_amd.nn.blocks import SO2TransformerBlock
+from gm_attention_amd.nn.nonlinearities import SO2ScalarGatedNonlinearity
+from gm_attention_amd.nn.normalization import SO2LayerNorm
+from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
+from oracle import modules
+from test_attention_gpu import close
+
+pytestmark = pytest.mark.gpu
+
+D64 = torch.float64
+
+
+def randomise(module, seed=3, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for p in module.parameters():
+            p.copy_(scale * torch.randn(p.shape, generator=g, dtype=D64).to(p.dtype))
+
+
+def close_bf16(got, want, name):
+    want, got = want.detach().double().cpu(), got.detach().double().cpu()
+    err = float((got - want).abs().max()) / max(float(want.abs().max()), 1e-30)
+    assert err <= 2e-2, f"{name}: bf16 error {err:.3e} of the largest entry"
+
+
+def split(ft, flat):
+    return {f: t for f, t in SO2FeatureField.from_flat(ft, flat).coefficients.items()}
+
+
+def run_pointwise(module, ft, flat, probe, oracle):
+    leaf = flat.clone().requires_grad_(True)
+    module.zero_grad(set_to_none=True)
+    if oracle:
+        out = modules.flat((modules.layer_norm if isinstance(module, SO2LayerNorm) else modules.gated)(
+            module, split(ft, leaf)))
+    else:
+        out = module.forward_flat(leaf)
+    (out.double() * probe.to(out.device)).sum().backward()
+    return out.detach(), leaf.grad, {n: p.grad for n, p in module.named_parameters()}
+
+
+FIELDS = [{0: 32, 1: 32, 2: 32}, {0: 3, 1: 5}, {1: 4, 2: 3}, {0: 70}, {0: 128, 1: 128, 2: 128}, {0: 7, 1: 1, 3: 2}]
+
+
+@pytest.mark.parametrize("kind", ["norm", "gate_silu", "gate_double_sigmoid"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+@pytest.mark.parametrize("field", FIELDS)
+def test_pointwise_ops_match_the_oracle(field, dtype, kind, cuda):
+    if kind != "norm" and 0 not in field:
+        pytest.skip("the gate needs scalar channels")
+    print(f"pointwise {kind} {field} {dtype}", flush=True)
+    ft = SO2FieldType(field)
+    if kind == "norm":
+        module = SO2LayerNorm(ft, eps=1e-3, dtype=D64)
+    else:
+        module = SO2ScalarGatedNonlinearity(ft, gate=kind[5:], dtype=D64)
+    randomise(module, 1, 0.5)
+    n = 301
+    x = problems.normal((n, ft.dimension), 2)
+    probe = problems.normal((n, ft.dimension), 3)
+    pdtype = torch.float32 if dtype == torch.bfloat16 else dtype
+    if dtype != D64:  # the oracle sees the rounded inputs and parameters
+        x = x.to(dtype).double()
+        module.load_state_dict({k: v.to(pdtype).double() for k, v in module.state_dict().items()})
+    want = run_pointwise(module, ft, x, probe, True)
+    gpu = module.to(device=cuda, dtype=pdtype)
+    got = run_pointwise(gpu, ft, x.to(cuda, dtype), probe.to(cuda), False)
+    assert got[0].dtype == dtype
+    if dtype == torch.bfloat16:
+        close_bf16(got[0], want[0], "out")
+        close_bf16(got[1], want[1], "dx")
+        for k in want[2]:
+            close_bf16(got[2][k], want[2][k], f"d{k}")
+        return
+    close(got[0], want[0], dtype, "out")
+    close(got[1], want[1], dtype, "dx")
+    for k in want[2]:
+        close(got[2][k], want[2][k], dtype, f"d{k}", reduction=True)
+
+
+def build(mixer, batched, batch=2, nlat=10, nlon=20, field=None, heads=2, seed=0):
+    disc = problems.discretization(nlat, nlon)
+    edges = disc.edge_geometry.tile(batch, n_sources=disc.n_nodes) if batch > 1 else disc.edge_geometry
+    torch.manual_seed(seed)
+    ft = SO2FieldType(field or {0: 8, 1: 8, 2: 8})
+    block = SO2TransformerBlock(ft, heads, ffn_multiplier=4, cutoff=disc.coverage_radius, n_radial_basis=4,
+                                mixer=mixer, attention_batched=batched, dtype=D64)
+    with torch.no_grad():  # nonzero biases and gains everywhere, moderate scores
+        for p in block.parameters():
+            p.add_(0.1 * torch.randn_like(p))
+    n = edges.row_ptr.shape[0] - 1
+    return block, problems.normal((n, ft.dimension), seed + 1), edges
+
+
+def run_block(block, flat, edges, probe, *, oracle=False, chunk=None, tolerance=None):
+    leaf = flat.clone().requires_grad_(True)
+    block.zero_grad(set_to_none=True)
+    if oracle:
+        out = modules.flat(modules.block_forward(block, split(block.field_type, leaf), edges, tolerance))
+    elif chunk is not None:
+        out = block.forward_chunked(SO2FeatureField.from_flat(block.field_type, leaf), edges,
+                                    chunk_size=chunk).to_flat()
+    else:
+        out = block(SO2FeatureField.from_flat(block.field_type, leaf), edges).to_flat()
+    (out.double() * probe.to(out.device)).sum().backward()
+    return out.detach(), leaf.grad, {n: p.grad for n, p in block.named_parameters() if p.grad is not None}
+
+
+BLOCKS = [("attention", True), ("attention", False), ("convolution", False)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("mixer,batched", BLOCKS)
+def test_block_matches_the_oracle(mixer, batched, dtype, cuda):
+    print(f"block {mixer} batched={batched} {dtype}", flush=True)
+    block, x, edges = build(mixer, batched)
+    probe = problems.normal(x.shape, 7)
+    if dtype == torch.float32:
+        block.load_state_dict({k: v.float().double() for k, v in block.state_dict().items()})
+        x = x.float().double()
+        edges_o = edges.to(None, torch.float32).to(None, D64)
+    else:
+        edges_o = edges
+    want = run_block(block, x, edges_o, probe, oracle=True, tolerance=1e-5 if dtype == torch.float32 else None)
+    gpu = SO2TransformerBlock(block.field_type, 2, ffn_multiplier=4, cutoff=problems.discretization(10, 20)
+                              .coverage_radius, n_radial_basis=4, mixer=mixer, attention_batched=batched,
+                              dtype=dtype, device=cuda)
+    gpu.load_state_dict({k: v.to(dtype) for k, v in block.state_dict().items()})
+    got = run_block(gpu, x.to(cuda, dtype), edges.to(cuda, dtype), probe.to(cuda))
+    close(got[0], want[0], dtype, "out")
+    close(got[1], want[1], dtype, "dx")
+    assert set(got[2]) == set(want[2])
+    for k in want[2]:
+        close(got[2][k], want[2][k], dtype, f"d{k}", reduction=True)
+
+
+@pytest.mark.parametrize("mixer,batched", [("attention", True), ("convolution", False)])
+def test_bf16_block_is_within_2e2_of_float64(mixer, batched, cuda):
+    """bfloat16 rows, float32 parameters (the C4 configuration) against the
+    float64 oracle on the same rounded input and parameters."""
+    block, x, edges = build(mixer, batched)
+    probe = problems.normal(x.shape, 7)
+    block.load_state_dict({k: v.float().double() for k, v in block.state_dict().items()})
+    x = x.to(torch.bfloat16).double()
+    want = run_block(block, x, edges.to(None, torch.float32).to(None, D64), probe, oracle=True, tolerance=1e-5)
+    gpu = SO2TransformerBlock(block.field_type, 2, ffn_multiplier=4, cutoff=problems.discretization(10, 20)
+                              .coverage_radius, n_radial_basis=4, mixer=mixer, attention_batched=batched,
+                              dtype=torch.float32, device=cuda)
+    gpu.load_state_dict({k: v.float() for k, v in block.state_dict().items()})
+    got = run_block(gpu, x.to(cuda, torch.bfloat16), edges.to(cuda, torch.float32), probe.to(cuda))
+    assert got[0].dtype == torch.bfloat16 and got[1].dtype == torch.bfloat16
+    close_bf16(got[0], want[0], "out")
+    close_bf16(got[1], want[1], "dx")
+    for k in want[2]:
+        w, g = want[2][k].double(), got[2][k].double().cpu()
+        err = float((g - w).norm()) / max(float(w.norm()), 1e-30)
+        assert err <= 2e-2 or float(w.abs().max()) < 1e-6, f"d{k}: bf16 relative error {err:.3e}"
+
+
+@pytest.mark.parametrize("mixer", ["attention", "convolution"])
+def test_block_is_gauge_equivariant(mixer, cuda):
+    nlat, nlon = 10, 20
+    grid = build_equiangular_grid(nlat, nlon)
+    cutoff = 3.0 * math.pi / (nlat - 1)
+    frames = build_tangent_frames(grid.nodes)
+    theta = torch.rand(grid.n_nodes, dtype=D64, generator=torch.Generator().manual_seed(4)) * 2 * math.pi
+    base = SphericalDiscretization.from_grid(grid, cutoff, frames=frames).edge_geometry.to(cuda, D64)
+    turned = SphericalDiscretization.from_grid(grid, cutoff, frames=rotate_tangent_frames(frames, theta)) \
+        .edge_geometry.to(cuda, D64)
+    torch.manual_seed(0)
+    ft = SO2FieldType({0: 4, 1: 4, 2: 4})
+    block = SO2TransformerBlock(ft, 2, cutoff=cutoff, n_radial_basis=4, mixer=mixer, attention_batched=True,
+                                dtype=D64, device=cuda)
+    x = SO2FeatureField.from_flat(ft, problems.normal((grid.n_nodes, ft.dimension), 1).to(cuda))
+    th = theta.to(cuda)
+    with torch.no_grad():
+        y = block(x, base)
+        y_turned = block(x.gauge_transform(th), turned)
+    expected = y.gauge_transform(th)
+    torch.testing.assert_close(y_turned.to_flat(), expected.to_flat(), rtol=1e-9, atol=1e-9)
+    assert float((y.to_flat() - expected.to_flat()).abs().max()) > 1e-3
+
+
+def test_chunked_equals_whole(cuda):
+    block, x, edges = build("attention", True)
+    gpu = block.to(cuda)
+    e = edges.to(cuda, D64)
+    probe = problems.normal(x.shape, 7).to(cuda)
+    whole = run_block(gpu, x.to(cuda), e, probe)
+    chunked = run_block(gpu, x.to(cuda), e, probe, chunk=37)
+    close(chunked[0], whole[0], D64, "out")
+    close(chunked[1], whole[1], D64, "dx")
+    for k in whole[2]:
+        close(chunked[2][k], whole[2][k], D64, f"d{k}")
