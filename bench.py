@@ -22,6 +22,12 @@ gradient, at 256x512, batch 2, with bfloat16 rows (residual stream, norms,
 gate, feed-forward GEMMs) and float32 parameters; the attention's kernels
 compute in float32.
 
+``--workload encoder`` runs C5's restrictions: two ``EquiEncode`` hops,
+128x256 ({0: 4}) -> 64x128 ({0: 64, 1: 64, 2: 64}) -> 32x64 ({0: 128, 1: 128,
+2: 128}), batch 8, forward + backward with every gradient, float32, over the
+GPU-built bipartite edges (radius two coarse row spacings, quartic window);
+the wide kernels run as output tiles of the fused factored aggregate.
+
 ``--workload softmax`` times the scores-and-softmax op alone (forward +
 backward) on the same shape.  ``--workload conv`` times the depthwise steerable
 convolution layer (``SO2Convolution(depthwise=True, n_radial_basis=4)``,
@@ -390,12 +396,151 @@ def run_geometry(args) -> None:
     print(json.dumps(line))
 
 
+def run_encoder(args) -> None:
+    """One step = both restriction hops forward and backward (C5's encoder transfers)."""
+    import torch
+
+    from gm_attention_amd import _native
+    from gm_attention_amd.discretization.grid import build_equiangular_grid
+    from gm_attention_amd.discretization.hierarchy import build_grid_hierarchy
+    from gm_attention_amd.nn import fused_factored
+    from gm_attention_amd.nn.blocks import EquiEncode
+    from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
+    from oracle import modules
+
+    device = torch.device("cuda:0")
+    shapes = [(128, 256), (64, 128), (32, 64)]
+    cutoffs = [2.0 * math.pi / (shapes[1][0] - 1), 2.0 * math.pi / (shapes[2][0] - 1)]
+    t0 = time.time()
+    h1 = build_grid_hierarchy([build_equiangular_grid(*s, device=device) for s in shapes], ["equiangular"] * 3, shapes,
+                              restrict_cutoffs=cutoffs, interpolate_cutoffs=cutoffs, local_cutoffs=[None, None, None])
+    h = h1.tile(8)
+    down = [e.to(device, torch.float32) for e in h.down_edges]
+    log(f"hierarchy {shapes}: down edges {[e.n_edges for e in down]} (batch 8) in {time.time() - t0:.1f}s")
+    types = [SO2FieldType({0: 4}), SO2FieldType({0: 64, 1: 64, 2: 64}), SO2FieldType({0: 128, 1: 128, 2: 128})]
+    torch.manual_seed(0)
+    encs = [EquiEncode(types[k], types[k + 1], cutoff=cutoffs[k], n_radial_basis=8, dtype=torch.float32, device=device)
+            for k in range(2)]
+    timer = OpTimer()
+    fac = _native.factored()
+    timer.wrap(fac, "forward", "factored_forward")
+    timer.wrap(fac, "aggregate", "factored_aggregate")
+    timer.wrap(fac, "backward_aggregated", "factored_backward_aggregated")
+    n0 = h.levels[0].n_nodes
+    gen = torch.Generator(device=device).manual_seed(1)
+    x = torch.rand(n0, types[0].dimension, device=device, generator=gen).requires_grad_(True)
+    upstream = torch.randn(h.levels[2].n_nodes, types[2].dimension, device=device, generator=gen)
+
+    def step():
+        y = encs[0](SO2FeatureField.from_flat(types[0], x), down[0])
+        z = encs[1](y, down[1]).to_flat()
+        torch.autograd.backward(z, upstream)
+
+    def clear():
+        x.grad = None
+        for e in encs:
+            e.zero_grad(set_to_none=True)
+
+    for _ in range(args.warmup):
+        step()
+        clear()
+    torch.cuda.synchronize()
+    timer.enabled = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+        clear()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer.enabled = False
+    ms_per_step = 1e3 * elapsed / args.steps
+    ops = timer.summary(args.steps)
+    log(f"step {ms_per_step:.2f} ms; ops: " + ", ".join(f"{k} {v['ms_per_step']:.2f} ms" for k, v in ops.items()))
+    # FLOPs of every tile of both hops: forward 2 K C + 8 wc, backward 4 K C + 8 wc per edge (C = 2 wc + wr)
+    flops = {"factored_forward": 0.0, "factored_backward_aggregated": 0.0}
+    for enc, e in zip(encs, down):
+        kern = enc.integral.kernel
+        K = kern.complex_head.in_features + 1
+        tl = fused_factored.tiles(kern)
+        shapes_t = [(len(t.zc_cols), len(t.zr_cols)) for t in tl] if tl else [
+            (fused_factored.plan(kern).wc, fused_factored.plan(kern).wr)]
+        for wc, wr in shapes_t:
+            C = 2 * wc + wr
+            flops["factored_forward"] += e.n_edges * (2.0 * K * C + 8 * wc)
+            flops["factored_backward_aggregated"] += e.n_edges * (4.0 * K * C + 8 * wc)
+    dominant = max(ops, key=lambda k: ops[k]["ms_per_step"])
+    if dominant not in flops:
+        dominant = "factored_backward_aggregated"
+    achieved = flops[dominant] / (ops[dominant]["ms_per_step"] * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / FP32_PEAK_TFLOPS, "traffic": None, "kernel": dominant,
+            "algorithmic_per_launch": {"flops_per_step": flops[dominant],
+                                       "launches_per_step": ops[dominant]["launches_per_step"]},
+            "note": "the op's launches (output tiles of both hops) differ in size: FLOPs and time per step"}
+    baseline = None
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        torch.set_num_threads(threads)
+        total, parts = 0.0, []
+        for k, (enc, e) in enumerate(zip(encs, down)):
+            host = EquiEncode(types[k], types[k + 1], cutoff=cutoffs[k], n_radial_basis=8, dtype=torch.float32)
+            host.load_state_dict({n: v.detach().cpu() for n, v in enc.state_dict().items()})
+            one = h1.down_edges[k].to("cpu")
+            n_t = max(1, int(torch.searchsorted(one.row_ptr, torch.tensor(args.cpu_budget_edges // 8)).item()))
+            sub = one.select(torch.arange(int(one.row_ptr[n_t])), n_nodes=n_t).to(None, torch.float32)
+            xs = torch.randn(h1.levels[k].n_nodes, types[k].dimension).requires_grad_(True)
+            g = torch.randn(n_t, types[k + 1].dimension)
+
+            def cpu_step():
+                out = modules.flat(modules.encode_forward(host.integral, dict(
+                    SO2FeatureField.from_flat(types[k], xs).coefficients), sub))
+                (out * g).sum().backward()
+                xs.grad = None
+                host.zero_grad(set_to_none=True)
+
+            cpu_step()
+            t1 = time.perf_counter()
+            cpu_step()
+            dt = time.perf_counter() - t1
+            total += dt / sub.n_edges * e.n_edges
+            parts.append(f"hop {k + 1}: {sub.n_edges} edges in {dt:.2f}s")
+        baseline = {"value": n0 / total, "unit": "fine-points/s", "cores": threads, "kind": "port",
+                    "sample": (f"oracle eager EquiEncode fwd+bwd (per-edge readout, float32, torch on {threads} "
+                               f"threads) over the first targets of one sample per hop ({'; '.join(parts)}), "
+                               f"extrapolated per edge to both hops' {down[0].n_edges} + {down[1].n_edges} edges")}
+        log(f"cpu baseline: {baseline['value']:.1f} fine-points/s ({baseline['sample']})")
+    line = {
+        "metric": "encoder restriction hops fwd+bwd fine-points/s at 128x256 B=8",
+        "value": n0 / (ms_per_step * 1e-3),
+        "unit": "fine-points/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: U(0,1) scalar input, N(0,1) upstream gradient, random-init weights, equiangular grids",
+        "config": {"workload": ("EquiEncode 128x256 {0:4} -> 64x128 {0:64,1:64,2:64} -> 32x64 {0:128,1:128,2:128}, "
+                                "quartic window, radius 2 coarse row spacings, n_radial_basis 8; input and every "
+                                "parameter gradient"),
+                   "batch": 8, "fine_points": n0, "edges": [e.n_edges for e in down],
+                   "tiles": [len(fused_factored.tiles(e.integral.kernel) or ()) for e in encs]},
+        "roofline": roof,
+        "ops": {name: {k: round(v2, 4) for k, v2 in v.items()} for name, v in ops.items()},
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line))
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry", "block"), default="attention")
+    ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry", "block", "encoder"),
+                    default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-edges", type=int, default=200_000)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -420,6 +565,9 @@ def main() -> None:
 
     if args.workload == "geometry":
         run_geometry(args)
+        return
+    if args.workload == "encoder":
+        run_encoder(args)
         return
 
     import torch

@@ -2,7 +2,8 @@
 
 Restates ``discretization/discretization.py`` of the reference: ``from_grid``
 (:119-168), ``edges_within`` (membership from the float64 lattice distances
-with ``EXACT_SLACK``, cached per radius; :447-481), ``tile`` (the batch as a
+with ``EXACT_SLACK``, cached per radius; :447-481), ``prepare_windows``
+(:483-493), ``tile`` (the batch as a
 disjoint union; :495-517) and ``to`` (:519-560).
 """
 
@@ -77,6 +78,11 @@ class SphericalDiscretization:
                 mask = within_cutoff(self.edge_geometry.distances, radius)
             self._radius_cache[key] = self.edge_geometry.select(mask)
         return self._radius_cache[key]
+
+    def prepare_windows(self, support_radii) -> None:
+        """Materialise the edge subset of every support radius (reference :483-493)."""
+        for radius in support_radii:
+            self.edges_within(radius)
 
     def tile(self, count: int) -> SphericalDiscretization:
         if count == 1:

@@ -14,7 +14,9 @@ Restates ``discretization/edge_geometry.py`` of the reference:
   in the target frame, the transport ``R = I + K + K^2 / (1 + <q, p>)``
   (:718-771), ``gamma = atan2`` of ``E_i^T R E_j`` (:574-585), quadrature
   ``w_j r / sin r`` (:588-591), ``phi = atan2`` of the log coordinates;
-* ``within_cutoff`` / ``cutoff_tolerance`` / ``GM_CUTOFF_RULE`` (:403-462).
+* ``within_cutoff`` / ``cutoff_tolerance`` / ``GM_CUTOFF_RULE`` (:403-462);
+* ``compute_bipartite_edge_geometry`` (:830-961) and its KD-tree search
+  (:964-998): edges between two grids, each side in its own numbering.
 
 A grid whose nodes are on the GPU is built by ``hip_builder`` (the same edge
 list from the same float64 rule, tables in one HIP pass).
@@ -239,3 +241,74 @@ def compute_edge_geometry(grid, frames: Tensor, coverage_radius: float, *,
     edge_index = edge_index[:, keep].to(nodes.device)
     return edge_geometry_from_index(nodes, frames, grid.quadrature_weights.contiguous(), edge_index, nodes.shape[0],
                                     max_frequency)
+
+
+def bipartite_radius_edges(source_nodes: Tensor, target_nodes: Tensor, cutoff: float, *, exact: bool = False,
+                           workers: int = -1) -> Tensor:
+    """Candidate ``target <- source`` pairs between two grids from a KD-tree over
+    the sources (float64 CPU), lexsorted target-major, source-minor (reference
+    :964-998)."""
+    src = source_nodes.detach().to("cpu", torch.float64).numpy()
+    tgt = target_nodes.detach().to("cpu", torch.float64).numpy()
+    lists = cKDTree(src).query_ball_point(tgt, r=_query_chord_radius(cutoff, source_nodes.dtype, exact=exact),
+                                          workers=workers)
+    counts = np.fromiter((len(x) for x in lists), dtype=np.int64, count=len(lists))
+    targets = np.repeat(np.arange(tgt.shape[0], dtype=np.int64), counts)
+    sources = np.concatenate([np.asarray(x, dtype=np.int64) for x in lists]) if counts.sum() else np.zeros(0, np.int64)
+    order = np.lexsort((sources, targets))
+    return torch.as_tensor(np.stack([targets[order], sources[order]]), dtype=torch.long)
+
+
+def _check_covered(edge_index: Tensor, n_target: int, cutoff: float) -> None:
+    covered = torch.zeros(n_target, dtype=torch.bool, device=edge_index.device)
+    covered[edge_index[0]] = True
+    if not bool(covered.all()):
+        missing = int((~covered).sum())
+        raise ValueError(f"{missing} of {n_target} target nodes have no source within cutoff={cutoff}. Widen the "
+                         "cutoff: an uncovered target aggregates to zero, which is indistinguishable from a genuine "
+                         "zero downstream.")
+
+
+def compute_bipartite_edge_geometry(source_nodes: Tensor, source_frames: Tensor,
+                                    source_spherical_quadrature_weights: Tensor, target_nodes: Tensor,
+                                    target_frames: Tensor, *, cutoff: float, max_frequency: int,
+                                    source_exact_nodes: Tensor | None = None,
+                                    target_exact_nodes: Tensor | None = None) -> EdgeGeometry:
+    """Edges ``target i <- source j`` between two grids (reference :830-961):
+    each side in its own numbering, ``row_ptr`` over the targets, quadrature
+    from the sources, log coordinates and transport in the targets' frames.
+    Membership from the float64 lattices with ``EXACT_SLACK`` when both are
+    given (else from the working nodes with the dtype's slack); every target
+    must have a source.  The tables are ``edge_geometry_from_index`` on the
+    concatenation (targets first), the source indices rewritten back.  Nodes on
+    the GPU take the GPU builder (same integers, tables in one HIP pass)."""
+    if cutoff <= 0.0:
+        raise ValueError(f"cutoff must be positive, got {cutoff}.")
+    n_target = target_nodes.shape[0]
+    exact = CUTOFF_RULE != "legacy" and source_exact_nodes is not None and target_exact_nodes is not None
+    from gm_attention_amd.discretization import hip_builder
+
+    if exact and hip_builder.ENABLED and target_nodes.device.type == "cuda":
+        return hip_builder.compute_bipartite_edge_geometry(
+            source_nodes, source_frames, source_spherical_quadrature_weights, target_nodes, target_frames,
+            cutoff=cutoff, max_frequency=max_frequency, source_exact_nodes=source_exact_nodes,
+            target_exact_nodes=target_exact_nodes)
+    src_search, tgt_search = (source_exact_nodes, target_exact_nodes) if exact else (source_nodes, target_nodes)
+    edge_index = bipartite_radius_edges(src_search, tgt_search, cutoff, exact=exact)
+    if CUTOFF_RULE != "legacy":
+        both = torch.cat([tgt_search.detach().cpu(), src_search.detach().cpu()], dim=0)
+        shifted = torch.stack([edge_index[0], edge_index[1] + n_target])
+        d = geodesic_distances(both.to(torch.float64) if exact else both, shifted)
+        keep = d <= cutoff + EXACT_SLACK if exact else within_cutoff(d, cutoff)
+        edge_index = edge_index[:, keep]
+    edge_index = edge_index.to(source_nodes.device)
+    _check_covered(edge_index, n_target, cutoff)
+    nodes = torch.cat([target_nodes, source_nodes], dim=0)
+    frames = torch.cat([target_frames, source_frames], dim=0)
+    weights = torch.cat([source_spherical_quadrature_weights.new_zeros(n_target), source_spherical_quadrature_weights])
+    combined = edge_geometry_from_index(nodes, frames, weights, torch.stack([edge_index[0], edge_index[1] + n_target]),
+                                        n_target, max_frequency)
+    return EdgeGeometry(torch.stack([combined.edge_index[0], combined.edge_index[1] - n_target]).contiguous(),
+                        *(getattr(combined, f) for f in ("row_ptr", "log_coordinates", "distances", "polar_angles",
+                                                        "transport_angles", "tangent_quadrature_weights",
+                                                        "angular_phases", "transport_phases")))

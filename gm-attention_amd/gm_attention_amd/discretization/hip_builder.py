@@ -80,3 +80,32 @@ def exact_distances(grid, edge_index: Tensor) -> Tensor:
     """Float64 lattice distances of the edges (the radius subsets' membership), on the edges' device."""
     exact = _lattice(grid, edge_index.device)
     return _native.geodesic_distances(exact, exact, edge_index)
+
+
+def compute_bipartite_edge_geometry(source_nodes: Tensor, source_frames: Tensor, source_quadrature: Tensor,
+                                    target_nodes: Tensor, target_frames: Tensor, *, cutoff: float,
+                                    max_frequency: int, source_exact_nodes: Tensor,
+                                    target_exact_nodes: Tensor):
+    """The bipartite EdgeGeometry (target <- source, own numbering on each side)
+    of edge_geometry.compute_bipartite_edge_geometry, from the two float64
+    lattices on the targets' device."""
+    from gm_attention_amd.discretization.edge_geometry import EXACT_SLACK, EdgeGeometry, _check_covered
+
+    device, dtype = target_nodes.device, target_nodes.dtype
+    src64 = source_exact_nodes.to(device=device, dtype=torch.float64).contiguous()
+    tgt64 = target_exact_nodes.to(device=device, dtype=torch.float64).contiguous()
+    edge_index, row_ptr = _native.radius_edges(tgt64, src64, float(cutoff) + EXACT_SLACK)
+    _check_covered(edge_index, target_nodes.shape[0], cutoff)
+    f64 = dict(device=device, dtype=torch.float64)
+    t = _native.edge_tables(target_nodes.to(**f64).contiguous(), target_frames.to(**f64).contiguous(),
+                            source_nodes.to(**f64).contiguous(), source_frames.to(**f64).contiguous(),
+                            source_quadrature.to(**f64).contiguous(), edge_index, max_frequency)
+    cdtype = complex_dtype(dtype)
+
+    def real(x: Tensor) -> Tensor:
+        return x if dtype == torch.float64 else x.to(dtype)
+
+    return EdgeGeometry(edge_index, row_ptr, real(t["log_coordinates"]), real(t["distances"]), real(t["polar_angles"]),
+                        real(t["transport_angles"]), real(t["tangent_quadrature_weights"]),
+                        torch.view_as_complex(t["angular_phases"]).to(cdtype),
+                        torch.view_as_complex(t["transport_phases"]).to(cdtype))

@@ -20,6 +20,12 @@ accumulation"): the norms and the gate read and write bfloat16 and compute in
 float32, the feed-forward GEMMs run in bfloat16 with float accumulation, and
 the mixer, whose kernels are float32, takes its input rounded up to float32 and
 hands back float32 that the residual addition rounds to bfloat16.
+
+``IcoEncode`` / ``EquiEncode`` (reference :359-505, :799-869) restrict a
+field from a fine grid onto a coarse one over bipartite edges
+(``discretization.hierarchy``): the steerable-kernel integral of
+``SO2Convolution`` with fine sources and coarse targets, through the fused
+factored aggregate (kernels wider than the op's bounds run as output tiles).
 """
 
 from __future__ import annotations
@@ -30,8 +36,11 @@ from typing import Literal
 import torch
 from torch import Tensor, nn
 
-from gm_attention_amd.nn.attention import SO2MHSA
+from gm_attention_amd.nn import fused_factored, kernels
+from gm_attention_amd.nn.attention import SO2MHSA, gather_to_edges, weighted_segment_sum
 from gm_attention_amd.nn.convolution import SO2Convolution
+from gm_attention_amd.nn.fused_attention import evaluate_aggregation_window
+from gm_attention_amd.nn.kernels import SO2SteerableKernel
 from gm_attention_amd.nn.linear import SO2Linear, flat_forward
 from gm_attention_amd.nn.nonlinearities import SO2ScalarGatedNonlinearity
 from gm_attention_amd.nn.normalization import SO2Dropout, SO2LayerNorm
@@ -139,3 +148,67 @@ class SO2TransformerBlock(nn.Module):
     def extra_repr(self) -> str:
         return (f"field_type={self.field_type!r}, hidden_field_type={self.hidden_field_type!r}, "
                 f"nonlinearity={self.nonlinearity!r}")
+
+
+class IcoEncode(nn.Module):
+    """Fine -> coarse restriction over bipartite edges (reference blocks.py:359-505)."""
+
+    def __init__(self, field_type_in: SO2FieldType, field_type_out: SO2FieldType, *, cutoff: float,
+                 window: str = "hard", n_radial_basis: int = 8, radial_hidden_features=(16,),
+                 radial_basis: str = "gaussian", bias: bool = True, dtype=None, device=None) -> None:
+        super().__init__()
+        if window not in ("hard", "quartic"):
+            raise ValueError(f"window must be 'hard' or 'quartic', got {window!r}.")
+        self.field_type_in = field_type_in
+        self.field_type_out = field_type_out
+        self.cutoff = float(cutoff)
+        self.window = window
+        self.kernel = SO2SteerableKernel(field_type_in, field_type_out, cutoff=cutoff, n_radial_basis=n_radial_basis,
+                                         radial_hidden_features=radial_hidden_features, radial_basis=radial_basis,
+                                         bias=bias, dtype=dtype, device=device)
+
+    def forward(self, x: SO2FeatureField, edges) -> SO2FeatureField:
+        """``y_i = sum_j c(v_ij) w_ij K(v_ij) rho(g_{i<-j}) x_j``, i a coarse target, j a fine source."""
+        if x.field_type != self.field_type_in:
+            raise ValueError(f"Expected a field of type {self.field_type_in!r}, got {x.field_type!r}.")
+        weight = evaluate_aggregation_window(edges.distances, self.cutoff, self.window) * \
+            edges.tangent_quadrature_weights
+        if kernels.factored_enabled():
+            products = self.kernel.node_products(x)
+            groups = (fused_factored.source_groups(edges.source_index,
+                                                   fused_factored.group_key(edges, 0, int(edges.n_edges)),
+                                                   owner=edges.edge_index)
+                      if fused_factored.enabled(self.kernel, x, edges) else None)
+            return self.kernel.forward_factored_aggregated(x, edges, weight, products, groups)
+        messages = self.kernel(gather_to_edges(x, edges.source_index), edges)
+        return SO2FeatureField(self.field_type_out,
+                               weighted_segment_sum(weight, messages.coefficients, edges.row_ptr))
+
+    def extra_repr(self) -> str:
+        return (f"field_type_in={self.field_type_in!r}, field_type_out={self.field_type_out!r}, "
+                f"cutoff={self.cutoff:.6g}, window={self.window!r}")
+
+
+class EquiEncode(nn.Module):
+    """Fine -> coarse restriction between two arbitrary grids (reference blocks.py:799-869)."""
+
+    def __init__(self, field_type_in: SO2FieldType, field_type_out: SO2FieldType, *, cutoff: float,
+                 mode: str = "learned_integral", window: str = "quartic", n_radial_basis: int = 8,
+                 radial_hidden_features=(16,), radial_basis: str = "gaussian", bias: bool = True, dtype=None,
+                 device=None) -> None:
+        super().__init__()
+        if mode != "learned_integral":
+            raise ValueError(f"mode must be 'learned_integral', got {mode!r}.")
+        self.field_type_in = field_type_in
+        self.field_type_out = field_type_out
+        self.mode = mode
+        self.cutoff = float(cutoff)
+        self.integral = IcoEncode(field_type_in, field_type_out, cutoff=cutoff, window=window,
+                                  n_radial_basis=n_radial_basis, radial_hidden_features=radial_hidden_features,
+                                  radial_basis=radial_basis, bias=bias, dtype=dtype, device=device)
+
+    def forward(self, x: SO2FeatureField, down_edges) -> SO2FeatureField:
+        return self.integral(x, down_edges)
+
+    def extra_repr(self) -> str:
+        return f"{self.field_type_in!r} -> {self.field_type_out!r}, mode={self.mode!r}, cutoff={self.cutoff:.6g}"

@@ -35,6 +35,7 @@ from gm_attention_amd import _native
 from gm_attention_amd.representations.field_type import SO2FeatureField
 
 MAX_K, MAX_OUT, MAX_BM, MAX_C, DESC = 20, 128, 32, 320, 8
+MAX_C_MFMA = 128  # packed columns the float32 MFMA kernels take (K <= 17)
 MODE = os.environ.get("GM_FUSED_FACTORED", "1")
 
 
@@ -192,10 +193,11 @@ def declined(kernel: Any, x: SO2FeatureField, edges: Any) -> str:
         return "the fused factored op runs on the GPU only (this build has no CPU driver)"
     if x.dtype not in (torch.float32, torch.float64):
         return f"the fused factored op takes float32 or float64, got {x.dtype}"
-    p = plan(kernel)
     trunk = kernel.complex_head.in_features if kernel.complex_head is not None else kernel.real_head.in_features
-    if trunk + 1 > MAX_K or p.d_out > MAX_OUT or p.max_bm > MAX_BM or 2 * p.wc + p.wr > MAX_C:
-        return "the kernel's widths exceed the fused op's bounds (K <= 20, d_out <= 128, b_m <= 32, 2wc + wr <= 320)"
+    if trunk + 1 > MAX_K:
+        return "the kernel's trunk exceeds the fused op's bound (K <= 20)"
+    if tiles(kernel) == ():
+        return "an output copy's blocks exceed the fused op's bounds even one copy at a time"
     if edges.n_edges == 0:
         return "no edges"
     return ""
@@ -292,13 +294,214 @@ def inputs(kernel: Any, x: SO2FeatureField, edges: Any, products: dict | None) -
                   edges.source_index.contiguous(), p)
 
 
+# ---------------------------------------------------------------- output tiles of wide kernels
+
+
+@dataclass(frozen=True)
+class Tile:
+    """A slice of a wide kernel's plan that fits the fused op: its descriptor
+    rows (offsets local to the tile), the full plan's complex and real mix
+    columns it reads, and the full output columns it writes, in tile order."""
+
+    rows: tuple[tuple[int, ...], ...]
+    zc_cols: tuple[int, ...]
+    zr_cols: tuple[int, ...]
+    out_cols: tuple[int, ...]
+    d_out: int
+    max_bm: int
+
+
+def _piece(p: Plan, m: int, c0: int, c1: int, base: tuple[int, int, int], start: int) -> tuple[list, list, list, list]:
+    """Output copies [c0, c1) of frequency m: every block writing them, cut to those copies."""
+    out0, zc0, zr0 = base
+    rows, zc_cols, zr_cols = [], [], []
+    width = (c1 - c0) * (1 if m == 0 else 2)
+    for b in p.blocks:
+        if b.block[1] != m:
+            continue
+        if b.kind == 0:
+            rows.append([0, zr0 + len(zr_cols), c1 - c0, 0, 0, 0, out0, 0])
+            zr_cols += range(c0, c1)
+        else:
+            rows.append([1, zc0 + len(zc_cols), c1 - c0, b.angular, b.transport, b.power, out0, b.take_real])
+            zc_cols += range(b.z_offset + c0, b.z_offset + c1)
+    out_cols = list(range(start + c0, start + c1)) if m == 0 else list(range(start + 2 * c0, start + 2 * c1))
+    assert len(out_cols) == width
+    return rows, zc_cols, zr_cols, out_cols
+
+
+def tiles(kernel: Any) -> tuple[Tile, ...] | None:
+    """``None`` when the kernel's plan fits the fused op as is; else the plan
+    cut into output tiles (each output frequency's copies in chunks of at most
+    ``MAX_BM``, halved until one chunk's blocks fit, chunks packed greedily
+    into tiles within ``MAX_OUT``, ``MAX_C`` and one real block); ``()`` when even single
+    copies do not fit.  Blocks are separable by output copy, so the tiles'
+    outputs side by side are the kernel's output."""
+    cached = kernel.__dict__.get("_fused_factored_tiles", False)
+    if cached is not False:
+        return cached
+    p = plan(kernel)
+    result: tuple[Tile, ...] | None = None
+    if p.d_out > MAX_OUT or p.max_bm > MAX_BM or 2 * p.wc + p.wr > MAX_C:
+        out_type = kernel.field_type_out
+        slices = out_type.slices()
+        # float32 tiles stay within the MFMA kernels' packed width
+        width = MAX_C_MFMA if next(kernel.parameters()).dtype == torch.float32 else MAX_C
+
+        def fits(rows, zc_cols, zr_cols, out_cols) -> bool:
+            # the op takes one real block, covering the tile's real mixes
+            return (len(out_cols) <= MAX_OUT and 2 * len(zc_cols) + len(zr_cols) <= width
+                    and sum(r[0] == 0 for r in rows) <= 1 and len(rows) <= 64)
+
+        built: list[Tile] = []
+        current: tuple[list, list, list, list] = ([], [], [], [])
+        ok = True
+        for m in out_type.frequencies:
+            copies = out_type.multiplicity(m)
+            chunk = MAX_BM
+            while chunk > 1 and not fits(*_piece(p, m, 0, min(chunk, copies), (0, 0, 0), slices[m].start)):
+                chunk //= 2
+            if not fits(*_piece(p, m, 0, min(chunk, copies), (0, 0, 0), slices[m].start)):
+                ok = False
+                break
+            for c0 in range(0, copies, chunk):
+                c1 = min(copies, c0 + chunk)
+                base = (len(current[3]), len(current[1]), len(current[2]))
+                piece = _piece(p, m, c0, c1, base, slices[m].start)
+                grown = tuple(a + b for a, b in zip(current, piece))
+                if current[3] and not fits(*grown):
+                    built.append(_tile(current))
+                    piece = _piece(p, m, c0, c1, (0, 0, 0), slices[m].start)
+                    grown = piece
+                current = grown
+        if ok and current[3]:
+            built.append(_tile(current))
+        result = tuple(built) if ok else ()
+    kernel.__dict__["_fused_factored_tiles"] = result
+    return result
+
+
+def _tile(parts: tuple[list, list, list, list]) -> Tile:
+    rows, zc_cols, zr_cols, out_cols = parts
+    return Tile(tuple(tuple(r) for r in rows), tuple(zc_cols), tuple(zr_cols), tuple(out_cols), len(out_cols),
+                max(r[2] for r in rows))
+
+
+def _tile_tensors(kernel: Any, t: Tile, index: int, device: torch.device) -> tuple[Tensor, Tensor, Tensor]:
+    cache = kernel.__dict__.setdefault("_fused_factored_tile_tensors", {})
+    key = (index, str(device))
+    if key not in cache:
+        cache[key] = (torch.tensor(t.rows, dtype=torch.int32, device=device),
+                      torch.tensor(t.zc_cols, dtype=torch.int64, device=device),
+                      torch.tensor(t.zr_cols, dtype=torch.int64, device=device))
+    return cache[key]
+
+
+def _untile(kernel: Any, parts: list[Tensor], device: torch.device) -> Tensor:
+    """The tiles' outputs side by side, reordered to the full output columns."""
+    cache = kernel.__dict__.setdefault("_fused_factored_untile", {})
+    key = str(device)
+    if key not in cache:
+        cols = [c for t in tiles(kernel) for c in t.out_cols]
+        inverse = torch.empty(len(cols), dtype=torch.int64)
+        inverse[torch.tensor(cols)] = torch.arange(len(cols))
+        cache[key] = inverse.to(device)
+    return torch.cat(parts, dim=1).index_select(1, cache[key])
+
+
+def _tiled(kernel: Any, i: "Inputs", launch) -> Tensor:
+    parts = []
+    for index, t in enumerate(tiles(kernel)):
+        desc, zc_cols, zr_cols = _tile_tensors(kernel, t, index, i.h.device)
+        zc = i.zc.index_select(2, zc_cols) if zc_cols.numel() else i.zc[:, :, :0]
+        zr = i.zr.index_select(2, zr_cols) if zr_cols.numel() else i.zr[:, :, :0]
+        parts.append(launch(zc.contiguous(), zr.contiguous(), desc, t.d_out, t.max_bm))
+    return _untile(kernel, parts, i.h.device)
+
+
+class TiledAggregate(torch.autograd.Function):
+    """A wide kernel's aggregate as one op over its output tiles: each tile's
+    mixes gathered from the full ``zc``/``zr``, the fused forward and
+    aggregate per tile, the outputs side by side in the full column order.
+    The backward writes every tile's mix gradient straight into its columns of
+    one ``dzc``/``dzr`` (the tiles partition the columns, so each is written
+    once) and accumulates ``dh`` and ``dweights`` in place."""
+
+    @staticmethod
+    def forward(ctx: Any, h: Tensor, zc: Tensor, zr: Tensor, weights: Tensor, angular: Tensor, transport: Tensor,
+                rho: Tensor, source: Tensor, target: Tensor, row_ptr: Tensor, order: Tensor, group_ptr: Tensor,
+                group_source: Tensor, kernel: Any) -> Tensor:
+        ext = extension(cuda=h.is_cuda)
+        parts, rows = [], []
+        with torch.profiler.record_function("gm::kernel/pairs_tiles"):
+            for index, t in enumerate(tiles(kernel)):
+                desc, zc_cols, zr_cols = _tile_tensors(kernel, t, index, h.device)
+                zc_t = zc.index_select(2, zc_cols).contiguous() if zc_cols.numel() else zc[:, :, :0].contiguous()
+                zr_t = zr.index_select(2, zr_cols).contiguous() if zr_cols.numel() else zr[:, :, :0].contiguous()
+                r = ext.forward(h, zc_t, zr_t, angular, transport, rho, desc, source, order, group_ptr, group_source,
+                                t.d_out, t.max_bm)
+                rows.append(r)
+                parts.append(ext.aggregate(r, weights, row_ptr))
+        ctx.save_for_backward(h, zc, zr, weights, angular, transport, rho, source, target, order, group_ptr,
+                              group_source, *rows)
+        ctx.kernel = kernel
+        return _untile(kernel, parts, h.device)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx: Any, grad_out: Tensor) -> tuple:
+        h, zc, zr, weights, angular, transport, rho, source, target, order, group_ptr, group_source = \
+            ctx.saved_tensors[:12]
+        rows = ctx.saved_tensors[12:]
+        kernel = ctx.kernel
+        ext = extension(cuda=h.is_cuda)
+        grad_out = grad_out.contiguous()
+        dzc, dzr = torch.empty_like(zc), torch.empty_like(zr)
+        dh = dweights = None
+        offset = 0
+        with torch.profiler.record_function("gm::kernel/pairs_tiles_backward"):
+            for index, (t, r) in enumerate(zip(tiles(kernel), rows)):
+                desc, zc_cols, zr_cols = _tile_tensors(kernel, t, index, h.device)
+                cols = _untile_columns(kernel, h.device)[offset:offset + t.d_out]
+                offset += t.d_out
+                g_t = grad_out.index_select(1, cols).contiguous()
+                zc_t = zc.index_select(2, zc_cols).contiguous() if zc_cols.numel() else zc[:, :, :0].contiguous()
+                zr_t = zr.index_select(2, zr_cols).contiguous() if zr_cols.numel() else zr[:, :, :0].contiguous()
+                dh_t, dzc_t, dzr_t, dw_t = ext.backward_aggregated(g_t, target, weights, r, h, zc_t, zr_t, angular,
+                                                                   transport, rho, desc, source, order, group_ptr,
+                                                                   group_source)
+                if zc_cols.numel():
+                    dzc.index_copy_(2, zc_cols, dzc_t)
+                if zr_cols.numel():
+                    dzr.index_copy_(2, zr_cols, dzr_t)
+                dh = dh_t if dh is None else dh.add_(dh_t)
+                dweights = dw_t if dweights is None else dweights.add_(dw_t)
+        return dh, dzc, dzr, dweights, None, None, None, None, None, None, None, None, None, None
+
+
+def _untile_columns(kernel: Any, device: torch.device) -> Tensor:
+    """The full output columns of the tiles' outputs side by side."""
+    cache = kernel.__dict__.setdefault("_fused_factored_tile_columns", {})
+    key = str(device)
+    if key not in cache:
+        cache[key] = torch.tensor([c for t in tiles(kernel) for c in t.out_cols], dtype=torch.int64, device=device)
+    return cache[key]
+
+
 def forward(kernel: Any, x: SO2FeatureField, edges: Any, products: dict | None = None,
             groups: tuple[Tensor, Tensor, Tensor] | None = None) -> SO2FeatureField:
     """The messages on the edges, ``(n_edges,)`` of the kernel's output type."""
     i = inputs(kernel, x, edges, products)
     order, group_ptr, group_source = groups_for(edges, i.source) if groups is None else groups
-    flat = Factored.apply(i.h, i.zc, i.zr, i.angular, i.transport, i.rho, i.desc, i.source, order, group_ptr,
-                          group_source, i.plan.d_out, i.plan.max_bm)
+
+    def launch(zc, zr, desc, d_out, max_bm):
+        return Factored.apply(i.h, zc, zr, i.angular, i.transport, i.rho, desc, i.source, order, group_ptr,
+                              group_source, d_out, max_bm)
+
+    if tiles(kernel) is None:
+        flat = launch(i.zc, i.zr, i.desc, i.plan.d_out, i.plan.max_bm)
+    else:
+        flat = _tiled(kernel, i, launch)
     return SO2FeatureField.from_flat(kernel.field_type_out, flat)
 
 
@@ -307,9 +510,15 @@ def forward_aggregated(kernel: Any, x: SO2FeatureField, edges: Any, weights: Ten
     """Each target's weighted sum of its messages, ``(n_targets,)`` of the output type."""
     i = inputs(kernel, x, edges, products)
     order, group_ptr, group_source = groups_for(edges, i.source) if groups is None else groups
-    flat = FactoredAggregate.apply(i.h, i.zc, i.zr, weights.to(i.h.dtype).contiguous(), i.angular, i.transport, i.rho,
-                                   i.desc, i.source, edges.target_index.contiguous(), edges.row_ptr.contiguous(),
-                                   order, group_ptr, group_source, i.plan.d_out, i.plan.max_bm)
+    w = weights.to(i.h.dtype).contiguous()
+    target, row_ptr = edges.target_index.contiguous(), edges.row_ptr.contiguous()
+
+    if tiles(kernel) is None:
+        flat = FactoredAggregate.apply(i.h, i.zc, i.zr, w, i.angular, i.transport, i.rho, i.desc, i.source, target,
+                                       row_ptr, order, group_ptr, group_source, i.plan.d_out, i.plan.max_bm)
+    else:
+        flat = TiledAggregate.apply(i.h, i.zc, i.zr, w, i.angular, i.transport, i.rho, i.source, target, row_ptr,
+                                    order, group_ptr, group_source, kernel)
     return SO2FeatureField.from_flat(kernel.field_type_out, flat)
 
 

@@ -415,3 +415,17 @@ def block_forward(block, x: dict[int, Tensor], edges, tolerance: float | None = 
     hidden = linear(block.linear1, layer_norm(block.norm2, x), block.hidden_field_type)
     hidden = linear(block.linear2, gated(block.activation, hidden), block.field_type)
     return {f: x[f] + hidden[f] for f in x}
+
+
+def encode_forward(enc, x: dict[int, Tensor], edges, tolerance: float | None = None) -> dict[int, Tensor]:
+    """``IcoEncode.forward`` (reference nn/blocks.py:427-493) on bipartite edges:
+    the per-edge readout of the kernel on the fine sources, times window times
+    quadrature, summed per coarse target."""
+    msgs = readout_messages(enc.kernel, x, edges.source_index, edges.distances, edges.angular_phases,
+                            edges.transport_phases)
+    d = edges.distances
+    tol = tolerance if tolerance is not None else (1e-10 if d.dtype == torch.float64 else 1e-5)
+    win = (d <= enc.cutoff + tol).to(d.dtype) if enc.window == "hard" else torch.relu(1.0 - (d / enc.cutoff) ** 2) ** 2
+    weight = win * edges.tangent_quadrature_weights
+    return {f: torch.segment_reduce(weight.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum", offsets=edges.row_ptr,
+                                    axis=0) for f, m in msgs.items()}

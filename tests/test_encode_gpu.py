@@ -1,0 +1,134 @@
+"""The fine -> coarse restriction (EquiEncode / IcoEncode) over bipartite
+edges on the HIP path, against the oracle (oracle.modules.encode_forward: the
+reference's per-edge readout, windowed and summed per coarse target, float64):
+
+* the GPU bipartite geometry and hierarchy equal the host's (edge lists bit
+  for bit, tables within 1e-11);
+* forward and every gradient in float32 (1e-5) and float64 (1e-10), for a
+  kernel within the fused op's bounds and for wide kernels that run as output
+  tiles (C5's 4 -> 64 and 64 -> 128 copies per frequency), batch 2;
+* gauge equivariance under independent random rotations of both grids'
+  frames."""
+
+import math
+
+import pytest
+import torch
+
+import problems
+from gm_attention_amd.discretization import edge_geometry as eg
+from gm_attention_amd.discretization.frames import build_tangent_frames, rotate_tangent_frames
+from gm_attention_amd.discretization.grid import build_equiangular_grid
+from gm_attention_amd.discretization.hierarchy import build_grid_hierarchy
+from gm_attention_amd.nn import fused_factored
+from gm_attention_amd.nn.blocks import EquiEncode
+from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
+from oracle import modules
+from test_attention_gpu import close
+
+pytestmark = pytest.mark.gpu
+
+D64 = torch.float64
+
+
+def levels(device=None):
+    grids = [build_equiangular_grid(17, 34, device=device), build_equiangular_grid(9, 18, device=device),
+             build_equiangular_grid(5, 10, device=device)]
+    return build_grid_hierarchy(grids, ["equiangular"] * 3, [(17, 34), (9, 18), (5, 10)],
+                                restrict_cutoffs=[1.5 * math.pi / 8, 1.5 * math.pi / 4],
+                                interpolate_cutoffs=[1.5 * math.pi / 8, 1.5 * math.pi / 4],
+                                local_cutoffs=[None, [3 * math.pi / 8], [3 * math.pi / 4]])
+
+
+def test_gpu_hierarchy_equals_the_host(cuda):
+    host, dev = levels(), levels(cuda)
+    for a, b in zip(host.down_edges + host.up_edges, dev.down_edges + dev.up_edges):
+        assert b.edge_index.device.type == "cuda"
+        assert torch.equal(a.edge_index, b.edge_index.cpu()) and torch.equal(a.row_ptr, b.row_ptr.cpu())
+        for name in ("log_coordinates", "distances", "tangent_quadrature_weights", "transport_phases"):
+            torch.testing.assert_close(getattr(b, name).cpu(), getattr(a, name), rtol=0, atol=1e-11, msg=name)
+        far = a.distances > 1e-9
+        torch.testing.assert_close(b.angular_phases.cpu()[far], a.angular_phases[far], rtol=0, atol=1e-11)
+
+
+def split(ft, flat):
+    return dict(SO2FeatureField.from_flat(ft, flat).coefficients)
+
+
+def run(enc, flat, edges, probe, *, oracle=False, tolerance=None):
+    leaf = flat.clone().requires_grad_(True)
+    enc.zero_grad(set_to_none=True)
+    if oracle:
+        out = modules.flat(modules.encode_forward(enc.integral, split(enc.field_type_in, leaf), edges, tolerance))
+    else:
+        out = enc(SO2FeatureField.from_flat(enc.field_type_in, leaf), edges).to_flat()
+    (out * probe.to(out.device, out.dtype)).sum().backward()
+    return out.detach(), leaf.grad, {n: p.grad for n, p in enc.named_parameters() if p.grad is not None}
+
+
+CASES = [({0: 2, 1: 2, 2: 2}, {0: 8, 1: 8, 2: 8}, "quartic", 0), ({0: 4}, {0: 64, 1: 64, 2: 64}, "quartic", 0),
+         ({0: 8, 1: 8, 2: 8}, {0: 40, 1: 40, 2: 40}, "hard", 0), ({0: 16, 1: 16, 2: 16}, {0: 40, 1: 24, 2: 36},
+                                                                  "quartic", 1)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("case", CASES)
+def test_encode_matches_the_oracle(case, dtype, cuda):
+    fin, fout, window, hop = case
+    print(f"encode {fin} -> {fout} hop {hop} {dtype}", flush=True)
+    h = levels().tile(2)
+    edges = h.down_edges[hop]
+    n_fine = h.levels[hop].n_nodes
+    torch.manual_seed(0)
+    enc = EquiEncode(SO2FieldType(fin), SO2FieldType(fout), cutoff=[1.5 * math.pi / 8, 1.5 * math.pi / 4][hop],
+                     window=window, n_radial_basis=4, dtype=D64)
+    with torch.no_grad():
+        for p in enc.parameters():
+            p.add_(0.1 * torch.randn_like(p))
+    x = problems.normal((n_fine, SO2FieldType(fin).dimension), 1)
+    probe = problems.normal((edges.row_ptr.shape[0] - 1, SO2FieldType(fout).dimension), 2)
+    if dtype == torch.float32:
+        enc.load_state_dict({k: v.float().double() for k, v in enc.state_dict().items()})
+        x = x.float().double()
+        edges_o = edges.to(None, torch.float32).to(None, D64)
+    else:
+        edges_o = edges
+    want = run(enc, x, edges_o, probe, oracle=True, tolerance=1e-5 if dtype == torch.float32 else None)
+    gpu = EquiEncode(SO2FieldType(fin), SO2FieldType(fout), cutoff=enc.cutoff, window=window, n_radial_basis=4,
+                     dtype=dtype, device=cuda)
+    gpu.load_state_dict({k: v.to(dtype) for k, v in enc.state_dict().items()})
+    assert fused_factored.enabled(gpu.integral.kernel, SO2FeatureField.from_flat(gpu.field_type_in, x.to(cuda, dtype)),
+                                  edges.to(cuda, dtype))
+    got = run(gpu, x.to(cuda, dtype), edges.to(cuda, dtype), probe)
+    close(got[0], want[0], dtype, "out")
+    close(got[1], want[1], dtype, "dx")
+    assert set(got[2]) == set(want[2])
+    for k in want[2]:
+        close(got[2][k], want[2][k], dtype, f"d{k}", reduction=True)
+
+
+def test_encode_is_gauge_equivariant(cuda):
+    fine, coarse = build_equiangular_grid(12, 24), build_equiangular_grid(7, 14)
+    cutoff = 1.5 * math.pi / 6
+    ff, cf = build_tangent_frames(fine.nodes), build_tangent_frames(coarse.nodes)
+    gen = torch.Generator().manual_seed(4)
+    tf = torch.rand(fine.n_nodes, dtype=D64, generator=gen) * 2 * math.pi
+    tc = torch.rand(coarse.n_nodes, dtype=D64, generator=gen) * 2 * math.pi
+
+    def edges(a, b):
+        return eg.compute_bipartite_edge_geometry(fine.nodes, a, fine.quadrature_weights, coarse.nodes, b,
+                                                  cutoff=cutoff, max_frequency=4, source_exact_nodes=fine.exact_nodes,
+                                                  target_exact_nodes=coarse.exact_nodes).to(cuda, D64)
+
+    base = edges(ff, cf)
+    turned = edges(rotate_tangent_frames(ff, tf), rotate_tangent_frames(cf, tc))
+    torch.manual_seed(0)
+    fin, fout = SO2FieldType({0: 4, 1: 4, 2: 4}), SO2FieldType({0: 40, 1: 40, 2: 40})
+    enc = EquiEncode(fin, fout, cutoff=cutoff, n_radial_basis=4, dtype=D64, device=cuda)
+    x = SO2FeatureField.from_flat(fin, problems.normal((fine.n_nodes, fin.dimension), 1).to(cuda))
+    with torch.no_grad():
+        y = enc(x, base)
+        y_turned = enc(x.gauge_transform(tf.to(cuda)), turned)
+    want = y.gauge_transform(tc.to(cuda))
+    torch.testing.assert_close(y_turned.to_flat(), want.to_flat(), rtol=1e-9, atol=1e-9)
+    assert float((y.to_flat() - want.to_flat()).abs().max()) > 1e-3
