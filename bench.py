@@ -760,6 +760,15 @@ def main() -> None:
                                f"edge, extrapolated to {E} edges")}
         log(f"cpu baseline: {baseline['value']:.1f} qp/s ({baseline['sample']})")
 
+    # the whole step's HBM traffic (every kernel's FETCH_SIZE + WRITE_SIZE of one steady-state step, measured
+    # with rocprofv3) over this run's step time: the layer's achieved HBM bandwidth
+    hbm = None
+    step_file = ROOT / "profiles" / f"{args.workload}_ns_step_traffic.json"
+    if step_file.exists():
+        step_bytes = json.loads(step_file.read_text())["step_bytes"]
+        achieved = step_bytes / (ms_per_step * 1e-3) / 1e9
+        hbm = {"achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+               "step_traffic": step_bytes, "source": str(step_file.relative_to(ROOT))}
     line = {
         "metric": {"attention": "attn fwd+bwd query-points/s at 256x512 B=4",
                    "softmax": "attn scores+softmax fwd+bwd query-points/s at 256x512 B=4",
@@ -780,6 +789,7 @@ def main() -> None:
                    "field": "{0:32,1:32,2:32}", "heads": HEADS, "radius": "3 row spacings", "window": "hard",
                    "query_points": N, "edges": E, "max_degree": g.max_degree},
         "roofline": roof,
+        "hbm_step": hbm,
         "ops": op_rates,
         "cpu_baseline": baseline,
     }

@@ -432,7 +432,7 @@ class TiledAggregate(torch.autograd.Function):
                 rho: Tensor, source: Tensor, target: Tensor, row_ptr: Tensor, order: Tensor, group_ptr: Tensor,
                 group_source: Tensor, kernel: Any) -> Tensor:
         ext = extension(cuda=h.is_cuda)
-        parts, rows = [], []
+        parts, saved = [], []
         with torch.profiler.record_function("gm::kernel/pairs_tiles"):
             for index, t in enumerate(tiles(kernel)):
                 desc, zc_cols, zr_cols = _tile_tensors(kernel, t, index, h.device)
@@ -440,33 +440,34 @@ class TiledAggregate(torch.autograd.Function):
                 zr_t = zr.index_select(2, zr_cols).contiguous() if zr_cols.numel() else zr[:, :, :0].contiguous()
                 r = ext.forward(h, zc_t, zr_t, angular, transport, rho, desc, source, order, group_ptr, group_source,
                                 t.d_out, t.max_bm)
-                rows.append(r)
+                saved += [r, zc_t, zr_t]  # the tiles' mixes together hold what zc and zr hold
                 parts.append(ext.aggregate(r, weights, row_ptr))
-        ctx.save_for_backward(h, zc, zr, weights, angular, transport, rho, source, target, order, group_ptr,
-                              group_source, *rows)
+        ctx.save_for_backward(h, weights, angular, transport, rho, source, target, order, group_ptr, group_source,
+                              *saved)
         ctx.kernel = kernel
+        ctx.shapes = (zc.shape, zr.shape, zc.dtype)
         return _untile(kernel, parts, h.device)
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad_out: Tensor) -> tuple:
-        h, zc, zr, weights, angular, transport, rho, source, target, order, group_ptr, group_source = \
-            ctx.saved_tensors[:12]
-        rows = ctx.saved_tensors[12:]
+        h, weights, angular, transport, rho, source, target, order, group_ptr, group_source = ctx.saved_tensors[:10]
+        per_tile = ctx.saved_tensors[10:]
         kernel = ctx.kernel
         ext = extension(cuda=h.is_cuda)
         grad_out = grad_out.contiguous()
-        dzc, dzr = torch.empty_like(zc), torch.empty_like(zr)
+        zc_shape, zr_shape, dtype = ctx.shapes
+        dzc = torch.empty(zc_shape, dtype=dtype, device=h.device)
+        dzr = torch.empty(zr_shape, dtype=dtype, device=h.device)
         dh = dweights = None
         offset = 0
         with torch.profiler.record_function("gm::kernel/pairs_tiles_backward"):
-            for index, (t, r) in enumerate(zip(tiles(kernel), rows)):
+            for index, t in enumerate(tiles(kernel)):
+                r, zc_t, zr_t = per_tile[3 * index:3 * index + 3]
                 desc, zc_cols, zr_cols = _tile_tensors(kernel, t, index, h.device)
                 cols = _untile_columns(kernel, h.device)[offset:offset + t.d_out]
                 offset += t.d_out
                 g_t = grad_out.index_select(1, cols).contiguous()
-                zc_t = zc.index_select(2, zc_cols).contiguous() if zc_cols.numel() else zc[:, :, :0].contiguous()
-                zr_t = zr.index_select(2, zr_cols).contiguous() if zr_cols.numel() else zr[:, :, :0].contiguous()
                 dh_t, dzc_t, dzr_t, dw_t = ext.backward_aggregated(g_t, target, weights, r, h, zc_t, zr_t, angular,
                                                                    transport, rho, desc, source, order, group_ptr,
                                                                    group_source)
