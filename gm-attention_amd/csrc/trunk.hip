@@ -12,12 +12,12 @@
 // apply_radial_trunk, :605-607 _trunk_hidden; one Linear + SiLU layer).
 //
 // Forward: one thread per edge for every head, the basis computed once from
-// rho, the heads' parameters as uniform operands.  Backward: a fixed grid whose threads
-// stride over the edges, per head accumulating their (T x B + T) gradient
-// terms in registers (recomputing the basis and pre-activation), then one
-// fixed-order reduction per workgroup into a partial row; a second kernel
-// sums the partial rows in order.  No atomics: the parameter gradients are
-// deterministic.
+// rho, the heads' parameters as uniform operands.  Backward: persistent
+// wavefronts over 16-edge tiles, the basis once per tile, every head's
+// pre-activation and its (T x B + T) gradient terms on MFMA with the
+// accumulators in registers across the wave's tiles, one partial row per
+// wavefront; a second kernel sums the partial rows in order.  No atomics:
+// the parameter gradients are deterministic.
 #include <hip/hip_runtime.h>
 
 #include "common.hpp"
@@ -38,6 +38,7 @@ struct TrunkArgs {
   int64_t n_edges;
   int H, T, B;
   float inv_width;      // 1 / sigma
+  int rho_vec4;         // backward: rho 16-byte aligned (4 edges per load)
 };
 
 // exp(x) as 2^(x log2 e) on the hardware exponential, and 1 / x on the
@@ -89,94 +90,160 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_forward_kernel(TrunkArgs 
   }
 }
 
-// A fixed grid whose threads stride over the edges; per head and per half of
-// its features, each thread accumulates its gradient terms in registers
-// (recomputing the basis and pre-activation, the next edge's loads issued
-// before this edge's arithmetic), then one fixed-order reduction per
-// workgroup into a partial row.
-template <int T, int B>
-__global__ __launch_bounds__(kTrunkThreads) void trunk_backward_kernel(TrunkArgs a) {
-  constexpr int P = T * B + T, TH = T / 2, PH = TH * B + TH;
-  __shared__ float red[kTrunkThreads / 64][PH];  // per-wave sums
-  const ConstPtr weight = as_const(a.weight), bias = as_const(a.bias), centers = as_const(a.centers);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // Waves 0-1 take features 0..TH-1 and waves 2-3 features TH..T-1 of the same edges in the
-  // same pass, so the second half of each dh row is read while its line is still in L2
-  // (one pass per head; the features' half is wave-uniform, so the weights stay scalar operands).
-  constexpr int kEdgeThreads = kTrunkThreads / 2;
-  const int t0 = (wave >> 1) * TH;
-  const int64_t stride = (int64_t)gridDim.x * kEdgeThreads;
-  const int64_t first = (int64_t)blockIdx.x * kEdgeThreads + (threadIdx.x & (kEdgeThreads - 1));
-  for (int hh = 0; hh < a.H; ++hh) {
-    const ConstPtr W = weight + hh * T * B;
-    float acc[PH];
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int kTrunkMaxHeads = 8;
+constexpr int kTrunkWaves = kTrunkThreads / 64;
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Persistent wavefronts over tiles of 16 edges (tile w, w + W, ... for wave w
+// of W).  Lane l = 16 q + c (q = l / 16, c = l % 16) of the 16x16x4 MFMA:
+//   pre (feature 4q + r, edge c), r < 4, = D1 = A1 B1 with
+//     A1[feature c][basis q + 4s] = W[c][q + 4s] and B1[basis q + 4s][edge c] = b_{q+4s}(edge c), s = 0, 1
+//     (the basis once per tile, shared by every head; the bias as the weight of a
+//     basis entry that is 1, in the first free slot), so a lane's four
+//     features of one edge come from one 16-byte load of its dh row;
+//   dp = dh * SiLU'(pre), turned through the wave's 1 KB LDS tile to
+//     B2_j[q][feature c] = dp(feature c, edge 4q + j), j < 4 (one 16-byte LDS read);
+//   D2[m][feature c] += sum over j of A2_j B2_j with
+//     A2_j[m = c][k = q] = b_c(edge 4q + j) (c < B), 1 at c = B, 0 above,
+//   so D2's rows m < B are dW^T and row B is db, accumulated over the wave's
+//   tiles in registers for every head.  Edges past the end read dh as zero and add nothing.
+template <int B>
+__global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a) {
+  constexpr int T = 16, P = T * B + T;
+  __shared__ float4 stage[kTrunkWaves][T * 4];  // per wave: dp as [feature][edge]
+  const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15, wv = threadIdx.x >> 6;
+  float* tile_lds = reinterpret_cast<float*>(stage[wv]);
+  const int64_t wave = (int64_t)blockIdx.x * kTrunkWaves + wv;
+  const int64_t n_waves = (int64_t)gridDim.x * kTrunkWaves;
+  const int64_t n_tiles = (a.n_edges + 15) / 16;
+  const ConstPtr centers = as_const(a.centers);
+  // A1 operands per head: basis index k = q + 4s takes W[c][k] for k < B, the bias at k = B (its basis
+  // entry is 1), zero above; B = 8 puts the bias in a third step (k = 8, lane q = 0)
+  float w0[kTrunkMaxHeads], w1[kTrunkMaxHeads], w2[kTrunkMaxHeads];
+  floatx4 acc[kTrunkMaxHeads];
+  auto a1_weight = [&](int h, int k) {
+    if (h >= a.H) return 0.f;
+    if (k < B) return a.weight[(h * T + c) * B + k];
+    return (k == B && a.bias) ? a.bias[h * T + c] : 0.f;
+  };
 #pragma unroll
-    for (int i = 0; i < PH; ++i) acc[i] = 0.f;
-    const float* dh = a.dh + (int64_t)hh * a.n_edges * T + t0;
-    float4 g[TH / 4];
-    float r = 0.f;
-    if (first < a.n_edges) {
-      r = a.rho[first];
+  for (int h = 0; h < kTrunkMaxHeads; ++h) {
+    w0[h] = a1_weight(h, q);
+    w1[h] = a1_weight(h, q + 4);
+    w2[h] = q == 0 ? a1_weight(h, 8) : 0.f;
+    acc[h] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float mu0 = q < B ? centers[q] : 0.f, mu1 = q + 4 < B ? centers[q + 4] : 0.f;
+  const float mu2 = c < B ? centers[c] : 0.f;
+  const float iw = a.inv_width;
+  auto gauss = [iw](float r, float mu) {
+    const float z = (r * r - mu) * iw;
+    return fast_exp(-0.5f * z * z);
+  };
+  // dh of head h for this lane's edge c of a tile, features 4q..4q+3 (zero past the end)
+  auto load_dh = [&](int64_t e0, int h) {
+    return (h < a.H && e0 + c < a.n_edges)
+               ? *reinterpret_cast<const float4*>(a.dh + ((int64_t)h * a.n_edges + e0 + c) * T + 4 * q)
+               : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  // rho of a tile: edge c (the B1 operand) and edges 4q..4q+3 (the A2 operands)
+  auto load_rho = [&](int64_t e0, float& rc, float* r4) {
+    rc = e0 + c < a.n_edges ? a.rho[e0 + c] : 0.f;
+    if (e0 + 16 <= a.n_edges && a.rho_vec4) {
+      const float4 v = *reinterpret_cast<const float4*>(a.rho + e0 + 4 * q);
+      r4[0] = v.x;
+      r4[1] = v.y;
+      r4[2] = v.z;
+      r4[3] = v.w;
+    } else {
 #pragma unroll
-      for (int u = 0; u < TH / 4; ++u) g[u] = *reinterpret_cast<const float4*>(dh + first * T + 4 * u);
+      for (int j = 0; j < 4; ++j) r4[j] = e0 + 4 * q + j < a.n_edges ? a.rho[e0 + 4 * q + j] : 0.f;
     }
-    // each thread's edges e = first, first + stride, ... in order
-    for (int64_t e = first; e < a.n_edges; e += stride) {
-      const float rc = r;
-      float gv[TH];
+  };
+  // Loads complete in issue order, so each tile issues the next tile's rho first and then, head by
+  // head, the next tile's dh into the register it has just consumed: nothing waited for is younger
+  // than what the wave needs next.
+  float rc, r4[4];
+  load_rho(wave * 16, rc, r4);
+  float4 g[kTrunkMaxHeads];
 #pragma unroll
-      for (int u = 0; u < TH / 4; ++u) {
-        gv[4 * u] = g[u].x;
-        gv[4 * u + 1] = g[u].y;
-        gv[4 * u + 2] = g[u].z;
-        gv[4 * u + 3] = g[u].w;
+  for (int h = 0; h < kTrunkMaxHeads; ++h) g[h] = load_dh(wave * 16, h);
+  for (int64_t tile = wave; tile < n_tiles; tile += n_waves) {
+    const int64_t e_next = (tile + n_waves) * 16;
+    float rc_next, r4_next[4];
+    load_rho(e_next, rc_next, r4_next);
+    const float b1_0 = q < B ? gauss(rc, mu0) : (q == B ? 1.f : 0.f);
+    const float b1_1 = q + 4 < B ? gauss(rc, mu1) : (q + 4 == B ? 1.f : 0.f);
+    const float b1_2 = q == 0 ? 1.f : 0.f;  // the bias step when B = 8
+    float a2[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a2[j] = c < B ? gauss(r4[j], mu2) : (c == B ? 1.f : 0.f);
+#pragma unroll
+    for (int h = 0; h < kTrunkMaxHeads; ++h) {
+      if (h >= a.H) break;
+      floatx4 pre = mfma16(w0[h], b1_0, floatx4{0.f, 0.f, 0.f, 0.f});
+      pre = mfma16(w1[h], b1_1, pre);
+      if (B == 8) pre = mfma16(w2[h], b1_2, pre);
+      const float gv[4] = {g[h].x, g[h].y, g[h].z, g[h].w};
+      g[h] = load_dh(e_next, h);
+      wave_sync();  // the previous head's LDS reads are done
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sg = sigmoid_of(pre[r]);
+        tile_lds[(4 * q + r) * 16 + c] = gv[r] * sg * (1.f + pre[r] * (1.f - sg));
       }
-      const int64_t en = e + stride;
-      if (en < a.n_edges) {
-        r = a.rho[en];
-#pragma unroll
-        for (int u = 0; u < TH / 4; ++u) g[u] = *reinterpret_cast<const float4*>(dh + en * T + 4 * u);
-      }
-      float b[B];
-      basis_of<B>(rc, centers, a.inv_width, b);
-#pragma unroll
-      for (int t = 0; t < TH; ++t) {
-        float p = bias ? bias[hh * T + t0 + t] : 0.f;
-#pragma unroll
-        for (int k = 0; k < B; ++k) p = fmaf(W[(t0 + t) * B + k], b[k], p);
-        const float sg = sigmoid_of(p);
-        const float dp = gv[t] * sg * (1.f + p * (1.f - sg));  // dh * d silu / d pre
-#pragma unroll
-        for (int k = 0; k < B; ++k) acc[t * B + k] = fmaf(dp, b[k], acc[t * B + k]);
-        acc[TH * B + t] += dp;
-      }
+      wave_sync();
+      const float4 dp = stage[wv][c * 4 + q];  // dp(feature c, edges 4q..4q+3)
+      acc[h] = mfma16(a2[0], dp.x, acc[h]);
+      acc[h] = mfma16(a2[1], dp.y, acc[h]);
+      acc[h] = mfma16(a2[2], dp.z, acc[h]);
+      acc[h] = mfma16(a2[3], dp.w, acc[h]);
     }
-    // the block's sum in a fixed order: a butterfly per wave, then the half's two waves in order
+    rc = rc_next;
 #pragma unroll
-    for (int i = 0; i < PH; ++i) {
-      float v = acc[i];
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-      if (lane == 0) red[wave][i] = v;
+    for (int j = 0; j < 4; ++j) r4[j] = r4_next[j];
+  }
+  // this wave's partial row: dW[h][c][m] for D2 rows m < B, db[h][c] for row m = B
+  float* out = a.partial + wave * a.H * P;
+#pragma unroll
+  for (int h = 0; h < kTrunkMaxHeads; ++h) {
+    if (h >= a.H) break;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * q + r;
+      if (m < B)
+        out[h * P + c * B + m] = acc[h][r];
+      else if (m == B)
+        out[h * P + T * B + c] = acc[h][r];
     }
-    __syncthreads();
-    for (int i = threadIdx.x; i < 2 * PH; i += blockDim.x) {
-      const int half = i / PH, j = i % PH;
-      const float sum = red[2 * half][j] + red[2 * half + 1][j];
-      // weights of features half * TH .. half * TH + TH - 1, then their biases
-      const int slot = j < TH * B ? half * TH * B + j : T * B + half * TH + (j - TH * B);
-      a.partial[((int64_t)blockIdx.x * a.H + hh) * P + slot] = sum;
-    }
-    __syncthreads();
   }
 }
 
-// out[h][i] = sum over blocks of partial[block][h][i], blocks in order.
-__global__ __launch_bounds__(256) void trunk_reduce_kernel(const float* partial, int64_t n_blocks, int HP, float* out) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= HP) return;
+// out[i] = sum over rows r of partial[r][i]: one workgroup per column, each
+// thread summing rows t, t + 256, ... in order, then a fixed tree.
+__global__ __launch_bounds__(256) void trunk_reduce_kernel(const float* partial, int64_t rows, int HP, float* out) {
+  __shared__ float buf[256];
+  const int i = blockIdx.x;
   float s = 0.f;
-  for (int64_t b = 0; b < n_blocks; ++b) s += partial[b * HP + i];
-  out[i] = s;
+  for (int64_t r = threadIdx.x; r < rows; r += 256) s += partial[r * HP + i];
+  buf[threadIdx.x] = s;
+  __syncthreads();
+  for (int step = 128; step > 0; step >>= 1) {
+    if (threadIdx.x < step) buf[threadIdx.x] += buf[threadIdx.x + step];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[i] = buf[0];
 }
 
 int prepare(TrunkArgs& a, const float* rho, const float* weight, const float* bias, const float* centers,
@@ -199,10 +266,10 @@ int prepare(TrunkArgs& a, const float* rho, const float* weight, const float* bi
   return GM_OK;
 }
 
-constexpr int64_t kTrunkBackwardBlocks = 2048;  // the backward's fixed grid (threads stride over the edges)
+constexpr int64_t kTrunkBackwardBlocks = 2048;  // the backward's fixed grid (waves stride over 16-edge tiles)
 
 int64_t backward_blocks(int64_t n_edges) {
-  const int64_t need = (n_edges + kTrunkThreads / 2 - 1) / (kTrunkThreads / 2);  // 128 edges per block pass
+  const int64_t need = (n_edges + 16 * kTrunkWaves - 1) / (16 * kTrunkWaves);  // one tile per wave
   return need < kTrunkBackwardBlocks ? (need > 0 ? need : 1) : kTrunkBackwardBlocks;
 }
 
@@ -213,7 +280,7 @@ void launch(bool forward, const TrunkArgs& a, hipStream_t stream) {
   if (forward)
     hipLaunchKernelGGL((trunk_forward_kernel<16, B>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((trunk_backward_kernel<16, B>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((trunk_backward_mfma<B>), grid, block, 0, stream, a);
 }
 
 void launch_any(bool forward, const TrunkArgs& a, hipStream_t stream) {
@@ -228,7 +295,8 @@ void launch_any(bool forward, const TrunkArgs& a, hipStream_t stream) {
 }  // namespace
 }  // namespace gm
 
-extern "C" int64_t gm_radial_trunk_partials(int64_t n_edges) { return gm::backward_blocks(n_edges); }
+// Partial rows of the backward: one per wavefront of its grid.
+extern "C" int64_t gm_radial_trunk_partials(int64_t n_edges) { return gm::backward_blocks(n_edges) * gm::kTrunkWaves; }
 
 extern "C" int gm_radial_trunk_forward_f32(const float* rho, const float* weight, const float* bias,
                                            const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B,
@@ -252,17 +320,18 @@ extern "C" int gm_radial_trunk_backward_f32(const float* dh, const float* rho, c
   GM_REQUIRE(dparams, "dparams must be a device pointer");
   const int HP = (int)(H * (T * B + T));
   if (n_edges == 0) {
-    hipLaunchKernelGGL(gm::trunk_reduce_kernel, dim3((HP + 255) / 256), dim3(256), 0, (hipStream_t)stream, partial,
-                       (int64_t)0, HP, dparams);
+    hipLaunchKernelGGL(gm::trunk_reduce_kernel, dim3(HP), dim3(256), 0, (hipStream_t)stream, partial, (int64_t)0, HP,
+                       dparams);
     return gm::check_launch("radial_trunk_backward (empty)");
   }
   GM_REQUIRE(dh && gm::aligned(dh, 16) && partial, "dh (16-byte aligned) and partial must be device pointers");
   a.dh = dh;
   a.partial = partial;
+  a.rho_vec4 = gm::aligned(rho, 16);
   gm::launch_any(false, a, (hipStream_t)stream);
   int rc = gm::check_launch("radial_trunk_backward");
   if (rc != GM_OK) return rc;
-  hipLaunchKernelGGL(gm::trunk_reduce_kernel, dim3((HP + 255) / 256), dim3(256), 0, (hipStream_t)stream, partial,
+  hipLaunchKernelGGL(gm::trunk_reduce_kernel, dim3(HP), dim3(256), 0, (hipStream_t)stream, partial,
                      gm_radial_trunk_partials(n_edges), HP, dparams);
   return gm::check_launch("radial_trunk_backward (reduce)");
 }
