@@ -11,12 +11,12 @@
 // torch ops (nn/kernels.py:191-231 _GaussianRadialBasis, :108-117
 // apply_radial_trunk, :605-607 _trunk_hidden; one Linear + SiLU layer).
 //
-// Forward: one thread per edge for every head, the basis computed once from
-// rho, the heads' parameters as uniform operands.  Backward: persistent
-// wavefronts over 16-edge tiles, the basis once per tile, every head's
-// pre-activation and its (T x B + T) gradient terms on MFMA with the
-// accumulators in registers across the wave's tiles, one partial row per
-// wavefront; a second kernel sums the partial rows in order.  No atomics:
+// Both directions: persistent wavefronts over 16-edge tiles, the basis once
+// per tile for every head, each head's pre-activations on MFMA.  The forward
+// stores SiLU(pre) as whole 1 KB tiles; the backward forms each head's
+// (T x B + T) gradient terms on MFMA with the accumulators in registers across
+// the wave's tiles, one partial row per wavefront, and a second kernel sums
+// the partial rows in a fixed order.  No atomics:
 // the parameter gradients are deterministic.
 #include <hip/hip_runtime.h>
 
@@ -54,41 +54,6 @@ __device__ __forceinline__ float sigmoid_of(float x) { return fast_rcp(1.f + fas
 // (scalar) loads and SGPR operands.
 typedef const __attribute__((address_space(4))) float* ConstPtr;
 __device__ __forceinline__ ConstPtr as_const(const float* p) { return (ConstPtr)p; }
-
-template <int B>
-__device__ __forceinline__ void basis_of(float r, ConstPtr centers, float inv_width, float* b) {
-  const float s = r * r;
-#pragma unroll
-  for (int k = 0; k < B; ++k) {
-    const float z = (s - centers[k]) * inv_width;
-    b[k] = fast_exp(-0.5f * z * z);
-  }
-}
-
-// One thread per edge for every head: the basis once, then each head's
-// Linear + SiLU with its parameters read as uniform (scalar) operands.
-template <int T, int B>
-__global__ __launch_bounds__(kTrunkThreads) void trunk_forward_kernel(TrunkArgs a) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= a.n_edges) return;
-  const ConstPtr weight = as_const(a.weight), bias = as_const(a.bias);
-  float b[B];
-  basis_of<B>(a.rho[e], as_const(a.centers), a.inv_width, b);
-  for (int hh = 0; hh < a.H; ++hh) {
-    const ConstPtr W = weight + hh * T * B;
-    float out[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      float p = bias ? bias[hh * T + t] : 0.f;
-#pragma unroll
-      for (int k = 0; k < B; ++k) p = fmaf(W[t * B + k], b[k], p);
-      out[t] = p * sigmoid_of(p);
-    }
-    float* dst = a.h + ((int64_t)hh * a.n_edges + e) * T;
-#pragma unroll
-    for (int t = 0; t < T; t += 4) *reinterpret_cast<float4*>(dst + t) = make_float4(out[t], out[t + 1], out[t + 2], out[t + 3]);
-  }
-}
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -230,6 +195,61 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
   }
 }
 
+// Persistent wavefronts over 16-edge tiles, as the backward: every head's
+// pre-activations (feature 4q + r, edge c) from the same two or three MFMAs
+// (the basis once per tile), SiLU in registers, and each lane's four features
+// of its edge stored as one 16-byte store (a head's tile is one contiguous 1 KB).
+template <int B>
+__global__ __launch_bounds__(kTrunkThreads) void trunk_forward_mfma(TrunkArgs a) {
+  constexpr int T = 16;
+  const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15;
+  const int64_t wave = (int64_t)blockIdx.x * kTrunkWaves + (threadIdx.x >> 6);
+  const int64_t n_waves = (int64_t)gridDim.x * kTrunkWaves;
+  const int64_t n_tiles = (a.n_edges + 15) / 16;
+  const ConstPtr centers = as_const(a.centers);
+  float w0[kTrunkMaxHeads], w1[kTrunkMaxHeads], w2[kTrunkMaxHeads];
+  auto a1_weight = [&](int h, int k) {
+    if (h >= a.H) return 0.f;
+    if (k < B) return a.weight[(h * T + c) * B + k];
+    return (k == B && a.bias) ? a.bias[h * T + c] : 0.f;
+  };
+#pragma unroll
+  for (int h = 0; h < kTrunkMaxHeads; ++h) {
+    w0[h] = a1_weight(h, q);
+    w1[h] = a1_weight(h, q + 4);
+    w2[h] = q == 0 ? a1_weight(h, 8) : 0.f;
+  }
+  const float mu0 = q < B ? centers[q] : 0.f, mu1 = q + 4 < B ? centers[q + 4] : 0.f;
+  const float iw = a.inv_width;
+  auto gauss = [iw](float r, float mu) {
+    const float z = (r * r - mu) * iw;
+    return fast_exp(-0.5f * z * z);
+  };
+  const float b1_2 = q == 0 ? 1.f : 0.f;
+  float rc = wave * 16 + c < a.n_edges ? a.rho[wave * 16 + c] : 0.f;
+  for (int64_t tile = wave; tile < n_tiles; tile += n_waves) {
+    const int64_t e0 = tile * 16, e_next = (tile + n_waves) * 16;
+    const bool edge_in = e0 + c < a.n_edges;
+    const float rn = e_next + c < a.n_edges ? a.rho[e_next + c] : 0.f;  // the next tile's, ahead of the stores
+    const float b1_0 = q < B ? gauss(rc, mu0) : (q == B ? 1.f : 0.f);
+    const float b1_1 = q + 4 < B ? gauss(rc, mu1) : (q + 4 == B ? 1.f : 0.f);
+#pragma unroll
+    for (int h = 0; h < kTrunkMaxHeads; ++h) {
+      if (h >= a.H) break;
+      floatx4 pre = mfma16(w0[h], b1_0, floatx4{0.f, 0.f, 0.f, 0.f});
+      pre = mfma16(w1[h], b1_1, pre);
+      if (B == 8) pre = mfma16(w2[h], b1_2, pre);
+      float4 out;
+      out.x = pre[0] * sigmoid_of(pre[0]);
+      out.y = pre[1] * sigmoid_of(pre[1]);
+      out.z = pre[2] * sigmoid_of(pre[2]);
+      out.w = pre[3] * sigmoid_of(pre[3]);
+      if (edge_in) *reinterpret_cast<float4*>(a.h + ((int64_t)h * a.n_edges + e0 + c) * T + 4 * q) = out;
+    }
+    rc = rn;
+  }
+}
+
 // out[i] = sum over rows r of partial[r][i]: one workgroup per column, each
 // thread summing rows t, t + 256, ... in order, then a fixed tree.
 __global__ __launch_bounds__(256) void trunk_reduce_kernel(const float* partial, int64_t rows, int HP, float* out) {
@@ -275,10 +295,9 @@ int64_t backward_blocks(int64_t n_edges) {
 
 template <int B>
 void launch(bool forward, const TrunkArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)(forward ? (a.n_edges + kTrunkThreads - 1) / kTrunkThreads : backward_blocks(a.n_edges))),
-      block(kTrunkThreads);
+  const dim3 grid((unsigned)backward_blocks(a.n_edges)), block(kTrunkThreads);
   if (forward)
-    hipLaunchKernelGGL((trunk_forward_kernel<16, B>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((trunk_forward_mfma<B>), grid, block, 0, stream, a);
   else
     hipLaunchKernelGGL((trunk_backward_mfma<B>), grid, block, 0, stream, a);
 }

@@ -17,15 +17,18 @@ from oracle import modules
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("n_basis,bias", [(8, True), (6, False), (4, True)])
-def test_trunk_matches_the_oracle(n_basis, bias, cuda):
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("n_basis,bias", [(8, True), (8, False), (6, True), (6, False), (4, True), (4, False)])
+def test_trunk_matches_the_oracle(n_basis, bias, offset, cuda):
+    """offset 1: the distances start one element into their storage (not 16-byte
+    aligned) and number no multiple of the 16-edge tiles."""
     disc = problems.discretization(16, 32)
     edges = disc.edge_geometry.tile(3, n_sources=disc.n_nodes)
     torch.manual_seed(1)
     kernels = [SO2SteerableKernel(SO2FieldType({0: 2, 1: 2}), SO2FieldType({0: 1, 1: 1}), cutoff=disc.coverage_radius,
                                   n_radial_basis=n_basis, bias=bias, dtype=torch.float32) for _ in range(5)]
-    d32 = edges.distances.float()
-    probe = problems.normal((5, edges.n_edges, 16), 4)
+    d32 = edges.distances.float()[offset:]
+    probe = problems.normal((5, d32.shape[0], 16), 4)
     # oracle: float64 on the rounded parameters and distances
     want, want_grads = [], []
     for k, pr in zip(kernels, probe):
@@ -42,7 +45,10 @@ def test_trunk_matches_the_oracle(n_basis, bias, cuda):
     for g, k in zip(gk, kernels):
         g.load_state_dict(k.state_dict())
     assert radial.eligible(gk, torch.float32, cuda)
-    rho = (d32 / disc.coverage_radius).to(cuda)
+    rho_all = (edges.distances.float() / disc.coverage_radius).to(cuda)
+    rho = rho_all[offset:]
+    if offset:
+        assert rho.data_ptr() % 16 != 0 and rho.shape[0] % 16 != 0
     h = radial.trunk_hidden_heads(gk, rho)
     (h * probe.float().to(cuda)).sum().backward()
     for head in range(5):
