@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -1223,6 +1224,7 @@ using SlotsF2 = StaticSlots<5, 20, 0x28380u, 0x70a80u, 0x79680u, 0x28884u, 0x300
 // frequencies 0..1, four copies each: 5 slots
 using SlotsF1 = StaticSlots<3, 12, 0x18380u, 0x60e80u, 0x18884u, 0x20084u, 0x61484u>;
 
+
 template <class P>
 __device__ __forceinline__ uint32_t slot_word(const FactArgs<float>& a, int s) {
   if constexpr (P::kStatic)
@@ -1273,28 +1275,173 @@ __device__ __forceinline__ void bstore4(floatx4 v, __amdgpu_buffer_rsrc_t r, int
 }
 constexpr int kDrop = 0x7FFFFFF0;  // a byte offset past every group's span: the access is dropped
 
+// SlotsF2 by Horner's rule.  With z = r e^{i phi}, w = e^{i gamma} and
+// p = z conj(w), the thirteen factors are
+//   output 0 (real part): 1, p, p^2                      (slots 0, 1, 2)
+//   output 1: z, w, z p, conj(z) w^2, z p^2               (slots 3 .. 7)
+//   output 2: z^2, z w, z^2 p, w^2, z^2 p^2               (slots 8 .. 12)
+// so each output is a leading power times a quadratic in p plus two single
+// terms: 75 operations a tile instead of a product per slot.
+template <class P>
+constexpr bool kHorner = std::is_same<P, SlotsF2>::value;
+
+struct F2Powers {
+  float pr, pi;    // p = z conj(w)
+  float z2r, z2i;  // z^2
+  float w2r, w2i;  // w^2
+  float zwr, zwi;  // z w
+  float cr, ci;    // conj(z) w^2
+};
+
+__device__ __forceinline__ F2Powers f2_powers(const floatx4& zw) {
+  const float zr = zw[0], zi = zw[1], wr = zw[2], wi = zw[3];
+  F2Powers f;
+  f.pr = zr * wr + zi * wi;
+  f.pi = zi * wr - zr * wi;
+  f.z2r = zr * zr - zi * zi;
+  f.z2i = 2.f * (zr * zi);
+  f.w2r = wr * wr - wi * wi;
+  f.w2i = 2.f * (wr * wi);
+  f.zwr = zr * wr - zi * wi;
+  f.zwi = zr * wi + zi * wr;
+  f.cr = zr * f.w2r + zi * f.w2i;
+  f.ci = zr * f.w2i - zi * f.w2r;
+  return f;
+}
+
+// x y + c (complex)
+__device__ __forceinline__ void cmac(float xr, float xi, float yr, float yi, float cr, float ci, float& r, float& i) {
+  r = fmaf(xr, yr, fmaf(-xi, yi, cr));
+  i = fmaf(xr, yi, fmaf(xi, yr, ci));
+}
+
+// conj(x) y
+__device__ __forceinline__ void cjmul(float xr, float xi, float yr, float yi, float& r, float& i) {
+  r = fmaf(xr, yr, xi * yi);
+  i = fmaf(xr, yi, -(xi * yr));
+}
+
+// Forward: edge m's three outputs from u (slot s at acc[s / 2][2 (s % 2)], +1 imaginary), stored.
+__device__ __forceinline__ void f2_forward_outputs(const floatx4 (&acc)[7], const floatx4& zw,
+                                                   __amdgpu_buffer_rsrc_t out_r, int row, int q) {
+  const F2Powers f = f2_powers(zw);
+#define GM_U(s) acc[(s) >> 1][2 * ((s)&1)], acc[(s) >> 1][2 * ((s)&1) + 1]
+  float tr, ti, vr, vi;
+  // output 0: Re(u0) + Re(p (u1 + p u2))
+  cmac(f.pr, f.pi, GM_U(2), GM_U(1), tr, ti);
+  bstore1(fmaf(f.pr, tr, fmaf(-f.pi, ti, acc[0][0])), out_r, (row + q) * 4);
+  // output 1: z (u3 + p (u5 + p u7)) + w u4 + conj(z) w^2 u6
+  const float zr = zw[0], zi = zw[1], wr = zw[2], wi = zw[3];
+  cmac(f.pr, f.pi, GM_U(7), GM_U(5), tr, ti);
+  cmac(f.pr, f.pi, tr, ti, GM_U(3), tr, ti);
+  vr = 0.f;
+  vi = 0.f;
+  cmac(f.cr, f.ci, GM_U(6), vr, vi, vr, vi);
+  cmac(wr, wi, GM_U(4), vr, vi, vr, vi);
+  cmac(zr, zi, tr, ti, vr, vi, vr, vi);
+  bstore2(vr, vi, out_r, (row + 4 + 2 * q) * 4);
+  // output 2: z^2 (u8 + p (u10 + p u12)) + z w u9 + w^2 u11
+  cmac(f.pr, f.pi, GM_U(12), GM_U(10), tr, ti);
+  cmac(f.pr, f.pi, tr, ti, GM_U(8), tr, ti);
+  vr = 0.f;
+  vi = 0.f;
+  cmac(f.w2r, f.w2i, GM_U(11), vr, vi, vr, vi);
+  cmac(f.zwr, f.zwi, GM_U(9), vr, vi, vr, vi);
+  cmac(f.z2r, f.z2i, tr, ti, vr, vi, vr, vi);
+  bstore2(vr, vi, out_r, (row + 12 + 2 * q) * 4);
+#undef GM_U
+}
+
+// Backward: W = conj(F) (w G) per slot for edge m, G_k = (gr[k], gi[k]) the
+// weighted gradient of output k (gi[0] unused: output 0 takes the real part).
+__device__ __forceinline__ void f2_backward_weights(const floatx4& zw, const float (&gr)[3], const float (&gi)[3],
+                                                    float (&wv)[7][4]) {
+  const F2Powers f = f2_powers(zw);
+  const float zr = zw[0], zi = zw[1], wr = zw[2], wi = zw[3];
+#define GM_W(s) wv[(s) >> 1][2 * ((s)&1)], wv[(s) >> 1][2 * ((s)&1) + 1]
+  // output 0: 1, p, p^2 applied to a real gradient
+  wv[0][0] = gr[0];
+  wv[0][1] = 0.f;
+  wv[0][2] = f.pr * gr[0];
+  wv[0][3] = -(f.pi * gr[0]);
+  cjmul(f.pr, f.pi, wv[0][2], wv[0][3], GM_W(2));
+  // output 1: z, w, z p, conj(z) w^2, z p^2
+  cjmul(zr, zi, gr[1], gi[1], GM_W(3));
+  cjmul(f.pr, f.pi, wv[1][2], wv[1][3], GM_W(5));
+  cjmul(f.pr, f.pi, wv[2][2], wv[2][3], GM_W(7));
+  cjmul(wr, wi, gr[1], gi[1], GM_W(4));
+  cjmul(f.cr, f.ci, gr[1], gi[1], GM_W(6));
+  // output 2: z^2, z w, z^2 p, w^2, z^2 p^2
+  cjmul(f.z2r, f.z2i, gr[2], gi[2], GM_W(8));
+  cjmul(f.pr, f.pi, wv[4][0], wv[4][1], GM_W(10));
+  cjmul(f.pr, f.pi, wv[5][0], wv[5][1], GM_W(12));
+  cjmul(f.zwr, f.zwi, gr[2], gi[2], GM_W(9));
+  cjmul(f.w2r, f.w2i, gr[2], gi[2], GM_W(11));
+  wv[6][2] = 0.f;  // slot 13 is empty
+  wv[6][3] = 0.f;
+#undef GM_W
+}
+
 // Z(j) into LDS in slot-column order, Zs[t * ZS + sc] for t < 17, zero in the
-// padding columns: per mix run, lane c reads column c's 17 mixes (17 loads in
-// flight, each row coalesced across the lanes) and writes them to its slot
-// column.
-template <int ZS>
-__device__ __forceinline__ void stage_z_slots(const FactArgs<float>& a, int64_t j, float* Zs, const uint8_t* colslot,
-                                              int lane) {
-  for (int i = lane; i < 17 * ZS / 4; i += kWave) reinterpret_cast<floatx4*>(Zs)[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  wave_sync();
-  for (int r = 0; r < a.n_seg; ++r) {
-    const ZSeg<float>& g = a.seg[r];
-    // the node's 17 mix rows of this run through one buffer: row t at byte t * ts * 4 (a scalar offset)
-    const int ts = g.t_stride;
-    const auto zr = span(g.z + j * g.node_stride, ((int64_t)16 * ts + g.width) * 4);
-    for (int c = lane; c < g.width; c += kWave) {
-      const int sc = colslot[g.c0 + c];
-      float v[17];
+// padding columns, in two steps so that a kernel can put its first tiles'
+// loads into the same memory round trip.  z_issue: when every run is at most
+// one wave wide, lane c requests column c of every run (all 17 rows of all
+// runs in flight together, each row coalesced across the lanes).  z_commit:
+// the padding cleared and the values written to their slot columns; wider
+// runs (and every run when Batch is false) are staged there run by run.
+struct ZStage {
+  float v[GM_FACT_MAX_SEG][17];
+  bool narrow;
+};
+
+template <bool Batch>
+__device__ __forceinline__ void z_issue(const FactArgs<float>& a, int64_t j, int lane, ZStage& st) {
+  st.narrow = Batch;
+  if (!Batch) return;  // runs staged one by one: fewer registers held
+  for (int r = 0; r < a.n_seg; ++r) st.narrow = st.narrow && a.seg[r].width <= kWave;
+  if (!st.narrow) return;
+#pragma unroll
+  for (int r = 0; r < GM_FACT_MAX_SEG; ++r) {
+    if (r < a.n_seg && lane < a.seg[r].width) {
+      const ZSeg<float>& g = a.seg[r];
+      // the node's 17 mix rows of this run through one buffer: row t at byte t * ts * 4 (a scalar offset)
+      const int ts = g.t_stride;
+      const auto zr = span(g.z + j * g.node_stride, ((int64_t)16 * ts + g.width) * 4);
 #pragma unroll
       for (int t = 0; t < 17; ++t)
-        v[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(zr, c * 4, t * ts * 4, 0));
+        st.v[r][t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(zr, lane * 4, t * ts * 4, 0));
+    }
+  }
+}
+
+template <int ZS>
+__device__ __forceinline__ void z_commit(const FactArgs<float>& a, int64_t j, float* Zs, const uint8_t* colslot,
+                                         int lane, const ZStage& st) {
+  for (int i = lane; i < 17 * ZS / 4; i += kWave) reinterpret_cast<floatx4*>(Zs)[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  wave_sync();
+  if (st.narrow) {
 #pragma unroll
-      for (int t = 0; t < 17; ++t) Zs[t * ZS + sc] = v[t];
+    for (int r = 0; r < GM_FACT_MAX_SEG; ++r) {
+      if (r < a.n_seg && lane < a.seg[r].width) {
+        const int sc = colslot[a.seg[r].c0 + lane];
+#pragma unroll
+        for (int t = 0; t < 17; ++t) Zs[t * ZS + sc] = st.v[r][t];
+      }
+    }
+  } else {
+    for (int r = 0; r < a.n_seg; ++r) {
+      const ZSeg<float>& g = a.seg[r];
+      const int ts = g.t_stride;
+      const auto zr = span(g.z + j * g.node_stride, ((int64_t)16 * ts + g.width) * 4);
+      for (int c = lane; c < g.width; c += kWave) {
+        const int sc = colslot[g.c0 + c];
+        float v[17];
+#pragma unroll
+        for (int t = 0; t < 17; ++t)
+          v[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(zr, c * 4, t * ts * 4, 0));
+#pragma unroll
+        for (int t = 0; t < 17; ++t) Zs[t * ZS + sc] = v[t];
+      }
     }
   }
   wave_sync();
@@ -1513,6 +1660,10 @@ __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const Fwd
   for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], h[s], acc[nt]);
+  if constexpr (kHorner<P>) {
+    f2_forward_outputs(acc, cur.ph.ph, out_r, (tb + m) * d_out, q);
+    return;
+  }
   Powers<P> pw;
   if constexpr (P::kStatic) {
     pw = powers<P>(cur.ph.ph);
@@ -1564,9 +1715,22 @@ factored_forward_lanes(FactArgs<float> a) {
   const int64_t j = a.group_source[gi];
   const int64_t g0 = a.group_ptr[gi];
   const int ng = (int)(a.group_ptr[gi + 1] - g0);
+  constexpr bool fused = FUSED;
+  const auto h_r = span(fused ? nullptr : a.h + g0 * 16, fused ? 0 : (int64_t)ng * 64);
+  const auto ph_r = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
+                               : span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
+  const auto rho_r = span(a.rho_g + g0, (int64_t)ng * 4);
+  const auto out_r = span(a.out + g0 * d_out, (int64_t)ng * d_out * 4);
+  // two tiles in flight: each buffer is refilled right after its tile's
+  // stores, so waiting for a tile never waits for the previous tile's stores.
+  // The first two are requested with the node's mixes (one round trip).
+  FwdTile<P> ta = load_fwd<P>(h_r, ph_r, rho_r, 0, m, q, fused);
+  FwdTile<P> tbf = load_fwd<P>(h_r, ph_r, rho_r, kMT, m, q, fused);
   stage_colslot(a, colslot, lane);
+  ZStage zst;
+  z_issue<P::kStatic>(a, j, lane, zst);
   wave_sync();
-  stage_z_slots<ZS>(a, j, Zs, colslot, lane);
+  z_commit<ZS>(a, j, Zs, colslot, lane, zst);
   float za[NT][4];
   floatx4 z0[NT];
 #pragma unroll
@@ -1575,18 +1739,8 @@ factored_forward_lanes(FactArgs<float> a) {
     for (int s = 0; s < 4; ++s) za[nt][s] = Zs[(1 + 4 * q + s) * ZS + 16 * nt + m];
     z0[nt] = *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q);
   }
-  constexpr bool fused = FUSED;
   TrunkLane tl{};
   if (fused) tl = trunk_lane(a, m, q);
-  const auto h_r = span(fused ? nullptr : a.h + g0 * 16, fused ? 0 : (int64_t)ng * 64);
-  const auto ph_r = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
-                               : span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
-  const auto rho_r = span(a.rho_g + g0, (int64_t)ng * 4);
-  const auto out_r = span(a.out + g0 * d_out, (int64_t)ng * d_out * 4);
-  // two tiles in flight: each buffer is refilled right after its tile's
-  // stores, so waiting for a tile never waits for the previous tile's stores
-  FwdTile<P> ta = load_fwd<P>(h_r, ph_r, rho_r, 0, m, q, fused);
-  FwdTile<P> tbf = load_fwd<P>(h_r, ph_r, rho_r, kMT, m, q, fused);
   for (int tb = 0;;) {
     forward_tile<NT, P>(a, ta, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
     ta = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
@@ -1686,7 +1840,18 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
   }
   float wv[NT][4];
   float dwp = 0.f;  // this lane's share of dweights(edge m)
-  if constexpr (P::kStatic) {
+  if constexpr (kHorner<P>) {
+    // the weighted gradient values w G of the three outputs (first slots 0, 3, 8)
+    float gr[3], gi[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int s = k == 0 ? 0 : (k == 1 ? 3 : 8);
+      dwp += outs.gr[s] * outs.rr[s] + outs.gi[s] * outs.ri[s];
+      gr[k] = cur.w * outs.gr[s];
+      gi[k] = cur.w * outs.gi[s];
+    }
+    f2_backward_weights(cur.ph.ph, gr, gi, wv);
+  } else if constexpr (P::kStatic) {
     const Powers<P> pw = powers<P>(cur.ph.ph);
     // the edge's weighted gradient values w G, once per output group
     float wgr[2 * NT], wgi[2 * NT];
@@ -1795,24 +1960,7 @@ factored_backward_lanes(FactArgs<float> a) {
   const int64_t j = a.group_source[gi];
   const int64_t g0 = a.group_ptr[gi];
   const int ng = (int)(a.group_ptr[gi + 1] - g0);
-  stage_colslot(a, colslot, lane);
-  wave_sync();
-  stage_z_slots<ZS>(a, j, Sh, colslot, lane);
-  // Z_t(j) for t = 1 + m at the lane's slot columns 16 nt + 4 q + r
-  floatx4 zb[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) zb[nt] = *reinterpret_cast<const floatx4*>(Sh + (1 + m) * ZS + 16 * nt + 4 * q);
-  wave_sync();
-  floatx4 dz[NT];
-  float dz0[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    dz[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    dz0[nt] = 0.f;
-  }
   constexpr bool fused = FUSED;
-  TrunkLane tl{};
-  if (fused) tl = trunk_lane(a, m, q);
   BwdSpans sp;
   sp.h = span(fused ? nullptr : a.h + g0 * 16, fused ? 0 : (int64_t)ng * 64);
   sp.ph = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
@@ -1827,15 +1975,41 @@ factored_backward_lanes(FactArgs<float> a) {
   // tile's stores); with static slots the targets run three tiles ahead and
   // the targets' gradient values and row values two, so no load is waited
   // for within the tile after the one that issued it.
+  // The first tiles' streams and targets are requested with the node's mixes
+  // (one round trip), then the targets' gradient values.
   BwdTile<P> ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, 0, m, q, fused);
   BwdTile<P> tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, kMT, m, q, fused);
+  int64_t t0 = 0, t1 = 0;
+  if constexpr (P::kStatic) {
+    t0 = bload_i64(sp.t, m * 8);
+    t1 = bload_i64(sp.t, (kMT + m) * 8);
+  }
+  stage_colslot(a, colslot, lane);
+  ZStage zst;
+  z_issue<P::kStatic>(a, j, lane, zst);
   OutVals<P::kStatic ? NT : 1> oa, ob;
   int64_t tn = 0;  // static slots: the targets of the tile two ahead of the current one
   if constexpr (P::kStatic) {
-    load_outs<NT, P>(oa, a.g, bload_i64(sp.t, m * 8), sp.rows, m * d_out, q);
-    load_outs<NT, P>(ob, a.g, bload_i64(sp.t, (kMT + m) * 8), sp.rows, (kMT + m) * d_out, q);
+    load_outs<NT, P>(oa, a.g, t0, sp.rows, m * d_out, q);
+    load_outs<NT, P>(ob, a.g, t1, sp.rows, (kMT + m) * d_out, q);
     tn = bload_i64(sp.t, (2 * kMT + m) * 8);
   }
+  wave_sync();
+  z_commit<ZS>(a, j, Sh, colslot, lane, zst);
+  // Z_t(j) for t = 1 + m at the lane's slot columns 16 nt + 4 q + r
+  floatx4 zb[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) zb[nt] = *reinterpret_cast<const floatx4*>(Sh + (1 + m) * ZS + 16 * nt + 4 * q);
+  wave_sync();
+  floatx4 dz[NT];
+  float dz0[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    dz[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    dz0[nt] = 0.f;
+  }
+  TrunkLane tl{};
+  if (fused) tl = trunk_lane(a, m, q);
   for (int tb = 0;;) {
     backward_tile<NT, P>(a, ta, oa, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl, fused);
     if constexpr (P::kStatic) {
