@@ -322,15 +322,24 @@ __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a
   const float* base = a.rows + (int64_t)hh * a.n_rows * a.d_out + 4 * c4;
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
   floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+  // the next batch's row indices are requested behind this batch's rows, so each
+  // batch waits for one round trip rather than an index load and then the rows
+  int64_t r[kAggStep];
+#pragma unroll
+  for (int u = 0; u < kAggStep; ++u) r[u] = e0 + u < e1 ? a.inv[e0 + u] : 0;
   for (int64_t e = e0; e < e1; e += kAggStep) {
     float w[kAggStep];
     floatx4 v[kAggStep];
 #pragma unroll
     for (int u = 0; u < kAggStep; ++u) {
       const bool in = live && e + u < e1;
-      const int64_t r = e + u < e1 ? a.inv[e + u] : 0;
       w[u] = in ? a.alpha[(e + u) * a.H + hh] : 0.f;
-      v[u] = in ? *reinterpret_cast<const floatx4*>(base + r * a.d_out) : floatx4{0.f, 0.f, 0.f, 0.f};
+      v[u] = in ? *reinterpret_cast<const floatx4*>(base + r[u] * a.d_out) : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < kAggStep; ++u) {
+      const int64_t n = e + kAggStep + u;
+      r[u] = n < e1 ? a.inv[n] : 0;
     }
 #pragma unroll
     for (int u = 0; u < kAggStep; ++u) s += w[u] * v[u];
