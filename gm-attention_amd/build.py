@@ -36,9 +36,13 @@ FLAGS = [
 ]
 
 
-#: Per-source extra flags.  The factored kernels keep their MFMA accumulators
-#: in VGPRs (the VALU reads every accumulator, so AGPRs would only add copies).
-EXTRA = {"factored.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+#: Per-source extra flags.  The factored and trunk kernels keep their MFMA
+#: accumulators in VGPRs: the VALU reads every accumulator (the factored slots,
+#: the trunk's SiLU and partial rows), so AGPRs would only add copies and
+#: registers (the trunk backward: 184 -> 151 VGPRs, three waves a SIMD).  The
+#: depthwise walk is left to the default, which measured faster there.
+_VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+EXTRA = {"factored.hip": _VGPR_MFMA, "trunk.hip": _VGPR_MFMA}
 
 
 def _compile(source: Path, verbose: bool) -> Path:
