@@ -117,10 +117,13 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
     return fast_exp(-0.5f * z * z);
   };
   // dh of head h for this lane's edge c of a tile, features 4q..4q+3 (zero past the end)
+  const int lane_off = c * T + 4 * q;  // the lane's 16 bytes within a tile's 1 KB of one head
   auto load_dh = [&](int64_t e0, int h) {
-    return (h < a.H && e0 + c < a.n_edges)
-               ? *reinterpret_cast<const float4*>(a.dh + ((int64_t)h * a.n_edges + e0 + c) * T + 4 * q)
-               : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float* tile_dh = a.dh + ((int64_t)h * a.n_edges + e0) * T;  // uniform: a scalar base
+    if (e0 + 16 <= a.n_edges)  // every tile but the last: no per-lane test
+      return *reinterpret_cast<const float4*>(tile_dh + lane_off);
+    return e0 + c < a.n_edges ? *reinterpret_cast<const float4*>(tile_dh + lane_off)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
   };
   // rho of a tile: edge c (the B1 operand) and edges 4q..4q+3 (the A2 operands)
   auto load_rho = [&](int64_t e0, float& rc, float* r4) {
@@ -143,7 +146,7 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
   load_rho(wave * 16, rc, r4);
   float4 g[kTrunkMaxHeads];
 #pragma unroll
-  for (int h = 0; h < kTrunkMaxHeads; ++h) g[h] = load_dh(wave * 16, h);
+  for (int h = 0; h < kTrunkMaxHeads; ++h) g[h] = h < a.H ? load_dh(wave * 16, h) : make_float4(0.f, 0.f, 0.f, 0.f);
   for (int64_t tile = wave; tile < n_tiles; tile += n_waves) {
     const int64_t e_next = (tile + n_waves) * 16;
     float rc_next, r4_next[4];
