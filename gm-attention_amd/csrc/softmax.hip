@@ -78,7 +78,65 @@ __device__ __forceinline__ T chunk_dot_pair(const T* q4, const Quad<T>& k, int n
   return acc;
 }
 
-template <typename T, int NCH>
+// Chunk c's frequency: compile-time when the plan's orders are packed in ORD
+// (four bits a chunk, ORD != 0), else the descriptor's.
+template <uint32_t ORD>
+__device__ __forceinline__ int chunk_order(const Chunks& C, int c) {
+  if constexpr (ORD != 0)
+    return (int)((ORD >> (4 * c)) & 15u);
+  else
+    return C.order[c];
+}
+
+constexpr int max_order_of(uint32_t ord) {
+  int m = 0;
+  for (int c = 0; c < 8; ++c)
+    if ((int)((ord >> (4 * c)) & 15u) > m) m = (int)((ord >> (4 * c)) & 15u);
+  return m;
+}
+
+__device__ __forceinline__ void ld_pair(const float* p, float& x, float& y) {
+  const float2 v = *reinterpret_cast<const float2*>(p);
+  x = v.x;
+  y = v.y;
+}
+__device__ __forceinline__ void ld_pair(const double* p, double& x, double& y) {
+  const double2 v = *reinterpret_cast<const double2*>(p);
+  x = v.x;
+  y = v.y;
+}
+
+// The transport (cos, sin) each chunk of one edge reads.  With compile-time
+// orders every order's pair is one 8-byte (16-byte) load and order 0 loads
+// nothing; otherwise one pair per chunk from the descriptor.
+template <typename T, int NCH, uint32_t ORD>
+__device__ __forceinline__ void transport_pairs(const Chunks& C, const T* tr, T (&tc)[NCH], T (&ts)[NCH]) {
+  if constexpr (ORD != 0) {
+    constexpr int MO = max_order_of(ORD);
+    T cs[MO + 1], sn[MO + 1];
+    cs[0] = T(1);
+    sn[0] = T(0);
+#pragma unroll
+    for (int o = 1; o <= MO; ++o) ld_pair(tr + 2 * o, cs[o], sn[o]);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      tc[c] = cs[chunk_order<ORD>(C, c)];
+      ts[c] = sn[chunk_order<ORD>(C, c)];
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      tc[c] = tr[2 * C.order[c]];
+      ts[c] = tr[2 * C.order[c] + 1];
+    }
+  }
+}
+
+// The chunk orders of heads with four copies of frequencies 0, 1 and 2 (one
+// scalar chunk, two chunks each of frequencies 1 and 2), compiled in.
+constexpr uint32_t kOrders012 = 0x22110u;
+
+template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x & 63;
@@ -113,11 +171,8 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
       const T* kj = a.k + ju[u] * a.D;
       const T* tr = a.transport + eu[u] * a.orders * 2;
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        kv[u][c] = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
-        tc[u][c] = tr[2 * a.C.order[c]];
-        tsn[u][c] = tr[2 * a.C.order[c] + 1];
-      }
+      for (int c = 0; c < NCH; ++c) kv[u][c] = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
+      transport_pairs<T, NCH, ORD>(a.C, tr, tc[u], tsn[u]);
       bias[u] = a.bias[eu[u]];
       in[u] = a.inside[eu[u]];
     }
@@ -126,7 +181,8 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
       if (e + u * S >= e1) break;
       T acc = T(0);
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) acc += chunk_dot_pair(&q[4 * c], kv[u][c], a.C.order[c], tc[u][c], tsn[u][c]);
+      for (int c = 0; c < NCH; ++c)
+        acc += chunk_dot_pair(&q[4 * c], kv[u][c], chunk_order<ORD>(a.C, c), tc[u][c], tsn[u][c]);
       T lw = a.scale * acc + bias[u];
       if (!in[u]) lw = neg_inf<T>();  // outside the window: excluded from the max and the sum
       a.alpha[eu[u] * H + h] = lw;
@@ -143,7 +199,7 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   }
 }
 
-template <typename T, int NCH>
+template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a) {
   const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x & 63;
@@ -177,11 +233,8 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
       const T* kj = a.k + ju[u] * a.D;
       const T* tr = a.transport + eu[u] * a.orders * 2;
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        kv[u][c] = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
-        tc[u][c] = tr[2 * a.C.order[c]];
-        tsn[u][c] = tr[2 * a.C.order[c] + 1];
-      }
+      for (int c = 0; c < NCH; ++c) kv[u][c] = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
+      transport_pairs<T, NCH, ORD>(a.C, tr, tc[u], tsn[u]);
     }
 #pragma unroll
     for (int u = 0; u < kSmStep; ++u) {
@@ -191,7 +244,7 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         const Quad<T>& k = kv[u][c];
-        if (a.C.order[c] == 0) {
+        if (chunk_order<ORD>(a.C, c) == 0) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * k.v[v];
         } else {
@@ -213,7 +266,7 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
   }
 }
 
-template <typename T, int NCH>
+template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a) {
   const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x & 63;
@@ -243,11 +296,8 @@ __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a)
       const T* qt = a.q + tu[u] * a.D;
       const T* tr = a.transport + eu[u] * a.orders * 2;
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        qv[u][c] = ld4(qt + a.C.base[c] + h * a.C.stride[c]);
-        tc[u][c] = tr[2 * a.C.order[c]];
-        tsn[u][c] = tr[2 * a.C.order[c] + 1];
-      }
+      for (int c = 0; c < NCH; ++c) qv[u][c] = ld4(qt + a.C.base[c] + h * a.C.stride[c]);
+      transport_pairs<T, NCH, ORD>(a.C, tr, tc[u], tsn[u]);
     }
 #pragma unroll
     for (int u = 0; u < kSmStep; ++u) {
@@ -256,7 +306,7 @@ __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a)
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         const Quad<T>& qq = qv[u][c];
-        if (a.C.order[c] == 0) {
+        if (chunk_order<ORD>(a.C, c) == 0) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * qq.v[v];
         } else {
@@ -425,24 +475,36 @@ __global__ __launch_bounds__(256) void softmax_backward_source_generic(SmArgs<T>
 
 enum class Kind { Forward, BackwardTarget, BackwardSource };
 
-template <typename T, int NCH>
+template <typename T, int NCH, uint32_t ORD = 0>
 void launch_fast_n(Kind kind, const SmArgs<T>& a, dim3 grid, hipStream_t stream) {
   switch (kind) {
     case Kind::Forward:
-      hipLaunchKernelGGL((softmax_forward_fast<T, NCH>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((softmax_forward_fast<T, NCH, ORD>), grid, dim3(256), 0, stream, a);
       break;
     case Kind::BackwardTarget:
-      hipLaunchKernelGGL((softmax_backward_target_fast<T, NCH>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((softmax_backward_target_fast<T, NCH, ORD>), grid, dim3(256), 0, stream, a);
       break;
     case Kind::BackwardSource:
-      hipLaunchKernelGGL((softmax_backward_source_fast<T, NCH>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((softmax_backward_source_fast<T, NCH, ORD>), grid, dim3(256), 0, stream, a);
       break;
   }
+}
+
+// Whether the descriptor's chunk orders are the packed word's.
+inline bool orders_are(const Chunks& C, int n, uint32_t ord) {
+  if (C.count != n) return false;
+  for (int c = 0; c < n; ++c)
+    if (C.order[c] != (int)((ord >> (4 * c)) & 15u)) return false;
+  return true;
 }
 
 template <typename T>
 void launch(Kind kind, bool fast, const SmArgs<T>& a, hipStream_t stream) {
   const dim3 grid((unsigned)blocks_for(a.n_nodes));
+  if (fast && orders_are(a.C, 5, kOrders012) && a.orders > max_order_of(kOrders012)) {
+    launch_fast_n<T, 5, kOrders012>(kind, a, grid, stream);
+    return;
+  }
   if (fast) {
     switch (a.C.count) {
 #define GM_CASE(n) \
