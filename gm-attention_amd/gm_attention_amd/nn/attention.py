@@ -39,7 +39,7 @@ from torch import Tensor, nn
 from gm_attention_amd.discretization.discretization import SphericalDiscretization
 from gm_attention_amd.nn import fused_attention, fused_factored, kernels, radial
 from gm_attention_amd.nn.kernels import SO2SteerableKernel
-from gm_attention_amd.nn.linear import SO2Linear, apply_linear
+from gm_attention_amd.nn.linear import FlatLinear, SO2Linear, apply_linear, block_matrix, flat_bias, weights_matrix
 from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
 
 REMATERIALIZE_CHUNKS = os.environ.get("GM_CHUNK_REMATERIALIZE", "1") != "0"
@@ -190,6 +190,9 @@ class SO2MHSA(nn.Module):
         edges = _resolve_edges(edges, self.cutoff)
         if self.batched:
             _validate_node_field(x, self.field_type_in, edges)
+            rows = _attend_batched_flat(self, x, edges)
+            if rows is not None:
+                return SO2FeatureField.from_flat(self.field_type_in, rows)
             return self.output_projection(SO2FeatureField(self.field_type_in, _attend_batched(self, x, edges)))
         fused = _concatenate_heads([head(x, edges) for head in self.heads], self.field_type_in)
         return self.output_projection(fused)
@@ -205,6 +208,65 @@ def _stacked_projection(linears: Sequence[SO2Linear], x: SO2FeatureField) -> SO2
     weights = {str(f): torch.cat([lin.weight[str(f)] for lin in linears], dim=0) for f in x.field_type.frequencies}
     bias = torch.cat([lin.bias for lin in linears]) if linears[0].has_bias else None
     return apply_linear(x.field_type, x.field_type.frequencies, weights, bias, x)
+
+
+def _stacked_flat(linears: Sequence[SO2Linear], field_type_out: SO2FieldType, rows: Tensor) -> Tensor:
+    """``_stacked_projection`` on flat rows: the heads' stacked intertwiner as one
+    ``(D_in, D_out)`` block matrix, one GEMM onto the direct sum's flat layout."""
+    lin = linears[0]
+    weights = {str(f): torch.cat([h.weight[str(f)] for h in linears], dim=0) for f in lin.common_frequencies}
+    bias = torch.cat([h.bias for h in linears]) if lin.has_bias else None
+    m = weights_matrix(lin.field_type_in, field_type_out, lin.common_frequencies, weights)
+    return FlatLinear.apply(rows, m, flat_bias(bias, field_type_out))
+
+
+def _heads_permutation(mhsa: SO2MHSA, device: torch.device) -> Tensor:
+    """For column ``head * d + c`` of the heads' outputs ``(N, H, d)`` (each in the
+    per-head flat layout), its column in the direct sum's flat layout."""
+    key = ("_heads_permutation", str(device))
+    perm = mhsa.__dict__.get(key)
+    if perm is None:
+        attn, full = mhsa.field_type_attn, mhsa.field_type_in
+        sa, sf = attn.slices(), full.slices()
+        cols = []
+        for head in range(mhsa.num_heads):
+            for f, a in attn.items():
+                dim = 1 if f == 0 else 2
+                for c in range(sa[f].stop - sa[f].start):
+                    cols.append(sf[f].start + (head * a + c // dim) * dim + c % dim)
+        perm = torch.tensor(cols, dtype=torch.long, device=device)
+        mhsa.__dict__[key] = perm
+    return perm
+
+
+def _attend_batched_flat(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> Tensor | None:
+    """The batched layer on flat rows when the fused softmax and the fused
+    factored heads serve it (else None): the stacked query and key
+    projections as one GEMM each, and the output projection reading the heads'
+    ``(N, H, d)`` outputs directly through its block matrix with the rows put
+    in the heads' column order -- no per-frequency splits or concatenations."""
+    heads = [cast(SO2Attention, h) for h in mhsa.heads]
+    values = [cast(SO2SteerableKernel, head.value) for head in heads]
+    if (not fused_attention.softmax_enabled(mhsa, x, edges) or not kernels.factored_enabled()
+            or not fused_factored.enabled(values[0], x, edges)):
+        return None
+    rows = x.to_flat()
+    if rows.ndim != 2:
+        return None
+    with torch.profiler.record_function("gm::attention/attend"):
+        queries = _stacked_flat([h.query for h in heads], mhsa.field_type_in, rows)
+        keys = _stacked_flat([h.key for h in heads], mhsa.field_type_in, rows)
+        alpha = fused_attention.softmax(mhsa, queries, keys, edges)  # (n_edges, n_heads)
+        groups = fused_factored.groups_for(edges, edges.source_index)
+        if radial.eligible(values, x.dtype, x.device):
+            h, trunk = None, functools.partial(radial.trunk_hidden_heads, values)
+        else:
+            h, trunk = torch.stack([k._trunk_hidden(edges.distances) for k in values]), None
+        out = fused_factored.forward_aggregated_heads(values, x, edges, alpha, h, groups, trunk)  # (N, H, d)
+    proj = mhsa.output_projection
+    m = block_matrix(proj).index_select(0, _heads_permutation(mhsa, rows.device))
+    return FlatLinear.apply(out.reshape(out.shape[0], -1), m,
+                            flat_bias(proj.bias if proj.has_bias else None, proj.field_type_out))
 
 
 def _attend_batched(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> dict[int, Tensor]:

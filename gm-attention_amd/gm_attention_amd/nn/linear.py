@@ -100,22 +100,31 @@ class FlatLinear(torch.autograd.Function):
 
 def block_matrix(lin: "SO2Linear") -> Tensor:
     """The layer as one ``(D_in, D_out)`` matrix acting on flat rows (zero off its frequency blocks)."""
-    fin, fout = lin.field_type_in, lin.field_type_out
+    return weights_matrix(lin.field_type_in, lin.field_type_out, lin.common_frequencies, lin.weight)
+
+
+def weights_matrix(fin: SO2FieldType, fout: SO2FieldType, common, weights) -> Tensor:
+    """Per-frequency intertwiner weights (``(b, a)`` real at 0, ``(b, a, 2)``
+    complex above) as one ``(D_in, D_out)`` matrix on flat rows."""
     sin, sout = fin.slices(), fout.slices()
-    ref = next(iter(lin.weight.values()))
+    ref = next(iter(weights.values()))
     m = ref.new_zeros(fin.dimension, fout.dimension)
-    for f in lin.common_frequencies:
-        w = lin.weight[str(f)]
+    for f in common:
+        w = weights[str(f)]
         m[sin[f], sout[f]] = w.T if f == 0 else complex_as_real(w)
     return m
 
 
+def flat_bias(bias: Tensor | None, fout: SO2FieldType) -> Tensor | None:
+    """A frequency-0 bias spread over the flat columns (zero elsewhere)."""
+    if bias is None:
+        return None
+    return torch.cat([bias, bias.new_zeros(fout.dimension - fout.multiplicity(0))])
+
+
 def flat_forward(lin: "SO2Linear", flat: Tensor) -> Tensor:
     """``lin`` on flat rows ``(N, D_in)`` -> ``(N, D_out)``."""
-    bias = None
-    if lin.has_bias:
-        b0 = lin.field_type_out.multiplicity(0)
-        bias = torch.cat([lin.bias, lin.bias.new_zeros(lin.field_type_out.dimension - b0)])
+    bias = flat_bias(lin.bias if lin.has_bias else None, lin.field_type_out)
     return FlatLinear.apply(flat, block_matrix(lin), bias)
 
 

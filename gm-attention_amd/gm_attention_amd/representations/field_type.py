@@ -102,7 +102,7 @@ class SO2FieldType:
 class SO2FeatureField:
     """Per-frequency coefficients: ``(*batch, a_0)`` at 0, ``(*batch, a_n, 2)`` above."""
 
-    __slots__ = ("coefficients", "field_type")
+    __slots__ = ("coefficients", "field_type", "_flat")
 
     def __init__(self, field_type: SO2FieldType, coefficients: Mapping[int, Tensor]) -> None:
         if set(coefficients) != set(field_type.frequencies):
@@ -120,6 +120,7 @@ class SO2FeatureField:
                 )
         self.field_type = field_type
         self.coefficients = dict(coefficients)
+        self._flat = None
 
     @classmethod
     def from_flat(cls, field_type: SO2FieldType, flat: Tensor) -> SO2FeatureField:
@@ -129,9 +130,18 @@ class SO2FeatureField:
         for frequency, multiplicity in field_type.items():
             block = flat[..., field_type.slices()[frequency]]
             out[frequency] = block if frequency == 0 else block.unflatten(-1, (multiplicity, 2))
-        return cls(field_type, out)
+        field = cls(field_type, out)
+        field._flat = (flat, out)  # to_flat hands the rows back while the coefficients are these views
+        return field
 
     def to_flat(self) -> Tensor:
+        """The flat rows (frequency 0, then each frequency's ``(a_n, 2)`` pairs):
+        the tensor a field was made from by ``from_flat`` while its coefficients
+        are still the views of it, otherwise a new concatenation."""
+        if self._flat is not None:
+            flat, views = self._flat
+            if all(self.coefficients[f] is v for f, v in views.items()):
+                return flat
         blocks = [self.coefficients[f] if f == 0 else self.coefficients[f].flatten(-2) for f in self.field_type.frequencies]
         return torch.cat(blocks, dim=-1)
 
