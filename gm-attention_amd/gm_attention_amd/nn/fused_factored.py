@@ -412,11 +412,39 @@ def _untile(kernel: Any, parts: list[Tensor], device: torch.device) -> Tensor:
 def _tiled(kernel: Any, i: "Inputs", launch) -> Tensor:
     parts = []
     for index, t in enumerate(tiles(kernel)):
-        desc, zc_cols, zr_cols = _tile_tensors(kernel, t, index, i.h.device)
-        zc = i.zc.index_select(2, zc_cols) if zc_cols.numel() else i.zc[:, :, :0]
-        zr = i.zr.index_select(2, zr_cols) if zr_cols.numel() else i.zr[:, :, :0]
-        parts.append(launch(zc.contiguous(), zr.contiguous(), desc, t.d_out, t.max_bm))
+        desc, _, _ = _tile_tensors(kernel, t, index, i.h.device)
+        parts.append(launch(_take_columns(i.zc, t.zc_cols), _take_columns(i.zr, t.zr_cols), desc, t.d_out, t.max_bm))
     return _untile(kernel, parts, i.h.device)
+
+
+def _ranges(cols: tuple[int, ...]) -> list[tuple[int, int]]:
+    """Ascending columns as maximal contiguous ``[start, stop)`` ranges."""
+    out: list[tuple[int, int]] = []
+    for c in cols:
+        if out and out[-1][1] == c:
+            out[-1] = (out[-1][0], c + 1)
+        else:
+            out.append((c, c + 1))
+    return out
+
+
+def _take_columns(z: Tensor, cols: tuple[int, ...]) -> Tensor:
+    """``z[:, :, cols]`` contiguous, copied range by range (a tile's columns are
+    a few contiguous ranges: slice copies rather than an indexed gather)."""
+    rs = _ranges(cols)
+    if not rs:
+        return z[:, :, :0].contiguous()
+    if len(rs) == 1:
+        return z[:, :, rs[0][0]:rs[0][1]].contiguous()
+    return torch.cat([z[:, :, lo:hi] for lo, hi in rs], dim=2)
+
+
+def _put_columns(dst: Tensor, cols: tuple[int, ...], src: Tensor) -> None:
+    """``dst[:, :, cols] = src`` range by range."""
+    at = 0
+    for lo, hi in _ranges(cols):
+        dst[:, :, lo:hi].copy_(src[:, :, at:at + hi - lo])
+        at += hi - lo
 
 
 class TiledAggregate(torch.autograd.Function):
@@ -435,9 +463,8 @@ class TiledAggregate(torch.autograd.Function):
         parts, saved = [], []
         with torch.profiler.record_function("gm::kernel/pairs_tiles"):
             for index, t in enumerate(tiles(kernel)):
-                desc, zc_cols, zr_cols = _tile_tensors(kernel, t, index, h.device)
-                zc_t = zc.index_select(2, zc_cols).contiguous() if zc_cols.numel() else zc[:, :, :0].contiguous()
-                zr_t = zr.index_select(2, zr_cols).contiguous() if zr_cols.numel() else zr[:, :, :0].contiguous()
+                desc, _, _ = _tile_tensors(kernel, t, index, h.device)
+                zc_t, zr_t = _take_columns(zc, t.zc_cols), _take_columns(zr, t.zr_cols)
                 r = ext.forward(h, zc_t, zr_t, angular, transport, rho, desc, source, order, group_ptr, group_source,
                                 t.d_out, t.max_bm)
                 saved += [r, zc_t, zr_t]  # the tiles' mixes together hold what zc and zr hold
@@ -464,17 +491,15 @@ class TiledAggregate(torch.autograd.Function):
         with torch.profiler.record_function("gm::kernel/pairs_tiles_backward"):
             for index, t in enumerate(tiles(kernel)):
                 r, zc_t, zr_t = per_tile[3 * index:3 * index + 3]
-                desc, zc_cols, zr_cols = _tile_tensors(kernel, t, index, h.device)
+                desc, _, _ = _tile_tensors(kernel, t, index, h.device)
                 cols = _untile_columns(kernel, h.device)[offset:offset + t.d_out]
                 offset += t.d_out
                 g_t = grad_out.index_select(1, cols).contiguous()
                 dh_t, dzc_t, dzr_t, dw_t = ext.backward_aggregated(g_t, target, weights, r, h, zc_t, zr_t, angular,
                                                                    transport, rho, desc, source, order, group_ptr,
                                                                    group_source)
-                if zc_cols.numel():
-                    dzc.index_copy_(2, zc_cols, dzc_t)
-                if zr_cols.numel():
-                    dzr.index_copy_(2, zr_cols, dzr_t)
+                _put_columns(dzc, t.zc_cols, dzc_t)
+                _put_columns(dzr, t.zr_cols, dzr_t)
                 dh = dh_t if dh is None else dh.add_(dh_t)
                 dweights = dw_t if dweights is None else dweights.add_(dw_t)
         return dh, dzc, dzr, dweights, None, None, None, None, None, None, None, None, None, None
