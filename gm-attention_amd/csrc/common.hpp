@@ -38,6 +38,20 @@ __device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
   return x * q + (x < r ? x : r) + (b >> 3);
 }
 
+// The same XCD assignment in chunks of 32 logical blocks dealt round-robin
+// (XCD x runs chunks x, x + 8, ...; the last partial round keeps its order):
+// every XCD then runs work from every latitude band.  Contiguous ranges are
+// even only when each XCD's range holds a pole and an equator alike (B = 4 on
+// eight XCDs); with two samples a range is a quarter of a sample and the
+// polar quarters carry about five times the edges of the equatorial ones.
+__device__ __forceinline__ int64_t xcd_spread_block(int64_t b, int64_t nb) {
+  constexpr int64_t kChunk = 32;
+  const int64_t full = nb / (8 * kChunk) * (8 * kChunk);
+  if (b >= full) return b;
+  const int64_t x = b & 7, i = b >> 3;
+  return ((i / kChunk) * 8 + x) * kChunk + (i % kChunk);
+}
+
 // Four consecutive elements (16 B for float, 32 B for double), aligned.
 template <typename T>
 struct Quad {

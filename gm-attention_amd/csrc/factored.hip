@@ -963,7 +963,7 @@ __global__ __launch_bounds__(64) void factored_forward_grouped(FactArgs<float> a
   for (int i = lane; i <= d_out; i += kWave) optr[i] = a.optr[i];
   for (int i = lane; i < a.optr[d_out]; i += kWave) olist[i] = a.olist[i];
   stage_desc(a, Bd, lane);
-  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
+  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_spread_block(blockIdx.x, gridDim.x);
   if (gi < 0 || gi >= a.n_groups) return;  // a malformed order names no group
   const int64_t j = a.group_source[gi];
   const int64_t g0 = a.group_ptr[gi], g1 = a.group_ptr[gi + 1];
@@ -1046,7 +1046,7 @@ __global__ __launch_bounds__(64) void factored_backward_grouped(FactArgs<float> 
   float* Ht = Wt + kMT * WP;                                       // [kMT][16]
   const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
   stage_desc(a, Bd, lane);
-  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
+  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_spread_block(blockIdx.x, gridDim.x);
   if (gi < 0 || gi >= a.n_groups) return;  // a malformed order names no group
   const int64_t j = a.group_source[gi];
   const int64_t g0 = a.group_ptr[gi], g1 = a.group_ptr[gi + 1];
@@ -1719,7 +1719,7 @@ factored_forward_lanes(FactArgs<float> a) {
   __shared__ __align__(16) uint8_t colslot[128];
   const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
   const int d_out = P::kStatic ? P::kDout : a.d_out;
-  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
+  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_spread_block(blockIdx.x, gridDim.x);
   if (gi < 0 || gi >= a.n_groups) return;  // a malformed order names no group
   const int64_t j = a.group_source[gi];
   const int64_t g0 = a.group_ptr[gi];
@@ -1964,7 +1964,7 @@ factored_backward_lanes(FactArgs<float> a) {
   __shared__ __align__(16) float Hs[kMT * kHsStride];  // the fused trunk's features, edge-major
   const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
   const int d_out = P::kStatic ? P::kDout : a.d_out;
-  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_block(blockIdx.x, gridDim.x);
+  const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_spread_block(blockIdx.x, gridDim.x);
   if (gi < 0 || gi >= a.n_groups) return;  // a malformed order names no group
   const int64_t j = a.group_source[gi];
   const int64_t g0 = a.group_ptr[gi];
