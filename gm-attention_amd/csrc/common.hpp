@@ -52,6 +52,26 @@ __device__ __forceinline__ int64_t xcd_spread_block(int64_t b, int64_t nb) {
   return ((i / kChunk) * 8 + x) * kChunk + (i % kChunk);
 }
 
+// xcd_block while its contiguous ranges hold about equal work (every range's
+// CSR entries within a quarter of an eighth of the total), else
+// xcd_spread_block.  `ptr` holds the CSR offsets of the n_items items the
+// blocks own, `per` items a block; every block reads the same nine offsets
+// and reaches the same choice.
+__device__ __forceinline__ int64_t xcd_balanced_block(int64_t b, int64_t nb, const int64_t* ptr, int64_t n_items,
+                                                      int per) {
+  const int64_t q = nb >> 3, r = nb & 7;
+  const int64_t first = ptr[0], total = ptr[n_items] - first;
+  int64_t worst = 0, prev = first;
+  for (int x = 1; x <= 8; ++x) {
+    int64_t item = (x * q + (x < r ? x : r)) * per;
+    if (item > n_items) item = n_items;
+    const int64_t e = ptr[item];
+    worst = e - prev > worst ? e - prev : worst;
+    prev = e;
+  }
+  return 32 * worst > 5 * total ? xcd_spread_block(b, nb) : xcd_block(b, nb);
+}
+
 // Four consecutive elements (16 B for float, 32 B for double), aligned.
 template <typename T>
 struct Quad {

@@ -313,7 +313,8 @@ struct AggHeadsArgs {
 constexpr int kAggStep = 8;
 
 __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a) {
-  const int64_t i = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t i = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_targets, kWavesPerBlock) * kWavesPerBlock +
+                    (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (i >= a.n_targets) return;
   const int q4 = a.d_out / 4, W4 = a.H * q4;

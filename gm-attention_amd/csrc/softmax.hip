@@ -138,7 +138,7 @@ constexpr uint32_t kOrders012 = 0x22110u;
 
 template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
-  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_nodes, kWavesPerBlock);
   const int lane = threadIdx.x & 63;
   const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
   if (i >= a.n_nodes) return;
@@ -201,7 +201,7 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
 
 template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a) {
-  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_nodes, kWavesPerBlock);
   const int lane = threadIdx.x & 63;
   const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
   if (i >= a.n_nodes) return;
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
 
 template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a) {
-  const int64_t blk = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.src_ptr, a.n_nodes, kWavesPerBlock);
   const int lane = threadIdx.x & 63;
   const int64_t j = blk * kWavesPerBlock + (threadIdx.x >> 6);
   if (j >= a.n_nodes) return;
