@@ -99,6 +99,32 @@ def test_mhsa_matches_the_oracle(case, dtype, batched, cuda):
         close(got[2][n], want[2][n], dtype, f"d{n}", reduction=True)
 
 
+def test_mhsa_float32_with_blocks_dealt_in_chunks_matches_the_oracle(cuda):
+    """Two samples of a 24x48 grid: enough blocks (576 for the softmax and the
+    aggregate, 2304 groups) that the kernels deal them to the XCDs in 32-block
+    chunks, which they do here because two samples make the contiguous eighths
+    uneven (the polar quarters hold most edges); float32 batched against the
+    oracle, every gradient."""
+    field, heads, window, batch = {0: 8, 1: 8, 2: 8}, 2, "hard", 2
+    mhsa, x, edges = build(field, heads, window, batch, nlat=24, nlon=48)
+    assert edges.row_ptr.shape[0] - 1 == 2 * 24 * 48
+    mhsa.batched = True
+    probe = problems.normal(x.shape, 7)
+    mhsa.load_state_dict({k: v.float().double() for k, v in mhsa.state_dict().items()})
+    x = x.float().double()
+    want = run(mhsa, x, edges.to(None, torch.float32).to(None, torch.float64), probe, oracle=True, tolerance=1e-5)
+    gpu = SO2MHSA(mhsa.field_type_in, heads, cutoff=mhsa.cutoff, window=window, batched=True, dtype=torch.float32,
+                  device=cuda)
+    gpu.load_state_dict({k: v.float() for k, v in mhsa.state_dict().items()})
+    got = run(gpu, x.to(cuda, torch.float32), edges.to(cuda, torch.float32), probe)
+    close(got[0], want[0], torch.float32, "out")
+    for f in want[1]:
+        close(got[1][f], want[1][f], torch.float32, f"dx[{f}]")
+    assert set(got[2]) == set(want[2])
+    for n in want[2]:
+        close(got[2][n], want[2][n], torch.float32, f"d{n}", reduction=True)
+
+
 def test_chunked_equals_whole(cuda):
     mhsa, x, edges = build({0: 8, 1: 8, 2: 8}, 4, "hard", 2)
     gpu = mhsa.to(cuda)
