@@ -433,7 +433,7 @@ def run_encoder(args) -> None:
 
     def step():
         y = encs[0](SO2FeatureField.from_flat(types[0], x), down[0])
-        z = encs[1](y, down[1]).to_flat()
+        z = encs[1](y, down[1])._rows()
         torch.autograd.backward(z, upstream)
 
     def clear():
@@ -636,7 +636,7 @@ def main() -> None:
     elif args.workload == "attention":
         def step():
             x = SO2FeatureField.from_flat(field, x_flat)
-            y = mhsa(x, edges).to_flat()
+            y = mhsa(x, edges)._rows()
             torch.autograd.backward(y, upstream)
         workload = ("SO2MHSA(batched) fwd+bwd: stacked Q/K projections, fused scores+softmax, 8 heads of node "
                     "products + radial trunk + fused factored value aggregation, output projection; input and "
@@ -651,7 +651,7 @@ def main() -> None:
 
         def step():
             x = SO2FeatureField.from_flat(field, x_flat)
-            y = conv(x, edges).to_flat()
+            y = conv(x, edges)._rows()
             torch.autograd.backward(y, upstream)
         workload = ("SO2Convolution(depthwise=True, n_radial_basis=4) fwd+bwd: radial trunk and readout heads, "
                     "fused depthwise walk (transport, coefficient products, weighting, segment sum); input and "

@@ -33,23 +33,25 @@ __device__ __forceinline__ T neg_inf() {
 // Blocks are dispatched round-robin over the eight XCDs, each with its own L2.
 // Remap so XCD x runs a contiguous range of logical blocks: neighbouring nodes
 // (which share most of their neighbours' rows) then share one L2.
-__device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
+__host__ __device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
   const int64_t q = nb >> 3, r = nb & 7, x = b & 7;
   return x * q + (x < r ? x : r) + (b >> 3);
 }
 
-// The same XCD assignment in chunks of 32 logical blocks dealt round-robin
+// The same XCD assignment in chunks of logical blocks dealt round-robin
 // (XCD x runs chunks x, x + 8, ...; the last partial round keeps its order):
 // every XCD then runs work from every latitude band.  Contiguous ranges are
 // even only when each XCD's range holds a pole and an equator alike (B = 4 on
 // eight XCDs); with two samples a range is a quarter of a sample and the
 // polar quarters carry about five times the edges of the equatorial ones.
-__device__ __forceinline__ int64_t xcd_spread_block(int64_t b, int64_t nb) {
-  constexpr int64_t kChunk = 32;
-  const int64_t full = nb / (8 * kChunk) * (8 * kChunk);
+// Chunks are 32 blocks from 256 blocks up, nb / 32 (at least 1) below, so a
+// small launch is still dealt in whole rounds.
+__host__ __device__ __forceinline__ int64_t xcd_spread_block(int64_t b, int64_t nb) {
+  const int64_t chunk = nb >= 256 ? 32 : (nb >= 64 ? nb >> 5 : 1);
+  const int64_t full = nb / (8 * chunk) * (8 * chunk);
   if (b >= full) return b;
   const int64_t x = b & 7, i = b >> 3;
-  return ((i / kChunk) * 8 + x) * kChunk + (i % kChunk);
+  return ((i / chunk) * 8 + x) * chunk + (i % chunk);
 }
 
 // xcd_block while its contiguous ranges hold about equal work (every range's
@@ -57,8 +59,8 @@ __device__ __forceinline__ int64_t xcd_spread_block(int64_t b, int64_t nb) {
 // xcd_spread_block.  `ptr` holds the CSR offsets of the n_items items the
 // blocks own, `per` items a block; every block reads the same nine offsets
 // and reaches the same choice.
-__device__ __forceinline__ int64_t xcd_balanced_block(int64_t b, int64_t nb, const int64_t* ptr, int64_t n_items,
-                                                      int per) {
+__host__ __device__ __forceinline__ int64_t xcd_balanced_block(int64_t b, int64_t nb, const int64_t* ptr,
+                                                               int64_t n_items, int per) {
   const int64_t q = nb >> 3, r = nb & 7;
   const int64_t first = ptr[0], total = ptr[n_items] - first;
   int64_t worst = 0, prev = first;

@@ -58,3 +58,13 @@ int parse_attention_layout(const int64_t* desc, int64_t F, int64_t H, int64_t D,
 extern "C" const char* gm_last_error(void) { return gm::last_error.c_str(); }
 
 extern "C" int gm_abi_version(void) { return 1; }
+
+extern "C" int gm_xcd_block_map(int64_t nb, int kind, const int64_t* ptr, int64_t n_items, int per, int64_t* out) {
+  GM_REQUIRE(nb >= 1 && out != nullptr, "nb must be positive and out a host array of nb entries");
+  GM_REQUIRE(kind >= 0 && kind <= 2, "kind must be 0 (contiguous), 1 (spread) or 2 (balanced)");
+  GM_REQUIRE(kind != 2 || (ptr != nullptr && n_items >= 1 && per >= 1), "the balanced map needs the CSR offsets");
+  for (int64_t b = 0; b < nb; ++b)
+    out[b] = kind == 0 ? gm::xcd_block(b, nb)
+                       : (kind == 1 ? gm::xcd_spread_block(b, nb) : gm::xcd_balanced_block(b, nb, ptr, n_items, per));
+  return GM_OK;
+}

@@ -122,7 +122,7 @@ class SO2Attention(nn.Module):
         if not fused_attention.softmax_head_enabled(self, x, edges):
             raise RuntimeError("the fused scores-and-softmax op is not enabled for this call "
                                "(GM_FUSED_ATTENTION=1 and device tensors required)")
-        alpha = fused_attention.softmax_head(self, q.to_flat(), k.to_flat(), edges)
+        alpha = fused_attention.softmax_head(self, q._rows(), k._rows(), edges)
         if not kernels.factored_enabled():  # the per-edge readout through the fused pair terms
             messages = self.value(gather_to_edges(x, edges.source_index), edges)
             return weighted_segment_sum(alpha, messages.coefficients, edges.row_ptr)
@@ -250,7 +250,7 @@ def _attend_batched_flat(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> Tensor | N
     if (not fused_attention.softmax_enabled(mhsa, x, edges) or not kernels.factored_enabled()
             or not fused_factored.enabled(values[0], x, edges)):
         return None
-    rows = x.to_flat()
+    rows = x._rows()
     if rows.ndim != 2:
         return None
     with torch.profiler.record_function("gm::attention/attend"):
@@ -277,7 +277,7 @@ def _attend_batched(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> dict[int, Tenso
         if not fused_attention.softmax_enabled(mhsa, x, edges):
             raise RuntimeError("the fused scores-and-softmax op is not enabled for this call "
                                "(GM_FUSED_ATTENTION=1 and device tensors required)")
-        alpha = fused_attention.softmax(mhsa, queries.to_flat(), keys.to_flat(), edges)  # (n_edges, n_heads)
+        alpha = fused_attention.softmax(mhsa, queries._rows(), keys._rows(), edges)  # (n_edges, n_heads)
         return _aggregated_factored(mhsa, x, edges, alpha)
 
 

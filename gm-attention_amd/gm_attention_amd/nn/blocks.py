@@ -126,12 +126,12 @@ class SO2TransformerBlock(nn.Module):
             out = self.attention(field, edges)
         else:
             out = self.attention.forward_chunked(field, edges, chunk_size=chunk_size)
-        return out.to_flat()
+        return out._rows()
 
     def _run(self, x: SO2FeatureField, edges, *, chunk_size: int | None) -> SO2FeatureField:
         if x.field_type != self.field_type:
             raise ValueError(f"Expected a field of type {self.field_type!r}, got {x.field_type!r}.")
-        flat = x.to_flat()
+        flat = x._rows()
         batch = flat.shape[:-1]
         rows = flat.reshape(-1, flat.shape[-1])
         return SO2FeatureField.from_flat(self.field_type, self.forward_flat(rows, edges, chunk_size).reshape(*batch, -1))

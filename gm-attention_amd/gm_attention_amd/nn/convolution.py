@@ -123,10 +123,10 @@ class SO2Convolution(nn.Module):
         assert isinstance(kernel, SO2DepthwiseKernel)
         kernel.validate_edges(edges)
         if depthwise_radial.eligible(kernel, x, edges):
-            flat = depthwise_radial.forward(self, x.to_flat(), edges)
+            flat = depthwise_radial.forward(self, x._rows(), edges)
             return SO2FeatureField.from_flat(self.field_type_out, flat).coefficients
         rc, cc = stacked_coefficients([kernel], edges)
-        flat = fused_attention.forward_depthwise(self, x.to_flat(), rc, cc, edges)
+        flat = fused_attention.forward_depthwise(self, x._rows(), rc, cc, edges)
         return SO2FeatureField.from_flat(self.field_type_out, flat).coefficients
 
     def forward_chunked(self, x: SO2FeatureField, edges, *, chunk_size: int) -> SO2FeatureField:

@@ -94,7 +94,7 @@ class SO2ScalarGatedNonlinearity(nn.Module):
     def forward_flat(self, flat: Tensor) -> Tensor:
         """The nonlinearity on flat rows ``(N, D)``."""
         if not self.uses_hip(flat):
-            return self._eager(SO2FeatureField.from_flat(self.field_type, flat)).to_flat()
+            return self._eager(SO2FeatureField.from_flat(self.field_type, flat))._rows()
         flat = flat.contiguous()
         layout = self._layout()
         if layout.G == 0:
@@ -106,7 +106,7 @@ class SO2ScalarGatedNonlinearity(nn.Module):
     def forward(self, x: SO2FeatureField) -> SO2FeatureField:
         if x.field_type != self.field_type:
             raise ValueError(f"Expected a field of type {self.field_type!r}, got {x.field_type!r}.")
-        flat = x.to_flat()
+        flat = x._rows()
         if not self.uses_hip(flat):
             return self._eager(x)
         batch = flat.shape[:-1]

@@ -92,7 +92,7 @@ class SO2LayerNorm(nn.Module):
     def forward_flat(self, flat: Tensor) -> Tensor:
         """The normalization of flat rows ``(N, D)``."""
         if not self.uses_hip(flat):
-            return self._eager(SO2FeatureField.from_flat(self.field_type, flat)).to_flat()
+            return self._eager(SO2FeatureField.from_flat(self.field_type, flat))._rows()
         pd = _native.param_dtype(flat.dtype)
         beta = self.beta.to(pd) if self.has_bias else None
         return LayerNormOp.apply(flat.contiguous(), self.gamma_flat(pd), beta, self._layout(), self.eps)
@@ -100,7 +100,7 @@ class SO2LayerNorm(nn.Module):
     def forward(self, x: SO2FeatureField) -> SO2FeatureField:
         if x.field_type != self.field_type:
             raise ValueError(f"Expected a field of type {self.field_type!r}, got {x.field_type!r}.")
-        flat = x.to_flat()
+        flat = x._rows()
         if not self.uses_hip(flat):
             return self._eager(x)
         batch = flat.shape[:-1]
@@ -162,7 +162,7 @@ class SO2Dropout(nn.Module):
     def forward_flat(self, flat: Tensor) -> Tensor:
         if not self.active():
             return flat
-        return self(SO2FeatureField.from_flat(self.field_type, flat)).to_flat()
+        return self(SO2FeatureField.from_flat(self.field_type, flat))._rows()
 
     def extra_repr(self) -> str:
         return f"field_type={self.field_type!r}, p={self.p:.3g}"

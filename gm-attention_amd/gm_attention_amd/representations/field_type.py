@@ -135,15 +135,21 @@ class SO2FeatureField:
         return field
 
     def to_flat(self) -> Tensor:
-        """The flat rows (frequency 0, then each frequency's ``(a_n, 2)`` pairs):
-        the tensor a field was made from by ``from_flat`` while its coefficients
-        are still the views of it, otherwise a new concatenation."""
+        """The flat rows (frequency 0, then each frequency's ``(a_n, 2)`` pairs)
+        as a new tensor (reference field_type.py:472-488)."""
+        blocks = [self.coefficients[f] if f == 0 else self.coefficients[f].flatten(-2) for f in self.field_type.frequencies]
+        return torch.cat(blocks, dim=-1)
+
+    def _rows(self) -> Tensor:
+        """The flat rows for the package's own read-only use: the tensor the
+        field was made from by ``from_flat`` while its coefficients are still
+        the views of it (no copy), otherwise :meth:`to_flat`.  Callers must not
+        write into the result."""
         if self._flat is not None:
             flat, views = self._flat
             if all(self.coefficients[f] is v for f, v in views.items()):
                 return flat
-        blocks = [self.coefficients[f] if f == 0 else self.coefficients[f].flatten(-2) for f in self.field_type.frequencies]
-        return torch.cat(blocks, dim=-1)
+        return self.to_flat()
 
     def apply_rotation(self, angles: Tensor) -> SO2FeatureField:
         return SO2FeatureField(self.field_type, {

@@ -61,6 +61,15 @@ const char* gm_last_error(void);
 /* ABI version of this library: bump when a signature changes. */
 int gm_abi_version(void);
 
+/* Host-side diagnostic, no counterpart in the reference: the logical block
+ * each hardware block b < nb runs under the kernels' XCD assignments, written
+ * to out[b] (HOST memory).  kind 0: contiguous eighths (xcd_block); 1: chunks
+ * dealt round-robin (xcd_spread_block); 2: contiguous unless some eighth of
+ * the items holds more than 5/4 of an eighth of the CSR entries
+ * (xcd_balanced_block over HOST ptr (n_items + 1), per items a block).
+ * Touches no GPU. */
+int gm_xcd_block_map(int64_t nb, int kind, const int64_t* ptr, int64_t n_items, int per, int64_t* out);
+
 /* ---------------- scores and neighbourhood softmax ----------------
  *
  * alpha[e, h] = softmax over target i's edges e of

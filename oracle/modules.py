@@ -35,17 +35,35 @@ def _phase(table: Tensor, order: int) -> Tensor:
     return col.conj() if order < 0 else col
 
 
+def gaussian_basis(distances: Tensor, n_basis: int, cutoff: float) -> Tensor:
+    """``_GaussianRadialBasis`` (reference kernels.py:191-231), from its
+    definition: ``phi_k(s) = exp(-(s - mu_k)^2 / (2 sigma^2))`` of
+    ``s = (r / cutoff)^2``, centres ``mu_k = k / (n - 1)`` evenly over
+    ``[0, 1]`` (one centre at 0 when ``n = 1``), ``sigma`` the spacing
+    ``1 / (n - 1)`` (1 when ``n = 1``)."""
+    spacing = 1.0 / (n_basis - 1) if n_basis > 1 else 1.0
+    centres = torch.tensor([k / (n_basis - 1) for k in range(n_basis)] if n_basis > 1 else [0.0],
+                           dtype=distances.dtype)
+    s = (distances / cutoff) * (distances / cutoff)
+    return torch.exp(-0.5 * ((s.unsqueeze(-1) - centres) / spacing) ** 2)
+
+
 def _trunk(kernel, distances: Tensor) -> Tensor:
-    """The Gaussian basis of ``(r / cutoff)^2`` then the ``Linear``/``SiLU`` trunk (kernels.py:191-231, 108-117)."""
+    """The Gaussian basis of ``(r / cutoff)^2`` then the ``Linear``/``SiLU`` trunk (kernels.py:191-231, 108-117).
+    Only the basis size and cutoff are read from the module; the basis itself is :func:`gaussian_basis`."""
     rb = kernel.radial_basis
-    s = (distances / rb.cutoff) * (distances / rb.cutoff)
-    hidden = torch.exp(-0.5 * ((s.unsqueeze(-1) - rb.centers) / rb.width) ** 2)
+    hidden = gaussian_basis(distances, rb.n_basis, rb.cutoff)
     for layer in kernel.radial_trunk:
         if isinstance(layer, torch.nn.Linear):
             hidden = hidden @ layer.weight.T + (layer.bias if layer.bias is not None else 0.0)
         else:
             hidden = torch.nn.functional.silu(hidden)
     return hidden
+
+
+def _apply(matrix: Tensor, v: Tensor) -> Tensor:
+    """Per edge, ``(E, b, a) @ (E, a) -> (E, b)``."""
+    return torch.matmul(matrix, v.unsqueeze(-1)).squeeze(-1)
 
 
 def layout(fin, fout) -> tuple[list[tuple[int, int, str, int, int]], int]:
@@ -76,11 +94,6 @@ def readout_messages(kernel, x: dict[int, Tensor], source: Tensor, distances: Te
     E = source.shape[0]
     hidden = _trunk(kernel, distances)
     ranges, _ = layout(fin, fout)
-    coeff = None
-    if kernel.complex_head is not None:
-        coeff = hidden @ kernel.complex_head.weight.T
-        if kernel.complex_head.bias is not None:
-            coeff = coeff + kernel.complex_head.bias
     real = None
     if kernel.real_head is not None:
         real = hidden @ kernel.real_head.weight.T
@@ -102,11 +115,16 @@ def readout_messages(kernel, x: dict[int, Tensor], source: Tensor, distances: Te
         return s.unsqueeze(-1)
 
     def matrix(n: int, m: int, role: str) -> Tensor:
+        # each block's rows of the complex head read out on their own (the same
+        # numbers as slicing the whole readout, without an (E, width) gradient per slice)
         for nn, mm, rr, start, _p in ranges:
             if (nn, mm, rr) == (n, m, role):
                 a, b = fin.multiplicity(n), fout.multiplicity(m)
-                block = coeff[:, start:start + 2 * a * b].reshape(E, b, a, 2)
-                return torch.view_as_complex(block.contiguous())
+                rows = slice(start, start + 2 * a * b)
+                block = hidden @ kernel.complex_head.weight[rows].T
+                if kernel.complex_head.bias is not None:
+                    block = block + kernel.complex_head.bias[rows]
+                return torch.view_as_complex(block.reshape(E, b, a, 2).contiguous())
         raise KeyError((n, m, role))
 
     out: dict[int, Tensor] = {}
@@ -116,19 +134,19 @@ def readout_messages(kernel, x: dict[int, Tensor], source: Tensor, distances: Te
         for n in fin.frequencies:
             a = fin.multiplicity(n)
             if n == 0 and m == 0:
-                acc = acc + (real.reshape(E, b, a) * xs[0].unsqueeze(-2)).sum(-1)
+                acc = acc + _apply(real.reshape(E, b, a), xs[0])
                 continue
             lin = matrix(n, m, "linear")
             if n == 0:
-                term = _phase(angular, m).unsqueeze(-1) * (lin * xs[0].to(lin.dtype).unsqueeze(-2)).sum(-1)
+                term = _phase(angular, m).unsqueeze(-1) * _apply(lin, xs[0].to(lin.dtype))
                 acc = acc + term * power(abs(m - n))
             elif m == 0:
                 rotated = _phase(angular, -n).unsqueeze(-1) * xs[n]
-                acc = acc + (lin * rotated.conj().unsqueeze(-2)).sum(-1).real * power(n)
+                acc = acc + _apply(lin, rotated.conj()).real * power(n)
             else:
                 anti = matrix(n, m, "antilinear")
-                lterm = (lin * (_phase(angular, m - n).unsqueeze(-1) * xs[n]).unsqueeze(-2)).sum(-1)
-                aterm = (anti * (_phase(angular, m + n).unsqueeze(-1) * xs[n].conj()).unsqueeze(-2)).sum(-1)
+                lterm = _apply(lin, _phase(angular, m - n).unsqueeze(-1) * xs[n])
+                aterm = _apply(anti, _phase(angular, m + n).unsqueeze(-1) * xs[n].conj())
                 acc = acc + lterm * power(abs(m - n)) + aterm * power(m + n)
         out[m] = acc if m == 0 else torch.view_as_real(acc)
     return out
@@ -193,7 +211,8 @@ def factored_messages(kernel, x: dict[int, Tensor], source: Tensor, distances: T
             n, mm, role = block
             if mm != m:
                 continue
-            combined = (h.unsqueeze(-1) * products[block].index_select(0, source)).sum(dim=1)
+            gathered = products[block].index_select(0, source)
+            combined = torch.matmul(h.to(gathered.dtype).unsqueeze(1), gathered).squeeze(1)
             if role == "real":
                 term = combined
             else:
@@ -271,20 +290,23 @@ def softmax_weights(q: dict[int, Tensor], k: dict[int, Tensor], edges, cutoff: f
     return u / torch.segment_reduce(u, "sum", offsets=edges.row_ptr, axis=0).index_select(0, target)
 
 
-def mhsa_forward(mhsa, x: dict[int, Tensor], edges, tolerance: float | None = None) -> dict[int, Tensor]:
+def mhsa_forward(mhsa, x: dict[int, Tensor], edges, tolerance: float | None = None,
+                 messages: str = "readout") -> dict[int, Tensor]:
     """``SO2MHSA.forward`` (reference attention.py:582-608), head by head
     (the function the batched pass computes, attention.py:858-909): each
     head's query and key maps, its softmax, its value kernel's per-edge
-    readout weighted and summed per target; heads concatenated head-major;
-    the output intertwiner."""
+    messages (``messages``: the per-edge readout, or the factored branch --
+    the same function regrouped, cheaper for wide fields) weighted and summed
+    per target; heads concatenated head-major; the output intertwiner."""
+    evaluate = {"readout": readout_messages, "factored": factored_messages}[messages]
     fin = mhsa.field_type_in
     outs = []
     for head in mhsa.heads:
         q = linear(head.query, x, head.field_type_attn)
         k = linear(head.key, x, head.field_type_attn)
         alpha = softmax_weights(q, k, edges, head.cutoff, head.window, 1, head._score_scale, tolerance)[:, 0]
-        msgs = readout_messages(head.value, x, edges.source_index, edges.distances, edges.angular_phases,
-                                edges.transport_phases)
+        msgs = evaluate(head.value, x, edges.source_index, edges.distances, edges.angular_phases,
+                        edges.transport_phases)
         agg = {f: torch.segment_reduce(alpha.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum", offsets=edges.row_ptr,
                                        axis=0) for f, m in msgs.items()}
         outs.append(agg)
@@ -403,12 +425,13 @@ def gated(act, x: dict[int, Tensor]) -> dict[int, Tensor]:
     return out
 
 
-def block_forward(block, x: dict[int, Tensor], edges, tolerance: float | None = None) -> dict[int, Tensor]:
+def block_forward(block, x: dict[int, Tensor], edges, tolerance: float | None = None,
+                  messages: str = "readout") -> dict[int, Tensor]:
     """``SO2TransformerBlock._run`` (reference nn/blocks.py:326-349) with
     dropout off: x + Mixer(LN1 x), then + W2 act(W1 LN2 x)."""
     normed = layer_norm(block.norm1, x)
     if block.mixer == "attention":
-        mixed = mhsa_forward(block.attention, normed, edges, tolerance)
+        mixed = mhsa_forward(block.attention, normed, edges, tolerance, messages)
     else:
         mixed = conv_forward(block.attention, normed, edges, tolerance)
     x = {f: x[f] + mixed[f] for f in x}
@@ -417,12 +440,13 @@ def block_forward(block, x: dict[int, Tensor], edges, tolerance: float | None = 
     return {f: x[f] + hidden[f] for f in x}
 
 
-def encode_forward(enc, x: dict[int, Tensor], edges, tolerance: float | None = None) -> dict[int, Tensor]:
+def encode_forward(enc, x: dict[int, Tensor], edges, tolerance: float | None = None,
+                   messages: str = "readout") -> dict[int, Tensor]:
     """``IcoEncode.forward`` (reference nn/blocks.py:427-493) on bipartite edges:
     the per-edge readout of the kernel on the fine sources, times window times
     quadrature, summed per coarse target."""
-    msgs = readout_messages(enc.kernel, x, edges.source_index, edges.distances, edges.angular_phases,
-                            edges.transport_phases)
+    evaluate = {"readout": readout_messages, "factored": factored_messages}[messages]
+    msgs = evaluate(enc.kernel, x, edges.source_index, edges.distances, edges.angular_phases, edges.transport_phases)
     d = edges.distances
     tol = tolerance if tolerance is not None else (1e-10 if d.dtype == torch.float64 else 1e-5)
     win = (d <= enc.cutoff + tol).to(d.dtype) if enc.window == "hard" else torch.relu(1.0 - (d / enc.cutoff) ** 2) ** 2

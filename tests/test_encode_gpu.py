@@ -55,11 +55,12 @@ def split(ft, flat):
     return dict(SO2FeatureField.from_flat(ft, flat).coefficients)
 
 
-def run(enc, flat, edges, probe, *, oracle=False, tolerance=None):
+def run(enc, flat, edges, probe, *, oracle=False, tolerance=None, messages="readout"):
     leaf = flat.clone().requires_grad_(True)
     enc.zero_grad(set_to_none=True)
     if oracle:
-        out = modules.flat(modules.encode_forward(enc.integral, split(enc.field_type_in, leaf), edges, tolerance))
+        out = modules.flat(modules.encode_forward(enc.integral, split(enc.field_type_in, leaf), edges, tolerance,
+                                                  messages))
     else:
         out = enc(SO2FeatureField.from_flat(enc.field_type_in, leaf), edges).to_flat()
     (out * probe.to(out.device, out.dtype)).sum().backward()
@@ -132,3 +133,35 @@ def test_encode_is_gauge_equivariant(cuda):
     want = y.gauge_transform(tc.to(cuda))
     torch.testing.assert_close(y_turned.to_flat(), want.to_flat(), rtol=1e-9, atol=1e-9)
     assert float((y.to_flat() - want.to_flat()).abs().max()) > 1e-3
+
+
+def test_c5_second_hop_matches_the_oracle(cuda):
+    """C5's second restriction, {0:64,1:64,2:64} -> {0:128,1:128,2:128} (beyond
+    the op's bounds: 40 output tiles), over the small hierarchy's second hop,
+    two samples, float32, every gradient; the oracle in the factored order
+    (the per-edge readout of a 64 -> 128 kernel is ~200k reals an edge)."""
+    print("encode C5 hop 2 {0:64,1:64,2:64} -> {0:128,1:128,2:128} f32", flush=True)
+    fin, fout = SO2FieldType({0: 64, 1: 64, 2: 64}), SO2FieldType({0: 128, 1: 128, 2: 128})
+    h = levels().tile(2)
+    edges = h.down_edges[1]
+    torch.manual_seed(0)
+    enc = EquiEncode(fin, fout, cutoff=1.5 * math.pi / 4, window="quartic", n_radial_basis=4, dtype=D64)
+    with torch.no_grad():
+        for p in enc.parameters():
+            p.add_(0.1 * torch.randn_like(p))
+    enc.load_state_dict({k: v.float().double() for k, v in enc.state_dict().items()})
+    x = problems.normal((h.levels[1].n_nodes, fin.dimension), 1).float().double()
+    probe = problems.normal((edges.row_ptr.shape[0] - 1, fout.dimension), 2)
+    want = run(enc, x, edges.to(None, torch.float32).to(None, D64), probe, oracle=True, tolerance=1e-5,
+               messages="factored")
+    gpu = EquiEncode(fin, fout, cutoff=enc.cutoff, window="quartic", n_radial_basis=4, dtype=torch.float32,
+                     device=cuda)
+    gpu.load_state_dict({k: v.float() for k, v in enc.state_dict().items()})
+    tiles = fused_factored.tiles(gpu.integral.kernel)
+    assert tiles is not None and len(tiles) == 40, tiles
+    got = run(gpu, x.to(cuda, torch.float32), edges.to(cuda, torch.float32), probe)
+    close(got[0], want[0], torch.float32, "out")
+    close(got[1], want[1], torch.float32, "dx")
+    assert set(got[2]) == set(want[2])
+    for k in want[2]:
+        close(got[2][k], want[2][k], torch.float32, f"d{k}", reduction=True)
