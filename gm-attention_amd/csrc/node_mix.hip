@@ -1,0 +1,589 @@
+// The factored kernel's node-side channel mixing (CDNA4, gfx950): every
+// head's node mixes Z_t(j) = W_t v_j for one input frequency as one real
+// product over the nodes,
+//
+//   forward   mix (N, C) = v (N, w) M (w, C)
+//   backward  dv (N, w)  = dmix M^T            (the node field's gradient)
+//             dM (w, C)  = v^T dmix            (the mixing matrix's gradient)
+//
+// with v the node field's frequency-n reals (w <= 128, a strided view of the
+// flat rows) and M the heads' real mixing matrix (every block's complex
+// product and input conjugation encoded as reals; C = H K C_n columns).  The
+// reference forms the same numbers as one complex einsum("ja,bat->jtb") per
+// node vector and block group (nn/kernels.py:575-603, over _block_weights
+// :506-536) and their gradients through autograd.
+//
+// All three are v_mfma_f32_16x16x4f32 products.  Lane l = 16 q + c of the
+// MFMA supplies A[c][q] and B[q][c] and holds D[4 q + i][c], i < 4.
+//
+// * forward: the contraction is short, so each wave keeps its columns of M in
+//   registers for the whole launch and streams 64-row tiles of v through LDS;
+//   M is the A operand (D = mix^T), so a lane's four D entries are four
+//   consecutive columns of one row: one 16-byte store each.
+// * input gradient: 128-row tiles, each wave 32 rows over the whole
+//   contraction, dmix and M staged per 64-column chunk in LDS; the
+//   accumulators restart every four chunks into a running total, so no fp32
+//   sum runs sequentially over more than 256 columns.
+// * weight gradient: split over row ranges into partial (w, C) matrices, each
+//   from 64-row chunks staged in LDS (up to 64-wide vectors: one partial per
+//   wave, each wave a quarter of every chunk over the workgroup's whole
+//   w x 64 tile, so an operand read feeds four MFMAs); a second pass sums the
+//   partials in a fixed order.  No atomics anywhere: results are deterministic.
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+
+namespace gm {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int kThreads = 256;
+constexpr floatx4 kZero4 = {0.f, 0.f, 0.f, 0.f};
+
+// ---------------------------------------------------------------- forward
+//
+// Workgroup (x, y): columns [x * 64 CT, (x + 1) * 64 CT), wave wv owning CT
+// 16-column tiles from col0 = x * 64 CT + 16 CT wv; row tiles y, y + gridDim.y, ...
+// Step s of the contraction pairs slot q with k = q (W / 4) + s, so a lane's
+// v operands for consecutive steps are consecutive floats of its row (read
+// four at a time from LDS).
+template <int W, int CT>
+__global__ __launch_bounds__(kThreads) void node_mix_forward_kernel(const float* __restrict__ v, int64_t ldv,
+                                                                    const float* __restrict__ M, int64_t N, int w,
+                                                                    int64_t C, float* __restrict__ out, int vec_v,
+                                                                    int vec_out) {
+  constexpr int KS = W / 4;    // contraction steps
+  constexpr int LDT = W + 4;   // LDS row stride: a 16-lane b128 read covers all 64 banks once
+  constexpr int QUADS = 64 * KS;  // 16-byte pieces of a 64-row tile (KS of them a row)
+  __shared__ __align__(16) float vt[64 * LDT];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
+  const int64_t col0 = (int64_t)blockIdx.x * (64 * CT) + 16 * CT * wv;
+  float mreg[KS][CT];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int k = q * KS + s;
+#pragma unroll
+    for (int j = 0; j < CT; ++j) {
+      const int64_t col = col0 + 16 * j + c;
+      mreg[s][j] = (k < w && col < C) ? M[(int64_t)k * C + col] : 0.f;
+    }
+  }
+  const int64_t n_tiles = (N + 63) / 64;
+  constexpr int PER = (QUADS + kThreads - 1) / kThreads;
+  float4 pre[PER];
+  auto fetch = [&](int64_t tile) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      const int row = idx / KS, kq = idx % KS;
+      const int64_t r = tile * 64 + row;
+      const int k = 4 * kq;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (idx < QUADS && r < N) {
+        const float* src = v + r * ldv + k;
+        if (vec_v && k + 3 < w) {
+          x = *reinterpret_cast<const float4*>(src);
+        } else {
+          x.x = k < w ? src[0] : 0.f;
+          x.y = k + 1 < w ? src[1] : 0.f;
+          x.z = k + 2 < w ? src[2] : 0.f;
+          x.w = k + 3 < w ? src[3] : 0.f;
+        }
+      }
+      pre[p] = x;
+    }
+  };
+  if ((int64_t)blockIdx.y < n_tiles) fetch(blockIdx.y);
+  for (int64_t tile = blockIdx.y; tile < n_tiles; tile += gridDim.y) {
+    __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      if (idx < QUADS) *reinterpret_cast<float4*>(&vt[(idx / KS) * LDT + 4 * (idx % KS)]) = pre[p];
+    }
+    __syncthreads();
+    if (tile + gridDim.y < n_tiles) fetch(tile + gridDim.y);
+    const int64_t row0 = tile * 64;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      float b[KS];
+#pragma unroll
+      for (int s4 = 0; s4 < KS / 4; ++s4) {
+        const float4 x = *reinterpret_cast<const float4*>(&vt[(16 * rt + c) * LDT + q * KS + 4 * s4]);
+        b[4 * s4] = x.x;
+        b[4 * s4 + 1] = x.y;
+        b[4 * s4 + 2] = x.z;
+        b[4 * s4 + 3] = x.w;
+      }
+      floatx4 acc[CT];
+#pragma unroll
+      for (int j = 0; j < CT; ++j) acc[j] = kZero4;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int j = 0; j < CT; ++j) acc[j] = mfma4(mreg[s][j], b[s], acc[j]);
+      }
+      const int64_t row = row0 + 16 * rt + c;
+      if (row < N) {
+        float* dst = out + row * C;
+#pragma unroll
+        for (int j = 0; j < CT; ++j) {
+          const int64_t col = col0 + 16 * j + 4 * q;
+          if (vec_out && col + 3 < C) {
+            *reinterpret_cast<float4*>(dst + col) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (col + i < C) dst[col + i] = acc[j][i];
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- input gradient
+//
+// Workgroup x: rows [128 x, 128 x + 128); wave wv rows 32 wv + 16 rt + c
+// (rt < 2) as the A operand, M's rows (the w columns of dv) as B.  Chunk
+// k-slot mapping: step s = 4 t + i of a chunk pairs slot q with column
+// c0 + 16 q + s, so both operands read four consecutive floats of an LDS row.
+// Two waves a SIMD: the compiler then keeps the accumulators with the operands
+// in VGPRs (measured 3.45 vs 3.66 ms at N = 524288, w = 64, C = 5440).
+template <int W>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void node_mix_dinput_kernel(const float* __restrict__ dmix,
+                                                                   const float* __restrict__ M, int64_t N, int w,
+                                                                   int64_t C, float* __restrict__ dv, int64_t lddv) {
+  constexpr int KC = 64, LDD = KC + 4, JW = W / 16;
+  constexpr int DQ = 128 * KC / 4 / kThreads;  // 16-byte pieces of the dmix tile per thread: 8
+  constexpr int MQ = W * KC / 4 / kThreads;    // of the M tile: W / 16
+  __shared__ __align__(16) float dt[128 * LDD];
+  __shared__ __align__(16) float mt[W * LDD];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * 128;
+  const int64_t n_chunks = (C + KC - 1) / KC;
+  float4 pd[DQ], pm[MQ];
+  auto fetch = [&](int64_t ch) {
+    const int64_t c0 = ch * KC;
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int64_t r = row0 + row, col = c0 + 4 * cq;
+      pd[p] = (r < N && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int p = 0; p < MQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int64_t col = c0 + 4 * cq;
+      pm[p] = (row < w && col < C) ? *reinterpret_cast<const float4*>(M + (int64_t)row * C + col)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  floatx4 acc[2][JW], tot[2][JW];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int j = 0; j < JW; ++j) acc[rt][j] = tot[rt][j] = kZero4;
+  fetch(0);
+  for (int64_t ch = 0; ch < n_chunks; ++ch) {
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      *reinterpret_cast<float4*>(&dt[(idx >> 4) * LDD + 4 * (idx & 15)]) = pd[p];
+    }
+#pragma unroll
+    for (int p = 0; p < MQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      *reinterpret_cast<float4*>(&mt[(idx >> 4) * LDD + 4 * (idx & 15)]) = pm[p];
+    }
+    __syncthreads();
+    if (ch + 1 < n_chunks) fetch(ch + 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float4 a[2], b[JW];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        a[rt] = *reinterpret_cast<const float4*>(&dt[(32 * wv + 16 * rt + c) * LDD + 16 * q + 4 * t]);
+#pragma unroll
+      for (int j = 0; j < JW; ++j) b[j] = *reinterpret_cast<const float4*>(&mt[(16 * j + c) * LDD + 16 * q + 4 * t]);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int j = 0; j < JW; ++j) {
+          acc[rt][j] = mfma4(a[rt].x, b[j].x, acc[rt][j]);
+          acc[rt][j] = mfma4(a[rt].y, b[j].y, acc[rt][j]);
+          acc[rt][j] = mfma4(a[rt].z, b[j].z, acc[rt][j]);
+          acc[rt][j] = mfma4(a[rt].w, b[j].w, acc[rt][j]);
+        }
+    }
+    if ((ch & 3) == 3 || ch + 1 == n_chunks) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int j = 0; j < JW; ++j) {
+          tot[rt][j] += acc[rt][j];
+          acc[rt][j] = kZero4;
+        }
+    }
+  }
+  // D[4 q + i][c]: dv row row0 + 32 wv + 16 rt + 4 q + i, column 16 j + c
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int j = 0; j < JW; ++j) {
+      const int col = 16 * j + c;
+      if (col >= w) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t r = row0 + 32 * wv + 16 * rt + 4 * q + i;
+        if (r < N) dv[r * lddv + col] = tot[rt][j][i];
+      }
+    }
+}
+
+// ---------------------------------------------------------------- weight gradient
+//
+// Vectors wider than 64 reals: workgroup (x, y) owns columns [128 x, 128 x + 128)
+// (wave wv: 32 wv + 16 jc + c, jc < 2) over rows [y rps, min(N, (y + 1) rps));
+// v^T as A (w rows in 16-row tiles), dmix as B.  Step s of a 64-row chunk
+// pairs slot q with row 4 s + q (so does the kernel below).
+template <int W>
+constexpr int dweight_ldv() {
+  return (W % 64 == 16 || W % 64 == 48) ? W : W + 16;  // rows 4 s + q land 16 banks apart
+}
+
+template <int W>
+__global__ __launch_bounds__(kThreads) void node_mix_dweight_kernel(const float* __restrict__ v, int64_t ldv,
+                                                                    const float* __restrict__ dmix, int64_t N, int w,
+                                                                    int64_t C, int64_t rps, float* __restrict__ partial,
+                                                                    int vec_v) {
+  constexpr int RC = 64, LDV = dweight_ldv<W>(), LDM = 128 + 16, IW = W / 16;
+  constexpr int VQ = (RC * W / 4 + kThreads - 1) / kThreads;  // 16-byte pieces of the v tile per thread
+  constexpr int DQ = RC * 128 / 4 / kThreads;                  // of the dmix tile: 8
+  __shared__ __align__(16) float vt[RC * LDV];
+  __shared__ __align__(16) float dt[RC * LDM];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 128;
+  const int64_t first = (int64_t)blockIdx.y * rps, last = first + rps < N ? first + rps : N;
+  float4 pv[VQ], pd[DQ];
+  auto fetch = [&](int64_t r0) {
+#pragma unroll
+    for (int p = 0; p < VQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx / (W / 4), k = 4 * (idx % (W / 4));
+      const int64_t r = r0 + row;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (idx < RC * W / 4 && r < last) {
+        const float* src = v + r * ldv + k;
+        if (vec_v && k + 3 < w) {
+          x = *reinterpret_cast<const float4*>(src);
+        } else {
+          x.x = k < w ? src[0] : 0.f;
+          x.y = k + 1 < w ? src[1] : 0.f;
+          x.z = k + 2 < w ? src[2] : 0.f;
+          x.w = k + 3 < w ? src[3] : 0.f;
+        }
+      }
+      pv[p] = x;
+    }
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx >> 5, cq = idx & 31;
+      const int64_t r = r0 + row, col = c0 + 4 * cq;
+      pd[p] = (r < last && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  floatx4 acc[IW][2], tot[IW][2];
+#pragma unroll
+  for (int i = 0; i < IW; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = tot[i][j] = kZero4;
+  int64_t chunk = 0;
+  if (first < last) fetch(first);
+  for (int64_t r0 = first; r0 < last; r0 += RC, ++chunk) {
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < VQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      if (idx < RC * W / 4) *reinterpret_cast<float4*>(&vt[(idx / (W / 4)) * LDV + 4 * (idx % (W / 4))]) = pv[p];
+    }
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      *reinterpret_cast<float4*>(&dt[(idx >> 5) * LDM + 4 * (idx & 31)]) = pd[p];
+    }
+    __syncthreads();
+    if (r0 + RC < last) fetch(r0 + RC);
+#pragma unroll 4
+    for (int s = 0; s < RC / 4; ++s) {
+      const int row = 4 * s + q;
+      float a[IW], b[2];
+#pragma unroll
+      for (int i = 0; i < IW; ++i) a[i] = vt[row * LDV + 16 * i + c];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = dt[row * LDM + 32 * wv + 16 * j + c];
+#pragma unroll
+      for (int i = 0; i < IW; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma4(a[i], b[j], acc[i][j]);
+    }
+    if ((chunk & 15) == 15) {
+#pragma unroll
+      for (int i = 0; i < IW; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          tot[i][j] += acc[i][j];
+          acc[i][j] = kZero4;
+        }
+    }
+  }
+  // D[4 q + ii][c]: dM row 16 i + 4 q + ii, column c0 + 32 wv + 16 j + c
+  float* out = partial + (int64_t)blockIdx.y * w * C;
+#pragma unroll
+  for (int i = 0; i < IW; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = c0 + 32 * wv + 16 * j + c;
+      if (col >= C) continue;
+      const floatx4 sum = tot[i][j] + acc[i][j];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int row = 16 * i + 4 * q + ii;
+        if (row < w) out[(int64_t)row * C + col] = sum[ii];
+      }
+    }
+}
+
+// Vectors up to 64 reals wide: workgroup (x, y) owns the whole (w x 64)-column
+// tile [64 x, 64 x + 64) over rows [y rps, min(N, (y + 1) rps)); its four waves
+// take rows 16 wv .. 16 wv + 15 of each 64-row chunk, each accumulating the whole
+// tile (so every operand read feeds four MFMAs), and write one partial each:
+// 4 S partial matrices.
+template <int W>
+__global__ __launch_bounds__(kThreads) void node_mix_dweight_k_kernel(const float* __restrict__ v, int64_t ldv,
+                                                                    const float* __restrict__ dmix, int64_t N, int w,
+                                                                    int64_t C, int64_t rps, float* __restrict__ partial,
+                                                                    int vec_v) {
+  constexpr int RC = 64, LDV = dweight_ldv<W>(), LDM = 64 + 16, IW = W / 16;
+  constexpr int VQ = (RC * W / 4 + kThreads - 1) / kThreads;
+  constexpr int DQ = RC * 64 / 4 / kThreads;  // 4
+  __shared__ __align__(16) float vt[RC * LDV];
+  __shared__ __align__(16) float dt[RC * LDM];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 64;
+  const int64_t first = (int64_t)blockIdx.y * rps, last = first + rps < N ? first + rps : N;
+  float4 pv[VQ], pd[DQ];
+  auto fetch = [&](int64_t r0) {
+#pragma unroll
+    for (int p = 0; p < VQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx / (W / 4), k = 4 * (idx % (W / 4));
+      const int64_t r = r0 + row;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (idx < RC * W / 4 && r < last) {
+        const float* src = v + r * ldv + k;
+        if (vec_v && k + 3 < w) {
+          x = *reinterpret_cast<const float4*>(src);
+        } else {
+          x.x = k < w ? src[0] : 0.f;
+          x.y = k + 1 < w ? src[1] : 0.f;
+          x.z = k + 2 < w ? src[2] : 0.f;
+          x.w = k + 3 < w ? src[3] : 0.f;
+        }
+      }
+      pv[p] = x;
+    }
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int64_t r = r0 + row, col = c0 + 4 * cq;
+      pd[p] = (r < last && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  floatx4 acc[IW][4];
+#pragma unroll
+  for (int i = 0; i < IW; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = kZero4;
+  if (first < last) fetch(first);
+  for (int64_t r0 = first; r0 < last; r0 += RC) {
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < VQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      if (idx < RC * W / 4) *reinterpret_cast<float4*>(&vt[(idx / (W / 4)) * LDV + 4 * (idx % (W / 4))]) = pv[p];
+    }
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      *reinterpret_cast<float4*>(&dt[(idx >> 4) * LDM + 4 * (idx & 15)]) = pd[p];
+    }
+    __syncthreads();
+    if (r0 + RC < last) fetch(r0 + RC);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int row = 16 * wv + 4 * s + q;
+      float a[IW], b[4];
+#pragma unroll
+      for (int i = 0; i < IW; ++i) a[i] = vt[row * LDV + 16 * i + c];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = dt[row * LDM + 16 * j + c];
+#pragma unroll
+      for (int i = 0; i < IW; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma4(a[i], b[j], acc[i][j]);
+    }
+  }
+  float* out = partial + ((int64_t)blockIdx.y * 4 + wv) * w * C;
+#pragma unroll
+  for (int i = 0; i < IW; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = c0 + 16 * j + c;
+      if (col >= C) continue;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int row = 16 * i + 4 * q + ii;
+        if (row < w) out[(int64_t)row * C + col] = acc[i][j][ii];
+      }
+    }
+}
+
+// dM[e] = sum over the splits y = 0, 1, ... of partial[y][e], in that order.
+__global__ __launch_bounds__(kThreads) void node_mix_reduce_kernel(const float* __restrict__ partial, int64_t n,
+                                                                   int64_t splits, float* __restrict__ dM) {
+  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (e >= n) return;
+  float s = 0.f;
+  for (int64_t y = 0; y < splits; ++y) s += partial[y * n + e];
+  dM[e] = s;
+}
+
+int check_shapes(int64_t N, int64_t w, int64_t C) {
+  GM_REQUIRE(N >= 0 && C >= 0, "N and C must be non-negative");
+  GM_REQUIRE(w >= 1 && w <= 128, "the node vector's width w must be in [1, 128]");
+  return GM_OK;
+}
+
+int width_class(int64_t w) { return w <= 16 ? 16 : (w <= 32 ? 32 : (w <= 64 ? 64 : 128)); }
+
+// Column tile of the weight gradient's workgroups: 64 columns for vectors up to
+// 64 reals (the four-partials kernel), 128 above.
+int64_t weight_tile(int64_t w) { return w <= 64 ? 64 : 128; }
+
+// Partial matrices a workgroup row writes: four for the four-partials kernel.
+int64_t weight_partials_per_split(int64_t w) { return w <= 64 ? 4 : 1; }
+
+// The weight gradient's row splits: about 1024 workgroups, whole 64-row chunks per split.
+void weight_splits(int64_t N, int64_t w, int64_t C, int64_t max_splits, int64_t& splits, int64_t& rps) {
+  const int64_t tile = weight_tile(w);
+  const int64_t nx = (C + tile - 1) / tile > 0 ? (C + tile - 1) / tile : 1;
+  const int64_t chunks = (N + 63) / 64;
+  int64_t s = (1024 + nx - 1) / nx;
+  if (s > chunks) s = chunks;
+  if (s > max_splits) s = max_splits;
+  if (s < 1) s = 1;
+  rps = ((chunks + s - 1) / s) * 64;
+  splits = rps > 0 ? (N + rps - 1) / rps : 1;
+  if (splits < 1) splits = 1;
+}
+
+int launch_dweight(const float* v, int64_t ldv, const float* dmix, int64_t N, int64_t w, int64_t C, int64_t splits,
+                   int64_t rps, float* partial, float* dM, hipStream_t stream) {
+  const int64_t tile = weight_tile(w), nx = (C + tile - 1) / tile;
+  if (N > 0 && nx > 0) {
+    const dim3 grid((unsigned)nx, (unsigned)splits), block(kThreads);
+    const int vec = aligned(v, 16) && ldv % 4 == 0;
+    switch (width_class(w)) {
+      case 16: hipLaunchKernelGGL(node_mix_dweight_k_kernel<16>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      case 32: hipLaunchKernelGGL(node_mix_dweight_k_kernel<32>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      case 64: hipLaunchKernelGGL(node_mix_dweight_k_kernel<64>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      default: hipLaunchKernelGGL(node_mix_dweight_kernel<128>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+    }
+    const int rc = check_launch("node_mix_backward_weight");
+    if (rc != GM_OK) return rc;
+  }
+  const int64_t n = w * C;
+  if (n > 0) {
+    const int64_t parts = (N > 0 && C > 0) ? splits * weight_partials_per_split(w) : (int64_t)0;
+    hipLaunchKernelGGL(node_mix_reduce_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       stream, partial, n, parts, dM);
+    return check_launch("node_mix_backward_weight (reduce)");
+  }
+  return GM_OK;
+}
+
+}  // namespace
+}  // namespace gm
+
+extern "C" int gm_node_mix_forward_f32(const float* v, int64_t ldv, const float* M, int64_t N, int64_t w, int64_t C,
+                                       float* out, void* stream) {
+  int rc = gm::check_shapes(N, w, C);
+  if (rc != GM_OK) return rc;
+  if (N == 0 || C == 0) return GM_OK;
+  GM_REQUIRE(v && M && out, "v, M and out must be device pointers");
+  GM_REQUIRE(ldv >= w, "ldv must be at least w");
+  const hipStream_t s = (hipStream_t)stream;
+  const int vec_v = gm::aligned(v, 16) && ldv % 4 == 0;
+  const int vec_out = gm::aligned(out, 16) && C % 4 == 0;
+  const int W = gm::width_class(w);
+  const int CT = W == 128 ? 2 : 4;
+  const int64_t nx = (C + 64 * CT - 1) / (64 * CT), n_tiles = (N + 63) / 64;
+  int64_t ny = (2048 + nx - 1) / nx;
+  if (ny > n_tiles) ny = n_tiles;
+  if (ny > 65535) ny = 65535;
+  const dim3 grid((unsigned)nx, (unsigned)ny), block(gm::kThreads);
+  switch (W) {
+    case 16: hipLaunchKernelGGL((gm::node_mix_forward_kernel<16, 4>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+    case 32: hipLaunchKernelGGL((gm::node_mix_forward_kernel<32, 4>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+    case 64: hipLaunchKernelGGL((gm::node_mix_forward_kernel<64, 4>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+    default: hipLaunchKernelGGL((gm::node_mix_forward_kernel<128, 2>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+  }
+  return gm::check_launch("node_mix_forward");
+}
+
+extern "C" int gm_node_mix_backward_input_f32(const float* dmix, const float* M, int64_t N, int64_t w, int64_t C,
+                                              float* dv, int64_t lddv, void* stream) {
+  int rc = gm::check_shapes(N, w, C);
+  if (rc != GM_OK) return rc;
+  if (N == 0) return GM_OK;
+  GM_REQUIRE(dv && lddv >= w, "dv must be a device pointer with lddv >= w");
+  GM_REQUIRE(C == 0 || (dmix && M), "dmix and M must be device pointers");
+  GM_REQUIRE(C % 4 == 0 && gm::aligned(dmix, 16) && gm::aligned(M, 16),
+             "dmix and M must be 16-byte aligned with C a multiple of 4");
+  const hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)((N + 127) / 128)), block(gm::kThreads);
+  switch (gm::width_class(w)) {
+    case 16: hipLaunchKernelGGL(gm::node_mix_dinput_kernel<16>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+    case 32: hipLaunchKernelGGL(gm::node_mix_dinput_kernel<32>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+    case 64: hipLaunchKernelGGL(gm::node_mix_dinput_kernel<64>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+    default: hipLaunchKernelGGL(gm::node_mix_dinput_kernel<128>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+  }
+  return gm::check_launch("node_mix_backward_input");
+}
+
+extern "C" int64_t gm_node_mix_weight_partials(int64_t N, int64_t w, int64_t C) {
+  int64_t splits = 1, rps = 64;
+  gm::weight_splits(N, w, C, 1 << 20, splits, rps);
+  return splits * gm::weight_partials_per_split(w) * w * C;
+}
+
+extern "C" int gm_node_mix_backward_weight_f32(const float* v, int64_t ldv, const float* dmix, int64_t N, int64_t w,
+                                               int64_t C, float* partial, float* dM, void* stream) {
+  int rc = gm::check_shapes(N, w, C);
+  if (rc != GM_OK) return rc;
+  if (w * C == 0) return GM_OK;
+  GM_REQUIRE(dM && partial, "partial and dM must be device pointers");
+  GM_REQUIRE(N == 0 || (v && dmix && ldv >= w), "v (ldv >= w) and dmix must be device pointers");
+  GM_REQUIRE(C % 4 == 0 && (N == 0 || gm::aligned(dmix, 16)), "dmix must be 16-byte aligned with C a multiple of 4");
+  int64_t splits = 1, rps = 64;
+  gm::weight_splits(N, w, C, 1 << 20, splits, rps);
+  return gm::launch_dweight(v, ldv, dmix, N, w, C, splits, rps, partial, dM, (hipStream_t)stream);
+}

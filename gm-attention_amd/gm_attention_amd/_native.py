@@ -53,6 +53,11 @@ SIGNATURES_F32 = {
     "gm_radial_trunk_forward_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_D, _P, _P]),
     "gm_radial_trunk_backward_f32": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_D, _P, _P, _P]),
     "gm_radial_trunk_partials": (ctypes.c_int64, [_I]),
+    "gm_node_mix_forward_f32": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P]),
+    "gm_node_mix_backward_input_f32": (ctypes.c_int, [_P, _P, _I, _I, _I, _P, _I, _P]),
+    "gm_node_mix_weight_partials": (ctypes.c_int64, [_I, _I, _I]),
+    "gm_node_mix_backward_weight_f32": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P]),
+    "gm_xcd_block_map": (ctypes.c_int, [_I, ctypes.c_int, _P, _I, ctypes.c_int, _P]),
     "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
                                         + [_P, _P]),
     "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
@@ -586,6 +591,53 @@ def radial_trunk_backward(dh: Tensor, rho: Tensor, weight: Tensor, bias: Tensor 
     _call("gm_radial_trunk_backward_f32", _ptr(dh), _ptr(rho), _ptr(weight), _ptr(bias) if bias is not None else None,
           _ptr(centers), rho.shape[0], H, T, B, float(width), _ptr(partial), _ptr(dparams), _stream(rho.device))
     return dparams[:, : T * B].reshape(H, T, B), dparams[:, T * B:]
+
+
+def _column_view(v: Tensor) -> tuple[int, int]:
+    """(rows, leading dimension) of a 2-D float32 view whose rows are evenly
+    strided and whose columns are contiguous (a column slice of flat rows)."""
+    _check(v.dim() == 2 and v.dtype == torch.float32 and v.device.type == "cuda",
+           "node vectors must be a 2-D float32 tensor on the GPU")
+    _check(v.stride(1) == 1 or v.shape[1] == 1, "node vectors must have contiguous columns")
+    return v.shape[0], (v.stride(0) if v.shape[0] > 1 else v.shape[1])
+
+
+def node_mix_forward(v: Tensor, m: Tensor) -> Tensor:
+    """``v (N, w) @ m (w, C)`` on MFMA: every head's node mixes for one input
+    frequency (``v`` may be a column slice of the flat node rows)."""
+    N, ldv = _column_view(v)
+    w, C = m.shape
+    _check(v.shape[1] == w and m.is_contiguous() and m.dtype == torch.float32 and m.device == v.device,
+           "the mixing matrix must be a contiguous float32 (w, C) on the node vectors' device")
+    out = torch.empty(N, C, dtype=torch.float32, device=v.device)
+    _call("gm_node_mix_forward_f32", _ptr(v), max(ldv, w), _ptr(m), N, w, C, _ptr(out), _stream(v.device))
+    return out
+
+
+def node_mix_backward_input(dmix: Tensor, m: Tensor, dv: Tensor) -> None:
+    """``dv (N, w) = dmix (N, C) @ m^T`` written into ``dv`` (a column slice of a
+    flat gradient is fine: its leading dimension is passed)."""
+    N, lddv = _column_view(dv)
+    w, C = m.shape
+    _require_device(dmix, m)
+    _check(dmix.shape == (N, C) and dv.shape[1] == w, "dmix must be (N, C) for m (w, C) and dv (N, w)")
+    _call("gm_node_mix_backward_input_f32", _ptr(dmix), _ptr(m), N, w, C, _ptr(dv), max(lddv, w), _stream(dv.device))
+
+
+def node_mix_backward_weight(v: Tensor, dmix: Tensor) -> Tensor:
+    """``v^T (w, N) @ dmix (N, C)`` summed over row ranges in a fixed order."""
+    N, ldv = _column_view(v)
+    w = v.shape[1]
+    _require_device(dmix)
+    C = dmix.shape[1]
+    _check(dmix.shape[0] == N, "dmix must have the node vectors' rows")
+    lib = library()
+    partial = torch.empty(max(int(lib.gm_node_mix_weight_partials(N, w, C)), 1), dtype=torch.float32,
+                          device=dmix.device)
+    dm = torch.empty(w, C, dtype=torch.float32, device=dmix.device)
+    _call("gm_node_mix_backward_weight_f32", _ptr(v), max(ldv, w), _ptr(dmix), N, w, C, _ptr(partial), _ptr(dm),
+          _stream(dmix.device))
+    return dm
 
 
 def _check_order(group_order: Tensor | None, group_source: Tensor) -> None:

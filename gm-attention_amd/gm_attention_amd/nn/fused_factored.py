@@ -673,6 +673,22 @@ def node_vectors(x: SO2FeatureField, hp: HeadsPlan) -> list[Tensor]:
     return [x[0] if n == 0 else x[n].reshape(n_nodes, -1) for n, *_ in hp.groups]
 
 
+def heads_mixes(x: SO2FeatureField, hp: HeadsPlan, mats: list[Tensor]) -> list[Tensor]:
+    """Every head's node mixes, one ``(N, H K C_n)`` array per input frequency:
+    the MFMA node-mix kernels on the flat rows where they serve the call
+    (:class:`node_products.NodeMixes`), else one matrix product per frequency."""
+    from gm_attention_amd.nn.node_products import NodeMixes, mixes_eligible
+
+    rows = x._rows()
+    slices = x.field_type.slices()
+    columns = tuple((slices[n].start, slices[n].stop - slices[n].start) for n, *_ in hp.groups)
+    if mixes_eligible(rows, [w for _, w in columns], mats):
+        return list(NodeMixes.apply(rows, columns, *[m.to(torch.float32) for m in mats]))
+    vecs = node_vectors(x, hp)
+    with torch.profiler.record_function("gm::kernel/node_products"):
+        return [v @ m.to(v.dtype) for v, m in zip(vecs, mats, strict=True)]
+
+
 class FactoredHeads(torch.autograd.Function):
     """Every head's factored value aggregation on the mixes ``X_n M_n``.
 
@@ -952,10 +968,7 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
     ok, pa, pt = grouped_eligible(hp, dtype, K)
     if ok:
         p = hp.plan
-        mats = heads_mixing(kernels, hp)
-        vecs = node_vectors(x, hp)
-        with torch.profiler.record_function("gm::kernel/node_products"):
-            mixes = [v @ m.to(v.dtype) for v, m in zip(vecs, mats, strict=True)]
+        mixes = heads_mixes(x, hp, heads_mixing(kernels, hp))
         order, group_ptr, group_source = groups
         st = grouped_streams(edges, order, kernels[0].radial_basis.cutoff, pa, pt, dtype)
         fused = FUSED_TRUNK and trunk is not None and _lanes_apply(kernels[0], hp, pa, pt)
@@ -997,10 +1010,7 @@ def _forward_aggregated_heads_seg(kernels: list[Any], x: SO2FeatureField, edges:
     """Every head's ``forward_factored_aggregated`` at once: ``(N, H, d_out)``."""
     hp = heads_plan(kernels[0])
     p = hp.plan
-    mats = heads_mixing(kernels, hp)
-    vecs = node_vectors(x, hp)
-    with torch.profiler.record_function("gm::kernel/node_products"):
-        mixes = [v @ m.to(v.dtype) for v, m in zip(vecs, mats, strict=True)]
+    mixes = heads_mixes(x, hp, heads_mixing(kernels, hp))
     order, group_ptr, group_source = groups
     angular = torch.view_as_real(edges.angular_phases.contiguous()).contiguous().to(h.dtype)
     transport = torch.view_as_real(edges.transport_phases.contiguous()).contiguous().to(h.dtype)

@@ -486,6 +486,32 @@ int gm_radial_trunk_backward_f32(const float* dh, const float* rho, const float*
                                  const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B, double width,
                                  float* partial, float* dparams, void* stream);
 
+/* ---------------- node mixes (the factored kernel's channel mixing) ----------------
+ *
+ * Every head's node mixes for one input frequency n as one real product over
+ * the nodes: mix (N, C) = v (N, w) M (w, C), v the node field's frequency-n
+ * reals (row stride ldv, columns contiguous: a column slice of the flat rows),
+ * M the heads' mixing matrix (each block's complex product and input
+ * conjugation as reals; C = H K C_n), 1 <= w <= 128, fp32, on MFMA.
+ * Replaces the reference's node_products, one complex einsum("ja,bat->jtb")
+ * per node vector over _block_weights (nn/kernels.py:575-603, :506-536),
+ * for all heads of a layer at once. */
+int gm_node_mix_forward_f32(const float* v, int64_t ldv, const float* M, int64_t N, int64_t w, int64_t C, float* out,
+                            void* stream);
+
+/* Its input gradient dv (N, w) = dmix (N, C) M^T, written into dv (row stride
+ * lddv, only its w columns touched); C a multiple of 4, dmix and M 16-byte
+ * aligned.  The reference takes it from autograd through the einsum. */
+int gm_node_mix_backward_input_f32(const float* dmix, const float* M, int64_t N, int64_t w, int64_t C, float* dv,
+                                   int64_t lddv, void* stream);
+
+/* Its weight gradient dM (w, C) = v^T dmix, summed over row ranges into
+ * `partial` (a workspace of gm_node_mix_weight_partials(N, w, C) floats) and
+ * then over the ranges in a fixed order: deterministic.  C a multiple of 4. */
+int64_t gm_node_mix_weight_partials(int64_t N, int64_t w, int64_t C);
+int gm_node_mix_backward_weight_f32(const float* v, int64_t ldv, const float* dmix, int64_t N, int64_t w, int64_t C,
+                                    float* partial, float* dM, void* stream);
+
 /* Every head's aggregate at once: out[i, h, :] = sum over target i's edges e
  * (CSR order) of alpha[e, h] rows[h, inv[e], :].  rows (H, n_edges, d_out)
  * holds each head's rows in the grouping's order (inv[e] = edge e's position

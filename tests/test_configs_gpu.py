@@ -15,10 +15,8 @@ The oracle evaluates the value kernels in the factored order (the node
 products gathered to the edges), which the regrouping identity pins to the
 per-edge readout (tests/test_oracle_factored.py).
 
-Tolerances (float32): the output elementwise within 1e-5 |want| + 1e-6, the
-input gradient within DX_BOUND times that (its value path contracts every
-head's node-mix gradient, ~4500 columns an input frequency, in one fp32
-product); a parameter gradient, a sum over every edge or node whose entries
+Tolerances (float32): the output and the input gradient elementwise within
+1e-5 |want| + 1e-6 (the ratio is printed); a parameter gradient, a sum over every edge or node whose entries
 can cancel to far below the summands, within 1e-5 of its norm and of its
 largest entry (the elementwise figure is printed: the reference's own eager
 path in float32 reaches 8.7x the elementwise bound on these sums at 16x32,
@@ -44,9 +42,6 @@ def strict_report(got, want):
     north star's elementwise bound."""
     got, want = got.detach().double().cpu(), want.detach().double().cpu()
     return float(((got - want).abs() / (1e-5 * want.abs() + 1e-6)).max())
-
-
-DX_BOUND = 1.5
 
 
 def assert_strict(got, want, name, bound=1.0):
@@ -104,7 +99,7 @@ def compare_mhsa(mhsa, x, edges, cuda, backward=True):
     if not backward:
         return
     print(f"  dx elementwise {strict_report(got[1], want[1]):.2f}", flush=True)
-    assert_strict(got[1], want[1], "dx", DX_BOUND)
+    assert_strict(got[1], want[1], "dx")
     assert set(got[2]) == set(want[2]) and len(want[2]) > 0
     for name in want[2]:
         assert_reduction(got[2][name], want[2][name], f"d{name}")
