@@ -31,7 +31,14 @@
 //   partials in a fixed order.  No atomics anywhere: results are deterministic.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "common.hpp"
+
+// The weight gradient's partials for gm_node_mix_backward_weight_noalloc_f32:
+// 2^23 floats (32 MiB) on every GPU the library runs on, held until the process
+// ends.  Host code reaches it only through the per-device address below.
+static __device__ __align__(256) float scratch[int64_t(1) << 23];
 
 namespace gm {
 namespace {
@@ -520,6 +527,30 @@ int launch_dweight(const float* v, int64_t ldv, const float* dmix, int64_t N, in
   return GM_OK;
 }
 
+constexpr int64_t kScratchFloats = int64_t(1) << 23;
+constexpr int kMaxDevices = 64;
+
+// Each device's address of `scratch`, looked up once with that device current.
+std::mutex scratch_mutex;
+float* scratch_address[kMaxDevices] = {};
+
+int scratch_on_current_device(float** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(GM_ERR_LAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(err));
+  GM_REQUIRE(device >= 0 && device < kMaxDevices, "the current device index is out of the scratch table's range");
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_address[device] == nullptr) {
+    void* address = nullptr;
+    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || address == nullptr)
+      return fail(GM_ERR_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(err));
+    scratch_address[device] = static_cast<float*>(address);
+  }
+  *out = scratch_address[device];
+  return GM_OK;
+}
+
 }  // namespace
 }  // namespace gm
 
@@ -585,5 +616,27 @@ extern "C" int gm_node_mix_backward_weight_f32(const float* v, int64_t ldv, cons
   GM_REQUIRE(C % 4 == 0 && (N == 0 || gm::aligned(dmix, 16)), "dmix must be 16-byte aligned with C a multiple of 4");
   int64_t splits = 1, rps = 64;
   gm::weight_splits(N, w, C, 1 << 20, splits, rps);
+  return gm::launch_dweight(v, ldv, dmix, N, w, C, splits, rps, partial, dM, (hipStream_t)stream);
+}
+
+extern "C" int gm_node_mix_backward_weight_noalloc_f32(const float* v, int64_t ldv, const float* dmix, int64_t N,
+                                                       int64_t w, int64_t C, float* dM, void* stream) {
+  int rc = gm::check_shapes(N, w, C);
+  if (rc != GM_OK) return rc;
+  if (w * C == 0) return GM_OK;
+  GM_REQUIRE(dM, "dM must be a device pointer");
+  GM_REQUIRE(N == 0 || (v && dmix && ldv >= w), "v (ldv >= w) and dmix must be device pointers");
+  GM_REQUIRE(C % 4 == 0 && (N == 0 || gm::aligned(dmix, 16)), "dmix must be 16-byte aligned with C a multiple of 4");
+  const int64_t per_split = gm::weight_partials_per_split(w) * w * C;
+  GM_REQUIRE(per_split <= gm::kScratchFloats,
+             "w * C is too large for the no-allocation weight gradient: its partials need " +
+                 std::to_string(per_split) + " floats a row split, the scratch holds " +
+                 std::to_string(gm::kScratchFloats));
+  float* partial = nullptr;
+  rc = gm::scratch_on_current_device(&partial);
+  if (rc != GM_OK) return rc;
+  // as many row splits as the scratch holds (every partial is written in full: nothing to clear)
+  int64_t splits = 1, rps = 64;
+  gm::weight_splits(N, w, C, gm::kScratchFloats / per_split, splits, rps);
   return gm::launch_dweight(v, ldv, dmix, N, w, C, splits, rps, partial, dM, (hipStream_t)stream);
 }

@@ -57,6 +57,7 @@ SIGNATURES_F32 = {
     "gm_node_mix_backward_input_f32": (ctypes.c_int, [_P, _P, _I, _I, _I, _P, _I, _P]),
     "gm_node_mix_weight_partials": (ctypes.c_int64, [_I, _I, _I]),
     "gm_node_mix_backward_weight_f32": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P]),
+    "gm_node_mix_backward_weight_noalloc_f32": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P]),
     "gm_xcd_block_map": (ctypes.c_int, [_I, ctypes.c_int, _P, _I, ctypes.c_int, _P]),
     "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
                                         + [_P, _P]),

@@ -512,6 +512,18 @@ int64_t gm_node_mix_weight_partials(int64_t N, int64_t w, int64_t C);
 int gm_node_mix_backward_weight_f32(const float* v, int64_t ldv, const float* dmix, int64_t N, int64_t w, int64_t C,
                                     float* partial, float* dM, void* stream);
 
+/* gm_node_mix_backward_weight_f32 without a workspace argument and without
+ * allocating: no counterpart in the reference; for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The partials live in a 32 MiB
+ * (2^23-float) device array of the library, one per GPU, held until the
+ * process ends; every call on a GPU uses that GPU's array, so calls that
+ * overlap on one GPU (different streams, or other host threads) race.  Fails
+ * with GM_ERR_ARGUMENT when w * C * (w <= 64 ? 4 : 1) exceeds 2^23.  Sums in
+ * a different split order than the workspace form (same bar, not bitwise). */
+int gm_node_mix_backward_weight_noalloc_f32(const float* v, int64_t ldv, const float* dmix, int64_t N, int64_t w,
+                                            int64_t C, float* dM, void* stream);
+
 /* Every head's aggregate at once: out[i, h, :] = sum over target i's edges e
  * (CSR order) of alpha[e, h] rows[h, inv[e], :].  rows (H, n_edges, d_out)
  * holds each head's rows in the grouping's order (inv[e] = edge e's position
