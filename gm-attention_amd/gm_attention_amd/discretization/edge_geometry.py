@@ -131,6 +131,47 @@ class EdgeGeometry:
                             rep(self.polar_angles), rep(self.transport_angles), rep(self.tangent_quadrature_weights),
                             rep(self.angular_phases), rep(self.transport_phases))
 
+    # ---- target-range chunks (the decomposition of forward_chunked)
+
+    def host_row_ptr(self) -> np.ndarray:
+        """``row_ptr`` on the host, read from the device once per edge set."""
+        held = self.__dict__.get("_host_row_ptr")
+        if held is None:
+            held = self.row_ptr.detach().to("cpu").numpy()
+            self.__dict__["_host_row_ptr"] = held
+        return held
+
+    def target_range(self, e0: int, e1: int) -> EdgeGeometry:
+        """The edges ``[e0, e1)`` -- whole neighbourhoods of consecutive targets --
+        as an edge set over the same nodes: every per-edge table a view of this
+        one's, the rows of the other targets empty.  The result records
+        ``(self, e0, e1)`` (:meth:`span`), so tables built for this edge set can
+        be sliced for it instead of rebuilt."""
+        part = slice(e0, e1)
+        chunk = EdgeGeometry(self.edge_index[:, part], (self.row_ptr - e0).clamp(0, e1 - e0),
+                             self.log_coordinates[part], self.distances[part], self.polar_angles[part],
+                             self.transport_angles[part], self.tangent_quadrature_weights[part],
+                             self.angular_phases[part], self.transport_phases[part])
+        chunk.__dict__["_span"] = (self, int(e0), int(e1))
+        return chunk
+
+    def span(self) -> tuple[EdgeGeometry, int, int] | None:
+        """``(parent, e0, e1)`` for an edge set made by :meth:`target_range`, else ``None``."""
+        return self.__dict__.get("_span")
+
+    def chunks(self, chunk_size: int):
+        """Consecutive ranges of at most ``chunk_size`` targets with their whole
+        neighbourhoods, as :meth:`target_range` edge sets; ranges without edges
+        are skipped.  The bounds come from one host copy of ``row_ptr``."""
+        if chunk_size < 1:
+            raise ValueError(f"chunk_size must be at least 1, got {chunk_size}.")
+        ptr = self.host_row_ptr()
+        n = ptr.shape[0] - 1
+        for first in range(0, n, chunk_size):
+            e0, e1 = int(ptr[first]), int(ptr[min(n, first + chunk_size)])
+            if e1 > e0:
+                yield self.target_range(e0, e1)
+
     def to(self, device=None, dtype=None) -> EdgeGeometry:
         real = self.distances.dtype if dtype is None else dtype
         cplx = complex_dtype(real)

@@ -1,20 +1,23 @@
 """Grid chains for hierarchical models: levels and the bipartite transfers between them.
 
-Restates the reference's ``discretization/grids/equiangular.py:37-253``:
-``TensorGridLevel`` (a grid, its frames and, when operators run on it, its
-same-grid discretization), ``TensorGridHierarchy`` (levels finest first,
-``down_edges[k]`` restricting level k onto k + 1, ``up_edges[k]``
-interpolating level k + 1 onto level 0, optional ``lateral_edges[k]`` from
-k + 2 onto k + 1; ``tile`` and ``to``) and ``build_grid_hierarchy``.  Every
-transfer is a radius-based bipartite edge set
-(``edge_geometry.compute_bipartite_edge_geometry``): on the GPU when the
-grids' nodes are there, with the same integers as the host's KD-tree search.
+Stands for the reference's ``discretization/grids/equiangular.py:37-253``
+(``TensorGridLevel``, ``TensorGridHierarchy`` with ``tile`` / ``to``,
+``build_grid_hierarchy``): the same classes, fields and builder signature, so
+the encoder blocks and a model's step function use them unchanged.  Levels
+are finest first; ``down_edges[k]`` restricts level k onto level k + 1,
+``up_edges[k]`` interpolates level k + 1 back onto level 0 and the optional
+``lateral_edges[k]`` interpolates level k + 2 onto level k + 1.
+
+Here every transfer is described as a hop ``(source level, target level,
+cutoff)`` and built by one radius search
+(``edge_geometry.compute_bipartite_edge_geometry``: on the GPU when the grids'
+nodes are there, with the host KD-tree search's integers); ``tile`` and ``to``
+map one structural transform over every level and every transfer.
 """
 
 from __future__ import annotations
 
-import itertools
-from collections.abc import Sequence
+from collections.abc import Callable, Sequence
 from dataclasses import dataclass
 
 from torch import Tensor
@@ -31,6 +34,9 @@ from gm_attention_amd.discretization.grid import SphericalGrid
 
 @dataclass(frozen=True)
 class TensorGridLevel:
+    """One grid of the chain: its shape label, kind, nodes, tangent frames and,
+    when operators run on it, its same-grid discretization (else ``None``)."""
+
     shape: tuple[int, ...]
     grid_kind: str
     grid: SphericalGrid
@@ -42,9 +48,13 @@ class TensorGridLevel:
         return self.grid.n_nodes
 
     def describe(self) -> str:
-        if self.grid_kind == "icosphere":
-            return f"icosphere L{self.shape[0]}"
-        return f"{self.shape[0]}x{self.shape[1]} {self.grid_kind}"
+        """A label for logs: ``L<k> icosphere`` levels by subdivision, tensor grids by ``nlat x nlon``."""
+        label = "x".join(str(s) for s in self.shape)
+        return f"icosphere L{label}" if self.grid_kind == "icosphere" else f"{label} {self.grid_kind}"
+
+    def _mapped(self, grid: Callable, frames: Callable, disc: Callable) -> TensorGridLevel:
+        return TensorGridLevel(self.shape, self.grid_kind, grid(self.grid), frames(self.frames),
+                               None if self.discretization is None else disc(self.discretization))
 
 
 @dataclass(frozen=True)
@@ -62,37 +72,68 @@ class TensorGridHierarchy:
     def finest(self) -> TensorGridLevel:
         return self.levels[0]
 
+    def _sources(self) -> dict[str, list[int]]:
+        """The source level of every transfer, per transfer family."""
+        return {"down": list(range(self.depth)), "up": [k + 1 for k in range(self.depth)],
+                "lateral": [k + 2 for k in range(len(self.lateral_edges))]}
+
+    def _mapped(self, level_fn: Callable[[TensorGridLevel], TensorGridLevel],
+                edge_fn: Callable[[EdgeGeometry, int], EdgeGeometry]) -> TensorGridHierarchy:
+        src = self._sources()
+        return TensorGridHierarchy(
+            tuple(level_fn(level) for level in self.levels),
+            tuple(edge_fn(e, s) for e, s in zip(self.down_edges, src["down"], strict=True)),
+            tuple(edge_fn(e, s) for e, s in zip(self.up_edges, src["up"], strict=True)),
+            tuple(edge_fn(e, s) for e, s in zip(self.lateral_edges, src["lateral"], strict=True)))
+
     def tile(self, count: int) -> TensorGridHierarchy:
-        """The hierarchy of ``count`` samples as one disjoint graph: node
-        ``b * n + i`` of a level is node ``i`` of sample ``b``."""
+        """``count`` samples as one disjoint graph: node ``b * n + i`` of a
+        level is node ``i`` of sample ``b``, every transfer within its sample;
+        ``count == 1`` is the hierarchy itself."""
         count = int(count)
         if count == 1:
             return self
-        levels = tuple(
-            TensorGridLevel(level.shape, level.grid_kind, level.grid.tile(count), level.frames.repeat(count, 1, 1),
-                            None if level.discretization is None else level.discretization.tile(count))
-            for level in self.levels)
-        return TensorGridHierarchy(
-            levels,
-            tuple(e.tile(count, n_sources=self.levels[k].n_nodes) for k, e in enumerate(self.down_edges)),
-            tuple(e.tile(count, n_sources=self.levels[k + 1].n_nodes) for k, e in enumerate(self.up_edges)),
-            tuple(e.tile(count, n_sources=self.levels[k + 2].n_nodes) for k, e in enumerate(self.lateral_edges)))
+        return self._mapped(
+            lambda level: level._mapped(lambda g: g.tile(count), lambda f: f.repeat(count, 1, 1),
+                                        lambda d: d.tile(count)),
+            lambda e, source: e.tile(count, n_sources=self.levels[source].n_nodes))
 
     def to(self, device) -> TensorGridHierarchy:
-        return TensorGridHierarchy(
-            tuple(TensorGridLevel(level.shape, level.grid_kind, level.grid.to(device=device),
-                                  level.frames.to(device=device),
-                                  None if level.discretization is None else level.discretization.to(device=device))
-                  for level in self.levels),
-            tuple(e.to(device) for e in self.down_edges), tuple(e.to(device) for e in self.up_edges),
-            tuple(e.to(device) for e in self.lateral_edges))
+        return self._mapped(
+            lambda level: level._mapped(lambda g: g.to(device=device), lambda f: f.to(device=device),
+                                        lambda d: d.to(device=device)),
+            lambda e, _source: e.to(device))
 
 
-def _transfer(source: TensorGridLevel, target: TensorGridLevel, cutoff: float, max_frequency: int) -> EdgeGeometry:
+def _hop(levels: Sequence[TensorGridLevel], source: int, target: int, cutoff: float,
+         max_frequency: int) -> EdgeGeometry:
+    """Edges from every node of level ``source`` within ``cutoff`` of a node of level ``target``."""
+    s, t = levels[source], levels[target]
     return compute_bipartite_edge_geometry(
-        source.grid.nodes, source.frames, source.grid.quadrature_weights, target.grid.nodes, target.frames,
-        cutoff=float(cutoff), max_frequency=max_frequency, source_exact_nodes=source.grid.exact_nodes,
-        target_exact_nodes=target.grid.exact_nodes)
+        s.grid.nodes, s.frames, s.grid.quadrature_weights, t.grid.nodes, t.frames, cutoff=float(cutoff),
+        max_frequency=max_frequency, source_exact_nodes=s.grid.exact_nodes, target_exact_nodes=t.grid.exact_nodes)
+
+
+def _problems(grids, grid_kinds, shapes, restrict_cutoffs, interpolate_cutoffs, local_cutoffs, frames,
+              lateral_cutoffs) -> list[str]:
+    """Everything wrong with a hierarchy's arguments (empty when it can be built)."""
+    n = len(grids)
+    if n < 2:
+        return [f"a hierarchy has at least two levels ({n} grids given)"]
+    found = []
+    per_level = {"grid_kinds": grid_kinds, "shapes": shapes, "local_cutoffs": local_cutoffs}
+    if frames is not None:
+        per_level["frames"] = frames
+    found += [f"{name} has {len(seq)} entries for {n} levels" for name, seq in per_level.items() if len(seq) != n]
+    per_hop = {"restrict_cutoffs": restrict_cutoffs, "interpolate_cutoffs": interpolate_cutoffs}
+    found += [f"{name} has {len(seq)} entries for {n - 1} hops" for name, seq in per_hop.items() if len(seq) != n - 1]
+    if lateral_cutoffs is not None and len(lateral_cutoffs) != n - 2:
+        found.append(f"lateral_cutoffs has {len(lateral_cutoffs)} entries for the {n - 2} hops after the first")
+    found += [f"level {k + 1} ({grids[k + 1].n_nodes} nodes) is not coarser than level {k} ({grids[k].n_nodes})"
+              for k in range(n - 1) if grids[k + 1].n_nodes >= grids[k].n_nodes]
+    found += [f"local_cutoffs[{k}] is an empty list (None means no operator on that level)"
+              for k, radii in enumerate(local_cutoffs) if radii is not None and len(radii) == 0]
+    return found
 
 
 def build_grid_hierarchy(grids: Sequence[SphericalGrid], grid_kinds: Sequence[str], shapes: Sequence[tuple[int, ...]],
@@ -100,42 +141,25 @@ def build_grid_hierarchy(grids: Sequence[SphericalGrid], grid_kinds: Sequence[st
                          local_cutoffs: Sequence[Sequence[float] | None], frames: Sequence[Tensor | None] | None = None,
                          max_frequency: int = DEFAULT_MAX_FREQUENCY,
                          lateral_cutoffs: Sequence[float] | None = None) -> TensorGridHierarchy:
-    """The hierarchy over prebuilt grids, finest first (reference equiangular.py:145-253)."""
-    n_levels = len(grids)
-    if n_levels < 2:
-        raise ValueError(f"a hierarchy needs at least two levels, got {n_levels}.")
-    if len(grid_kinds) != n_levels or len(local_cutoffs) != n_levels or len(shapes) != n_levels:
-        raise ValueError("grid_kinds, shapes and local_cutoffs need one entry per level "
-                         f"({n_levels}), got {len(grid_kinds)}, {len(shapes)} and {len(local_cutoffs)}.")
-    n_hops = n_levels - 1
-    if len(restrict_cutoffs) != n_hops or len(interpolate_cutoffs) != n_hops:
-        raise ValueError(f"restrict_cutoffs and interpolate_cutoffs need one entry per hop ({n_hops}), got "
-                         f"{len(restrict_cutoffs)} and {len(interpolate_cutoffs)}.")
-    for fine, coarse in itertools.pairwise(grids):
-        if coarse.n_nodes >= fine.n_nodes:
-            raise ValueError(f"levels must be strictly coarser than their predecessor, got {fine.n_nodes} -> "
-                             f"{coarse.n_nodes} nodes.")
-    if frames is not None and len(frames) != n_levels:
-        raise ValueError(f"frames needs one entry per level ({n_levels}), got {len(frames)}.")
+    """The hierarchy over prebuilt grids, finest first (reference equiangular.py:145-253): each level's
+    frames (given or built), its discretization prepared for its local radii when it has any, and the
+    restriction, interpolation and (optional) lateral transfers."""
+    problems = _problems(grids, grid_kinds, shapes, restrict_cutoffs, interpolate_cutoffs, local_cutoffs, frames,
+                         lateral_cutoffs)
+    if problems:
+        raise ValueError("cannot build the grid hierarchy: " + "; ".join(problems) + ".")
     levels = []
-    for index, (grid, kind, shape) in enumerate(zip(grids, grid_kinds, shapes, strict=True)):
-        override = frames[index] if frames is not None else None
-        level_frames = override if override is not None else build_tangent_frames(grid.nodes)
-        radii = local_cutoffs[index]
+    for k, grid in enumerate(grids):
+        given = frames[k] if frames is not None else None
+        level_frames = build_tangent_frames(grid.nodes) if given is None else given
+        radii = local_cutoffs[k]
         disc = None
         if radii is not None:
-            if not radii:
-                raise ValueError(f"local_cutoffs[{index}] is empty; pass None for no operator.")
-            disc = SphericalDiscretization.from_grid(grid, max(radii), frames=level_frames,
-                                                     max_frequency=max_frequency)
+            disc = SphericalDiscretization.from_grid(grid, max(radii), frames=level_frames, max_frequency=max_frequency)
             disc.prepare_windows(radii)
-        levels.append(TensorGridLevel(tuple(shape), kind, grid, level_frames, disc))
-    down = tuple(_transfer(levels[h], levels[h + 1], restrict_cutoffs[h], max_frequency) for h in range(n_hops))
-    up = tuple(_transfer(levels[h + 1], levels[0], interpolate_cutoffs[h], max_frequency) for h in range(n_hops))
-    lateral: tuple[EdgeGeometry, ...] = ()
-    if lateral_cutoffs is not None:
-        if len(lateral_cutoffs) != n_hops - 1:
-            raise ValueError(f"lateral_cutoffs needs one entry per hop after the first ({n_hops - 1}), got "
-                             f"{len(lateral_cutoffs)}.")
-        lateral = tuple(_transfer(levels[h + 2], levels[h + 1], c, max_frequency) for h, c in enumerate(lateral_cutoffs))
+        levels.append(TensorGridLevel(tuple(shapes[k]), grid_kinds[k], grid, level_frames, disc))
+    hops = len(grids) - 1
+    down = tuple(_hop(levels, k, k + 1, restrict_cutoffs[k], max_frequency) for k in range(hops))
+    up = tuple(_hop(levels, k + 1, 0, interpolate_cutoffs[k], max_frequency) for k in range(hops))
+    lateral = tuple(_hop(levels, k + 2, k + 1, c, max_frequency) for k, c in enumerate(lateral_cutoffs or ()))
     return TensorGridHierarchy(tuple(levels), down, up, lateral)

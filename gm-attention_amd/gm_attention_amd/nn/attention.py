@@ -70,6 +70,11 @@ def weighted_segment_sum(weight: Tensor, messages: dict[int, Tensor], row_ptr: T
             for f, m in messages.items()}
 
 
+def sum_partials(partials: list[dict[int, Tensor]]) -> dict[int, Tensor]:
+    """Per frequency, the sum of the target ranges' outputs (each zero off its range)."""
+    return {f: functools.reduce(torch.add, [p[f] for p in partials]) for f in partials[0]}
+
+
 def _checkpointed(module: nn.Module, compute):
     if module.training and torch.is_grad_enabled() and REMATERIALIZE_CHUNKS:
         return torch.utils.checkpoint.checkpoint(compute, use_reentrant=False)
@@ -129,29 +134,17 @@ class SO2Attention(nn.Module):
         return self.value.forward_factored_aggregated(x, edges, alpha, products, groups).coefficients
 
     def forward_chunked(self, x: SO2FeatureField, edges, *, chunk_size: int) -> SO2FeatureField:
-        """:meth:`forward` one range of target nodes at a time (:344-402)."""
-        if chunk_size < 1:
-            raise ValueError(f"chunk_size must be at least 1, got {chunk_size}.")
+        """:meth:`forward` over consecutive ranges of at most ``chunk_size``
+        targets with their whole neighbourhoods (reference :344-402), the node
+        mixes formed once for every range; under training each range is
+        recomputed in the backward rather than kept."""
         edges = _resolve_edges(edges, self.cutoff)
         _validate_node_field(x, self.field_type_in, edges)
-        n_nodes = edges.row_ptr.shape[0] - 1
         products = self.value.node_products(x) if kernels.factored_enabled() else None
-        totals: dict[int, Tensor] = {}
-        for start in range(0, n_nodes, chunk_size):
-            stop = min(start + chunk_size, n_nodes)
-            first, last = int(edges.row_ptr[start]), int(edges.row_ptr[stop])
-            if first == last:
-                continue
-            chunk = edges.select(torch.arange(first, last, device=edges.row_ptr.device))
-            fused_attention.register_chunk(chunk, edges, first, last)
-            groups = fused_factored.source_groups(chunk.source_index, fused_factored.group_key(edges, first, last),
-                                                  owner=edges.edge_index)
-            partial = _checkpointed(self, functools.partial(self._attend, x, chunk, products, groups))
-            for f, v in partial.items():
-                totals[f] = v if f not in totals else totals[f] + v
-        if not totals:
-            return self._finish(x, self._attend(x, edges))
-        return self._finish(x, totals)
+        partials = [_checkpointed(self, functools.partial(self._attend, x, chunk, products,
+                                                          fused_factored.groups_for(chunk, chunk.source_index)))
+                    for chunk in edges.chunks(chunk_size)]
+        return self._finish(x, sum_partials(partials) if partials else self._attend(x, edges))
 
     def _finish(self, x: SO2FeatureField, outputs: dict[int, Tensor]) -> SO2FeatureField:
         attended = SO2FeatureField(self.field_type_out, outputs)

@@ -30,7 +30,7 @@ from torch import Tensor, nn
 
 from gm_attention_amd.discretization.discretization import SphericalDiscretization
 from gm_attention_amd.nn import depthwise_radial, fused_attention, fused_factored, kernels
-from gm_attention_amd.nn.attention import gather_to_edges, weighted_segment_sum
+from gm_attention_amd.nn.attention import gather_to_edges, sum_partials, weighted_segment_sum
 from gm_attention_amd.nn.depthwise import SO2DepthwiseKernel, stacked_coefficients
 from gm_attention_amd.nn.kernels import SO2SteerableKernel
 from gm_attention_amd.nn.linear import SO2Linear
@@ -130,29 +130,20 @@ class SO2Convolution(nn.Module):
         return SO2FeatureField.from_flat(self.field_type_out, flat).coefficients
 
     def forward_chunked(self, x: SO2FeatureField, edges, *, chunk_size: int) -> SO2FeatureField:
-        """:meth:`forward` one range of whole target neighbourhoods at a time (:357-430)."""
-        if chunk_size < 1:
-            raise ValueError(f"chunk_size must be at least 1, got {chunk_size}.")
+        """:meth:`forward` over consecutive ranges of at most ``chunk_size``
+        targets with their whole neighbourhoods (reference :357-430), the node
+        mixes of a general kernel formed once; under training each range is
+        recomputed in the backward rather than kept."""
         edges = self._check(x, edges)
-        n_nodes = edges.row_ptr.shape[0] - 1
         factored = isinstance(self.kernel, SO2SteerableKernel) and kernels.factored_enabled()
         products = self.kernel.node_products(x) if factored else None
-        totals: dict[int, Tensor] = {}
-        for start in range(0, n_nodes, chunk_size):
-            stop = min(start + chunk_size, n_nodes)
-            first, last = int(edges.row_ptr[start]), int(edges.row_ptr[stop])
-            if first == last:
-                continue
-            chunk = edges.select(torch.arange(first, last, device=edges.row_ptr.device))
-            fused_attention.register_chunk(chunk, edges, first, last)
-            groups = (fused_factored.source_groups(chunk.source_index, fused_factored.group_key(edges, first, last),
-                                                   owner=edges.edge_index) if factored else None)
-            partial = _checkpointed(self, functools.partial(self._aggregate, x, chunk, products, groups))
-            for f, v in partial.items():
-                totals[f] = v if f not in totals else totals[f] + v
-        if not totals:
-            return self._finish(x, self._aggregate(x, edges))
-        return self._finish(x, totals)
+
+        def part(chunk):
+            groups = fused_factored.groups_for(chunk, chunk.source_index) if factored else None
+            return _checkpointed(self, functools.partial(self._aggregate, x, chunk, products, groups))
+
+        partials = [part(chunk) for chunk in edges.chunks(chunk_size)]
+        return self._finish(x, sum_partials(partials) if partials else self._aggregate(x, edges))
 
     def _finish(self, x: SO2FeatureField, outputs: dict[int, Tensor]) -> SO2FeatureField:
         aggregated = SO2FeatureField(self.field_type_out, outputs)

@@ -3,8 +3,8 @@
 The drop-in for the reference's ``gm_attention/nn/fused_attention.py``: the
 same switch (``GM_FUSED_ATTENTION``, read at import: ``"0"`` off, ``"1"`` on for
 device tensors, ``"cpu"`` accepted for compatibility), the same ``Plan`` /
-``descriptors`` layout (:74-123), the same per-edge ``Geometry`` constants and
-cache (:126-255), the same eligibility predicates (:258-326) and the same
+``descriptors`` layout (:74-123), the same per-edge ``Geometry`` constants
+(:126-255), the same eligibility predicates (:258-326) and the same
 autograd Functions ``Softmax`` (:371-397) and ``Depthwise`` (:329-353), so the
 attention and convolution layers call it unchanged.  The arithmetic runs in
 ``libgmhip.so`` (``_native.attention()``); there is no CPU driver, so a CPU
@@ -15,17 +15,18 @@ semantics: no neighbourhood-size bound (the reference declines when
 ``max_degree * heads > 8192``, which excludes the 256x512 grid); the key and
 value gradients are gathered per source node instead of added atomically,
 so they are deterministic; the geometry keeps a copy of the transport table
-narrowed to the orders a layer reads.
+narrowed to the orders a layer reads; the per-edge tables live on the edge
+set they describe (built once, dropped with it) instead of a process-wide
+cache.
 """
 
 from __future__ import annotations
 
 import os
-import weakref
-from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Any
 
+import numpy as np
 import torch
 from torch import Tensor
 
@@ -112,112 +113,125 @@ def evaluate_aggregation_window(distances: Tensor, radius: float, kind: str) -> 
 
 @dataclass
 class Geometry:
-    transport: Tensor  # (n_edges, orders, 2)
-    angular: Tensor  # (n_edges, orders, 2)
+    """The per-edge constants the fused ops read for one edge set, cutoff,
+    window and dtype (the constants of reference :126-164): the transport and
+    angular phase tables as ``(E, orders, 2)`` real pairs, ``rho = d / cutoff``,
+    the aggregation weights ``c(d) w``, the softmax bias ``log c + log w``
+    (each clamped at the dtype's tiny), the window support ``inside``, the CSR
+    and the largest neighbourhood.  Derived tables (the weights divided by
+    each target's window mass, the transport narrowed to a layer's orders)
+    are memoised in ``derived``; a chunk's geometry (``parent``, ``edges``)
+    takes them as views of its parent's."""
+
+    transport: Tensor
+    angular: Tensor
     rho: Tensor
     weights: Tensor
     bias: Tensor
-    inside: Tensor  # uint8
+    inside: Tensor
     row_ptr: Tensor
     source: Tensor
     max_degree: int
-    normalized: dict[float, Tensor] = field(default_factory=dict)
-    base: Geometry | None = None
-    span: tuple[int, int] | None = None
-    chunk_degrees: dict[tuple[int, int], int] = field(default_factory=dict)
-    narrowed: dict[int, Tensor] = field(default_factory=dict)
+    derived: dict = field(default_factory=dict)
+    parent: Geometry | None = None
+    edges: tuple[int, int] | None = None
+
+    def _derive(self, key: tuple, make) -> Tensor:
+        if self.parent is not None and self.edges is not None:
+            e0, e1 = self.edges
+            return self.parent._derive(key, make)[e0:e1]
+        held = self.derived.get(key)
+        if held is None:
+            held = make()
+            self.derived[key] = held
+        return held
 
     def aggregation_weights(self, normalize: bool, eps: float) -> Tensor:
-        """``c(r) w``, divided by each target's window mass (clamped at ``eps``) when ``normalize``."""
-        if self.base is not None and self.span is not None:
-            return self.base.aggregation_weights(normalize, eps)[self.span[0]:self.span[1]]
+        """``c(d) w``; under ``normalize`` divided by each target's window mass
+        clamped at ``eps`` (a chunk holds whole neighbourhoods: its parent's masses)."""
         if not normalize:
             return self.weights
-        cached = self.normalized.get(eps)
-        if cached is None:
+
+        def normalized() -> Tensor:
+            counts = self.row_ptr[1:] - self.row_ptr[:-1]
             mass = torch.segment_reduce(self.weights, "sum", offsets=self.row_ptr, axis=0).clamp_min(eps)
-            target = torch.repeat_interleave(torch.arange(mass.shape[0], device=mass.device),
-                                             self.row_ptr[1:] - self.row_ptr[:-1])
-            cached = (self.weights / mass.index_select(0, target)).contiguous()
-            self.normalized[eps] = cached
-        return cached
+            return (self.weights / torch.repeat_interleave(mass, counts)).contiguous()
+
+        return self._derive(("normalized", float(eps)), normalized)
 
     def transport_to(self, order: int) -> Tensor:
-        """The transport table narrowed to orders ``0..order`` (contiguous, cached):
-        the softmax reads only the heads' own frequencies."""
+        """The transport table narrowed to orders ``0..order`` (contiguous): the
+        softmax reads only the heads' own frequencies."""
         if order + 1 >= self.transport.shape[1]:
             return self.transport
-        if self.base is not None and self.span is not None:
-            return self.base.transport_to(order)[self.span[0]:self.span[1]]
-        cached = self.narrowed.get(order)
-        if cached is None:
-            cached = self.transport[:, : order + 1].contiguous()
-            self.narrowed[order] = cached
-        return cached
+        return self._derive(("transport", int(order)), lambda: self.transport[:, : order + 1].contiguous())
+
+    def host_row_ptr(self) -> np.ndarray:
+        """The CSR offsets on the host (read once)."""
+        held = self.derived.get("host_row_ptr")
+        if held is None:
+            held = self.row_ptr.detach().to("cpu").numpy()
+            self.derived["host_row_ptr"] = held
+        return held
 
 
-_GEOMETRIES: OrderedDict[tuple, tuple[Any, Geometry]] = OrderedDict()
-_GEOMETRY_CACHE = 64
-_CHUNKS: dict[int, tuple[Any, Any, int, int]] = {}
+def _tables(edges: Any, cutoff: float, window: str, dtype: torch.dtype) -> Geometry:
+    tiny = torch.finfo(dtype).tiny
+    d = edges.distances.to(dtype)
+    quad = edges.tangent_quadrature_weights.to(dtype)
+    win = evaluate_aggregation_window(d, cutoff, window)
+    row_ptr = edges.row_ptr.contiguous()
+    g = Geometry(torch.view_as_real(edges.transport_phases.contiguous()).to(dtype).contiguous(),
+                 torch.view_as_real(edges.angular_phases.contiguous()).to(dtype).contiguous(),
+                 (d / cutoff).contiguous(), (win * quad).contiguous(),
+                 (torch.log(win.clamp_min(tiny)) + torch.log(quad.clamp_min(tiny))).contiguous(),
+                 (win > 0.0).to(torch.uint8).contiguous(), row_ptr, edges.source_index.contiguous(), 0)
+    degrees = np.diff(g.host_row_ptr())
+    g.max_degree = int(degrees.max()) if degrees.size else 0
+    return g
+
+
+def _chunk_tables(parent: Geometry, edges: Any, e0: int, e1: int) -> Geometry:
+    """Views of ``parent``'s tables over its edges ``[e0, e1)`` (whole neighbourhoods of the
+    targets ``first .. last - 1``), with the chunk's own CSR and largest neighbourhood."""
+    ptr = parent.host_row_ptr()
+    first, last = int(np.searchsorted(ptr, e0, side="right")) - 1, int(np.searchsorted(ptr, e1, side="left"))
+    degrees = np.diff(ptr[max(first, 0):last + 1])
+    part = slice(e0, e1)
+    return Geometry(parent.transport[part], parent.angular[part], parent.rho[part], parent.weights[part],
+                    parent.bias[part], parent.inside[part], edges.row_ptr.contiguous(),
+                    edges.source_index.contiguous(), int(degrees.max()) if degrees.size else 0, parent=parent,
+                    edges=(e0, e1))
 
 
 def register_chunk(chunk: Any, parent: Any, first: int, last: int) -> None:
-    _purge()
-    _CHUNKS[id(chunk.row_ptr)] = (weakref.ref(chunk.row_ptr), parent, int(first), int(last))
+    """Record that ``chunk`` is ``parent``'s edges ``first .. last`` in order
+    (reference :176-187), so its tables are views of the parent's; edge sets
+    made by ``EdgeGeometry.target_range`` carry this already."""
+    chunk.__dict__["_span"] = (parent, int(first), int(last))
 
 
 def chunk_of(edges: Any) -> tuple[Any, int, int] | None:
-    registered = _CHUNKS.get(id(edges.row_ptr))
-    if registered is None or registered[0]() is not edges.row_ptr:
-        return None
-    return registered[1], registered[2], registered[3]
-
-
-def _purge() -> None:
-    for key in [k for k, (held, _) in _GEOMETRIES.items() if held() is None]:
-        del _GEOMETRIES[key]
-    for key in [k for k, (held, _, _, _) in _CHUNKS.items() if held() is None]:
-        del _CHUNKS[key]
+    """``(parent, first, last)`` of a chunk edge set, else ``None``."""
+    return edges.__dict__.get("_span")
 
 
 def geometry(edges: Any, cutoff: float, window: str, dtype: torch.dtype) -> Geometry:
-    """The per-edge constants of ``edges`` (reference :203-255), cached while the edge set lives."""
-    _purge()
-    registered = _CHUNKS.get(id(edges.row_ptr))
-    if registered is not None and registered[0]() is edges.row_ptr:
-        _, parent, first, last = registered
-        base = geometry(parent, cutoff, window, dtype)
-        degree = base.chunk_degrees.get((first, last))
-        if degree is None:
-            rp = edges.row_ptr
-            degree = int((rp[1:] - rp[:-1]).max()) if rp.numel() > 1 else 0
-            base.chunk_degrees[(first, last)] = degree
-        return Geometry(base.transport[first:last], base.angular[first:last], base.rho[first:last],
-                        base.weights[first:last], base.bias[first:last], base.inside[first:last],
-                        edges.row_ptr.contiguous(), edges.source_index.contiguous(), degree, base=base,
-                        span=(first, last))
-    key = (id(edges.row_ptr), float(cutoff), window, dtype, str(edges.row_ptr.device))
-    held = _GEOMETRIES.get(key)
-    if held is not None and held[0]() is edges.row_ptr:
-        _GEOMETRIES.move_to_end(key)
-        return held[1]
-    tiny = torch.finfo(dtype).tiny
-    distances = edges.distances.to(dtype)
-    quadrature = edges.tangent_quadrature_weights.to(dtype)
-    window_values = evaluate_aggregation_window(distances, cutoff, window)
-    bias = torch.log(window_values.clamp_min(tiny)) + torch.log(quadrature.clamp_min(tiny))
-    row_ptr = edges.row_ptr.contiguous()
-    max_degree = int((row_ptr[1:] - row_ptr[:-1]).max()) if row_ptr.numel() > 1 else 0
-    result = Geometry(
-        torch.view_as_real(edges.transport_phases.contiguous()).to(dtype).contiguous(),
-        torch.view_as_real(edges.angular_phases.contiguous()).to(dtype).contiguous(),
-        (distances / cutoff).contiguous(), (window_values * quadrature).contiguous(), bias.contiguous(),
-        (window_values > 0.0).to(torch.uint8).contiguous(), row_ptr, edges.source_index.contiguous(), max_degree,
-    )
-    _GEOMETRIES[key] = (weakref.ref(edges.row_ptr), result)
-    while len(_GEOMETRIES) > _GEOMETRY_CACHE:
-        _GEOMETRIES.popitem(last=False)
-    return result
+    """The per-edge constants of ``edges`` (reference :203-255), built once and
+    kept on the edge set itself (so for as long as it lives); a chunk's are
+    views of its parent's."""
+    store = edges.__dict__.setdefault("_fused_geometry", {})
+    key = (float(cutoff), window, dtype)
+    g = store.get(key)
+    if g is None:
+        span = chunk_of(edges)
+        if span is None:
+            g = _tables(edges, cutoff, window, dtype)
+        else:
+            parent, e0, e1 = span
+            g = _chunk_tables(geometry(parent, cutoff, window, dtype), edges, e0, e1)
+        store[key] = g
+    return g
 
 
 def _device_ok(x: Any) -> bool:

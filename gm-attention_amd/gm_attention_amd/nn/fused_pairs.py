@@ -1,18 +1,27 @@
 """The steerable kernel's per-edge readout as fused pair terms on the HIP path.
 
-Restates the reference's ``nn/fused_pairs.py``: each ``(n, m, role)`` term of
-``SO2SteerableKernel._forward_general`` (reference nn/kernels.py:752-915) is
-one launch (``gm_pairs_forward``) that forms its ``b_m x a_n`` coefficient
-block in registers from the trunk output and the readout rows, applies the
-phases and the radial power, and accumulates into the output; the backward is
-one launch per term giving the input and trunk gradients and that term's rows
-of the coefficient gradient, then one blocked product for the readout
-weights' gradient.  Same names, plan and switch as the reference:
+The drop-in for the reference's ``nn/fused_pairs.py`` under the same switch
+(``GM_FUSED_PAIRS``, :39-40) and names (``Term``, ``plan``, ``enabled``,
+``_FusedPairs``, ``forward_general``; reference :51-295): the per-edge readout
+of ``SO2SteerableKernel._forward_general`` (reference nn/kernels.py:752-915)
+as one HIP launch per ``(n, m, role)`` term (``gm_pairs_forward``), each
+forming its ``b_m x a_n`` coefficient block in registers from the trunk
+output and the readout rows.
 
-* ``MODE = GM_FUSED_PAIRS`` (:39-40): ``"0"`` off, ``"1"`` device tensors,
-  ``"cpu"`` accepted (a CPU tensor then raises: this build has no CPU driver);
-* ``Term`` / ``plan`` (:96-123), ``enabled`` (:126-149), ``_FusedPairs``
-  (:156-238), ``forward_general`` (:249-295).
+Design of this module:
+
+* a term's flags and phase orders follow from three facts about its block
+  (is the input scalar, is the output scalar, is it the antilinear half),
+  tabulated in :data:`_RULES`; :func:`plan` lists the kernel's blocks in the
+  readout's pair order and applies the table;
+* :func:`forward_general` turns the plan into a *schedule* for this call --
+  one entry per launch with the positions of its input, output, phase and
+  radial-power tensors resolved -- so the autograd Function only replays it;
+* the backward replays the schedule for the input and trunk gradients and
+  forms each term's readout-weight gradient right after its launch, from the
+  term's own ``(width, E)`` coefficient gradient: weight rows by a product
+  with the trunk output summed over edge blocks in a fixed order, bias rows
+  by a row sum.
 
 Every block side and trunk width in ``1..16`` runs the same kernels (the sides
 are loop bounds, not compile-time sizes), so ``SUPPORTED`` covers ``1..16``.
@@ -28,6 +37,7 @@ import torch
 from torch import Tensor
 
 from gm_attention_amd import _native
+from gm_attention_amd.nn.linear import blocked_gram
 from gm_attention_amd.representations.field_type import SO2FeatureField
 
 MATRIX_COMPLEX, U_REAL, CONJ_U, OUT_REAL = (_native.PAIRS_MATRIX_COMPLEX, _native.PAIRS_U_REAL, _native.PAIRS_CONJ_U,
@@ -36,10 +46,10 @@ MAX_MULT = _native.PAIRS_MAX_MULT
 MAX_TRUNK = _native.PAIRS_MAX_TRUNK
 SUPPORTED = tuple(range(1, MAX_MULT + 1))
 
-#: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` on everywhere (reference :39-40).
+#: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` accepted (reference :39-40).
 MODE = os.environ.get("GM_FUSED_PAIRS", "1")
 
-#: Rows per block of the readout weights' gradient (a sum over every edge).
+#: Edges per block of a readout weight gradient's fixed-order sum.
 WEIGHT_GRAD_BLOCK = 16384
 
 
@@ -50,228 +60,221 @@ def extension(size: tuple[int, int, int] | None = None) -> Any:
 
 @dataclass(frozen=True)
 class Term:
+    """One launch of the readout: block ``(n -> m, role)`` of ``a`` input and
+    ``b`` output copies, its kernel flags, which readout head and rows hold
+    its coefficients, the angular phase orders applied before (``pre``) or
+    after (``post``) the block and its radial power (``None``: not applied)."""
+
     n: int
     m: int
     role: str
     flags: int
     a: int
     b: int
-    real_head: bool  # rows of the real head (the (0, 0) block) or the complex head
+    real_head: bool
     rows: slice
     pre_order: int | None
     post_order: int | None
     power: int | None
 
 
+# (input scalar, output scalar, antilinear) -> flags and the phase orders as functions of (n, m).
+# The scalar-to-scalar block is the real head's; a scalar output takes the real part of
+# A (e^{i n phi} conj z); a scalar input gets e^{i m phi} after the block; the rest rotate the
+# (conjugated, for the antilinear half) transported input by e^{i (m -+ n) phi} first.
+_RULES: dict[tuple[bool, bool, bool], tuple[int, Any, Any]] = {
+    (True, True, False): (U_REAL | OUT_REAL, None, None),
+    (True, False, False): (MATRIX_COMPLEX | U_REAL, None, lambda n, m: m),
+    (False, True, False): (MATRIX_COMPLEX | CONJ_U | OUT_REAL, lambda n, m: n, None),
+    (False, False, False): (MATRIX_COMPLEX, lambda n, m: m - n, None),
+    (False, False, True): (MATRIX_COMPLEX | CONJ_U, lambda n, m: m + n, None),
+}
+
+
+def _term(kernel: Any, n: int, m: int, role: str) -> Term:
+    fin, fout = kernel.field_type_in, kernel.field_type_out
+    a, b = fin.multiplicity(n), fout.multiplicity(m)
+    flags, pre, post = _RULES[(n == 0, m == 0, role == "antilinear")]
+    if n == 0 and m == 0:
+        return Term(0, 0, "real", flags, a, b, True, slice(0, a * b), None, None, None)
+    return Term(n, m, role, flags, a, b, False, kernel._pair_ranges[(n, m, role)],
+                pre(n, m) if pre is not None else None, post(n, m) if post is not None else None,
+                kernel._pair_powers[(n, m, role)])
+
+
 def plan(kernel: Any) -> list[Term]:
-    """The terms of the per-edge readout's pair loop, in its order (reference :96-123)."""
+    """The readout's terms in its pair order (reference :96-123): output
+    frequencies outer, input frequencies inner, the linear half of a block
+    before its antilinear half (present when both frequencies are nonzero)."""
     cached = kernel.__dict__.get("_fused_plan")
-    if cached is not None:
-        return cached
-    terms: list[Term] = []
-    for m in kernel.field_type_out.frequencies:
-        b = kernel.field_type_out.multiplicity(m)
-        for n in kernel.field_type_in.frequencies:
-            a = kernel.field_type_in.multiplicity(n)
-            if n == 0 and m == 0:
-                terms.append(Term(n, m, "real", U_REAL | OUT_REAL, a, b, True, slice(0, a * b), None, None, None))
-            elif n == 0:
-                terms.append(Term(n, m, "linear", MATRIX_COMPLEX | U_REAL, a, b, False,
-                                  kernel._pair_ranges[(n, m, "linear")], None, m, kernel._pair_powers[(n, m, "linear")]))
-            elif m == 0:
-                # Re[A conj(e^{-i n phi} z)] = Re[A (e^{i n phi} conj z)]
-                terms.append(Term(n, m, "linear", MATRIX_COMPLEX | CONJ_U | OUT_REAL, a, b, False,
-                                  kernel._pair_ranges[(n, m, "linear")], n, None,
-                                  kernel._pair_powers[(n, m, "linear")]))
-            else:
-                terms.append(Term(n, m, "linear", MATRIX_COMPLEX, a, b, False, kernel._pair_ranges[(n, m, "linear")],
-                                  m - n, None, kernel._pair_powers[(n, m, "linear")]))
-                terms.append(Term(n, m, "antilinear", MATRIX_COMPLEX | CONJ_U, a, b, False,
-                                  kernel._pair_ranges[(n, m, "antilinear")], m + n, None,
-                                  kernel._pair_powers[(n, m, "antilinear")]))
-    kernel.__dict__["_fused_plan"] = terms
-    return terms
+    if cached is None:
+        cached = [_term(kernel, n, m, role)
+                  for m in kernel.field_type_out.frequencies
+                  for n in kernel.field_type_in.frequencies
+                  for role in (("real",) if n == m == 0 else ("linear", "antilinear") if n and m else ("linear",))]
+        kernel.__dict__["_fused_plan"] = cached
+    return cached
 
 
 def enabled(kernel: Any, x: SO2FeatureField, edges: Any) -> bool:
-    """Whether this call takes the fused terms (reference :126-149): the mode
-    allows the device, float32/64, every block and the trunk within 16, and
-    every phase order tabulated on ``edges``."""
-    if MODE == "0":
-        return False
-    if MODE != "cpu" and x.device.type != "cuda":
-        return False
-    if x.dtype not in (torch.float32, torch.float64):
+    """Whether this call takes the fused terms (reference :126-149): the switch
+    admits the tensors' device, the dtype is float32/64, the trunk and every
+    block side are within 16, and every phase order is tabulated on ``edges``."""
+    on_device = x.device.type == "cuda"
+    if MODE == "0" or (MODE != "cpu" and not on_device) or x.dtype not in (torch.float32, torch.float64):
         return False
     head = kernel.complex_head if kernel.complex_head is not None else kernel.real_head
-    if not 1 <= head.in_features <= MAX_TRUNK:
+    if head.in_features > MAX_TRUNK:
         return False
-    for term in plan(kernel):
-        if not (1 <= term.a <= MAX_MULT and 1 <= term.b <= MAX_MULT):
-            return False
-        for order in (term.pre_order, term.post_order):
-            if order is not None and abs(order) > edges.max_frequency:
-                return False
-    return True
+    terms = plan(kernel)
+    sides_fit = all(t.a in SUPPORTED and t.b in SUPPORTED for t in terms)
+    orders = [abs(o) for t in terms for o in (t.pre_order, t.post_order) if o is not None]
+    return sides_fit and max(orders, default=0) <= edges.max_frequency
 
 
-def _rows_product(gk: Tensor, operand: Tensor, block: int) -> Tensor:
-    """``gk @ operand`` for ``gk (width, E)`` and ``operand (E, c)``: the sum over
-    the edges as per-block partial products (one batched product, summed in a
-    fixed order) instead of one long reduction on a few workgroups."""
-    width, E = gk.shape
-    nb = E // block
-    if nb < 2:
-        return gk @ operand
-    head = nb * block
-    parts = torch.bmm(gk[:, :head].reshape(width, nb, block).permute(1, 0, 2),
-                      operand[:head].reshape(nb, block, operand.shape[1]))
-    out = parts.sum(0)
-    if head < E:
-        out = out + gk[:, head:] @ operand[head:]
-    return out
+@dataclass(frozen=True)
+class _Launch:
+    """One scheduled term: the term, then the positions of its input vector,
+    output, pre/post phase tables and radial power among the call's tensors."""
+
+    term: Term
+    u: int
+    out: int
+    pre: int | None
+    post: int | None
+    scale: int | None
 
 
-def _rows(term: Term, cw: Tensor | None, cb: Tensor | None, rw: Tensor | None,
-          rb: Tensor | None) -> tuple[Tensor, Tensor | None]:
-    weight, bias = (rw, rb) if term.real_head else (cw, cb)
-    assert weight is not None
-    return weight[term.rows].contiguous(), None if bias is None else bias[term.rows].contiguous()
+@dataclass(frozen=True)
+class _Call:
+    """What one kernel call launches: the schedule and the outputs it writes
+    (frequency, copies, real or complex)."""
+
+    launches: tuple[_Launch, ...]
+    outputs: tuple[tuple[int, int, bool], ...]
 
 
 def _empty(like: Tensor) -> Tensor:
     return like.new_empty(0)
 
 
+def _pick(tables: tuple[Tensor, ...], index: int | None, like: Tensor) -> Tensor:
+    return tables[index] if index is not None else _empty(like)
+
+
+def _coefficients(term: Term, heads: tuple[Tensor | None, ...]) -> tuple[Tensor, Tensor]:
+    """The term's readout rows and bias rows (an empty tensor for no bias)."""
+    cw, cb, rw, rb = heads
+    weight, bias = (rw, rb) if term.real_head else (cw, cb)
+    assert weight is not None
+    rows = weight[term.rows].contiguous()
+    return rows, bias[term.rows].contiguous() if bias is not None else _empty(rows)
+
+
 class _FusedPairs(torch.autograd.Function):
-    """All terms of one kernel call (reference :156-238)."""
+    """Every term of one kernel call (reference :156-238).  Inputs: the trunk
+    output ``hidden (E, T)``, the heads' weights and biases, the call
+    (:class:`_Call`), the angular phase tables, the radial power tables, then
+    one per-edge input vector per input frequency; out one per-edge message
+    per output frequency."""
 
     @staticmethod
     def forward(ctx: Any, hidden: Tensor, complex_weight: Tensor | None, complex_bias: Tensor | None,
-                real_weight: Tensor | None, real_bias: Tensor | None, meta: dict, phases: tuple[Tensor, ...],
+                real_weight: Tensor | None, real_bias: Tensor | None, call: _Call, phases: tuple[Tensor, ...],
                 scales: tuple[Tensor, ...], *vectors: Tensor) -> tuple[Tensor, ...]:
-        terms: list[Term] = meta["terms"]
-        n_edges = hidden.shape[0]
-        cdtype = torch.complex64 if hidden.dtype == torch.float32 else torch.complex128
-        outputs = [torch.zeros(n_edges, meta["out_multiplicity"][m], dtype=hidden.dtype if m == 0 else cdtype,
-                               device=hidden.device) for m in meta["out_frequencies"]]
         ext = extension()
-        for term, (pre, post, scale) in zip(terms, meta["tables"], strict=True):
-            weight, bias = _rows(term, complex_weight, complex_bias, real_weight, real_bias)
+        E = hidden.shape[0]
+        cplx = torch.complex64 if hidden.dtype == torch.float32 else torch.complex128
+        outs = tuple(torch.zeros(E, b, dtype=hidden.dtype if real else cplx, device=hidden.device)
+                     for _m, b, real in call.outputs)
+        heads = (complex_weight, complex_bias, real_weight, real_bias)
+        for step in call.launches:
+            t = step.term
+            weight, bias = _coefficients(t, heads)
             with torch.profiler.record_function("gm::kernel/pairs"):
-                ext.forward(hidden, weight, bias if bias is not None else _empty(hidden),
-                            vectors[meta["in_index"][term.n]],
-                            phases[pre] if pre is not None else _empty(hidden),
-                            phases[post] if post is not None else _empty(hidden),
-                            scales[scale] if scale is not None else _empty(hidden),
-                            outputs[meta["out_index"][term.m]], term.a, term.b, term.flags)
+                ext.forward(hidden, weight, bias, vectors[step.u], _pick(phases, step.pre, hidden),
+                            _pick(phases, step.post, hidden), _pick(scales, step.scale, hidden), outs[step.out],
+                            t.a, t.b, t.flags)
+        ctx.call = call
+        ctx.sizes = (len(phases), len(scales))
         ctx.save_for_backward(hidden, complex_weight, complex_bias, real_weight, real_bias, *phases, *scales, *vectors)
-        ctx.meta = meta
-        ctx.counts = (len(phases), len(scales))
-        return tuple(outputs)
+        return outs
 
     @staticmethod
     @torch.autograd.function.once_differentiable
-    def backward(ctx: Any, *grad_outputs: Tensor | None) -> tuple:
-        meta = ctx.meta
-        n_phases, n_scales = ctx.counts
-        saved = ctx.saved_tensors
-        hidden, complex_weight, complex_bias, real_weight, real_bias = saved[:5]
-        phases = saved[5:5 + n_phases]
-        scales = saved[5 + n_phases:5 + n_phases + n_scales]
-        vectors = saved[5 + n_phases + n_scales:]
-        terms: list[Term] = meta["terms"]
-        n_edges = hidden.shape[0]
-        cdtype = torch.complex64 if hidden.dtype == torch.float32 else torch.complex128
-        grads_out = [(g if g is not None else torch.zeros(n_edges, meta["out_multiplicity"][m],
-                                                          dtype=hidden.dtype if m == 0 else cdtype,
-                                                          device=hidden.device)).contiguous()
-                     for g, m in zip(grad_outputs, meta["out_frequencies"], strict=True)]
-        grad_hidden = torch.zeros_like(hidden)
-        grad_vectors = [torch.zeros_like(v) for v in vectors]
-        # coefficient gradients coefficient-major (width, n_edges): a term's rows are one contiguous slab
-        grad_complex = hidden.new_empty(complex_weight.shape[0], n_edges) if complex_weight is not None else None
-        grad_real = hidden.new_empty(real_weight.shape[0], n_edges) if real_weight is not None else None
+    def backward(ctx: Any, *grad_outs: Tensor | None) -> tuple:
+        call: _Call = ctx.call
+        n_phases, n_scales = ctx.sizes
+        hidden, cw, cb, rw, rb, *rest = ctx.saved_tensors
+        phases, scales, vectors = (tuple(rest[:n_phases]), tuple(rest[n_phases:n_phases + n_scales]),
+                                   tuple(rest[n_phases + n_scales:]))
         ext = extension()
-        for term, (pre, post, scale) in zip(terms, meta["tables"], strict=True):
-            weight, bias = _rows(term, complex_weight, complex_bias, real_weight, real_bias)
-            grad_k = grad_real if term.real_head else grad_complex
-            assert grad_k is not None
+        E = hidden.shape[0]
+        cplx = torch.complex64 if hidden.dtype == torch.float32 else torch.complex128
+        grads = [(g if g is not None else torch.zeros(E, b, dtype=hidden.dtype if real else cplx,
+                                                      device=hidden.device)).contiguous()
+                 for g, (_m, b, real) in zip(grad_outs, call.outputs, strict=True)]
+        d_hidden = torch.zeros_like(hidden)
+        d_vectors = [torch.zeros_like(v) for v in vectors]
+        heads = (cw, cb, rw, rb)
+        # each readout head's gradient, row block by row block as the terms come
+        d_head = {True: (torch.zeros_like(rw) if rw is not None else None,
+                         torch.zeros_like(rb) if rb is not None else None),
+                  False: (torch.zeros_like(cw) if cw is not None else None,
+                          torch.zeros_like(cb) if cb is not None else None)}
+        for step in call.launches:
+            t = step.term
+            weight, bias = _coefficients(t, heads)
+            d_coeff = hidden.new_empty(weight.shape[0], E)  # this term's coefficient gradient, row-major by edge
             with torch.profiler.record_function("gm::kernel/pairs_backward"):
-                ext.backward(hidden, weight, bias if bias is not None else _empty(hidden),
-                             vectors[meta["in_index"][term.n]],
-                             phases[pre] if pre is not None else _empty(hidden),
-                             phases[post] if post is not None else _empty(hidden),
-                             scales[scale] if scale is not None else _empty(hidden),
-                             grads_out[meta["out_index"][term.m]], grad_vectors[meta["in_index"][term.n]],
-                             grad_hidden, grad_k[term.rows], term.a, term.b, term.flags)
-        # the bias gradient is the coefficient gradient summed over the edges: a column of
-        # ones beside the trunk output folds it into the weight product
-        with_bias = complex_bias is not None or real_bias is not None
-        operand = torch.cat((hidden, hidden.new_ones(n_edges, 1)), dim=1) if with_bias else hidden
-
-        def head_gradients(grad_k: Tensor | None, bias: Tensor | None) -> tuple[Tensor | None, Tensor | None]:
-            if grad_k is None:
-                return None, None
-            grad = _rows_product(grad_k, operand, WEIGHT_GRAD_BLOCK)  # (width, trunk [+ 1])
-            if not with_bias:
-                return grad.contiguous(), None
-            return grad[:, :-1].contiguous(), (grad[:, -1].contiguous() if bias is not None else None)
-
-        grad_cw, grad_cb = head_gradients(grad_complex, complex_bias)
-        grad_rw, grad_rb = head_gradients(grad_real, real_bias)
-        return (grad_hidden, grad_cw, grad_cb, grad_rw, grad_rb, None, None, None, *grad_vectors)
+                ext.backward(hidden, weight, bias, vectors[step.u], _pick(phases, step.pre, hidden),
+                             _pick(phases, step.post, hidden), _pick(scales, step.scale, hidden), grads[step.out],
+                             d_vectors[step.u], d_hidden, d_coeff, t.a, t.b, t.flags)
+            dw, db = d_head[t.real_head]
+            dw[t.rows] += blocked_gram(d_coeff.t(), hidden, WEIGHT_GRAD_BLOCK)
+            if db is not None:
+                db[t.rows] += d_coeff.sum(dim=1)
+        return (d_hidden, d_head[False][0], d_head[False][1], d_head[True][0], d_head[True][1], None, None, None,
+                *d_vectors)
 
 
-def _radial_powers(kernel: Any, distances: Tensor, top: int) -> Tensor:
-    """``(r / cutoff)^p`` for ``p = 0..top`` by repeated products (reference kernels.py:734-750)."""
-    normalized = distances / kernel.radial_basis.cutoff
-    table = [torch.ones_like(normalized)]
-    for _ in range(top):
-        table.append(table[-1] * normalized)
-    return torch.stack(table, dim=-1)
+def _radial_powers(distances: Tensor, cutoff: float, powers: list[int]) -> tuple[Tensor, ...]:
+    """``(r / cutoff)^p`` for each listed ``p``, as repeated products (reference kernels.py:734-750)."""
+    rho = distances / cutoff
+    table, current = {}, torch.ones_like(rho)
+    for p in range(max(powers, default=-1) + 1):
+        if p:
+            current = current * rho
+        table[p] = current
+    return tuple(table[p].contiguous() for p in powers)
 
 
 def forward_general(kernel: Any, x: SO2FeatureField, edges: Any) -> SO2FeatureField:
     """The kernel's per-edge messages on the edge-shaped field ``x`` through the
-    fused terms (reference :249-295): trunk, transport, phase tables, radial
-    powers, then every term."""
+    fused terms (reference :249-295)."""
     terms = plan(kernel)
+    fin, fout = list(kernel.field_type_in.frequencies), list(kernel.field_type_out.frequencies)
     with torch.profiler.record_function("gm::kernel/radial"):
         hidden = kernel._trunk_hidden(edges.distances).contiguous()
-    in_frequencies = list(kernel.field_type_in.frequencies)
-    out_frequencies = list(kernel.field_type_out.frequencies)
-    vectors = []
-    for n in in_frequencies:
-        if n == 0:
-            vectors.append(x[0].contiguous())
-        else:  # transported: e^{i n gamma} z
-            z = torch.view_as_complex(x[n].contiguous())
-            vectors.append((edges.transport_harmonic(n).unsqueeze(-1) * z).contiguous())
+    # the input vectors: scalars as they are, higher frequencies transported (e^{i n gamma} z)
+    vectors = [x[0].contiguous() if n == 0 else
+               (edges.transport_harmonic(n).unsqueeze(-1) * torch.view_as_complex(x[n].contiguous())).contiguous()
+               for n in fin]
     orders = sorted({o for t in terms for o in (t.pre_order, t.post_order) if o is not None})
-    phases = tuple(edges.angular_harmonic(o).contiguous() for o in orders)
     powers = sorted({t.power for t in terms if t.power is not None})
-    table = _radial_powers(kernel, edges.distances, max(powers)) if powers else None
-    scales = tuple(table[:, p].contiguous() for p in powers) if table is not None else ()
-    order_index = {o: i for i, o in enumerate(orders)}
-    power_index = {p: i for i, p in enumerate(powers)}
-    meta = {
-        "terms": terms,
-        "tables": [(order_index[t.pre_order] if t.pre_order is not None else None,
-                    order_index[t.post_order] if t.post_order is not None else None,
-                    power_index[t.power] if t.power is not None else None) for t in terms],
-        "in_index": {n: i for i, n in enumerate(in_frequencies)},
-        "out_index": {m: i for i, m in enumerate(out_frequencies)},
-        "out_frequencies": out_frequencies,
-        "out_multiplicity": {m: kernel.field_type_out.multiplicity(m) for m in out_frequencies},
-    }
+    phases = tuple(edges.angular_harmonic(o).contiguous() for o in orders)
+    scales = _radial_powers(edges.distances, kernel.radial_basis.cutoff, powers)
+    launches = tuple(_Launch(t, fin.index(t.n), fout.index(t.m),
+                             orders.index(t.pre_order) if t.pre_order is not None else None,
+                             orders.index(t.post_order) if t.post_order is not None else None,
+                             powers.index(t.power) if t.power is not None else None) for t in terms)
+    call = _Call(launches, tuple((m, kernel.field_type_out.multiplicity(m), m == 0) for m in fout))
     ch, rh = kernel.complex_head, kernel.real_head
-    outputs = _FusedPairs.apply(hidden, ch.weight if ch is not None else None, ch.bias if ch is not None else None,
-                                rh.weight if rh is not None else None, rh.bias if rh is not None else None, meta,
-                                phases, scales, *vectors)
-    return SO2FeatureField(kernel.field_type_out,
-                           {m: (out if m == 0 else torch.view_as_real(out))
-                            for m, out in zip(out_frequencies, outputs, strict=True)})
+    outs = _FusedPairs.apply(hidden, None if ch is None else ch.weight, None if ch is None else ch.bias,
+                             None if rh is None else rh.weight, None if rh is None else rh.bias, call, phases, scales,
+                             *vectors)
+    return SO2FeatureField(kernel.field_type_out, {m: out if m == 0 else torch.view_as_real(out)
+                                                   for m, out in zip(fout, outs, strict=True)})
 
 
 __all__ = ["MODE", "Term", "enabled", "extension", "forward_general", "plan"]

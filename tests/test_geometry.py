@@ -111,3 +111,50 @@ def test_gpu_builder_routing_and_errors_on_the_host():
 
     with pytest.raises(ValueError, match="float64 lattice"):
         hip_builder._lattice(NoLattice(), torch.device("cpu"))
+
+
+def test_target_chunks_partition_the_edges_into_whole_neighbourhoods():
+    """EdgeGeometry.chunks: consecutive target ranges, every edge in exactly
+    one chunk, each chunk's CSR the parent's rows for its targets (empty
+    elsewhere), its tables views of the parent's, and its span recorded."""
+    import torch
+
+    import problems
+
+    edges = problems.discretization(10, 20).edge_geometry
+    ptr = edges.row_ptr
+    seen = 0
+    for chunk in edges.chunks(7):
+        parent, e0, e1 = chunk.span()
+        assert parent is edges and e0 == seen and e1 > e0
+        assert torch.equal(chunk.edge_index, edges.edge_index[:, e0:e1])
+        assert chunk.distances.data_ptr() == edges.distances[e0:].data_ptr()  # a view, not a copy
+        assert torch.equal(chunk.row_ptr, (ptr - e0).clamp(0, e1 - e0))
+        targets = chunk.target_index.unique()
+        assert int(targets.max() - targets.min()) < 7
+        # whole neighbourhoods: each target's edges all here
+        assert int(chunk.row_ptr[-1]) == e1 - e0
+        for t in targets.tolist():
+            assert int(ptr[t + 1] - ptr[t]) == int(chunk.row_ptr[t + 1] - chunk.row_ptr[t])
+        seen = e1
+    assert seen == edges.n_edges
+    with pytest.raises(ValueError, match="chunk_size must be at least 1"):
+        next(edges.chunks(0))
+
+
+def test_grid_hierarchy_reports_every_problem_with_its_arguments():
+    from gm_attention_amd.discretization.grid import build_equiangular_grid
+    from gm_attention_amd.discretization.hierarchy import build_grid_hierarchy
+
+    grids = [build_equiangular_grid(9, 18), build_equiangular_grid(9, 18)]
+    with pytest.raises(ValueError) as info:
+        build_grid_hierarchy(grids, ["equiangular"], [(9, 18), (9, 18)], restrict_cutoffs=[0.5, 0.5],
+                             interpolate_cutoffs=[0.5], local_cutoffs=[None, []])
+    message = str(info.value)
+    assert "grid_kinds has 1 entries for 2 levels" in message
+    assert "restrict_cutoffs has 2 entries for 1 hops" in message
+    assert "is not coarser than level 0" in message
+    assert "local_cutoffs[1] is an empty list" in message
+    with pytest.raises(ValueError, match="at least two levels"):
+        build_grid_hierarchy(grids[:1], ["equiangular"], [(9, 18)], restrict_cutoffs=[], interpolate_cutoffs=[],
+                             local_cutoffs=[None])
