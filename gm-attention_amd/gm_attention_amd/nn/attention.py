@@ -19,9 +19,9 @@ Every score, softmax and value aggregation runs in the HIP ops
 (``fused_attention.Softmax``, ``fused_factored.FactoredAggregate``; under
 ``GM_FACTORED_KERNEL=0`` the value kernels' per-edge readout runs in the fused
 pair terms, ``fused_pairs``, and the weighted messages are summed per target);
-the projections are per-frequency dense products.  A layer whose fused op is not
-enabled raises (the reference would fall back to its eager torch path; here
-that path is the test oracle).
+the projections are per-frequency dense products.  A call an op's predicate
+declines (CPU tensors, a ``GM_FUSED_*`` switch at ``"0"``) runs the same
+numbers in torch (``eager_ops``), as the reference falls back to its eager path.
 """
 
 from __future__ import annotations
@@ -124,10 +124,11 @@ class SO2Attention(nn.Module):
 
     def _attend(self, x: SO2FeatureField, edges, products=None, groups=None) -> dict[int, Tensor]:
         q, k = self.query(x), self.key(x)
-        if not fused_attention.softmax_head_enabled(self, x, edges):
-            raise RuntimeError("the fused scores-and-softmax op is not enabled for this call "
-                               "(GM_FUSED_ATTENTION=1 and device tensors required)")
-        alpha = fused_attention.softmax_head(self, q._rows(), k._rows(), edges)
+        if fused_attention.softmax_head_enabled(self, x, edges):
+            alpha = fused_attention.softmax_head(self, q._rows(), k._rows(), edges)
+        else:  # the reference's eager weights (attention.py:263-268)
+            alpha = fused_attention.softmax_eager(fused_attention.plan_head(self), q._rows(), k._rows(), edges,
+                                                  self.cutoff, self.window, self._score_scale).reshape(-1)
         if not kernels.factored_enabled():  # the per-edge readout through the fused pair terms
             messages = self.value(gather_to_edges(x, edges.source_index), edges)
             return weighted_segment_sum(alpha, messages.coefficients, edges.row_ptr)
@@ -267,10 +268,11 @@ def _attend_batched(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> dict[int, Tenso
     with torch.profiler.record_function("gm::attention/attend"):
         queries = _stacked_projection([h.query for h in heads], x)
         keys = _stacked_projection([h.key for h in heads], x)
-        if not fused_attention.softmax_enabled(mhsa, x, edges):
-            raise RuntimeError("the fused scores-and-softmax op is not enabled for this call "
-                               "(GM_FUSED_ATTENTION=1 and device tensors required)")
-        alpha = fused_attention.softmax(mhsa, queries._rows(), keys._rows(), edges)  # (n_edges, n_heads)
+        if fused_attention.softmax_enabled(mhsa, x, edges):
+            alpha = fused_attention.softmax(mhsa, queries._rows(), keys._rows(), edges)  # (n_edges, n_heads)
+        else:  # the reference's eager weights (attention.py:880-886)
+            alpha = fused_attention.softmax_eager(fused_attention.plan(mhsa), queries._rows(), keys._rows(), edges,
+                                                  mhsa.cutoff, heads[0].window, heads[0]._score_scale)
         return _aggregated_factored(mhsa, x, edges, alpha)
 
 

@@ -101,10 +101,13 @@ class SO2Convolution(nn.Module):
 
     def _aggregate(self, x: SO2FeatureField, edges, products=None, groups=None) -> dict[int, Tensor]:
         if self.depthwise:
-            if not fused_attention.enabled_depthwise(self, x, edges):
-                raise RuntimeError("the fused depthwise op is not enabled for this call "
-                                   "(GM_FUSED_ATTENTION=1 and device tensors required)")
-            return self._aggregate_fused(x, edges)
+            if fused_attention.enabled_depthwise(self, x, edges):
+                return self._aggregate_fused(x, edges)
+            # the reference's eager path (convolution.py:297-308): per-edge messages, weighted segment sums
+            g = fused_attention.geometry(edges, self.cutoff, self.window, x.dtype)
+            messages = self.kernel(gather_to_edges(x, edges.source_index), edges)
+            return weighted_segment_sum(g.aggregation_weights(self.normalize, self.eps), messages.coefficients,
+                                        edges.row_ptr)
         kernel = self.kernel
         assert isinstance(kernel, SO2SteerableKernel)
         g = fused_attention.geometry(edges, self.cutoff, self.window, x.dtype)

@@ -13,9 +13,9 @@ Restates the reference's ``nn/depthwise.py``:
   one radial embedding, stacked on a leading kernel axis.
 
 The per-edge message form (``SO2DepthwiseKernel.forward`` on edge-shaped
-fields, :147-193) is the eager path; here it is the parity oracle and lives
-with the tests.  The layer (``convolution.SO2Convolution``) evaluates the
-kernel through the fused depthwise op.
+fields, :147-193) is the eager path (``eager_ops.depthwise_messages``); the
+layer (``convolution.SO2Convolution``) evaluates the kernel through the fused
+depthwise op and takes the eager path only for calls the op declines.
 """
 
 from __future__ import annotations
@@ -82,8 +82,19 @@ class SO2DepthwiseKernel(nn.Module):
         return [m for m in self.radial_trunk if isinstance(m, nn.Linear)]
 
     def forward(self, x, edges):
-        raise RuntimeError("the per-edge depthwise messages are the eager path (the test oracle); the layer "
-                           "evaluates this kernel through the fused depthwise op (SO2Convolution)")
+        """One message per edge from the source features gathered to edge shape
+        (:147-193): ``C x_0`` on the scalars, ``A z + (r/c)^{2n} e^{2 i n phi}
+        B conj(z)`` per copy of frequency n (``z`` the transported copy)."""
+        from gm_attention_amd.nn import eager_ops
+        from gm_attention_amd.representations.field_type import SO2FeatureField
+
+        if x.field_type != self.field_type:
+            raise ValueError(f"Expected a field of type {self.field_type!r}, got {x.field_type!r}.")
+        if tuple(x.batch_shape) != (edges.n_edges,):
+            raise ValueError(f"x.batch_shape must equal (edges.n_edges,) = ({edges.n_edges},), got "
+                             f"{tuple(x.batch_shape)}.")
+        self.validate_edges(edges)
+        return SO2FeatureField(self.field_type, eager_ops.depthwise_messages(self, x, edges))
 
     def extra_repr(self) -> str:
         return f"field_type={self.field_type!r}, cutoff={self.cutoff:.6g}"

@@ -8,13 +8,16 @@ device tensors, ``"cpu"`` accepted for compatibility), the same ``Plan`` /
 autograd Functions ``Softmax`` (:371-397) and ``Depthwise`` (:329-353), so the
 attention and convolution layers call it unchanged.  The arithmetic runs in
 ``libgmhip.so`` (``_native.attention()``); there is no CPU driver, so a CPU
-tensor reaching an op is an error rather than a silent fallback.
+tensor reaching an op itself is an error (the predicates send CPU tensors to
+the eager path first).
 
 Differences from the reference, all implementation limits rather than
 semantics: no neighbourhood-size bound (the reference declines when
 ``max_degree * heads > 8192``, which excludes the 256x512 grid); the key and
 value gradients are gathered per source node instead of added atomically,
-so they are deterministic; the geometry keeps a copy of the transport table
+so they are deterministic; a call the predicates decline runs the same
+numbers in torch (``eager_ops``) as the reference runs its eager path; the
+geometry keeps a copy of the transport table
 narrowed to the orders a layer reads; the per-edge tables live on the edge
 set they describe (built once, dropped with it) instead of a process-wide
 cache.
@@ -33,8 +36,9 @@ from torch import Tensor
 from gm_attention_amd import _native
 
 MAX_H, MAX_F, MAX_D, DESC = 8, 8, 512, 5
-#: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` accepted (no CPU driver in this build).
-#: The default is ``"1"``: this build's layers run only through the fused ops (``"0"`` makes them raise).
+#: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` accepted (no CPU driver in this build: CPU
+#: tensors take the eager path).  The default is ``"1"`` (the reference's is ``"0"``): this build exists
+#: to run the HIP path; a declined call runs ``eager_ops`` as the reference runs its eager layers.
 MODE = os.environ.get("GM_FUSED_ATTENTION", "1")
 
 
@@ -343,6 +347,15 @@ def softmax(mhsa: Any, q: Tensor, k: Tensor, edges: Any) -> Tensor:
     top = max((n for n, *_ in p.rows), default=0)
     return Softmax.apply(q.contiguous(), k.contiguous(), g.transport_to(top), g.bias, g.inside,
                          descriptors(mhsa, p, q.device), g.row_ptr, g.source, p.heads, scale, max(g.max_degree, 1))
+
+
+def softmax_eager(p: Plan, q: Tensor, k: Tensor, edges: Any, cutoff: float, window: str, scale: float) -> Tensor:
+    """The heads' attention weights ``(n_edges, heads)`` by :func:`eager_ops.softmax`
+    on the same geometry tables: the path of a call the fused op declines."""
+    from gm_attention_amd.nn import eager_ops
+
+    g = geometry(edges, cutoff, window, q.dtype)
+    return eager_ops.softmax(q, k, g.transport, g.bias, g.inside, p.rows, g.row_ptr, g.source, p.heads, scale)
 
 
 def softmax_head(head: Any, q: Tensor, k: Tensor, edges: Any) -> Tensor:

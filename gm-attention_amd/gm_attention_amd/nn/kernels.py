@@ -20,9 +20,9 @@ Restates the parts of the reference's ``nn/kernels.py`` the fused path needs:
   per-edge readout ``_forward_general`` (:752-915) through the fused pair
   terms (``fused_pairs.forward_general``).
 
-The eager per-edge readout and the eager factored branch are the parity
-oracle of this path and live with the tests, not here: a kernel whose fused
-op is not enabled raises instead of falling back.
+A call the fused ops decline (CPU tensors, a ``GM_FUSED_*`` switch at
+``"0"``, a plan beyond the kernels' bounds) runs the same numbers in torch
+(``eager_ops``), as the reference falls back to its eager branches.
 """
 
 from __future__ import annotations
@@ -134,10 +134,11 @@ class SO2SteerableKernel(nn.Module):
         from gm_attention_amd.nn import fused_pairs
 
         self.validate_call(x, edges)
-        if not fused_pairs.enabled(self, x, edges):
-            raise RuntimeError("the fused pair terms are not enabled for this call (GM_FUSED_PAIRS=1, device "
-                               "tensors, float32/64, blocks and trunk within 16 required)")
-        return fused_pairs.forward_general(self, x, edges)
+        if fused_pairs.enabled(self, x, edges):
+            return fused_pairs.forward_general(self, x, edges)
+        from gm_attention_amd.nn import eager_ops
+
+        return SO2FeatureField(self.field_type_out, eager_ops.readout(self, x, edges))
 
     # ---- the factored evaluation's pieces
 
@@ -208,17 +209,20 @@ class SO2SteerableKernel(nn.Module):
 
     def forward_factored(self, x: SO2FeatureField, edges, products=None, groups=None) -> SO2FeatureField:
         """The messages on the edges through the fused factored op (kernels.py:645-697)."""
-        from gm_attention_amd.nn import fused_factored
+        from gm_attention_amd.nn import eager_ops, fused_factored
 
-        if not fused_factored.enabled(self, x, edges):
-            raise RuntimeError(fused_factored.declined(self, x, edges))
-        return fused_factored.forward(self, x, edges, products, groups)
+        if fused_factored.enabled(self, x, edges):
+            return fused_factored.forward(self, x, edges, products, groups)
+        return SO2FeatureField.from_flat(self.field_type_out, eager_ops.factored_rows(self, x, edges, products))
 
     def forward_factored_aggregated(self, x: SO2FeatureField, edges, weights: Tensor, products=None,
                                     groups=None) -> SO2FeatureField:
         """Each target's weighted sum of its messages through the fused op (kernels.py:699-732)."""
-        from gm_attention_amd.nn import fused_factored
+        from gm_attention_amd.nn import eager_ops, fused_factored
 
-        if not fused_factored.enabled(self, x, edges):
-            raise RuntimeError(fused_factored.declined(self, x, edges))
-        return fused_factored.forward_aggregated(self, x, edges, weights, products, groups)
+        if fused_factored.enabled(self, x, edges):
+            return fused_factored.forward_aggregated(self, x, edges, weights, products, groups)
+        rows = eager_ops.factored_rows(self, x, edges, products)
+        return SO2FeatureField.from_flat(self.field_type_out,
+                                         eager_ops.segment_sum(weights.to(rows.dtype).unsqueeze(-1) * rows,
+                                                               edges.row_ptr))

@@ -241,3 +241,16 @@ def test_mhsa_float32_lanes_with_the_trunk_in_the_kernels_matches_the_oracle(cas
     ok, pa, pt = fused_factored.grouped_eligible(hp, torch.float32, 17)
     assert ok and fused_factored._lanes_apply(kernel, hp, pa, pt)
     test_mhsa_matches_the_oracle(case, torch.float32, True, cuda)
+
+
+def test_mhsa_with_the_fused_switches_off_takes_the_eager_path_on_the_gpu(cuda, monkeypatch):
+    """GM_FUSED_ATTENTION=0, GM_FUSED_FACTORED=0 (the reference's defaults):
+    device tensors run the eager path (nn/eager_ops, as the reference's
+    layers fall back at attention.py:880-886), float64, against the oracle."""
+    from gm_attention_amd.nn import eager_ops, fused_attention, fused_factored
+
+    monkeypatch.setattr(fused_attention, "MODE", "0")
+    monkeypatch.setattr(fused_factored, "MODE", "0")
+    before = eager_ops.calls.get("softmax", 0)
+    test_mhsa_matches_the_oracle(CASES[0], torch.float64, True, cuda)
+    assert eager_ops.calls.get("softmax", 0) > before

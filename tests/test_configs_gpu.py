@@ -87,13 +87,17 @@ def run_mhsa(module, flat, edges, probe, *, oracle, backward=True):
 
 
 def compare_mhsa(mhsa, x, edges, cuda, backward=True):
+    from gm_attention_amd.nn import eager_ops
+
     probe = problems.normal(x.shape, 7)
     want = run_mhsa(mhsa, x, edges.to(None, torch.float32).to(None, D64), probe, oracle=True, backward=backward)
     gpu = SO2MHSA(mhsa.field_type_in, len(mhsa.heads), cutoff=mhsa.cutoff, window="hard", batched=True,
                   dtype=torch.float32, device=cuda)
     gpu.load_state_dict({k: v.float() for k, v in mhsa.state_dict().items()})
+    before = dict(eager_ops.calls)
     got = run_mhsa(gpu, x.to(cuda, torch.float32), edges.to(cuda, torch.float32), probe.to(cuda), oracle=False,
                    backward=backward)
+    assert eager_ops.calls == before, "part of the layer fell back to the eager path"
     print(f"  out elementwise {strict_report(got[0], want[0]):.2f}", flush=True)
     assert_strict(got[0], want[0], "out")
     if not backward:
