@@ -302,89 +302,117 @@ __global__ __launch_bounds__(256) void aggregate_kernel(AggArgs<T> a) {
 // step with their loads in flight together, so every sum has a fixed order.
 struct AggHeadsArgs {
   const float* rows;   // (H, n_rows, d_out)
-  const float* alpha;  // (n_edges, H)
+  const float* alpha;  // (n_edges, H / split): row heads h and h' share a column when h / split == h' / split
   const int64_t* inv;
   const int64_t* row_ptr;
   float* out;  // (n_targets, H, d_out)
   int64_t n_targets, n_rows;
-  int H, d_out;
+  int H, d_out, split;
 };
 
 constexpr int kAggStep = 8;
 
+// One wave per target, lane l owning the 16-byte pieces l, l + 64, ...,
+// l + 64 (P - 1) of the target's H d_out outputs (piece o: row head o / q4,
+// columns 4 (o % q4) ..).  The rows are read in the CSR's edge order, so the
+// sums are each head's sums in that order.
+template <int P>
 __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a) {
   const int64_t i = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_targets, kWavesPerBlock) * kWavesPerBlock +
                     (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (i >= a.n_targets) return;
-  const int q4 = a.d_out / 4, W4 = a.H * q4;
-  const bool live = lane < W4;
-  const int hh = live ? lane / q4 : 0, c4 = live ? lane - hh * q4 : 0;
-  const float* base = a.rows + (int64_t)hh * a.n_rows * a.d_out + 4 * c4;
+  const int q4 = a.d_out / 4, W4 = a.H * q4, Ha = a.H / a.split;
+  bool live[P];
+  int ha[P];
+  const float* base[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int o = lane + 64 * p;
+    live[p] = o < W4;
+    const int hh = live[p] ? o / q4 : 0, c4 = live[p] ? o - hh * q4 : 0;
+    ha[p] = hh / a.split;
+    base[p] = a.rows + (int64_t)hh * a.n_rows * a.d_out + 4 * c4;
+  }
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
-  floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 s[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) s[p] = floatx4{0.f, 0.f, 0.f, 0.f};
   // the next batch's row indices are requested behind this batch's rows, so each
   // batch waits for one round trip rather than an index load and then the rows
   int64_t r[kAggStep];
 #pragma unroll
   for (int u = 0; u < kAggStep; ++u) r[u] = e0 + u < e1 ? a.inv[e0 + u] : 0;
   for (int64_t e = e0; e < e1; e += kAggStep) {
-    float w[kAggStep];
-    floatx4 v[kAggStep];
+    float w[kAggStep][P];
+    floatx4 v[kAggStep][P];
 #pragma unroll
-    for (int u = 0; u < kAggStep; ++u) {
-      const bool in = live && e + u < e1;
-      w[u] = in ? a.alpha[(e + u) * a.H + hh] : 0.f;
-      v[u] = in ? *reinterpret_cast<const floatx4*>(base + r[u] * a.d_out) : floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int u = 0; u < kAggStep; ++u)
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const bool in = live[p] && e + u < e1;
+        w[u][p] = in ? a.alpha[(e + u) * Ha + ha[p]] : 0.f;
+        v[u][p] = in ? *reinterpret_cast<const floatx4*>(base[p] + r[u] * a.d_out) : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
     for (int u = 0; u < kAggStep; ++u) {
       const int64_t n = e + kAggStep + u;
       r[u] = n < e1 ? a.inv[n] : 0;
     }
 #pragma unroll
-    for (int u = 0; u < kAggStep; ++u) s += w[u] * v[u];
+    for (int u = 0; u < kAggStep; ++u)
+#pragma unroll
+      for (int p = 0; p < P; ++p) s[p] += w[u][p] * v[u][p];
   }
-  if (live) *reinterpret_cast<floatx4*>(a.out + i * (int64_t)a.H * a.d_out + 4 * lane) = s;
+  float* o = a.out + i * (int64_t)a.H * a.d_out;
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+    if (live[p]) *reinterpret_cast<floatx4*>(o + 4 * (lane + 64 * p)) = s[p];
 }
+
+// Any d_out: lane l owns outputs l, l + 64, ... (at most kAggScalar of them).
+constexpr int kAggScalar = 16;
 
 __global__ __launch_bounds__(256) void aggregate_heads_kernel(AggHeadsArgs a) {
   const int64_t i = xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (i >= a.n_targets) return;
-  const int W = a.H * a.d_out;
-  int hh[3], cc[3];
-  bool live[3];
-#pragma unroll
-  for (int k = 0; k < 3; ++k) {
-    const int o = lane + 64 * k;
-    live[k] = o < W;
-    hh[k] = live[k] ? o / a.d_out : 0;
-    cc[k] = live[k] ? o - hh[k] * a.d_out : 0;
-  }
+  const int W = a.H * a.d_out, Ha = a.H / a.split;
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
-  float s[3] = {0.f, 0.f, 0.f};
-  for (int64_t e = e0; e < e1; e += 4) {
-    float w[4][3], v[4][3];
+  float* o = a.out + i * W;
+  for (int k0 = 0; k0 < kAggScalar; k0 += 4) {
+    if (64 * k0 >= W) break;
+    int hh[4], cc[4];
+    bool live[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const bool in = e + u < e1;
-      const int64_t r = in ? a.inv[e + u] : 0;
+    for (int k = 0; k < 4; ++k) {
+      const int c = lane + 64 * (k0 + k);
+      live[k] = c < W;
+      hh[k] = live[k] ? c / a.d_out : 0;
+      cc[k] = live[k] ? c - hh[k] * a.d_out : 0;
+    }
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t e = e0; e < e1; e += 4) {
+      float w[4][4], v[4][4];
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        w[u][k] = in && live[k] ? a.alpha[(e + u) * a.H + hh[k]] : 0.f;
-        v[u][k] = in && live[k] ? a.rows[((int64_t)hh[k] * a.n_rows + r) * a.d_out + cc[k]] : 0.f;
+      for (int u = 0; u < 4; ++u) {
+        const bool in = e + u < e1;
+        const int64_t r = in ? a.inv[e + u] : 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          w[u][k] = in && live[k] ? a.alpha[(e + u) * Ha + hh[k] / a.split] : 0.f;
+          v[u][k] = in && live[k] ? a.rows[((int64_t)hh[k] * a.n_rows + r) * a.d_out + cc[k]] : 0.f;
+        }
       }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s[k] += w[u][k] * v[u][k];
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int k = 0; k < 3; ++k) s[k] += w[u][k] * v[u][k];
+    for (int k = 0; k < 4; ++k)
+      if (live[k]) o[lane + 64 * (k0 + k)] = s[k];
   }
-  float* o = a.out + i * W;
-#pragma unroll
-  for (int k = 0; k < 3; ++k)
-    if (live[k]) o[lane + 64 * k] = s[k];
 }
 
 // dst_t[h, g] = src[perm[g], h] (a row gather and a transpose), and its
@@ -2758,21 +2786,28 @@ extern "C" int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, in
 
 extern "C" int gm_factored_aggregate_heads_f32(const float* rows, const int64_t* inv, const float* alpha,
                                                const int64_t* row_ptr, int64_t n_targets, int64_t n_edges, int64_t H,
-                                               int64_t d_out, float* out, void* stream) {
+                                               int64_t d_out, int64_t split, float* out, void* stream) {
   GM_REQUIRE(n_targets >= 0 && n_edges >= 0, "sizes must be non-negative");
-  GM_REQUIRE(H >= 1 && d_out >= 1 && H * d_out <= 192, "H d_out must be in [1, 192]");
+  GM_REQUIRE(H >= 1 && d_out >= 1 && H * d_out <= 64 * gm::kAggScalar, "H d_out must be in [1, 1024]");
+  GM_REQUIRE(split >= 1 && H % split == 0, "split must divide H");
   GM_REQUIRE(n_targets < (int64_t(1) << 31) * gm::kWavesPerBlock, "too many targets for one launch");
   if (n_targets == 0) return GM_OK;
   GM_REQUIRE(row_ptr && out && (n_edges == 0 || (rows && inv && alpha)),
              "rows, inv, alpha, row_ptr and out must be device pointers");
-  const gm::AggHeadsArgs a{rows, alpha, inv, row_ptr, out, n_targets, n_edges, (int)H, (int)d_out};
-  const bool vec = d_out % 4 == 0 && H * d_out <= 256 && gm::aligned(rows, 16) && gm::aligned(out, 16);
-  if (vec)
-    hipLaunchKernelGGL(gm::aggregate_heads_vec_kernel, dim3((unsigned)gm::blocks_for(n_targets)), dim3(256), 0,
-                       (hipStream_t)stream, a);
+  const gm::AggHeadsArgs a{rows, alpha, inv, row_ptr, out, n_targets, n_edges, (int)H, (int)d_out, (int)split};
+  const dim3 grid((unsigned)gm::blocks_for(n_targets)), block(256);
+  const int64_t pieces = d_out % 4 == 0 ? H * d_out / 4 : 0;
+  const bool vec = pieces > 0 && pieces <= 64 * 4 && gm::aligned(rows, 16) && gm::aligned(out, 16);
+  if (vec && pieces <= 64)
+    hipLaunchKernelGGL(gm::aggregate_heads_vec_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+  else if (vec && pieces <= 128)
+    hipLaunchKernelGGL(gm::aggregate_heads_vec_kernel<2>, grid, block, 0, (hipStream_t)stream, a);
+  else if (vec && pieces <= 192)
+    hipLaunchKernelGGL(gm::aggregate_heads_vec_kernel<3>, grid, block, 0, (hipStream_t)stream, a);
+  else if (vec)
+    hipLaunchKernelGGL(gm::aggregate_heads_vec_kernel<4>, grid, block, 0, (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL(gm::aggregate_heads_kernel, dim3((unsigned)gm::blocks_for(n_targets)), dim3(256), 0,
-                       (hipStream_t)stream, a);
+    hipLaunchKernelGGL(gm::aggregate_heads_kernel, grid, block, 0, (hipStream_t)stream, a);
   return gm::check_launch("factored_aggregate_heads");
 }
 

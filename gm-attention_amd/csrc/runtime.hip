@@ -28,8 +28,8 @@ int check_launch(const char* what) {
 int parse_attention_layout(const int64_t* desc, int64_t F, int64_t H, int64_t D, int64_t orders, AttnLayout& L) {
   GM_REQUIRE(desc != nullptr, "desc must be a host pointer to (F, 5) int64");
   GM_REQUIRE(F >= 0 && F <= GM_ATTN_MAX_F, "desc must have at most 8 frequency rows");
-  GM_REQUIRE(H >= 1 && H <= GM_ATTN_MAX_H, "at most 8 heads");
-  GM_REQUIRE(D >= 1 && D <= GM_ATTN_MAX_D, "D must be in [1, 512]");
+  GM_REQUIRE(H >= 1 && H <= GM_ATTN_MAX_H, "at most 16 heads");
+  GM_REQUIRE(D >= 1 && D <= GM_ATTN_MAX_D, "D must be in [1, 1024]");
   GM_REQUIRE(orders >= 1, "the phase tables need at least one order");
   L.F = (int)F;
   L.H = (int)H;

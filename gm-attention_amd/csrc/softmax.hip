@@ -53,7 +53,7 @@ struct SmArgs {
 };
 
 // ---------------------------------------------------------------- fast path
-// Every head segment is whole chunks of four reals; H in {1, 2, 4, 8}.
+// Every head segment is whole chunks of four reals; H in {1, 2, 4, 8, 16}.
 
 template <typename T>
 __device__ __forceinline__ T chunk_dot(const T* q4, const Quad<T>& k, int n, const T* tr) {
@@ -554,8 +554,8 @@ int prepare(SmArgs<T>& a, bool& fast, const T* q, const T* k, const T* transport
   a.H = (int)H;
   a.S = gm::kWave / (int)H;
   a.scale = (T)scale;
-  const bool pow2 = (H == 1 || H == 2 || H == 4 || H == 8);
-  a.hshift = H == 1 ? 0 : H == 2 ? 1 : H == 4 ? 2 : 3;
+  const bool pow2 = (H == 1 || H == 2 || H == 4 || H == 8 || H == 16);
+  a.hshift = H == 1 ? 0 : H == 2 ? 1 : H == 4 ? 2 : H == 8 ? 3 : 4;
   fast = pow2 && make_chunks(a.L, a.C) && aligned(q, 4 * sizeof(T)) && aligned(k, 4 * sizeof(T));
   return GM_OK;
 }

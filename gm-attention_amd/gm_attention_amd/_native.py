@@ -65,7 +65,7 @@ SIGNATURES_F32 = {
                                          + [_P] * 3),
     "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
     "gm_factored_lane_tables": (ctypes.c_int, [_P] + [_I] * 6 + [_P] * 3),
-    "gm_factored_aggregate_heads_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_P, _P]),
+    "gm_factored_aggregate_heads_f32": (ctypes.c_int, [_P] * 4 + [_I] * 5 + [_P, _P]),
     "gm_gather_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
     "gm_scatter_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
     "gm_conv_radial_partial_row": (ctypes.c_int64, []),
@@ -231,7 +231,7 @@ class AttentionExtension:
         for t in (k, transport, bias):
             _check(t.dtype == q.dtype, "q, k and the tables must share a dtype")
         _check(k.shape == q.shape, "q and k must share a shape")
-        _check(1 <= H <= 8, "at most 8 heads")
+        _check(1 <= H <= 16, "at most 16 heads")
         _check(transport.dim() == 3 and transport.shape[0] == e and transport.shape[2] == 2,
                "transport must be (n_edges, orders, 2)")
         _check(bias.dim() == 1 and bias.shape[0] == e, "bias must be (n_edges,)")
@@ -740,20 +740,22 @@ def lane_tables(desc: Tensor, wc: int, wr: int, d_out: int, pa: int, pt: int) ->
     return n.value, list(slot), list(slotcol)
 
 
-def aggregate_heads(rows: Tensor, inv: Tensor, alpha: Tensor, row_ptr: Tensor) -> Tensor:
-    """``out[i, h] = sum_e alpha[e, h] rows[h, inv[e]]`` over each target's
-    edges: rows ``(H, E, d_out)``, alpha ``(E, H)``; ``(N, H, d_out)`` out."""
+def aggregate_heads(rows: Tensor, inv: Tensor, alpha: Tensor, row_ptr: Tensor, split: int = 1) -> Tensor:
+    """``out[i, h] = sum_e alpha[e, h // split] rows[h, inv[e]]`` over each
+    target's edges: rows ``(H, E, d_out)``, alpha ``(E, H / split)``;
+    ``(N, H, d_out)`` out."""
     H, E, d_out = rows.shape
     n_targets = row_ptr.shape[0] - 1
     out = torch.empty(n_targets, H, d_out, dtype=rows.dtype, device=rows.device)
-    if rows.dtype != torch.float32 or alpha.dtype != torch.float32 or alpha.shape != (E, H):
-        raise ValueError("rows (H, E, d_out) and alpha (E, H) must be float32")
+    if split < 1 or H % split or rows.dtype != torch.float32 or alpha.dtype != torch.float32 \
+            or alpha.shape != (E, H // split):
+        raise ValueError("rows (H, E, d_out) and alpha (E, H / split) must be float32, split dividing H")
     if not (rows.is_contiguous() and alpha.is_contiguous() and inv.is_contiguous() and row_ptr.is_contiguous()):
         raise ValueError("rows, alpha, inv and row_ptr must be contiguous")
     if n_targets == 0:
         return out
     _call("gm_factored_aggregate_heads_f32", _ptr(rows), _ptr(inv), _ptr(alpha), _ptr(row_ptr), n_targets, E, H,
-          d_out, _ptr(out), _stream(rows.device))
+          d_out, split, _ptr(out), _stream(rows.device))
     return out
 
 

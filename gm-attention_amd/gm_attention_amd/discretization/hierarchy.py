@@ -98,11 +98,14 @@ class TensorGridHierarchy:
                                         lambda d: d.tile(count)),
             lambda e, source: e.tile(count, n_sources=self.levels[source].n_nodes))
 
-    def to(self, device) -> TensorGridHierarchy:
+    def to(self, device=None, dtype=None) -> TensorGridHierarchy:
+        """Every level and transfer on ``device``, the real tables in ``dtype``
+        (unchanged when None); neighbourhood membership stays the float64
+        construction's."""
         return self._mapped(
-            lambda level: level._mapped(lambda g: g.to(device=device), lambda f: f.to(device=device),
-                                        lambda d: d.to(device=device)),
-            lambda e, _source: e.to(device))
+            lambda level: level._mapped(lambda g: g.to(device, dtype), lambda f: f.to(device=device, dtype=dtype),
+                                        lambda d: d.to(device, dtype)),
+            lambda e, _source: e.to(device, dtype))
 
 
 def _hop(levels: Sequence[TensorGridLevel], source: int, target: int, cutoff: float,

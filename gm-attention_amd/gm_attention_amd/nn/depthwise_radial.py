@@ -13,9 +13,11 @@ weights and biases by the packing's autograd), the trunk's ``dW1``, ``db1``
 and ``dv``; parameter gradients are reduced in a fixed order.
 
 Serves float32 depthwise kernels with a ``Linear(B, 16) + SiLU`` trunk
-(``B`` in 4, 6, 8), at most 32 scalar copies and 64 copies of frequencies 1
-and 2 together, every multiplicity a multiple of 4; other kernels take the
-reference's split (``stacked_coefficients`` + ``fused_attention.Depthwise``).
+(``B`` in 4, 6, 8) and frequencies up to 2, every multiplicity a multiple of
+4.  One walk takes at most 32 scalar copies and 64 copies of frequencies 1
+and 2 together; a wider field runs as equal groups of copies, one walk each
+(``channel_groups``).  Other kernels take the reference's split
+(``stacked_coefficients`` + ``fused_attention.Depthwise``).
 """
 
 from __future__ import annotations
@@ -36,6 +38,23 @@ NS, NC = _native.RADIAL_TILES_SCALAR, _native.RADIAL_TILES_COMPLEX
 NT = NS + NC
 
 
+def channel_groups(ft: Any) -> tuple[tuple[tuple[int, int, int], ...], ...] | None:
+    """``None`` when one walk takes the whole field; else the field cut into
+    ``G`` equal groups of copies (each frequency's copies in G contiguous
+    ranges, a multiple of 4 each) that each fit one walk, as ``(n, start,
+    stop)`` per frequency; ``()`` when no such cut exists.  A depthwise
+    kernel maps every copy to itself from one radial trunk, so the groups'
+    outputs side by side are the layer's."""
+    a0 = ft.multiplicity(0) if 0 in ft else 0
+    complex_copies = sum(ft.multiplicity(n) for n in ft.frequencies if n != 0)
+    if a0 <= 16 * NS and complex_copies <= 4 * NC:
+        return None
+    g = max(-(-a0 // (16 * NS)), -(-complex_copies // (4 * NC)))
+    if any(m % (4 * g) for m in ft.multiplicities):
+        return ()
+    return tuple(tuple((n, k * m // g, (k + 1) * m // g) for n, m in ft.items()) for k in range(g))
+
+
 def eligible(kernel: Any, x: Any, edges: Any) -> bool:
     if not ENABLED or x.dtype != torch.float32 or x.device.type != "cuda":
         return False
@@ -45,50 +64,54 @@ def eligible(kernel: Any, x: Any, edges: Any) -> bool:
     if layers[0].out_features != 16 or layers[0].in_features not in (4, 6, 8):
         return False
     ft = kernel.field_type
-    a0 = ft.multiplicity(0) if 0 in ft else 0
-    complex_copies = 0
-    for n in ft.frequencies:
-        if n == 0:
-            continue
-        if n > 2 or ft.multiplicity(n) % 4 != 0:
-            return False
-        complex_copies += ft.multiplicity(n)
-    if a0 % 4 != 0 or a0 > 16 * NS or complex_copies > 4 * NC:
+    if any(n > 2 for n in ft.frequencies) or any(m % 4 for m in ft.multiplicities):
+        return False
+    if channel_groups(ft) == ():
         return False
     return edges.max_frequency >= 4 and edges.n_edges > 0
 
 
 class Packing:
-    """Where every row of the packed readout comes from, and the complex tiles."""
+    """Where every row of the packed readout comes from, the complex tiles and,
+    for a group of copies (``(n, start, stop)`` per frequency; None: every
+    copy), the node field's columns the group reads, in the walk's layout."""
 
-    def __init__(self, kernel: Any, device: torch.device):
+    def __init__(self, kernel: Any, device: torch.device, group: tuple[tuple[int, int, int], ...] | None = None):
         ft = kernel.field_type
-        a0 = ft.multiplicity(0) if 0 in ft else 0
+        ranges = {n: (0, m) for n, m in ft.items()} if group is None else {n: (c0, c1) for n, c0, c1 in group}
+        full_a0 = ft.multiplicity(0) if 0 in ft else 0
         wc = sum(4 * ft.multiplicity(n) for n in ft.frequencies if n != 0)
-        zero = a0 + wc  # index of the zero row in cat(real rows, complex rows, zero)
+        zero = full_a0 + wc  # index of the zero row in cat(real rows, complex rows, zero)
         rowmap = [zero] * (NT * 16)
+        s0, s1 = ranges.get(0, (0, 0))
+        a0 = s1 - s0
         for a in range(a0):
-            rowmap[a] = a
+            rowmap[a] = s0 + a
+        slices = ft.slices()
+        columns = list(range(slices[0].start + s0, slices[0].start + s1)) if 0 in ft else []
         tile_n, tile_col = [], []
-        copies = []  # (n, copy, coefficient offset, flat column) of every complex copy in tile order
-        coff, col = 0, a0
+        copies = []  # (n, copy, coefficient offset, column in the walk's layout) of every complex copy in tile order
+        coff = 0
         for n in ft.frequencies:
             if n == 0:
                 continue
             an = ft.multiplicity(n)
-            copies += [(n, cidx, coff, col) for cidx in range(an)]
+            c0, c1 = ranges[n]
+            for cidx in range(c0, c1):
+                copies.append((n, cidx, coff, len(columns)))
+                columns += [slices[n].start + 2 * cidx, slices[n].start + 2 * cidx + 1]
             coff += 4 * an
-            col += 2 * an
-        for u, (n, cidx, off, col0) in enumerate(copies):
+        for u, (n, cidx, off, col) in enumerate(copies):
             m, q = divmod(u, 4)
             an = ft.multiplicity(n)
             base = 16 * (NS + m) + 4 * q
             for r, src in enumerate((off + 2 * cidx, off + 2 * cidx + 1, off + 2 * an + 2 * cidx,
                                      off + 2 * an + 2 * cidx + 1)):
-                rowmap[base + r] = a0 + src
+                rowmap[base + r] = full_a0 + src
             if q == 0:
                 tile_n.append(n)
-                tile_col.append(col0 + 2 * cidx)
+                tile_col.append(col)
+        self.columns = None if group is None else torch.tensor(columns, dtype=torch.int64, device=device)
         self.a0 = a0
         self.ns = (a0 + 15) // 16
         self.rowmap = torch.tensor(rowmap, dtype=torch.int64, device=device)
@@ -113,11 +136,11 @@ class Packing:
         self.width = float(rb.width)
 
 
-def packing(kernel: Any, device: torch.device) -> Packing:
-    key = ("_radial_packing", str(device))
+def packing(kernel: Any, device: torch.device, group: tuple | None = None) -> Packing:
+    key = ("_radial_packing", str(device), group)
     p = kernel.__dict__.get(key)
     if p is None:
-        p = Packing(kernel, device)
+        p = Packing(kernel, device, group)
         kernel.__dict__[key] = p
     return p
 
@@ -175,12 +198,35 @@ class ConvRadial(torch.autograd.Function):
         return dv, dR, dw1, db1, None
 
 
+def _ungroup(kernel: Any, groups: tuple, device: torch.device) -> Tensor:
+    """For every column of the flat layout, its position in the groups' outputs side by side."""
+    key = ("_radial_ungroup", str(device))
+    inv = kernel.__dict__.get(key)
+    if inv is None:
+        cols = torch.cat([packing(kernel, device, g).columns for g in groups]).cpu()
+        inv = torch.empty_like(cols)
+        inv[cols] = torch.arange(cols.shape[0])
+        inv = inv.to(device)
+        kernel.__dict__[key] = inv
+    return inv
+
+
 def forward(conv: Any, v: Tensor, edges: Any) -> Tensor:
-    """The depthwise layer's aggregation ``(N, D)`` on the flat node field ``v``."""
+    """The depthwise layer's aggregation ``(N, D)`` on the flat node field
+    ``v``: one walk, or one walk per group of copies for fields wider than a
+    walk takes (each group reading its columns of ``v``, sharing the trunk)."""
     kernel = conv.kernel
-    p = packing(kernel, v.device)
     g = fused_attention.geometry(edges, conv.cutoff, conv.window, v.dtype)
     trunk = list(kernel.radial_trunk)[0]
-    meta = dict(packing=p, geometry=g, weights=g.aggregation_weights(bool(conv.normalize), float(conv.eps)),
-                centers=p.centers, width=p.width)
-    return ConvRadial.apply(v.contiguous(), packed_readout(kernel, p), trunk.weight, trunk.bias, meta)
+    weights = g.aggregation_weights(bool(conv.normalize), float(conv.eps))
+    groups = channel_groups(kernel.field_type)
+    v = v.contiguous()
+    outs = []
+    for group in (None,) if groups is None else groups:
+        p = packing(kernel, v.device, group)
+        meta = dict(packing=p, geometry=g, weights=weights, centers=p.centers, width=p.width)
+        vg = v if group is None else v.index_select(1, p.columns)
+        outs.append(ConvRadial.apply(vg, packed_readout(kernel, p), trunk.weight, trunk.bias, meta))
+    if groups is None:
+        return outs[0]
+    return torch.cat(outs, dim=1).index_select(1, _ungroup(kernel, groups, v.device))

@@ -35,7 +35,7 @@ from torch import Tensor
 
 from gm_attention_amd import _native
 
-MAX_H, MAX_F, MAX_D, DESC = 8, 8, 512, 5
+MAX_H, MAX_F, MAX_D, DESC = 16, 8, 1024, 5
 #: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` accepted (no CPU driver in this build: CPU
 #: tensors take the eager path).  The default is ``"1"`` (the reference's is ``"0"``): this build exists
 #: to run the HIP path; a declined call runs ``eager_ops`` as the reference runs its eager layers.

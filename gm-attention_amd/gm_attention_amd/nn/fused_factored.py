@@ -32,7 +32,7 @@ import torch
 from torch import Tensor
 
 from gm_attention_amd import _native
-from gm_attention_amd.representations.field_type import SO2FeatureField
+from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
 
 MAX_K, MAX_OUT, MAX_BM, MAX_C, DESC = 20, 128, 32, 320, 8
 MAX_C_MFMA = 128  # packed columns the float32 MFMA kernels take (K <= 17)
@@ -595,27 +595,93 @@ def heads_plan(kernel: Any) -> HeadsPlan:
     return result
 
 
-def _heads_mixing_from(kernels: list[Any], hp: HeadsPlan, params: list[list[Tensor | None]]) -> list[Tensor]:
-    """``heads_mixing`` from stand-in readout parameters (one list per head)."""
+class SubHead:
+    """The value kernel of one head restricted to an equal share of its output
+    copies: copies ``[s b_m / split, (s + 1) b_m / split)`` of every output
+    frequency, share ``s``.  A kernel's blocks are separable by output copy,
+    so a head's rows are its shares' rows side by side (per frequency); the
+    shares have the head's blocks, harmonic orders and powers, ``b_m / split``
+    copies each.  Stands in for the kernel where only the plan is read."""
+
+    def __init__(self, kernel: Any, split: int) -> None:
+        out = kernel.field_type_out
+        if any(m % split for m in out.multiplicities):
+            raise ValueError(f"split {split} does not divide every multiplicity of {out!r}")
+        self.kernel = kernel
+        self.split = split
+        self.field_type_in = kernel.field_type_in
+        self.field_type_out = SO2FieldType({f: m // split for f, m in out.items()})
+        self._pair_powers = kernel._pair_powers
+        self.complex_head, self.real_head = kernel.complex_head, kernel.real_head
+        self.radial_basis = kernel.radial_basis
+
+    def _blocks(self) -> list[tuple[int, int, str]]:
+        return self.kernel._blocks()
+
+
+def sub_head(kernel: Any, split: int) -> Any:
+    """``kernel`` itself for ``split == 1``, else its :class:`SubHead` (cached)."""
+    if split == 1:
+        return kernel
+    key = ("_sub_head", split)
+    sub = kernel.__dict__.get(key)
+    if sub is None:
+        sub = SubHead(kernel, split)
+        kernel.__dict__[key] = sub
+    return sub
+
+
+def share_columns(kernel: Any, split: int, heads: int, device: torch.device) -> Tensor:
+    """For column ``h d + c`` of the heads' rows ``(N, H, d)`` (each head in
+    the per-head flat layout), its column in the shares' rows
+    ``(N, H split, d / split)`` -- the gather that puts the shares' outputs
+    back side by side."""
+    key = ("_share_columns", split, heads, str(device))
+    cols = kernel.__dict__.get(key)
+    if cols is None:
+        out = kernel.field_type_out
+        part = SO2FieldType({f: m // split for f, m in out.items()})
+        full_s, part_s = out.slices(), part.slices()
+        d_part = part.dimension
+        index = []
+        for head in range(heads):
+            for f, m in out.items():
+                dim = 1 if f == 0 else 2
+                per = m // split
+                for c in range(full_s[f].stop - full_s[f].start):
+                    copy, re = divmod(c, dim)
+                    share, local = divmod(copy, per)
+                    index.append((head * split + share) * d_part + part_s[f].start + local * dim + re)
+        cols = torch.tensor(index, dtype=torch.int64, device=device)
+        kernel.__dict__[key] = cols
+    return cols
+
+
+def _heads_mixing_from(kernels: list[Any], hp: HeadsPlan, params: list[list[Tensor | None]],
+                       split: int = 1) -> list[Tensor]:
+    """``heads_mixing`` from stand-in readout parameters (one list per head);
+    with ``split > 1`` the columns run over the heads' shares (head-major)."""
     from gm_attention_amd.nn.node_products import mixing_matrix
 
     mats = []
     for n, blocks, _cw, _rw in hp.groups:
-        per_head = []
+        per_share = []
         for k, pk in zip(kernels, params, strict=True):
-            pieces = []
-            for b in blocks:
-                w = k._block_weights(b.block, pk)  # (b_m, a_n, K)
-                if b.kind == 0:
-                    m = mixing_matrix(w, "real")  # (a_0, K * b_0)
+            weights = {b.block: k._block_weights(b.block, pk) for b in blocks}  # (b_m, a_n, K) of the full head
+            for share in range(split):
+                pieces = []
+                for b in blocks:
+                    w = weights[b.block][share * b.b_m:(share + 1) * b.b_m]
+                    if b.kind == 0:
+                        m = mixing_matrix(w, "real")  # (a_0, K * b_0)
+                        pieces.append(m.reshape(m.shape[0], w.shape[-1], -1))
+                        continue
+                    bn, bm, role = b.block
+                    mode = "promote" if bn == 0 else ("conj" if (bm == 0 or role == "antilinear") else "plain")
+                    m = mixing_matrix(w, mode)  # (w_n, K * b_m * 2)
                     pieces.append(m.reshape(m.shape[0], w.shape[-1], -1))
-                    continue
-                bn, bm, role = b.block
-                mode = "promote" if bn == 0 else ("conj" if (bm == 0 or role == "antilinear") else "plain")
-                m = mixing_matrix(w, mode)  # (w_n, K * b_m * 2)
-                pieces.append(m.reshape(m.shape[0], w.shape[-1], -1))
-            per_head.append(torch.cat(pieces, dim=-1))  # (w_n, K, C_n)
-        stacked = torch.stack(per_head, dim=1)  # (w_n, H, K, C_n)
+                per_share.append(torch.cat(pieces, dim=-1))  # (w_n, K, C_n)
+        stacked = torch.stack(per_share, dim=1)  # (w_n, H split, K, C_n)
         mats.append(stacked.reshape(stacked.shape[0], -1))
     return mats
 
@@ -623,14 +689,14 @@ def _heads_mixing_from(kernels: list[Any], hp: HeadsPlan, params: list[list[Tens
 _MIXING_MAPS: OrderedDict = OrderedDict()
 
 
-def _mixing_maps(kernels: list[Any], hp: HeadsPlan) -> list[tuple[Tensor, Tensor]]:
+def _mixing_maps(kernels: list[Any], hp: HeadsPlan, split: int = 1) -> list[tuple[Tensor, Tensor]]:
     """Per input frequency, (index, sign) with ``M_n = sign * flat[index]``,
     ``flat`` the heads' readout parameters concatenated (``readout_parameters``
     order, head by head): found once by running the construction on the
     parameters' positions (+1) as float64 values, which it only moves and
     negates."""
     shapes = tuple(tuple(None if p is None else tuple(p.shape) for p in k.readout_parameters()) for k in kernels)
-    key = (tuple(id(k) for k in kernels), shapes)
+    key = (tuple(id(k) for k in kernels), shapes, split)
     hit = _MIXING_MAPS.get(key)
     if hit is not None:
         return hit
@@ -646,7 +712,7 @@ def _mixing_maps(kernels: list[Any], hp: HeadsPlan) -> list[tuple[Tensor, Tensor
             offset += p.numel()
         ids.append(per)
     maps = []
-    for m in _heads_mixing_from(kernels, hp, ids):
+    for m in _heads_mixing_from(kernels, hp, ids, split):
         index = (m.abs().round().long() - 1).clamp_min(0)
         maps.append((index.to(device), torch.sign(m).to(device)))
     _MIXING_MAPS[key] = maps
@@ -655,14 +721,16 @@ def _mixing_maps(kernels: list[Any], hp: HeadsPlan) -> list[tuple[Tensor, Tensor
     return maps
 
 
-def heads_mixing(kernels: list[Any], hp: HeadsPlan) -> list[Tensor]:
+def heads_mixing(kernels: list[Any], hp: HeadsPlan, split: int = 1) -> list[Tensor]:
     """Per input frequency n, ``M_n`` of ``(reals of x_n, H * K * C_n)``: columns
     ``(head, t, [complex pairs in packed order | the real block's columns])``,
     so ``X_n M_n`` is every head's ``Z_t`` for the blocks reading x_n.  Every
     entry is one readout parameter, possibly negated, or zero: the matrices
     are one gather from the heads' concatenated parameters (a handful of
-    kernels, differentiable) rather than a per-head, per-block build."""
-    maps = _mixing_maps(kernels, hp)
+    kernels, differentiable) rather than a per-head, per-block build.  With
+    ``split > 1``, ``hp`` is the shares' plan and the columns run over
+    ``H * split`` shares."""
+    maps = _mixing_maps(kernels, hp, split)
     flat = torch.cat([p.reshape(-1) for k in kernels for p in k.readout_parameters() if p is not None])
     return [flat[index] * sign.to(flat.dtype) for index, sign in maps]
 
@@ -828,22 +896,26 @@ def grouped_eligible(hp: HeadsPlan, h_dtype: torch.dtype, K: int) -> tuple[bool,
 class FactoredHeadsGrouped(torch.autograd.Function):
     """:class:`FactoredHeads` over the grouped streams: ``h_g (H, E, 16)`` in
     the grouping's order, ``alpha (E, H)`` in edge order, the mix arrays;
-    out ``(N, H, d_out)``; gradients ``dh_g``, ``dalpha`` and the mixes'."""
+    out ``(N, H split, d_out)``; gradients ``dh_g``, ``dalpha`` and the mixes'.
+    With ``meta["split"] > 1`` the launches run over the heads' shares (share
+    ``v`` of head ``v // split``), which read their head's trunk features and
+    attention weights."""
 
     @staticmethod
     def forward(ctx: Any, h_g: Tensor, alpha: Tensor, meta: dict, *mixes: Tensor) -> Tensor:
-        H, E = h_g.shape[0], h_g.shape[1]
+        E, split = h_g.shape[1], meta["split"]
         st: GroupedStreams = meta["streams"]
-        rows = torch.empty(H, E, meta["d_out"], dtype=h_g.dtype, device=h_g.device)
-        for head in range(H):
-            runs = _heads_runs(meta, mixes, head, None)
+        shares = meta["heads"]
+        rows = torch.empty(shares, E, meta["d_out"], dtype=h_g.dtype, device=h_g.device)
+        for v in range(shares):
+            runs = _heads_runs(meta, mixes, v, None)
             with torch.profiler.record_function("gm::kernel/pairs"):
-                _native.factored_forward_grouped(h_g[head], runs, meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g,
-                                                 st.pa, st.pt, meta["desc"], meta["group_ptr"], meta["group_source"],
-                                                 meta["group_order"], meta["K"], meta["wc"], meta["wr"],
-                                                 meta["d_out"], out=rows[head])
+                _native.factored_forward_grouped(h_g[v // split], runs, meta["n_nodes"], st.phase_g, st.rho_g,
+                                                 st.zw_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
+                                                 meta["group_source"], meta["group_order"], meta["K"], meta["wc"],
+                                                 meta["wr"], meta["d_out"], out=rows[v])
         with torch.profiler.record_function("gm::kernel/aggregate"):
-            out = _native.aggregate_heads(rows, st.inv, alpha, meta["row_ptr"])
+            out = _native.aggregate_heads(rows, st.inv, alpha, meta["row_ptr"], split)
         ctx.meta = meta
         ctx.save_for_backward(h_g, alpha, rows, *mixes)
         return out
@@ -854,22 +926,29 @@ class FactoredHeadsGrouped(torch.autograd.Function):
         meta = ctx.meta
         st: GroupedStreams = meta["streams"]
         h_g, alpha, rows, *mixes = ctx.saved_tensors
-        H = h_g.shape[0]
+        split, shares = meta["split"], meta["heads"]
         # every source node has a group (and so every mix row is written) unless some node has no edge out
         fill = torch.zeros_like if meta["group_source"].shape[0] < meta["n_nodes"] else torch.empty_like
         dmixes = [fill(m) for m in mixes]
         dh_g = torch.empty_like(h_g)
         alpha_gt = _native.gather_transpose(alpha, st.perm)  # (H, E) in the grouping's order
         dalpha_gt = torch.empty_like(alpha_gt)
+        part_dh = torch.empty_like(h_g[0]) if split > 1 else None
+        part_da = torch.empty_like(alpha_gt[0]) if split > 1 else None
         grad = grad.contiguous()
-        for head in range(H):
-            runs = _heads_runs(meta, mixes, head, dmixes)
+        for v in range(shares):
+            head, share = divmod(v, split)
+            runs = _heads_runs(meta, mixes, v, dmixes)
+            first = share == 0
             with torch.profiler.record_function("gm::kernel/pairs_backward"):
                 _native.factored_backward_grouped(
-                    grad[:, head].contiguous(), st.target_g, alpha_gt[head], rows[head], h_g[head], runs,
+                    grad[:, v].contiguous(), st.target_g, alpha_gt[head], rows[v], h_g[head], runs,
                     meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
-                    meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"], dh_g[head],
-                    dweights=dalpha_gt[head])
+                    meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"],
+                    dh_g[head] if first else part_dh, dweights=dalpha_gt[head] if first else part_da)
+            if not first:  # the head's shares read the same trunk features and weights: their gradients add
+                dh_g[head].add_(part_dh)
+                dalpha_gt[head].add_(part_da)
         dalpha = _native.scatter_transpose(dalpha_gt, st.perm)
         return (dh_g, dalpha, None, *dmixes)
 
@@ -954,6 +1033,26 @@ def _lanes_apply(kernel: Any, hp: HeadsPlan, pa: int, pt: int) -> bool:
     return hit
 
 
+def head_split(kernel: Any, K: int) -> int:
+    """Into how many shares of output copies each head's value kernel is cut
+    for the grouped kernels: 1 when its plan fits them as is, else the
+    smallest power of two (at most 8) dividing every output multiplicity
+    whose shares fit (packed mix width ``2 wc + wr <= 128``); 0 when none does."""
+    key = ("_head_split", K, os.environ.get("GM_FACTORED_GROUPED", "1"))
+    hit = kernel.__dict__.get(key)
+    if hit is None:
+        hit = 0
+        for split in (1, 2, 4, 8):
+            if any(m % split for m in kernel.field_type_out.multiplicities):
+                break
+            ok, _, _ = grouped_eligible(heads_plan(sub_head(kernel, split)), torch.float32, K)
+            if ok:
+                hit = split
+                break
+        kernel.__dict__[key] = hit
+    return hit
+
+
 def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any, alpha: Tensor, h: Tensor | None,
                              groups: tuple[Tensor, Tensor, Tensor], trunk=None) -> Tensor:
     """Every head's ``forward_factored_aggregated`` at once: ``(N, H, d_out)``.
@@ -961,23 +1060,27 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
     ``h`` is every head's trunk features in edge order; alternatively
     ``trunk(rho)`` computes them from ``rho = d / cutoff`` in whatever order
     it is given, which lets the grouped kernels have them in the grouping's
-    order directly."""
-    hp = heads_plan(kernels[0])
+    order directly.  Heads too wide for the grouped kernels run there as
+    shares of their output copies (:func:`head_split`)."""
     K = (h.shape[2] if h is not None else kernels[0].complex_head.in_features) + 1
     dtype = h.dtype if h is not None else x.dtype
+    split = head_split(kernels[0], K) if dtype == torch.float32 else 0
+    hp = heads_plan(sub_head(kernels[0], max(split, 1)))
     ok, pa, pt = grouped_eligible(hp, dtype, K)
-    if ok:
+    if ok and split:
         p = hp.plan
-        mixes = heads_mixes(x, hp, heads_mixing(kernels, hp))
+        unit = sub_head(kernels[0], split)
+        mixes = heads_mixes(x, hp, heads_mixing(kernels, hp, split))
         order, group_ptr, group_source = groups
         st = grouped_streams(edges, order, kernels[0].radial_basis.cutoff, pa, pt, dtype)
-        fused = FUSED_TRUNK and trunk is not None and _lanes_apply(kernels[0], hp, pa, pt)
+        fused = (FUSED_TRUNK and split == 1 and len(kernels) <= 8 and trunk is not None
+                 and _lanes_apply(kernels[0], hp, pa, pt))
         h_g = None if fused else (trunk(st.rho_g) if trunk is not None else h.index_select(1, st.perm))
         if st.group_order is None and os.environ.get("GM_FACTORED_LPT", "0") == "1":
             # the groups largest first: the long pole groups start early instead of trailing the launch
             st.group_order = torch.argsort(group_ptr[1:] - group_ptr[:-1], descending=True, stable=True).contiguous()
-        meta = dict(n_nodes=x.batch_shape[0], heads=len(kernels), K=K, wc=p.wc, wr=p.wr, d_out=p.d_out,
-                    groups=hp.groups, desc=_heads_desc(kernels[0], hp, x.device), group_ptr=group_ptr,
+        meta = dict(n_nodes=x.batch_shape[0], heads=len(kernels) * split, split=split, K=K, wc=p.wc, wr=p.wr,
+                    d_out=p.d_out, groups=hp.groups, desc=_heads_desc(unit, hp, x.device), group_ptr=group_ptr,
                     group_source=group_source, row_ptr=edges.row_ptr.contiguous(), streams=st,
                     group_order=st.group_order if os.environ.get("GM_FACTORED_LPT", "0") == "1" else None)
         if fused:
@@ -990,7 +1093,12 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
                 kernels[0].__dict__["_centers_host"] = centers
             meta.update(centers=centers, centers_t=rb.centers.contiguous(), width=float(rb.width))
             return FactoredHeadsTrunk.apply(w, b, alpha.to(dtype).contiguous(), meta, *mixes)
-        return FactoredHeadsGrouped.apply(h_g.contiguous(), alpha.to(dtype).contiguous(), meta, *mixes)
+        out = FactoredHeadsGrouped.apply(h_g.contiguous(), alpha.to(dtype).contiguous(), meta, *mixes)
+        if split == 1:
+            return out
+        n = out.shape[0]
+        cols = share_columns(kernels[0], split, len(kernels), out.device)
+        return out.reshape(n, -1).index_select(1, cols).reshape(n, len(kernels), -1)
     if h is None:
         h = trunk((edges.distances / kernels[0].radial_basis.cutoff).to(dtype).contiguous())
     return _forward_aggregated_heads_seg(kernels, x, edges, alpha, h, groups)

@@ -68,10 +68,20 @@ def stacked_trunk(kernels: list[Any]) -> tuple[Tensor, Tensor | None, Any]:
     return weight, None if biases[0] is None else torch.stack(biases), kernels[0].radial_basis
 
 
+#: heads one trunk launch evaluates (the kernel keeps every head's weights in registers)
+HEADS_PER_LAUNCH = 8
+
+
 def trunk_hidden_heads(kernels: list[Any], rho: Tensor) -> Tensor:
-    """The stacked heads' trunk features ``(H, E, 16)`` on ``rho = d / cutoff``."""
-    weight = torch.stack([list(k.radial_trunk)[0].weight for k in kernels])
-    biases = [list(k.radial_trunk)[0].bias for k in kernels]
-    bias = None if biases[0] is None else torch.stack(biases)
+    """The stacked heads' trunk features ``(H, E, 16)`` on ``rho = d / cutoff``,
+    at most ``HEADS_PER_LAUNCH`` heads a launch."""
     rb = kernels[0].radial_basis
-    return RadialTrunk.apply(rho.contiguous(), weight, bias, rb.centers.contiguous(), float(rb.width))
+    rho = rho.contiguous()
+    parts = []
+    for h0 in range(0, len(kernels), HEADS_PER_LAUNCH):
+        chunk = kernels[h0:h0 + HEADS_PER_LAUNCH]
+        weight = torch.stack([list(k.radial_trunk)[0].weight for k in chunk])
+        biases = [list(k.radial_trunk)[0].bias for k in chunk]
+        bias = None if biases[0] is None else torch.stack(biases)
+        parts.append(RadialTrunk.apply(rho, weight, bias, rb.centers.contiguous(), float(rb.width)))
+    return parts[0] if len(parts) == 1 else torch.cat(parts, dim=0)

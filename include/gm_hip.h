@@ -41,8 +41,8 @@ enum {
  * fused_attention.Plan.rows (fused_attention.py:74-114, fused/attention.h:57-63). */
 #define GM_ATTN_DESC 5
 #define GM_ATTN_MAX_F 8
-#define GM_ATTN_MAX_H 8
-#define GM_ATTN_MAX_D 512
+#define GM_ATTN_MAX_H 16
+#define GM_ATTN_MAX_D 1024
 
 /* Factored descriptor: one row per coefficient block, GM_FACT_DESC int32 columns
  * (kind, z_offset, b_m, angular, transport, power, out_offset, take_real) --
@@ -525,16 +525,18 @@ int gm_node_mix_backward_weight_noalloc_f32(const float* v, int64_t ldv, const f
                                             int64_t C, float* dM, void* stream);
 
 /* Every head's aggregate at once: out[i, h, :] = sum over target i's edges e
- * (CSR order) of alpha[e, h] rows[h, inv[e], :].  rows (H, n_edges, d_out)
- * holds each head's rows in the grouping's order (inv[e] = edge e's position
- * there), alpha (n_edges, H) and out (n_targets, H, d_out); H d_out <= 192.
+ * (CSR order) of alpha[e, h / split] rows[h, inv[e], :].  rows (H, n_edges,
+ * d_out) holds each row head's rows in the grouping's order (inv[e] = edge
+ * e's position there), alpha (n_edges, H / split) and out (n_targets, H,
+ * d_out); H d_out <= 1024.  split > 1 serves a layer whose heads' value rows
+ * are computed in split pieces of output copies sharing one attention weight.
  * Serves the heads of one layer at once where the reference aggregates each
  * head on its own (fused/factored_cpu.cpp:110-130 `aggregate`, called from
  * fused_factored.py:273-299 FactoredAggregate); the per-head sums are the
  * same, in the same edge order. */
 int gm_factored_aggregate_heads_f32(const float* rows, const int64_t* inv, const float* alpha, const int64_t* row_ptr,
-                                    int64_t n_targets, int64_t n_edges, int64_t H, int64_t d_out, float* out,
-                                    void* stream);
+                                    int64_t n_targets, int64_t n_edges, int64_t H, int64_t d_out, int64_t split,
+                                    float* out, void* stream);
 
 /* A row gather fused with a transpose, and its inverse:
  *   gm_gather_transpose_f32:  dst_t[h, g] = src[perm[g], h]   src (n, width), dst_t (width, n)

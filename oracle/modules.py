@@ -355,17 +355,19 @@ def depthwise_layer_messages(kernel, x: dict[int, Tensor], edges) -> dict[int, T
     return out
 
 
-def conv_forward(conv, x: dict[int, Tensor], edges, tolerance: float | None = None) -> dict[int, Tensor]:
+def conv_forward(conv, x: dict[int, Tensor], edges, tolerance: float | None = None,
+                 messages: str = "readout") -> dict[int, Tensor]:
     """``SO2Convolution.forward`` eagerly (reference nn/convolution.py:271-355):
     per-edge messages (the depthwise kernel's, or the general kernel's
-    per-edge readout), each weighted by the window times the quadrature
-    weight, summed per target, divided by the window mass under
-    ``normalize``, plus the self-intertwiner."""
+    per-edge readout or factored branch), each weighted by the window times
+    the quadrature weight, summed per target, divided by the window mass
+    under ``normalize``, plus the self-intertwiner."""
     if conv.depthwise:
         msgs = depthwise_layer_messages(conv.kernel, x, edges)
     else:
-        msgs = readout_messages(conv.kernel, x, edges.source_index, edges.distances, edges.angular_phases,
-                                edges.transport_phases)
+        evaluate = {"readout": readout_messages, "factored": factored_messages}[messages]
+        msgs = evaluate(conv.kernel, x, edges.source_index, edges.distances, edges.angular_phases,
+                        edges.transport_phases)
     d = edges.distances
     tol = tolerance if tolerance is not None else (1e-10 if d.dtype == torch.float64 else 1e-5)
     win = (d <= conv.cutoff + tol).to(d.dtype) if conv.window == "hard" else torch.relu(1.0 - (d / conv.cutoff) ** 2) ** 2
@@ -453,3 +455,72 @@ def encode_forward(enc, x: dict[int, Tensor], edges, tolerance: float | None = N
     weight = win * edges.tangent_quadrature_weights
     return {f: torch.segment_reduce(weight.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum", offsets=edges.row_ptr,
                                     axis=0) for f, m in msgs.items()}
+
+
+# ---------------------------------------------------------------- segmentation stage (C5)
+
+
+def low_pass(restriction, x0: Tensor, edges) -> Tensor:
+    """``IcoLowPassRestriction.forward`` (reference nn/blocks.py:508-600) on a
+    scalar field: per target, sum_j c(r) q x_j / max(sum_j c(r) q, eps), c the
+    quartic or hard window of the restriction's cutoff."""
+    d = edges.distances
+    if restriction.window == "hard":
+        win = (d <= restriction.cutoff + (1e-10 if d.dtype == torch.float64 else 1e-5)).to(d.dtype)
+    else:
+        win = torch.relu(1.0 - (d / restriction.cutoff) ** 2) ** 2
+    w = win * edges.tangent_quadrature_weights
+    mass = torch.segment_reduce(w, "sum", offsets=edges.row_ptr, axis=0).clamp_min(restriction.eps)
+    num = torch.segment_reduce(w.unsqueeze(-1) * x0.index_select(0, edges.source_index), "sum",
+                               offsets=edges.row_ptr, axis=0)
+    return num / mass.unsqueeze(-1)
+
+
+def segformer_block_forward(block, x: dict[int, Tensor], disc, tolerance: float | None = None,
+                            messages: str = "readout") -> dict[int, Tensor]:
+    """``GmSegformerBlock.forward`` (reference experiments/stanford_2d3ds/
+    model.py:225-237) without drop path: x + MHSA(LN1 x), then
+    x + W_out act(DWConv(W_in LN2 x)); each operator on the level's edges
+    within its own radius."""
+    attn = block.attention
+    mixed = mhsa_forward(attn, layer_norm(block.norm1, x), disc.edges_within(attn.cutoff), tolerance, messages)
+    x = {f: x[f] + mixed[f] for f in x}
+    hidden = linear(block.linear_in, layer_norm(block.norm2, x), block.hidden_field_type)
+    hidden = conv_forward(block.mix, hidden, disc.edges_within(block.mix.cutoff), tolerance)
+    hidden = linear(block.linear_out, gated(block.activation, hidden), block.field_type)
+    return {f: x[f] + hidden[f] for f in x}
+
+
+def segformer_forward(model, x0: Tensor, hierarchy, tolerance: float | None = None,
+                      messages: str = "readout") -> Tensor:
+    """``GmSegformer.forward`` (reference model.py:728-764 ``encode``, :823-880
+    ``decode``) for the benchmark's options: per stage the learned restriction
+    and its norm, the blocks, the stage norm; per stage a convolution readout
+    onto scalars; the fusion decoder (GELU(Linear) of the coarsest readout,
+    then per finer stage the carried channels low-passed over the lateral
+    edges, joined with the readout, GELU(Linear)); the low pass onto the input
+    grid over up_edges[0]; the head intertwiner.  ``x0`` is the input's
+    scalars; returns the logits ``(n_input, classes)``."""
+    feature = {0: x0}
+    features = []
+    for i in range(len(model.stages)):
+        disc = hierarchy.levels[i + 1].discretization
+        feature = encode_forward(model.merges[i].integral, feature, hierarchy.down_edges[i], tolerance, messages)
+        feature = layer_norm(model.merge_norms[i], feature)
+        for block in model.stages[i]:
+            feature = segformer_block_forward(block, feature, disc, tolerance, messages)
+        feature = layer_norm(model.stage_norms[i], feature)
+        features.append(feature)
+    readouts = []
+    for i, f in enumerate(features):
+        conv = model.readouts[i]
+        disc = hierarchy.levels[i + 1].discretization
+        readouts.append(conv_forward(conv, f, disc.edges_within(conv.cutoff), tolerance, messages)[0])
+    gelu = torch.nn.functional.gelu
+    fused = gelu(readouts[-1] @ model.fusion_in.weight.T + model.fusion_in.bias)
+    for j, k in enumerate(range(len(features) - 2, -1, -1)):
+        up = low_pass(model.lateral_interpolations[j], fused, hierarchy.lateral_edges[k])
+        lin = model.fusions[j]
+        fused = gelu(torch.cat([readouts[k], up], dim=-1) @ lin.weight.T + lin.bias)
+    fine = low_pass(model.final_interpolation, fused, hierarchy.up_edges[0])
+    return linear(model.head, {0: fine}, model.output_field_type)[0]

@@ -67,7 +67,9 @@ def run(module, flat, edges, probe, *, oracle=False, chunk=None, tolerance=None)
                                                   if p.grad is not None}
 
 
-CASES = [({0: 8, 1: 8, 2: 8}, 4, "hard", 2), ({0: 4, 1: 4, 2: 4}, 2, "quartic", 1), ({0: 6, 1: 3}, 3, "hard", 1)]
+CASES = [({0: 8, 1: 8, 2: 8}, 4, "hard", 2), ({0: 4, 1: 4, 2: 4}, 2, "quartic", 1), ({0: 6, 1: 3}, 3, "hard", 1),
+         # heads of {0: 8, 1: 8, 2: 8}: float32 runs the grouped kernels on two shares of each head's copies
+         ({0: 16, 1: 16, 2: 16}, 2, "hard", 1)]
 
 
 @pytest.mark.parametrize("batched", [True, False])

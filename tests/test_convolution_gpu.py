@@ -129,6 +129,9 @@ RADIAL_CASES = [
     ({0: 8, 2: 4}, "hard", False, "none", 1, 6),
     ({1: 8}, "quartic", False, "none", 1, 4),
     ({0: 20, 1: 12, 2: 28}, "hard", True, "none", 1, 8),
+    # wider than one walk: two and four groups of {0: 32, 1: 32, 2: 32} (the C5 stages' mixes)
+    ({0: 64, 1: 64, 2: 64}, "hard", True, "none", 1, 8),
+    ({0: 128, 1: 128, 2: 128}, "quartic", False, "none", 1, 8),
 ]
 
 
@@ -152,6 +155,8 @@ def test_radial_walk_matches_the_oracle(case, cuda):
     gpu.load_state_dict({k: v.float() for k, v in conv.state_dict().items()})
     e = edges.to(cuda, torch.float32)
     assert depthwise_radial.eligible(gpu.kernel, SO2FeatureField.from_flat(gpu.field_type_in, x.to(cuda).float()), e)
+    groups = depthwise_radial.channel_groups(gpu.kernel.field_type)
+    assert groups is None or len(groups) == max(field.values()) // 32
     got = run(gpu, x.to(cuda, torch.float32), e, probe)
     close(got[0], want[0], torch.float32, "out")
     close(got[1], want[1], torch.float32, "dx")

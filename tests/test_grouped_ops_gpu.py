@@ -17,21 +17,25 @@ def csr(degrees):
     return row_ptr
 
 
-@pytest.mark.parametrize("H,d_out", [(8, 20), (2, 12), (3, 6), (1, 1)])
-def test_aggregate_heads_matches_a_csr_sum(H, d_out, cuda):
-    """fp32: within 1e-5 of the largest |value| (sums of up to 70 products)."""
+@pytest.mark.parametrize("H,d_out,split", [(8, 20, 1), (2, 12, 1), (3, 6, 1), (1, 1, 1), (16, 20, 2), (32, 20, 2),
+                                           (16, 16, 4), (40, 7, 2), (64, 16, 1)])
+def test_aggregate_heads_matches_a_csr_sum(H, d_out, split, cuda):
+    """fp32: within 1e-5 of the largest |value| (sums of up to 70 products);
+    row heads h share alpha's column h // split; the 16-byte kernels take one
+    to four pieces a lane, other widths the scalar kernel."""
     g = torch.Generator().manual_seed(H * 100 + d_out)
     degrees = [0, 1, 5, 70, 3, 0, 17, 8, 64, 9]  # empty targets, one edge, more than one step of eight
     row_ptr = csr(degrees)
     E = int(row_ptr[-1])
     rows = torch.randn(H, E, d_out, generator=g)
-    alpha = torch.rand(E, H, generator=g)
+    alpha = torch.rand(E, H // split, generator=g)
     inv = torch.randperm(E, generator=g)
+    wide = alpha.repeat_interleave(split, dim=1)
     want = torch.zeros(len(degrees), H, d_out, dtype=torch.float64)
     for i in range(len(degrees)):
         for e in range(int(row_ptr[i]), int(row_ptr[i + 1])):
-            want[i] += alpha[e].double()[:, None] * rows[:, inv[e]].double()
-    got = _native.aggregate_heads(rows.to(cuda), inv.to(cuda), alpha.to(cuda), row_ptr.to(cuda)).cpu().double()
+            want[i] += wide[e].double()[:, None] * rows[:, inv[e]].double()
+    got = _native.aggregate_heads(rows.to(cuda), inv.to(cuda), alpha.to(cuda), row_ptr.to(cuda), split).cpu().double()
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5 * float(want.abs().max()))
 
 

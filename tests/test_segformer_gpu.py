@@ -1,0 +1,80 @@
+"""The C5 stage's model on the HIP path at the benchmark's widths and heads
+({0: 64, 1: 64, 2: 64} in 8 heads, then {0: 128, 1: 128, 2: 128} in 16: the
+heads' value kernels as two shares each on the grouped kernels, the mixes as
+two and four channel groups of the in-walk radial depthwise kernel, the
+softmax at D = 640, the restrictions' tiled factored aggregates, the low-pass
+interpolations on the gather kernels) on a small two-sample hierarchy,
+float32, against the oracle's float64 composition of the reference's model
+(oracle.modules.segformer_forward): the logits and the input's gradient
+elementwise within 1e-5 relative / 1e-6 absolute (of the largest entry),
+every parameter gradient within 1e-5 of its norm and its largest entry, or,
+for a gradient whose float32 value is dominated by cancellation (a query
+bias: a sum over every node of softmax gradients that sum to zero per
+target), no further from float64 than twice the eager float32 path's own
+error (the layers' torch path on the CPU, the reference's pure-PyTorch
+arithmetic); and nothing fell back to the eager path."""
+
+import pytest
+import torch
+
+import problems
+from gm_attention_amd.nn import eager_ops
+from gm_attention_amd.nn.segformer import build_stage_hierarchy, stage_radii
+from test_segformer import IMG, STAGES, run, small_model
+
+pytestmark = pytest.mark.gpu
+
+C5_TYPES = [{0: 64, 1: 64, 2: 64}, {0: 128, 1: 128, 2: 128}]
+C5_HEADS = (8, 16)
+
+
+def report(got, want):
+    """max |g - w| / (1e-5 |w| + 1e-6 max|w|): at most 1 passes."""
+    want, got = want.double().cpu(), got.double().cpu()
+    return float(((got - want).abs() / (1e-5 * want.abs() + 1e-6 * float(want.abs().max()))).max())
+
+
+def test_c5_model_matches_the_oracle(cuda):
+    radii = stage_radii(STAGES)
+    h = build_stage_hierarchy(IMG, STAGES, radii).tile(2)
+    print(f"c5 model on {IMG} -> {STAGES}, batch 2", flush=True)
+    model = small_model(C5_TYPES, C5_HEADS, radii, normalized_mix=True, normalized_readout=True)
+    model.eval()
+    model.load_state_dict({k: v.float().double() for k, v in model.state_dict().items()})
+    n0 = h.levels[0].n_nodes
+    x0 = torch.rand(n0, 4, generator=torch.Generator().manual_seed(1), dtype=torch.float64).float().double()
+    probe = problems.normal((n0, 13), 2)
+    want = run(model, x0, h.to(None, torch.float32).to(None, torch.float64), probe, oracle=True, tolerance=1e-5,
+               messages="factored")
+    gpu = small_model(C5_TYPES, C5_HEADS, radii, dtype=torch.float32, device=cuda, normalized_mix=True,
+                      normalized_readout=True)
+    gpu.eval()
+    gpu.load_state_dict({k: v.float() for k, v in model.state_dict().items()})
+    cpu32 = small_model(C5_TYPES, C5_HEADS, radii, dtype=torch.float32, normalized_mix=True, normalized_readout=True)
+    cpu32.eval()
+    cpu32.load_state_dict({k: v.float() for k, v in model.state_dict().items()})
+    eager = run(cpu32, x0.float(), h.to(None, torch.float32), probe)
+    before = dict(eager_ops.calls)
+    got = run(gpu, x0.float().to(cuda), h.to(cuda, torch.float32), probe)
+    assert eager_ops.calls == before, "part of the model fell back to the eager path"
+    out, dx = report(got[0], want[0]), report(got[1], want[1])
+    print(f"strict ratio: logits {out:.3f}, dx {dx:.3f}", flush=True)
+    assert out <= 1.0 and dx <= 1.0
+    assert set(got[2]) == set(want[2])
+    worst = 0.0
+    for name in want[2]:
+        g, w = got[2][name].double().cpu(), want[2][name].double().cpu()
+        if float(w.abs().max()) < 1e-6:  # a gradient the softmax or a zero-mean norm makes vanish
+            assert float(g.abs().max()) <= 1e-5, name
+            continue
+        err = float((g - w).norm() / w.norm())
+        peak = float((g - w).abs().max() / w.abs().max())
+        worst = max(worst, err, peak)
+        if err <= 1e-5 and peak <= 1e-5:
+            continue
+        e = eager[2][name].double()
+        e_err, e_peak = float((e - w).norm() / w.norm()), float((e - w).abs().max() / w.abs().max())
+        print(f"{name}: relative error {err:.3e}, peak {peak:.3e}; eager float32 {e_err:.3e}, {e_peak:.3e}",
+              flush=True)
+        assert err <= 2 * e_err and peak <= 2 * e_peak, f"{name}: further from float64 than the eager float32 path"
+    print(f"parameter gradients: worst norm/peak error {worst:.3e}", flush=True)

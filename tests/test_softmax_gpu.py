@@ -23,9 +23,12 @@ CASES = [
     (16, 32, 2, {0: 32, 1: 32, 2: 32}, 8, "quartic"),
     (12, 24, 1, {0: 4, 1: 4}, 1, "quartic"),
     (12, 24, 1, {0: 8, 2: 8}, 2, "hard"),
-    # ... and the generic path (odd segments, three heads)
+    (16, 32, 1, {0: 128, 1: 128, 2: 128}, 16, "hard"),  # D = 640, 16 heads of ten chunks
+    (12, 24, 1, {0: 64, 1: 64, 2: 64}, 8, "quartic"),
+    # ... and the generic path (odd segments, three heads; sixteen heads of 20 chunks)
     (12, 24, 1, {0: 6, 1: 4, 2: 2}, 2, "quartic"),
     (10, 20, 1, {0: 3, 1: 3, 2: 3}, 3, "hard"),
+    (10, 20, 1, {0: 256, 1: 128, 2: 128}, 16, "hard"),  # D = 768
 ]
 
 
@@ -115,9 +118,9 @@ def test_checks_raise_the_reference_messages(cuda):
     with pytest.raises(RuntimeError, match="q and k must share a shape"):
         ext.softmax_forward(q, q[:, :4].contiguous(), t.transport.float().to(cuda), t.bias.float().to(cuda),
                             t.inside.to(cuda), desc.to(cuda), t.row_ptr.to(cuda), t.source.to(cuda), 2, scale, 1)
-    with pytest.raises(RuntimeError, match="at most 8 heads"):
+    with pytest.raises(RuntimeError, match="at most 16 heads"):
         ext.softmax_forward(q, q, t.transport.float().to(cuda), t.bias.float().to(cuda), t.inside.to(cuda),
-                            desc.to(cuda), t.row_ptr.to(cuda), t.source.to(cuda), 9, scale, 1)
+                            desc.to(cuda), t.row_ptr.to(cuda), t.source.to(cuda), 17, scale, 1)
     with pytest.raises(RuntimeError, match="GPU only"):
         ext.softmax_forward(q.cpu(), q.cpu(), t.transport.float(), t.bias.float(), t.inside, desc, t.row_ptr,
                             t.source, 2, scale, 1)
