@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "split.hpp"
 
 namespace gm {
 namespace {
@@ -1682,22 +1683,12 @@ __device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amd
   return t;
 }
 
-// One forward tile: 16 edges from tb, the rows stored through out_r.
+// Edge m's outputs from u (slot s at acc[s / 2][2 (s % 2)], +1 imaginary):
+// V = F u per slot, summed over each output's slots and stored.
 template <int NT, class P>
-__device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const FwdTile<P>& cur, const float (&za)[NT][4],
-                                             const floatx4 (&z0)[NT], float* Ph, __amdgpu_buffer_rsrc_t out_r,
-                                             int d_out, int tb, int m, int q, const TrunkLane& tl, bool fused) {
-  // h(edge m)[4 q .. 4 q + 3]: read, or the trunk's features evaluated here
-  floatx4 pre;
-  const floatx4 h = fused ? trunk_features(a, tl, q, cur.rho, pre) : cur.h;
-  // u(e) = Z0 + sum_t h_t Z_t: lane (m, q) ends with edge m's slot columns 16 nt + 4 q + r
-  floatx4 acc[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) acc[nt] = z0[nt];
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], h[s], acc[nt]);
+__device__ __forceinline__ void forward_outputs(const FactArgs<float>& a, const FwdTile<P>& cur,
+                                                const floatx4 (&acc)[NT], float* Ph, __amdgpu_buffer_rsrc_t out_r,
+                                                int d_out, int tb, int m, int q) {
   if constexpr (kHorner<P>) {
     f2_forward_outputs(acc, cur.ph.ph, out_r, (tb + m) * d_out, q);
     return;
@@ -1739,9 +1730,47 @@ __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const Fwd
   if constexpr (!P::kStatic) wave_sync();
 }
 
-template <int NT, class P, bool FUSED>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED ? 3 : 4) : 1))) void
+// One forward tile: 16 edges from tb, the rows stored through out_r.
+template <int NT, class P>
+__device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const FwdTile<P>& cur, const float (&za)[NT][4],
+                                             const floatx4 (&z0)[NT], float* Ph, __amdgpu_buffer_rsrc_t out_r,
+                                             int d_out, int tb, int m, int q, const TrunkLane& tl, bool fused) {
+  // h(edge m)[4 q .. 4 q + 3]: read, or the trunk's features evaluated here
+  floatx4 pre;
+  const floatx4 h = fused ? trunk_features(a, tl, q, cur.rho, pre) : cur.h;
+  // u(e) = Z0 + sum_t h_t Z_t: lane (m, q) ends with edge m's slot columns 16 nt + 4 q + r
+  floatx4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = z0[nt];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], h[s], acc[nt]);
+  forward_outputs<NT, P>(a, cur, acc, Ph, out_r, d_out, tb, m, q);
+}
+
+// forward_tile with the product on the bf16 matrix cores (fixed slots, trunk
+// features read): Z's pieces for the lane's features 4 q .. 4 q + 3 at columns
+// 16 nt + m are held for the group, h's are split per tile.
+// Z's row 0 (the bias feature) is read from the LDS copy per tile.
+template <int NT, class P>
+__device__ __forceinline__ void forward_tile_split(const FactArgs<float>& a, const FwdTile<P>& cur,
+                                                   const SplitA (&zs)[NT], const float* Zs, float* Ph,
+                                                   __amdgpu_buffer_rsrc_t out_r, int d_out, int tb, int m, int q) {
+  const SplitB hb = split_b(cur.h[0], cur.h[1], cur.h[2], cur.h[3]);
+  floatx4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    acc[nt] = mfma_split(zs[nt], hb, *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q));
+  forward_outputs<NT, P>(a, cur, acc, Ph, out_r, d_out, tb, m, q);
+}
+
+// SPLIT (fixed slots, trunk features read): the product on the bf16 matrix
+// cores in fp32 accuracy.
+template <int NT, class P, bool FUSED, bool SPLIT>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED || SPLIT ? 3 : 4) : 1))) void
 factored_forward_lanes(FactArgs<float> a) {
+  static_assert(!SPLIT || (P::kStatic && !FUSED), "the split product serves fixed slots with trunk features read");
   constexpr int ZS = 16 * NT + 4;
   __shared__ __align__(16) float Zs[17 * ZS];
   __shared__ __align__(16) float Ph[P::kStatic ? 4 : kMT * kPhStride];
@@ -1769,22 +1798,36 @@ factored_forward_lanes(FactArgs<float> a) {
   z_issue<P::kStatic>(a, j, lane, zst);
   wave_sync();
   z_commit<ZS>(a, j, Zs, colslot, lane, zst);
-  float za[NT][4];
-  floatx4 z0[NT];
+  float za[SPLIT ? 1 : NT][4];
+  SplitA zs[SPLIT ? NT : 1];
+  floatx4 z0[SPLIT ? 1 : NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
+    float zt[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) za[nt][s] = Zs[(1 + 4 * q + s) * ZS + 16 * nt + m];
-    z0[nt] = *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q);
+    for (int s = 0; s < 4; ++s) zt[s] = Zs[(1 + 4 * q + s) * ZS + 16 * nt + m];
+    if constexpr (SPLIT) {
+      zs[nt] = split_a(zt[0], zt[1], zt[2], zt[3]);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) za[nt][s] = zt[s];
+      z0[nt] = *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q);
+    }
   }
   TrunkLane tl{};
   if (fused) tl = trunk_lane(a, m, q);
   for (int tb = 0;;) {
-    forward_tile<NT, P>(a, ta, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
+    if constexpr (SPLIT)
+      forward_tile_split<NT, P>(a, ta, zs, Zs, Ph, out_r, d_out, tb, m, q);
+    else
+      forward_tile<NT, P>(a, ta, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
     ta = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
     tb += kMT;
     if (tb >= ng) break;
-    forward_tile<NT, P>(a, tbf, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
+    if constexpr (SPLIT)
+      forward_tile_split<NT, P>(a, tbf, zs, Zs, Ph, out_r, d_out, tb, m, q);
+    else
+      forward_tile<NT, P>(a, tbf, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
     tbf = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
     tb += kMT;
     if (tb >= ng) break;
@@ -2432,9 +2475,11 @@ void launch_lanes_nt(bool forward, const FactArgs<float>& a, hipStream_t stream)
   const bool fused = a.trunk_w != nullptr;  // the trunk evaluated in the kernels: their own instantiation
   if (forward) {
     if (fused)
-      hipLaunchKernelGGL((factored_forward_lanes<NT, P, true>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((factored_forward_lanes<NT, P, true, false>), grid, block, 0, stream, a);
+    else if (P::kStatic && split_products())
+      hipLaunchKernelGGL((factored_forward_lanes<NT, P, false, P::kStatic>), grid, block, 0, stream, a);
     else
-      hipLaunchKernelGGL((factored_forward_lanes<NT, P, false>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((factored_forward_lanes<NT, P, false, false>), grid, block, 0, stream, a);
   } else {
     if (fused)
       hipLaunchKernelGGL((factored_backward_lanes<NT, P, true>), grid, block, 0, stream, a);

@@ -34,6 +34,7 @@
 #include <mutex>
 
 #include "common.hpp"
+#include "split.hpp"
 
 // The weight gradient's partials for gm_node_mix_backward_weight_noalloc_f32:
 // 2^23 floats (32 MiB) on every GPU the library runs on, held until the process
@@ -463,6 +464,303 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_k_kernel(const floa
     }
 }
 
+// ---------------------------------------------------------------- split products
+//
+// The same three products for vectors up to 64 reals, with every fp32 product
+// formed as six bf16 products on v_mfma_f32_16x16x32_bf16 (three-piece splits,
+// fp32 accuracy: split.hpp).  A 16-deep contraction chunk kc gives lane
+// (c, q) the indices 16 kc + 4 q + s, s < 4, in both operands.
+
+// Forward: wave wv of workgroup x owns columns x * 128 + 32 wv + 16 j + c
+// (j < 2); the pieces of M at those columns are split once per wave and held
+// in registers; v's 64-row tiles come through LDS as in the fp32 kernel and
+// each wave splits its B operands from them.
+template <int W>
+__global__ __launch_bounds__(kThreads) void node_mix_forward_split(const float* __restrict__ v, int64_t ldv,
+                                                                   const float* __restrict__ M, int64_t N, int w,
+                                                                   int64_t C, float* __restrict__ out, int vec_v,
+                                                                   int vec_out) {
+  constexpr int KC = W / 16, CT = 2;
+  constexpr int LDT = W + 4;
+  constexpr int QUADS = 64 * W / 4;
+  constexpr int PER = (QUADS + kThreads - 1) / kThreads;
+  __shared__ __align__(16) float vt[64 * LDT];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
+  const int64_t col0 = (int64_t)blockIdx.x * (64 * CT) + 16 * CT * wv;
+  SplitA ma[KC][CT];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+    for (int j = 0; j < CT; ++j) {
+      const int64_t col = col0 + 16 * j + c;
+      float x[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int k = 16 * kc + 4 * q + s;
+        x[s] = (k < w && col < C) ? M[(int64_t)k * C + col] : 0.f;
+      }
+      ma[kc][j] = split_a(x[0], x[1], x[2], x[3]);
+    }
+  const int64_t n_tiles = (N + 63) / 64;
+  float4 pre[PER];
+  auto fetch = [&](int64_t tile) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      const int row = idx / (W / 4), k = 4 * (idx % (W / 4));
+      const int64_t r = tile * 64 + row;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (idx < QUADS && r < N) {
+        const float* src = v + r * ldv + k;
+        if (vec_v && k + 3 < w) {
+          x = *reinterpret_cast<const float4*>(src);
+        } else {
+          x.x = k < w ? src[0] : 0.f;
+          x.y = k + 1 < w ? src[1] : 0.f;
+          x.z = k + 2 < w ? src[2] : 0.f;
+          x.w = k + 3 < w ? src[3] : 0.f;
+        }
+      }
+      pre[p] = x;
+    }
+  };
+  if ((int64_t)blockIdx.y < n_tiles) fetch(blockIdx.y);
+  for (int64_t tile = blockIdx.y; tile < n_tiles; tile += gridDim.y) {
+    __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      if (idx < QUADS) *reinterpret_cast<float4*>(&vt[(idx / (W / 4)) * LDT + 4 * (idx % (W / 4))]) = pre[p];
+    }
+    __syncthreads();
+    if (tile + gridDim.y < n_tiles) fetch(tile + gridDim.y);
+    const int64_t row0 = tile * 64;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      floatx4 acc[CT];
+#pragma unroll
+      for (int j = 0; j < CT; ++j) acc[j] = kZero4;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const float4 x = *reinterpret_cast<const float4*>(&vt[(16 * rt + c) * LDT + 16 * kc + 4 * q]);
+        const SplitB b = split_b(x.x, x.y, x.z, x.w);
+#pragma unroll
+        for (int j = 0; j < CT; ++j) acc[j] = mfma_split(ma[kc][j], b, acc[j]);
+      }
+      const int64_t row = row0 + 16 * rt + c;
+      if (row < N) {
+        float* dst = out + row * C;
+#pragma unroll
+        for (int j = 0; j < CT; ++j) {
+          const int64_t col = col0 + 16 * j + 4 * q;
+          if (vec_out && col + 3 < C) {
+            *reinterpret_cast<float4*>(dst + col) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (col + i < C) dst[col + i] = acc[j][i];
+          }
+        }
+      }
+    }
+  }
+}
+
+// Input gradient: 128-row tiles as in the fp32 kernel, each wave 32 rows over
+// the whole contraction; a 64-column chunk of dmix is staged as fp32 (each
+// wave splits its own rows' A operands), the chunk of M as three bf16 planes
+// split once per workgroup; running totals every four chunks.
+template <int W>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void node_mix_dinput_split(const float* __restrict__ dmix,
+                                                                  const float* __restrict__ M, int64_t N, int w,
+                                                                  int64_t C, float* __restrict__ dv, int64_t lddv) {
+  constexpr int KC = 64, LDD = KC + 4, LDM = KC + 8, JW = W / 16;
+  constexpr int DQ = 128 * KC / 4 / kThreads;
+  constexpr int MQ = W * KC / 4 / kThreads;
+  __shared__ __align__(16) float dt[128 * LDD];
+  __shared__ __align__(16) uint16_t mp[3][W * LDM];  // M's hi, mid and lo pieces, row k of M at k * LDM
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * 128;
+  const int64_t n_chunks = (C + KC - 1) / KC;
+  float4 pd[DQ], pm[MQ];
+  auto fetch = [&](int64_t ch) {
+    const int64_t c0 = ch * KC;
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int64_t r = row0 + row, col = c0 + 4 * cq;
+      pd[p] = (r < N && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int p = 0; p < MQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int64_t col = c0 + 4 * cq;
+      pm[p] = (row < w && col < C) ? *reinterpret_cast<const float4*>(M + (int64_t)row * C + col)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  floatx4 acc[2][JW], tot[2][JW];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int j = 0; j < JW; ++j) acc[rt][j] = tot[rt][j] = kZero4;
+  fetch(0);
+  for (int64_t ch = 0; ch < n_chunks; ++ch) {
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      *reinterpret_cast<float4*>(&dt[(idx >> 4) * LDD + 4 * (idx & 15)]) = pd[p];
+    }
+#pragma unroll
+    for (int p = 0; p < MQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, at = (idx >> 4) * LDM + 4 * (idx & 15);
+      const Split4 sp = split4(pm[p].x, pm[p].y, pm[p].z, pm[p].w);
+      *reinterpret_cast<uint2*>(&mp[0][at]) = make_uint2(sp.hi[0], sp.hi[1]);
+      *reinterpret_cast<uint2*>(&mp[1][at]) = make_uint2(sp.mid[0], sp.mid[1]);
+      *reinterpret_cast<uint2*>(&mp[2][at]) = make_uint2(sp.lo[0], sp.lo[1]);
+    }
+    __syncthreads();
+    if (ch + 1 < n_chunks) fetch(ch + 1);
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      SplitA a[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const float4 x = *reinterpret_cast<const float4*>(&dt[(32 * wv + 16 * rt + c) * LDD + 16 * kc + 4 * q]);
+        a[rt] = split_a(x.x, x.y, x.z, x.w);
+      }
+#pragma unroll
+      for (int j = 0; j < JW; ++j) {
+        const int at = (16 * j + c) * LDM + 16 * kc + 4 * q;
+        const uint2 hi = *reinterpret_cast<const uint2*>(&mp[0][at]);
+        const uint2 mid = *reinterpret_cast<const uint2*>(&mp[1][at]);
+        const uint2 lo = *reinterpret_cast<const uint2*>(&mp[2][at]);
+        const SplitB b{u32x4{hi.x, hi.y, hi.x, hi.y}, u32x4{mid.x, mid.y, mid.x, mid.y}, u32x4{lo.x, lo.y, hi.x, hi.y}};
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) acc[rt][j] = mfma_split(a[rt], b, acc[rt][j]);
+      }
+    }
+    if ((ch & 3) == 3 || ch + 1 == n_chunks) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int j = 0; j < JW; ++j) {
+          tot[rt][j] += acc[rt][j];
+          acc[rt][j] = kZero4;
+        }
+    }
+  }
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int j = 0; j < JW; ++j) {
+      const int col = 16 * j + c;
+      if (col >= w) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t r = row0 + 32 * wv + 16 * rt + 4 * q + i;
+        if (r < N) dv[r * lddv + col] = tot[rt][j][i];
+      }
+    }
+}
+
+// Weight gradient for vectors up to 64 reals: the fp32 four-partials kernel's
+// tiling (each wave 16 rows of every 64-row chunk over the workgroup's whole
+// w x 64 tile, one partial per wave), a wave's 16 rows forming one contraction
+// chunk of split products.
+template <int W>
+__global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const float* __restrict__ v, int64_t ldv,
+                                                                   const float* __restrict__ dmix, int64_t N, int w,
+                                                                   int64_t C, int64_t rps, float* __restrict__ partial,
+                                                                   int vec_v) {
+  constexpr int RC = 64, LDV = dweight_ldv<W>(), LDM = 64 + 16, IW = W / 16;
+  constexpr int VQ = (RC * W / 4 + kThreads - 1) / kThreads;
+  constexpr int DQ = RC * 64 / 4 / kThreads;
+  __shared__ __align__(16) float vt[RC * LDV];
+  __shared__ __align__(16) float dt[RC * LDM];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 64;
+  const int64_t first = (int64_t)blockIdx.y * rps, last = first + rps < N ? first + rps : N;
+  float4 pv[VQ], pd[DQ];
+  auto fetch = [&](int64_t r0) {
+#pragma unroll
+    for (int p = 0; p < VQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx / (W / 4), k = 4 * (idx % (W / 4));
+      const int64_t r = r0 + row;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (idx < RC * W / 4 && r < last) {
+        const float* src = v + r * ldv + k;
+        if (vec_v && k + 3 < w) {
+          x = *reinterpret_cast<const float4*>(src);
+        } else {
+          x.x = k < w ? src[0] : 0.f;
+          x.y = k + 1 < w ? src[1] : 0.f;
+          x.z = k + 2 < w ? src[2] : 0.f;
+          x.w = k + 3 < w ? src[3] : 0.f;
+        }
+      }
+      pv[p] = x;
+    }
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int64_t r = r0 + row, col = c0 + 4 * cq;
+      pd[p] = (r < last && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  floatx4 acc[IW][4];
+#pragma unroll
+  for (int i = 0; i < IW; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = kZero4;
+  if (first < last) fetch(first);
+  for (int64_t r0 = first; r0 < last; r0 += RC) {
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < VQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      if (idx < RC * W / 4) *reinterpret_cast<float4*>(&vt[(idx / (W / 4)) * LDV + 4 * (idx % (W / 4))]) = pv[p];
+    }
+#pragma unroll
+    for (int p = 0; p < DQ; ++p) {
+      const int idx = threadIdx.x + p * kThreads;
+      *reinterpret_cast<float4*>(&dt[(idx >> 4) * LDM + 4 * (idx & 15)]) = pd[p];
+    }
+    __syncthreads();
+    if (r0 + RC < last) fetch(r0 + RC);
+    // rows 16 wv + 4 q + s of the chunk are contraction indices 4 q + s
+    const int rb = 16 * wv + 4 * q;
+    SplitA a[IW];
+#pragma unroll
+    for (int i = 0; i < IW; ++i)
+      a[i] = split_a(vt[rb * LDV + 16 * i + c], vt[(rb + 1) * LDV + 16 * i + c], vt[(rb + 2) * LDV + 16 * i + c],
+                     vt[(rb + 3) * LDV + 16 * i + c]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const SplitB b = split_b(dt[rb * LDM + 16 * j + c], dt[(rb + 1) * LDM + 16 * j + c],
+                               dt[(rb + 2) * LDM + 16 * j + c], dt[(rb + 3) * LDM + 16 * j + c]);
+#pragma unroll
+      for (int i = 0; i < IW; ++i) acc[i][j] = mfma_split(a[i], b, acc[i][j]);
+    }
+  }
+  float* out = partial + ((int64_t)blockIdx.y * 4 + wv) * w * C;
+#pragma unroll
+  for (int i = 0; i < IW; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = c0 + 16 * j + c;
+      if (col >= C) continue;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int row = 16 * i + 4 * q + ii;
+        if (row < w) out[(int64_t)row * C + col] = acc[i][j][ii];
+      }
+    }
+}
+
 // dM[e] = sum over the splits y = 0, 1, ... of partial[y][e], in that order.
 __global__ __launch_bounds__(kThreads) void node_mix_reduce_kernel(const float* __restrict__ partial, int64_t n,
                                                                    int64_t splits, float* __restrict__ dM) {
@@ -508,10 +806,20 @@ int launch_dweight(const float* v, int64_t ldv, const float* dmix, int64_t N, in
   if (N > 0 && nx > 0) {
     const dim3 grid((unsigned)nx, (unsigned)splits), block(kThreads);
     const int vec = aligned(v, 16) && ldv % 4 == 0;
+    const bool sp = split_products();
     switch (width_class(w)) {
-      case 16: hipLaunchKernelGGL(node_mix_dweight_k_kernel<16>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
-      case 32: hipLaunchKernelGGL(node_mix_dweight_k_kernel<32>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
-      case 64: hipLaunchKernelGGL(node_mix_dweight_k_kernel<64>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      case 16:
+        if (sp) hipLaunchKernelGGL(node_mix_dweight_split<16>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        else hipLaunchKernelGGL(node_mix_dweight_k_kernel<16>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        break;
+      case 32:
+        if (sp) hipLaunchKernelGGL(node_mix_dweight_split<32>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        else hipLaunchKernelGGL(node_mix_dweight_k_kernel<32>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        break;
+      case 64:
+        if (sp) hipLaunchKernelGGL(node_mix_dweight_split<64>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        else hipLaunchKernelGGL(node_mix_dweight_k_kernel<64>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        break;
       default: hipLaunchKernelGGL(node_mix_dweight_kernel<128>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
     }
     const int rc = check_launch("node_mix_backward_weight");
@@ -565,12 +873,21 @@ extern "C" int gm_node_mix_forward_f32(const float* v, int64_t ldv, const float*
   const int vec_v = gm::aligned(v, 16) && ldv % 4 == 0;
   const int vec_out = gm::aligned(out, 16) && C % 4 == 0;
   const int W = gm::width_class(w);
-  const int CT = W == 128 ? 2 : 4;
+  const bool sp = W <= 64 && gm::split_products();
+  const int CT = (W == 128 || sp) ? 2 : 4;
   const int64_t nx = (C + 64 * CT - 1) / (64 * CT), n_tiles = (N + 63) / 64;
   int64_t ny = (2048 + nx - 1) / nx;
   if (ny > n_tiles) ny = n_tiles;
   if (ny > 65535) ny = 65535;
   const dim3 grid((unsigned)nx, (unsigned)ny), block(gm::kThreads);
+  if (sp) {
+    switch (W) {
+      case 16: hipLaunchKernelGGL((gm::node_mix_forward_split<16>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+      case 32: hipLaunchKernelGGL((gm::node_mix_forward_split<32>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+      default: hipLaunchKernelGGL((gm::node_mix_forward_split<64>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+    }
+    return gm::check_launch("node_mix_forward");
+  }
   switch (W) {
     case 16: hipLaunchKernelGGL((gm::node_mix_forward_kernel<16, 4>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
     case 32: hipLaunchKernelGGL((gm::node_mix_forward_kernel<32, 4>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
@@ -591,6 +908,14 @@ extern "C" int gm_node_mix_backward_input_f32(const float* dmix, const float* M,
              "dmix and M must be 16-byte aligned with C a multiple of 4");
   const hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)((N + 127) / 128)), block(gm::kThreads);
+  if (gm::width_class(w) <= 64 && gm::split_products()) {
+    switch (gm::width_class(w)) {
+      case 16: hipLaunchKernelGGL(gm::node_mix_dinput_split<16>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+      case 32: hipLaunchKernelGGL(gm::node_mix_dinput_split<32>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+      default: hipLaunchKernelGGL(gm::node_mix_dinput_split<64>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+    }
+    return gm::check_launch("node_mix_backward_input");
+  }
   switch (gm::width_class(w)) {
     case 16: hipLaunchKernelGGL(gm::node_mix_dinput_kernel<16>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
     case 32: hipLaunchKernelGGL(gm::node_mix_dinput_kernel<32>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
