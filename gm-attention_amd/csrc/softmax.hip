@@ -14,11 +14,14 @@
 // of the neighbourhood, holding its head's query columns in registers, and
 // the 8 lanes of one edge read that edge's key row as contiguous 16-byte
 // pieces.  The softmax is online per lane (running max and sum) and merged
-// across the slots of a head with lane shuffles; the raw scores park in alpha
-// and are normalised by a second walk over the same lines (L2 hits).
+// across the slots of a head with lane shuffles; a lane's first scores stay in
+// registers and are normalised there (alpha written once), scores past them
+// park in alpha and are normalised by a second walk over those edges.
 // The backward is two passes: per target (the adjoint's per-head total, ds,
 // and dq) and per source over the edges grouped by source (dk), so no atomics
-// are used and the result is deterministic.
+// are used and the result is deterministic; ds is written to its edge's place
+// in the source grouping and the per-source pass reads ds, the targets and the
+// transport rows as streams.
 #include <hip/hip_runtime.h>
 
 #include "common.hpp"
@@ -44,7 +47,9 @@ struct SmArgs {
   T* dk;
   const int64_t* src_ptr;
   const int64_t* src_order;
-  const int64_t* target;
+  const int32_t* target_s;  // each edge's target, in the source grouping's order
+  const int32_t* inv;       // each edge's place in the source grouping
+  const T* transport_s;     // the transport rows in the source grouping's order
   int64_t n_nodes;
   int D, orders, H, S, hshift;  // hshift = log2(H) on the fast path
   T scale;
@@ -65,10 +70,12 @@ __device__ __forceinline__ T chunk_dot(const T* q4, const Quad<T>& k, int n, con
   return acc;
 }
 
-// The edges of one lane go in steps of U: every index, key row piece and
-// transport pair of the step is loaded before any of them is used, so U
-// gathers are in flight at once.
-constexpr int kSmStep = 2;
+// The edges of one lane go in steps of kSmStep edges, each step's row gathers
+// issued together after the next step's ids were requested.  One edge a step
+// measured fastest at NS (backward 8.0 -> 7.4 ms against two or four a step):
+// the kernels are bound by L2 gathers of the rows, and fewer registers buy
+// more waves a SIMD than a wider step buys gathers in flight.
+constexpr int kSmStep = 1;
 
 template <typename T>
 __device__ __forceinline__ T chunk_dot_pair(const T* q4, const Quad<T>& k, int n, T c, T s) {
@@ -136,8 +143,40 @@ __device__ __forceinline__ void transport_pairs(const Chunks& C, const T* tr, T 
 // scalar chunk, two chunks each of frequencies 1 and 2), compiled in.
 constexpr uint32_t kOrders012 = 0x22110u;
 
+// Scores a lane keeps in registers: rows of up to S * kSmRegs edges (128 at
+// eight heads) are normalised from registers, so alpha is written once; the
+// edges past that park their raw score in alpha and are normalised by a
+// second walk over them.
+constexpr int kSmRegs = 8;
+constexpr bool kSmPrefetch = true;  // next step's source ids requested before this step's rows are used
+
+// One step's gathers for kSmStep edges of a lane: the chunks of the gathered
+// (key or query) rows and the transport pairs.
+template <typename T, int NCH>
+struct Gather {
+  Quad<T> row[kSmStep][NCH];
+  T tc[kSmStep][NCH], ts[kSmStep][NCH];
+};
+
+template <typename T, int NCH, uint32_t ORD>
+__device__ __forceinline__ void gather(const SmArgs<T>& a, Gather<T, NCH>& g, const T* rows,
+                                       const int64_t (&node)[kSmStep], const T* transport,
+                                       const int64_t (&te)[kSmStep], int h) {
+#pragma unroll
+  for (int u = 0; u < kSmStep; ++u) {
+    const T* r = rows + node[u] * a.D;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) g.row[u][c] = ld4(r + a.C.base[c] + h * a.C.stride[c]);
+    transport_pairs<T, NCH, ORD>(a.C, transport + te[u] * a.orders * 2, g.tc[u], g.ts[u]);
+  }
+}
+
+// Forward.  The lane's edges are e0 + s + r S; every step requests the next
+// step's source ids before it waits for its own rows, so a step costs one
+// memory round trip.
 template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
+  constexpr int U = kSmStep, R = kSmRegs;
   const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_nodes, kWavesPerBlock);
   const int lane = threadIdx.x & 63;
   const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
@@ -154,53 +193,95 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) q[4 * c + u] = x.v[u];
   }
-
-  T m = neg_inf<T>(), l = T(0);
-  for (int64_t e = e0 + s; e < e1; e += kSmStep * S) {
-    int64_t eu[kSmStep], ju[kSmStep];
+  int64_t jn[U];
+  if constexpr (kSmPrefetch) {
 #pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      eu[u] = e + u * S < e1 ? e + u * S : e;  // a step past the row's end repeats its first edge (not stored)
-      ju[u] = a.source[eu[u]];
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = e0 + s + (int64_t)u * S;
+      jn[u] = e < e1 ? a.source[e] : 0;
     }
-    Quad<T> kv[kSmStep][NCH];
-    T tc[kSmStep][NCH], tsn[kSmStep][NCH], bias[kSmStep];
-    uint8_t in[kSmStep];
+  }
+  // one step from eb: scores of the live edges into lw (dead ones -inf)
+  auto step = [&](int64_t eb, T (&lw)[U]) {
+    int64_t jc[U], te[U];
+    bool live[U];
 #pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      const T* kj = a.k + ju[u] * a.D;
-      const T* tr = a.transport + eu[u] * a.orders * 2;
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = eb + (int64_t)u * S;
+      live[u] = e < e1;
+      te[u] = live[u] ? e : eb;
+      jc[u] = kSmPrefetch ? jn[u] : a.source[te[u]];
+    }
+    if constexpr (kSmPrefetch) {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) kv[u][c] = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
-      transport_pairs<T, NCH, ORD>(a.C, tr, tc[u], tsn[u]);
-      bias[u] = a.bias[eu[u]];
-      in[u] = a.inside[eu[u]];
+      for (int u = 0; u < U; ++u) {
+        const int64_t e = eb + (int64_t)(U + u) * S;
+        jn[u] = e < e1 ? a.source[e] : 0;
+      }
+    }
+    Gather<T, NCH> g;
+    gather<T, NCH, ORD>(a, g, a.k, jc, a.transport, te, h);
+    T bias[U];
+    uint8_t in[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      bias[u] = a.bias[te[u]];
+      in[u] = a.inside[te[u]];
     }
 #pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      if (e + u * S >= e1) break;
+    for (int u = 0; u < U; ++u) {
       T acc = T(0);
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        acc += chunk_dot_pair(&q[4 * c], kv[u][c], chunk_order<ORD>(a.C, c), tc[u][c], tsn[u][c]);
-      T lw = a.scale * acc + bias[u];
-      if (!in[u]) lw = neg_inf<T>();  // outside the window: excluded from the max and the sum
-      a.alpha[eu[u] * H + h] = lw;
-      online_add(m, l, lw);
+        acc += chunk_dot_pair(&q[4 * c], g.row[u][c], chunk_order<ORD>(a.C, c), g.tc[u][c], g.ts[u][c]);
+      lw[u] = (live[u] && in[u]) ? a.scale * acc + bias[u] : neg_inf<T>();  // outside the window: excluded
+    }
+  };
+  T sc[R > 0 ? R : 1];
+  T m = neg_inf<T>(), l = T(0);
+#pragma unroll
+  for (int t = 0; t < R / U; ++t) {
+    const int64_t eb = e0 + s + (int64_t)t * U * S;
+    if (eb >= e1) break;
+    T lw[U];
+    step(eb, lw);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      sc[t * U + u] = lw[u];
+      online_add(m, l, lw[u]);
+    }
+  }
+  for (int64_t eb = e0 + s + (int64_t)R * S; eb < e1; eb += (int64_t)U * S) {
+    T lw[U];
+    step(eb, lw);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = eb + (int64_t)u * S;
+      if (e < e1) a.alpha[e * H + h] = lw[u];
+      online_add(m, l, lw[u]);
     }
   }
   for (int off = H; off < kWave; off <<= 1) {
     const T mo = __shfl_xor(m, off, kWave), lo = __shfl_xor(l, off, kWave);
     online_merge(m, l, mo, lo);
   }
-  for (int64_t e = e0 + s; e < e1; e += S) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t e = e0 + s + (int64_t)r * S;
+    if (e < e1) a.alpha[e * H + h] = gm_exp(sc[r] - m) / l;  // an excluded edge is exp(-inf) = 0
+  }
+  for (int64_t e = e0 + s + (int64_t)R * S; e < e1; e += S) {
     const T lw = a.alpha[e * H + h];
-    a.alpha[e * H + h] = gm_exp(lw - m) / l;  // an excluded edge is exp(-inf) = 0
+    a.alpha[e * H + h] = gm_exp(lw - m) / l;
   }
 }
 
+// Backward per target: the adjoint's per-head total, ds, and dq.  ds goes to
+// its edge's place in the source grouping (inv), so the per-source pass reads
+// it as one stream.
 template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a) {
+  constexpr int U = kSmStep;
   const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_nodes, kWavesPerBlock);
   const int lane = threadIdx.x & 63;
   const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
@@ -210,45 +291,64 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
 
   T total = T(0);
-  for (int64_t e = e0 + s; e < e1; e += S) total += a.alpha_in[e * H + h] * a.dalpha[e * H + h];
+  for (int64_t e = e0 + s; e < e1; e += 4 * S) {
+    T p[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t f = e + (int64_t)u * S;
+      p[u] = f < e1 ? a.alpha_in[f * H + h] * a.dalpha[f * H + h] : T(0);
+    }
+    total += (p[0] + p[1]) + (p[2] + p[3]);
+  }
   total = group_sum_pow2(total, H);
 
+  int64_t jn[U];
+  int32_t pn[U];
+  T an[U], dn[U];
+  auto fetch = [&](int64_t eb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = eb + (int64_t)u * S;
+      const bool live = e < e1;
+      jn[u] = live ? a.source[e] : 0;
+      pn[u] = live ? a.inv[e] : 0;
+      an[u] = live ? a.alpha_in[e * H + h] : T(0);
+      dn[u] = live ? a.dalpha[e * H + h] : T(0);
+    }
+  };
   T acc[NCH * 4];
 #pragma unroll
   for (int u = 0; u < NCH * 4; ++u) acc[u] = T(0);
-  for (int64_t e = e0 + s; e < e1; e += kSmStep * S) {
-    int64_t eu[kSmStep], ju[kSmStep];
-    T al[kSmStep], da[kSmStep];
+  fetch(e0 + s);
+  for (int64_t eb = e0 + s; eb < e1; eb += (int64_t)U * S) {
+    int64_t jc[U], te[U];
+    int32_t pc[U];
+    T al[U], da[U];
 #pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      eu[u] = e + u * S < e1 ? e + u * S : e;
-      ju[u] = a.source[eu[u]];
-      al[u] = a.alpha_in[eu[u] * H + h];
-      da[u] = a.dalpha[eu[u] * H + h];
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = eb + (int64_t)u * S;
+      te[u] = e < e1 ? e : eb;
+      jc[u] = jn[u];
+      pc[u] = pn[u];
+      al[u] = an[u];
+      da[u] = dn[u];
     }
-    Quad<T> kv[kSmStep][NCH];
-    T tc[kSmStep][NCH], tsn[kSmStep][NCH];
+    fetch(eb + (int64_t)U * S);
+    Gather<T, NCH> g;
+    gather<T, NCH, ORD>(a, g, a.k, jc, a.transport, te, h);
 #pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      const T* kj = a.k + ju[u] * a.D;
-      const T* tr = a.transport + eu[u] * a.orders * 2;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) kv[u][c] = ld4(kj + a.C.base[c] + h * a.C.stride[c]);
-      transport_pairs<T, NCH, ORD>(a.C, tr, tc[u], tsn[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      if (e + u * S >= e1) break;
+    for (int u = 0; u < U; ++u) {
+      if (eb + (int64_t)u * S >= e1) break;
       const T ds = a.scale * al[u] * (da[u] - total);
-      a.ds[eu[u] * H + h] = ds;
+      a.ds[(int64_t)pc[u] * H + h] = ds;
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        const Quad<T>& k = kv[u][c];
+        const Quad<T>& k = g.row[u][c];
         if (chunk_order<ORD>(a.C, c) == 0) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * k.v[v];
         } else {
-          const T cr = tc[u][c], ci = tsn[u][c];
+          const T cr = g.tc[u][c], ci = g.ts[u][c];
           acc[4 * c + 0] += ds * (cr * k.v[0] - ci * k.v[1]);
           acc[4 * c + 1] += ds * (cr * k.v[1] + ci * k.v[0]);
           acc[4 * c + 2] += ds * (cr * k.v[2] - ci * k.v[3]);
@@ -266,8 +366,12 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
   }
 }
 
+// Backward per source over the edges grouped by source: ds, the targets and
+// the transport rows are streams in that order (ds written there by the
+// per-target pass), the query rows are gathered.
 template <typename T, int NCH, uint32_t ORD>
 __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a) {
+  constexpr int U = kSmStep;
   const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.src_ptr, a.n_nodes, kWavesPerBlock);
   const int lane = threadIdx.x & 63;
   const int64_t j = blk * kWavesPerBlock + (threadIdx.x >> 6);
@@ -276,41 +380,46 @@ __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a)
   const int h = lane & (H - 1), s = lane >> a.hshift;
   const int64_t g0 = a.src_ptr[j], g1 = a.src_ptr[j + 1];
 
+  int64_t tn[U];
+  T dn[U];
+  auto fetch = [&](int64_t gb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t g = gb + (int64_t)u * S;
+      const bool live = g < g1;
+      tn[u] = live ? a.target_s[g] : 0;
+      dn[u] = live ? a.ds[g * H + h] : T(0);
+    }
+  };
   T acc[NCH * 4];
 #pragma unroll
   for (int u = 0; u < NCH * 4; ++u) acc[u] = T(0);
-  for (int64_t g = g0 + s; g < g1; g += kSmStep * S) {
-    int64_t eu[kSmStep], tu[kSmStep];
+  fetch(g0 + s);
+  for (int64_t gb = g0 + s; gb < g1; gb += (int64_t)U * S) {
+    int64_t tc[U], te[U];
+    T dsu[U];
 #pragma unroll
-    for (int u = 0; u < kSmStep; ++u) eu[u] = a.src_order[g + u * S < g1 ? g + u * S : g];
-    T dsu[kSmStep];
-#pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      tu[u] = a.target[eu[u]];
-      dsu[u] = a.ds[eu[u] * H + h];
+    for (int u = 0; u < U; ++u) {
+      const int64_t g = gb + (int64_t)u * S;
+      te[u] = g < g1 ? g : gb;
+      tc[u] = tn[u];
+      dsu[u] = dn[u];
     }
-    Quad<T> qv[kSmStep][NCH];
-    T tc[kSmStep][NCH], tsn[kSmStep][NCH];
+    fetch(gb + (int64_t)U * S);
+    Gather<T, NCH> gq;
+    gather<T, NCH, ORD>(a, gq, a.q, tc, a.transport_s, te, h);
 #pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      const T* qt = a.q + tu[u] * a.D;
-      const T* tr = a.transport + eu[u] * a.orders * 2;
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) qv[u][c] = ld4(qt + a.C.base[c] + h * a.C.stride[c]);
-      transport_pairs<T, NCH, ORD>(a.C, tr, tc[u], tsn[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < kSmStep; ++u) {
-      if (g + u * S >= g1) break;
+    for (int u = 0; u < U; ++u) {
+      if (gb + (int64_t)u * S >= g1) break;
       const T ds = dsu[u];
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
-        const Quad<T>& qq = qv[u][c];
+        const Quad<T>& qq = gq.row[u][c];
         if (chunk_order<ORD>(a.C, c) == 0) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * qq.v[v];
         } else {
-          const T cr = tc[u][c], ci = tsn[u][c];
+          const T cr = gq.tc[u][c], ci = gq.ts[u][c];
           // conj(tau) q = (c q0 + s q1, c q1 - s q0)
           acc[4 * c + 0] += ds * (cr * qq.v[0] + ci * qq.v[1]);
           acc[4 * c + 1] += ds * (cr * qq.v[1] - ci * qq.v[0]);
@@ -454,11 +563,11 @@ __global__ __launch_bounds__(256) void softmax_backward_source_generic(SmArgs<T>
       for (int64_t g = g0; g < g1; ++g) {
         const int64_t e = a.src_order[g];
         const T ds = a.ds[e * H + col.h];
-        const T* qt = a.q + a.target[e] * a.D;
+        const T* qt = a.q + (int64_t)a.target_s[g] * a.D;
         if (col.n == 0) {
           acc += ds * qt[c];
         } else {
-          const T* tr = a.transport + e * a.orders * 2;
+          const T* tr = a.transport_s + g * a.orders * 2;
           const T cr = tr[2 * col.n], ci = tr[2 * col.n + 1];
           const T q0 = qt[col.pair], q1 = qt[col.pair + 1];
           acc += ds * (col.part == 0 ? cr * q0 + ci * q1 : cr * q1 - ci * q0);
@@ -581,8 +690,8 @@ template <typename T>
 int softmax_backward(const T* dalpha, const T* q, const T* k, const T* transport, const T* bias, const uint8_t* inside,
                      const int64_t* desc, const int64_t* row_ptr, const int64_t* source, const T* alpha,
                      int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H, double scale,
-                     const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, T* ds, T* dq, T* dk,
-                     hipStream_t stream) {
+                     const int64_t* src_ptr, const int64_t* src_order, const int32_t* target_s, const int32_t* inv,
+                     const T* transport_s, T* ds, T* dq, T* dk, hipStream_t stream) {
   SmArgs<T> a;
   bool fast = false;
   const int rc = prepare(a, fast, q, k, transport, bias, inside, desc, row_ptr, source, n_nodes, n_edges, D, orders,
@@ -590,7 +699,11 @@ int softmax_backward(const T* dalpha, const T* q, const T* k, const T* transport
   if (rc != GM_OK) return rc;
   if (n_nodes == 0) return GM_OK;
   GM_REQUIRE(dq && dk && src_ptr, "dq, dk and src_ptr must be device pointers");
-  if (n_edges > 0) GM_REQUIRE(dalpha && alpha && src_order && target && ds, "dalpha, alpha, src_order, target and ds must be device pointers");
+  if (n_edges > 0)
+    GM_REQUIRE(dalpha && alpha && src_order && target_s && inv && transport_s && ds,
+               "dalpha, alpha, src_order, target_s, inv, transport_s and ds must be device pointers");
+  GM_REQUIRE(n_nodes < (int64_t(1) << 31) && n_edges < (int64_t(1) << 31),
+             "the source-grouped streams index nodes and edges in 32 bits");
   fast = fast && aligned(dq, 4 * sizeof(T)) && aligned(dk, 4 * sizeof(T));
   a.alpha_in = alpha;
   a.dalpha = dalpha;
@@ -599,7 +712,9 @@ int softmax_backward(const T* dalpha, const T* q, const T* k, const T* transport
   a.dk = dk;
   a.src_ptr = src_ptr;
   a.src_order = src_order;
-  a.target = target;
+  a.target_s = target_s;
+  a.inv = inv;
+  a.transport_s = transport_s;
   launch(Kind::BackwardTarget, fast, a, stream);
   int status = check_launch("softmax_backward (per target)");
   if (status != GM_OK) return status;
@@ -635,12 +750,12 @@ extern "C" int gm_softmax_backward_f32(const float* dalpha, const float* q, cons
                                        const int64_t* row_ptr, const int64_t* source, const float* alpha,
                                        int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F,
                                        int64_t H, double scale, int64_t deg_max, const int64_t* src_ptr,
-                                       const int64_t* src_order, const int64_t* target, float* ds, float* dq,
-                                       float* dk, void* stream) {
+                                       const int64_t* src_order, const int32_t* target_s, const int32_t* inv,
+                                       const float* transport_s, float* ds, float* dq, float* dk, void* stream) {
   (void)deg_max;
   return gm::softmax_backward<float>(dalpha, q, k, transport, bias, inside, desc, row_ptr, source, alpha, n_nodes,
-                                     n_edges, D, orders, F, H, scale, src_ptr, src_order, target, ds, dq, dk,
-                                     (hipStream_t)stream);
+                                     n_edges, D, orders, F, H, scale, src_ptr, src_order, target_s, inv, transport_s,
+                                     ds, dq, dk, (hipStream_t)stream);
 }
 
 extern "C" int gm_softmax_backward_f64(const double* dalpha, const double* q, const double* k,
@@ -648,10 +763,11 @@ extern "C" int gm_softmax_backward_f64(const double* dalpha, const double* q, co
                                        const int64_t* desc, const int64_t* row_ptr, const int64_t* source,
                                        const double* alpha, int64_t n_nodes, int64_t n_edges, int64_t D,
                                        int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
-                                       const int64_t* src_ptr, const int64_t* src_order, const int64_t* target,
-                                       double* ds, double* dq, double* dk, void* stream) {
+                                       const int64_t* src_ptr, const int64_t* src_order, const int32_t* target_s,
+                                       const int32_t* inv, const double* transport_s, double* ds, double* dq,
+                                       double* dk, void* stream) {
   (void)deg_max;
   return gm::softmax_backward<double>(dalpha, q, k, transport, bias, inside, desc, row_ptr, source, alpha, n_nodes,
-                                      n_edges, D, orders, F, H, scale, src_ptr, src_order, target, ds, dq, dk,
-                                      (hipStream_t)stream);
+                                      n_edges, D, orders, F, H, scale, src_ptr, src_order, target_s, inv,
+                                      transport_s, ds, dq, dk, (hipStream_t)stream);
 }

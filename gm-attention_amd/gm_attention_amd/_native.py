@@ -36,7 +36,7 @@ _D = ctypes.c_double
 #: C signatures, in include/gm_hip.h order (the return type is int everywhere).
 SIGNATURES: dict[str, list[Any]] = {
     "gm_softmax_forward": [_P] * 8 + [_I] * 6 + [_D, _I, _P, _P],
-    "gm_softmax_backward": [_P] * 10 + [_I] * 6 + [_D, _I] + [_P] * 7,
+    "gm_softmax_backward": [_P] * 10 + [_I] * 6 + [_D, _I] + [_P] * 9,
     "gm_conv_forward": [_P] * 10 + [_I] * 7 + [_P, _P],
     "gm_conv_backward": [_P] * 11 + [_I] * 7 + [_P] * 7,
     "gm_factored_forward": [_P] * 10 + [_I] * 10 + [_P, _P],
@@ -211,6 +211,35 @@ def source_major(source: Tensor, row_ptr: Tensor) -> tuple[Tensor, Tensor, Tenso
     return result
 
 
+_GROUPED_TABLES: dict[tuple, tuple[Any, Any, tuple[Tensor, Tensor, Tensor]]] = {}
+
+
+def source_grouped_tables(source: Tensor, row_ptr: Tensor, transport: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """``(target_s, inv, transport_s)`` for the per-source backward passes:
+    each edge's target (int32) and transport row in the source grouping's
+    order, and every edge's place in that order (int32).  Built on the device
+    once per edge set and transport table, cached against both tensors."""
+    src_ptr, src_order, target = source_major(source, row_ptr)
+    key = (id(source), source.data_ptr(), source._version, id(transport), transport.data_ptr(), transport._version,
+           tuple(transport.shape))
+    held = _GROUPED_TABLES.get(key)
+    if held is not None and held[0]() is source and held[1]() is transport:
+        return held[2]
+    _check(row_ptr.shape[0] - 1 < 2**31 and source.shape[0] < 2**31,
+           "the source-grouped streams index nodes and edges in 32 bits")
+    target_s = target.index_select(0, src_order).to(torch.int32)
+    inv = torch.empty(source.shape[0], dtype=torch.int32, device=source.device)
+    inv[src_order] = torch.arange(source.shape[0], dtype=torch.int32, device=source.device)
+    transport_s = transport.index_select(0, src_order).contiguous()
+    result = (target_s.contiguous(), inv, transport_s)
+    for stale in [k for k, (a, b, _) in _GROUPED_TABLES.items() if a() is None or b() is None]:
+        del _GROUPED_TABLES[stale]
+    _GROUPED_TABLES[key] = (weakref.ref(source), weakref.ref(transport), result)
+    while len(_GROUPED_TABLES) > 8:
+        del _GROUPED_TABLES[next(iter(_GROUPED_TABLES))]
+    return result
+
+
 # ---------------------------------------------------------------- attention
 
 
@@ -268,13 +297,15 @@ class AttentionExtension:
         dk = torch.empty_like(q)
         if q.shape[0] == 0:
             return [dq, dk]
-        src_ptr, src_order, target = source_major(source, row_ptr)
+        src_ptr, src_order, _ = source_major(source, row_ptr)
+        target_s, inv, transport_s = source_grouped_tables(source, row_ptr, transport.contiguous())
         ds = torch.empty(source.shape[0], H, dtype=q.dtype, device=q.device)
         hd = host_desc(desc)
         _call("gm_softmax_backward" + _suffix(q.dtype), _ptr(dalpha), _ptr(q), _ptr(k), _ptr(transport), _ptr(bias),
               _ptr(inside), hd.data_ptr(), _ptr(row_ptr), _ptr(source), _ptr(alpha), q.shape[0], source.shape[0],
               q.shape[1], transport.shape[1], hd.shape[0], H, float(scale), int(deg_max), _ptr(src_ptr),
-              _ptr(src_order), _ptr(target), _ptr(ds), _ptr(dq), _ptr(dk), _stream(q.device))
+              _ptr(src_order), _ptr(target_s), _ptr(inv), _ptr(transport_s), _ptr(ds), _ptr(dq), _ptr(dk),
+              _stream(q.device))
         return [dq, dk]
 
     # ---- depthwise convolution (attention_cpu.cpp:42-145) ----

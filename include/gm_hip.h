@@ -101,24 +101,27 @@ int gm_softmax_forward_f64(const double* q, const double* k, const double* trans
  * (fused/attention_cpu.cpp:222-252; called from fused_attention.py:395).
  * Unlike the reference (atomic adds on dk, attention_cuda.cu:20-28) the key
  * gradient is gathered per source, so it is deterministic; that pass reads
- * the edges grouped by source:
- *   src_ptr   (n_nodes + 1,)  group offsets into src_order
- *   src_order (n_edges,)      edge ids sorted by source (stable)
- *   target    (n_edges,)      each edge's target node
- *   ds        (n_edges, H)    workspace of the element type
- * bias and inside are accepted for signature parity and not read. */
+ * the edges grouped by source, its per-edge inputs as streams in that order:
+ *   src_ptr     (n_nodes + 1,)        group offsets into src_order
+ *   src_order   (n_edges,)            edge ids sorted by source (stable)
+ *   target_s    (n_edges,) int32      target of edge src_order[g], at g
+ *   inv         (n_edges,) int32      inverse of src_order (edge e sits at inv[e])
+ *   transport_s (n_edges, orders, 2)  transport row of edge src_order[g], at g
+ *   ds          (n_edges, H)          workspace of the element type
+ * (n_nodes and n_edges below 2^31).  bias and inside are accepted for
+ * signature parity and not read. */
 int gm_softmax_backward_f32(const float* dalpha, const float* q, const float* k, const float* transport,
                             const float* bias, const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr,
                             const int64_t* source, const float* alpha, int64_t n_nodes, int64_t n_edges, int64_t D,
                             int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
-                            const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, float* ds,
-                            float* dq, float* dk, void* stream);
+                            const int64_t* src_ptr, const int64_t* src_order, const int32_t* target_s,
+                            const int32_t* inv, const float* transport_s, float* ds, float* dq, float* dk, void* stream);
 int gm_softmax_backward_f64(const double* dalpha, const double* q, const double* k, const double* transport,
                             const double* bias, const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr,
                             const int64_t* source, const double* alpha, int64_t n_nodes, int64_t n_edges, int64_t D,
                             int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
-                            const int64_t* src_ptr, const int64_t* src_order, const int64_t* target, double* ds,
-                            double* dq, double* dk, void* stream);
+                            const int64_t* src_ptr, const int64_t* src_order, const int32_t* target_s,
+                            const int32_t* inv, const double* transport_s, double* ds, double* dq, double* dk, void* stream);
 
 /* ---------------- depthwise steerable convolution ----------------
  *
