@@ -396,6 +396,165 @@ def run_geometry(args) -> None:
     print(json.dumps(line))
 
 
+C5_IMG, C5_STAGES, C5_BATCH = (128, 256), ((64, 128), (32, 64)), 8
+C5_TYPES, C5_HEADS = ({0: 64, 1: 64, 2: 64}, {0: 128, 1: 128, 2: 128}), (8, 16)
+
+
+def run_stage(args) -> None:
+    """One step = the C5 model forward and backward: per stage the learned
+    restriction (EquiEncode) and its norm, one GmSegformer block (8 / 16-head
+    SO2MHSA, depthwise steerable Mix-FFN), the stage norm; the readout
+    convolutions, the fusion decoder's interpolations and the 13-class head on
+    the 128x256 input grid; cross-entropy against random labels."""
+    import torch
+
+    from gm_attention_amd import _native
+    from gm_attention_amd.nn import eager_ops
+    from gm_attention_amd.nn.segformer import GmSegformer, build_stage_hierarchy, stage_radii
+    from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
+
+    device = torch.device("cuda:0")
+    t0 = time.time()
+    radii = stage_radii(C5_STAGES)
+    h = build_stage_hierarchy(C5_IMG, C5_STAGES, radii, device=device).tile(C5_BATCH).to(device, torch.float32)
+    n0 = h.levels[0].n_nodes
+    down = [e.n_edges for e in h.down_edges]
+    local = [h.levels[i + 1].discretization.n_edges for i in range(len(C5_STAGES))]
+    log(f"hierarchy {C5_IMG} -> {C5_STAGES}, batch {C5_BATCH}: {n0} input points, restriction edges {down}, "
+        f"stage edges {local} in {time.time() - t0:.1f}s")
+    torch.manual_seed(0)
+    model = GmSegformer(in_channels=4, num_classes=13, stage_field_types=[SO2FieldType(t) for t in C5_TYPES],
+                        heads=C5_HEADS, depths=(1, 1), merge_cutoffs=radii.merge, attention_cutoffs=radii.attention,
+                        mix_cutoffs=radii.mix, interpolate_cutoffs=radii.interpolate, readout_cutoffs=radii.readout,
+                        readout_channels=(32, 32), decoder_channels=32, n_radial_basis=8, dtype=torch.float32,
+                        device=device)
+    timer = OpTimer()
+    att, fac = _native.attention(), _native.factored()
+    for name in ("softmax_forward", "softmax_backward"):
+        timer.wrap(att, name, name)
+    for mod, name, key in ((fac, "aggregate", "factored_aggregate"),
+                           (fac, "backward_aggregated", "factored_backward_aggregated"),
+                           (fac, "forward", "factored_forward"),
+                           (_native, "factored_forward_grouped", "factored_forward"),
+                           (_native, "factored_backward_grouped", "factored_backward_aggregated"),
+                           (_native, "aggregate_heads", "factored_aggregate"),
+                           (_native, "radial_trunk_forward", "radial_trunk_forward"),
+                           (_native, "radial_trunk_backward", "radial_trunk_backward"),
+                           (_native, "conv_radial_forward", "conv_radial_forward"),
+                           (_native, "conv_radial_backward", "conv_radial_backward")):
+        if hasattr(mod, name):
+            timer.wrap(mod, name, key)
+    gen = torch.Generator(device=device).manual_seed(1)
+    x0 = torch.rand(n0, 4, device=device, generator=gen).requires_grad_(True)
+    labels = torch.randint(0, 13, (n0,), device=device, generator=gen)
+
+    def step():
+        logits = model(SO2FeatureField(model.input_field_type, {0: x0}), h)[0]
+        torch.nn.functional.cross_entropy(logits, labels).backward()
+
+    def clear():
+        x0.grad = None
+        model.zero_grad(set_to_none=True)
+
+    before = dict(eager_ops.calls)
+    for _ in range(args.warmup):
+        step()
+        clear()
+    if eager_ops.calls != before:
+        raise RuntimeError(f"part of the C5 model ran on the eager path: {eager_ops.calls}")
+    torch.cuda.synchronize()
+    timer.enabled = True
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+        clear()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t1
+    timer.enabled = False
+    ms_per_step = 1e3 * elapsed / args.steps
+    ops = timer.summary(args.steps)
+    log(f"step {ms_per_step:.2f} ms; ops: " + ", ".join(f"{k} {v['ms_per_step']:.2f} ms" for k, v in ops.items()))
+    dominant = max(ops, key=lambda k: ops[k]["ms_per_step"])
+    line = {
+        "metric": "C5 stage fwd+bwd fine-points/s at 128x256 B=8",
+        "value": n0 / (ms_per_step * 1e-3),
+        "unit": "fine-points/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: U(0,1) 4-channel input, uniform random labels of 13 classes, random-init weights, "
+                "equiangular grids",
+        "config": {"workload": ("GmSegformer encoder stages + fusion decoder: 128x256 {0:4} -> EquiEncode -> 64x128 "
+                                "{0:64,1:64,2:64} (8-head SO2MHSA + depthwise Mix-FFN block) -> EquiEncode -> 32x64 "
+                                "{0:128,1:128,2:128} (16-head block); readouts, fusion decoder, 13-class head, "
+                                "cross-entropy; input and every parameter gradient"),
+                   "batch": C5_BATCH, "fine_points": n0, "restriction_edges": down, "stage_edges": local},
+        "roofline": None,
+        "dominant_op": dominant,
+        "ops": {name: {k: round(v2, 4) for k, v2 in v.items()} for name, v in ops.items()},
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_stage(model),
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline_stage(model_gpu) -> dict:
+    """The oracle's composition of the C5 model (oracle.modules.segformer_forward,
+    factored order) forward + backward with cross-entropy, float32, on the
+    host's cores (all of them), on the same model's widths and heads over a
+    32x64 input grid (stages 16x32 and 8x16), batch 1: the rate measured on
+    that sample, not extrapolated (the oracle's cost grows faster than the
+    points with the grid, so the full 128x256 x 8 rate would be lower)."""
+    import torch
+
+    from gm_attention_amd.nn.segformer import GmSegformer, build_stage_hierarchy, stage_radii
+    from gm_attention_amd.representations.field_type import SO2FieldType
+    from oracle import modules
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    img = (32, 64)
+    stages = ((16, 32), (8, 16))
+    radii = stage_radii(stages)
+    h = build_stage_hierarchy(img, stages, radii).to(None, torch.float32)
+    model = GmSegformer(in_channels=4, num_classes=13, stage_field_types=[SO2FieldType(t) for t in C5_TYPES],
+                        heads=C5_HEADS, depths=(1, 1), merge_cutoffs=radii.merge, attention_cutoffs=radii.attention,
+                        mix_cutoffs=radii.mix, interpolate_cutoffs=radii.interpolate, readout_cutoffs=radii.readout,
+                        readout_channels=(32, 32), decoder_channels=32, n_radial_basis=8, dtype=torch.float32)
+    model.load_state_dict({k: v.detach().cpu() for k, v in model_gpu.state_dict().items()})
+    n0 = h.levels[0].n_nodes
+    gen = torch.Generator().manual_seed(3)
+    x0 = torch.rand(n0, 4, generator=gen).requires_grad_(True)
+    labels = torch.randint(0, 13, (n0,), generator=gen)
+    t0 = time.perf_counter()
+    out = modules.segformer_forward(model, x0, h, None, "factored")
+    torch.nn.functional.cross_entropy(out, labels).backward()
+    dt = time.perf_counter() - t0
+    log(f"cpu baseline: C5 oracle at {img} batch 1: {dt:.2f}s on {threads} threads")
+    return {"value": n0 / dt, "unit": "fine-points/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": (f"oracle composition of the C5 model (same widths, heads and radii in row spacings) fwd+bwd "
+                       f"with cross-entropy, float32, torch on {threads} threads, on a {img[0]}x{img[1]} input grid "
+                       f"(stages 16x32, 8x16), batch 1: {n0} points in {dt:.2f}s, the rate on that sample (not "
+                       "extrapolated)")}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu / /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def run_encoder(args) -> None:
     """One step = both restriction hops forward and backward (C5's encoder transfers)."""
     import torch
@@ -539,7 +698,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry", "block", "encoder"),
+    ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry", "block", "encoder", "hops"),
                     default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-edges", type=int, default=200_000)
@@ -566,8 +725,11 @@ def main() -> None:
     if args.workload == "geometry":
         run_geometry(args)
         return
-    if args.workload == "encoder":
+    if args.workload == "hops":
         run_encoder(args)
+        return
+    if args.workload == "encoder":
+        run_stage(args)
         return
 
     import torch

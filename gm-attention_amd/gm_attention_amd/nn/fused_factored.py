@@ -1036,13 +1036,15 @@ def _lanes_apply(kernel: Any, hp: HeadsPlan, pa: int, pt: int) -> bool:
 def head_split(kernel: Any, K: int) -> int:
     """Into how many shares of output copies each head's value kernel is cut
     for the grouped kernels: 1 when its plan fits them as is, else the
-    smallest power of two (at most 8) dividing every output multiplicity
-    whose shares fit (packed mix width ``2 wc + wr <= 128``); 0 when none does."""
+    smallest power of two (at most 64) dividing every output multiplicity
+    whose shares fit (packed mix width ``2 wc + wr <= 128``); 0 when none does.
+    A restriction onto 128 copies of frequencies 0..2 runs as 32 shares of
+    four copies each, the attention heads' shape."""
     key = ("_head_split", K, os.environ.get("GM_FACTORED_GROUPED", "1"))
     hit = kernel.__dict__.get(key)
     if hit is None:
         hit = 0
-        for split in (1, 2, 4, 8):
+        for split in (1, 2, 4, 8, 16, 32, 64):
             if any(m % split for m in kernel.field_type_out.multiplicities):
                 break
             ok, _, _ = grouped_eligible(heads_plan(sub_head(kernel, split)), torch.float32, K)
