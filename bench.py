@@ -68,6 +68,26 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def cpu_threads() -> int:
+    """Threads for the CPU baselines: the box's CPU share for one GPU (16), or
+    fewer where the host has fewer.  The GPU boxes report many more cores in
+    os.cpu_count() than one GPU's job may use (OMP_NUM_THREADS is 16 there);
+    torch on all of them would oversubscribe the share, not add cores."""
+    return min(16, os.cpu_count() or 1)
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (as lscpu reports it, from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 # ---------------------------------------------------------------- algorithmic cost per launch
 
 
@@ -184,7 +204,7 @@ def cpu_baseline_attention(edges, cutoff, mhsa_gpu, budget_edges: int):
     from gm_attention_amd.representations.field_type import SO2FeatureField
     from oracle import modules
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     row_ptr = edges.row_ptr
     n = row_ptr.shape[0] - 1
@@ -222,16 +242,20 @@ def cpu_baseline_attention(edges, cutoff, mhsa_gpu, budget_edges: int):
         mhsa.zero_grad(set_to_none=True)
 
     points = []
-    for budget in (budget_edges // 4, budget_edges):
+    for budget in (budget_edges // 4, budget_edges // 2, budget_edges):
         sub = sample(budget)
         step(sub)  # warm-up
         t0 = time.perf_counter()
         step(sub)
         points.append((sub.n_edges, time.perf_counter() - t0))
-    (e1, t1), (e2, t2) = points
-    per_edge = (t2 - t1) / (e2 - e1)
-    per_sample_nodes = max(0.0, t1 - per_edge * e1)
-    return dict(per_edge=per_edge, per_sample_nodes=per_sample_nodes, points=points, threads=threads, cpu_s=t1 + t2)
+    # least squares t = per_sample_nodes + per_edge e over the three samples
+    n = len(points)
+    me = sum(e for e, _ in points) / n
+    mt = sum(t for _, t in points) / n
+    per_edge = sum((e - me) * (t - mt) for e, t in points) / sum((e - me) ** 2 for e, _ in points)
+    per_sample_nodes = max(0.0, mt - per_edge * me)
+    return dict(per_edge=per_edge, per_sample_nodes=per_sample_nodes, points=points, threads=threads,
+                cpu_s=sum(t for _, t in points))
 
 
 def cpu_baseline_ffn(block_gpu, n_nodes: int):
@@ -244,7 +268,7 @@ def cpu_baseline_ffn(block_gpu, n_nodes: int):
     from gm_attention_amd.representations.field_type import SO2FeatureField
     from oracle import modules
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     ft = block_gpu.field_type
     block = SO2TransformerBlock(ft, HEADS, ffn_multiplier=4, cutoff=1.0, attention_batched=True, dtype=torch.float32)
@@ -280,7 +304,7 @@ def cpu_baseline_conv(edges, cutoff, conv_gpu, budget_edges: int):
     from gm_attention_amd.representations.field_type import SO2FeatureField
     from oracle import modules
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     row_ptr = edges.row_ptr
     n = row_ptr.shape[0] - 1
@@ -358,7 +382,7 @@ def run_geometry(args) -> None:
                     "issue and LDS latency, so neither the HBM nor the MFMA roofline applies to it")
     baseline = None
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         torch.set_num_threads(threads)
         host = build_equiangular_grid(NLAT, NLON)
         hframes = build_tangent_frames(host.nodes)
@@ -368,7 +392,7 @@ def run_geometry(args) -> None:
         edges_cpu = eg.edge_geometry_from_index(host.nodes, hframes, host.quadrature_weights, candidates[:, keep],
                                                 N, K)
         seconds = time.perf_counter() - t0
-        baseline = {"value": edges_cpu.n_edges / seconds, "unit": "edges/s", "cores": threads, "kind": "port",
+        baseline = {"value": edges_cpu.n_edges / seconds, "unit": "edges/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
                     "sample": (f"the host builder on one whole 256x512 sample ({edges_cpu.n_edges} edges): scipy "
                                f"cKDTree ball query ({threads} workers), float64 exact filter and torch per-edge "
                                f"arithmetic ({threads} threads) in {seconds:.2f}s")}
@@ -515,7 +539,7 @@ def cpu_baseline_stage(model_gpu) -> dict:
     from gm_attention_amd.representations.field_type import SO2FieldType
     from oracle import modules
 
-    threads = os.cpu_count() or 1
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     img = (32, 64)
     stages = ((16, 32), (8, 16))
@@ -541,18 +565,6 @@ def cpu_baseline_stage(model_gpu) -> dict:
                        f"with cross-entropy, float32, torch on {threads} threads, on a {img[0]}x{img[1]} input grid "
                        f"(stages 16x32, 8x16), batch 1: {n0} points in {dt:.2f}s, the rate on that sample (not "
                        "extrapolated)")}
-
-
-def cpu_model() -> str:
-    """The host CPU's model name (lscpu / /proc/cpuinfo)."""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
 
 
 def run_encoder(args) -> None:
@@ -638,7 +650,7 @@ def run_encoder(args) -> None:
             "note": "the op's launches (output tiles of both hops) differ in size: FLOPs and time per step"}
     baseline = None
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         torch.set_num_threads(threads)
         total, parts = 0.0, []
         for k, (enc, e) in enumerate(zip(encs, down)):
@@ -663,7 +675,7 @@ def run_encoder(args) -> None:
             dt = time.perf_counter() - t1
             total += dt / sub.n_edges * e.n_edges
             parts.append(f"hop {k + 1}: {sub.n_edges} edges in {dt:.2f}s")
-        baseline = {"value": n0 / total, "unit": "fine-points/s", "cores": threads, "kind": "port",
+        baseline = {"value": n0 / total, "unit": "fine-points/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
                     "sample": (f"oracle eager EquiEncode fwd+bwd (per-edge readout, float32, torch on {threads} "
                                f"threads) over the first targets of one sample per hop ({'; '.join(parts)}), "
                                f"extrapolated per edge to both hops' {down[0].n_edges} + {down[1].n_edges} edges")}
@@ -892,11 +904,12 @@ def main() -> None:
     if not args.no_cpu_baseline and args.workload == "attention":
         b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges)
         cpu_step = b["per_sample_nodes"] * batch + b["per_edge"] * E
-        (e1, t1), (e2, t2) = b["points"]
+        pts = "; ".join(f"{e} edges in {t:.2f}s" for e, t in b["points"])
         baseline = {"value": N / cpu_step, "unit": "query-points/s", "cores": b["threads"], "kind": "port",
+                    "cpu_model": cpu_model(), "host_cpu_count": os.cpu_count(),
                     "sample": (f"oracle eager SO2MHSA fwd+bwd (factored order, float32, torch on {b['threads']} "
                                f"threads) on one 256x512 sample's nodes with the edges of its first (pole) targets "
-                               f"and equator rows: {e1} edges in {t1:.2f}s, {e2} edges in {t2:.2f}s; the fit "
+                               f"and equator rows, three sizes: {pts}; the least-squares fit "
                                f"{b['per_sample_nodes']:.2f}s per sample's nodes + {b['per_edge'] * 1e6:.1f}us per "
                                f"edge, extrapolated to {batch} samples and {E} edges")}
         log(f"cpu baseline: {baseline['value']:.1f} qp/s ({baseline['sample']})")
@@ -904,11 +917,12 @@ def main() -> None:
         b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges)
         ffn_s, _ = cpu_baseline_ffn(block, N // batch)
         cpu_step = (b["per_sample_nodes"] + ffn_s) * batch + b["per_edge"] * E
-        (e1, t1), (e2, t2) = b["points"]
+        pts = ", ".join(f"{e} edges in {t:.2f}s" for e, t in b["points"])
         baseline = {"value": N / cpu_step, "unit": "query-points/s", "cores": b["threads"], "kind": "port",
+                    "cpu_model": cpu_model(), "host_cpu_count": os.cpu_count(),
                     "sample": (f"oracle eager block fwd+bwd in float32 (torch on {b['threads']} threads): the "
-                               f"SO2MHSA as in the attention workload ({e1} edges in {t1:.2f}s, {e2} edges in "
-                               f"{t2:.2f}s; {b['per_sample_nodes']:.2f}s per sample's nodes + "
+                               f"SO2MHSA as in the attention workload ({pts}; "
+                               f"{b['per_sample_nodes']:.2f}s per sample's nodes + "
                                f"{b['per_edge'] * 1e6:.1f}us per edge) plus both layer norms, the feed-forward and "
                                f"the gate over one sample's {N // batch} nodes in {ffn_s:.2f}s, extrapolated to "
                                f"{batch} samples and {E} edges")}
@@ -916,6 +930,7 @@ def main() -> None:
     elif not args.no_cpu_baseline and args.workload == "conv":
         b = cpu_baseline_conv(edges_cpu, cutoff, conv, args.cpu_budget_edges)
         baseline = {"value": N / (b["per_edge"] * E), "unit": "query-points/s", "cores": b["threads"], "kind": "port",
+                    "cpu_model": cpu_model(), "host_cpu_count": os.cpu_count(),
                     "sample": (f"oracle eager SO2Convolution(depthwise) fwd+bwd (float32, torch on {b['threads']} "
                                f"threads) over the edges of one 256x512 sample's first (pole) targets and equator "
                                f"rows: {b['edges']} edges in {b['seconds']:.2f}s, {b['per_edge'] * 1e6:.2f}us per "

@@ -1262,6 +1262,10 @@ using SlotsF2 = StaticSlots<5, 20, 0x28380u, 0x70a80u, 0x79680u, 0x28884u, 0x300
                             0x2908cu, 0x3088cu, 0x7188cu, 0x3808cu, 0x7a48cu>;
 // frequencies 0..1, four copies each: 5 slots
 using SlotsF1 = StaticSlots<3, 12, 0x18380u, 0x60e80u, 0x18884u, 0x20084u, 0x61484u>;
+// scalar input onto frequencies 0..2, sixteen copies each (a restriction from
+// scalar channels cut into shares of sixteen copies): 12 slots
+using SlotsS16 = StaticSlots<3, 80, 0x18780u, 0x18784u, 0x18788u, 0x1878cu, 0x18c90u, 0x18c98u, 0x18ca0u, 0x18ca8u,
+                             0x194b0u, 0x194b8u, 0x194c0u, 0x194c8u>;
 
 
 template <class P>
@@ -2024,7 +2028,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
 }
 
 template <int NT, class P, bool FUSED>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED ? 2 : 3) : 1))) void
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED || P::kDout > 40 ? 2 : 3) : 1))) void
 factored_backward_lanes(FactArgs<float> a) {
   constexpr int ZS = 16 * NT + 4;
   constexpr int kZWords = 17 * ZS, kWWords = 16 * NT * kWtStride;
@@ -2503,6 +2507,7 @@ void launch_grouped(bool forward, const FactArgs<float>& a, hipStream_t stream) 
     const bool fixed = (env == nullptr || env[0] != '0') && a.zw_g != nullptr;
     if (fixed && matches<SlotsF2>(a)) return launch_lanes_nt<(SlotsF2::kSlots + 1) / 2, SlotsF2>(forward, a, stream);
     if (fixed && matches<SlotsF1>(a)) return launch_lanes_nt<(SlotsF1::kSlots + 1) / 2, SlotsF1>(forward, a, stream);
+    if (fixed && matches<SlotsS16>(a)) return launch_lanes_nt<(SlotsS16::kSlots + 1) / 2, SlotsS16>(forward, a, stream);
     switch ((a.n_slots + 1) / 2) {
       case 1: launch_lanes_nt<1>(forward, a, stream); return;
       case 2: launch_lanes_nt<2>(forward, a, stream); return;

@@ -3,7 +3,8 @@
 // factored.h, included where they lie under /root/reference; nothing of them
 // is copied).  Test infrastructure only: it builds oracle/_ref/libgmref.so,
 // the compiled reference the Python restatement in oracle/eager.py is pinned
-// against, and the CPU baseline bench.py times.  The loops below are this
+// against (bench.py's CPU baselines time the Python restatement, not this
+// library).  The loops below are this
 // file's own; they fill the headers' Args structs and call their per-node
 // routines in node order, as the reference's attention_cpu.cpp and
 // factored_cpu.cpp do (attention_cpu.cpp:197-252, 94-145;
