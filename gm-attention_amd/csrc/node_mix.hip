@@ -466,6 +466,24 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_k_kernel(const floa
 
 // ---------------------------------------------------------------- split products
 //
+// Four consecutive reals k .. k + 3 (< w) of a node vector at src, float32 or
+// bfloat16 (widened exactly); vec: 16-byte (8-byte) aligned whole quads.
+__device__ __forceinline__ float4 load_v4(const float* src, int k, int w, int vec) {
+  if (vec && k + 3 < w) return *reinterpret_cast<const float4*>(src);
+  return make_float4(k < w ? src[0] : 0.f, k + 1 < w ? src[1] : 0.f, k + 2 < w ? src[2] : 0.f,
+                     k + 3 < w ? src[3] : 0.f);
+}
+__device__ __forceinline__ float bf16_at(const uint16_t* p) { return __uint_as_float((uint32_t)*p << 16); }
+__device__ __forceinline__ float4 load_v4(const uint16_t* src, int k, int w, int vec) {
+  if (vec && k + 3 < w) {
+    const uint2 u = *reinterpret_cast<const uint2*>(src);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xFFFF0000u));
+  }
+  return make_float4(k < w ? bf16_at(src) : 0.f, k + 1 < w ? bf16_at(src + 1) : 0.f,
+                     k + 2 < w ? bf16_at(src + 2) : 0.f, k + 3 < w ? bf16_at(src + 3) : 0.f);
+}
+//
 // The same three products for vectors up to 64 reals, with every fp32 product
 // formed as six bf16 products on v_mfma_f32_16x16x32_bf16 (three-piece splits,
 // fp32 accuracy: split.hpp).  A 16-deep contraction chunk kc gives lane
@@ -475,8 +493,8 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_k_kernel(const floa
 // (j < 2); the pieces of M at those columns are split once per wave and held
 // in registers; v's 64-row tiles come through LDS as in the fp32 kernel and
 // each wave splits its B operands from them.
-template <int W>
-__global__ __launch_bounds__(kThreads) void node_mix_forward_split(const float* __restrict__ v, int64_t ldv,
+template <int W, typename V = float>
+__global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __restrict__ v, int64_t ldv,
                                                                    const float* __restrict__ M, int64_t N, int w,
                                                                    int64_t C, float* __restrict__ out, int vec_v,
                                                                    int vec_out) {
@@ -509,19 +527,7 @@ __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const float* 
       const int idx = threadIdx.x + p * kThreads;
       const int row = idx / (W / 4), k = 4 * (idx % (W / 4));
       const int64_t r = tile * 64 + row;
-      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (idx < QUADS && r < N) {
-        const float* src = v + r * ldv + k;
-        if (vec_v && k + 3 < w) {
-          x = *reinterpret_cast<const float4*>(src);
-        } else {
-          x.x = k < w ? src[0] : 0.f;
-          x.y = k + 1 < w ? src[1] : 0.f;
-          x.z = k + 2 < w ? src[2] : 0.f;
-          x.w = k + 3 < w ? src[3] : 0.f;
-        }
-      }
-      pre[p] = x;
+      pre[p] = (idx < QUADS && r < N) ? load_v4(v + r * ldv + k, k, w, vec_v) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
   if ((int64_t)blockIdx.y < n_tiles) fetch(blockIdx.y);
@@ -670,8 +676,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 // tiling (each wave 16 rows of every 64-row chunk over the workgroup's whole
 // w x 64 tile, one partial per wave), a wave's 16 rows forming one contraction
 // chunk of split products.
-template <int W>
-__global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const float* __restrict__ v, int64_t ldv,
+template <int W, typename V = float>
+__global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __restrict__ v, int64_t ldv,
                                                                    const float* __restrict__ dmix, int64_t N, int w,
                                                                    int64_t C, int64_t rps, float* __restrict__ partial,
                                                                    int vec_v) {
@@ -689,19 +695,7 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const float* 
     for (int p = 0; p < VQ; ++p) {
       const int idx = threadIdx.x + p * kThreads, row = idx / (W / 4), k = 4 * (idx % (W / 4));
       const int64_t r = r0 + row;
-      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (idx < RC * W / 4 && r < last) {
-        const float* src = v + r * ldv + k;
-        if (vec_v && k + 3 < w) {
-          x = *reinterpret_cast<const float4*>(src);
-        } else {
-          x.x = k < w ? src[0] : 0.f;
-          x.y = k + 1 < w ? src[1] : 0.f;
-          x.z = k + 2 < w ? src[2] : 0.f;
-          x.w = k + 3 < w ? src[3] : 0.f;
-        }
-      }
-      pv[p] = x;
+      pv[p] = (idx < RC * W / 4 && r < last) ? load_v4(v + r * ldv + k, k, w, vec_v) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (int p = 0; p < DQ; ++p) {
@@ -964,4 +958,63 @@ extern "C" int gm_node_mix_backward_weight_noalloc_f32(const float* v, int64_t l
   int64_t splits = 1, rps = 64;
   gm::weight_splits(N, w, C, gm::kScratchFloats / per_split, splits, rps);
   return gm::launch_dweight(v, ldv, dmix, N, w, C, splits, rps, partial, dM, (hipStream_t)stream);
+}
+
+// bfloat16 node vectors (the rows of a bfloat16 field): the split kernels widen
+// them exactly while staging, so the products and outputs are the float32
+// entry points' on the widened values.  Vectors up to 64 reals.
+extern "C" int gm_node_mix_forward_bf16(const uint16_t* v, int64_t ldv, const float* M, int64_t N, int64_t w,
+                                        int64_t C, float* out, void* stream) {
+  int rc = gm::check_shapes(N, w, C);
+  if (rc != GM_OK) return rc;
+  GM_REQUIRE(w <= 64, "bfloat16 node vectors at most 64 reals wide");
+  if (N == 0 || C == 0) return GM_OK;
+  GM_REQUIRE(v && M && out, "v, M and out must be device pointers");
+  GM_REQUIRE(ldv >= w, "ldv must be at least w");
+  const hipStream_t s = (hipStream_t)stream;
+  const int vec_v = gm::aligned(v, 8) && ldv % 4 == 0;
+  const int vec_out = gm::aligned(out, 16) && C % 4 == 0;
+  const int W = gm::width_class(w);
+  const int64_t nx = (C + 127) / 128, n_tiles = (N + 63) / 64;
+  int64_t ny = (2048 + nx - 1) / nx;
+  if (ny > n_tiles) ny = n_tiles;
+  if (ny > 65535) ny = 65535;
+  const dim3 grid((unsigned)nx, (unsigned)ny), block(gm::kThreads);
+  switch (W) {
+    case 16: hipLaunchKernelGGL((gm::node_mix_forward_split<16, uint16_t>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+    case 32: hipLaunchKernelGGL((gm::node_mix_forward_split<32, uint16_t>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+    default: hipLaunchKernelGGL((gm::node_mix_forward_split<64, uint16_t>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+  }
+  return gm::check_launch("node_mix_forward (bfloat16 vectors)");
+}
+
+extern "C" int gm_node_mix_backward_weight_bf16(const uint16_t* v, int64_t ldv, const float* dmix, int64_t N,
+                                                int64_t w, int64_t C, float* partial, float* dM, void* stream) {
+  int rc = gm::check_shapes(N, w, C);
+  if (rc != GM_OK) return rc;
+  GM_REQUIRE(w <= 64, "bfloat16 node vectors at most 64 reals wide");
+  if (w * C == 0) return GM_OK;
+  GM_REQUIRE(dM && partial, "partial and dM must be device pointers");
+  GM_REQUIRE(N == 0 || (v && dmix && ldv >= w), "v (ldv >= w) and dmix must be device pointers");
+  GM_REQUIRE(C % 4 == 0 && (N == 0 || gm::aligned(dmix, 16)), "dmix must be 16-byte aligned with C a multiple of 4");
+  int64_t splits = 1, rps = 64;
+  gm::weight_splits(N, w, C, 1 << 20, splits, rps);
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t nx = (C + 63) / 64;
+  if (N > 0 && nx > 0) {
+    const dim3 grid((unsigned)nx, (unsigned)splits), block(gm::kThreads);
+    const int vec = gm::aligned(v, 8) && ldv % 4 == 0;
+    switch (gm::width_class(w)) {
+      case 16: hipLaunchKernelGGL((gm::node_mix_dweight_split<16, uint16_t>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      case 32: hipLaunchKernelGGL((gm::node_mix_dweight_split<32, uint16_t>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      default: hipLaunchKernelGGL((gm::node_mix_dweight_split<64, uint16_t>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+    }
+    rc = gm::check_launch("node_mix_backward_weight (bfloat16 vectors)");
+    if (rc != GM_OK) return rc;
+  }
+  const int64_t n = w * C;
+  const int64_t parts = (N > 0 && C > 0) ? splits * gm::weight_partials_per_split(w) : (int64_t)0;
+  hipLaunchKernelGGL(gm::node_mix_reduce_kernel, dim3((unsigned)((n + gm::kThreads - 1) / gm::kThreads)),
+                     dim3(gm::kThreads), 0, s, partial, n, parts, dM);
+  return gm::check_launch("node_mix_backward_weight (reduce)");
 }

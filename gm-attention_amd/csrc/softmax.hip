@@ -24,6 +24,8 @@
 // transport rows as streams.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "layout.hpp"
 
@@ -34,6 +36,8 @@ template <typename T>
 struct SmArgs {
   const T* q;
   const T* k;
+  const uint16_t* qb;  // bfloat16 rows (the bf16 entry points; T = float): read in place of q and k
+  const uint16_t* kb;
   const T* transport;  // (n_edges, orders, 2)
   const T* bias;
   const uint8_t* inside;
@@ -158,15 +162,36 @@ struct Gather {
   T tc[kSmStep][NCH], ts[kSmStep][NCH];
 };
 
-template <typename T, int NCH, uint32_t ORD>
-__device__ __forceinline__ void gather(const SmArgs<T>& a, Gather<T, NCH>& g, const T* rows,
+// A row's four reals at p as the element type (bfloat16 rows widened exactly).
+template <typename T>
+__device__ __forceinline__ Quad<T> row4(const T* p) {
+  return ld4(p);
+}
+template <typename T>
+__device__ __forceinline__ Quad<T> row4(const uint16_t* p) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p);
+  return {{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u), __uint_as_float(v.y << 16),
+           __uint_as_float(v.y & 0xFFFF0000u)}};
+}
+
+// The query (KEY false) or key rows: the element type's, or bfloat16 under B16.
+template <typename T, bool B16, bool KEY>
+__device__ __forceinline__ auto rows_of(const SmArgs<T>& a) {
+  if constexpr (B16)
+    return KEY ? a.kb : a.qb;
+  else
+    return KEY ? a.k : a.q;
+}
+
+template <typename T, int NCH, uint32_t ORD, typename R>
+__device__ __forceinline__ void gather(const SmArgs<T>& a, Gather<T, NCH>& g, const R* rows,
                                        const int64_t (&node)[kSmStep], const T* transport,
                                        const int64_t (&te)[kSmStep], int h) {
 #pragma unroll
   for (int u = 0; u < kSmStep; ++u) {
-    const T* r = rows + node[u] * a.D;
+    const R* r = rows + node[u] * a.D;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) g.row[u][c] = ld4(r + a.C.base[c] + h * a.C.stride[c]);
+    for (int c = 0; c < NCH; ++c) g.row[u][c] = row4<T>(r + a.C.base[c] + h * a.C.stride[c]);
     transport_pairs<T, NCH, ORD>(a.C, transport + te[u] * a.orders * 2, g.tc[u], g.ts[u]);
   }
 }
@@ -174,7 +199,7 @@ __device__ __forceinline__ void gather(const SmArgs<T>& a, Gather<T, NCH>& g, co
 // Forward.  The lane's edges are e0 + s + r S; every step requests the next
 // step's source ids before it waits for its own rows, so a step costs one
 // memory round trip.
-template <typename T, int NCH, uint32_t ORD>
+template <typename T, int NCH, uint32_t ORD, bool B16>
 __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   constexpr int U = kSmStep, R = kSmRegs;
   const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_nodes, kWavesPerBlock);
@@ -186,10 +211,10 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
 
   T q[NCH * 4];
-  const T* qi = a.q + i * a.D;
+  const auto qi = rows_of<T, B16, false>(a) + i * a.D;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const Quad<T> x = ld4(qi + a.C.base[c] + h * a.C.stride[c]);
+    const Quad<T> x = row4<T>(qi + a.C.base[c] + h * a.C.stride[c]);
 #pragma unroll
     for (int u = 0; u < 4; ++u) q[4 * c + u] = x.v[u];
   }
@@ -220,7 +245,7 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
       }
     }
     Gather<T, NCH> g;
-    gather<T, NCH, ORD>(a, g, a.k, jc, a.transport, te, h);
+    gather<T, NCH, ORD>(a, g, rows_of<T, B16, true>(a), jc, a.transport, te, h);
     T bias[U];
     uint8_t in[U];
 #pragma unroll
@@ -279,7 +304,7 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
 // Backward per target: the adjoint's per-head total, ds, and dq.  ds goes to
 // its edge's place in the source grouping (inv), so the per-source pass reads
 // it as one stream.
-template <typename T, int NCH, uint32_t ORD>
+template <typename T, int NCH, uint32_t ORD, bool B16>
 __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a) {
   constexpr int U = kSmStep;
   const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_nodes, kWavesPerBlock);
@@ -335,7 +360,7 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
     }
     fetch(eb + (int64_t)U * S);
     Gather<T, NCH> g;
-    gather<T, NCH, ORD>(a, g, a.k, jc, a.transport, te, h);
+    gather<T, NCH, ORD>(a, g, rows_of<T, B16, true>(a), jc, a.transport, te, h);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (eb + (int64_t)u * S >= e1) break;
@@ -369,7 +394,7 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
 // Backward per source over the edges grouped by source: ds, the targets and
 // the transport rows are streams in that order (ds written there by the
 // per-target pass), the query rows are gathered.
-template <typename T, int NCH, uint32_t ORD>
+template <typename T, int NCH, uint32_t ORD, bool B16>
 __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a) {
   constexpr int U = kSmStep;
   const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.src_ptr, a.n_nodes, kWavesPerBlock);
@@ -407,7 +432,7 @@ __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a)
     }
     fetch(gb + (int64_t)U * S);
     Gather<T, NCH> gq;
-    gather<T, NCH, ORD>(a, gq, a.q, tc, a.transport_s, te, h);
+    gather<T, NCH, ORD>(a, gq, rows_of<T, B16, false>(a), tc, a.transport_s, te, h);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (gb + (int64_t)u * S >= g1) break;
@@ -586,15 +611,31 @@ enum class Kind { Forward, BackwardTarget, BackwardSource };
 
 template <typename T, int NCH, uint32_t ORD = 0>
 void launch_fast_n(Kind kind, const SmArgs<T>& a, dim3 grid, hipStream_t stream) {
+  if (a.qb != nullptr) {
+    if constexpr (std::is_same<T, float>::value) {
+      switch (kind) {
+        case Kind::Forward:
+          hipLaunchKernelGGL((softmax_forward_fast<T, NCH, ORD, true>), grid, dim3(256), 0, stream, a);
+          break;
+        case Kind::BackwardTarget:
+          hipLaunchKernelGGL((softmax_backward_target_fast<T, NCH, ORD, true>), grid, dim3(256), 0, stream, a);
+          break;
+        case Kind::BackwardSource:
+          hipLaunchKernelGGL((softmax_backward_source_fast<T, NCH, ORD, true>), grid, dim3(256), 0, stream, a);
+          break;
+      }
+    }
+    return;
+  }
   switch (kind) {
     case Kind::Forward:
-      hipLaunchKernelGGL((softmax_forward_fast<T, NCH, ORD>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((softmax_forward_fast<T, NCH, ORD, false>), grid, dim3(256), 0, stream, a);
       break;
     case Kind::BackwardTarget:
-      hipLaunchKernelGGL((softmax_backward_target_fast<T, NCH, ORD>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((softmax_backward_target_fast<T, NCH, ORD, false>), grid, dim3(256), 0, stream, a);
       break;
     case Kind::BackwardSource:
-      hipLaunchKernelGGL((softmax_backward_source_fast<T, NCH, ORD>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((softmax_backward_source_fast<T, NCH, ORD, false>), grid, dim3(256), 0, stream, a);
       break;
   }
 }
@@ -610,6 +651,7 @@ inline bool orders_are(const Chunks& C, int n, uint32_t ord) {
 template <typename T>
 void launch(Kind kind, bool fast, const SmArgs<T>& a, hipStream_t stream) {
   const dim3 grid((unsigned)blocks_for(a.n_nodes));
+  if (a.qb != nullptr && !fast) return;  // unreachable: prepare refuses bfloat16 rows off the fast kernels
   if (fast && orders_are(a.C, 5, kOrders012) && a.orders > max_order_of(kOrders012)) {
     launch_fast_n<T, 5, kOrders012>(kind, a, grid, stream);
     return;
@@ -639,19 +681,25 @@ void launch(Kind kind, bool fast, const SmArgs<T>& a, hipStream_t stream) {
   }
 }
 
+// q and k are T rows, or bfloat16 rows (qb, kb) with T = float: then only the
+// fast kernels serve the call.
 template <typename T>
 int prepare(SmArgs<T>& a, bool& fast, const T* q, const T* k, const T* transport, const T* bias,
             const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr, const int64_t* source,
-            int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H, double scale) {
+            int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H, double scale,
+            const uint16_t* qb = nullptr, const uint16_t* kb = nullptr) {
   GM_REQUIRE(n_nodes >= 0 && n_edges >= 0, "sizes must be non-negative");
   GM_REQUIRE(n_nodes < (int64_t(1) << 31) * kWavesPerBlock, "too many nodes for one launch");
   a = SmArgs<T>{};
   const int rc = parse_attention_layout(desc, F, H, D, orders, a.L);
   if (rc != GM_OK) return rc;
-  if (n_nodes > 0) GM_REQUIRE(q && k && row_ptr, "q, k and row_ptr must be device pointers");
+  const bool b16 = qb != nullptr || kb != nullptr;
+  if (n_nodes > 0) GM_REQUIRE(b16 ? (qb && kb && row_ptr) : (q && k && row_ptr), "q, k and row_ptr must be device pointers");
   if (n_edges > 0) GM_REQUIRE(transport && bias && inside && source, "the per-edge tables must be device pointers");
   a.q = q;
   a.k = k;
+  a.qb = qb;
+  a.kb = kb;
   a.transport = transport;
   a.bias = bias;
   a.inside = inside;
@@ -665,7 +713,11 @@ int prepare(SmArgs<T>& a, bool& fast, const T* q, const T* k, const T* transport
   a.scale = (T)scale;
   const bool pow2 = (H == 1 || H == 2 || H == 4 || H == 8 || H == 16);
   a.hshift = H == 1 ? 0 : H == 2 ? 1 : H == 4 ? 2 : H == 8 ? 3 : 4;
-  fast = pow2 && make_chunks(a.L, a.C) && aligned(q, 4 * sizeof(T)) && aligned(k, 4 * sizeof(T));
+  fast = pow2 && make_chunks(a.L, a.C) &&
+         (b16 ? aligned(qb, 8) && aligned(kb, 8) : aligned(q, 4 * sizeof(T)) && aligned(k, 4 * sizeof(T)));
+  if (b16)
+    GM_REQUIRE(fast, "bfloat16 rows need heads whose segments are whole chunks of four reals (H a power of two "
+                     "up to 16) and 8-byte aligned rows");
   return GM_OK;
 }
 
@@ -673,11 +725,11 @@ template <typename T>
 int softmax_forward(const T* q, const T* k, const T* transport, const T* bias, const uint8_t* inside,
                     const int64_t* desc, const int64_t* row_ptr, const int64_t* source, int64_t n_nodes,
                     int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H, double scale, T* alpha,
-                    hipStream_t stream) {
+                    hipStream_t stream, const uint16_t* qb = nullptr, const uint16_t* kb = nullptr) {
   SmArgs<T> a;
   bool fast = false;
   const int rc = prepare(a, fast, q, k, transport, bias, inside, desc, row_ptr, source, n_nodes, n_edges, D, orders,
-                         F, H, scale);
+                         F, H, scale, qb, kb);
   if (rc != GM_OK) return rc;
   if (n_nodes == 0 || n_edges == 0) return GM_OK;
   GM_REQUIRE(alpha, "alpha must be a device pointer");
@@ -691,11 +743,12 @@ int softmax_backward(const T* dalpha, const T* q, const T* k, const T* transport
                      const int64_t* desc, const int64_t* row_ptr, const int64_t* source, const T* alpha,
                      int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H, double scale,
                      const int64_t* src_ptr, const int64_t* src_order, const int32_t* target_s, const int32_t* inv,
-                     const T* transport_s, T* ds, T* dq, T* dk, hipStream_t stream) {
+                     const T* transport_s, T* ds, T* dq, T* dk, hipStream_t stream, const uint16_t* qb = nullptr,
+                     const uint16_t* kb = nullptr) {
   SmArgs<T> a;
   bool fast = false;
   const int rc = prepare(a, fast, q, k, transport, bias, inside, desc, row_ptr, source, n_nodes, n_edges, D, orders,
-                         F, H, scale);
+                         F, H, scale, qb, kb);
   if (rc != GM_OK) return rc;
   if (n_nodes == 0) return GM_OK;
   GM_REQUIRE(dq && dk && src_ptr, "dq, dk and src_ptr must be device pointers");
@@ -705,6 +758,7 @@ int softmax_backward(const T* dalpha, const T* q, const T* k, const T* transport
   GM_REQUIRE(n_nodes < (int64_t(1) << 31) && n_edges < (int64_t(1) << 31),
              "the source-grouped streams index nodes and edges in 32 bits");
   fast = fast && aligned(dq, 4 * sizeof(T)) && aligned(dk, 4 * sizeof(T));
+  if (qb) GM_REQUIRE(fast, "bfloat16 rows need 16-byte aligned dq and dk");
   a.alpha_in = alpha;
   a.dalpha = dalpha;
   a.ds = ds;
@@ -770,4 +824,28 @@ extern "C" int gm_softmax_backward_f64(const double* dalpha, const double* q, co
   return gm::softmax_backward<double>(dalpha, q, k, transport, bias, inside, desc, row_ptr, source, alpha, n_nodes,
                                       n_edges, D, orders, F, H, scale, src_ptr, src_order, target_s, inv,
                                       transport_s, ds, dq, dk, (hipStream_t)stream);
+}
+
+extern "C" int gm_softmax_forward_bf16(const uint16_t* q, const uint16_t* k, const float* transport, const float* bias,
+                                       const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr,
+                                       const int64_t* source, int64_t n_nodes, int64_t n_edges, int64_t D,
+                                       int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
+                                       float* alpha, void* stream) {
+  (void)deg_max;
+  return gm::softmax_forward<float>(nullptr, nullptr, transport, bias, inside, desc, row_ptr, source, n_nodes,
+                                    n_edges, D, orders, F, H, scale, alpha, (hipStream_t)stream, q, k);
+}
+
+extern "C" int gm_softmax_backward_bf16(const float* dalpha, const uint16_t* q, const uint16_t* k,
+                                        const float* transport, const float* bias, const uint8_t* inside,
+                                        const int64_t* desc, const int64_t* row_ptr, const int64_t* source,
+                                        const float* alpha, int64_t n_nodes, int64_t n_edges, int64_t D,
+                                        int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
+                                        const int64_t* src_ptr, const int64_t* src_order, const int32_t* target_s,
+                                        const int32_t* inv, const float* transport_s, float* ds, float* dq,
+                                        float* dk, void* stream) {
+  (void)deg_max;
+  return gm::softmax_backward<float>(dalpha, nullptr, nullptr, transport, bias, inside, desc, row_ptr, source, alpha,
+                                     n_nodes, n_edges, D, orders, F, H, scale, src_ptr, src_order, target_s, inv,
+                                     transport_s, ds, dq, dk, (hipStream_t)stream, q, k);
 }

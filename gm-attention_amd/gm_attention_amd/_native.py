@@ -50,6 +50,8 @@ SIGNATURES: dict[str, list[Any]] = {
 
 #: fp32-only and host-only entry points (name -> (restype, argtypes)).
 SIGNATURES_F32 = {
+    "gm_softmax_forward_bf16": (ctypes.c_int, [_P] * 8 + [_I] * 6 + [_D, _I, _P, _P]),
+    "gm_softmax_backward_bf16": (ctypes.c_int, [_P] * 10 + [_I] * 6 + [_D, _I] + [_P] * 9),
     "gm_radial_trunk_forward_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_D, _P, _P]),
     "gm_radial_trunk_backward_f32": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_D, _P, _P, _P]),
     "gm_radial_trunk_partials": (ctypes.c_int64, [_I]),
@@ -58,6 +60,8 @@ SIGNATURES_F32 = {
     "gm_node_mix_weight_partials": (ctypes.c_int64, [_I, _I, _I]),
     "gm_node_mix_backward_weight_f32": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P]),
     "gm_node_mix_backward_weight_noalloc_f32": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P]),
+    "gm_node_mix_forward_bf16": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P]),
+    "gm_node_mix_backward_weight_bf16": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P]),
     "gm_xcd_block_map": (ctypes.c_int, [_I, ctypes.c_int, _P, _I, ctypes.c_int, _P]),
     "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
                                         + [_P, _P]),
@@ -137,6 +141,11 @@ def _suffix(dtype: torch.dtype) -> str:
     if dtype == torch.float64:
         return "_f64"
     raise RuntimeError(f"libgmhip supports float32 and float64, got {dtype}")
+
+
+def _row_suffix(dtype: torch.dtype) -> str:
+    """The softmax entry points' suffix: bfloat16 rows have their own (float32 tables)."""
+    return "_bf16" if dtype == torch.bfloat16 else _suffix(dtype)
 
 
 def _stream(device: torch.device) -> int:
@@ -257,8 +266,11 @@ class AttentionExtension:
         _require_device(q, k, transport, bias, inside, row_ptr, source)
         _check(desc.is_contiguous(), "every tensor must be contiguous")
         n, e = q.shape[0], source.shape[0]
-        for t in (k, transport, bias):
-            _check(t.dtype == q.dtype, "q, k and the tables must share a dtype")
+        _check(k.dtype == q.dtype, "q and k must share a dtype")
+        # bfloat16 rows read float32 tables (and give float32 weights and gradients)
+        table = torch.float32 if q.dtype == torch.bfloat16 else q.dtype
+        for t in (transport, bias):
+            _check(t.dtype == table, "the tables must be q's dtype (float32 for bfloat16 rows)")
         _check(k.shape == q.shape, "q and k must share a shape")
         _check(1 <= H <= 16, "at most 16 heads")
         _check(transport.dim() == 3 and transport.shape[0] == e and transport.shape[2] == 2,
@@ -276,11 +288,11 @@ class AttentionExtension:
                         row_ptr: Tensor, source: Tensor, H: int, scale: float, deg_max: int) -> Tensor:
         """alpha (n_edges, H): the heads' neighbourhood softmax of the transported scores."""
         self._check_softmax(q, k, transport, bias, inside, desc, row_ptr, source, H)
-        alpha = torch.empty(source.shape[0], H, dtype=q.dtype, device=q.device)
+        alpha = torch.empty(source.shape[0], H, dtype=transport.dtype, device=q.device)
         if q.shape[0] == 0:
             return alpha
         hd = host_desc(desc)
-        _call("gm_softmax_forward" + _suffix(q.dtype), _ptr(q), _ptr(k), _ptr(transport), _ptr(bias), _ptr(inside),
+        _call("gm_softmax_forward" + _row_suffix(q.dtype), _ptr(q), _ptr(k), _ptr(transport), _ptr(bias), _ptr(inside),
               hd.data_ptr(), _ptr(row_ptr), _ptr(source), q.shape[0], source.shape[0], q.shape[1], transport.shape[1],
               hd.shape[0], H, float(scale), int(deg_max), _ptr(alpha), _stream(q.device))
         return alpha
@@ -292,16 +304,18 @@ class AttentionExtension:
         self._check_softmax(q, k, transport, bias, inside, desc, row_ptr, source, H)
         for t in (alpha, dalpha):
             _check(t.is_contiguous() and t.dim() == 2 and t.shape[0] == source.shape[0] and t.shape[1] == H
-                   and t.dtype == q.dtype, "alpha and dalpha must be contiguous (n_edges, H) in q's dtype")
-        dq = torch.empty_like(q)
-        dk = torch.empty_like(q)
+                   and t.dtype == transport.dtype,
+                   "alpha and dalpha must be contiguous (n_edges, H) in the tables' dtype")
+        # the gradients in the arithmetic's dtype (float32 for bfloat16 rows)
+        dq = torch.empty(q.shape, dtype=transport.dtype, device=q.device)
+        dk = torch.empty(q.shape, dtype=transport.dtype, device=q.device)
         if q.shape[0] == 0:
             return [dq, dk]
         src_ptr, src_order, _ = source_major(source, row_ptr)
         target_s, inv, transport_s = source_grouped_tables(source, row_ptr, transport.contiguous())
-        ds = torch.empty(source.shape[0], H, dtype=q.dtype, device=q.device)
+        ds = torch.empty(source.shape[0], H, dtype=transport.dtype, device=q.device)
         hd = host_desc(desc)
-        _call("gm_softmax_backward" + _suffix(q.dtype), _ptr(dalpha), _ptr(q), _ptr(k), _ptr(transport), _ptr(bias),
+        _call("gm_softmax_backward" + _row_suffix(q.dtype), _ptr(dalpha), _ptr(q), _ptr(k), _ptr(transport), _ptr(bias),
               _ptr(inside), hd.data_ptr(), _ptr(row_ptr), _ptr(source), _ptr(alpha), q.shape[0], source.shape[0],
               q.shape[1], transport.shape[1], hd.shape[0], H, float(scale), int(deg_max), _ptr(src_ptr),
               _ptr(src_order), _ptr(target_s), _ptr(inv), _ptr(transport_s), _ptr(ds), _ptr(dq), _ptr(dk),
@@ -626,10 +640,10 @@ def radial_trunk_backward(dh: Tensor, rho: Tensor, weight: Tensor, bias: Tensor 
 
 
 def _column_view(v: Tensor) -> tuple[int, int]:
-    """(rows, leading dimension) of a 2-D float32 view whose rows are evenly
-    strided and whose columns are contiguous (a column slice of flat rows)."""
-    _check(v.dim() == 2 and v.dtype == torch.float32 and v.device.type == "cuda",
-           "node vectors must be a 2-D float32 tensor on the GPU")
+    """(rows, leading dimension) of a 2-D float32 (or bfloat16) view whose rows
+    are evenly strided and whose columns are contiguous (a column slice of flat rows)."""
+    _check(v.dim() == 2 and v.dtype in (torch.float32, torch.bfloat16) and v.device.type == "cuda",
+           "node vectors must be a 2-D float32 or bfloat16 tensor on the GPU")
     _check(v.stride(1) == 1 or v.shape[1] == 1, "node vectors must have contiguous columns")
     return v.shape[0], (v.stride(0) if v.shape[0] > 1 else v.shape[1])
 
@@ -642,7 +656,8 @@ def node_mix_forward(v: Tensor, m: Tensor) -> Tensor:
     _check(v.shape[1] == w and m.is_contiguous() and m.dtype == torch.float32 and m.device == v.device,
            "the mixing matrix must be a contiguous float32 (w, C) on the node vectors' device")
     out = torch.empty(N, C, dtype=torch.float32, device=v.device)
-    _call("gm_node_mix_forward_f32", _ptr(v), max(ldv, w), _ptr(m), N, w, C, _ptr(out), _stream(v.device))
+    name = "gm_node_mix_forward_bf16" if v.dtype == torch.bfloat16 else "gm_node_mix_forward_f32"
+    _call(name, _ptr(v), max(ldv, w), _ptr(m), N, w, C, _ptr(out), _stream(v.device))
     return out
 
 
@@ -667,8 +682,8 @@ def node_mix_backward_weight(v: Tensor, dmix: Tensor) -> Tensor:
     partial = torch.empty(max(int(lib.gm_node_mix_weight_partials(N, w, C)), 1), dtype=torch.float32,
                           device=dmix.device)
     dm = torch.empty(w, C, dtype=torch.float32, device=dmix.device)
-    _call("gm_node_mix_backward_weight_f32", _ptr(v), max(ldv, w), _ptr(dmix), N, w, C, _ptr(partial), _ptr(dm),
-          _stream(dmix.device))
+    name = "gm_node_mix_backward_weight_bf16" if v.dtype == torch.bfloat16 else "gm_node_mix_backward_weight_f32"
+    _call(name, _ptr(v), max(ldv, w), _ptr(dmix), N, w, C, _ptr(partial), _ptr(dm), _stream(dmix.device))
     return dm
 
 

@@ -233,6 +233,18 @@ def _heads_permutation(mhsa: SO2MHSA, device: torch.device) -> Tensor:
     return perm
 
 
+def batched_flat_serves(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> bool:
+    """Whether :func:`_attend_batched_flat` serves ``x`` (bfloat16 rows are
+    served only there: the scores read them in place of float32 rows, the
+    node mixes read them, everything after runs in float32)."""
+    if not mhsa.batched or x._rows().ndim != 2:
+        return False
+    edges = _resolve_edges(edges, mhsa.cutoff)
+    values = [cast(SO2SteerableKernel, head.value) for head in mhsa.heads]
+    return (fused_attention.softmax_enabled(mhsa, x, edges) and kernels.factored_enabled()
+            and fused_factored.enabled(values[0], x, edges))
+
+
 def _attend_batched_flat(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> Tensor | None:
     """The batched layer on flat rows when the fused softmax and the fused
     factored heads serve it (else None): the stacked query and key
@@ -252,7 +264,8 @@ def _attend_batched_flat(mhsa: SO2MHSA, x: SO2FeatureField, edges) -> Tensor | N
         keys = _stacked_flat([h.key for h in heads], mhsa.field_type_in, rows)
         alpha = fused_attention.softmax(mhsa, queries, keys, edges)  # (n_edges, n_heads)
         groups = fused_factored.groups_for(edges, edges.source_index)
-        if radial.eligible(values, x.dtype, x.device):
+        compute = torch.float32 if x.dtype == torch.bfloat16 else x.dtype
+        if radial.eligible(values, compute, x.device):
             h, trunk = None, functools.partial(radial.trunk_hidden_heads, values)
         else:
             h, trunk = torch.stack([k._trunk_hidden(edges.distances) for k in values]), None

@@ -37,7 +37,7 @@ import torch
 from torch import Tensor, nn
 
 from gm_attention_amd.nn import fused_factored, kernels, radial
-from gm_attention_amd.nn.attention import SO2MHSA, gather_to_edges, weighted_segment_sum
+from gm_attention_amd.nn.attention import SO2MHSA, batched_flat_serves, gather_to_edges, weighted_segment_sum
 from gm_attention_amd.nn.convolution import SO2Convolution
 from gm_attention_amd.nn.fused_attention import evaluate_aggregation_window
 from gm_attention_amd.nn.kernels import SO2SteerableKernel
@@ -119,7 +119,14 @@ class SO2TransformerBlock(nn.Module):
         return self._run(x, edges, chunk_size=chunk_size)
 
     def _mix(self, h: Tensor, edges, chunk_size: int | None) -> Tensor:
-        """The mixer on flat rows, in the mixer's parameter dtype, back in the rows' dtype."""
+        """The mixer on flat rows: bfloat16 rows straight into the batched
+        attention's fused path where it serves them (its scores and node mixes
+        read them, its arithmetic is float32), else the rows in the mixer's
+        parameter dtype; the result in float32 or that dtype."""
+        if h.dtype == torch.bfloat16 and chunk_size is None and self.mixer == "attention":
+            field = SO2FeatureField.from_flat(self.field_type, h)
+            if batched_flat_serves(self.attention, field, edges):
+                return self.attention(field, edges)._rows()
         pdtype = next(self.attention.parameters()).dtype
         field = SO2FeatureField.from_flat(self.field_type, h.to(pdtype))
         if chunk_size is None:

@@ -246,9 +246,17 @@ def _device_ok(x: Any) -> bool:
     return x.dtype in (torch.float32, torch.float64)
 
 
+def _rows_ok(x: Any, heads: int) -> bool:
+    """The scores' rows: the element types of _device_ok, or bfloat16 rows on
+    the GPU whose heads the fast kernels serve (a power of two up to 16)."""
+    if x.dtype == torch.bfloat16:
+        return MODE not in ("0", "cpu") and x.device.type == "cuda" and heads in (1, 2, 4, 8, 16)
+    return _device_ok(x)
+
+
 def softmax_enabled(mhsa: Any, x: Any, edges: Any) -> bool:
     """Whether the batched attention takes the fused scores-and-softmax op."""
-    if not _device_ok(x) or mhsa.num_heads > MAX_H:
+    if not _rows_ok(x, mhsa.num_heads) or mhsa.num_heads > MAX_H:
         return False
     p = plan(mhsa)
     if len(p.rows) > MAX_F or p.width > MAX_D or max((n for n, *_ in p.rows), default=0) > edges.max_frequency:
@@ -340,9 +348,10 @@ class Softmax(torch.autograd.Function):
 
 
 def softmax(mhsa: Any, q: Tensor, k: Tensor, edges: Any) -> Tensor:
-    """The heads' attention weights ``(n_edges, n_heads)`` (reference :400-410)."""
+    """The heads' attention weights ``(n_edges, n_heads)`` (reference :400-410);
+    bfloat16 rows take float32 tables and give float32 weights."""
     p = plan(mhsa)
-    g = geometry(edges, mhsa.cutoff, mhsa.heads[0].window, q.dtype)
+    g = geometry(edges, mhsa.cutoff, mhsa.heads[0].window, torch.float32 if q.dtype == torch.bfloat16 else q.dtype)
     scale = float(mhsa.heads[0]._score_scale)
     top = max((n for n, *_ in p.rows), default=0)
     return Softmax.apply(q.contiguous(), k.contiguous(), g.transport_to(top), g.bias, g.inside,

@@ -191,11 +191,16 @@ def declined(kernel: Any, x: SO2FeatureField, edges: Any) -> str:
         return "GM_FUSED_FACTORED=0: this build implements the factored kernel only through the fused HIP op"
     if x.device.type != "cuda":
         return "the fused factored op runs on the GPU only (this build has no CPU driver)"
-    if x.dtype not in (torch.float32, torch.float64):
-        return f"the fused factored op takes float32 or float64, got {x.dtype}"
+    if x.dtype not in (torch.float32, torch.float64, torch.bfloat16):
+        return f"the fused factored op takes float32, float64 or bfloat16 rows, got {x.dtype}"
     trunk = kernel.complex_head.in_features if kernel.complex_head is not None else kernel.real_head.in_features
     if trunk + 1 > MAX_K:
         return "the kernel's trunk exceeds the fused op's bound (K <= 20)"
+    if x.dtype == torch.bfloat16:
+        widest = max((m if f == 0 else 2 * m) for f, m in kernel.field_type_in.items())
+        if head_split(kernel, trunk + 1) == 0 or widest > 64:
+            return ("bfloat16 rows take the grouped kernels only (float32 arithmetic, node vectors at most 64 "
+                    "reals); this kernel does not fit them")
     if tiles(kernel) == ():
         return "an output copy's blocks exceed the fused op's bounds even one copy at a time"
     if edges.n_edges == 0:
@@ -1065,7 +1070,8 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
     order directly.  Heads too wide for the grouped kernels run there as
     shares of their output copies (:func:`head_split`)."""
     K = (h.shape[2] if h is not None else kernels[0].complex_head.in_features) + 1
-    dtype = h.dtype if h is not None else x.dtype
+    # bfloat16 rows: the node mixes read them as they are, everything after runs in float32
+    dtype = h.dtype if h is not None else (torch.float32 if x.dtype == torch.bfloat16 else x.dtype)
     split = head_split(kernels[0], K) if dtype == torch.float32 else 0
     hp = heads_plan(sub_head(kernels[0], max(split, 1)))
     ok, pa, pt = grouped_eligible(hp, dtype, K)

@@ -107,13 +107,14 @@ class NodeMixes(torch.autograd.Function):
                 disjoint = all(a[0] + a[1] <= b[0] for a, b in zip(ranges, ranges[1:]))
                 covered = (disjoint and sum(w for _, w in columns) == rows.shape[1]
                            and all(d is not None for d in dmixes))
-                dx = torch.empty_like(rows) if covered else torch.zeros_like(rows)
+                # the input gradient in float32 (bfloat16 rows: autograd rounds it into their dtype)
+                dx = (torch.empty if covered else torch.zeros)(rows.shape, dtype=torch.float32, device=rows.device)
                 written: list[tuple[int, int]] = []
                 for (off, w), m, d in zip(columns, mats, dmixes, strict=True):
                     if d is None:
                         continue
                     if any(off < o + ww and o < off + w for o, ww in written):
-                        part = torch.empty(rows.shape[0], w, dtype=rows.dtype, device=rows.device)
+                        part = torch.empty(rows.shape[0], w, dtype=torch.float32, device=rows.device)
                         _native.node_mix_backward_input(d.contiguous(), m, part)
                         dx[:, off:off + w] += part
                     else:
@@ -132,6 +133,8 @@ class NodeMixes(torch.autograd.Function):
 
 def mixes_eligible(rows: Tensor, widths: list[int], mats: list[Tensor]) -> bool:
     """Whether :class:`NodeMixes` serves these products: float32 flat rows on
-    the GPU, node vectors at most 128 reals wide, mix widths a multiple of 4."""
-    return (rows.dtype == torch.float32 and rows.device.type == "cuda" and rows.dim() == 2
-            and all(1 <= w <= 128 for w in widths) and all(m.shape[1] % 4 == 0 for m in mats))
+    the GPU with node vectors at most 128 reals wide, or bfloat16 rows with
+    vectors at most 64 wide (float32 mixes either way); mix widths a multiple of 4."""
+    widest = 128 if rows.dtype == torch.float32 else (64 if rows.dtype == torch.bfloat16 else 0)
+    return (rows.device.type == "cuda" and rows.dim() == 2 and all(1 <= w <= widest for w in widths)
+            and all(m.shape[1] % 4 == 0 for m in mats))

@@ -93,6 +93,24 @@ int gm_softmax_forward_f64(const double* q, const double* k, const double* trans
                            int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H,
                            double scale, int64_t deg_max, double* alpha, void* stream);
 
+/* bfloat16 rows for q and k (widened exactly in the kernels), every other
+ * tensor float32: the arithmetic of the _f32 entry points, alpha, dq and dk
+ * float32.  Build-specific, no counterpart in the reference's op (whose
+ * tensors share one dtype); the attention layer reaches them for bfloat16
+ * rows.  Heads a power of two up to 16 whose segments are whole chunks of four
+ * reals, rows 8-byte aligned (else GM_ERR_ARGUMENT). */
+int gm_softmax_forward_bf16(const uint16_t* q, const uint16_t* k, const float* transport, const float* bias,
+                            const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr, const int64_t* source,
+                            int64_t n_nodes, int64_t n_edges, int64_t D, int64_t orders, int64_t F, int64_t H,
+                            double scale, int64_t deg_max, float* alpha, void* stream);
+int gm_softmax_backward_bf16(const float* dalpha, const uint16_t* q, const uint16_t* k, const float* transport,
+                             const float* bias, const uint8_t* inside, const int64_t* desc, const int64_t* row_ptr,
+                             const int64_t* source, const float* alpha, int64_t n_nodes, int64_t n_edges, int64_t D,
+                             int64_t orders, int64_t F, int64_t H, double scale, int64_t deg_max,
+                             const int64_t* src_ptr, const int64_t* src_order, const int32_t* target_s,
+                             const int32_t* inv, const float* transport_s, float* ds, float* dq, float* dk,
+                             void* stream);
+
 /* The softmax adjoint and the scores' backward: dq (n_nodes, D) written, dk
  * (n_nodes, D) written (every row, zero where a node is nobody's source).
  *
@@ -514,6 +532,17 @@ int gm_node_mix_backward_input_f32(const float* dmix, const float* M, int64_t N,
 int64_t gm_node_mix_weight_partials(int64_t N, int64_t w, int64_t C);
 int gm_node_mix_backward_weight_f32(const float* v, int64_t ldv, const float* dmix, int64_t N, int64_t w, int64_t C,
                                     float* partial, float* dM, void* stream);
+
+/* The forward and the weight gradient for bfloat16 node vectors (the rows of
+ * a bfloat16 field, widened exactly while staged; w <= 64), M, dmix, out and
+ * dM float32: the products of the float32 entry points on the widened values.
+ * Build-specific, no counterpart in the reference's op (whose tensors share
+ * one dtype); the layers reach them for bfloat16 rows.  The input gradient of
+ * a bfloat16 field is gm_node_mix_backward_input_f32's float32 dv. */
+int gm_node_mix_forward_bf16(const uint16_t* v, int64_t ldv, const float* M, int64_t N, int64_t w, int64_t C,
+                             float* out, void* stream);
+int gm_node_mix_backward_weight_bf16(const uint16_t* v, int64_t ldv, const float* dmix, int64_t N, int64_t w,
+                                     int64_t C, float* partial, float* dM, void* stream);
 
 /* gm_node_mix_backward_weight_f32 without a workspace argument and without
  * allocating: no counterpart in the reference; for callers that cannot
