@@ -69,6 +69,7 @@ struct FactArgs {
   const T* rows;          // aggregated form or null
   T* dh;
   T* dweights;
+  int accumulate;  // grouped backward: add dh and dweights into the outputs instead of writing them
   int64_t n_groups;
   int K, wc, wr, C, KP, CP, n_f, n_blocks, d_out;
   int tile;  // backward: edges per LDS tile (a power of two <= 64)
@@ -1120,7 +1121,7 @@ __global__ __launch_bounds__(64) void factored_backward_grouped(FactArgs<float> 
       const float* gr = Gt + lane * d_out;
       float sum = 0.f;
       for (int o = 0; o < d_out; ++o) sum += gr[o] * r[o];
-      a.dweights[base + lane] = sum;
+      a.dweights[base + lane] = a.accumulate ? a.dweights[base + lane] + sum : sum;
     }
     float w[NT][4];
 #pragma unroll
@@ -1153,7 +1154,7 @@ __global__ __launch_bounds__(64) void factored_backward_grouped(FactArgs<float> 
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int e = 4 * q + r;
-      if (e < n && m + 1 < a.K) a.dh[(base + e) * 16 + m] = dh[r];
+      if (e < n && m + 1 < a.K) a.dh[(base + e) * 16 + m] = a.accumulate ? a.dh[(base + e) * 16 + m] + dh[r] : dh[r];
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -1844,12 +1845,15 @@ struct BwdTile {
   PhaseRegs<P> ph;  // as in the forward
   float rho, w;     // edge m (rho: runtime slots or the fused trunk)
   int64_t tgt;      // runtime slots: the target of edge m
+  floatx4 dh_old;   // accumulating: dh(edge m)[4 q .. 4 q + 3] already in the output
+  float dw_old;     // accumulating: dweights(edge m) already in the output
 };
 
 template <class P>
 __device__ __forceinline__ BwdTile<P> load_bwd(__amdgpu_buffer_rsrc_t h_r, __amdgpu_buffer_rsrc_t ph_r,
                                                __amdgpu_buffer_rsrc_t rho_r, __amdgpu_buffer_rsrc_t w_r,
-                                               __amdgpu_buffer_rsrc_t t_r, int tb, int m, int q, bool fused) {
+                                               __amdgpu_buffer_rsrc_t t_r, int tb, int m, int q, bool fused,
+                                               __amdgpu_buffer_rsrc_t dh_r, __amdgpu_buffer_rsrc_t dw_r, bool acc) {
   BwdTile<P> t;
   if (fused) {
     t.h = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -1868,6 +1872,13 @@ __device__ __forceinline__ BwdTile<P> load_bwd(__amdgpu_buffer_rsrc_t h_r, __amd
     t.rho = bload1(rho_r, e * 4);
   }
   t.w = bload1(w_r, e * 4);
+  if (acc) {
+    t.dh_old = bload4(dh_r, (e * 16 + 4 * q) * 4);
+    t.dw_old = bload1(dw_r, e * 4);
+  } else {
+    t.dh_old = floatx4{0.f, 0.f, 0.f, 0.f};
+    t.dw_old = 0.f;
+  }
   return t;
 }
 
@@ -1996,7 +2007,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
   // dweights = <g(target), row>: the four lanes' shares of edge m
   dwp += __shfl_xor(dwp, 16, kWave);
   dwp += __shfl_xor(dwp, 32, kWave);
-  bstore1(dwp, sp.dw, q == 0 ? (tb + m) * 4 : kDrop);
+  bstore1(dwp + cur.dw_old, sp.dw, q == 0 ? (tb + m) * 4 : kDrop);
   // dh(e)_t = sum_c W(e)_c Z_t,c: lane (m, q) ends with edge m's features 4 q .. 4 q + 3
   floatx4 dh = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -2004,7 +2015,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       if (kstep_live<P>(a, nt, r)) dh = mfma16(zb[nt][r], wv[nt][r], dh);
-  bstore4(dh, sp.dh, ((tb + m) * 16 + 4 * q) * 4);
+  bstore4(dh + cur.dh_old, sp.dh, ((tb + m) * 16 + 4 * q) * 4);
   // W through LDS, column-major, for dZ's edge-major operand
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
@@ -2027,7 +2038,8 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
   wave_sync();
 }
 
-template <int NT, class P, bool FUSED>
+// ACC: dh and dweights added into the outputs (a later share of a head).
+template <int NT, class P, bool FUSED, bool ACC>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED || P::kDout > 40 ? 2 : 3) : 1))) void
 factored_backward_lanes(FactArgs<float> a) {
   constexpr int ZS = 16 * NT + 4;
@@ -2056,14 +2068,15 @@ factored_backward_lanes(FactArgs<float> a) {
   sp.rows = span(a.rows + g0 * d_out, (int64_t)ng * d_out * 4);
   sp.dh = span(a.dh + g0 * 16, (int64_t)ng * 64);
   sp.dw = span(a.dweights + g0, (int64_t)ng * 4);
+  constexpr bool acc = ACC;
   // Two tiles in flight (buffers A and B, each refilled right after its
   // tile's stores); with static slots the targets run three tiles ahead and
   // the targets' gradient values and row values two, so no load is waited
   // for within the tile after the one that issued it.
   // The first tiles' streams and targets are requested with the node's mixes
   // (one round trip), then the targets' gradient values.
-  BwdTile<P> ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, 0, m, q, fused);
-  BwdTile<P> tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, kMT, m, q, fused);
+  BwdTile<P> ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, 0, m, q, fused, sp.dh, sp.dw, acc);
+  BwdTile<P> tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, kMT, m, q, fused, sp.dh, sp.dw, acc);
   int64_t t0 = 0, t1 = 0;
   if constexpr (P::kStatic) {
     t0 = bload_i64(sp.t, m * 8);
@@ -2101,7 +2114,7 @@ factored_backward_lanes(FactArgs<float> a) {
       load_outs<NT, P>(oa, a.g, tn, sp.rows, (tb + 2 * kMT + m) * d_out, q);
       tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
     }
-    ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused);
+    ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused, sp.dh, sp.dw, acc);
     tb += kMT;
     if (tb >= ng) break;
     backward_tile<NT, P>(a, tbf, ob, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl, fused);
@@ -2109,7 +2122,7 @@ factored_backward_lanes(FactArgs<float> a) {
       load_outs<NT, P>(ob, a.g, tn, sp.rows, (tb + 2 * kMT + m) * d_out, q);
       tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
     }
-    tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused);
+    tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused, sp.dh, sp.dw, acc);
     tb += kMT;
     if (tb >= ng) break;
   }
@@ -2486,9 +2499,11 @@ void launch_lanes_nt(bool forward, const FactArgs<float>& a, hipStream_t stream)
       hipLaunchKernelGGL((factored_forward_lanes<NT, P, false, false>), grid, block, 0, stream, a);
   } else {
     if (fused)
-      hipLaunchKernelGGL((factored_backward_lanes<NT, P, true>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((factored_backward_lanes<NT, P, true, false>), grid, block, 0, stream, a);
+    else if (a.accumulate)
+      hipLaunchKernelGGL((factored_backward_lanes<NT, P, false, true>), grid, block, 0, stream, a);
     else
-      hipLaunchKernelGGL((factored_backward_lanes<NT, P, false>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((factored_backward_lanes<NT, P, false, false>), grid, block, 0, stream, a);
   }
 }
 
@@ -2769,7 +2784,7 @@ extern "C" int gm_factored_backward_grouped_f32(
     const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
     int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
     int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
-    int64_t trunk_nb, double trunk_width, float* dh_g, float* dweights_g, void* stream) {
+    int64_t trunk_nb, double trunk_width, int64_t accumulate, float* dh_g, float* dweights_g, void* stream) {
   GM_REQUIRE(z && dz && node_stride && t_stride && width, "the mix runs must be host arrays");
   const gm::Runs<float> runs{z, dz, node_stride, t_stride, width, n_runs};
   gm::FactArgs<float> a;
@@ -2790,6 +2805,8 @@ extern "C" int gm_factored_backward_grouped_f32(
   a.rows = rows_g;
   a.dh = dh_g;
   a.dweights = dweights_g;
+  a.accumulate = accumulate != 0;
+  GM_REQUIRE(!(a.accumulate && trunk_w), "the fused trunk's backward writes dh_g and dweights_g (no accumulate)");
   gm::launch_grouped(false, a, (hipStream_t)stream);
   return gm::check_launch("factored_backward_grouped");
 }

@@ -580,7 +580,7 @@ template <int W>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void node_mix_dinput_split(const float* __restrict__ dmix,
                                                                   const float* __restrict__ M, int64_t N, int w,
                                                                   int64_t C, float* __restrict__ dv, int64_t lddv) {
-  constexpr int KC = 64, LDD = KC + 4, LDM = KC + 8, JW = W / 16;
+  constexpr int KC = 64, LDD = KC + 4, LDM = KC + 4, JW = W / 16;  // LDM: a 16-lane 8-byte read covers 32 banks once
   constexpr int DQ = 128 * KC / 4 / kThreads;
   constexpr int MQ = W * KC / 4 / kThreads;
   __shared__ __align__(16) float dt[128 * LDD];
@@ -681,7 +681,9 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __re
                                                                    const float* __restrict__ dmix, int64_t N, int w,
                                                                    int64_t C, int64_t rps, float* __restrict__ partial,
                                                                    int vec_v) {
-  constexpr int RC = 64, LDV = dweight_ldv<W>(), LDM = 64 + 16, IW = W / 16;
+  // lanes (c, q) read rows 16 wv + 4 q + s: strides with 4 LD = 16 (mod 64) words put a quarter-wave's
+  // rows in distinct banks
+  constexpr int RC = 64, LDV = W + 4, LDM = 64 + 4, IW = W / 16;
   constexpr int VQ = (RC * W / 4 + kThreads - 1) / kThreads;
   constexpr int DQ = RC * 64 / 4 / kThreads;
   __shared__ __align__(16) float vt[RC * LDV];

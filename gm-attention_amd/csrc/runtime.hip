@@ -57,7 +57,7 @@ int parse_attention_layout(const int64_t* desc, int64_t F, int64_t H, int64_t D,
 
 extern "C" const char* gm_last_error(void) { return gm::last_error.c_str(); }
 
-extern "C" int gm_abi_version(void) { return 2; }
+extern "C" int gm_abi_version(void) { return 3; }
 
 extern "C" int gm_xcd_block_map(int64_t nb, int kind, const int64_t* ptr, int64_t n_items, int per, int64_t* out) {
   GM_REQUIRE(nb >= 1 && out != nullptr, "nb must be positive and out a host array of nb entries");

@@ -66,7 +66,7 @@ SIGNATURES_F32 = {
     "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
                                         + [_P, _P]),
     "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
-                                         + [_P] * 3),
+                                         + [_I] + [_P] * 3),
     "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
     "gm_factored_lane_tables": (ctypes.c_int, [_P] + [_I] * 6 + [_P] * 3),
     "gm_factored_aggregate_heads_f32": (ctypes.c_int, [_P] * 4 + [_I] * 5 + [_P, _P]),
@@ -748,11 +748,16 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
                               runs: MixRuns, n_nodes: int, phase_g: Tensor, rho_g: Tensor, zw_g: Tensor | None,
                               pa: int, pt: int, desc: Tensor, group_ptr: Tensor, group_source: Tensor,
                               group_order: Tensor | None, K: int, wc: int, wr: int, dh_g: Tensor,
-                              dweights: Tensor | None = None, trunk: FusedTrunk | None = None) -> Tensor:
+                              dweights: Tensor | None = None, trunk: FusedTrunk | None = None,
+                              accumulate: bool = False) -> Tensor:
     """dh (grouping order) into ``dh_g``, the mix gradients into the runs'
     gradient arrays; returns dweights in the grouping's order (into
     ``dweights`` when given).  With ``trunk`` the kernels evaluate h from
-    ``rho_g`` and ``h_g`` may be None."""
+    ``rho_g`` and ``h_g`` may be None.  ``accumulate``: dh and dweights are
+    added to ``dh_g`` and ``dweights`` (which must then be given) instead of
+    written."""
+    if accumulate and dweights is None:
+        raise ValueError("accumulate needs the dweights to add to")
     if h_g is None and trunk is None:
         raise ValueError("h_g is required without a fused trunk")
     if dweights is None:
@@ -769,8 +774,8 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
           ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),
           _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, n_edges, group_source.shape[0], K,
-          wc, wr, pa, pt, hd.shape[0], g.shape[1], *(trunk.args() if trunk is not None else _NO_TRUNK), _ptr(dh_g),
-          _ptr(dweights), _stream(rho_g.device))
+          wc, wr, pa, pt, hd.shape[0], g.shape[1], *(trunk.args() if trunk is not None else _NO_TRUNK),
+          int(accumulate), _ptr(dh_g), _ptr(dweights), _stream(rho_g.device))
     return dweights
 
 

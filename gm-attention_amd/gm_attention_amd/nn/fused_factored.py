@@ -938,22 +938,17 @@ class FactoredHeadsGrouped(torch.autograd.Function):
         dh_g = torch.empty_like(h_g)
         alpha_gt = _native.gather_transpose(alpha, st.perm)  # (H, E) in the grouping's order
         dalpha_gt = torch.empty_like(alpha_gt)
-        part_dh = torch.empty_like(h_g[0]) if split > 1 else None
-        part_da = torch.empty_like(alpha_gt[0]) if split > 1 else None
         grad = grad.contiguous()
         for v in range(shares):
             head, share = divmod(v, split)
             runs = _heads_runs(meta, mixes, v, dmixes)
-            first = share == 0
+            # a head's shares read the same trunk features and weights: the later shares add their gradients
             with torch.profiler.record_function("gm::kernel/pairs_backward"):
                 _native.factored_backward_grouped(
                     grad[:, v].contiguous(), st.target_g, alpha_gt[head], rows[v], h_g[head], runs,
                     meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
                     meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"],
-                    dh_g[head] if first else part_dh, dweights=dalpha_gt[head] if first else part_da)
-            if not first:  # the head's shares read the same trunk features and weights: their gradients add
-                dh_g[head].add_(part_dh)
-                dalpha_gt[head].add_(part_da)
+                    dh_g[head], dweights=dalpha_gt[head], accumulate=share > 0)
         dalpha = _native.scatter_transpose(dalpha_gt, st.perm)
         return (dh_g, dalpha, None, *dmixes)
 

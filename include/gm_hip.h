@@ -456,7 +456,10 @@ int gm_factored_backward_seg_f64(const double* g, const int64_t* target, const d
  * may be NULL (the reference's separate trunk, nn/kernels.py:191-231,
  * 605-607, then never writes h).  Plans that take the generic grouped kernels
  * are rejected under it (gm_factored_lane_tables reports which).  dh_g is
- * still written by the backward. */
+ * still written by the backward. * accumulate != 0: dh_g and dweights_g are added to (the shares of one head's
+ * output copies, run one launch each, read the same trunk features and weights)
+ * instead of written.
+ */
 int gm_factored_forward_grouped_f32(const float* h_g, const float* const* z, const int64_t* node_stride,
                                     const int64_t* t_stride, const int64_t* width, int64_t n_runs,
                                     const float* phase_g, const float* rho_g, const float* zw_g,
@@ -474,8 +477,8 @@ int gm_factored_backward_grouped_f32(const float* g, const int64_t* target_g, co
                                      const int64_t* group_order, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
                                      int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
                                      int64_t d_out, const float* trunk_w, const float* trunk_b,
-                                     const float* trunk_centers, int64_t trunk_nb, double trunk_width, float* dh_g,
-                                     float* dweights_g, void* stream);
+                                     const float* trunk_centers, int64_t trunk_nb, double trunk_width,
+                                     int64_t accumulate, float* dh_g, float* dweights_g, void* stream);
 
 /* gm_factored_aggregate with edge e's row at rows[inv[e]] (rows kept in the
  * grouping's order; inv is the grouping's inverse permutation). */

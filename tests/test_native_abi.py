@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.library()
     missing = [n for n in sorted(declared()) if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.gm_abi_version() == 2
+    assert lib.gm_abi_version() == 3
     for stem in _native.SIGNATURES:
         assert stem + "_f32" in declared() and stem + "_f64" in declared()
     undeclared = sorted(set(_native.SIGNATURES_F32) - declared())
