@@ -489,20 +489,47 @@ __device__ __forceinline__ float4 load_v4(const uint16_t* src, int k, int w, int
 // fp32 accuracy: split.hpp).  A 16-deep contraction chunk kc gives lane
 // (c, q) the indices 16 kc + 4 q + s, s < 4, in both operands.
 
-// Forward: wave wv of workgroup x owns columns x * 128 + 32 wv + 16 j + c
-// (j < 2); the pieces of M at those columns are split once per wave and held
-// in registers; v's 64-row tiles come through LDS as in the fp32 kernel and
-// each wave splits its B operands from them.
+// The split kernels' tiling by vector width: columns a forward wave owns
+// (16 SplitCT), rows an input-gradient wave owns (16 SplitRT) and columns a
+// weight-gradient workgroup owns (16 SplitJT); the widest vectors take the
+// narrower tiles so the accumulators and held operands stay within a wave's
+// registers.
+template <int W>
+constexpr int SplitCT = W == 128 ? 1 : 2;
+template <int W>
+constexpr int SplitRT = W == 128 ? 1 : 2;
+template <int W>
+constexpr int SplitJT = W == 128 ? 2 : 4;
+
+// A SplitB operand from three bf16 planes (four contraction indices each).
+__device__ __forceinline__ SplitB split_b_planes(uint2 hi, uint2 mid, uint2 lo) {
+  return SplitB{u32x4{hi.x, hi.y, hi.x, hi.y}, u32x4{mid.x, mid.y, mid.x, mid.y}, u32x4{lo.x, lo.y, hi.x, hi.y}};
+}
+
+// Four values' three pieces into three bf16 planes at element `at`.
+__device__ __forceinline__ void store_planes(uint16_t* plane0, uint16_t* plane1, uint16_t* plane2, int at,
+                                             float4 x) {
+  const Split4 sp = split4(x.x, x.y, x.z, x.w);
+  *reinterpret_cast<uint2*>(plane0 + at) = make_uint2(sp.hi[0], sp.hi[1]);
+  *reinterpret_cast<uint2*>(plane1 + at) = make_uint2(sp.mid[0], sp.mid[1]);
+  *reinterpret_cast<uint2*>(plane2 + at) = make_uint2(sp.lo[0], sp.lo[1]);
+}
+
+// Forward: wave wv of workgroup x owns columns x * 64 CT + 16 CT wv + 16 j + c
+// (j < CT); the pieces of M at those columns are split once per wave and held
+// in registers; each 64-row tile of v is split once per workgroup into three
+// bf16 planes in LDS (row stride W + 4 halfwords: a 16-lane 8-byte read covers
+// 32 banks once), from which every wave assembles its B operands.
 template <int W, typename V = float>
 __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __restrict__ v, int64_t ldv,
                                                                    const float* __restrict__ M, int64_t N, int w,
                                                                    int64_t C, float* __restrict__ out, int vec_v,
                                                                    int vec_out) {
-  constexpr int KC = W / 16, CT = 2;
-  constexpr int LDT = W + 4;
+  constexpr int KC = W / 16, CT = SplitCT<W>;
+  constexpr int LDP = W + 4;
   constexpr int QUADS = 64 * W / 4;
   constexpr int PER = (QUADS + kThreads - 1) / kThreads;
-  __shared__ __align__(16) float vt[64 * LDT];
+  __shared__ __align__(16) uint16_t vp[3][64 * LDP];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
   const int64_t col0 = (int64_t)blockIdx.x * (64 * CT) + 16 * CT * wv;
   SplitA ma[KC][CT];
@@ -513,9 +540,9 @@ __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __re
       const int64_t col = col0 + 16 * j + c;
       float x[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int k = 16 * kc + 4 * q + s;
-        x[s] = (k < w && col < C) ? M[(int64_t)k * C + col] : 0.f;
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int k = 16 * kc + 4 * q + s4;
+        x[s4] = (k < w && col < C) ? M[(int64_t)k * C + col] : 0.f;
       }
       ma[kc][j] = split_a(x[0], x[1], x[2], x[3]);
     }
@@ -536,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __re
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
       const int idx = threadIdx.x + p * kThreads;
-      if (idx < QUADS) *reinterpret_cast<float4*>(&vt[(idx / (W / 4)) * LDT + 4 * (idx % (W / 4))]) = pre[p];
+      if (idx < QUADS) store_planes(vp[0], vp[1], vp[2], (idx / (W / 4)) * LDP + 4 * (idx % (W / 4)), pre[p]);
     }
     __syncthreads();
     if (tile + gridDim.y < n_tiles) fetch(tile + gridDim.y);
@@ -548,8 +575,10 @@ __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __re
       for (int j = 0; j < CT; ++j) acc[j] = kZero4;
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        const float4 x = *reinterpret_cast<const float4*>(&vt[(16 * rt + c) * LDT + 16 * kc + 4 * q]);
-        const SplitB b = split_b(x.x, x.y, x.z, x.w);
+        const int at = (16 * rt + c) * LDP + 16 * kc + 4 * q;
+        const SplitB b = split_b_planes(*reinterpret_cast<const uint2*>(&vp[0][at]),
+                                        *reinterpret_cast<const uint2*>(&vp[1][at]),
+                                        *reinterpret_cast<const uint2*>(&vp[2][at]));
 #pragma unroll
         for (int j = 0; j < CT; ++j) acc[j] = mfma_split(ma[kc][j], b, acc[j]);
       }
@@ -572,43 +601,48 @@ __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __re
   }
 }
 
-// Input gradient: 128-row tiles as in the fp32 kernel, each wave 32 rows over
-// the whole contraction; a 64-column chunk of dmix is staged as fp32 (each
-// wave splits its own rows' A operands), the chunk of M as three bf16 planes
-// split once per workgroup; running totals every four chunks.
+// Input gradient: tiles of 64 RT rows, each wave 16 RT rows over the whole
+// contraction; a 64-column chunk of dmix is staged as fp32 (each wave splits
+// its own rows' A operands), the chunk of M as three bf16 planes split once
+// per workgroup; running totals every four chunks.
 template <int W>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void node_mix_dinput_split(const float* __restrict__ dmix,
                                                                   const float* __restrict__ M, int64_t N, int w,
                                                                   int64_t C, float* __restrict__ dv, int64_t lddv) {
-  constexpr int KC = 64, LDD = KC + 4, LDM = KC + 4, JW = W / 16;  // LDM: a 16-lane 8-byte read covers 32 banks once
-  constexpr int DQ = 128 * KC / 4 / kThreads;
+  constexpr int RT = SplitRT<W>, ROWS = 64 * RT;
+  // chunks of KC columns (32 for the widest vectors: fewer staged registers); LDM: a 16-lane 8-byte read
+  // covers 32 banks once
+  constexpr int KC = W == 128 ? 32 : 64, LDD = KC + 4, LDM = KC + 4, JW = W / 16, KS = KC / 16;
+  constexpr int TOTAL_EVERY = 256 / KC;  // chunks a running sum spans before it joins the total
+  constexpr int DQ = ROWS * KC / 4 / kThreads;
   constexpr int MQ = W * KC / 4 / kThreads;
-  __shared__ __align__(16) float dt[128 * LDD];
+  __shared__ __align__(16) float dt[ROWS * LDD];
   __shared__ __align__(16) uint16_t mp[3][W * LDM];  // M's hi, mid and lo pieces, row k of M at k * LDM
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
-  const int64_t row0 = (int64_t)blockIdx.x * 128;
+  const int64_t row0 = (int64_t)blockIdx.x * ROWS;
   const int64_t n_chunks = (C + KC - 1) / KC;
+  constexpr int CQ = KC / 4;  // 16-byte pieces of a chunk row
   float4 pd[DQ], pm[MQ];
   auto fetch = [&](int64_t ch) {
     const int64_t c0 = ch * KC;
 #pragma unroll
     for (int p = 0; p < DQ; ++p) {
-      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int idx = threadIdx.x + p * kThreads, row = idx / CQ, cq = idx % CQ;
       const int64_t r = row0 + row, col = c0 + 4 * cq;
       pd[p] = (r < N && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
                                  : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (int p = 0; p < MQ; ++p) {
-      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int idx = threadIdx.x + p * kThreads, row = idx / CQ, cq = idx % CQ;
       const int64_t col = c0 + 4 * cq;
       pm[p] = (row < w && col < C) ? *reinterpret_cast<const float4*>(M + (int64_t)row * C + col)
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  floatx4 acc[2][JW], tot[2][JW];
+  floatx4 acc[RT][JW], tot[RT][JW];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int j = 0; j < JW; ++j) acc[rt][j] = tot[rt][j] = kZero4;
   fetch(0);
@@ -617,40 +651,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int p = 0; p < DQ; ++p) {
       const int idx = threadIdx.x + p * kThreads;
-      *reinterpret_cast<float4*>(&dt[(idx >> 4) * LDD + 4 * (idx & 15)]) = pd[p];
+      *reinterpret_cast<float4*>(&dt[(idx / CQ) * LDD + 4 * (idx % CQ)]) = pd[p];
     }
 #pragma unroll
     for (int p = 0; p < MQ; ++p) {
-      const int idx = threadIdx.x + p * kThreads, at = (idx >> 4) * LDM + 4 * (idx & 15);
-      const Split4 sp = split4(pm[p].x, pm[p].y, pm[p].z, pm[p].w);
-      *reinterpret_cast<uint2*>(&mp[0][at]) = make_uint2(sp.hi[0], sp.hi[1]);
-      *reinterpret_cast<uint2*>(&mp[1][at]) = make_uint2(sp.mid[0], sp.mid[1]);
-      *reinterpret_cast<uint2*>(&mp[2][at]) = make_uint2(sp.lo[0], sp.lo[1]);
+      const int idx = threadIdx.x + p * kThreads;
+      store_planes(mp[0], mp[1], mp[2], (idx / CQ) * LDM + 4 * (idx % CQ), pm[p]);
     }
     __syncthreads();
     if (ch + 1 < n_chunks) fetch(ch + 1);
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      SplitA a[2];
+    for (int kc = 0; kc < KS; ++kc) {
+      SplitA a[RT];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const float4 x = *reinterpret_cast<const float4*>(&dt[(32 * wv + 16 * rt + c) * LDD + 16 * kc + 4 * q]);
+      for (int rt = 0; rt < RT; ++rt) {
+        const float4 x = *reinterpret_cast<const float4*>(&dt[(16 * RT * wv + 16 * rt + c) * LDD + 16 * kc + 4 * q]);
         a[rt] = split_a(x.x, x.y, x.z, x.w);
       }
 #pragma unroll
       for (int j = 0; j < JW; ++j) {
         const int at = (16 * j + c) * LDM + 16 * kc + 4 * q;
-        const uint2 hi = *reinterpret_cast<const uint2*>(&mp[0][at]);
-        const uint2 mid = *reinterpret_cast<const uint2*>(&mp[1][at]);
-        const uint2 lo = *reinterpret_cast<const uint2*>(&mp[2][at]);
-        const SplitB b{u32x4{hi.x, hi.y, hi.x, hi.y}, u32x4{mid.x, mid.y, mid.x, mid.y}, u32x4{lo.x, lo.y, hi.x, hi.y}};
+        const SplitB b = split_b_planes(*reinterpret_cast<const uint2*>(&mp[0][at]),
+                                        *reinterpret_cast<const uint2*>(&mp[1][at]),
+                                        *reinterpret_cast<const uint2*>(&mp[2][at]));
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) acc[rt][j] = mfma_split(a[rt], b, acc[rt][j]);
+        for (int rt = 0; rt < RT; ++rt) acc[rt][j] = mfma_split(a[rt], b, acc[rt][j]);
       }
     }
-    if ((ch & 3) == 3 || ch + 1 == n_chunks) {
+    if (ch % TOTAL_EVERY == TOTAL_EVERY - 1 || ch + 1 == n_chunks) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int j = 0; j < JW; ++j) {
           tot[rt][j] += acc[rt][j];
@@ -659,37 +689,40 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   }
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int j = 0; j < JW; ++j) {
       const int col = 16 * j + c;
       if (col >= w) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t r = row0 + 32 * wv + 16 * rt + 4 * q + i;
+        const int64_t r = row0 + 16 * RT * wv + 16 * rt + 4 * q + i;
         if (r < N) dv[r * lddv + col] = tot[rt][j][i];
       }
     }
 }
 
-// Weight gradient for vectors up to 64 reals: the fp32 four-partials kernel's
-// tiling (each wave 16 rows of every 64-row chunk over the workgroup's whole
-// w x 64 tile, one partial per wave), a wave's 16 rows forming one contraction
-// chunk of split products.
+// Weight gradient: workgroup (x, y) owns the whole (w x 16 JT)-column tile
+// [16 JT x, 16 JT (x + 1)) over rows [y rps, min(N, (y + 1) rps)); its four
+// waves take rows 16 wv .. 16 wv + 15 of each 64-row chunk, a wave's 16 rows
+// forming one contraction chunk of split products, each wave accumulating the
+// whole tile and writing one partial: 4 S partial matrices.
 template <int W, typename V = float>
 __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __restrict__ v, int64_t ldv,
                                                                    const float* __restrict__ dmix, int64_t N, int w,
                                                                    int64_t C, int64_t rps, float* __restrict__ partial,
                                                                    int vec_v) {
+  constexpr int JT = SplitJT<W>, COLS = 16 * JT;
   // lanes (c, q) read rows 16 wv + 4 q + s: strides with 4 LD = 16 (mod 64) words put a quarter-wave's
   // rows in distinct banks
-  constexpr int RC = 64, LDV = W + 4, LDM = 64 + 4, IW = W / 16;
+  constexpr int RC = 64, LDV = W + 4, LDM = COLS + 4, IW = W / 16;
   constexpr int VQ = (RC * W / 4 + kThreads - 1) / kThreads;
-  constexpr int DQ = RC * 64 / 4 / kThreads;
+  constexpr int CQ = COLS / 4;  // 16-byte pieces of a dmix row
+  constexpr int DQ = (RC * CQ + kThreads - 1) / kThreads;
   __shared__ __align__(16) float vt[RC * LDV];
   __shared__ __align__(16) float dt[RC * LDM];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
-  const int64_t c0 = (int64_t)blockIdx.x * 64;
+  const int64_t c0 = (int64_t)blockIdx.x * COLS;
   const int64_t first = (int64_t)blockIdx.y * rps, last = first + rps < N ? first + rps : N;
   float4 pv[VQ], pd[DQ];
   auto fetch = [&](int64_t r0) {
@@ -701,17 +734,17 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __re
     }
 #pragma unroll
     for (int p = 0; p < DQ; ++p) {
-      const int idx = threadIdx.x + p * kThreads, row = idx >> 4, cq = idx & 15;
+      const int idx = threadIdx.x + p * kThreads, row = idx / CQ, cq = idx % CQ;
       const int64_t r = r0 + row, col = c0 + 4 * cq;
-      pd[p] = (r < last && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      pd[p] = (idx < RC * CQ && r < last && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
+                                                     : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  floatx4 acc[IW][4];
+  floatx4 acc[IW][JT];
 #pragma unroll
   for (int i = 0; i < IW; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = kZero4;
+    for (int j = 0; j < JT; ++j) acc[i][j] = kZero4;
   if (first < last) fetch(first);
   for (int64_t r0 = first; r0 < last; r0 += RC) {
     __syncthreads();
@@ -723,7 +756,7 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __re
 #pragma unroll
     for (int p = 0; p < DQ; ++p) {
       const int idx = threadIdx.x + p * kThreads;
-      *reinterpret_cast<float4*>(&dt[(idx >> 4) * LDM + 4 * (idx & 15)]) = pd[p];
+      if (idx < RC * CQ) *reinterpret_cast<float4*>(&dt[(idx / CQ) * LDM + 4 * (idx % CQ)]) = pd[p];
     }
     __syncthreads();
     if (r0 + RC < last) fetch(r0 + RC);
@@ -735,7 +768,7 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __re
       a[i] = split_a(vt[rb * LDV + 16 * i + c], vt[(rb + 1) * LDV + 16 * i + c], vt[(rb + 2) * LDV + 16 * i + c],
                      vt[(rb + 3) * LDV + 16 * i + c]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < JT; ++j) {
       const SplitB b = split_b(dt[rb * LDM + 16 * j + c], dt[(rb + 1) * LDM + 16 * j + c],
                                dt[(rb + 2) * LDM + 16 * j + c], dt[(rb + 3) * LDM + 16 * j + c]);
 #pragma unroll
@@ -746,7 +779,7 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __re
 #pragma unroll
   for (int i = 0; i < IW; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < JT; ++j) {
       const int64_t col = c0 + 16 * j + c;
       if (col >= C) continue;
 #pragma unroll
@@ -776,11 +809,12 @@ int check_shapes(int64_t N, int64_t w, int64_t C) {
 int width_class(int64_t w) { return w <= 16 ? 16 : (w <= 32 ? 32 : (w <= 64 ? 64 : 128)); }
 
 // Column tile of the weight gradient's workgroups: 64 columns for vectors up to
-// 64 reals (the four-partials kernel), 128 above.
-int64_t weight_tile(int64_t w) { return w <= 64 ? 64 : 128; }
+// 64 reals; above, 32 for the split kernel and 128 for the fp32 one.
+int64_t weight_tile(int64_t w) { return w <= 64 ? 64 : (split_products() ? 32 : 128); }
 
-// Partial matrices a workgroup row writes: four for the four-partials kernel.
-int64_t weight_partials_per_split(int64_t w) { return w <= 64 ? 4 : 1; }
+// Partial matrices a workgroup row writes: four (one a wave) but for the fp32
+// kernel of vectors above 64 reals (one).
+int64_t weight_partials_per_split(int64_t w) { return (w <= 64 || split_products()) ? 4 : 1; }
 
 // The weight gradient's row splits: about 1024 workgroups, whole 64-row chunks per split.
 void weight_splits(int64_t N, int64_t w, int64_t C, int64_t max_splits, int64_t& splits, int64_t& rps) {
@@ -816,7 +850,10 @@ int launch_dweight(const float* v, int64_t ldv, const float* dmix, int64_t N, in
         if (sp) hipLaunchKernelGGL(node_mix_dweight_split<64>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
         else hipLaunchKernelGGL(node_mix_dweight_k_kernel<64>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
         break;
-      default: hipLaunchKernelGGL(node_mix_dweight_kernel<128>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      default:
+        if (sp) hipLaunchKernelGGL(node_mix_dweight_split<128>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        else hipLaunchKernelGGL(node_mix_dweight_kernel<128>, grid, block, 0, stream, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        break;
     }
     const int rc = check_launch("node_mix_backward_weight");
     if (rc != GM_OK) return rc;
@@ -869,8 +906,8 @@ extern "C" int gm_node_mix_forward_f32(const float* v, int64_t ldv, const float*
   const int vec_v = gm::aligned(v, 16) && ldv % 4 == 0;
   const int vec_out = gm::aligned(out, 16) && C % 4 == 0;
   const int W = gm::width_class(w);
-  const bool sp = W <= 64 && gm::split_products();
-  const int CT = (W == 128 || sp) ? 2 : 4;
+  const bool sp = gm::split_products();
+  const int CT = sp ? (W == 128 ? gm::SplitCT<128> : gm::SplitCT<64>) : (W == 128 ? 2 : 4);
   const int64_t nx = (C + 64 * CT - 1) / (64 * CT), n_tiles = (N + 63) / 64;
   int64_t ny = (2048 + nx - 1) / nx;
   if (ny > n_tiles) ny = n_tiles;
@@ -880,7 +917,8 @@ extern "C" int gm_node_mix_forward_f32(const float* v, int64_t ldv, const float*
     switch (W) {
       case 16: hipLaunchKernelGGL((gm::node_mix_forward_split<16>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
       case 32: hipLaunchKernelGGL((gm::node_mix_forward_split<32>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
-      default: hipLaunchKernelGGL((gm::node_mix_forward_split<64>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+      case 64: hipLaunchKernelGGL((gm::node_mix_forward_split<64>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
+      default: hipLaunchKernelGGL((gm::node_mix_forward_split<128>), grid, block, 0, s, v, ldv, M, N, (int)w, C, out, vec_v, vec_out); break;
     }
     return gm::check_launch("node_mix_forward");
   }
@@ -904,11 +942,13 @@ extern "C" int gm_node_mix_backward_input_f32(const float* dmix, const float* M,
              "dmix and M must be 16-byte aligned with C a multiple of 4");
   const hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)((N + 127) / 128)), block(gm::kThreads);
-  if (gm::width_class(w) <= 64 && gm::split_products()) {
+  if (gm::split_products()) {
+    const dim3 grid128((unsigned)((N + 64 * gm::SplitRT<128> - 1) / (64 * gm::SplitRT<128>)));
     switch (gm::width_class(w)) {
       case 16: hipLaunchKernelGGL(gm::node_mix_dinput_split<16>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
       case 32: hipLaunchKernelGGL(gm::node_mix_dinput_split<32>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
-      default: hipLaunchKernelGGL(gm::node_mix_dinput_split<64>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+      case 64: hipLaunchKernelGGL(gm::node_mix_dinput_split<64>, grid, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
+      default: hipLaunchKernelGGL(gm::node_mix_dinput_split<128>, grid128, block, 0, s, dmix, M, N, (int)w, C, dv, lddv); break;
     }
     return gm::check_launch("node_mix_backward_input");
   }

@@ -554,7 +554,8 @@ int gm_node_mix_backward_weight_bf16(const uint16_t* v, int64_t ldv, const float
  * (2^23-float) device array of the library, one per GPU, held until the
  * process ends; every call on a GPU uses that GPU's array, so calls that
  * overlap on one GPU (different streams, or other host threads) race.  Fails
- * with GM_ERR_ARGUMENT when w * C * (w <= 64 ? 4 : 1) exceeds 2^23.  Sums in
+ * with GM_ERR_ARGUMENT when 4 w C (the fp32 kernel of w > 64 under
+ * GM_SPLIT_PRODUCTS=0: w C) exceeds 2^23.  Sums in
  * a different split order than the workspace form (same bar, not bitwise). */
 int gm_node_mix_backward_weight_noalloc_f32(const float* v, int64_t ldv, const float* dmix, int64_t N, int64_t w,
                                             int64_t C, float* dM, void* stream);
