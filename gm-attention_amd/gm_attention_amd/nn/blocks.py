@@ -36,7 +36,7 @@ from typing import Literal
 import torch
 from torch import Tensor, nn
 
-from gm_attention_amd.nn import fused_factored, kernels, radial
+from gm_attention_amd.nn import fused_factored, kernels
 from gm_attention_amd.nn.attention import SO2MHSA, batched_flat_serves, gather_to_edges, weighted_segment_sum
 from gm_attention_amd.nn.convolution import SO2Convolution
 from gm_attention_amd.nn.fused_attention import evaluate_aggregation_window
@@ -186,16 +186,10 @@ class IcoEncode(nn.Module):
                                                    fused_factored.group_key(edges, 0, int(edges.n_edges)),
                                                    owner=edges.edge_index)
                       if enabled else None)
-            K = self.kernel.complex_head.in_features + 1
-            if enabled and x.dtype == torch.float32 and fused_factored.head_split(self.kernel, K) > 0:
-                # the grouped kernels over shares of the output copies (one "head"), the weights as its alpha
-                values = [self.kernel]
-                if radial.eligible(values, x.dtype, x.device):
-                    h, trunk = None, partial(radial.trunk_hidden_heads, values)
-                else:
-                    h, trunk = self.kernel._trunk_hidden(edges.distances).unsqueeze(0), None
-                out = fused_factored.forward_aggregated_heads(values, x, edges, weight.unsqueeze(1), h, groups, trunk)
-                return SO2FeatureField.from_flat(self.field_type_out, out.reshape(out.shape[0], -1))
+            if enabled:  # float32 rows: the grouped kernels over shares of the output copies
+                shares = fused_factored.forward_aggregated_shares(self.kernel, x, edges, weight, groups)
+                if shares is not None:
+                    return shares
             products = self.kernel.node_products(x)
             return self.kernel.forward_factored_aggregated(x, edges, weight, products, groups)
         messages = self.kernel(gather_to_edges(x, edges.source_index), edges)

@@ -1107,6 +1107,30 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
     return _forward_aggregated_heads_seg(kernels, x, edges, alpha, h, groups)
 
 
+def forward_aggregated_shares(kernel: Any, x: SO2FeatureField, edges: Any, weights: Tensor,
+                              groups: tuple[Tensor, Tensor, Tensor] | None = None) -> SO2FeatureField | None:
+    """One kernel's weighted aggregate on the grouped kernels, as a single head
+    cut into shares of its output copies (:func:`head_split`) with the edge
+    weights as the head's ``alpha``; ``None`` where they do not serve it (rows
+    other than float32, or no share fits).  A kernel wider than the MFMA
+    kernels' 128 packed columns -- a readout onto 32 scalars from 64 or 128
+    copies of frequencies 0..2 has 160 -- then still runs on matrix cores."""
+    from gm_attention_amd.nn import radial
+
+    head = kernel.complex_head if kernel.complex_head is not None else kernel.real_head
+    if x.dtype != torch.float32 or head_split(kernel, head.in_features + 1) == 0:
+        return None
+    if groups is None:
+        groups = groups_for(edges, edges.source_index)
+    values = [kernel]
+    if radial.eligible(values, x.dtype, x.device):
+        h, trunk = None, lambda rho: radial.trunk_hidden_heads(values, rho)
+    else:
+        h, trunk = kernel._trunk_hidden(edges.distances).unsqueeze(0), None
+    out = forward_aggregated_heads(values, x, edges, weights.unsqueeze(1), h, groups, trunk)
+    return SO2FeatureField.from_flat(kernel.field_type_out, out.reshape(out.shape[0], -1))
+
+
 def _heads_desc(kernel: Any, hp: HeadsPlan, device: torch.device) -> Tensor:
     key = ("_fused_heads_desc", str(device))
     desc = kernel.__dict__.get(key)

@@ -221,6 +221,10 @@ class SO2SteerableKernel(nn.Module):
         from gm_attention_amd.nn import eager_ops, fused_factored
 
         if fused_factored.enabled(self, x, edges):
+            if products is None:  # float32 rows on the grouped kernels where a share of the output copies fits
+                shares = fused_factored.forward_aggregated_shares(self, x, edges, weights, groups)
+                if shares is not None:
+                    return shares
             return fused_factored.forward_aggregated(self, x, edges, weights, products, groups)
         rows = eager_ops.factored_rows(self, x, edges, products)
         return SO2FeatureField.from_flat(self.field_type_out,

@@ -21,12 +21,13 @@ from test_attention_gpu import close
 pytestmark = pytest.mark.gpu
 
 
-def build(field, depthwise, window, normalize, self_interaction, batch, n_basis=4, seed=0, nlat=10, nlon=20):
+def build(field, depthwise, window, normalize, self_interaction, batch, n_basis=4, seed=0, nlat=10, nlon=20,
+          field_out=None):
     disc = problems.discretization(nlat, nlon)
     edges = disc.edge_geometry.tile(batch, n_sources=disc.n_nodes) if batch > 1 else disc.edge_geometry
     torch.manual_seed(seed)
     ft = SO2FieldType(field)
-    conv = SO2Convolution(ft, ft, cutoff=disc.coverage_radius, window=window, depthwise=depthwise,
+    conv = SO2Convolution(ft, SO2FieldType(field_out or field), cutoff=disc.coverage_radius, window=window, depthwise=depthwise,
                           normalize=normalize, self_interaction=self_interaction, n_radial_basis=n_basis,
                           dtype=torch.float64)
     with torch.no_grad():  # nonzero biases everywhere
@@ -84,6 +85,39 @@ def test_convolution_matches_the_oracle(case, dtype, cuda):
     assert set(got[2]) == set(want[2])
     for n in want[2]:
         close(got[2][n], want[2][n], dtype, f"d{n}", reduction=True)
+
+
+READOUTS = [({0: 64, 1: 64, 2: 64}, {0: 32}, 2), ({0: 16, 1: 16, 2: 16}, {0: 24}, 1), ({0: 4}, {0: 8, 1: 8, 2: 8}, 1)]
+
+
+@pytest.mark.parametrize("readout", READOUTS)
+def test_general_convolution_on_output_shares_matches_the_oracle(readout, cuda):
+    """General kernels between different field types in float32 -- the segformer's
+    readouts onto scalars (160 packed mix columns: two shares of 16 copies on
+    the grouped kernels), a narrower one taken whole, and a lift from scalars
+    -- against the float64 oracle, every gradient."""
+    from gm_attention_amd.nn import eager_ops, fused_factored
+
+    field_in, field_out, split = readout
+    print(f"conv readout {field_in} -> {field_out}", flush=True)
+    conv, x, edges = build(field_in, False, "hard", False, "linear", 2, field_out=field_out)
+    conv.load_state_dict({k: v.float().double() for k, v in conv.state_dict().items()})
+    x = x.float().double()
+    probe = problems.normal((x.shape[0], conv.field_type_out.dimension), 7)
+    want = run(conv, x, edges.to(None, torch.float32).to(None, torch.float64), probe, oracle=True, tolerance=1e-5)
+    gpu = SO2Convolution(conv.field_type_in, conv.field_type_out, cutoff=conv.cutoff, window="hard",
+                         self_interaction="linear", n_radial_basis=conv.kernel.radial_basis.n_basis,
+                         dtype=torch.float32, device=cuda)
+    gpu.load_state_dict({k: v.float() for k, v in conv.state_dict().items()})
+    assert fused_factored.head_split(gpu.kernel, gpu.kernel.complex_head.in_features + 1) == split
+    before = dict(eager_ops.calls)
+    got = run(gpu, x.to(cuda, torch.float32), edges.to(cuda, torch.float32), probe)
+    assert eager_ops.calls == before, "part of the layer fell back to the eager path"
+    close(got[0], want[0], torch.float32, "out")
+    close(got[1], want[1], torch.float32, "dx")
+    assert set(got[2]) == set(want[2])
+    for n in want[2]:
+        close(got[2][n], want[2][n], torch.float32, f"d{n}", reduction=True)
 
 
 @pytest.mark.parametrize("depthwise", [True, False])
