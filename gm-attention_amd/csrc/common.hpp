@@ -18,6 +18,21 @@ void set_error(const std::string& message);
 int fail(int code, const std::string& message);  // set_error + return code
 int check_launch(const char* what);               // hipGetLastError after a launch
 
+// ---- launch geometry (runtime.hip) ----
+// Workgroups of `kernel` (`threads` threads, `lds` bytes of dynamic LDS)
+// resident on the current device at once, CUs x workgroups per CU; 0 when the
+// runtime cannot say (no device).  Cached per device and kernel.
+int64_t resident_blocks(const void* kernel, int threads, size_t lds = 0);
+// The workgroups of a grid whose workgroups share the work evenly: about
+// `want`, in whole rounds of `slots` resident ones (r slots, r = want / slots
+// rounded, at least one), so that no last round runs on a fraction of the
+// chip; `want` itself when the occupancy is unknown.
+inline int64_t whole_rounds(int64_t want, int64_t slots) {
+  if (slots <= 0) return want;
+  int64_t r = (want + slots / 2) / slots;
+  return (r < 1 ? 1 : r) * slots;
+}
+
 #define GM_REQUIRE(cond, message)                                   \
   do {                                                              \
     if (!(cond)) return ::gm::fail(GM_ERR_ARGUMENT, (message));     \

@@ -816,12 +816,38 @@ int64_t weight_tile(int64_t w) { return w <= 64 ? 64 : (split_products() ? 32 : 
 // kernel of vectors above 64 reals (one).
 int64_t weight_partials_per_split(int64_t w) { return (w <= 64 || split_products()) ? 4 : 1; }
 
-// The weight gradient's row splits: about 1024 workgroups, whole 64-row chunks per split.
+// Row groups g of a grid of nx x g workgroups whose rows each workgroup loops
+// over in equal shares: about `want` workgroups in whole rounds of the
+// `slots` resident ones (g = floor(r slots / nx), r = want / slots rounded,
+// at least one), so that no last round runs on a fraction of the chip;
+// ceil(want / nx) when the occupancy is unknown or a round holds fewer
+// workgroups than there are column tiles.
+int64_t round_groups(int64_t nx, int64_t want, int64_t slots) {
+  if (nx < 1) nx = 1;
+  if (slots < nx) return (want + nx - 1) / nx;
+  int64_t r = (want + slots / 2) / slots;
+  if (r < 1) r = 1;
+  return (r * slots) / nx;
+}
+
+// The weight gradient's kernel for vectors of w reals (float vectors; the
+// bfloat16 form shares its workspace, so its grid follows this one).
+const void* dweight_kernel(int64_t w) {
+  const bool sp = split_products();
+  switch (width_class(w)) {
+    case 16: return sp ? (const void*)node_mix_dweight_split<16> : (const void*)node_mix_dweight_k_kernel<16>;
+    case 32: return sp ? (const void*)node_mix_dweight_split<32> : (const void*)node_mix_dweight_k_kernel<32>;
+    case 64: return sp ? (const void*)node_mix_dweight_split<64> : (const void*)node_mix_dweight_k_kernel<64>;
+    default: return sp ? (const void*)node_mix_dweight_split<128> : (const void*)node_mix_dweight_kernel<128>;
+  }
+}
+
+// The weight gradient's row splits: about 1024 workgroups in whole rounds, whole 64-row chunks per split.
 void weight_splits(int64_t N, int64_t w, int64_t C, int64_t max_splits, int64_t& splits, int64_t& rps) {
   const int64_t tile = weight_tile(w);
   const int64_t nx = (C + tile - 1) / tile > 0 ? (C + tile - 1) / tile : 1;
   const int64_t chunks = (N + 63) / 64;
-  int64_t s = (1024 + nx - 1) / nx;
+  int64_t s = round_groups(nx, 1024, resident_blocks(dweight_kernel(w), kThreads));
   if (s > chunks) s = chunks;
   if (s > max_splits) s = max_splits;
   if (s < 1) s = 1;
@@ -909,7 +935,14 @@ extern "C" int gm_node_mix_forward_f32(const float* v, int64_t ldv, const float*
   const bool sp = gm::split_products();
   const int CT = sp ? (W == 128 ? gm::SplitCT<128> : gm::SplitCT<64>) : (W == 128 ? 2 : 4);
   const int64_t nx = (C + 64 * CT - 1) / (64 * CT), n_tiles = (N + 63) / 64;
-  int64_t ny = (2048 + nx - 1) / nx;
+  const void* kernel = nullptr;
+  switch (W) {
+    case 16: kernel = sp ? (const void*)gm::node_mix_forward_split<16> : (const void*)gm::node_mix_forward_kernel<16, 4>; break;
+    case 32: kernel = sp ? (const void*)gm::node_mix_forward_split<32> : (const void*)gm::node_mix_forward_kernel<32, 4>; break;
+    case 64: kernel = sp ? (const void*)gm::node_mix_forward_split<64> : (const void*)gm::node_mix_forward_kernel<64, 4>; break;
+    default: kernel = sp ? (const void*)gm::node_mix_forward_split<128> : (const void*)gm::node_mix_forward_kernel<128, 2>; break;
+  }
+  int64_t ny = gm::round_groups(nx, 2048, gm::resident_blocks(kernel, gm::kThreads));
   if (ny > n_tiles) ny = n_tiles;
   if (ny > 65535) ny = 65535;
   const dim3 grid((unsigned)nx, (unsigned)ny), block(gm::kThreads);
@@ -1018,7 +1051,10 @@ extern "C" int gm_node_mix_forward_bf16(const uint16_t* v, int64_t ldv, const fl
   const int vec_out = gm::aligned(out, 16) && C % 4 == 0;
   const int W = gm::width_class(w);
   const int64_t nx = (C + 127) / 128, n_tiles = (N + 63) / 64;
-  int64_t ny = (2048 + nx - 1) / nx;
+  const void* kernel = W == 16 ? (const void*)gm::node_mix_forward_split<16, uint16_t>
+                       : W == 32 ? (const void*)gm::node_mix_forward_split<32, uint16_t>
+                                 : (const void*)gm::node_mix_forward_split<64, uint16_t>;
+  int64_t ny = gm::round_groups(nx, 2048, gm::resident_blocks(kernel, gm::kThreads));
   if (ny > n_tiles) ny = n_tiles;
   if (ny > 65535) ny = 65535;
   const dim3 grid((unsigned)nx, (unsigned)ny), block(gm::kThreads);

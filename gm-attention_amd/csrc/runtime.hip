@@ -1,7 +1,10 @@
 // Error state and version of libgmhip.so.
 #include <hip/hip_runtime.h>
 
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "common.hpp"
 #include "layout.hpp"
@@ -23,6 +26,29 @@ int check_launch(const char* what) {
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(GM_ERR_LAUNCH, std::string(what) + ": " + hipGetErrorString(err));
   return GM_OK;
+}
+
+int64_t resident_blocks(const void* kernel, int threads, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int64_t> cache;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();  // not left for the next launch check
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, kernel);
+  const auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int cus = 0, per = 0;
+  int64_t slots = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) == hipSuccess)
+    slots = (int64_t)cus * per;
+  else
+    (void)hipGetLastError();
+  cache[key] = slots;
+  return slots;
 }
 
 int parse_attention_layout(const int64_t* desc, int64_t F, int64_t H, int64_t D, int64_t orders, AttnLayout& L) {

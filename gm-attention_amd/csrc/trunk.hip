@@ -289,16 +289,25 @@ int prepare(TrunkArgs& a, const float* rho, const float* weight, const float* bi
   return GM_OK;
 }
 
-constexpr int64_t kTrunkBackwardBlocks = 2048;  // the backward's fixed grid (waves stride over 16-edge tiles)
+constexpr int64_t kTrunkBlocks = 2048;  // about this many workgroups (waves stride over 16-edge tiles)
 
-int64_t backward_blocks(int64_t n_edges) {
+// The grid of a pass over n_edges: one tile per wave up to about kTrunkBlocks
+// workgroups, in whole rounds of the kernel's resident workgroups (the waves'
+// shares differ by at most a tile, so a partial last round would run on a
+// fraction of the chip).  The backward's grid (and so its partial rows)
+// follows the B = 8 instance's occupancy for every basis size.
+int64_t trunk_blocks(int64_t n_edges, bool forward) {
   const int64_t need = (n_edges + 16 * kTrunkWaves - 1) / (16 * kTrunkWaves);  // one tile per wave
-  return need < kTrunkBackwardBlocks ? (need > 0 ? need : 1) : kTrunkBackwardBlocks;
+  const void* kernel = forward ? (const void*)trunk_forward_mfma<8> : (const void*)trunk_backward_mfma<8>;
+  const int64_t full = whole_rounds(kTrunkBlocks, resident_blocks(kernel, kTrunkThreads));
+  return need < full ? (need > 0 ? need : 1) : full;
 }
+
+int64_t backward_blocks(int64_t n_edges) { return trunk_blocks(n_edges, false); }
 
 template <int B>
 void launch(bool forward, const TrunkArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)backward_blocks(a.n_edges)), block(kTrunkThreads);
+  const dim3 grid((unsigned)trunk_blocks(a.n_edges, forward)), block(kTrunkThreads);
   if (forward)
     hipLaunchKernelGGL((trunk_forward_mfma<B>), grid, block, 0, stream, a);
   else
