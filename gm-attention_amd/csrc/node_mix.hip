@@ -483,6 +483,14 @@ __device__ __forceinline__ float4 load_v4(const uint16_t* src, int k, int w, int
   return make_float4(k < w ? bf16_at(src) : 0.f, k + 1 < w ? bf16_at(src + 1) : 0.f,
                      k + 2 < w ? bf16_at(src + 2) : 0.f, k + 3 < w ? bf16_at(src + 3) : 0.f);
 }
+// Four consecutive entries of a mix-gradient row, float32 or bfloat16 (widened
+// exactly; 8-byte aligned quads).
+__device__ __forceinline__ float4 load_dm4(const float* src) { return *reinterpret_cast<const float4*>(src); }
+__device__ __forceinline__ float4 load_dm4(const uint16_t* src) {
+  const uint2 u = *reinterpret_cast<const uint2*>(src);
+  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u), __uint_as_float(u.y << 16),
+                     __uint_as_float(u.y & 0xFFFF0000u));
+}
 //
 // The same three products for vectors up to 64 reals, with every fp32 product
 // formed as six bf16 products on v_mfma_f32_16x16x32_bf16 (three-piece splits,
@@ -707,9 +715,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 // waves take rows 16 wv .. 16 wv + 15 of each 64-row chunk, a wave's 16 rows
 // forming one contraction chunk of split products, each wave accumulating the
 // whole tile and writing one partial: 4 S partial matrices.
-template <int W, typename V = float>
+template <int W, typename V = float, typename DM = float>
 __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __restrict__ v, int64_t ldv,
-                                                                   const float* __restrict__ dmix, int64_t N, int w,
+                                                                   const DM* __restrict__ dmix, int64_t N, int w,
                                                                    int64_t C, int64_t rps, float* __restrict__ partial,
                                                                    int vec_v) {
   constexpr int JT = SplitJT<W>, COLS = 16 * JT;
@@ -736,8 +744,7 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __re
     for (int p = 0; p < DQ; ++p) {
       const int idx = threadIdx.x + p * kThreads, row = idx / CQ, cq = idx % CQ;
       const int64_t r = r0 + row, col = c0 + 4 * cq;
-      pd[p] = (idx < RC * CQ && r < last && col < C) ? *reinterpret_cast<const float4*>(dmix + r * C + col)
-                                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      pd[p] = (idx < RC * CQ && r < last && col < C) ? load_dm4(dmix + r * C + col) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
   floatx4 acc[IW][JT];
@@ -790,14 +797,50 @@ __global__ __launch_bounds__(kThreads) void node_mix_dweight_split(const V* __re
     }
 }
 
-// dM[e] = sum over the splits y = 0, 1, ... of partial[y][e], in that order.
+// dM[e] = sum over y = 0, 1, ..., count - 1 of partial[y stride][e], in that order.
 __global__ __launch_bounds__(kThreads) void node_mix_reduce_kernel(const float* __restrict__ partial, int64_t n,
-                                                                   int64_t splits, float* __restrict__ dM) {
+                                                                   int64_t count, int64_t stride,
+                                                                   float* __restrict__ dM) {
   const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (e >= n) return;
   float s = 0.f;
-  for (int64_t y = 0; y < splits; ++y) s += partial[y * n + e];
+  for (int64_t y = 0; y < count; ++y) s += partial[y * stride * n + e];
   dM[e] = s;
+}
+
+// Partial sums over slices of kReduceSlice consecutive partial matrices, each
+// in order and written over its slice's first matrix (the one partial no other
+// thread reads at e), so a second pass adds kReduceSlice times fewer rows.
+constexpr int64_t kReduceSlice = 32;
+
+__global__ __launch_bounds__(kThreads) void node_mix_reduce_slices_kernel(float* __restrict__ partial, int64_t n,
+                                                                          int64_t parts) {
+  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (e >= n) return;
+  const int64_t y0 = (int64_t)blockIdx.y * kReduceSlice;
+  const int64_t y1 = y0 + kReduceSlice < parts ? y0 + kReduceSlice : parts;
+  float s = 0.f;
+  for (int64_t y = y0; y < y1; ++y) s += partial[y * n + e];
+  partial[y0 * n + e] = s;
+}
+
+// dM = the sum of the `parts` partial matrices of n entries in a fixed order:
+// directly for a few, else by slices of kReduceSlice then over the slices.
+int launch_reduce(float* partial, int64_t n, int64_t parts, float* dM, hipStream_t stream) {
+  const unsigned blocks = (unsigned)((n + kThreads - 1) / kThreads);
+  if (parts <= 2 * kReduceSlice) {
+    hipLaunchKernelGGL(node_mix_reduce_kernel, dim3(blocks), dim3(kThreads), 0, stream, partial, n, parts, (int64_t)1,
+                       dM);
+    return check_launch("node_mix_backward_weight (reduce)");
+  }
+  const int64_t slices = (parts + kReduceSlice - 1) / kReduceSlice;
+  hipLaunchKernelGGL(node_mix_reduce_slices_kernel, dim3(blocks, (unsigned)slices), dim3(kThreads), 0, stream, partial,
+                     n, parts);
+  const int rc = check_launch("node_mix_backward_weight (reduce slices)");
+  if (rc != GM_OK) return rc;
+  hipLaunchKernelGGL(node_mix_reduce_kernel, dim3(blocks), dim3(kThreads), 0, stream, partial, n, slices,
+                     kReduceSlice, dM);
+  return check_launch("node_mix_backward_weight (reduce)");
 }
 
 int check_shapes(int64_t N, int64_t w, int64_t C) {
@@ -887,9 +930,7 @@ int launch_dweight(const float* v, int64_t ldv, const float* dmix, int64_t N, in
   const int64_t n = w * C;
   if (n > 0) {
     const int64_t parts = (N > 0 && C > 0) ? splits * weight_partials_per_split(w) : (int64_t)0;
-    hipLaunchKernelGGL(node_mix_reduce_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       stream, partial, n, parts, dM);
-    return check_launch("node_mix_backward_weight (reduce)");
+    return launch_reduce(partial, n, parts, dM, stream);
   }
   return GM_OK;
 }
@@ -1066,6 +1107,40 @@ extern "C" int gm_node_mix_forward_bf16(const uint16_t* v, int64_t ldv, const fl
   return gm::check_launch("node_mix_forward (bfloat16 vectors)");
 }
 
+namespace gm {
+namespace {
+
+// The split weight gradient for node vectors of type V and mix gradients of
+// type DM (bfloat16 widened exactly while staged): partials, then the
+// fixed-order reduction.
+template <typename V, typename DM>
+int split_dweight(const V* v, int64_t ldv, const DM* dmix, int64_t N, int64_t w, int64_t C, float* partial, float* dM,
+                  hipStream_t s) {
+  int64_t splits = 1, rps = 64;
+  weight_splits(N, w, C, 1 << 20, splits, rps);
+  const int64_t tile = weight_tile(w), nx = (C + tile - 1) / tile;
+  if (N > 0 && nx > 0) {
+    const dim3 grid((unsigned)nx, (unsigned)splits), block(kThreads);
+    const int vec = aligned(v, sizeof(V) == 2 ? 8 : 16) && ldv % 4 == 0;
+    switch (width_class(w)) {
+      case 16: hipLaunchKernelGGL((node_mix_dweight_split<16, V, DM>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      case 32: hipLaunchKernelGGL((node_mix_dweight_split<32, V, DM>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      case 64: hipLaunchKernelGGL((node_mix_dweight_split<64, V, DM>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
+      default:
+        if constexpr (sizeof(V) == 4)
+          hipLaunchKernelGGL((node_mix_dweight_split<128, V, DM>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec);
+        break;
+    }
+    const int rc = check_launch("node_mix_backward_weight");
+    if (rc != GM_OK) return rc;
+  }
+  const int64_t parts = (N > 0 && C > 0) ? splits * weight_partials_per_split(w) : (int64_t)0;
+  return launch_reduce(partial, w * C, parts, dM, s);
+}
+
+}  // namespace
+}  // namespace gm
+
 extern "C" int gm_node_mix_backward_weight_bf16(const uint16_t* v, int64_t ldv, const float* dmix, int64_t N,
                                                 int64_t w, int64_t C, float* partial, float* dM, void* stream) {
   int rc = gm::check_shapes(N, w, C);
@@ -1075,24 +1150,30 @@ extern "C" int gm_node_mix_backward_weight_bf16(const uint16_t* v, int64_t ldv, 
   GM_REQUIRE(dM && partial, "partial and dM must be device pointers");
   GM_REQUIRE(N == 0 || (v && dmix && ldv >= w), "v (ldv >= w) and dmix must be device pointers");
   GM_REQUIRE(C % 4 == 0 && (N == 0 || gm::aligned(dmix, 16)), "dmix must be 16-byte aligned with C a multiple of 4");
-  int64_t splits = 1, rps = 64;
-  gm::weight_splits(N, w, C, 1 << 20, splits, rps);
-  const hipStream_t s = (hipStream_t)stream;
-  const int64_t nx = (C + 63) / 64;
-  if (N > 0 && nx > 0) {
-    const dim3 grid((unsigned)nx, (unsigned)splits), block(gm::kThreads);
-    const int vec = gm::aligned(v, 8) && ldv % 4 == 0;
-    switch (gm::width_class(w)) {
-      case 16: hipLaunchKernelGGL((gm::node_mix_dweight_split<16, uint16_t>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
-      case 32: hipLaunchKernelGGL((gm::node_mix_dweight_split<32, uint16_t>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
-      default: hipLaunchKernelGGL((gm::node_mix_dweight_split<64, uint16_t>), grid, block, 0, s, v, ldv, dmix, N, (int)w, C, rps, partial, vec); break;
-    }
-    rc = gm::check_launch("node_mix_backward_weight (bfloat16 vectors)");
-    if (rc != GM_OK) return rc;
-  }
-  const int64_t n = w * C;
-  const int64_t parts = (N > 0 && C > 0) ? splits * gm::weight_partials_per_split(w) : (int64_t)0;
-  hipLaunchKernelGGL(gm::node_mix_reduce_kernel, dim3((unsigned)((n + gm::kThreads - 1) / gm::kThreads)),
-                     dim3(gm::kThreads), 0, s, partial, n, parts, dM);
-  return gm::check_launch("node_mix_backward_weight (reduce)");
+  return gm::split_dweight(v, ldv, dmix, N, w, C, partial, dM, (hipStream_t)stream);
+}
+
+extern "C" int gm_node_mix_backward_weight_bf16_bf16(const uint16_t* v, int64_t ldv, const uint16_t* dmix, int64_t N,
+                                                     int64_t w, int64_t C, float* partial, float* dM, void* stream) {
+  int rc = gm::check_shapes(N, w, C);
+  if (rc != GM_OK) return rc;
+  GM_REQUIRE(w <= 64, "bfloat16 node vectors at most 64 reals wide");
+  GM_REQUIRE(gm::split_products(), "bfloat16 mix gradients need the split products (GM_SPLIT_PRODUCTS unset or 1)");
+  if (w * C == 0) return GM_OK;
+  GM_REQUIRE(dM && partial, "partial and dM must be device pointers");
+  GM_REQUIRE(N == 0 || (v && dmix && ldv >= w), "v (ldv >= w) and dmix must be device pointers");
+  GM_REQUIRE(C % 4 == 0 && (N == 0 || gm::aligned(dmix, 8)), "dmix must be 8-byte aligned with C a multiple of 4");
+  return gm::split_dweight(v, ldv, dmix, N, w, C, partial, dM, (hipStream_t)stream);
+}
+
+extern "C" int gm_node_mix_backward_weight_f32_bf16(const float* v, int64_t ldv, const uint16_t* dmix, int64_t N,
+                                                    int64_t w, int64_t C, float* partial, float* dM, void* stream) {
+  int rc = gm::check_shapes(N, w, C);
+  if (rc != GM_OK) return rc;
+  GM_REQUIRE(gm::split_products(), "bfloat16 mix gradients need the split products (GM_SPLIT_PRODUCTS unset or 1)");
+  if (w * C == 0) return GM_OK;
+  GM_REQUIRE(dM && partial, "partial and dM must be device pointers");
+  GM_REQUIRE(N == 0 || (v && dmix && ldv >= w), "v (ldv >= w) and dmix must be device pointers");
+  GM_REQUIRE(C % 4 == 0 && (N == 0 || gm::aligned(dmix, 8)), "dmix must be 8-byte aligned with C a multiple of 4");
+  return gm::split_dweight(v, ldv, dmix, N, w, C, partial, dM, (hipStream_t)stream);
 }

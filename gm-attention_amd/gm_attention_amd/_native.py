@@ -62,6 +62,8 @@ SIGNATURES_F32 = {
     "gm_node_mix_backward_weight_noalloc_f32": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P]),
     "gm_node_mix_forward_bf16": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P]),
     "gm_node_mix_backward_weight_bf16": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P]),
+    "gm_node_mix_backward_weight_bf16_bf16": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P]),
+    "gm_node_mix_backward_weight_f32_bf16": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P, _P]),
     "gm_xcd_block_map": (ctypes.c_int, [_I, ctypes.c_int, _P, _I, ctypes.c_int, _P]),
     "gm_factored_forward_grouped_f32": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
                                         + [_P, _P]),
@@ -83,6 +85,9 @@ SIGNATURES_F32 = {
     "gm_geodesic_distances_f64": (ctypes.c_int, [_P] * 3 + [_I] * 3 + [_P, _P]),
     "gm_edge_tables_f64": (ctypes.c_int, [_P] * 6 + [_I] * 4 + [_P] * 7 + [_P]),
     "gm_layer_norm_partial_rows": (ctypes.c_int64, [_I]),
+    "gm_ffn_partial_rows": (ctypes.c_int64, [_I]),
+    "gm_ffn_forward_bf16": (ctypes.c_int, [_P, _I, _I, _I, _D, ctypes.c_int] + [_P] * 12),
+    "gm_ffn_backward_bf16": (ctypes.c_int, [_P, _P, _I, _I, _I, _D, ctypes.c_int] + [_P] * 20),
     **{f"gm_layer_norm_forward_{sfx}": (ctypes.c_int, [_P] * 3 + [_I] * 4 + [_P, _P, _D] + [_P] * 4)
        for sfx in ("f32", "f64", "bf16")},
     **{f"gm_layer_norm_backward_{sfx}": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_P] * 2 + [_P] * 4)
@@ -678,11 +683,14 @@ def node_mix_backward_weight(v: Tensor, dmix: Tensor) -> Tensor:
     _require_device(dmix)
     C = dmix.shape[1]
     _check(dmix.shape[0] == N, "dmix must have the node vectors' rows")
+    _check(dmix.dtype in (torch.float32, torch.bfloat16) and dmix.is_contiguous(),
+           "dmix must be contiguous float32 or bfloat16")
     lib = library()
     partial = torch.empty(max(int(lib.gm_node_mix_weight_partials(N, w, C)), 1), dtype=torch.float32,
                           device=dmix.device)
     dm = torch.empty(w, C, dtype=torch.float32, device=dmix.device)
-    name = "gm_node_mix_backward_weight_bf16" if v.dtype == torch.bfloat16 else "gm_node_mix_backward_weight_f32"
+    vs = "bf16" if v.dtype == torch.bfloat16 else "f32"
+    name = f"gm_node_mix_backward_weight_{vs}" + ("_bf16" if dmix.dtype == torch.bfloat16 else "")
     _call(name, _ptr(v), max(ldv, w), _ptr(dmix), N, w, C, _ptr(partial), _ptr(dm), _stream(dmix.device))
     return dm
 
@@ -1080,6 +1088,85 @@ class PointwiseLayout:
 
     def args(self) -> tuple:
         return (self.D, self.a0, self.nf, ctypes.cast(self.offsets, _P), ctypes.cast(self.mults, _P))
+
+
+def _pointers(ts: list[Tensor]) -> Any:
+    """A host array of the tensors' device pointers (kept alive by the caller's reference)."""
+    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+
+
+def _ffn_check_weights(A: int, B: int, w1t: list[Tensor], wg: Tensor, w2t: list[Tensor]) -> None:
+    for f, (a, b) in enumerate(((A, B), (2 * A, 2 * B), (2 * A, 2 * B))):
+        _check(w1t[f].dtype == torch.bfloat16 and w1t[f].shape == (b, a) and w1t[f].is_contiguous(),
+               f"w1t[{f}] must be a contiguous ({b}, {a}) bfloat16 block")
+        _check(w2t[f].dtype == torch.bfloat16 and w2t[f].shape == (a, b) and w2t[f].is_contiguous(),
+               f"w2t[{f}] must be a contiguous ({a}, {b}) bfloat16 block")
+    _check(wg.dtype == torch.bfloat16 and wg.shape == (2 * B, B) and wg.is_contiguous(),
+           f"wg must be a contiguous ({2 * B}, {B}) bfloat16 matrix")
+
+
+def _ffn_check_params(x: Tensor, A: int, B: int, gamma: Tensor, beta: Tensor | None, b1: Tensor | None,
+                      bg: Tensor | None, b2: Tensor | None) -> None:
+    _require_device(x, gamma)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.shape[1] == 5 * A and x.is_contiguous(),
+           f"x must be contiguous (N, {5 * A}) bfloat16 rows")
+    for name, t, n in (("gamma", gamma, 5 * A), ("beta", beta, A), ("b1", b1, B), ("bg", bg, 2 * B), ("b2", b2, A)):
+        _check(t is None or (t.dtype == torch.float32 and t.shape == (n,) and t.is_contiguous()),
+               f"{name} must be a contiguous ({n},) float32 vector")
+
+
+def ffn_forward(x: Tensor, A: int, B: int, eps: float, double_sigmoid: bool, gamma: Tensor, beta: Tensor | None,
+                w1t: list[Tensor], b1: Tensor | None, wg: Tensor, bg: Tensor | None, w2t: list[Tensor],
+                b2: Tensor | None) -> tuple[Tensor, Tensor, Tensor]:
+    """``(x + y, mean, inv_d)``: the block's fused feed-forward on bfloat16 rows (``gm_ffn_forward_bf16``)."""
+    _ffn_check_params(x, A, B, gamma, beta, b1, bg, b2)
+    _ffn_check_weights(A, B, w1t, wg, w2t)
+    n = x.shape[0]
+    out = torch.empty_like(x)
+    mean = torch.empty(n, dtype=torch.float32, device=x.device)
+    inv_d = torch.empty(n, dtype=torch.float32, device=x.device)
+    p1, p2 = _pointers(w1t), _pointers(w2t)
+    _call("gm_ffn_forward_bf16", _ptr(x), n, A, B, float(eps), int(double_sigmoid), _ptr(gamma), _ptr(beta),
+          ctypes.cast(p1, _P), _ptr(b1), _ptr(wg), _ptr(bg), ctypes.cast(p2, _P), _ptr(b2), _ptr(out), _ptr(mean),
+          _ptr(inv_d), _stream(x.device))
+    return out, mean, inv_d
+
+
+def ffn_backward(dz: Tensor, x: Tensor, A: int, B: int, eps: float, double_sigmoid: bool, gamma: Tensor,
+                 beta: Tensor | None, w1t: list[Tensor], w1n: list[Tensor], b1: Tensor | None, wg: Tensor,
+                 wgt: Tensor, bg: Tensor | None, w2t: list[Tensor], w2n: list[Tensor], mean: Tensor,
+                 inv_d: Tensor) -> dict[str, Any]:
+    """The fused feed-forward's backward (``gm_ffn_backward_bf16``): ``dx`` and the
+    factors of the parameter gradients (``xhat``, ``hidden0``, ``outs``,
+    ``dhidden``, ``dpre``), with ``dgb`` = (dgamma | dbeta) summed over the tiles."""
+    _ffn_check_params(x, A, B, gamma, beta, b1, bg, None)
+    _ffn_check_weights(A, B, w1t, wg, w2t)
+    for f, (a, b) in enumerate(((A, B), (2 * A, 2 * B), (2 * A, 2 * B))):
+        _check(w1n[f].dtype == torch.bfloat16 and w1n[f].shape == (a, b) and w1n[f].is_contiguous(),
+               f"w1n[{f}] must be a contiguous ({a}, {b}) bfloat16 block")
+        _check(w2n[f].dtype == torch.bfloat16 and w2n[f].shape == (b, a) and w2n[f].is_contiguous(),
+               f"w2n[{f}] must be a contiguous ({b}, {a}) bfloat16 block")
+    _check(wgt.dtype == torch.bfloat16 and wgt.shape == (B, 2 * B) and wgt.is_contiguous(),
+           f"wgt must be a contiguous ({B}, {2 * B}) bfloat16 matrix")
+    _require_device(dz, mean, inv_d)
+    _check(dz.dtype == torch.bfloat16 and dz.shape == x.shape and dz.is_contiguous(), "dz must match x")
+    n, dev = x.shape[0], x.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    dx = torch.empty_like(x)
+    xhat = torch.empty_like(x)
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    hidden0 = torch.empty(n, B, **f32)
+    outs = [torch.empty(n, w, **bf) for w in (B, 2 * B, 2 * B)]
+    dhidden = [torch.empty(n, w, **bf) for w in (B, 2 * B, 2 * B)]
+    dpre = torch.empty(n, 2 * B, **bf)
+    partial = torch.empty(max(int(library().gm_ffn_partial_rows(n)), 1), 6 * A, **f32)
+    arrays = [_pointers(w1t), _pointers(w1n), _pointers(w2t), _pointers(w2n), _pointers(outs), _pointers(dhidden)]
+    p1t, p1n, p2t, p2n, po, pd = (ctypes.cast(a, _P) for a in arrays)
+    _call("gm_ffn_backward_bf16", _ptr(dz), _ptr(x), n, A, B, float(eps), int(double_sigmoid), _ptr(gamma),
+          _ptr(beta), p1t, p1n, _ptr(b1), _ptr(wg), _ptr(wgt), _ptr(bg), p2t, p2n, _ptr(mean), _ptr(inv_d),
+          _ptr(dx), _ptr(xhat), _ptr(hidden0), po, pd, _ptr(dpre), _ptr(partial), _stream(dev))
+    dgb = partial[: int(library().gm_ffn_partial_rows(n))].sum(0) if n > 0 else torch.zeros(6 * A, **f32)
+    return dict(dx=dx, xhat=xhat, hidden0=hidden0, outs=outs, dhidden=dhidden, dpre=dpre, dgb=dgb)
 
 
 def param_dtype(dtype: torch.dtype) -> torch.dtype:

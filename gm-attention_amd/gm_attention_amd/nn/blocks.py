@@ -41,6 +41,7 @@ from gm_attention_amd.nn.attention import SO2MHSA, batched_flat_serves, gather_t
 from gm_attention_amd.nn.convolution import SO2Convolution
 from gm_attention_amd.nn.fused_attention import evaluate_aggregation_window
 from gm_attention_amd.nn.kernels import SO2SteerableKernel
+from gm_attention_amd.nn import ffn
 from gm_attention_amd.nn.linear import SO2Linear, flat_forward
 from gm_attention_amd.nn.nonlinearities import SO2ScalarGatedNonlinearity
 from gm_attention_amd.nn.normalization import SO2Dropout, SO2LayerNorm
@@ -147,6 +148,8 @@ class SO2TransformerBlock(nn.Module):
         """The block on flat rows ``(N, D)``; returns ``(N, D)`` in the rows' dtype."""
         attended = self._mix(self.norm1.forward_flat(rows), edges, chunk_size)
         rows = rows + self.attention_dropout.forward_flat(attended).to(rows.dtype)
+        if ffn.serves(self, rows):  # bfloat16 rows: the whole feed-forward as one fused pass per direction
+            return ffn.forward(self, rows)
         hidden = flat_forward(self.linear1, self.norm2.forward_flat(rows))
         hidden = self.activation.forward_flat(hidden)
         hidden = flat_forward(self.linear2, hidden)

@@ -329,6 +329,35 @@ int gm_gate_backward_bf16(const uint16_t* gy, const uint16_t* h, const uint16_t*
                           int64_t a0, int64_t nf, const int64_t* offsets, const int64_t* mults, int64_t double_sigmoid,
                           uint16_t* dh, uint16_t* dpre, void* stream);
 
+/* Fused feed-forward of the transformer block; replaces the norm2 -> linear1 ->
+ * activation -> linear2 -> residual sequence of SO2TransformerBlock.forward
+ * (nn/blocks.py:326-349, with nn/normalization.py:117-178,
+ * nn/nonlinearities.py:140-166 and nn/linear.py:130-190) for bfloat16 rows of a
+ * field with frequencies 0, 1, 2 of A = 32 copies each, widened to B = 64 or
+ * 128 copies each, the dropout inactive: out = x + linear2(act(linear1(norm(x)))).
+ * Weights are the layers' flat-matrix blocks per frequency f in bfloat16:
+ * w1t[f] = M1_f^T (Dh_f, D_f) and w2t[f] = M2_f^T (D_f, Dh_f), row-major, with
+ * D_f = A, 2A, 2A and Dh_f = B, 2B, 2B; wg (2B, B) the gates' nn.Linear weights
+ * stacked frequency-major; gamma (5A) per flat coordinate, beta (A), b1 (B),
+ * bg (2B), b2 (A) float32 or null.  The forward saves mean and inv_d per node.
+ * The backward takes the blocks' other orientation too (w1n[f] = M1_f,
+ * w2n[f] = M2_f, wgt = wg^T), writes dx = dz + the branch's input gradient and
+ * the factors of the parameter gradients: xhat (N x 5A), outs[f] and dhidden[f]
+ * (N x Dh_f), dpre (N x 2B) in bfloat16, hidden0 (N x B) float32, and per
+ * 16-node tile one row of (dgamma | dbeta) partials (gm_ffn_partial_rows(N)
+ * rows of 6A). */
+int64_t gm_ffn_partial_rows(int64_t N);
+int gm_ffn_forward_bf16(const uint16_t* x, int64_t N, int64_t A, int64_t B, double eps, int double_sigmoid,
+                        const float* gamma, const float* beta, const uint16_t* const* w1t, const float* b1,
+                        const uint16_t* wg, const float* bg, const uint16_t* const* w2t, const float* b2,
+                        uint16_t* out, float* mean, float* inv_d, void* stream);
+int gm_ffn_backward_bf16(const uint16_t* dz, const uint16_t* x, int64_t N, int64_t A, int64_t B, double eps,
+                         int double_sigmoid, const float* gamma, const float* beta, const uint16_t* const* w1t,
+                         const uint16_t* const* w1n, const float* b1, const uint16_t* wg, const uint16_t* wgt,
+                         const float* bg, const uint16_t* const* w2t, const uint16_t* const* w2n, const float* mean,
+                         const float* inv_d, uint16_t* dx, uint16_t* xhat, float* hidden0, uint16_t* const* outs,
+                         uint16_t* const* dhidden, uint16_t* dpre, float* partial, void* stream);
+
 /* ---------------- factored steerable kernel ----------------
  *
  * Per edge e = (i <- j) with h~ = (1, h(e)): every block b's combination
@@ -546,6 +575,17 @@ int gm_node_mix_forward_bf16(const uint16_t* v, int64_t ldv, const float* M, int
                              float* out, void* stream);
 int gm_node_mix_backward_weight_bf16(const uint16_t* v, int64_t ldv, const float* dmix, int64_t N, int64_t w,
                                      int64_t C, float* partial, float* dM, void* stream);
+/* The weight gradient with bfloat16 mix gradients (widened exactly): v bfloat16
+ * (w <= 64) or float32 (w <= 128), dmix (N, C) bfloat16, 8-byte aligned; the
+ * partials workspace as gm_node_mix_weight_partials(N, w, C).  The reference
+ * has no such entry: they take the fused feed-forward's parameter gradients,
+ * x^T g over the nodes (SO2Linear and the gates' nn.Linear, nn/linear.py:130-190,
+ * nn/nonlinearities.py:140-166), from the factors its backward writes.  They
+ * need the split products (GM_SPLIT_PRODUCTS unset or 1). */
+int gm_node_mix_backward_weight_bf16_bf16(const uint16_t* v, int64_t ldv, const uint16_t* dmix, int64_t N, int64_t w,
+                                          int64_t C, float* partial, float* dM, void* stream);
+int gm_node_mix_backward_weight_f32_bf16(const float* v, int64_t ldv, const uint16_t* dmix, int64_t N, int64_t w,
+                                         int64_t C, float* partial, float* dM, void* stream);
 
 /* gm_node_mix_backward_weight_f32 without a workspace argument and without
  * allocating: no counterpart in the reference; for callers that cannot

@@ -27,6 +27,7 @@ import pytest
 import torch
 
 import problems
+from gm_attention_amd.nn import ffn
 from gm_attention_amd.nn.attention import SO2MHSA, batched_flat_serves
 from gm_attention_amd.nn.blocks import SO2TransformerBlock
 from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
@@ -166,6 +167,8 @@ def test_c4_block_in_bfloat16_is_within_2e2(cuda):
     # the bfloat16 rows go into the fused attention as they are (bf16 scores and node-mix kernels)
     assert batched_flat_serves(gpu.attention, SO2FeatureField.from_flat(ft, x.to(cuda, torch.bfloat16)),
                                edges.to(cuda, torch.float32))
+    # and the feed-forward runs as the fused pass (LN -> SO2Linear -> gate -> SO2Linear on bf16 MFMA)
+    assert ffn.serves(gpu, x.to(cuda, torch.bfloat16))
     got = run(gpu, x.to(cuda, torch.bfloat16), edges.to(cuda, torch.float32), False)
     assert got[0].dtype == torch.bfloat16 and got[1].dtype == torch.bfloat16
     for name, g, w in (("out", got[0], want[0]), ("dx", got[1], want[1])):
