@@ -262,11 +262,8 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
       lw[u] = (live[u] && in[u]) ? a.scale * acc + bias[u] : neg_inf<T>();  // outside the window: excluded
     }
   };
-  // The scores held in registers need only their maximum while they arrive:
-  // each is exponentiated once at the end (p = exp(x - m_r)), and the row's
-  // weights are p exp(m_r - M) / L.  The parked ones keep the online state.
   T sc[R > 0 ? R : 1];
-  T mr = neg_inf<T>();
+  T m = neg_inf<T>(), l = T(0);
 #pragma unroll
   for (int t = 0; t < R / U; ++t) {
     const int64_t eb = e0 + s + (int64_t)t * U * S;
@@ -276,10 +273,9 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       sc[t * U + u] = lw[u];
-      mr = lw[u] > mr ? lw[u] : mr;
+      online_add(m, l, lw[u]);
     }
   }
-  T m = neg_inf<T>(), l = T(0);
   for (int64_t eb = e0 + s + (int64_t)R * S; eb < e1; eb += (int64_t)U * S) {
     T lw[U];
     step(eb, lw);
@@ -290,23 +286,14 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
       online_add(m, l, lw[u]);
     }
   }
-  T lr = T(0);
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t e = e0 + s + (int64_t)r * S;
-    sc[r] = (e < e1 && mr != neg_inf<T>()) ? gm_exp(sc[r] - mr) : T(0);  // an excluded edge is exp(-inf) = 0
-    lr += sc[r];
-  }
-  online_merge(m, l, mr, lr);
   for (int off = H; off < kWave; off <<= 1) {
     const T mo = __shfl_xor(m, off, kWave), lo = __shfl_xor(l, off, kWave);
     online_merge(m, l, mo, lo);
   }
-  const T rescale = mr == neg_inf<T>() ? T(0) : gm_exp(mr - m) / l;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t e = e0 + s + (int64_t)r * S;
-    if (e < e1) a.alpha[e * H + h] = sc[r] * rescale;
+    if (e < e1) a.alpha[e * H + h] = gm_exp(sc[r] - m) / l;  // an excluded edge is exp(-inf) = 0
   }
   for (int64_t e = e0 + s + (int64_t)R * S; e < e1; e += S) {
     const T lw = a.alpha[e * H + h];
