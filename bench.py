@@ -22,11 +22,17 @@ gradient, at 256x512, batch 2, with bfloat16 rows (residual stream, norms,
 gate, feed-forward GEMMs) and float32 parameters; the attention's kernels
 compute in float32.
 
-``--workload encoder`` runs C5's restrictions: two ``EquiEncode`` hops,
-128x256 ({0: 4}) -> 64x128 ({0: 64, 1: 64, 2: 64}) -> 32x64 ({0: 128, 1: 128,
-2: 128}), batch 8, forward + backward with every gradient, float32, over the
-GPU-built bipartite edges (radius two coarse row spacings, quartic window);
-the wide kernels run as output tiles of the fused factored aggregate.
+``--workload encoder`` runs the C5 stage model end to end (``GmSegformer``:
+restrictions 128x256 ({0: 4}) -> 64x128 ({0: 64, 1: 64, 2: 64}) -> 32x64
+({0: 128, 1: 128, 2: 128}), an 8-head then a 16-head block, readouts, fusion
+decoder, 13-class head and cross-entropy), batch 8, forward + backward with
+every gradient, float32; ``--workload hops`` times its two restrictions alone.
+
+The default run also measures the other configurations (C3 ``conv``, C4
+``block``, C5 ``encoder`` and the GPU ``geometry`` build), each in a process of
+its own after the headline measurement, and reports their rates, step times
+and roofline objects under ``other_workloads`` in the same JSON line
+(``--no-other-workloads`` skips them).
 
 ``--workload softmax`` times the scores-and-softmax op alone (forward +
 backward) on the same shape.  ``--workload conv`` times the depthwise steerable
@@ -705,6 +711,35 @@ def run_encoder(args) -> None:
     print(json.dumps(line))
 
 
+OTHER_WORKLOADS = (("conv", 5), ("block", 5), ("encoder", 3), ("geometry", 5))
+
+
+def other_workloads() -> dict:
+    """Every other configuration's line, from a child process each (warm-up 2, a few timed steps, no CPU
+    baseline): rate, step time and roofline, or the error it ended with."""
+    import subprocess
+
+    out = {}
+    for name, steps in OTHER_WORKLOADS:
+        log(f"other workload: {name} ({steps} steps)")
+        cmd = [sys.executable, str(Path(__file__).resolve()), "--workload", name, "--steps", str(steps), "--warmup",
+               "2", "--no-cpu-baseline"]
+        try:
+            run = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+        except subprocess.TimeoutExpired:
+            out[name] = {"error": "timed out after 300 s"}
+            continue
+        lines = [x for x in run.stdout.splitlines() if x.startswith("{")]
+        if run.returncode != 0 or not lines:
+            tail = (run.stderr or run.stdout).strip().splitlines()[-1:] or [""]
+            out[name] = {"error": f"exit {run.returncode}: {tail[0][:300]}"}
+            continue
+        rec = json.loads(lines[-1])
+        out[name] = {k: rec.get(k) for k in ("metric", "value", "unit", "ms_per_step", "steps", "dtype", "roofline")}
+        log(f"{name}: {rec.get('ms_per_step')} ms per step")
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -713,6 +748,8 @@ def main() -> None:
     ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry", "block", "encoder", "hops"),
                     default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-workloads", action="store_true",
+                    help="the default attention run skips measuring the other configurations")
     ap.add_argument("--cpu-budget-edges", type=int, default=200_000)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB between two device buffers three times (the reference reading for the "
@@ -970,6 +1007,14 @@ def main() -> None:
         "ops": op_rates,
         "cpu_baseline": baseline,
     }
+    if args.workload == "attention" and not args.no_other_workloads:
+        # the headline's tensors go back to the device before the other configurations run beside this process
+        del x_flat, upstream, mhsa, module
+        import gc
+
+        gc.collect()
+        torch.cuda.empty_cache()
+        line["other_workloads"] = other_workloads()
     print(json.dumps(line))
 
 
