@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256) void aggregate_kernel(AggArgs<T> a) {
 // rows[h, inv[e], :] (rows kept per head in the grouping's order).  One wave
 // per target: with d_out a multiple of four, lane l < H d_out / 4 owns the
 // four outputs 4 l .. 4 l + 3 (one 16-byte row piece a load), else lane l
-// owns the outputs l, l + 64, l + 128.  The edges go in CSR order, eight a
+// owns the outputs l, l + 64, l + 128.  The edges go in CSR order, kAggStep a
 // step with their loads in flight together, so every sum has a fixed order.
 struct AggHeadsArgs {
   const float* rows;   // (H, n_rows, d_out)
@@ -312,7 +312,7 @@ struct AggHeadsArgs {
   int H, d_out, split;
 };
 
-constexpr int kAggStep = 8;
+constexpr int kAggStep = 4;  // edges a step: 55 VGPRs, eight waves a SIMD (eight a step: five waves, 10.4 vs 9.0 ms at NS)
 
 // One wave per target, lane l owning the 16-byte pieces l, l + 64, ...,
 // l + 64 (P - 1) of the target's H d_out outputs (piece o: row head o / q4,
