@@ -77,7 +77,9 @@ __device__ __forceinline__ void wave_sync() {
 //     (the basis once per tile, shared by every head; the bias as the weight of a
 //     basis entry that is 1, in the first free slot), so a lane's four
 //     features of one edge come from one 16-byte load of its dh row;
-//   dp = dh * SiLU'(pre), turned through the wave's 1 KB LDS tile to
+//   dp = dh * SiLU'(pre), turned through the wave's LDS tile (feature rows of
+//     16 edges padded to 20 floats, so neither the writes nor the 16-byte
+//     reads meet in a bank) to
 //     B2_j[q][feature c] = dp(feature c, edge 4q + j), j < 4 (one 16-byte LDS read);
 //   D2[m][feature c] += sum over j of A2_j B2_j with
 //     A2_j[m = c][k = q] = b_c(edge 4q + j) (c < B), 1 at c = B, 0 above,
@@ -85,10 +87,10 @@ __device__ __forceinline__ void wave_sync() {
 //   tiles in registers for every head.  Edges past the end read dh as zero and add nothing.
 template <int B>
 __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a) {
-  constexpr int T = 16, P = T * B + T;
-  __shared__ float4 stage[kTrunkWaves][T * 4];  // per wave: dp as [feature][edge]
+  constexpr int T = 16, P = T * B + T, LDT = T + 4;
+  __shared__ __align__(16) float stage[kTrunkWaves][T * LDT];  // per wave: dp as [feature][edge]
   const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15, wv = threadIdx.x >> 6;
-  float* tile_lds = reinterpret_cast<float*>(stage[wv]);
+  float* tile_lds = stage[wv];
   const int64_t wave = (int64_t)blockIdx.x * kTrunkWaves + wv;
   const int64_t n_waves = (int64_t)gridDim.x * kTrunkWaves;
   const int64_t n_tiles = (a.n_edges + 15) / 16;
@@ -169,10 +171,10 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float sg = sigmoid_of(pre[r]);
-        tile_lds[(4 * q + r) * 16 + c] = gv[r] * sg * (1.f + pre[r] * (1.f - sg));
+        tile_lds[(4 * q + r) * LDT + c] = gv[r] * sg * (1.f + pre[r] * (1.f - sg));
       }
       wave_sync();
-      const float4 dp = stage[wv][c * 4 + q];  // dp(feature c, edges 4q..4q+3)
+      const float4 dp = *reinterpret_cast<const float4*>(tile_lds + c * LDT + 4 * q);  // dp(feature c, edges 4q..4q+3)
       acc[h] = mfma16(a2[0], dp.x, acc[h]);
       acc[h] = mfma16(a2[1], dp.y, acc[h]);
       acc[h] = mfma16(a2[2], dp.z, acc[h]);
