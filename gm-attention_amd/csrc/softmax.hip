@@ -13,10 +13,10 @@
 // head h) with S = 64 / H slots, so a lane scores its head on every S-th edge
 // of the neighbourhood, holding its head's query columns in registers, and
 // the 8 lanes of one edge read that edge's key row as contiguous 16-byte
-// pieces.  The softmax is online per lane (running max and sum) and merged
-// across the slots of a head with lane shuffles; a lane's first scores stay in
-// registers and are normalised there (alpha written once), scores past them
-// park in alpha and are normalised by a second walk over those edges.
+// pieces.  The forward takes the eager softmax's steps (the scores and their
+// maximum, the sum of exponentials, the quotients), each reduced across the
+// slots of a head with lane shuffles; a lane's first scores stay in registers
+// (alpha written once), scores past them park in alpha and are read back.
 // The backward is two passes: per target (the adjoint's per-head total, ds,
 // and dq) and per source over the edges grouped by source (dk), so no atomics
 // are used and the result is deterministic; ds is written to its edge's place
@@ -147,10 +147,10 @@ __device__ __forceinline__ void transport_pairs(const Chunks& C, const T* tr, T 
 // scalar chunk, two chunks each of frequencies 1 and 2), compiled in.
 constexpr uint32_t kOrders012 = 0x22110u;
 
-// Scores a lane keeps in registers: rows of up to S * kSmRegs edges (256 at
+// Scores a lane keeps in registers: rows of up to S * kSmRegs edges (128 at
 // eight heads) are normalised from registers, so alpha is written once; the
-// edges past that park their raw score in alpha and are normalised by a
-// second walk over them.
+// edges past that park their raw score in alpha and are read back for the sum
+// and for the quotient.
 constexpr int kSmRegs = 16;
 constexpr bool kSmPrefetch = true;  // next step's source ids requested before this step's rows are used
 
@@ -196,9 +196,65 @@ __device__ __forceinline__ void gather(const SmArgs<T>& a, Gather<T, NCH>& g, co
   }
 }
 
-// Forward.  The lane's edges are e0 + s + r S; every step requests the next
-// step's source ids before it waits for its own rows, so a step costs one
-// memory round trip.
+// The same from the lane's chunk offsets, computed once per wave (one 64-bit
+// add per chunk and edge).
+template <typename T, int NCH, uint32_t ORD, typename R>
+__device__ __forceinline__ void gather_at(const SmArgs<T>& a, Gather<T, NCH>& g, const R* rows,
+                                          const int64_t (&node)[kSmStep], const T* transport,
+                                          const int64_t (&te)[kSmStep], const int64_t (&off)[NCH]) {
+#pragma unroll
+  for (int u = 0; u < kSmStep; ++u) {
+    const R* r = rows + node[u] * a.D;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) g.row[u][c] = row4<T>(r + off[c]);
+    transport_pairs<T, NCH, ORD>(a.C, transport + te[u] * a.orders * 2, g.tc[u], g.ts[u]);
+  }
+}
+
+// Re< q, tau k > summed over a head's chunks.  With compile-time orders the
+// chunks of one order share their rotation: per order the two sums
+// A = sum q.k and B = sum (q1 k0 - q0 k1) over the pairs, then c A + s B
+// (tau k = (c k0 - s k1, c k1 + s k0) per pair).
+template <typename T, int NCH, uint32_t ORD>
+__device__ __forceinline__ T score_dot(const Chunks& C, const T (&q)[NCH * 4], const Gather<T, NCH>& g, int u) {
+  if constexpr (ORD != 0) {
+    constexpr int MO = max_order_of(ORD);
+    T A[MO + 1], B[MO + 1], cs[MO + 1], sn[MO + 1];
+#pragma unroll
+    for (int o = 0; o <= MO; ++o) A[o] = B[o] = cs[o] = sn[o] = T(0);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int o = chunk_order<ORD>(C, c);
+      const T* q4 = &q[4 * c];
+      const Quad<T>& k = g.row[u][c];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) A[o] = fma(q4[v], k.v[v], A[o]);
+      if (o != 0) {
+#pragma unroll
+        for (int v = 0; v < 4; v += 2) B[o] = fma(-q4[v], k.v[v + 1], fma(q4[v + 1], k.v[v], B[o]));
+        cs[o] = g.tc[u][c];
+        sn[o] = g.ts[u][c];
+      }
+    }
+    T acc = A[0];
+#pragma unroll
+    for (int o = 1; o <= MO; ++o) acc += cs[o] * A[o] + sn[o] * B[o];
+    return acc;
+  } else {
+    T acc = T(0);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      acc += chunk_dot_pair(&q[4 * c], g.row[u][c], chunk_order<ORD>(C, c), g.tc[u][c], g.ts[u][c]);
+    return acc;
+  }
+}
+
+// Forward, in the eager softmax's own steps: the scores and their maximum,
+// the sum of exp(s - max), the quotients.  The lane's edges are e0 + s + r S;
+// every step requests the next step's source ids before it waits for its own
+// rows, so a step costs one memory round trip.  A lane's first R scores stay
+// in registers; later ones park in alpha and are read back for the sum and
+// for the quotient (their exponential taken again: cheaper than a store).
 template <typename T, int NCH, uint32_t ORD, bool B16>
 __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   constexpr int U = kSmStep, R = kSmRegs;
@@ -210,11 +266,13 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   const int h = lane & (H - 1), s = lane >> a.hshift;
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
 
+  int64_t off[NCH];
   T q[NCH * 4];
   const auto qi = rows_of<T, B16, false>(a) + i * a.D;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const Quad<T> x = row4<T>(qi + a.C.base[c] + h * a.C.stride[c]);
+    off[c] = a.C.base[c] + h * a.C.stride[c];
+    const Quad<T> x = row4<T>(qi + off[c]);
 #pragma unroll
     for (int u = 0; u < 4; ++u) q[4 * c + u] = x.v[u];
   }
@@ -245,7 +303,7 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
       }
     }
     Gather<T, NCH> g;
-    gather<T, NCH, ORD>(a, g, rows_of<T, B16, true>(a), jc, a.transport, te, h);
+    gather_at<T, NCH, ORD>(a, g, rows_of<T, B16, true>(a), jc, a.transport, te, off);
     T bias[U];
     uint8_t in[U];
 #pragma unroll
@@ -255,15 +313,12 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      T acc = T(0);
-#pragma unroll
-      for (int c = 0; c < NCH; ++c)
-        acc += chunk_dot_pair(&q[4 * c], g.row[u][c], chunk_order<ORD>(a.C, c), g.tc[u][c], g.ts[u][c]);
+      const T acc = score_dot<T, NCH, ORD>(a.C, q, g, u);
       lw[u] = (live[u] && in[u]) ? a.scale * acc + bias[u] : neg_inf<T>();  // outside the window: excluded
     }
   };
   T sc[R > 0 ? R : 1];
-  T m = neg_inf<T>(), l = T(0);
+  T m = neg_inf<T>();
 #pragma unroll
   for (int t = 0; t < R / U; ++t) {
     const int64_t eb = e0 + s + (int64_t)t * U * S;
@@ -273,32 +328,42 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       sc[t * U + u] = lw[u];
-      online_add(m, l, lw[u]);
+      m = lw[u] > m ? lw[u] : m;
     }
   }
-  for (int64_t eb = e0 + s + (int64_t)R * S; eb < e1; eb += (int64_t)U * S) {
+  const int64_t tail = e0 + s + (int64_t)R * S;
+  for (int64_t eb = tail; eb < e1; eb += (int64_t)U * S) {
     T lw[U];
     step(eb, lw);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t e = eb + (int64_t)u * S;
       if (e < e1) a.alpha[e * H + h] = lw[u];
-      online_add(m, l, lw[u]);
+      m = lw[u] > m ? lw[u] : m;
     }
   }
-  for (int off = H; off < kWave; off <<= 1) {
-    const T mo = __shfl_xor(m, off, kWave), lo = __shfl_xor(l, off, kWave);
-    online_merge(m, l, mo, lo);
+  for (int o = H; o < kWave; o <<= 1) {
+    const T mo = __shfl_xor(m, o, kWave);
+    m = mo > m ? mo : m;
   }
+  // an excluded edge is exp(-inf) = 0; a row with none inside has max -inf and
+  // gives NaN, as the eager division 0 / 0 does
+  T l = T(0);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (e0 + s + (int64_t)r * S < e1) {
+      sc[r] = gm_exp(sc[r] - m);
+      l += sc[r];
+    }
+  }
+  for (int64_t e = tail; e < e1; e += S) l += gm_exp(a.alpha[e * H + h] - m);
+  l = group_sum_pow2(l, H);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t e = e0 + s + (int64_t)r * S;
-    if (e < e1) a.alpha[e * H + h] = gm_exp(sc[r] - m) / l;  // an excluded edge is exp(-inf) = 0
+    if (e < e1) a.alpha[e * H + h] = sc[r] / l;
   }
-  for (int64_t e = e0 + s + (int64_t)R * S; e < e1; e += S) {
-    const T lw = a.alpha[e * H + h];
-    a.alpha[e * H + h] = gm_exp(lw - m) / l;
-  }
+  for (int64_t e = tail; e < e1; e += S) a.alpha[e * H + h] = gm_exp(a.alpha[e * H + h] - m) / l;
 }
 
 // Backward per target: the adjoint's per-head total, ds, and dq.  ds goes to
