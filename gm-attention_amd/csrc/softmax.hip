@@ -24,6 +24,7 @@
 // transport rows as streams.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.hpp"
@@ -366,6 +367,136 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
   for (int64_t e = tail; e < e1; e += S) a.alpha[e * H + h] = gm_exp(a.alpha[e * H + h] - m) / l;
 }
 
+// The forward for compiled-in chunk orders, with each edge's own entries
+// (source id, bias and window flag, transport pairs) read once per 64 edges:
+// lane l loads edge base + l's entries (one batch ahead) and every step takes
+// its edge's from lane t S + s by a lane shuffle.  The 8 lanes of an edge
+// would otherwise load the same entries on every step; the texture data path
+// that returns loads is the kernels' bound, and it counts wave instructions,
+// not bytes.  Same arithmetic and order of operations as softmax_forward_fast.
+template <int MO>
+struct EdgeBatch {
+  int src;            // source id (node ids fit 31 bits)
+  float bm;           // bias, or -inf outside the window and past the row
+  float tr[2 * MO];   // (cos, sin) of orders 1 .. MO
+};
+
+template <typename T, int NCH, uint32_t ORD, bool B16, int S>
+__global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
+  static_assert(ORD != 0 && std::is_same<T, float>::value, "compiled-in orders, float arithmetic");
+  constexpr int R = kSmRegs, MO = max_order_of(ORD), SB = kWave / S;  // steps a batch
+  static_assert(R % SB == 0, "whole batches in registers");
+  const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_nodes, kWavesPerBlock);
+  const int lane = threadIdx.x & 63;
+  const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
+  if (i >= a.n_nodes) return;
+  const int H = kWave / S;
+  const int h = lane & (H - 1), s = lane / H;
+  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
+
+  int64_t off[NCH];
+  float q[NCH * 4];
+  const auto qi = rows_of<T, B16, false>(a) + i * a.D;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    off[c] = a.C.base[c] + h * a.C.stride[c];
+    const Quad<float> x = row4<float>(qi + off[c]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[4 * c + u] = x.v[u];
+  }
+  auto load_batch = [&](int64_t base, EdgeBatch<MO>& b) {
+    const int64_t e = base + lane;
+    if (e < e1) {
+      b.src = (int)a.source[e];
+      b.bm = a.inside[e] ? a.bias[e] : neg_inf<float>();
+      const float* tr = a.transport + e * a.orders * 2;
+#pragma unroll
+      for (int o = 1; o <= MO; ++o) ld_pair(tr + 2 * o, b.tr[2 * o - 2], b.tr[2 * o - 1]);
+    } else {
+      b.src = 0;
+      b.bm = neg_inf<float>();
+#pragma unroll
+      for (int o = 0; o < 2 * MO; ++o) b.tr[o] = 0.f;
+    }
+  };
+  const auto krows = rows_of<T, B16, true>(a);
+  // score of step t of batch b (edge base + t S + s; -inf when excluded or past the row)
+  auto score = [&](const EdgeBatch<MO>& b, int t) {
+    const int from = t * S + s;
+    const int j = __shfl(b.src, from, kWave);
+    Gather<float, NCH> g;
+    const auto r = krows + (int64_t)j * a.D;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) g.row[0][c] = row4<float>(r + off[c]);
+    const float bm = __shfl(b.bm, from, kWave);
+    float cs[MO + 1], sn[MO + 1];
+    cs[0] = 1.f;
+    sn[0] = 0.f;
+#pragma unroll
+    for (int o = 1; o <= MO; ++o) {
+      cs[o] = __shfl(b.tr[2 * o - 2], from, kWave);
+      sn[o] = __shfl(b.tr[2 * o - 1], from, kWave);
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      g.tc[0][c] = cs[chunk_order<ORD>(a.C, c)];
+      g.ts[0][c] = sn[chunk_order<ORD>(a.C, c)];
+    }
+    const float acc = score_dot<float, NCH, ORD>(a.C, q, g, 0);
+    return bm == neg_inf<float>() ? neg_inf<float>() : a.scale * acc + bm;
+  };
+  EdgeBatch<MO> cur, nxt;
+  load_batch(e0, cur);
+  float sc[R];
+  float m = neg_inf<float>();
+#pragma unroll
+  for (int bi = 0; bi < R / SB; ++bi) {
+    const int64_t base = e0 + (int64_t)bi * kWave;
+    if (base >= e1) break;
+    if (base + kWave < e1) load_batch(base + kWave, nxt);
+#pragma unroll
+    for (int t = 0; t < SB; ++t) {
+      const float lw = base + t * S < e1 ? score(cur, t) : neg_inf<float>();
+      sc[bi * SB + t] = lw;
+      m = lw > m ? lw : m;
+    }
+    cur = nxt;
+  }
+  const int64_t tail = e0 + (int64_t)R * S;
+  for (int64_t base = tail; base < e1; base += kWave) {
+    if (base + kWave < e1) load_batch(base + kWave, nxt);
+#pragma unroll
+    for (int t = 0; t < SB; ++t) {
+      if (base + t * S >= e1) break;
+      const float lw = score(cur, t);
+      const int64_t e = base + t * S + s;
+      if (e < e1) a.alpha[e * H + h] = lw;
+      m = lw > m ? lw : m;
+    }
+    cur = nxt;
+  }
+  for (int o = H; o < kWave; o <<= 1) {
+    const float mo = __shfl_xor(m, o, kWave);
+    m = mo > m ? mo : m;
+  }
+  float l = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (e0 + s + (int64_t)r * S < e1) {
+      sc[r] = gm_exp(sc[r] - m);
+      l += sc[r];
+    }
+  }
+  for (int64_t e = tail + s; e < e1; e += S) l += gm_exp(a.alpha[e * H + h] - m);
+  l = group_sum_pow2(l, H);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t e = e0 + s + (int64_t)r * S;
+    if (e < e1) a.alpha[e * H + h] = sc[r] / l;
+  }
+  for (int64_t e = tail + s; e < e1; e += S) a.alpha[e * H + h] = gm_exp(a.alpha[e * H + h] - m) / l;
+}
+
 // Backward per target: the adjoint's per-head total, ds, and dq.  ds goes to
 // its edge's place in the source grouping (inv), so the per-source pass reads
 // it as one stream.
@@ -528,6 +659,112 @@ __global__ __launch_bounds__(256) void softmax_backward_source_fast(SmArgs<T> a)
   }
 }
 
+// The per-source backward pass for compiled-in orders with each edge's own
+// entries (target id, transport pairs) read once per 64 edges and shared by
+// lane shuffles, as the batched forward; same edges in the same order and the
+// same arithmetic as softmax_backward_source_fast.  (The per-target pass in
+// this form, its source ids, grouping places and transport batched, measured
+// slower than softmax_backward_target_fast at NS: 4.80 vs 4.65 ms.)
+template <int MO>
+struct IdBatch {
+  int id;
+  float tr[2 * MO];
+};
+
+template <int MO, typename IdT>
+__device__ __forceinline__ void load_ids(IdBatch<MO>& b, int64_t e, int64_t end, const IdT* ids,
+                                         const float* transport, int orders) {
+  if (e < end) {
+    b.id = (int)ids[e];
+    const float* tr = transport + e * orders * 2;
+#pragma unroll
+    for (int o = 1; o <= MO; ++o) ld_pair(tr + 2 * o, b.tr[2 * o - 2], b.tr[2 * o - 1]);
+  } else {
+    b.id = 0;
+#pragma unroll
+    for (int o = 0; o < 2 * MO; ++o) b.tr[o] = 0.f;
+  }
+}
+
+// Step t's shared entries: the id and (cos, sin) of orders 0 .. MO from lane `from`.
+template <int MO>
+__device__ __forceinline__ int take_ids(const IdBatch<MO>& b, int from, float (&cs)[MO + 1], float (&sn)[MO + 1]) {
+  cs[0] = 1.f;
+  sn[0] = 0.f;
+#pragma unroll
+  for (int o = 1; o <= MO; ++o) {
+    cs[o] = __shfl(b.tr[2 * o - 2], from, kWave);
+    sn[o] = __shfl(b.tr[2 * o - 1], from, kWave);
+  }
+  return __shfl(b.id, from, kWave);
+}
+
+template <typename T, int NCH, uint32_t ORD, bool B16, int S>
+__global__ __launch_bounds__(256) void softmax_backward_source_batched(SmArgs<T> a) {
+  static_assert(ORD != 0 && std::is_same<T, float>::value, "compiled-in orders, float arithmetic");
+  constexpr int MO = max_order_of(ORD), SB = kWave / S;
+  const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.src_ptr, a.n_nodes, kWavesPerBlock);
+  const int lane = threadIdx.x & 63;
+  const int64_t j = blk * kWavesPerBlock + (threadIdx.x >> 6);
+  if (j >= a.n_nodes) return;
+  const int H = kWave / S;
+  const int h = lane & (H - 1), s = lane / H;
+  const int64_t g0 = a.src_ptr[j], g1 = a.src_ptr[j + 1];
+
+  int64_t off[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) off[c] = a.C.base[c] + h * a.C.stride[c];
+  const auto qrows = rows_of<T, B16, false>(a);
+  float acc[NCH * 4];
+#pragma unroll
+  for (int u = 0; u < NCH * 4; ++u) acc[u] = 0.f;
+  IdBatch<MO> cur, nxt;
+  load_ids<MO>(cur, g0 + lane, g1, a.target_s, a.transport_s, a.orders);
+  for (int64_t base = g0; base < g1; base += kWave) {
+    if (base + kWave < g1)
+      load_ids<MO>(nxt, base + kWave + lane, g1, a.target_s, a.transport_s, a.orders);
+#pragma unroll
+    for (int t = 0; t < SB; ++t) {
+      if (base + t * S >= g1) break;
+      const int from = t * S + s;
+      const int64_t g = base + from;
+      const bool live = g < g1;
+      float cs[MO + 1], sn[MO + 1];
+      const int ti = take_ids<MO>(cur, from, cs, sn);
+      const float ds = live ? a.ds[g * H + h] : 0.f;
+      Quad<float> qq[NCH];
+      const auto r = qrows + (int64_t)ti * a.D;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) qq[c] = row4<float>(r + off[c]);
+      if (live) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const int o = chunk_order<ORD>(a.C, c);
+          if (o == 0) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * qq[c].v[v];
+          } else {
+            const float cr = cs[o], ci = sn[o];
+            // conj(tau) q = (c q0 + s q1, c q1 - s q0)
+            acc[4 * c + 0] += ds * (cr * qq[c].v[0] + ci * qq[c].v[1]);
+            acc[4 * c + 1] += ds * (cr * qq[c].v[1] - ci * qq[c].v[0]);
+            acc[4 * c + 2] += ds * (cr * qq[c].v[2] + ci * qq[c].v[3]);
+            acc[4 * c + 3] += ds * (cr * qq[c].v[3] - ci * qq[c].v[2]);
+          }
+        }
+      }
+    }
+    cur = nxt;
+  }
+#pragma unroll
+  for (int u = 0; u < NCH * 4; ++u) acc[u] = group_sum_pow2(acc[u], H);
+  if (s == 0) {
+    float* dkj = a.dk + j * a.D;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) st4(dkj + off[c], &acc[4 * c]);
+  }
+}
+
 // ------------------------------------------------------------- generic path
 // Any descriptor within the bounds: lanes (slot, head) for the scores, lanes
 // over flat columns with a serial edge walk for dq and dk.
@@ -674,8 +911,52 @@ __global__ __launch_bounds__(256) void softmax_backward_source_generic(SmArgs<T>
 
 enum class Kind { Forward, BackwardTarget, BackwardSource };
 
+// GM_SOFTMAX_BATCHED=0 keeps the per-step entry loads.
+inline bool batched_kernels() {
+  static const bool on = [] {
+    const char* v = std::getenv("GM_SOFTMAX_BATCHED");
+    return v == nullptr || v[0] != '0';
+  }();
+  return on;
+}
+
+// The batched forward and per-source kernels for compiled-in orders (float
+// arithmetic, S = 64 / H slots of 4 to 32); false when they do not serve the
+// call.
+template <typename T, int NCH, uint32_t ORD, bool B16, int S>
+void launch_batched_s(Kind kind, const SmArgs<T>& a, dim3 grid, hipStream_t stream) {
+  switch (kind) {
+    case Kind::Forward:
+      hipLaunchKernelGGL((softmax_forward_batched<T, NCH, ORD, B16, S>), grid, dim3(256), 0, stream, a);
+      break;
+    case Kind::BackwardSource:
+      hipLaunchKernelGGL((softmax_backward_source_batched<T, NCH, ORD, B16, S>), grid, dim3(256), 0, stream, a);
+      break;
+    default:
+      break;
+  }
+}
+
+template <typename T, int NCH, uint32_t ORD, bool B16>
+bool launch_batched(Kind kind, const SmArgs<T>& a, dim3 grid, hipStream_t stream) {
+  if (kind == Kind::BackwardTarget) return false;
+  if constexpr (ORD != 0 && std::is_same<T, float>::value) {
+    switch (a.S) {
+      case 4: launch_batched_s<T, NCH, ORD, B16, 4>(kind, a, grid, stream); return true;
+      case 8: launch_batched_s<T, NCH, ORD, B16, 8>(kind, a, grid, stream); return true;
+      case 16: launch_batched_s<T, NCH, ORD, B16, 16>(kind, a, grid, stream); return true;
+      case 32: launch_batched_s<T, NCH, ORD, B16, 32>(kind, a, grid, stream); return true;
+      default: return false;
+    }
+  }
+  return false;
+}
+
 template <typename T, int NCH, uint32_t ORD = 0>
 void launch_fast_n(Kind kind, const SmArgs<T>& a, dim3 grid, hipStream_t stream) {
+  if (batched_kernels() && (a.qb != nullptr ? launch_batched<T, NCH, ORD, true>(kind, a, grid, stream)
+                                            : launch_batched<T, NCH, ORD, false>(kind, a, grid, stream)))
+    return;
   if (a.qb != nullptr) {
     if constexpr (std::is_same<T, float>::value) {
       switch (kind) {
