@@ -317,11 +317,16 @@ constexpr int kAggStep = 4;  // edges a step: 55 VGPRs, eight waves a SIMD (eigh
 // One wave per target, lane l owning the 16-byte pieces l, l + 64, ...,
 // l + 64 (P - 1) of the target's H d_out outputs (piece o: row head o / q4,
 // columns 4 (o % q4) ..).  The rows are read in the CSR's edge order, so the
-// sums are each head's sums in that order.
+// sums are each head's sums in that order.  The target is wave-uniform, so the
+// row indices are scalar loads; with Ha <= 16 weight columns the weights of EW
+// edges (64 / Ha rounded down to whole steps) come in one vector load (lane
+// u Ha + h: edge u, column h) and reach the lanes that use them by lane
+// shuffles, so an edge costs its row pieces' vector load alone.
+
 template <int P>
 __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a) {
   const int64_t i = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_targets, kWavesPerBlock) * kWavesPerBlock +
-                    (threadIdx.x >> 6);
+                    __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (i >= a.n_targets) return;
   const int q4 = a.d_out / 4, W4 = a.H * q4, Ha = a.H / a.split;
@@ -340,6 +345,14 @@ __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a
   floatx4 s[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) s[p] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // the weights of edges eb .. eb + EW - 1: lane u Ha + h holds edge eb + u's column h
+  const int EW = Ha <= 16 ? kWave / Ha / kAggStep * kAggStep : 0;
+  auto load_w = [&](int64_t eb) {
+    const int64_t k = eb * Ha + lane;
+    return lane < EW * Ha && k < e1 * Ha ? a.alpha[k] : 0.f;
+  };
+  float wb = EW ? load_w(e0) : 0.f;
+  int in_batch = 0;  // the step's first edge within its weight batch
   // the next batch's row indices are requested behind this batch's rows, so each
   // batch waits for one round trip rather than an index load and then the rows
   int64_t r[kAggStep];
@@ -353,13 +366,23 @@ __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         const bool in = live[p] && e + u < e1;
-        w[u][p] = in ? a.alpha[(e + u) * Ha + ha[p]] : 0.f;
+        if (EW) {
+          w[u][p] = __shfl(wb, (in_batch + u) * Ha + ha[p], kWave);
+          if (!in) w[u][p] = 0.f;
+        } else {
+          w[u][p] = in ? a.alpha[(e + u) * Ha + ha[p]] : 0.f;
+        }
         v[u][p] = in ? *reinterpret_cast<const floatx4*>(base[p] + r[u] * a.d_out) : floatx4{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
     for (int u = 0; u < kAggStep; ++u) {
       const int64_t n = e + kAggStep + u;
       r[u] = n < e1 ? a.inv[n] : 0;
+    }
+    in_batch += kAggStep;
+    if (in_batch == EW) {
+      in_batch = 0;
+      wb = load_w(e + kAggStep);
     }
 #pragma unroll
     for (int u = 0; u < kAggStep; ++u)
