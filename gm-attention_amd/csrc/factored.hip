@@ -597,7 +597,7 @@ __global__ __launch_bounds__(64) void factored_backward_kernel(FactArgs<T> a) {
 
 
 constexpr int kMT = 16;  // edges per MFMA tile
-constexpr int kHsStride = 16;  // floats per edge row of the fused trunk's LDS tile
+constexpr int kHsStride = 20;  // floats per edge row of the backward's h tile in LDS: 16 features + 4 (no bank shared by a read's lanes)
 
 // The MFMA kernels run one wave per workgroup, and a wave's LDS operations
 // execute in order, so handing LDS data between its lanes needs only a
@@ -1864,7 +1864,7 @@ factored_forward_lanes(FactArgs<float> a) {
 
 template <class P>
 struct BwdTile {
-  floatx4 h;        // h(edge 4 q + i)[m], i < 4 (read; zero under the fused trunk)
+  floatx4 h;        // h(edge m)[4 q .. 4 q + 3] (read; zero under the fused trunk)
   PhaseRegs<P> ph;  // as in the forward
   float rho, w;     // edge m (rho: runtime slots or the fused trunk)
   int64_t tgt;      // runtime slots: the target of edge m
@@ -1878,13 +1878,8 @@ __device__ __forceinline__ BwdTile<P> load_bwd(__amdgpu_buffer_rsrc_t h_r, __amd
                                                __amdgpu_buffer_rsrc_t t_r, int tb, int m, int q, bool fused,
                                                __amdgpu_buffer_rsrc_t dh_r, __amdgpu_buffer_rsrc_t dw_r, bool acc) {
   BwdTile<P> t;
-  if (fused) {
-    t.h = floatx4{0.f, 0.f, 0.f, 0.f};
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t.h[i] = bload1(h_r, ((tb + 4 * q + i) * 16 + m) * 4);
-  }
   const int e = tb + m;
+  t.h = fused ? floatx4{0.f, 0.f, 0.f, 0.f} : bload4(h_r, (e * 16 + 4 * q) * 4);
   if constexpr (P::kStatic) {
     t.ph.ph = bload4(ph_r, e * 16);
     t.tgt = 0;
@@ -1950,13 +1945,12 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
                                               int d_out, int ng, int tb, int m, int q, const TrunkLane& tl,
                                               bool fused) {
   const int row = (tb + m) * d_out;
-  // the fused trunk: edge m's features 4 q .. 4 q + 3 here, handed to the dZ operand's
-  // layout (feature m of edges 4 q + i) through Hs with the W transpose below
+  // edge m's features 4 q .. 4 q + 3 (read as one 16-byte piece, or the fused trunk's),
+  // handed to the dZ operand's layout (feature m of edges 4 q + i) through Hs with the
+  // W transpose below
   floatx4 pre;
-  if (fused) {
-    const floatx4 hf = trunk_features(a, tl, q, cur.rho, pre);
-    *reinterpret_cast<floatx4*>(Hs + m * kHsStride + 4 * q) = hf;
-  }
+  const floatx4 hf = fused ? trunk_features(a, tl, q, cur.rho, pre) : cur.h;
+  *reinterpret_cast<floatx4*>(Hs + m * kHsStride + 4 * q) = hf;
   float wv[NT][4];
   float dwp = 0.f;  // this lane's share of dweights(edge m)
   if constexpr (kHorner<P>) {
@@ -2045,11 +2039,9 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
 #pragma unroll
     for (int r = 0; r < 4; ++r) Sh[(16 * nt + 4 * q + r) * kWtStride + m] = wv[nt][r];
   wave_sync();
-  floatx4 hb = cur.h;
-  if (fused) {
+  floatx4 hb;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hb[i] = Hs[(4 * q + i) * kHsStride + m];
-  }
+  for (int i = 0; i < 4; ++i) hb[i] = Hs[(4 * q + i) * kHsStride + m];
   // dZ_t,c += sum_e h_t(e) W(e)_c over edges 4 q' + i; the t = 0 column sums W
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -2072,7 +2064,7 @@ factored_backward_lanes(FactArgs<float> a) {
   __shared__ __align__(16) float Gt[P::kStatic ? 4 : kMT * (GM_FACT_MAX_OUT + 4)];
   __shared__ __align__(16) uint8_t colslot[128];
   __shared__ int64_t Tg[P::kStatic ? 1 : kMT];
-  __shared__ __align__(16) float Hs[kMT * kHsStride];  // the fused trunk's features, edge-major
+  __shared__ __align__(16) float Hs[kMT * kHsStride];  // the tile's trunk features, edge-major
   const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
   const int d_out = P::kStatic ? P::kDout : a.d_out;
   const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_spread_block(blockIdx.x, gridDim.x);
