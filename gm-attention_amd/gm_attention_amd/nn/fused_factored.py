@@ -694,12 +694,13 @@ def _heads_mixing_from(kernels: list[Any], hp: HeadsPlan, params: list[list[Tens
 _MIXING_MAPS: OrderedDict = OrderedDict()
 
 
-def _mixing_maps(kernels: list[Any], hp: HeadsPlan, split: int = 1) -> list[tuple[Tensor, Tensor]]:
-    """Per input frequency, (index, sign) with ``M_n = sign * flat[index]``,
-    ``flat`` the heads' readout parameters concatenated (``readout_parameters``
-    order, head by head): found once by running the construction on the
-    parameters' positions (+1) as float64 values, which it only moves and
-    negates."""
+def _mixing_maps(kernels: list[Any], hp: HeadsPlan, split: int = 1) -> dict:
+    """``{"maps": [(index, sign) per input frequency]}`` with ``M_n = sign *
+    flat[index]``, ``flat`` the heads' readout parameters concatenated
+    (``readout_parameters`` order, head by head): found once by running the
+    construction on the parameters' positions (+1) as float64 values, which it
+    only moves and negates.  :class:`_SignedGather` keeps its gradient plan in
+    the same dictionary."""
     shapes = tuple(tuple(None if p is None else tuple(p.shape) for p in k.readout_parameters()) for k in kernels)
     key = (tuple(id(k) for k in kernels), shapes, split)
     hit = _MIXING_MAPS.get(key)
@@ -720,10 +721,63 @@ def _mixing_maps(kernels: list[Any], hp: HeadsPlan, split: int = 1) -> list[tupl
     for m in _heads_mixing_from(kernels, hp, ids, split):
         index = (m.abs().round().long() - 1).clamp_min(0)
         maps.append((index.to(device), torch.sign(m).to(device)))
+    maps = dict(maps=maps)  # the gather's gradient plan joins it on the first backward
     _MIXING_MAPS[key] = maps
     while len(_MIXING_MAPS) > 16:
         _MIXING_MAPS.popitem(last=False)
     return maps
+
+
+class _SignedGather(torch.autograd.Function):
+    """``[flat[index] * sign for each map]`` with a gradient that sums each
+    parameter's uses in a fixed order, prepared once per set of maps: the
+    maps' positions sorted by the parameter they read (stable, so a
+    parameter's uses keep their order), then per parameter its uses' values
+    added in that order -- as up to kMaxUses padded columns (the heads' maps
+    use a parameter at most twice), else one segment sum.  (Autograd's own
+    gradient of the indexing sorts the indices on every call.)"""
+
+    kMaxUses = 16
+
+    @staticmethod
+    def forward(ctx: Any, flat: Tensor, plan: dict, *maps: tuple) -> tuple:
+        ctx.plan = plan
+        ctx.shapes = [index.shape for index, _ in plan["maps"]]
+        ctx.n = flat.numel()
+        return tuple(flat.index_select(0, index.reshape(-1)).reshape(index.shape) * sign.to(flat.dtype)
+                     for index, sign in plan["maps"])
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx: Any, *grads: Tensor) -> tuple:
+        plan = ctx.plan
+        if "order" not in plan:
+            index = torch.cat([i.reshape(-1) for i, _ in plan["maps"]])
+            plan["sign"] = torch.cat([s.reshape(-1) for _, s in plan["maps"]])
+            plan["order"] = torch.argsort(index, stable=True)
+            counts = torch.bincount(index, minlength=ctx.n)
+            plan["offsets"] = torch.cat([counts.new_zeros(1), torch.cumsum(counts, 0)])
+            uses = int(counts.max()) if counts.numel() else 0
+            if uses <= _SignedGather.kMaxUses:
+                # column j: each parameter's j-th use (its position), or the appended zero
+                total = index.numel()
+                srt = index.index_select(0, plan["order"])
+                rank = torch.arange(total, device=index.device) - plan["offsets"].index_select(0, srt)
+                cols = torch.full((max(uses, 1), ctx.n), total, dtype=torch.int64, device=index.device)
+                cols[rank, srt] = plan["order"]
+                plan["cols"] = cols
+        g = torch.cat([(gi if gi is not None else torch.zeros(sh, dtype=plan["sign"].dtype, device=plan["sign"].device))
+                       .reshape(-1) for gi, sh in zip(grads, ctx.shapes, strict=True)])
+        vals = g * plan["sign"].to(g.dtype)
+        if "cols" in plan:
+            vals = torch.cat([vals, vals.new_zeros(1)])
+            cols = plan["cols"]
+            dflat = vals.index_select(0, cols[0])
+            for j in range(1, cols.shape[0]):
+                dflat = dflat + vals.index_select(0, cols[j])
+        else:
+            dflat = torch.segment_reduce(vals.index_select(0, plan["order"]), "sum", offsets=plan["offsets"], axis=0)
+        return (dflat, None)
 
 
 def heads_mixing(kernels: list[Any], hp: HeadsPlan, split: int = 1) -> list[Tensor]:
@@ -735,9 +789,9 @@ def heads_mixing(kernels: list[Any], hp: HeadsPlan, split: int = 1) -> list[Tens
     kernels, differentiable) rather than a per-head, per-block build.  With
     ``split > 1``, ``hp`` is the shares' plan and the columns run over
     ``H * split`` shares."""
-    maps = _mixing_maps(kernels, hp, split)
+    plan = _mixing_maps(kernels, hp, split)
     flat = torch.cat([p.reshape(-1) for k in kernels for p in k.readout_parameters() if p is not None])
-    return [flat[index] * sign.to(flat.dtype) for index, sign in maps]
+    return list(_SignedGather.apply(flat, plan))
 
 
 def node_vectors(x: SO2FeatureField, hp: HeadsPlan) -> list[Tensor]:
