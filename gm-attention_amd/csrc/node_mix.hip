@@ -523,11 +523,29 @@ __device__ __forceinline__ void store_planes(uint16_t* plane0, uint16_t* plane1,
   *reinterpret_cast<uint2*>(plane2 + at) = make_uint2(sp.lo[0], sp.lo[1]);
 }
 
+// Four values' pieces as the three B operands themselves, one 16-byte record
+// each ([hi, hi], [mid, mid], [lo, hi] slot pairs): a wave then reads an
+// operand straight into its registers instead of assembling it from planes.
+__device__ __forceinline__ void store_operands(uint4* rec, float4 x) {
+  const Split4 sp = split4(x.x, x.y, x.z, x.w);
+  rec[0] = make_uint4(sp.hi[0], sp.hi[1], sp.hi[0], sp.hi[1]);
+  rec[1] = make_uint4(sp.mid[0], sp.mid[1], sp.mid[0], sp.mid[1]);
+  rec[2] = make_uint4(sp.lo[0], sp.lo[1], sp.hi[0], sp.hi[1]);
+}
+
+__device__ __forceinline__ SplitB load_operands(const uint4* rec) {
+  const uint4 hh = rec[0], mm = rec[1], lh = rec[2];
+  return SplitB{u32x4{hh.x, hh.y, hh.z, hh.w}, u32x4{mm.x, mm.y, mm.z, mm.w}, u32x4{lh.x, lh.y, lh.z, lh.w}};
+}
+
 // Forward: wave wv of workgroup x owns columns x * 64 CT + 16 CT wv + 16 j + c
 // (j < CT); the pieces of M at those columns are split once per wave and held
-// in registers; each 64-row tile of v is split once per workgroup into three
-// bf16 planes in LDS (row stride W + 4 halfwords: a 16-lane 8-byte read covers
-// 32 banks once), from which every wave assembles its B operands.
+// in registers; each 64-row tile of v is split once per workgroup into LDS, from
+// which every wave takes its B operands: for 64 reals as the operands
+// themselves (48 bytes a four-value group, rows of W / 4 + 1 groups so neither
+// the staging writes nor a 16-lane read meet in a bank), for the other widths
+// as three bf16 planes (row stride W + 4 halfwords: a 16-lane 8-byte read
+// covers 32 banks once) assembled into operands by each wave.
 template <int W, typename V = float>
 __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __restrict__ v, int64_t ldv,
                                                                    const float* __restrict__ M, int64_t N, int w,
@@ -537,7 +555,10 @@ __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __re
   constexpr int LDP = W + 4;
   constexpr int QUADS = 64 * W / 4;
   constexpr int PER = (QUADS + kThreads - 1) / kThreads;
-  __shared__ __align__(16) uint16_t vp[3][64 * LDP];
+  constexpr bool OPS = W == 64;       // operands staged as records (w = 64: 3.39 -> 3.32 ms at NS; w = 32 slower)
+  constexpr int GP = W / 4 + 1;       // record groups a staged row
+  __shared__ __align__(16) uint16_t vp[OPS ? 1 : 3][OPS ? 8 : 64 * LDP];
+  __shared__ __align__(16) uint4 vr[OPS ? 64 * GP * 3 : 1];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, c = lane & 15, q = lane >> 4;
   const int64_t col0 = (int64_t)blockIdx.x * (64 * CT) + 16 * CT * wv;
   SplitA ma[KC][CT];
@@ -571,7 +592,12 @@ __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __re
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
       const int idx = threadIdx.x + p * kThreads;
-      if (idx < QUADS) store_planes(vp[0], vp[1], vp[2], (idx / (W / 4)) * LDP + 4 * (idx % (W / 4)), pre[p]);
+      if (idx < QUADS) {
+        if constexpr (OPS)
+          store_operands(&vr[((idx / (W / 4)) * GP + idx % (W / 4)) * 3], pre[p]);
+        else
+          store_planes(vp[0], vp[1], vp[2], (idx / (W / 4)) * LDP + 4 * (idx % (W / 4)), pre[p]);
+      }
     }
     __syncthreads();
     if (tile + gridDim.y < n_tiles) fetch(tile + gridDim.y);
@@ -583,10 +609,14 @@ __global__ __launch_bounds__(kThreads) void node_mix_forward_split(const V* __re
       for (int j = 0; j < CT; ++j) acc[j] = kZero4;
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        const int at = (16 * rt + c) * LDP + 16 * kc + 4 * q;
-        const SplitB b = split_b_planes(*reinterpret_cast<const uint2*>(&vp[0][at]),
-                                        *reinterpret_cast<const uint2*>(&vp[1][at]),
-                                        *reinterpret_cast<const uint2*>(&vp[2][at]));
+        SplitB b;
+        if constexpr (OPS) {
+          b = load_operands(&vr[((16 * rt + c) * GP + 4 * kc + q) * 3]);
+        } else {
+          const int at = (16 * rt + c) * LDP + 16 * kc + 4 * q;
+          b = split_b_planes(*reinterpret_cast<const uint2*>(&vp[0][at]), *reinterpret_cast<const uint2*>(&vp[1][at]),
+                             *reinterpret_cast<const uint2*>(&vp[2][at]));
+        }
 #pragma unroll
         for (int j = 0; j < CT; ++j) acc[j] = mfma_split(ma[kc][j], b, acc[j]);
       }
