@@ -376,10 +376,16 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
 // not bytes.  Same arithmetic and order of operations as softmax_forward_fast.
 template <int MO>
 struct EdgeBatch {
-  int src;            // source id (node ids fit 31 bits)
+  int64_t src;        // source id
   float bm;           // bias, or -inf outside the window and past the row
   float tr[2 * MO];   // (cos, sin) of orders 1 .. MO
 };
+
+// A 64-bit value of lane `from` (two 32-bit shuffles).
+__device__ __forceinline__ int64_t shfl64(int64_t v, int from) {
+  const int lo = __shfl((int)(uint32_t)v, from, kWave), hi = __shfl((int)(v >> 32), from, kWave);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
 
 template <typename T, int NCH, uint32_t ORD, bool B16, int S>
 __global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
@@ -407,7 +413,7 @@ __global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
   auto load_batch = [&](int64_t base, EdgeBatch<MO>& b) {
     const int64_t e = base + lane;
     if (e < e1) {
-      b.src = (int)a.source[e];
+      b.src = a.source[e];
       b.bm = a.inside[e] ? a.bias[e] : neg_inf<float>();
       const float* tr = a.transport + e * a.orders * 2;
 #pragma unroll
@@ -423,9 +429,9 @@ __global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
   // score of step t of batch b (edge base + t S + s; -inf when excluded or past the row)
   auto score = [&](const EdgeBatch<MO>& b, int t) {
     const int from = t * S + s;
-    const int j = __shfl(b.src, from, kWave);
+    const int64_t j = shfl64(b.src, from);
     Gather<float, NCH> g;
-    const auto r = krows + (int64_t)j * a.D;
+    const auto r = krows + j * a.D;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) g.row[0][c] = row4<float>(r + off[c]);
     const float bm = __shfl(b.bm, from, kWave);
