@@ -25,6 +25,10 @@ CASES = [
     (12, 24, 1, {0: 8, 2: 8}, 2, "hard"),
     (16, 32, 1, {0: 128, 1: 128, 2: 128}, 16, "hard"),  # D = 640, 16 heads of ten chunks
     (12, 24, 1, {0: 64, 1: 64, 2: 64}, 8, "quartic"),
+    # the batched kernels (four copies of frequencies 0..2 a head) at every slot count: S = 16 and 8 above,
+    # S = 4 (sixteen heads) and S = 32 (two heads) here
+    (12, 24, 1, {0: 64, 1: 64, 2: 64}, 16, "hard"),
+    (12, 24, 2, {0: 8, 1: 8, 2: 8}, 2, "quartic"),
     # ... and the generic path (odd segments, three heads; sixteen heads of 20 chunks)
     (12, 24, 1, {0: 6, 1: 4, 2: 2}, 2, "quartic"),
     (10, 20, 1, {0: 3, 1: 3, 2: 3}, 3, "hard"),
@@ -73,7 +77,8 @@ def test_the_library_is_the_path_that_runs(cuda):
     assert "libgmhip.so" in open("/proc/self/maps").read()
 
 
-def test_nodes_without_edges_and_empty_graphs(cuda):
+@pytest.mark.parametrize("field", [{0: 8, 1: 8, 2: 8}, {0: 16, 1: 16, 2: 16}])  # per-step and batched kernels
+def test_nodes_without_edges_and_empty_graphs(field, cuda):
     """A graph where some targets have no edges and some nodes are nobody's
     source: alpha only on real edges, dq and dk exactly zero on the bare rows."""
     t = problems.tables(12, 24, window="hard")
@@ -82,7 +87,7 @@ def test_nodes_without_edges_and_empty_graphs(cuda):
     source = t.source[keep].contiguous()
     row_ptr = torch.zeros(t.n_nodes + 1, dtype=torch.int64)
     row_ptr[1:] = torch.cumsum(torch.bincount(target, minlength=t.n_nodes), 0)
-    p, desc, scale = problems.attention_layout({0: 8, 1: 8, 2: 8}, 4)
+    p, desc, scale = problems.attention_layout(field, 4)
     q = problems.normal((t.n_nodes, p.width), 5).float().to(cuda).requires_grad_(True)
     k = problems.normal((t.n_nodes, p.width), 6).float().to(cuda).requires_grad_(True)
     tr, bias, inside = t.transport[keep].float(), t.bias[keep].float(), t.inside[keep]
