@@ -72,6 +72,7 @@ struct FactArgs {
   int accumulate;  // grouped backward: add dh and dweights into the outputs instead of writing them
   int64_t n_groups;
   int K, wc, wr, C, KP, CP, n_f, n_blocks, d_out;
+  int64_t g_ld;  // grouped backward: floats between consecutive rows of g (d_out unless a strided view)
   int tile;  // backward: edges per LDS tile (a power of two <= 64)
   int real_ooff;  // the real block's output offset (when wr > 0)
   Block desc[GM_FACT_MAX_BLOCKS];
@@ -1134,7 +1135,7 @@ __global__ __launch_bounds__(64) void factored_backward_grouped(FactArgs<float> 
     }
     wave_sync();
     for (int e = q; e < kMT; e += 4) {
-      const float* grow = e < n ? a.g + Tg[e] * d_out : nullptr;
+      const float* grow = e < n ? a.g + Tg[e] * a.g_ld : nullptr;
       for (int o = m; o < d_out; o += kMT) Gt[e * d_out + o] = grow ? grow[o] : 0.f;
     }
     factors_grouped(a, Bd, Ph, Rh, Ft, lane);
@@ -1908,21 +1909,21 @@ struct OutVals {
 };
 
 template <int NT, class P>
-__device__ __forceinline__ void load_outs(OutVals<NT>& v, const float* g, int64_t tgt, __amdgpu_buffer_rsrc_t rows_r,
-                                          int row, int q) {
+__device__ __forceinline__ void load_outs(OutVals<NT>& v, const float* grow, __amdgpu_buffer_rsrc_t rows_r, int row,
+                                          int q) {
 #pragma unroll
   for (int s = 0; s < 2 * NT; ++s) {
     const uint32_t w = P::word(s);
     if (!(w & kSlotActive) || group_start<P>(s) != s) continue;
     if (w & kSlotScalar) {
       const int o = slot_ob(w) + q;
-      v.gr[s] = g[tgt * P::kDout + o];
+      v.gr[s] = grow[o];
       v.gi[s] = 0.f;
       v.rr[s] = bload1(rows_r, (row + o) * 4);
       v.ri[s] = 0.f;
     } else {
       const int o = slot_ob(w) + 2 * q;
-      const float2 gv = *reinterpret_cast<const float2*>(g + tgt * P::kDout + o);
+      const float2 gv = *reinterpret_cast<const float2*>(grow + o);
       const float2 rv = bload2(rows_r, (row + o) * 4);
       v.gr[s] = gv.x;
       v.gi[s] = gv.y;
@@ -2002,7 +2003,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
     if (q == 0) Tg[m] = cur.tgt;
     wave_sync();
     for (int e = q; e < kMT; e += 4) {
-      const float* grow = tb + e < ng ? a.g + Tg[e] * d_out : nullptr;
+      const float* grow = tb + e < ng ? a.g + Tg[e] * a.g_ld : nullptr;
       for (int o = m; o < GS; o += kMT) Gt[e * GS + o] = grow && o < d_out ? grow[o] : 0.f;
     }
     wave_sync();
@@ -2103,8 +2104,8 @@ factored_backward_lanes(FactArgs<float> a) {
   OutVals<P::kStatic ? NT : 1> oa, ob;
   int64_t tn = 0;  // static slots: the targets of the tile two ahead of the current one
   if constexpr (P::kStatic) {
-    load_outs<NT, P>(oa, a.g, t0, sp.rows, m * d_out, q);
-    load_outs<NT, P>(ob, a.g, t1, sp.rows, (kMT + m) * d_out, q);
+    load_outs<NT, P>(oa, a.g + t0 * a.g_ld, sp.rows, m * d_out, q);
+    load_outs<NT, P>(ob, a.g + t1 * a.g_ld, sp.rows, (kMT + m) * d_out, q);
     tn = bload_i64(sp.t, (2 * kMT + m) * 8);
   }
   wave_sync();
@@ -2126,7 +2127,7 @@ factored_backward_lanes(FactArgs<float> a) {
   for (int tb = 0;;) {
     backward_tile<NT, P>(a, ta, oa, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl, fused);
     if constexpr (P::kStatic) {
-      load_outs<NT, P>(oa, a.g, tn, sp.rows, (tb + 2 * kMT + m) * d_out, q);
+      load_outs<NT, P>(oa, a.g + tn * a.g_ld, sp.rows, (tb + 2 * kMT + m) * d_out, q);
       tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
     }
     ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused, sp.dh, sp.dw, acc);
@@ -2134,7 +2135,7 @@ factored_backward_lanes(FactArgs<float> a) {
     if (tb >= ng) break;
     backward_tile<NT, P>(a, tbf, ob, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl, fused);
     if constexpr (P::kStatic) {
-      load_outs<NT, P>(ob, a.g, tn, sp.rows, (tb + 2 * kMT + m) * d_out, q);
+      load_outs<NT, P>(ob, a.g + tn * a.g_ld, sp.rows, (tb + 2 * kMT + m) * d_out, q);
       tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
     }
     tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused, sp.dh, sp.dw, acc);
@@ -2193,6 +2194,7 @@ int prepare(FactArgs<T>& a, const T* h, const Runs<T>& runs, const T* angular, c
   a.n_f = (int)n_f;
   a.n_blocks = (int)n_blocks;
   a.d_out = (int)d_out;
+  a.g_ld = d_out;
   a.n_groups = n_groups;
   // Every packed column belongs to exactly one block, and the blocks sharing
   // an output slot are consecutive, alike in width and kind of output.
@@ -2792,15 +2794,18 @@ extern "C" int gm_factored_forward_grouped_f32(
   return gm::check_launch("factored_forward_grouped");
 }
 
-extern "C" int gm_factored_backward_grouped_f32(
-    const float* g, const int64_t* target_g, const float* weights_g, const float* rows_g, const float* h_g,
-    const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
+extern "C" int gm_factored_backward_grouped_ld_f32(
+    const float* g, int64_t g_ld, const int64_t* target_g, const float* weights_g, const float* rows_g,
+    const float* h_g, const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
     const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
     const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
     int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
     int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
     int64_t trunk_nb, double trunk_width, int64_t accumulate, float* dh_g, float* dweights_g, void* stream) {
   GM_REQUIRE(z && dz && node_stride && t_stride && width, "the mix runs must be host arrays");
+  GM_REQUIRE(g_ld >= d_out, "g_ld must be at least d_out");
+  GM_REQUIRE(g_ld == d_out || (g_ld % 2 == 0 && gm::aligned(g, 8)),
+             "strided gradient rows need an even row stride and 8-byte aligned rows");
   const gm::Runs<float> runs{z, dz, node_stride, t_stride, width, n_runs};
   gm::FactArgs<float> a;
   const gm::TrunkParams trunk{trunk_w, trunk_b, trunk_centers, trunk_nb, trunk_width};
@@ -2812,6 +2817,7 @@ extern "C" int gm_factored_backward_grouped_f32(
              "g, target_g, weights_g, rows_g, dh_g and dweights_g must be device pointers");
   for (int r = 0; r < a.n_seg; ++r) GM_REQUIRE(a.seg[r].dz != nullptr, "every mix gradient run must be a device pointer");
   a.g = g;
+  a.g_ld = g_ld;
   a.group_order = group_order;
   GM_REQUIRE(zw_g == nullptr || gm::aligned(zw_g, 16), "zw_g must be a 16-byte aligned device pointer (or null)");
   a.zw_g = zw_g;
@@ -2824,6 +2830,21 @@ extern "C" int gm_factored_backward_grouped_f32(
   GM_REQUIRE(!(a.accumulate && trunk_w), "the fused trunk's backward writes dh_g and dweights_g (no accumulate)");
   gm::launch_grouped(false, a, (hipStream_t)stream);
   return gm::check_launch("factored_backward_grouped");
+}
+
+extern "C" int gm_factored_backward_grouped_f32(
+    const float* g, const int64_t* target_g, const float* weights_g, const float* rows_g, const float* h_g,
+    const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
+    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
+    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+    int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
+    int64_t trunk_nb, double trunk_width, int64_t accumulate, float* dh_g, float* dweights_g, void* stream) {
+  return gm_factored_backward_grouped_ld_f32(g, d_out, target_g, weights_g, rows_g, h_g, z, dz, node_stride, t_stride,
+                                             width, n_runs, phase_g, rho_g, zw_g, desc, group_ptr, group_source,
+                                             group_order, n_nodes, n_edges, n_groups, K, wc, wr, pa, pt, n_blocks,
+                                             d_out, trunk_w, trunk_b, trunk_centers, trunk_nb, trunk_width, accumulate,
+                                             dh_g, dweights_g, stream);
 }
 
 extern "C" int gm_factored_aggregate_gather_f32(const float* rows, const int64_t* inv, const float* weights,

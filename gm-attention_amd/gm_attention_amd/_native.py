@@ -69,6 +69,8 @@ SIGNATURES_F32 = {
                                         + [_P, _P]),
     "gm_factored_backward_grouped_f32": (ctypes.c_int, [_P] * 10 + [_I] + [_P] * 7 + [_I] * 10 + [_P] * 3 + [_I, _D]
                                          + [_I] + [_P] * 3),
+    "gm_factored_backward_grouped_ld_f32": (ctypes.c_int, [_P, _I] + [_P] * 9 + [_I] + [_P] * 7 + [_I] * 10
+                                            + [_P] * 3 + [_I, _D] + [_I] + [_P] * 3),
     "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
     "gm_factored_lane_tables": (ctypes.c_int, [_P] + [_I] * 6 + [_P] * 3),
     "gm_factored_aggregate_heads_f32": (ctypes.c_int, [_P] * 4 + [_I] * 5 + [_P, _P]),
@@ -760,7 +762,9 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
                               accumulate: bool = False) -> Tensor:
     """dh (grouping order) into ``dh_g``, the mix gradients into the runs'
     gradient arrays; returns dweights in the grouping's order (into
-    ``dweights`` when given).  With ``trunk`` the kernels evaluate h from
+    ``dweights`` when given).  ``g`` (n_targets, d_out) may be a view with
+    rows further apart (one head of the heads' gradient), read in place.
+    With ``trunk`` the kernels evaluate h from
     ``rho_g`` and ``h_g`` may be None.  ``accumulate``: dh and dweights are
     added to ``dh_g`` and ``dweights`` (which must then be given) instead of
     written."""
@@ -777,7 +781,11 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
         return dweights
     _check_order(group_order, group_source)
     hd = host_desc32(desc)
-    _call("gm_factored_backward_grouped_f32", _ptr(g), _ptr(target_g), _ptr(weights_g), _ptr(rows_g), _ptr(h_g),
+    # g may be one head's columns of a wider gradient array, read in place (rows g_ld floats apart)
+    g_ld = g.stride(0) if g.dim() == 2 and g.stride(1) == 1 else -1
+    if g_ld != g.shape[1] and not (g_ld >= g.shape[1] and g_ld % 2 == 0 and g.data_ptr() % 8 == 0):
+        g, g_ld = g.contiguous(), g.shape[1]
+    _call("gm_factored_backward_grouped_ld_f32", _ptr(g), g_ld, _ptr(target_g), _ptr(weights_g), _ptr(rows_g), _ptr(h_g),
           ctypes.cast(runs.z, ctypes.c_void_p), ctypes.cast(runs.dz, ctypes.c_void_p),
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
           ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),

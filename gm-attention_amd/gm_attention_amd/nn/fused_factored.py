@@ -999,7 +999,7 @@ class FactoredHeadsGrouped(torch.autograd.Function):
             # a head's shares read the same trunk features and weights: the later shares add their gradients
             with torch.profiler.record_function("gm::kernel/pairs_backward"):
                 _native.factored_backward_grouped(
-                    grad[:, v].contiguous(), st.target_g, alpha_gt[head], rows[v], h_g[head], runs,
+                    grad[:, v], st.target_g, alpha_gt[head], rows[v], h_g[head], runs,
                     meta["n_nodes"], st.phase_g, st.rho_g, st.zw_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
                     meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"],
                     dh_g[head], dweights=dalpha_gt[head], accumulate=share > 0)
@@ -1055,7 +1055,7 @@ class FactoredHeadsTrunk(torch.autograd.Function):
             runs = _heads_runs(meta, mixes, head, dmixes)
             with torch.profiler.record_function("gm::kernel/pairs_backward"):
                 _native.factored_backward_grouped(
-                    grad[:, head].contiguous(), st.target_g, alpha_gt[head], rows[head], None, runs, meta["n_nodes"],
+                    grad[:, head], st.target_g, alpha_gt[head], rows[head], None, runs, meta["n_nodes"],
                     st.phase_g, st.rho_g, st.zw_g, st.pa, st.pt, meta["desc"], meta["group_ptr"],
                     meta["group_source"], meta["group_order"], meta["K"], meta["wc"], meta["wr"], dh_g[head],
                     dweights=dalpha_gt[head], trunk=ctx.trunks[head])

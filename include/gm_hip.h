@@ -509,6 +509,23 @@ int gm_factored_backward_grouped_f32(const float* g, const int64_t* target_g, co
                                      const float* trunk_centers, int64_t trunk_nb, double trunk_width,
                                      int64_t accumulate, float* dh_g, float* dweights_g, void* stream);
 
+/* gm_factored_backward_grouped with the gradient rows g[target * g_ld ..
+ * + d_out) read in place from a wider array (one head's columns of the
+ * heads' (n_targets, H, d_out) gradient: g_ld = H d_out, even, rows 8-byte
+ * aligned).  Build-specific, no counterpart in the reference; the entry
+ * above is this one with g_ld = d_out. */
+int gm_factored_backward_grouped_ld_f32(const float* g, int64_t g_ld, const int64_t* target_g, const float* weights_g,
+                                        const float* rows_g, const float* h_g, const float* const* z,
+                                        float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
+                                        const int64_t* width, int64_t n_runs, const float* phase_g,
+                                        const float* rho_g, const float* zw_g, const int32_t* desc,
+                                        const int64_t* group_ptr, const int64_t* group_source,
+                                        const int64_t* group_order, int64_t n_nodes, int64_t n_edges,
+                                        int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+                                        int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b,
+                                        const float* trunk_centers, int64_t trunk_nb, double trunk_width,
+                                        int64_t accumulate, float* dh_g, float* dweights_g, void* stream);
+
 /* gm_factored_aggregate with edge e's row at rows[inv[e]] (rows kept in the
  * grouping's order; inv is the grouping's inverse permutation). */
 int gm_factored_aggregate_gather_f32(const float* rows, const int64_t* inv, const float* weights,

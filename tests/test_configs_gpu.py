@@ -183,3 +183,38 @@ def test_c4_block_in_bfloat16_is_within_2e2(cuda):
             continue
         err = float((g - w).norm()) / float(w.norm())
         assert err <= 2e-2, f"d{k}: bf16 relative error {err:.3e}"
+
+
+def test_grouped_backward_reads_head_columns_in_place(cuda, monkeypatch):
+    """The grouped factored backward reads each head's gradient rows as a view
+    of the heads' (N, H, d_out) gradient (rows H d_out floats apart): every
+    gradient is bit-identical to the call on contiguous copies."""
+    import copy
+
+    from gm_attention_amd import _native
+
+    mhsa, x, edges = mhsa_case({0: 32, 1: 32, 2: 32}, 8, 16, 32, batch=2)
+    gpu = copy.deepcopy(mhsa).to(cuda, torch.float32)
+    e32 = edges.to(cuda, torch.float32)
+    flat = x.float().to(cuda)
+    probe = problems.normal(tuple(flat.shape), 11).to(cuda)
+    seen = []
+    real = _native.factored_backward_grouped
+
+    def spy(g, *args, **kwargs):
+        seen.append(g.is_contiguous())
+        return real(g, *args, **kwargs)
+
+    monkeypatch.setattr(_native, "factored_backward_grouped", spy)
+    out, dx, dp = run_mhsa(gpu, flat, e32, probe, oracle=False)
+    assert seen and not any(seen), "the heads' gradient rows were copied before the call"
+
+    def contiguous(g, *args, **kwargs):
+        return real(g.contiguous(), *args, **kwargs)
+
+    monkeypatch.setattr(_native, "factored_backward_grouped", contiguous)
+    out2, dx2, dp2 = run_mhsa(gpu, flat, e32, probe, oracle=False)
+    assert torch.equal(out, out2) and torch.equal(dx, dx2)
+    assert set(dp) == set(dp2)
+    for name in dp:
+        assert torch.equal(dp[name], dp2[name]), name
