@@ -968,23 +968,34 @@ int launch_dweight(const float* v, int64_t ldv, const float* dmix, int64_t N, in
 constexpr int64_t kScratchFloats = int64_t(1) << 23;
 constexpr int kMaxDevices = 64;
 
-// Each device's address of `scratch`, looked up once with that device current.
+// Each device's address of `scratch`, looked up once with that device current,
+// and an event per device that orders the calls sharing that device's array:
+// each call's stream waits for the previous call's kernels (on whatever stream
+// they ran) before it writes the partials, and the call records the event
+// after its reduction.  The mutex is held from the wait to the record, so calls
+// from several host threads or streams serialise on the GPU instead of racing.
 std::mutex scratch_mutex;
 float* scratch_address[kMaxDevices] = {};
+hipEvent_t scratch_done[kMaxDevices] = {};
 
-int scratch_on_current_device(float** out) {
+int scratch_on_current_device(int* device_out, float** out) {
   int device = -1;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return fail(GM_ERR_LAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(err));
   GM_REQUIRE(device >= 0 && device < kMaxDevices, "the current device index is out of the scratch table's range");
-  std::lock_guard<std::mutex> lock(scratch_mutex);
   if (scratch_address[device] == nullptr) {
     void* address = nullptr;
     err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
     if (err != hipSuccess || address == nullptr)
       return fail(GM_ERR_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(err));
+    hipEvent_t done = nullptr;
+    err = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+    if (err != hipSuccess)
+      return fail(GM_ERR_LAUNCH, std::string("hipEventCreateWithFlags(scratch): ") + hipGetErrorString(err));
+    scratch_done[device] = done;
     scratch_address[device] = static_cast<float*>(address);
   }
+  *device_out = device;
   *out = scratch_address[device];
   return GM_OK;
 }
@@ -1097,13 +1108,31 @@ extern "C" int gm_node_mix_backward_weight_noalloc_f32(const float* v, int64_t l
              "w * C is too large for the no-allocation weight gradient: its partials need " +
                  std::to_string(per_split) + " floats a row split, the scratch holds " +
                  std::to_string(gm::kScratchFloats));
+  const hipStream_t s = (hipStream_t)stream;
+  std::lock_guard<std::mutex> lock(gm::scratch_mutex);
   float* partial = nullptr;
-  rc = gm::scratch_on_current_device(&partial);
+  int device = -1;
+  rc = gm::scratch_on_current_device(&device, &partial);
   if (rc != GM_OK) return rc;
+  // Under stream capture the ordering is the graph's (an event recorded outside
+  // a capture cannot be waited on inside it): replays of the graph and other
+  // calls on that GPU must not overlap.
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  hipError_t err = hipStreamIsCapturing(s, &capture);
+  if (err != hipSuccess) return gm::fail(GM_ERR_LAUNCH, std::string("hipStreamIsCapturing: ") + hipGetErrorString(err));
+  const bool ordered = capture == hipStreamCaptureStatusNone;
+  if (ordered) {
+    err = hipStreamWaitEvent(s, gm::scratch_done[device], 0);
+    if (err != hipSuccess) return gm::fail(GM_ERR_LAUNCH, std::string("hipStreamWaitEvent: ") + hipGetErrorString(err));
+  }
   // as many row splits as the scratch holds (every partial is written in full: nothing to clear)
   int64_t splits = 1, rps = 64;
   gm::weight_splits(N, w, C, gm::kScratchFloats / per_split, splits, rps);
-  return gm::launch_dweight(v, ldv, dmix, N, w, C, splits, rps, partial, dM, (hipStream_t)stream);
+  rc = gm::launch_dweight(v, ldv, dmix, N, w, C, splits, rps, partial, dM, s);
+  if (rc != GM_OK || !ordered) return rc;
+  err = hipEventRecord(gm::scratch_done[device], s);
+  if (err != hipSuccess) return gm::fail(GM_ERR_LAUNCH, std::string("hipEventRecord: ") + hipGetErrorString(err));
+  return GM_OK;
 }
 
 // bfloat16 node vectors (the rows of a bfloat16 field): the split kernels widen

@@ -2,14 +2,15 @@
 
 The drop-in for the reference's ``gm_attention/nn/fused_attention.py``: the
 same switch (``GM_FUSED_ATTENTION``, read at import: ``"0"`` off, ``"1"`` on for
-device tensors, ``"cpu"`` accepted for compatibility), the same ``Plan`` /
+device tensors, ``"cpu"`` on everywhere), the same ``Plan`` /
 ``descriptors`` layout (:74-123), the same per-edge ``Geometry`` constants
 (:126-255), the same eligibility predicates (:258-326) and the same
 autograd Functions ``Softmax`` (:371-397) and ``Depthwise`` (:329-353), so the
 attention and convolution layers call it unchanged.  The arithmetic runs in
-``libgmhip.so`` (``_native.attention()``); there is no CPU driver, so a CPU
-tensor reaching an op itself is an error (the predicates send CPU tensors to
-the eager path first).
+``libgmhip.so`` (``_native.attention()``); there is no CPU driver, so under
+every switch value the predicates send CPU tensors to the eager path (the
+reference's ``"cpu"`` runs its CPU driver of the same function there,
+attention_cpu.cpp:256-261), and a CPU tensor reaching an op itself is an error.
 
 Differences from the reference, all implementation limits rather than
 semantics: no neighbourhood-size bound (the reference declines when
@@ -36,8 +37,8 @@ from torch import Tensor
 from gm_attention_amd import _native
 
 MAX_H, MAX_F, MAX_D, DESC = 16, 8, 1024, 5
-#: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` accepted (no CPU driver in this build: CPU
-#: tensors take the eager path).  The default is ``"1"`` (the reference's is ``"0"``): this build exists
+#: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` on everywhere: device tensors take the HIP
+#: ops and CPU tensors the eager path, this build having no CPU driver (reference :43-60).  The default is ``"1"`` (the reference's is ``"0"``): this build exists
 #: to run the HIP path; a declined call runs ``eager_ops`` as the reference runs its eager layers.
 MODE = os.environ.get("GM_FUSED_ATTENTION", "1")
 
@@ -239,9 +240,9 @@ def geometry(edges: Any, cutoff: float, window: str, dtype: torch.dtype) -> Geom
 
 
 def _device_ok(x: Any) -> bool:
-    if MODE == "0":
-        return False
-    if MODE != "cpu" and x.device.type != "cuda":
+    """Device tensors of the ops' element types under ``"1"`` and ``"cpu"``;
+    CPU tensors never (they run the eager path under every switch value)."""
+    if MODE == "0" or x.device.type != "cuda":
         return False
     return x.dtype in (torch.float32, torch.float64)
 
@@ -250,7 +251,7 @@ def _rows_ok(x: Any, heads: int) -> bool:
     """The scores' rows: the element types of _device_ok, or bfloat16 rows on
     the GPU whose heads the fast kernels serve (a power of two up to 16)."""
     if x.dtype == torch.bfloat16:
-        return MODE not in ("0", "cpu") and x.device.type == "cuda" and heads in (1, 2, 4, 8, 16)
+        return MODE != "0" and x.device.type == "cuda" and heads in (1, 2, 4, 8, 16)
     return _device_ok(x)
 
 

@@ -46,7 +46,8 @@ MAX_MULT = _native.PAIRS_MAX_MULT
 MAX_TRUNK = _native.PAIRS_MAX_TRUNK
 SUPPORTED = tuple(range(1, MAX_MULT + 1))
 
-#: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` accepted (reference :39-40).
+#: ``"0"`` off, ``"1"`` on for device tensors, ``"cpu"`` on everywhere (reference :39-40): device tensors
+#: take the HIP terms, CPU tensors the eager readout (this build has no CPU driver).
 MODE = os.environ.get("GM_FUSED_PAIRS", "1")
 
 #: Edges per block of a readout weight gradient's fixed-order sum.
@@ -120,8 +121,7 @@ def enabled(kernel: Any, x: SO2FeatureField, edges: Any) -> bool:
     """Whether this call takes the fused terms (reference :126-149): the switch
     admits the tensors' device, the dtype is float32/64, the trunk and every
     block side are within 16, and every phase order is tabulated on ``edges``."""
-    on_device = x.device.type == "cuda"
-    if MODE == "0" or (MODE != "cpu" and not on_device) or x.dtype not in (torch.float32, torch.float64):
+    if MODE == "0" or x.device.type != "cuda" or x.dtype not in (torch.float32, torch.float64):
         return False
     head = kernel.complex_head if kernel.complex_head is not None else kernel.real_head
     if head.in_features > MAX_TRUNK:

@@ -39,7 +39,10 @@ from gm_attention_amd.representations import so2
 from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
 
 #: ``GM_FACTORED_KERNEL``: the layers evaluate their value kernels in the factored order
-#: (reference kernels.py:39-46).  This build implements only that order.
+#: (reference kernels.py:39-46).  The default is ``"1"`` (the reference's is ``"0"``, the per-edge
+#: readout): the factored order is the one the north-star shape fits in memory (the readout
+#: materialises (E, 2 b a) coefficients per head); ``"0"`` selects the readout through the fused pair
+#: terms.  Both orders compute the same function to summation order.
 FACTORED = os.environ.get("GM_FACTORED_KERNEL", "1") != "0"
 
 

@@ -609,8 +609,12 @@ int gm_node_mix_backward_weight_f32_bf16(const float* v, int64_t ldv, const uint
  * allocate device memory (code under graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  The partials live in a 32 MiB
  * (2^23-float) device array of the library, one per GPU, held until the
- * process ends; every call on a GPU uses that GPU's array, so calls that
- * overlap on one GPU (different streams, or other host threads) race.  Fails
+ * process ends; every call on a GPU uses that GPU's array.  Calls on one GPU
+ * are ordered by an event per GPU (created with the array's lookup on the
+ * first call): each call's stream waits for the previous call's kernels, on
+ * whatever stream or host thread it came from, and the call records the event
+ * after its own.  Under stream capture that ordering is not applied: replays
+ * of a captured call must not overlap other calls on the same GPU.  Fails
  * with GM_ERR_ARGUMENT when 4 w C (the fp32 kernel of w > 64 under
  * GM_SPLIT_PRODUCTS=0: w C) exceeds 2^23.  Sums in
  * a different split order than the workspace form (same bar, not bitwise). */

@@ -26,6 +26,8 @@ identity gate, gauge equivariance).
 
 from __future__ import annotations
 
+import math
+
 import torch
 from torch import Tensor
 
@@ -290,6 +292,35 @@ def softmax_weights(q: dict[int, Tensor], k: dict[int, Tensor], edges, cutoff: f
     return u / torch.segment_reduce(u, "sum", offsets=edges.row_ptr, axis=0).index_select(0, target)
 
 
+class HeadType:
+    """The oracle's own per-head field type: ``{frequency: multiplicity}`` with
+    the two accessors :func:`linear` reads.  Its dimension counts one real per
+    frequency-0 copy and two (re, im) per copy above (reference
+    representations/field_type.py: a frequency-n copy is a real 2-vector)."""
+
+    def __init__(self, multiplicities: dict[int, int]):
+        self.multiplicities = {int(f): int(m) for f, m in multiplicities.items() if m}
+        self.frequencies = sorted(self.multiplicities)
+        self.dimension = sum(m if f == 0 else 2 * m for f, m in self.multiplicities.items())
+
+    def multiplicity(self, f: int) -> int:
+        return self.multiplicities[f]
+
+
+def head_type(multiplicities: dict[int, int], n_heads: int) -> HeadType:
+    """Each head's type: every frequency's multiplicity divided by the head
+    count (reference attention.py:551-556; the head count must divide each)."""
+    for f, m in multiplicities.items():
+        if m % n_heads:
+            raise ValueError(f"{n_heads} heads do not divide frequency {f}'s {m} copies")
+    return HeadType({f: m // n_heads for f, m in multiplicities.items()})
+
+
+def score_scale(attn: HeadType) -> float:
+    """``S(q, k) = <q, k> / sqrt(dim rho_attn)`` (reference attention.py:216-217)."""
+    return 1.0 / math.sqrt(attn.dimension)
+
+
 def mhsa_forward(mhsa, x: dict[int, Tensor], edges, tolerance: float | None = None,
                  messages: str = "readout") -> dict[int, Tensor]:
     """``SO2MHSA.forward`` (reference attention.py:582-608), head by head
@@ -300,11 +331,14 @@ def mhsa_forward(mhsa, x: dict[int, Tensor], edges, tolerance: float | None = No
     per target; heads concatenated head-major; the output intertwiner."""
     evaluate = {"readout": readout_messages, "factored": factored_messages}[messages]
     fin = mhsa.field_type_in
+    # the per-head type and score scale from the input type and head count alone,
+    # never from the module under test
+    attn = head_type({f: fin.multiplicity(f) for f in fin.frequencies}, len(mhsa.heads))
     outs = []
     for head in mhsa.heads:
-        q = linear(head.query, x, head.field_type_attn)
-        k = linear(head.key, x, head.field_type_attn)
-        alpha = softmax_weights(q, k, edges, head.cutoff, head.window, 1, head._score_scale, tolerance)[:, 0]
+        q = linear(head.query, x, attn)
+        k = linear(head.key, x, attn)
+        alpha = softmax_weights(q, k, edges, head.cutoff, head.window, 1, score_scale(attn), tolerance)[:, 0]
         msgs = evaluate(head.value, x, edges.source_index, edges.distances, edges.angular_phases,
                         edges.transport_phases)
         agg = {f: torch.segment_reduce(alpha.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum", offsets=edges.row_ptr,

@@ -172,13 +172,17 @@ def test_single_head_attention_matches_the_oracle(cuda):
     head = mhsa.heads[0]
     probe = problems.normal((x.shape[0], head.field_type_out.dimension), 3)
 
+    # the head's type and score scale derived by the oracle from the input type and head count
+    fin = mhsa.field_type_in
+    attn = modules.head_type({f: fin.multiplicity(f) for f in fin.frequencies}, len(mhsa.heads))
+
     def run_head(module, flat, eds, oracle):
         xx = SO2FeatureField.from_flat(mhsa.field_type_in, flat.clone().requires_grad_(True))
         module.zero_grad(set_to_none=True)
         if oracle:
-            q = modules.linear(module.query, xx.coefficients, module.field_type_attn)
-            k = modules.linear(module.key, xx.coefficients, module.field_type_attn)
-            alpha = modules.softmax_weights(q, k, eds, module.cutoff, module.window, 1, module._score_scale)[:, 0]
+            q = modules.linear(module.query, xx.coefficients, attn)
+            k = modules.linear(module.key, xx.coefficients, attn)
+            alpha = modules.softmax_weights(q, k, eds, module.cutoff, module.window, 1, modules.score_scale(attn))[:, 0]
             msgs = modules.readout_messages(module.value, xx.coefficients, eds.source_index, eds.distances,
                                             eds.angular_phases, eds.transport_phases)
             out = torch.segment_reduce(alpha.unsqueeze(-1) * modules.flat(msgs), "sum", offsets=eds.row_ptr, axis=0)

@@ -123,3 +123,35 @@ def test_value_kernel_readout_and_depthwise_messages_on_edges():
     want = modules.depthwise_layer_messages(dw, x.coefficients, edges)
     for f in want:
         torch.testing.assert_close(got[f], want[f], rtol=1e-11, atol=1e-12)
+
+
+@pytest.mark.parametrize("readout", [False, True])
+def test_cpu_switch_value_runs_cpu_tensors(monkeypatch, readout):
+    """``GM_FUSED_{ATTENTION,FACTORED,PAIRS}=cpu`` means "on everywhere" in the
+    reference (fused_attention.py:43-60, fused_factored.py:50-51,
+    fused_pairs.py:39-40): CPU tensors must run, not raise.  This build has no
+    CPU driver, so under ``"cpu"`` they take the eager path, in both value
+    orders (``GM_FACTORED_KERNEL``: factored, or the per-edge readout the
+    fused pair terms serve on the GPU)."""
+    from gm_attention_amd.nn import fused_attention, fused_factored, fused_pairs, kernels
+
+    for mod in (fused_attention, fused_factored, fused_pairs):
+        monkeypatch.setattr(mod, "MODE", "cpu")
+    monkeypatch.setattr(kernels, "FACTORED", not readout)
+    disc = problems.discretization(10, 20)
+    ft = SO2FieldType({0: 4, 1: 4, 2: 4})
+    torch.manual_seed(5)
+    mhsa = SO2MHSA(ft, 2, cutoff=disc.coverage_radius, window="hard", batched=True, dtype=D64)
+    flat = problems.normal((disc.n_nodes, ft.dimension), 6)
+    got, want = _run(mhsa, ft, flat, disc.edge_geometry, modules.mhsa_forward)
+    _compare(got, want)
+    for depthwise in (True, False):
+        conv = SO2Convolution(ft, ft, cutoff=disc.coverage_radius, depthwise=depthwise, n_radial_basis=4, dtype=D64)
+        got, want = _run(conv, ft, flat, disc.edge_geometry, modules.conv_forward)
+        _compare(got, want)
+    # the predicates decline CPU tensors under "cpu" and admit device tensors
+    x = SO2FeatureField.from_flat(ft, flat)
+    assert not fused_attention.softmax_enabled(mhsa, flat, disc.edge_geometry)
+    assert not fused_attention.enabled_depthwise(conv, flat, disc.edge_geometry)
+    assert not fused_pairs.enabled(mhsa.heads[0].value, x, disc.edge_geometry)
+    assert fused_factored.declined(mhsa.heads[0].value, x, disc.edge_geometry) != ""

@@ -16,7 +16,11 @@ product:
   ``M + iN`` of frequency n acting on each ``(re, im)`` pair as
   ``[[M, -N], [N, M]]``), on non-square maps with frequencies the other side
   lacks, plus a hand-computed answer; and the dense matrix commutes with
-  every rotation (an intertwiner)."""
+  every rotation (an intertwiner);
+* ``modules.head_type`` / ``modules.score_scale`` (the per-head type and
+  score scale ``mhsa_forward`` derives itself) take hand-computed values at
+  C1's and C2's fields (20 reals a head, 1/sqrt(20)) and on a field whose
+  head width differs from D / H, and the product's heads carry the same."""
 
 import math
 
@@ -213,3 +217,38 @@ def test_linear_known_answer():
     y = modules.linear(lin, x, ft)
     assert float(y[0][0, 0].detach()) == 6.5
     assert y[1][0, 0].detach().tolist() == [-5.0, 10.0]
+
+
+# ---------------------------------------------------------------- head type and score scale
+
+
+@pytest.mark.parametrize("mult, heads, dim, want_types", [
+    ({0: 16, 1: 16, 2: 16}, 4, 20, {0: 4, 1: 4, 2: 4}),   # C1: 16 + 2*16 + 2*16 = 80 reals, 4 heads
+    ({0: 32, 1: 32, 2: 32}, 8, 20, {0: 4, 1: 4, 2: 4}),   # C2 / NS: 160 reals, 8 heads
+    ({0: 8, 2: 4}, 4, 4, {0: 2, 2: 1}),                    # 16 reals, 4 heads: D / H = 4 by luck of 2 + 2*1
+    ({0: 6, 1: 3}, 3, 4, {0: 2, 1: 1}),                    # 12 reals, 3 heads
+    ({0: 4, 1: 8}, 4, 5, {0: 1, 1: 2}),                    # 20 reals, 4 heads: D / H = 5
+    ({1: 4, 2: 2}, 2, 6, {1: 2, 2: 1}),                    # no scalar channel
+])
+def test_head_type_and_score_scale_known_answers(mult, heads, dim, want_types):
+    attn = modules.head_type(mult, heads)
+    assert attn.multiplicities == want_types
+    assert attn.dimension == dim
+    assert modules.score_scale(attn) == pytest.approx(1.0 / math.sqrt(dim), rel=1e-15)
+    # the product (reference attention.py:217, :551-556) carries the same type and scale
+    from gm_attention_amd.nn.attention import SO2MHSA
+
+    mhsa = SO2MHSA(SO2FieldType(mult), heads, cutoff=0.3, batched=True, dtype=D64)
+    for head in mhsa.heads:
+        assert {f: head.field_type_attn.multiplicity(f) for f in head.field_type_attn.frequencies} == want_types
+        assert head._score_scale == pytest.approx(modules.score_scale(attn), rel=1e-15)
+
+
+def test_score_scale_numbers():
+    """The scales as literal numbers, so a dimension counted per copy instead
+    of per real (12 for C2, not 20) or the whole width (160) cannot hide."""
+    c2 = modules.head_type({0: 32, 1: 32, 2: 32}, 8)
+    assert modules.score_scale(c2) == pytest.approx(0.22360679774997896, rel=1e-15)
+    assert modules.score_scale(modules.head_type({0: 16, 1: 16, 2: 16}, 4)) == pytest.approx(0.22360679774997896)
+    with pytest.raises(ValueError):
+        modules.head_type({0: 6, 1: 4}, 4)

@@ -3,8 +3,9 @@
 point gm_node_mix_backward_weight_f32, both called through the C ABI: two
 calls in a row on one GPU, the second smaller, each within fp32 summation
 tolerance of the workspace form (the two sum the row splits in different
-orders) and of a float64 product; and a size beyond the array rejected with
-a message before anything is launched."""
+orders) and of a float64 product; two calls on two streams issued back to
+back (ordered by the library's event, not by the caller); and a size beyond
+the array rejected with a message before anything is launched."""
 
 import ctypes
 
@@ -50,6 +51,32 @@ def test_no_alloc_weight_gradient_matches_the_workspace_form_twice(first, second
         assert not bool(torch.isnan(got).any())
         assert float((got.double().cpu() - want.double().cpu()).abs().max()) <= 2e-6 * scale
         assert float((got.double().cpu() - exact).abs().max()) <= 2e-6 * scale
+
+
+def test_no_alloc_calls_on_two_streams_do_not_race(cuda):
+    """Two calls on two streams, issued with no synchronisation between them:
+    the second stream waits for the first call's kernels before it writes the
+    shared partials, so both results match the workspace form."""
+    lib = _native.library()
+    shapes = [(524288 // 4, 64, 5440), (300000, 64, 4000)]
+    inputs = []
+    for N, w, C in shapes:
+        g = torch.Generator().manual_seed(N + C)
+        inputs.append((torch.randn(N, w, generator=g).to(cuda), torch.randn(N, C, generator=g).to(cuda)))
+    main = torch.cuda.current_stream(cuda)
+    wants = [_workspace_form(lib, v, w, dmix, N, w, C, main.cuda_stream)
+             for (v, dmix), (N, w, C) in zip(inputs, shapes)]
+    outs = [torch.full((w, C), float("nan"), device=cuda) for (N, w, C) in shapes]
+    streams = [torch.cuda.Stream(cuda), torch.cuda.Stream(cuda)]
+    torch.cuda.synchronize()
+    print("no-alloc dM on two streams", flush=True)
+    for s, (v, dmix), (N, w, C), out in zip(streams, inputs, shapes, outs):
+        assert lib.gm_node_mix_backward_weight_noalloc_f32(v.data_ptr(), w, dmix.data_ptr(), N, w, C, out.data_ptr(),
+                                                           s.cuda_stream) == 0, lib.gm_last_error()
+    torch.cuda.synchronize()
+    for got, want in zip(outs, wants):
+        scale = float(want.abs().max())
+        assert float((got - want).abs().max()) <= 2e-6 * scale
 
 
 def test_no_alloc_weight_gradient_rejects_what_the_array_cannot_hold(cuda):
