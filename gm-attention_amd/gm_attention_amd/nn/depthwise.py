@@ -10,7 +10,8 @@ Restates the reference's ``nn/depthwise.py``:
   head of ``sum_n 4 a_n`` outputs laid out per frequency as ``(2, a_n, 2)``
   = (A | B, copy, re/im) (:106-127, 175-191);
 * ``stacked_coefficients`` (:206-238): every kernel's ``(rc, cc)`` readouts of
-  one radial embedding, stacked on a leading kernel axis.
+  one radial embedding on a leading kernel axis, each kernel read out by its
+  own trunk and heads.
 
 The per-edge message form (``SO2DepthwiseKernel.forward`` on edge-shaped
 fields, :147-193) is the eager path (``eager_ops.depthwise_messages``); the
@@ -21,8 +22,6 @@ depthwise op and takes the eager path only for calls the op declines.
 from __future__ import annotations
 
 from collections.abc import Sequence
-from typing import cast
-
 import torch
 from torch import Tensor, nn
 
@@ -78,8 +77,13 @@ class SO2DepthwiseKernel(nn.Module):
                                  f"({self.cutoff:.6g}).")
             self._validated_edge_geometry_ids.add(id(edges))
 
-    def trunk_linears(self) -> list[nn.Linear]:
-        return [m for m in self.radial_trunk if isinstance(m, nn.Linear)]
+    def radial_readouts(self, embedding: Tensor) -> tuple[Tensor | None, Tensor | None]:
+        """The real head's ``(E, a_0)`` and the complex head's ``(E, sum 4 a_n)``
+        outputs on a radial embedding of the edges: the trunk's features once
+        (its ``Linear`` + ``SiLU`` modules in order), then each head's ``Linear``."""
+        features = self.radial_trunk(embedding)
+        return tuple(None if head is None else head(features)  # type: ignore[return-value]
+                     for head in (self.real_head, self.complex_head))
 
     def forward(self, x, edges):
         """One message per edge from the source features gathered to edge shape
@@ -100,38 +104,23 @@ class SO2DepthwiseKernel(nn.Module):
         return f"field_type={self.field_type!r}, cutoff={self.cutoff:.6g}"
 
 
-def _stacked(parameters: Sequence[Tensor | None]) -> Tensor | None:
-    if parameters[0] is None:
-        return None
-    return torch.stack([cast(Tensor, p) for p in parameters])
-
-
-def _linear(hidden: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
-    """``hidden (K, E, in) -> (K, E, out)`` under stacked ``weight (K, out, in)`` and ``bias (K, out)``."""
-    out = torch.bmm(hidden, weight.transpose(1, 2).contiguous())
-    return out if bias is None else out + bias.unsqueeze(1)
-
-
 def stacked_coefficients(kernels: Sequence[SO2DepthwiseKernel], edges) -> tuple[Tensor | None, Tensor | None]:
     """Every kernel's ``rc (K, E, a_0)`` and ``cc (K, E, sum 4 a_n)`` on the
-    edges, through one radial embedding and the kernels' stacked trunks
-    (:206-238); ``None`` for a head the type does not have."""
-    first = kernels[0]
-    first.validate_edges(edges)
-    with torch.profiler.record_function("gm::kernel/radial"):
-        embedding = first.radial_basis(edges.distances)
-        hidden = embedding.unsqueeze(0).expand(len(kernels), -1, -1).contiguous()
-        trunks = [k.trunk_linears() for k in kernels]
-        for layer in range(len(trunks[0])):
-            weight = torch.stack([t[layer].weight for t in trunks])
-            bias = _stacked([t[layer].bias for t in trunks])
-            hidden = torch.nn.functional.silu(_linear(hidden, weight, bias))
-
-    def readout(heads: Sequence[nn.Linear | None]) -> Tensor | None:
-        if heads[0] is None:
-            return None
-        weight = torch.stack([cast(nn.Linear, h).weight for h in heads])
-        bias = _stacked([cast(nn.Linear, h).bias for h in heads])
-        return _linear(hidden, weight, bias)
-
-    return readout([k.real_head for k in kernels]), readout([k.complex_head for k in kernels])
+    edges, kernels on the leading axis (reference :206-238); ``None`` for a
+    head the type does not have.  The kernels of one layer share the radial
+    basis (one cutoff), so the edges' embedding is evaluated once and read
+    out by each kernel's own modules (:meth:`SO2DepthwiseKernel.radial_readouts`);
+    a single kernel's readouts gain the kernel axis as a view."""
+    for kernel in kernels:
+        kernel.validate_edges(edges)
+    with torch.profiler.record_function("gm::depthwise/readouts"):
+        embedding = kernels[0].radial_basis(edges.distances)
+        readouts = [kernel.radial_readouts(embedding) for kernel in kernels]
+    heads = []
+    for which in range(2):
+        parts = [r[which] for r in readouts]
+        if parts[0] is None:
+            heads.append(None)
+        else:
+            heads.append(parts[0].unsqueeze(0) if len(parts) == 1 else torch.stack(parts))
+    return heads[0], heads[1]

@@ -134,3 +134,22 @@ def test_layer_rejects_mismatched_types_and_bad_arguments():
         SO2Convolution(a, a, cutoff=0.3, eps=0.0)
     with pytest.raises(ValueError):
         SO2Convolution(a, a, cutoff=0.3, self_interaction="affine")
+
+
+def test_stacked_coefficients_of_several_kernels_stack_each_kernels_readouts():
+    """Three kernels of one field on one edge set: the stacked readouts are
+    each kernel's own (its trunk and heads), kernel by kernel, and equal the
+    oracle's trunk and heads (``modules._trunk`` and the heads' weights)."""
+    field = {0: 3, 1: 2, 2: 2}
+    kernels = [_depthwise(field, seed=11 + i) for i in range(3)]
+    edges = problems.discretization(10, 20).edge_geometry
+    rc, cc = stacked_coefficients(kernels, edges)
+    assert rc.shape == (3, edges.n_edges, 3) and cc.shape == (3, edges.n_edges, 4 * 2 + 4 * 2)
+    for i, k in enumerate(kernels):
+        alone = stacked_coefficients([k], edges)
+        torch.testing.assert_close(rc[i], alone[0][0], rtol=0, atol=0)
+        torch.testing.assert_close(cc[i], alone[1][0], rtol=0, atol=0)
+        hidden = modules._trunk(k, edges.distances)
+        torch.testing.assert_close(rc[i], hidden @ k.real_head.weight.T + k.real_head.bias, rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(cc[i], hidden @ k.complex_head.weight.T + k.complex_head.bias, rtol=1e-12,
+                                   atol=1e-12)
