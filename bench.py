@@ -15,12 +15,18 @@ neighbourhoods, CSR and per-edge geometry (float64 lattice membership, tables
 in float64) from the grid's nodes and frames resident on the device; its CPU
 baseline is the host builder (KD-tree + exact filter + torch arithmetic).
 
+``--workload c1`` and ``--workload c2`` run BASELINE's attention rows: C1 the
+same layer forward only on the 32x64 grid, batch 1, field {0: 16, 1: 16, 2:
+16}, 4 heads; C2 forward + backward on the 128x256 grid, batch 4, the
+headline's field and heads.
+
 ``--workload block`` runs the C4 configuration: one
 ``SO2TransformerBlock(ffn_multiplier=4)`` (pre-norm: batched 8-head SO2MHSA,
 then the 160 -> 640 -> 160 gated feed-forward), forward + backward with every
-gradient, at 256x512, batch 2, with bfloat16 rows (residual stream, norms,
-gate, feed-forward GEMMs) and float32 parameters; the attention's kernels
-compute in float32.
+gradient, at 256x512, batch 2, with bfloat16 rows and float32 parameters: the
+attention's Q/K projections, scores and node mixes read the bfloat16 rows and
+compute from the node mixes on in float32; the feed-forward (layer norm,
+SO2Linear, gate, SO2Linear, residual) is one bf16-MFMA kernel per direction.
 
 ``--workload encoder`` runs the C5 stage model end to end (``GmSegformer``:
 restrictions 128x256 ({0: 4}) -> 64x128 ({0: 64, 1: 64, 2: 64}) -> 32x64
@@ -28,11 +34,12 @@ restrictions 128x256 ({0: 4}) -> 64x128 ({0: 64, 1: 64, 2: 64}) -> 32x64
 decoder, 13-class head and cross-entropy), batch 8, forward + backward with
 every gradient, float32; ``--workload hops`` times its two restrictions alone.
 
-The default run also measures the other configurations (C3 ``conv``, C4
-``block``, C5 ``encoder`` and the GPU ``geometry`` build), each in a process of
-its own after the headline measurement, and reports their rates, step times
-and roofline objects under ``other_workloads`` in the same JSON line
-(``--no-other-workloads`` skips them).
+The default run also measures the other configurations (C1, C2, C3 ``conv``,
+C4 ``block``, C5 ``encoder`` and the GPU ``geometry`` build), each in a
+process of its own after the headline measurement, and reports their rates,
+step times, roofline objects, op coverage and (C1, C2, C3) CPU baselines under
+``other_workloads`` in the same JSON line (``--no-other-workloads`` skips
+them).
 
 ``--workload softmax`` times the scores-and-softmax op alone (forward +
 backward) on the same shape.  ``--workload conv`` times the depthwise steerable
@@ -40,12 +47,17 @@ convolution layer (``SO2Convolution(depthwise=True, n_radial_basis=4)``,
 forward + backward with every parameter gradient) on the same grid, batch
 and field: the C3 configuration.
 
-Prints one JSON line.  Each fused op is timed live with HIP events on the
-stream it launches on; the roofline entry is the op with the largest share of
-the step, its algorithmic bytes or FLOPs per launch (formulas below) over its
-average launch time.  The CPU baseline is the eager PyTorch restatement of
-the reference's path (oracle/, the factored order) on a bounded sample of the
-same workload on this host's cores, extrapolated per edge.
+Prints one JSON line.  Every native entry point the layers call (the
+softmax, the radial trunk, the node mixes, the factored forward, aggregate
+and backward, the gather/scatter transposes, the depthwise walks, the block's
+pointwise kernels) and the flat projections' GEMMs are timed live with HIP
+events on the stream they launch on, each call's algorithmic bytes and FLOPs
+computed from its arguments; ``ops_coverage`` says how much of the step they
+account for.  The roofline entry is the op with the largest share of the
+step: the larger of its HBM time and its FP32 matrix time over its measured
+time.  The CPU baseline is the eager PyTorch restatement of the reference's
+path (oracle/, the factored order) on a bounded sample of the same workload on
+this host's cores, extrapolated per edge.
 """
 
 from __future__ import annotations
@@ -95,69 +107,250 @@ def cpu_model() -> str:
 
 
 # ---------------------------------------------------------------- algorithmic cost per launch
+#
+# Each native entry point the layers call is timed with HIP events on its
+# stream, and its algorithmic cost is computed from the call's own arguments:
+# every tensor crossing the op boundary read or written once (int64 indices,
+# the rows' element size, transport orders 0..2 as (cos, sin) pairs), and the
+# multiply-adds of the contraction (x2 FLOPs).  An op's roofline is the larger
+# of its HBM time (bytes / 8 TB/s) and its FP32 matrix time (FLOPs / 157.3
+# TFLOP/s) over its measured time.
 
 
-def softmax_cost(E: int, N: int, D: int, H: int) -> dict[str, tuple[float, float]]:
-    """(bytes, flops) of one launch of each softmax entry point: every tensor
-    crossing the op boundary once (int64 indices, fp32 values, transport orders 0..2)."""
-    return {
-        "softmax_forward": (E * (8 + 24 + 4 + 1 + 4 * H) + N * (8 * D + 8), E * 2.0 * D),
-        "softmax_backward": (E * (8 + 24 + 8 * H) + N * (16 * D + 8), E * 4.0 * D),
-    }
+def _es(t) -> int:
+    return t.element_size()
 
 
-def conv_cost(E: int, N: int, D: int, A0: int, W: int) -> dict[str, tuple[float, float]]:
-    """(bytes, flops) of one launch of the depthwise walk at the reference's
-    boundary: per edge the source index, the coefficient rows (A0 + W floats),
-    the transport and angular tables (48 B) and rho and the weight; per node
-    the value row in and the output row out.  The backward also reads the
-    transposed CSR (source order, target) and writes the coefficient
-    gradients; per node it reads the value and upstream rows and writes dv."""
-    return {
-        "conv_forward": (E * (8 + 4 * A0 + 4 * W + 48 + 8) + N * (8 * D + 8), E * 12.0 * D),
-        "conv_backward": (E * (16 + 8 * (A0 + W) + 48 + 8) + N * (12 * D + 16), E * 24.0 * D),
-        "conv_radial_forward": (E * (8 + 48 + 8) + N * (8 * D + 8), E * (2.0 * 17 * (A0 + W) + 12 * D)),
-        "conv_radial_backward": (E * (16 + 48 + 8) + N * (12 * D + 16), E * (6.0 * 17 * (A0 + W) + 24 * D)),
-    }
+def cost_softmax_forward(a, kw, out):
+    q, k, transport, bias, inside, desc, row_ptr, source, H = a[:9]
+    E, N, D = source.shape[0], q.shape[0], q.shape[1]
+    return E * (8 + 24 + 4 + 1 + 4 * H) + N * (2 * D * _es(q) + 8), E * 2.0 * D
 
 
-def factored_cost(E: int, N: int, K: int, C: int, wc: int, d_out: int, H: int) -> dict[str, tuple[float, float]]:
-    """(bytes, flops) of one launch of the grouped factored ops.  Forward (per
-    head): h (K - 1 floats), zw (4 floats) in and the row (d_out floats) out
-    per edge, Z(j) (K C floats) once per node.  Backward (per head): h, zw,
-    weight, target, the row and the target's gradient row in, dh and dweight
-    out per edge; Z(j) in and dZ(j) out per node.  Aggregate (all heads at
-    once): inv, alpha's row and every head's row per edge, the output row per
-    node.  FLOPs: 2 K C per edge forward (the K-long combination of each
-    packed column) plus the block factors, 4 K C backward (dh and dZ)."""
-    z = N * 4 * K * C
-    fwd_edge = 4 * (K - 1) + 16 + 4 * d_out
-    bwd_edge = 4 * (K - 1) + 16 + 4 + 8 + 2 * 4 * d_out + 4 * (K - 1) + 4
-    return {
-        "factored_forward": (E * fwd_edge + z, E * (2.0 * K * C + 8 * wc)),
-        "factored_aggregate": (E * (8 + 4 * H + 4 * H * d_out) + N * 4 * H * d_out, E * 2.0 * H * d_out),
-        "factored_backward_aggregated": (E * bwd_edge + 2 * z, E * (4.0 * K * C + 8 * wc)),
-    }
+def cost_softmax_backward(a, kw, out):
+    dalpha, q, k, transport, bias, inside, desc, row_ptr, source, alpha, H = a[:11]
+    E, N, D = source.shape[0], q.shape[0], q.shape[1]
+    return E * (8 + 24 + 8 * H) + N * (2 * D * _es(q) + 8 * D + 8), E * 4.0 * D
+
+
+def _factored_shape(K, wc, wr):
+    return K, 2 * wc + wr, wc
+
+
+def cost_factored_forward_grouped(a, kw, out):
+    h_g, runs, n_nodes, phase_g, rho_g = a[:5]
+    K, C, wc = _factored_shape(*a[12:15])
+    d_out = a[15]
+    E = rho_g.shape[0]
+    h_bytes = 4 * (K - 1) if h_g is not None else 4
+    return E * (h_bytes + 16 + 4 * d_out) + n_nodes * 4 * K * C, E * (2.0 * K * C + 8 * wc)
+
+
+def cost_factored_backward_grouped(a, kw, out):
+    g, target_g, weights_g, rows_g, h_g, runs, n_nodes, phase_g, rho_g = a[:9]
+    K, C, wc = _factored_shape(*a[16:19])
+    d_out = g.shape[1]
+    E = rho_g.shape[0]
+    h_bytes = 4 * (K - 1) if h_g is not None else 4
+    per_edge = h_bytes + 16 + 4 + 8 + 2 * 4 * d_out + 4 * (K - 1) + 4
+    return E * per_edge + 2 * n_nodes * 4 * K * C, E * (4.0 * K * C + 8 * wc)
+
+
+def cost_factored_forward(a, kw, out):
+    h, zc, zr = a[:3]
+    E, N, K, wc, wr = h.shape[0], zc.shape[0], zc.shape[1], zc.shape[2], zr.shape[2]
+    C, d_out = 2 * wc + wr, a[11]
+    return E * (4 * h.shape[1] + 48 + 4 + 8 + 4 * d_out) + N * 4 * K * C, E * (2.0 * K * C + 8 * wc)
+
+
+def cost_factored_backward_aggregated(a, kw, out):
+    g, target, weights, rows, h, zc, zr = a[:7]
+    E, N, K, wc, wr = h.shape[0], zc.shape[0], zc.shape[1], zc.shape[2], zr.shape[2]
+    C, d_out = 2 * wc + wr, g.shape[1]
+    return (E * (8 + 4 + 4 * d_out + 8 * h.shape[1] + 48 + 4 + 8 + 4 * d_out + 4) + 2 * N * 4 * K * C,
+            E * (4.0 * K * C + 8 * wc))
+
+
+def cost_factored_aggregate(a, kw, out):
+    rows, weights, row_ptr = a[:3]
+    E, d_out = rows.shape
+    return E * (4 * d_out + 4) + (row_ptr.shape[0] - 1) * (4 * d_out + 8), E * 2.0 * d_out
+
+
+def cost_aggregate_heads(a, kw, out):
+    rows, inv, alpha, row_ptr = a[:4]
+    H, E, d_out = rows.shape
+    N = row_ptr.shape[0] - 1
+    return E * (8 + 4 * alpha.shape[1] + 4 * H * d_out) + N * (4 * H * d_out + 8), E * 2.0 * H * d_out
+
+
+def cost_trunk_forward(a, kw, out):
+    rho, weight = a[:2]
+    H, T, B = weight.shape
+    E = rho.shape[0]
+    return E * (4 + 4 * H * T), E * H * (2.0 * T * B + 20 * T)
+
+
+def cost_trunk_backward(a, kw, out):
+    dh, rho, weight = a[:3]
+    H, T, B = weight.shape
+    E = rho.shape[0]
+    return E * (4 + 4 * H * T), E * H * (4.0 * T * B + 30 * T)
+
+
+def cost_node_mix_forward(a, kw, out):
+    v, m = a[:2]
+    (N, w), C = v.shape, m.shape[1]
+    return N * (w * _es(v) + 4 * C) + 4 * w * C, 2.0 * N * w * C
+
+
+def cost_node_mix_backward_input(a, kw, out):
+    dmix, m = a[:2]
+    (N, C), w = dmix.shape, m.shape[0]
+    return N * (4 * C + 4 * w) + 4 * w * C, 2.0 * N * w * C
+
+
+def cost_node_mix_backward_weight(a, kw, out):
+    v, dmix = a[:2]
+    (N, w), C = v.shape, dmix.shape[1]
+    return N * (w * _es(v) + C * _es(dmix)) + 4 * w * C, 2.0 * N * w * C
+
+
+def cost_gather_transpose(a, kw, out):
+    src = a[0]
+    n, width = src.shape
+    return n * (8 + 2 * 4 * width), 0.0
+
+
+def cost_scatter_transpose(a, kw, out):
+    src_t = a[0]
+    width, n = src_t.shape
+    return n * (8 + 2 * 4 * width), 0.0
+
+
+def cost_projection_forward(a, kw, out):
+    ctx, x, m = a[:3]
+    (N, din), dout = x.shape, m.shape[1]
+    return N * (din + dout) * _es(x) + 4 * din * dout, 2.0 * N * din * dout
+
+
+def cost_projection_backward(a, kw, out):
+    ctx, g = a[:2]
+    x, m = ctx.saved_tensors
+    (N, din), dout = x.shape, m.shape[1]
+    return N * (2 * din + dout) * _es(x) + 8 * din * dout, 4.0 * N * din * dout
+
+
+def cost_conv_forward(a, kw, out):
+    v, rc, cc, transport, angular, rho, weights, desc, row_ptr, source, A0, W = a[:12]
+    E, (N, D) = source.shape[0], v.shape
+    return E * (8 + 4 * A0 + 4 * W + 48 + 8) + N * (8 * D + 8), E * 12.0 * D
+
+
+def cost_conv_backward(a, kw, out):
+    g, v, rc, cc = a[:4]
+    source, A0, W = a[10], a[11], a[12]
+    E, (N, D) = source.shape[0], v.shape
+    return E * (16 + 8 * (A0 + W) + 48 + 8) + N * (12 * D + 16), E * 24.0 * D
+
+
+def _radial_width(v, a0):
+    D = v.shape[1]
+    return a0, 4 * (D - a0) // 2
+
+
+def cost_conv_radial_forward(a, kw, out):
+    v, source, a0 = a[0], a[12], a[13]
+    A0, W = _radial_width(v, a0)
+    E, (N, D) = source.shape[0], v.shape
+    return E * (8 + 48 + 8) + N * (8 * D + 8), E * (2.0 * 17 * (A0 + W) + 12 * D)
+
+
+def cost_conv_radial_backward(a, kw, out):
+    g, v, source, a0 = a[0], a[1], a[13], a[15]
+    A0, W = _radial_width(v, a0)
+    E, (N, D) = source.shape[0], v.shape
+    return E * (16 + 48 + 8) + N * (12 * D + 16), E * (6.0 * 17 * (A0 + W) + 24 * D)
+
+
+def cost_layer_norm_forward(a, kw, out):
+    x = a[0]
+    return 2 * x.numel() * _es(x) + 8 * x.shape[0], 0.0
+
+
+def cost_layer_norm_backward(a, kw, out):
+    gy = a[0]
+    return 3 * gy.numel() * _es(gy) + 8 * gy.shape[0], 0.0
+
+
+def cost_gate_forward(a, kw, out):
+    h, pre = a[:2]
+    return (2 * h.numel() + pre.numel()) * _es(h), 0.0
+
+
+def cost_gate_backward(a, kw, out):
+    gy, h, pre = a[:3]
+    return (3 * h.numel() + 2 * pre.numel()) * _es(h), 0.0
+
+
+def _ffn_flops(N, A, B):
+    # per node: LN, the first linear (frequency 0: A x B; frequencies 1, 2: complex 2A x 2B each),
+    # the gate's linear, the second linear back (B x A, 2B x 2A complex)
+    return 2.0 * N * (A * B + 2 * (2 * A) * (2 * B) + 2 * B * B + B * A + 2 * (2 * B) * (2 * A))
+
+
+def cost_ffn_forward(a, kw, out):
+    x, A, B = a[:3]
+    return x.shape[0] * (2 * x.shape[1] * _es(x) + 8), _ffn_flops(x.shape[0], A, B)
+
+
+def cost_ffn_backward(a, kw, out):
+    dz, x, A, B = a[:4]
+    return x.shape[0] * (4 * x.shape[1] * _es(x) + 16), 1.65 * _ffn_flops(x.shape[0], A, B)
+
+
+def roofline(nbytes: float, flops: float, seconds: float) -> dict:
+    """The op's roofline: the larger of its HBM time and its FP32 matrix time
+    over its measured time (``bound`` names which)."""
+    t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+    t_mfma = flops / (FP32_PEAK_TFLOPS * 1e12)
+    both = {"frac_hbm": t_hbm / seconds, "frac_mfma": t_mfma / seconds}
+    if t_mfma > t_hbm:
+        achieved = flops / seconds / 1e12
+        return {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": achieved / FP32_PEAK_TFLOPS, **both}
+    achieved = nbytes / seconds / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+            **both}
 
 
 # ---------------------------------------------------------------- live op timing
 
 
 class OpTimer:
-    """Wraps the native entry points with HIP events on the launching stream."""
+    """Wraps the native entry points with HIP events on the launching stream
+    (torch's current stream, the one every entry point launches on) and sums
+    each call's algorithmic bytes and FLOPs."""
 
     def __init__(self):
         self.events = defaultdict(list)
+        self.cost = defaultdict(lambda: [0.0, 0.0])
         self.enabled = False
 
-    def wrap(self, obj, name, label):
+    def wrap(self, obj, name, label, cost=None, static=False):
         import torch
 
+        if not hasattr(obj, name):
+            return
         inner = getattr(obj, name)
 
         def timed(*args, **kwargs):
             if not self.enabled:
                 return inner(*args, **kwargs)
+            if cost is not None:  # from the arguments, before the call (a backward's saved tensors go with it)
+                b, f = cost(args, kwargs, None)
+                self.cost[label][0] += b
+                self.cost[label][1] += f
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()
             out = inner(*args, **kwargs)
@@ -165,21 +358,99 @@ class OpTimer:
             self.events[label].append((start, end))
             return out
 
-        setattr(obj, name, timed)
+        setattr(obj, name, staticmethod(timed) if static else timed)
+
+    def wrap_layers(self):
+        """Every native entry point the attention, convolution, block and
+        encoder layers reach, plus the flat projections' GEMMs."""
+        from gm_attention_amd import _native
+        from gm_attention_amd.nn import linear
+
+        att, fac = _native.attention(), _native.factored()
+        for obj, name, label, cost in (
+                (att, "softmax_forward", "softmax_forward", cost_softmax_forward),
+                (att, "softmax_backward", "softmax_backward", cost_softmax_backward),
+                (att, "conv_forward", "conv_forward", cost_conv_forward),
+                (att, "conv_backward", "conv_backward", cost_conv_backward),
+                (fac, "forward", "factored_forward", cost_factored_forward),
+                (fac, "aggregate", "factored_aggregate", cost_factored_aggregate),
+                (fac, "backward_aggregated", "factored_backward_aggregated", cost_factored_backward_aggregated),
+                (_native, "factored_forward_grouped", "factored_forward", cost_factored_forward_grouped),
+                (_native, "factored_backward_grouped", "factored_backward_aggregated", cost_factored_backward_grouped),
+                (_native, "aggregate_heads", "factored_aggregate", cost_aggregate_heads),
+                (_native, "radial_trunk_forward", "radial_trunk_forward", cost_trunk_forward),
+                (_native, "radial_trunk_backward", "radial_trunk_backward", cost_trunk_backward),
+                (_native, "node_mix_forward", "node_mix_forward", cost_node_mix_forward),
+                (_native, "node_mix_backward_input", "node_mix_backward_input", cost_node_mix_backward_input),
+                (_native, "node_mix_backward_weight", "node_mix_backward_weight", cost_node_mix_backward_weight),
+                (_native, "gather_transpose", "gather_transpose", cost_gather_transpose),
+                (_native, "scatter_transpose", "scatter_transpose", cost_scatter_transpose),
+                (_native, "conv_radial_forward", "conv_radial_forward", cost_conv_radial_forward),
+                (_native, "conv_radial_backward", "conv_radial_backward", cost_conv_radial_backward),
+                (_native, "layer_norm_forward", "layer_norm_forward", cost_layer_norm_forward),
+                (_native, "layer_norm_backward", "layer_norm_backward", cost_layer_norm_backward),
+                (_native, "gate_forward", "gate_forward", cost_gate_forward),
+                (_native, "gate_backward", "gate_backward", cost_gate_backward),
+                (_native, "ffn_forward", "ffn_forward", cost_ffn_forward),
+                (_native, "ffn_backward", "ffn_backward", cost_ffn_backward)):
+            self.wrap(obj, name, label, cost)
+        self.wrap(linear.FlatLinear, "forward", "projection_forward", cost_projection_forward, static=True)
+        self.wrap(linear.FlatLinear, "backward", "projection_backward", cost_projection_backward, static=True)
 
     def summary(self, steps: int) -> dict[str, dict[str, float]]:
         out = {}
         for label, pairs in self.events.items():
             times = [s.elapsed_time(e) for s, e in pairs]
-            out[label] = {"launches_per_step": len(times) / steps, "avg_ms": sum(times) / len(times),
-                          "ms_per_step": sum(times) / steps}
+            total_s = sum(times) * 1e-3
+            nbytes, flops = self.cost[label]
+            rec = {"launches_per_step": len(times) / steps, "avg_ms": sum(times) / len(times),
+                   "ms_per_step": sum(times) / steps, "bytes_per_launch": nbytes / len(times),
+                   "flops_per_launch": flops / len(times)}
+            if total_s > 0:
+                rec["GB/s"] = nbytes / total_s / 1e9
+                rec["TFLOP/s"] = flops / total_s / 1e12
+                r = roofline(nbytes, flops, total_s)
+                rec["bound"], rec["frac"] = r["bound"], r["frac"]
+            out[label] = rec
         return out
+
+    def line_roofline(self, ops: dict, dominant: str, workload_tag: str) -> dict:
+        """The dominant op's roofline object for the JSON line, with the
+        counter-measured traffic per launch where a profile holds it."""
+        rec = ops[dominant]
+        n = rec["launches_per_step"]
+        r = roofline(rec["bytes_per_launch"] * n, rec["flops_per_launch"] * n, rec["ms_per_step"] * 1e-3)
+        traffic_file = ROOT / "profiles" / f"{dominant}_{workload_tag}_traffic.json"
+        r["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch") if traffic_file.exists() else None
+        r["kernel"] = dominant
+        r["algorithmic_per_launch"] = {"bytes": rec["bytes_per_launch"], "flops": rec["flops_per_launch"]}
+        r["launches_per_step"] = n
+        return r
+
+
+def ops_coverage(ops: dict, ms_per_step: float) -> dict:
+    """How much of the step the timed entry points account for; the rest is
+    torch's own kernels (copies, index gathers, sums, the allocator) and host time."""
+    total = sum(v["ms_per_step"] for v in ops.values())
+    return {"ops_ms_per_step": total, "step_ms": ms_per_step, "fraction": total / ms_per_step,
+            "other_ms_per_step": ms_per_step - total}
 
 
 # ---------------------------------------------------------------- problem
 
 
-def build_edges(device, batch: int = BATCH):
+#: The attention configurations: the north-star shape (the headline) and BASELINE's C1 and C2.
+LAYERS = {
+    "attention": dict(nlat=NLAT, nlon=NLON, batch=BATCH, heads=HEADS, field=FIELD, backward=True,
+                      metric="attn fwd+bwd query-points/s at 256x512 B=4", tag="ns"),
+    "c2": dict(nlat=128, nlon=256, batch=4, heads=8, field=FIELD, backward=True,
+               metric="attn fwd+bwd query-points/s at 128x256 B=4 (C2)", tag="c2"),
+    "c1": dict(nlat=32, nlon=64, batch=1, heads=4, field={0: 16, 1: 16, 2: 16}, backward=False,
+               metric="attn fwd query-points/s at 32x64 B=1 (C1)", tag="c1"),
+}
+
+
+def build_edges(device, batch: int = BATCH, nlat: int = NLAT, nlon: int = NLON):
     import torch
 
     from gm_attention_amd.discretization.edge_geometry import compute_edge_geometry
@@ -187,81 +458,103 @@ def build_edges(device, batch: int = BATCH):
     from gm_attention_amd.discretization.grid import build_equiangular_grid
 
     t0 = time.time()
-    cutoff = 3.0 * math.pi / (NLAT - 1)
-    grid = build_equiangular_grid(NLAT, NLON)
+    cutoff = 3.0 * math.pi / (nlat - 1)
+    grid = build_equiangular_grid(nlat, nlon)
     edges = compute_edge_geometry(grid, build_tangent_frames(grid.nodes), cutoff)
-    log(f"geometry {NLAT}x{NLON}: {edges.n_edges} edges per sample in {time.time() - t0:.1f}s")
+    log(f"geometry {nlat}x{nlon}: {edges.n_edges} edges per sample in {time.time() - t0:.1f}s")
     tiled = edges.to(device, torch.float32).tile(batch, n_sources=grid.n_nodes)
     return edges, tiled, cutoff
 
 
-def cpu_baseline_attention(edges, cutoff, mhsa_gpu, budget_edges: int):
-    """The eager restatement (oracle.modules, factored order as under
-    GM_FACTORED_KERNEL=1) of one SO2MHSA forward + backward in float32 on the
-    host's cores (at most 16 threads, one GPU's share of the box), over the
-    targets of a mixed sample of one 256x512 sample: the first (pole) targets
-    and whole equator rows.  The node-side work (projections, node products)
-    always covers one sample's 131,072 nodes; the edge-side work scales with
-    the sampled edges.  Two sample sizes (``budget_edges / 4`` and
-    ``budget_edges``) give both costs, extrapolated to the step's nodes and edges."""
+def cpu_baseline_attention(edges, cutoff, mhsa_gpu, budget_edges: int, cfg: dict | None = None):
+    """The eager restatement of one SO2MHSA layer (``oracle.modules.mhsa_forward``,
+    the factored order as under GM_FACTORED_KERNEL=1, per-head types and scales
+    derived by the oracle) forward (+ backward when the configuration has it)
+    in float32 on the host's cores (at most 16 threads, one GPU's share of the
+    box), over one sample's nodes and the edges of a mixed sample of its
+    targets: the first (pole) targets and whole equator rows.  The node-side
+    work (projections, node products) always covers the sample's nodes; the
+    edge-side work scales with the sampled edges.  Three sample sizes give
+    both costs by least squares, extrapolated to the step's nodes and edges.
+    A sample with fewer edges than the budget is timed whole (one point)."""
     import torch
 
     from gm_attention_amd.nn.attention import SO2MHSA
     from gm_attention_amd.representations.field_type import SO2FeatureField
     from oracle import modules
 
+    cfg = cfg or LAYERS["attention"]
+    nlat, nlon = cfg["nlat"], cfg["nlon"]
     threads = cpu_threads()
     torch.set_num_threads(threads)
     row_ptr = edges.row_ptr
     n = row_ptr.shape[0] - 1
-    mhsa = SO2MHSA(mhsa_gpu.field_type_in, HEADS, cutoff=cutoff, window="hard", batched=True, dtype=torch.float32)
+    mhsa = SO2MHSA(mhsa_gpu.field_type_in, cfg["heads"], cutoff=cutoff, window="hard", batched=True,
+                   dtype=torch.float32)
     mhsa.load_state_dict({k: v.detach().cpu() for k, v in mhsa_gpu.state_dict().items()})
     fin = mhsa.field_type_in
     gen = torch.Generator().manual_seed(3)
-    x = torch.randn(n, fin.dimension, generator=gen).requires_grad_(True)
+    x = torch.randn(n, fin.dimension, generator=gen).requires_grad_(cfg["backward"])
     g = torch.randn(n, fin.dimension, generator=gen)
 
     def sample(budget):
+        if budget >= edges.n_edges:
+            return edges.to(None, torch.float32)
         pole_last = max(1, int(torch.searchsorted(row_ptr, torch.tensor(budget // 2)).item()))
-        eq_first = (NLAT // 2) * NLON
-        eq_last = eq_first + NLON
-        while int(row_ptr[eq_last] - row_ptr[eq_first]) < budget // 2 and eq_last + NLON <= n:
-            eq_last += NLON
+        eq_first = (nlat // 2) * nlon
+        eq_last = eq_first + nlon
+        while int(row_ptr[eq_last] - row_ptr[eq_first]) < budget // 2 and eq_last + nlon <= n:
+            eq_last += nlon
         sel = torch.cat([torch.arange(int(row_ptr[a]), int(row_ptr[b])) for a, b in ((0, pole_last), (eq_first, eq_last))])
         return edges.select(sel, n_nodes=n).to(None, torch.float32)
 
     def step(sub):
         xs = SO2FeatureField.from_flat(fin, x).coefficients
-        heads = []
-        for head in mhsa.heads:
-            q = modules.linear(head.query, xs, head.field_type_attn)
-            k = modules.linear(head.key, xs, head.field_type_attn)
-            alpha = modules.softmax_weights(q, k, sub, head.cutoff, head.window, 1, head._score_scale)[:, 0]
-            msgs = modules.factored_messages(head.value, xs, sub.source_index, sub.distances, sub.angular_phases,
-                                             sub.transport_phases)
-            heads.append({f: torch.segment_reduce(alpha.reshape(-1, *([1] * (m.ndim - 1))) * m, "sum",
-                                                  offsets=sub.row_ptr, axis=0) for f, m in msgs.items()})
-        fused = {f: torch.cat([o[f] for o in heads], dim=-1 if f == 0 else -2) for f in fin.frequencies}
-        out = modules.flat(modules.linear(mhsa.output_projection, fused, fin))
-        (out * g).sum().backward()
-        x.grad = None
-        mhsa.zero_grad(set_to_none=True)
+        out = modules.flat(modules.mhsa_forward(mhsa, xs, sub, messages="factored"))
+        if cfg["backward"]:
+            (out * g).sum().backward()
+            x.grad = None
+            mhsa.zero_grad(set_to_none=True)
 
+    budgets = (budget_edges // 4, budget_edges // 2, budget_edges) if edges.n_edges > budget_edges else (edges.n_edges,)
     points = []
-    for budget in (budget_edges // 4, budget_edges // 2, budget_edges):
+    for budget in budgets:
         sub = sample(budget)
-        step(sub)  # warm-up
-        t0 = time.perf_counter()
-        step(sub)
+        with torch.set_grad_enabled(cfg["backward"]):
+            step(sub)  # warm-up
+            t0 = time.perf_counter()
+            step(sub)
         points.append((sub.n_edges, time.perf_counter() - t0))
+    if len(points) == 1:  # the whole sample: no extrapolation in edges
+        return dict(per_edge=0.0, per_sample_nodes=points[0][1], points=points, threads=threads, whole=True)
     # least squares t = per_sample_nodes + per_edge e over the three samples
-    n = len(points)
-    me = sum(e for e, _ in points) / n
-    mt = sum(t for _, t in points) / n
+    k = len(points)
+    me = sum(e for e, _ in points) / k
+    mt = sum(t for _, t in points) / k
     per_edge = sum((e - me) * (t - mt) for e, t in points) / sum((e - me) ** 2 for e, _ in points)
     per_sample_nodes = max(0.0, mt - per_edge * me)
-    return dict(per_edge=per_edge, per_sample_nodes=per_sample_nodes, points=points, threads=threads,
-                cpu_s=sum(t for _, t in points))
+    return dict(per_edge=per_edge, per_sample_nodes=per_sample_nodes, points=points, threads=threads, whole=False)
+
+
+def attention_baseline_line(b: dict, cfg: dict, N: int, E: int, batch: int) -> dict:
+    """The CPU baseline's entry of the JSON line from ``cpu_baseline_attention``'s result."""
+    direction = "fwd+bwd" if cfg["backward"] else "fwd"
+    grid = f"{cfg['nlat']}x{cfg['nlon']}"
+    if b["whole"]:
+        cpu_step = b["per_sample_nodes"] * batch
+        e, t = b["points"][0]
+        how = (f"on one whole {grid} sample ({e} edges) in {t:.2f}s, the rate on that sample"
+               + (f" x {batch} samples" if batch > 1 else ""))
+    else:
+        cpu_step = b["per_sample_nodes"] * batch + b["per_edge"] * E
+        pts = "; ".join(f"{e} edges in {t:.2f}s" for e, t in b["points"])
+        how = (f"on one {grid} sample's nodes with the edges of its first (pole) targets and equator rows, three "
+               f"sizes: {pts}; the least-squares fit {b['per_sample_nodes']:.2f}s per sample's nodes + "
+               f"{b['per_edge'] * 1e6:.1f}us per edge, extrapolated to {batch} samples and {E} edges")
+    return {"value": N / cpu_step, "unit": "query-points/s", "cores": b["threads"], "kind": "port",
+            "cpu_model": cpu_model(), "host_cpu_count": os.cpu_count(),
+            "sample": (f"oracle eager SO2MHSA {direction} (oracle.modules.mhsa_forward, factored order, float32, "
+                       f"torch on {b['threads']} threads) {how}")}
 
 
 def cpu_baseline_ffn(block_gpu, n_nodes: int):
@@ -403,7 +696,8 @@ def run_geometry(args) -> None:
                                f"cKDTree ball query ({threads} workers), float64 exact filter and torch per-edge "
                                f"arithmetic ({threads} threads) in {seconds:.2f}s")}
         log(f"cpu baseline: {baseline['value']:.3g} edges/s ({baseline['sample']})")
-    op_rates = {name: {k: round(x, 4) for k, x in v.items()} for name, v in ops.items()}
+    op_rates = {name: {k: (round(x, 4) if isinstance(x, float) else x) for k, x in v.items()}
+                for name, v in ops.items()}
     line = {
         "metric": "edge-geometry build edges/s at 256x512 (one sample)",
         "value": E / (ms_per_step * 1e-3),
@@ -438,7 +732,6 @@ def run_stage(args) -> None:
     the 128x256 input grid; cross-entropy against random labels."""
     import torch
 
-    from gm_attention_amd import _native
     from gm_attention_amd.nn import eager_ops
     from gm_attention_amd.nn.segformer import GmSegformer, build_stage_hierarchy, stage_radii
     from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
@@ -459,21 +752,7 @@ def run_stage(args) -> None:
                         readout_channels=(32, 32), decoder_channels=32, n_radial_basis=8, dtype=torch.float32,
                         device=device)
     timer = OpTimer()
-    att, fac = _native.attention(), _native.factored()
-    for name in ("softmax_forward", "softmax_backward"):
-        timer.wrap(att, name, name)
-    for mod, name, key in ((fac, "aggregate", "factored_aggregate"),
-                           (fac, "backward_aggregated", "factored_backward_aggregated"),
-                           (fac, "forward", "factored_forward"),
-                           (_native, "factored_forward_grouped", "factored_forward"),
-                           (_native, "factored_backward_grouped", "factored_backward_aggregated"),
-                           (_native, "aggregate_heads", "factored_aggregate"),
-                           (_native, "radial_trunk_forward", "radial_trunk_forward"),
-                           (_native, "radial_trunk_backward", "radial_trunk_backward"),
-                           (_native, "conv_radial_forward", "conv_radial_forward"),
-                           (_native, "conv_radial_backward", "conv_radial_backward")):
-        if hasattr(mod, name):
-            timer.wrap(mod, name, key)
+    timer.wrap_layers()
     gen = torch.Generator(device=device).manual_seed(1)
     x0 = torch.rand(n0, 4, device=device, generator=gen).requires_grad_(True)
     labels = torch.randint(0, 13, (n0,), device=device, generator=gen)
@@ -524,9 +803,10 @@ def run_stage(args) -> None:
                                 "{0:128,1:128,2:128} (16-head block); readouts, fusion decoder, 13-class head, "
                                 "cross-entropy; input and every parameter gradient"),
                    "batch": C5_BATCH, "fine_points": n0, "restriction_edges": down, "stage_edges": local},
-        "roofline": None,
-        "dominant_op": dominant,
-        "ops": {name: {k: round(v2, 4) for k, v2 in v.items()} for name, v in ops.items()},
+        "roofline": timer.line_roofline(ops, dominant, "c5"),
+        "ops": {name: {k: (round(x, 4) if isinstance(x, float) else x) for k, x in v.items()}
+                for name, v in ops.items()},
+        "ops_coverage": ops_coverage(ops, ms_per_step),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_stage(model),
     }
     print(json.dumps(line))
@@ -577,7 +857,6 @@ def run_encoder(args) -> None:
     """One step = both restriction hops forward and backward (C5's encoder transfers)."""
     import torch
 
-    from gm_attention_amd import _native
     from gm_attention_amd.discretization.grid import build_equiangular_grid
     from gm_attention_amd.discretization.hierarchy import build_grid_hierarchy
     from gm_attention_amd.nn import fused_factored
@@ -599,10 +878,7 @@ def run_encoder(args) -> None:
     encs = [EquiEncode(types[k], types[k + 1], cutoff=cutoffs[k], n_radial_basis=8, dtype=torch.float32, device=device)
             for k in range(2)]
     timer = OpTimer()
-    fac = _native.factored()
-    timer.wrap(fac, "forward", "factored_forward")
-    timer.wrap(fac, "aggregate", "factored_aggregate")
-    timer.wrap(fac, "backward_aggregated", "factored_backward_aggregated")
+    timer.wrap_layers()
     n0 = h.levels[0].n_nodes
     gen = torch.Generator(device=device).manual_seed(1)
     x = torch.rand(n0, types[0].dimension, device=device, generator=gen).requires_grad_(True)
@@ -633,27 +909,9 @@ def run_encoder(args) -> None:
     ms_per_step = 1e3 * elapsed / args.steps
     ops = timer.summary(args.steps)
     log(f"step {ms_per_step:.2f} ms; ops: " + ", ".join(f"{k} {v['ms_per_step']:.2f} ms" for k, v in ops.items()))
-    # FLOPs of every tile of both hops: forward 2 K C + 8 wc, backward 4 K C + 8 wc per edge (C = 2 wc + wr)
-    flops = {"factored_forward": 0.0, "factored_backward_aggregated": 0.0}
-    for enc, e in zip(encs, down):
-        kern = enc.integral.kernel
-        K = kern.complex_head.in_features + 1
-        tl = fused_factored.tiles(kern)
-        shapes_t = [(len(t.zc_cols), len(t.zr_cols)) for t in tl] if tl else [
-            (fused_factored.plan(kern).wc, fused_factored.plan(kern).wr)]
-        for wc, wr in shapes_t:
-            C = 2 * wc + wr
-            flops["factored_forward"] += e.n_edges * (2.0 * K * C + 8 * wc)
-            flops["factored_backward_aggregated"] += e.n_edges * (4.0 * K * C + 8 * wc)
     dominant = max(ops, key=lambda k: ops[k]["ms_per_step"])
-    if dominant not in flops:
-        dominant = "factored_backward_aggregated"
-    achieved = flops[dominant] / (ops[dominant]["ms_per_step"] * 1e-3) / 1e12
-    roof = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": achieved / FP32_PEAK_TFLOPS, "traffic": None, "kernel": dominant,
-            "algorithmic_per_launch": {"flops_per_step": flops[dominant],
-                                       "launches_per_step": ops[dominant]["launches_per_step"]},
-            "note": "the op's launches (output tiles of both hops) differ in size: FLOPs and time per step"}
+    roof = timer.line_roofline(ops, dominant, "hops")
+    roof["note"] = "the op's launches (output tiles of both hops) differ in size: bytes and FLOPs summed per call"
     baseline = None
     if not args.no_cpu_baseline:
         threads = cpu_threads()
@@ -705,25 +963,31 @@ def run_encoder(args) -> None:
                    "batch": 8, "fine_points": n0, "edges": [e.n_edges for e in down],
                    "tiles": [len(fused_factored.tiles(e.integral.kernel) or ()) for e in encs]},
         "roofline": roof,
-        "ops": {name: {k: round(v2, 4) for k, v2 in v.items()} for name, v in ops.items()},
+        "ops": {name: {k: (round(x, 4) if isinstance(x, float) else x) for k, x in v.items()}
+                for name, v in ops.items()},
+        "ops_coverage": ops_coverage(ops, ms_per_step),
         "cpu_baseline": baseline,
     }
     print(json.dumps(line))
 
 
-OTHER_WORKLOADS = (("conv", 5), ("block", 5), ("encoder", 3), ("geometry", 5))
+#: The other configurations the default run measures after the headline: (workload, timed steps, with its
+#: CPU baseline, extra arguments).  C1 and C2 are BASELINE's attention rows, conv is C3, block C4, encoder C5.
+OTHER_WORKLOADS = (("c1", 10, True, ()), ("c2", 5, True, ("--cpu-budget-edges", "100000")), ("conv", 5, True, ()),
+                   ("block", 5, False, ()), ("encoder", 3, False, ()), ("geometry", 5, False, ()))
 
 
 def other_workloads() -> dict:
-    """Every other configuration's line, from a child process each (warm-up 2, a few timed steps, no CPU
-    baseline): rate, step time and roofline, or the error it ended with."""
+    """Every other configuration's line, from a child process each (warm-up 2, a few timed steps; the CPU
+    baseline where OTHER_WORKLOADS asks for it): rate, step time, roofline and op coverage, or the error it
+    ended with."""
     import subprocess
 
     out = {}
-    for name, steps in OTHER_WORKLOADS:
-        log(f"other workload: {name} ({steps} steps)")
+    for name, steps, cpu, extra in OTHER_WORKLOADS:
+        log(f"other workload: {name} ({steps} steps{', CPU baseline' if cpu else ''})")
         cmd = [sys.executable, str(Path(__file__).resolve()), "--workload", name, "--steps", str(steps), "--warmup",
-               "2", "--no-cpu-baseline"]
+               "2", *extra] + ([] if cpu else ["--no-cpu-baseline"])
         try:
             run = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
         except subprocess.TimeoutExpired:
@@ -735,7 +999,8 @@ def other_workloads() -> dict:
             out[name] = {"error": f"exit {run.returncode}: {tail[0][:300]}"}
             continue
         rec = json.loads(lines[-1])
-        out[name] = {k: rec.get(k) for k in ("metric", "value", "unit", "ms_per_step", "steps", "dtype", "roofline")}
+        out[name] = {k: rec.get(k) for k in ("metric", "value", "unit", "ms_per_step", "steps", "dtype", "roofline",
+                                             "ops_coverage", "cpu_baseline")}
         log(f"{name}: {rec.get('ms_per_step')} ms per step")
     return out
 
@@ -745,8 +1010,8 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=("attention", "softmax", "conv", "geometry", "block", "encoder", "hops"),
-                    default="attention")
+    ap.add_argument("--workload", choices=("attention", "c1", "c2", "softmax", "conv", "geometry", "block", "encoder",
+                                           "hops"), default="attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-workloads", action="store_true",
                     help="the default attention run skips measuring the other configurations")
@@ -780,58 +1045,47 @@ def main() -> None:
     if args.workload == "encoder":
         run_stage(args)
         return
+    run_layer(args)
 
+
+def run_layer(args) -> None:
+    """The attention layer at a configuration of ``LAYERS`` (the headline,
+    C1, C2), the scores-and-softmax op alone, the C3 depthwise convolution or
+    the C4 block, each on its equiangular grid and batch."""
     import torch
 
-    from gm_attention_amd import _native
-    from gm_attention_amd.nn import fused_attention, fused_factored
+    from gm_attention_amd.nn import fused_attention
     from gm_attention_amd.nn.attention import SO2MHSA
     from gm_attention_amd.representations.field_type import SO2FeatureField, SO2FieldType
 
     device = torch.device("cuda:0")
+    cfg = dict(LAYERS.get(args.workload, LAYERS["attention"]))
+    if args.workload == "block":
+        cfg.update(batch=2, tag="c4")
     timer = OpTimer()
-    att, fac = _native.attention(), _native.factored()
-    for name in ("softmax_forward", "softmax_backward"):
-        timer.wrap(att, name, name)
-    timer.wrap(fac, "forward", "factored_forward")
-    timer.wrap(fac, "aggregate", "factored_aggregate")
-    timer.wrap(fac, "backward_aggregated", "factored_backward_aggregated")
-    timer.wrap(_native, "factored_forward_seg", "factored_forward")
-    timer.wrap(_native, "factored_backward_seg", "factored_backward_aggregated")
-    timer.wrap(_native, "factored_forward_grouped", "factored_forward")
-    timer.wrap(_native, "factored_backward_grouped", "factored_backward_aggregated")
-    timer.wrap(_native, "aggregate_gather", "factored_aggregate")
-    timer.wrap(_native, "aggregate_heads", "factored_aggregate")
-    timer.wrap(_native, "radial_trunk_forward", "radial_trunk_forward")
-    timer.wrap(_native, "radial_trunk_backward", "radial_trunk_backward")
-    timer.wrap(att, "conv_forward", "conv_forward")
-    timer.wrap(att, "conv_backward", "conv_backward")
-    if hasattr(_native, "conv_radial_forward"):
-        timer.wrap(_native, "conv_radial_forward", "conv_radial_forward")
-        timer.wrap(_native, "conv_radial_backward", "conv_radial_backward")
-
-    batch = 2 if args.workload == "block" else BATCH
-    for name in ("layer_norm_forward", "layer_norm_backward", "gate_forward", "gate_backward"):
-        timer.wrap(_native, name, name)
-    edges_cpu, edges, cutoff = build_edges(device, batch)
+    timer.wrap_layers()
+    batch = cfg["batch"]
+    edges_cpu, edges, cutoff = build_edges(device, batch, cfg["nlat"], cfg["nlon"])
     N = edges.row_ptr.shape[0] - 1
     E = edges.n_edges
-    field = SO2FieldType(FIELD)
+    field = SO2FieldType(cfg["field"])
     D = field.dimension
+    heads = cfg["heads"]
     torch.manual_seed(0)
-    mhsa = SO2MHSA(field, HEADS, cutoff=cutoff, window="hard", batched=True, dtype=torch.float32, device=device)
+    mhsa = SO2MHSA(field, heads, cutoff=cutoff, window="hard", batched=True, dtype=torch.float32, device=device)
     gen = torch.Generator(device=device).manual_seed(1)
-    x_flat = torch.randn(N, D, device=device, generator=gen).requires_grad_(True)
+    x_flat = torch.randn(N, D, device=device, generator=gen).requires_grad_(cfg["backward"])
     upstream = torch.randn(N, D, device=device, generator=gen)
     g = fused_attention.geometry(edges, cutoff, "hard", torch.float32)
-    log(f"problem: N={N} E={E} D={D} H={HEADS} max_degree={g.max_degree}")
+    log(f"problem: N={N} E={E} D={D} H={heads} max_degree={g.max_degree}")
     module = mhsa  # the module whose parameter gradients the loop clears
+    grid = f"{cfg['nlat']}x{cfg['nlon']}"
 
     if args.workload == "block":
         from gm_attention_amd.nn.blocks import SO2TransformerBlock
 
         torch.manual_seed(0)
-        block = SO2TransformerBlock(field, HEADS, ffn_multiplier=4, cutoff=cutoff, window="hard",
+        block = SO2TransformerBlock(field, heads, ffn_multiplier=4, cutoff=cutoff, window="hard",
                                     attention_batched=True, dtype=torch.float32, device=device)
         module = block
         mhsa = block.attention
@@ -841,17 +1095,21 @@ def main() -> None:
         def step():
             y = block.forward_flat(x_flat, edges)
             torch.autograd.backward(y, upstream)
-        workload = ("SO2TransformerBlock(ffn_multiplier=4) fwd+bwd: layer norm, batched 8-head SO2MHSA (float32 "
-                    "kernels), residual, layer norm, SO2Linear 160->640 (bf16 GEMM), scalar gate (double sigmoid), "
-                    "SO2Linear 640->160, residual; bf16 rows, float32 parameters; input and every parameter gradient")
-    elif args.workload == "attention":
+        workload = ("SO2TransformerBlock(ffn_multiplier=4) fwd+bwd: layer norm, batched 8-head SO2MHSA (bf16 Q/K "
+                    "projections, scores reading bf16 q and k, node mixes reading bf16 rows, float32 from the mixes "
+                    "on), residual, then the fused feed-forward (layer norm, SO2Linear 160->640, scalar gate, "
+                    "SO2Linear 640->160, residual: one bf16-MFMA kernel per direction); bf16 rows, float32 "
+                    "parameters; input and every parameter gradient")
+    elif args.workload in LAYERS:
         def step():
             x = SO2FeatureField.from_flat(field, x_flat)
             y = mhsa(x, edges)._rows()
-            torch.autograd.backward(y, upstream)
-        workload = ("SO2MHSA(batched) fwd+bwd: stacked Q/K projections, fused scores+softmax, 8 heads of node "
-                    "products + radial trunk + fused factored value aggregation, output projection; input and "
-                    "every parameter gradient")
+            if cfg["backward"]:
+                torch.autograd.backward(y, upstream)
+        workload = (f"SO2MHSA(batched) {'fwd+bwd' if cfg['backward'] else 'fwd'}: stacked Q/K projections, fused "
+                    f"scores+softmax, {heads} heads of node products + radial trunk + fused factored value "
+                    "aggregation, output projection" + ("; input and every parameter gradient" if cfg["backward"]
+                                                        else ""))
     elif args.workload == "conv":
         from gm_attention_amd.nn.convolution import SO2Convolution
 
@@ -873,85 +1131,45 @@ def main() -> None:
         scale = float(mhsa.heads[0]._score_scale)
         q = torch.randn(N, D, device=device, generator=gen).requires_grad_(True)
         k = torch.randn(N, D, device=device, generator=gen).requires_grad_(True)
-        dalpha = torch.randn(E, HEADS, device=device, generator=gen)
+        dalpha = torch.randn(E, heads, device=device, generator=gen)
         transport = g.transport_to(2)
 
         def step():
-            alpha = fused_attention.Softmax.apply(q, k, transport, g.bias, g.inside, desc, g.row_ptr, g.source, HEADS,
+            alpha = fused_attention.Softmax.apply(q, k, transport, g.bias, g.inside, desc, g.row_ptr, g.source, heads,
                                                   scale, g.max_degree)
             torch.autograd.backward(alpha, dalpha)
         workload = "Softmax.apply fwd+bwd: neighbourhood scores + softmax over CSR (gauge-transported keys)"
 
-    for _ in range(args.warmup):
-        step()
+    def clear():
         module.zero_grad(set_to_none=True)
         x_flat.grad = None
-    torch.cuda.synchronize()
-    timer.enabled = True
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-        module.zero_grad(set_to_none=True)
-        x_flat.grad = None
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+
+    with torch.set_grad_enabled(cfg["backward"] or args.workload not in LAYERS):
+        for _ in range(args.warmup):
+            step()
+            clear()
+        torch.cuda.synchronize()
+        timer.enabled = True
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+            clear()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
     timer.enabled = False
     ms_per_step = 1e3 * elapsed / args.steps
     ops = timer.summary(args.steps)
     log(f"step {ms_per_step:.2f} ms; ops: " + ", ".join(f"{k} {v['ms_per_step']:.2f} ms" for k, v in ops.items()))
-
-    costs = softmax_cost(E, N, D, HEADS)
-    kern = mhsa.heads[0].value
-    fp = fused_factored.plan(kern)
-    K = kern.complex_head.in_features + 1
-    costs.update(factored_cost(E, N, K, 2 * fp.wc + fp.wr, fp.wc, fp.d_out, HEADS))
-    # the radial trunk for all heads: rho in, h (H, E, T) out; 2 T B + ~20 T FLOPs per edge and head
-    costs["radial_trunk_forward"] = (E * (4 + HEADS * 4 * (K - 1)), E * HEADS * (2.0 * (K - 1) * 8 + 20 * (K - 1)))
-    costs["radial_trunk_backward"] = (E * (4 + HEADS * 4 * (K - 1)), E * HEADS * (4.0 * (K - 1) * 8 + 30 * (K - 1)))
-    a0 = field.multiplicity(0)
-    costs.update(conv_cost(E, N, D, a0, 4 * (D - a0) // 2))
     dominant = max(ops, key=lambda k: ops[k]["ms_per_step"])
-    nbytes, flops = costs[dominant]
-    avg_s = ops[dominant]["avg_ms"] * 1e-3
-    if dominant.startswith(("softmax", "radial", "conv_forward", "conv_backward")) or dominant == "factored_aggregate":
-        roof = {"bound": "hbm", "achieved": nbytes / avg_s / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
-    else:
-        roof = {"bound": "mfma", "achieved": flops / avg_s / 1e12, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s"}
-    roof["frac"] = roof["achieved"] / roof["peak"]
-    traffic_file = ROOT / "profiles" / f"{dominant}_{'c4' if args.workload == 'block' else 'ns'}_traffic.json"
-    roof["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch") if traffic_file.exists() else None
-    roof["kernel"] = dominant
-    roof["algorithmic_per_launch"] = {"bytes": nbytes, "flops": flops}
-    # pointwise block operators: bytes of the rows (and gate pre-activations) each reads and writes
-    rb = 2 if args.workload == "block" else 4
-    if args.workload == "block":
-        hd = block.hidden_field_type.dimension
-        G = sum(m for n, m in block.hidden_field_type.items() if n != 0)
-        costs["layer_norm_forward"] = (N * D * 2 * rb + 8 * N, 0.0)
-        costs["layer_norm_backward"] = (N * D * 3 * rb + 8 * N, 0.0)
-        costs["gate_forward"] = (N * (2 * hd + G) * rb, 0.0)
-        costs["gate_backward"] = (N * (3 * hd + 2 * G) * rb, 0.0)
-    op_rates = {}
-    for name, v in ops.items():
-        b, f = costs[name]
-        op_rates[name] = {**{k: round(x, 4) for k, x in v.items()}, "GB/s": b / (v["avg_ms"] * 1e-3) / 1e9,
-                          "TFLOP/s": f / (v["avg_ms"] * 1e-3) / 1e12}
+    roof = timer.line_roofline(ops, dominant, cfg["tag"])
 
     baseline = None
-    if not args.no_cpu_baseline and args.workload == "attention":
-        b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges)
-        cpu_step = b["per_sample_nodes"] * batch + b["per_edge"] * E
-        pts = "; ".join(f"{e} edges in {t:.2f}s" for e, t in b["points"])
-        baseline = {"value": N / cpu_step, "unit": "query-points/s", "cores": b["threads"], "kind": "port",
-                    "cpu_model": cpu_model(), "host_cpu_count": os.cpu_count(),
-                    "sample": (f"oracle eager SO2MHSA fwd+bwd (factored order, float32, torch on {b['threads']} "
-                               f"threads) on one 256x512 sample's nodes with the edges of its first (pole) targets "
-                               f"and equator rows, three sizes: {pts}; the least-squares fit "
-                               f"{b['per_sample_nodes']:.2f}s per sample's nodes + {b['per_edge'] * 1e6:.1f}us per "
-                               f"edge, extrapolated to {batch} samples and {E} edges")}
+    if not args.no_cpu_baseline and args.workload in LAYERS:
+        b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges, cfg)
+        baseline = attention_baseline_line(b, cfg, N, E, batch)
         log(f"cpu baseline: {baseline['value']:.1f} qp/s ({baseline['sample']})")
     elif not args.no_cpu_baseline and args.workload == "block":
-        b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges)
+        b = cpu_baseline_attention(edges_cpu, cutoff, mhsa, args.cpu_budget_edges, cfg)
         ffn_s, _ = cpu_baseline_ffn(block, N // batch)
         cpu_step = (b["per_sample_nodes"] + ffn_s) * batch + b["per_edge"] * E
         pts = ", ".join(f"{e} edges in {t:.2f}s" for e, t in b["points"])
@@ -983,11 +1201,12 @@ def main() -> None:
         achieved = step_bytes / (ms_per_step * 1e-3) / 1e9
         hbm = {"achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                "step_traffic": step_bytes, "source": str(step_file.relative_to(ROOT))}
+    metric = cfg["metric"] if args.workload in LAYERS else {
+        "softmax": "attn scores+softmax fwd+bwd query-points/s at 256x512 B=4",
+        "conv": "depthwise conv fwd+bwd query-points/s at 256x512 B=4",
+        "block": "transformer block fwd+bwd query-points/s at 256x512 B=2"}[args.workload]
     line = {
-        "metric": {"attention": "attn fwd+bwd query-points/s at 256x512 B=4",
-                   "softmax": "attn scores+softmax fwd+bwd query-points/s at 256x512 B=4",
-                   "conv": "depthwise conv fwd+bwd query-points/s at 256x512 B=4",
-                   "block": "transformer block fwd+bwd query-points/s at 256x512 B=2"}[args.workload],
+        "metric": metric,
         "value": N / (ms_per_step * 1e-3),
         "unit": "query-points/s",
         "n_gpus": 1,
@@ -999,12 +1218,15 @@ def main() -> None:
         "vs_baseline": None,
         "dtype": "bf16" if args.workload == "block" else "f32",
         "data": "synthetic: N(0,1) input field and upstream gradient, random-init weights, equiangular grid geometry",
-        "config": {"workload": workload, "grid": f"{NLAT}x{NLON} equiangular", "batch": batch,
-                   "field": "{0:32,1:32,2:32}", "heads": HEADS, "radius": "3 row spacings", "window": "hard",
-                   "query_points": N, "edges": E, "max_degree": g.max_degree},
+        "config": {"workload": workload, "grid": f"{grid} equiangular", "batch": batch,
+                   "field": "{" + ",".join(f"{f}:{m}" for f, m in cfg["field"].items()) + "}", "heads": heads,
+                   "radius": "3 row spacings", "window": "hard", "query_points": N, "edges": E,
+                   "max_degree": g.max_degree},
         "roofline": roof,
         "hbm_step": hbm,
-        "ops": op_rates,
+        "ops": {name: {k: (round(x, 4) if isinstance(x, float) else x) for k, x in v.items()}
+                for name, v in ops.items()},
+        "ops_coverage": ops_coverage(ops, ms_per_step),
         "cpu_baseline": baseline,
     }
     if args.workload == "attention" and not args.no_other_workloads:
