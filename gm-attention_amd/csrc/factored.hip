@@ -23,6 +23,7 @@
 // a fixed summation order.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -101,6 +102,16 @@ struct FactArgs {
   uint32_t colslot32[32];  // packed column -> slot column, four bytes a word
   uint32_t kmask;
   int n_slots, gstride;
+  // mixes staged by direct-to-LDS loads (lane-owned backward): the runs
+  // merged into blocks contiguous in memory (a block's rows t = 0 .. 16 are
+  // `zq_w` floats apart, the row a block's width), staged per node in LDS from
+  // row zq_t0 on, block b at float zq_loff[b]; per slot column where its rows
+  // sit (the padding columns at a zero word past the blocks, width 0)
+  const float* zq_base[GM_FACT_MAX_SEG];
+  int64_t zq_ns[GM_FACT_MAX_SEG];
+  int zq_w[GM_FACT_MAX_SEG], zq_loff[GM_FACT_MAX_SEG];
+  int n_zq, zq_t0, zq_words;  // blocks, first staged row, LDS floats in all
+  uint32_t zq_slot[128];       // per slot column: its row zq_t0's float in the area | block width << 16
   // the value kernel's radial trunk evaluated in the lane kernels from rho_g
   // (h_t = SiLU(W1 b + b1) over the Gaussian basis b_k = exp(-((rho^2 - c_k)
   // inv_width)^2 / 2)) instead of reading h; trunk_w null: h is read
@@ -2054,10 +2065,46 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
   wave_sync();
 }
 
+// --------------------------------------------------- mixes by direct-to-LDS loads
+//
+// The lane-owned backward's mixes Z(j), rows t = 1 .. 16 (the only rows it
+// reads: dh pairs W with Z_{1..16}, and dZ's row 0 is W's column sum), staged
+// by direct-to-LDS buffer loads instead of a load and an LDS write per run,
+// row and lane.  The mix runs are merged into the blocks they form in memory
+// (each head's rows of one input frequency: (17, width) contiguous per node),
+// so a node's mixes are a few 16-byte-per-lane loads; they land in the area
+// the W transposes use later, in block layout, and each lane reads its dh
+// operands Z_{1+m}(slot columns 16 nt + 4 q + r) through a per-slot-column
+// table (block row offset | block width << 16) staged with them.
+
+#ifndef GM_FACT_STREAM_WORDS
+#define GM_FACT_STREAM_WORDS (17 * 128 + 4 * 4 + 4)
+#endif
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8).  The compiler inserts no wait for the LDS writes of a
+// direct-to-LDS load, so its readers wait explicitly.
+constexpr unsigned kWaitVm0 = 0x0F70;  // vmcnt(0)
+
+// Node j's mixes, rows zq_t0 .. 16 of every block, into Zq by direct-to-LDS
+// loads (lane i of a load writes its 16 bytes at the load's LDS base + 16 i).
+__device__ __forceinline__ void z_stream(const FactArgs<float>& a, int64_t j, float* Zq, int lane) {
+  const int rows = 17 - a.zq_t0;
+  for (int b = 0; b < a.n_zq; ++b) {
+    const int n = rows * a.zq_w[b];  // floats of the block's rows
+    const auto r = span(a.zq_base[b] + j * a.zq_ns[b] + (int64_t)a.zq_t0 * a.zq_w[b], (int64_t)n * 4);
+    for (int u = 0; 256 * u < n; ++u)
+      if (64 * u + lane < (n + 3) / 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, Zq + a.zq_loff[b] + 256 * u, 16, (64 * u + lane) * 16, 0, 0, 0);
+  }
+}
+
 // ACC: dh and dweights added into the outputs (a later share of a head).
-template <int NT, class P, bool FUSED, bool ACC>
+// ZDMA (compiled-in slots, trunk read): the mixes by direct-to-LDS loads (z_stream).
+template <int NT, class P, bool FUSED, bool ACC, bool ZDMA = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED || P::kDout > 40 ? 2 : 3) : 1))) void
 factored_backward_lanes(FactArgs<float> a) {
+  static_assert(!ZDMA || (P::kStatic && !FUSED), "the staged-mix form serves fixed slots with trunk features read");
   constexpr int ZS = 16 * NT + 4;
   constexpr int kZWords = 17 * ZS, kWWords = 16 * NT * kWtStride;
   __shared__ __align__(16) float Sh[kZWords > kWWords ? kZWords : kWWords];  // Z in, then W's transpose, then dZ out
@@ -2066,6 +2113,7 @@ factored_backward_lanes(FactArgs<float> a) {
   __shared__ __align__(16) uint8_t colslot[128];
   __shared__ int64_t Tg[P::kStatic ? 1 : kMT];
   __shared__ __align__(16) float Hs[kMT * kHsStride];  // the tile's trunk features, edge-major
+  __shared__ __align__(16) uint32_t zsl[ZDMA ? 16 * NT : 1];  // ZDMA: where each slot column's rows sit
   const int lane = threadIdx.x, m = lane & 15, q = lane >> 4;
   const int d_out = P::kStatic ? P::kDout : a.d_out;
   const int64_t gi = a.group_order ? a.group_order[blockIdx.x] : xcd_spread_block(blockIdx.x, gridDim.x);
@@ -2100,7 +2148,13 @@ factored_backward_lanes(FactArgs<float> a) {
   }
   stage_colslot(a, colslot, lane);
   ZStage zst;
-  z_issue<P::kStatic>(a, j, lane, zst);
+  if constexpr (ZDMA) {
+    z_stream(a, j, Sh, lane);
+    for (int i = lane; i < 16 * NT; i += kWave) zsl[i] = a.zq_slot[i];
+    if (lane == 0) Sh[a.zq_words] = 0.f;
+  } else {
+    z_issue<P::kStatic>(a, j, lane, zst);
+  }
   OutVals<P::kStatic ? NT : 1> oa, ob;
   int64_t tn = 0;  // static slots: the targets of the tile two ahead of the current one
   if constexpr (P::kStatic) {
@@ -2108,12 +2162,24 @@ factored_backward_lanes(FactArgs<float> a) {
     load_outs<NT, P>(ob, a.g + t1 * a.g_ld, sp.rows, (kMT + m) * d_out, q);
     tn = bload_i64(sp.t, (2 * kMT + m) * 8);
   }
-  wave_sync();
-  z_commit<ZS>(a, j, Sh, colslot, lane, zst);
   // Z_t(j) for t = 1 + m at the lane's slot columns 16 nt + 4 q + r
   floatx4 zb[NT];
+  if constexpr (ZDMA) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // the direct-to-LDS loads have landed (the compiler does not track them)
+    wave_sync();
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) zb[nt] = *reinterpret_cast<const floatx4*>(Sh + (1 + m) * ZS + 16 * nt + 4 * q);
+    for (int nt = 0; nt < NT; ++nt) {
+      const uint4 w = *reinterpret_cast<const uint4*>(zsl + 16 * nt + 4 * q);
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) zb[nt][r] = Sh[(ws[r] & 0xFFFFu) + m * (ws[r] >> 16)];
+    }
+  } else {
+    wave_sync();
+    z_commit<ZS>(a, j, Sh, colslot, lane, zst);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) zb[nt] = *reinterpret_cast<const floatx4*>(Sh + (1 + m) * ZS + 16 * nt + 4 * q);
+  }
   wave_sync();
   floatx4 dz[NT];
   float dz0[NT];
@@ -2503,6 +2569,63 @@ void launch_grouped_nt(bool forward, const FactArgs<float>& a, hipStream_t strea
     hipLaunchKernelGGL(factored_backward_grouped<NT>, grid, block, lds_backward_grouped(a, NT), stream, a);
 }
 
+// The staged mixes' blocks (FactArgs::zq_*) from row t0 on, for an LDS area of
+// `capacity` floats: the runs merged where one continues another in memory
+// with the same strides, each block's rows contiguous (its t stride its width)
+// and 16-byte aligned at every node (the direct-to-LDS loads move 16 bytes a
+// lane), and the per-slot-column table of where each column's rows sit.
+// False when the runs do not form such blocks or the rows exceed the area.
+bool prepare_zq(FactArgs<float>& a, int t0, int capacity) {
+  a.n_zq = 0;
+  a.zq_t0 = t0;
+  int order[GM_FACT_MAX_SEG];
+  for (int r = 0; r < a.n_seg; ++r) order[r] = r;
+  std::sort(order, order + a.n_seg, [&](int x, int y) { return a.seg[x].z < a.seg[y].z; });
+  int blk_of[GM_FACT_MAX_SEG], off_in[GM_FACT_MAX_SEG];
+  int64_t ts[GM_FACT_MAX_SEG];
+  for (int i = 0; i < a.n_seg; ++i) {
+    const ZSeg<float>& g = a.seg[order[i]];
+    const int b = a.n_zq - 1;
+    if (b >= 0 && g.z == a.zq_base[b] + a.zq_w[b] && g.node_stride == a.zq_ns[b] && g.t_stride == ts[b]) {
+      blk_of[order[i]] = b;
+      off_in[order[i]] = a.zq_w[b];
+      a.zq_w[b] += g.width;
+    } else {
+      a.zq_base[a.n_zq] = g.z;
+      a.zq_ns[a.n_zq] = g.node_stride;
+      ts[a.n_zq] = g.t_stride;
+      a.zq_w[a.n_zq] = g.width;
+      blk_of[order[i]] = a.n_zq;
+      off_in[order[i]] = 0;
+      ++a.n_zq;
+    }
+  }
+  int words = 0;
+  for (int b = 0; b < a.n_zq; ++b) {
+    if (ts[b] != a.zq_w[b]) return false;  // a block's rows are not contiguous
+    if (!aligned(a.zq_base[b], 16) || a.zq_ns[b] % 4 != 0 || ((int64_t)t0 * a.zq_w[b]) % 4 != 0) return false;
+    a.zq_loff[b] = words;
+    words += ((17 - t0) * a.zq_w[b] + 3) / 4 * 4;
+  }
+  if (words + 1 > capacity) return false;
+  a.zq_words = words;
+  for (int sc = 0; sc < 128; ++sc) a.zq_slot[sc] = (uint32_t)words;  // padding: the zero word, width 0
+  for (int r = 0; r < a.n_seg; ++r)
+    for (int c = 0; c < a.seg[r].width; ++c) {
+      const int p = a.seg[r].c0 + c, b = blk_of[r];
+      for (int sc = 0; sc < 128; ++sc)
+        if (a.slotcol[sc] == p) a.zq_slot[sc] = (uint32_t)(a.zq_loff[b] + off_in[r] + c) | (uint32_t)a.zq_w[b] << 16;
+    }
+  return true;
+}
+
+// GM_FACTORED_ZDMA=0: the lane-owned backward stages its mixes by register loads and LDS writes
+// (read at every launch, as GM_FACTORED_STATIC is).
+inline bool zdma_backward() {
+  const char* v = std::getenv("GM_FACTORED_ZDMA");
+  return v == nullptr || v[0] != '0';
+}
+
 template <int NT, class P = RuntimeSlots>
 void launch_lanes_nt(bool forward, const FactArgs<float>& a, hipStream_t stream) {
   const dim3 grid((unsigned)a.n_groups), block(64);
@@ -2515,6 +2638,18 @@ void launch_lanes_nt(bool forward, const FactArgs<float>& a, hipStream_t stream)
     else
       hipLaunchKernelGGL((factored_forward_lanes<NT, P, false, false>), grid, block, 0, stream, a);
   } else {
+    if constexpr (P::kStatic) {
+      // the mixes by direct-to-LDS loads into the W-transpose area (16 rows of every block)
+      constexpr int area = 17 * (16 * NT + 4) > 16 * NT * kWtStride ? 17 * (16 * NT + 4) : 16 * NT * kWtStride;
+      FactArgs<float> za = a;
+      if (!fused && zdma_backward() && prepare_zq(za, 1, area)) {
+        if (a.accumulate)
+          hipLaunchKernelGGL((factored_backward_lanes<NT, P, false, true, true>), grid, block, 0, stream, za);
+        else
+          hipLaunchKernelGGL((factored_backward_lanes<NT, P, false, false, true>), grid, block, 0, stream, za);
+        return;
+      }
+    }
     if (fused)
       hipLaunchKernelGGL((factored_backward_lanes<NT, P, true, false>), grid, block, 0, stream, a);
     else if (a.accumulate)

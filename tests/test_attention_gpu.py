@@ -260,3 +260,36 @@ def test_mhsa_with_the_fused_switches_off_takes_the_eager_path_on_the_gpu(cuda, 
     before = eager_ops.calls.get("softmax", 0)
     test_mhsa_matches_the_oracle(CASES[0], torch.float64, True, cuda)
     assert eager_ops.calls.get("softmax", 0) > before
+
+
+@pytest.mark.parametrize("case", [({0: 8, 1: 8, 2: 8}, 2, "hard", 2), ({0: 16, 1: 16, 2: 16}, 2, "quartic", 2),
+                                  ({0: 8, 1: 8}, 2, "hard", 1)])
+def test_staged_mixes_backward_equals_the_register_staged_one(case, cuda, monkeypatch):
+    """The lane-owned backward with its mixes staged by direct-to-LDS loads
+    (the default for the compiled-in slot tables) against the same kernel
+    staging them by register loads and LDS writes (GM_FACTORED_ZDMA=0): the
+    same tiles in the same order, so every output and gradient agrees to
+    float32 rounding (the two instantiations' instruction selection may fuse
+    a multiply-add differently), on a 24x48 grid whose groups span one to
+    many tiles; the second case's heads run as two shares, the second adding
+    into dh and dweights."""
+    field, heads, window, batch = case
+    mhsa, x, edges = build(field, heads, window, batch, nlat=24, nlon=48)
+    mhsa = mhsa.to(cuda, torch.float32)
+    probe = problems.normal((x.shape[0], mhsa.field_type_in.dimension), 5)
+    results = []
+    for stream in ("1", "0"):
+        monkeypatch.setenv("GM_FACTORED_ZDMA", stream)
+        print(f"staged-mix backward {case} GM_FACTORED_ZDMA={stream}", flush=True)
+        results.append(run(mhsa, x.to(cuda, torch.float32), edges.to(cuda, torch.float32), probe))
+
+    def near(got, want, name):
+        scale = float(want.abs().max())
+        err = float((got - want).abs().max())
+        assert err <= 1e-6 * scale, f"{name}: {err:.3e} of {scale:.3e}"
+
+    near(results[0][0], results[1][0], "out")
+    near(results[0][1]["x"], results[1][1]["x"], "x")
+    assert set(results[0][2]) == set(results[1][2])
+    for n in results[1][2]:  # sums over every edge or node (a vanishing key bias is rounding noise in both)
+        close(results[0][2][n], results[1][2][n], torch.float32, n, reduction=True)
