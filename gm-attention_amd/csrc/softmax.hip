@@ -154,6 +154,8 @@ constexpr uint32_t kOrders012 = 0x22110u;
 // and for the quotient.
 constexpr int kSmRegs = 16;
 constexpr bool kSmPrefetch = true;  // next step's source ids requested before this step's rows are used
+// Edges a lane of the per-target backward keeps alpha and dalpha of in registers (a multiple of 4).
+constexpr int kSmBwdRegs = 8;
 
 // One step's gathers for kSmStep edges of a lane: the chunks of the gathered
 // (key or query) rows and the transport pairs.
@@ -505,10 +507,13 @@ __global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
 
 // Backward per target: the adjoint's per-head total, ds, and dq.  ds goes to
 // its edge's place in the source grouping (inv), so the per-source pass reads
-// it as one stream.
+// it as one stream.  A lane's first RB edges keep their alpha and dalpha in
+// registers from the totals pass (rows up to RB * S edges, 64 at eight heads,
+// read them once); later edges read them again in the main loop.
 template <typename T, int NCH, uint32_t ORD, bool B16>
 __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a) {
-  constexpr int U = kSmStep;
+  static_assert(kSmStep == 1, "one edge a step");
+  constexpr int RB = kSmBwdRegs;
   const int64_t blk = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_nodes, kWavesPerBlock);
   const int lane = threadIdx.x & 63;
   const int64_t i = blk * kWavesPerBlock + (threadIdx.x >> 6);
@@ -517,8 +522,18 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
   const int h = lane & (H - 1), s = lane >> a.hshift;
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
 
+  T ar[RB], dr[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const int64_t f = e0 + s + (int64_t)r * S;
+    ar[r] = f < e1 ? a.alpha_in[f * H + h] : T(0);
+    dr[r] = f < e1 ? a.dalpha[f * H + h] : T(0);
+  }
   T total = T(0);
-  for (int64_t e = e0 + s; e < e1; e += 4 * S) {
+#pragma unroll
+  for (int r = 0; r < RB; r += 4)
+    total += (ar[r] * dr[r] + ar[r + 1] * dr[r + 1]) + (ar[r + 2] * dr[r + 2] + ar[r + 3] * dr[r + 3]);
+  for (int64_t e = e0 + s + (int64_t)RB * S; e < e1; e += 4 * S) {
     T p[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -529,60 +544,61 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
   }
   total = group_sum_pow2(total, H);
 
-  int64_t jn[U];
-  int32_t pn[U];
-  T an[U], dn[U];
-  auto fetch = [&](int64_t eb) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t e = eb + (int64_t)u * S;
-      const bool live = e < e1;
-      jn[u] = live ? a.source[e] : 0;
-      pn[u] = live ? a.inv[e] : 0;
-      an[u] = live ? a.alpha_in[e * H + h] : T(0);
-      dn[u] = live ? a.dalpha[e * H + h] : T(0);
+  int64_t jn = 0;
+  int32_t pn = 0;
+  T an = T(0), dn = T(0);
+  auto fetch = [&](int64_t e, bool values) {
+    const bool live = e < e1;
+    jn = live ? a.source[e] : 0;
+    pn = live ? a.inv[e] : 0;
+    if (values) {
+      an = live ? a.alpha_in[e * H + h] : T(0);
+      dn = live ? a.dalpha[e * H + h] : T(0);
     }
   };
   T acc[NCH * 4];
 #pragma unroll
   for (int u = 0; u < NCH * 4; ++u) acc[u] = T(0);
-  fetch(e0 + s);
-  for (int64_t eb = e0 + s; eb < e1; eb += (int64_t)U * S) {
-    int64_t jc[U], te[U];
-    int32_t pc[U];
-    T al[U], da[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t e = eb + (int64_t)u * S;
-      te[u] = e < e1 ? e : eb;
-      jc[u] = jn[u];
-      pc[u] = pn[u];
-      al[u] = an[u];
-      da[u] = dn[u];
-    }
-    fetch(eb + (int64_t)U * S);
+  // edge e of this lane (its gathers run whether or not it is live, on a clamped index), its source j
+  // and grouping place pc: ds and dq's terms
+  auto edge = [&](int64_t e, bool live, int64_t j, int32_t pc, T al, T da) {
+    int64_t jc[1] = {j}, te[1] = {live ? e : e0};
     Gather<T, NCH> g;
     gather<T, NCH, ORD>(a, g, rows_of<T, B16, true>(a), jc, a.transport, te, h);
+    if (!live) return;
+    const T ds = a.scale * al * (da - total);
+    a.ds[(int64_t)pc * H + h] = ds;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (eb + (int64_t)u * S >= e1) break;
-      const T ds = a.scale * al[u] * (da[u] - total);
-      a.ds[(int64_t)pc[u] * H + h] = ds;
+    for (int c = 0; c < NCH; ++c) {
+      const Quad<T>& k = g.row[0][c];
+      if (chunk_order<ORD>(a.C, c) == 0) {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const Quad<T>& k = g.row[u][c];
-        if (chunk_order<ORD>(a.C, c) == 0) {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * k.v[v];
-        } else {
-          const T cr = g.tc[u][c], ci = g.ts[u][c];
-          acc[4 * c + 0] += ds * (cr * k.v[0] - ci * k.v[1]);
-          acc[4 * c + 1] += ds * (cr * k.v[1] + ci * k.v[0]);
-          acc[4 * c + 2] += ds * (cr * k.v[2] - ci * k.v[3]);
-          acc[4 * c + 3] += ds * (cr * k.v[3] + ci * k.v[2]);
-        }
+        for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * k.v[v];
+      } else {
+        const T cr = g.tc[0][c], ci = g.ts[0][c];
+        acc[4 * c + 0] += ds * (cr * k.v[0] - ci * k.v[1]);
+        acc[4 * c + 1] += ds * (cr * k.v[1] + ci * k.v[0]);
+        acc[4 * c + 2] += ds * (cr * k.v[2] - ci * k.v[3]);
+        acc[4 * c + 3] += ds * (cr * k.v[3] + ci * k.v[2]);
       }
     }
+  };
+  fetch(e0 + s, false);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    if (e0 + (int64_t)r * S >= e1) break;  // the whole row is done (wave-uniform)
+    const int64_t e = e0 + s + (int64_t)r * S;
+    const int64_t jc = jn;
+    const int32_t pc = pn;
+    fetch(e + S, r + 1 == RB);  // the next step's ids (and, past the registers, its values)
+    edge(e, e < e1, jc, pc, ar[r], dr[r]);
+  }
+  for (int64_t e = e0 + s + (int64_t)RB * S; e < e1; e += S) {
+    const int64_t jc = jn;
+    const int32_t pc = pn;
+    const T al = an, da = dn;
+    fetch(e + S, true);
+    edge(e, true, jc, pc, al, da);
   }
 #pragma unroll
   for (int u = 0; u < NCH * 4; ++u) acc[u] = group_sum_pow2(acc[u], H);
