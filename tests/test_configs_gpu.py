@@ -6,6 +6,9 @@ oracle, at grid sizes the float64 oracle finishes in seconds:
   samples of 16x32 and of 24x48, the output, the input's gradient and every
   parameter's gradient;
 * C1: the 4-head {0:16,1:16,2:16} layer (D = 80) on one 32x64 sample, forward;
+* C3: ``SO2Convolution(depthwise=True, n_radial_basis=4)`` on {0:32,1:32,2:32},
+  hard window, radius 3 row spacings, the radial heads inside the walk,
+  two samples of 16x32 and of 24x48, every gradient;
 * C4: ``SO2TransformerBlock(ffn_multiplier=4)`` with 8 heads on
   {0:32,1:32,2:32} (160 -> 640 -> 160), bfloat16 rows and float32
   parameters, two 16x32 samples, against the float64 block on the same
@@ -127,6 +130,55 @@ def test_c1_layer_forward_matches_the_oracle(cuda):
     mhsa, x, edges = mhsa_case({0: 16, 1: 16, 2: 16}, 4, 32, 64, batch=1)
     assert mhsa.field_type_in.dimension == 80 and edges.source_index.shape[0] == 172288
     compare_mhsa(mhsa, x, edges, cuda, backward=False)
+
+
+@pytest.mark.parametrize("grid", [(16, 32), (24, 48)])
+def test_c3_convolution_matches_the_oracle(grid, cuda):
+    """C3: the depthwise steerable convolution with 4 radial functions on
+    {0:32,1:32,2:32}, two samples, float32 with the radial heads evaluated in
+    the walk, against the float64 oracle on the same rounded parameters and
+    inputs: the output and the input gradient at the north star's
+    elementwise bound, every parameter gradient as the sums they are."""
+    from gm_attention_amd.nn import depthwise_radial
+    from gm_attention_amd.nn.convolution import SO2Convolution
+
+    print(f"C3 convolution {grid} B=2", flush=True)
+    disc = problems.discretization(*grid)
+    edges = disc.edge_geometry.tile(2, n_sources=disc.n_nodes)
+    ft = SO2FieldType({0: 32, 1: 32, 2: 32})
+    torch.manual_seed(0)
+    conv = SO2Convolution(ft, ft, cutoff=disc.coverage_radius, window="hard", depthwise=True, n_radial_basis=4,
+                          dtype=D64)
+    conv.load_state_dict({k: v.float().double() for k, v in conv.state_dict().items()})
+    n = edges.row_ptr.shape[0] - 1
+    x = problems.normal((n, ft.dimension), 1).float().double()
+    probe = problems.normal(x.shape, 7)
+
+    def run(module, flat, eds, oracle):
+        leaf = flat.clone().requires_grad_(True)
+        module.zero_grad(set_to_none=True)
+        if oracle:
+            out = modules.flat(modules.conv_forward(module, dict(SO2FeatureField.from_flat(ft, leaf).coefficients),
+                                                    eds, 1e-5))
+        else:
+            out = module(SO2FeatureField.from_flat(ft, leaf), eds).to_flat()
+        (out.double() * probe.to(out.device)).sum().backward()
+        return out.detach(), leaf.grad, {k: p.grad for k, p in module.named_parameters() if p.grad is not None}
+
+    want = run(conv, x, edges.to(None, torch.float32).to(None, D64), True)
+    gpu = SO2Convolution(ft, ft, cutoff=disc.coverage_radius, window="hard", depthwise=True, n_radial_basis=4,
+                         dtype=torch.float32, device=cuda)
+    gpu.load_state_dict({k: v.float() for k, v in conv.state_dict().items()})
+    e32 = edges.to(cuda, torch.float32)
+    assert depthwise_radial.eligible(gpu.kernel, SO2FeatureField.from_flat(ft, x.to(cuda, torch.float32)), e32)
+    got = run(gpu, x.to(cuda, torch.float32), e32, False)
+    print(f"  out elementwise {strict_report(got[0], want[0]):.2f}", flush=True)
+    assert_strict(got[0], want[0], "out")
+    print(f"  dx elementwise {strict_report(got[1], want[1]):.2f}", flush=True)
+    assert_strict(got[1], want[1], "dx")
+    assert set(got[2]) == set(want[2]) and len(want[2]) > 0
+    for name in want[2]:
+        assert_reduction(got[2][name], want[2][name], f"d{name}")
 
 
 def test_c4_block_in_bfloat16_is_within_2e2(cuda):

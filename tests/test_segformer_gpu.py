@@ -6,7 +6,8 @@ softmax at D = 640, the restrictions' tiled factored aggregates, the low-pass
 interpolations on the gather kernels) on a small two-sample hierarchy,
 float32, against the oracle's float64 composition of the reference's model
 (oracle.modules.segformer_forward): the logits and the input's gradient
-elementwise within 1e-5 relative / 1e-6 absolute (of the largest entry),
+elementwise within 1e-5 |want| + 1e-6 (the north star's bound, the absolute
+term unscaled),
 every parameter gradient within 1e-5 of its norm and its largest entry, or,
 for a gradient whose float32 value is dominated by cancellation (a query
 bias: a sum over every node of softmax gradients that sum to zero per
@@ -34,6 +35,12 @@ def report(got, want):
     return float(((got - want).abs() / (1e-5 * want.abs() + 1e-6 * float(want.abs().max()))).max())
 
 
+def strict(got, want):
+    """max |g - w| / (1e-5 |w| + 1e-6): the north star's elementwise bound with an unscaled absolute term."""
+    want, got = want.double().cpu(), got.double().cpu()
+    return float(((got - want).abs() / (1e-5 * want.abs() + 1e-6)).max())
+
+
 def test_c5_model_matches_the_oracle(cuda):
     radii = stage_radii(STAGES)
     h = build_stage_hierarchy(IMG, STAGES, radii).tile(2)
@@ -58,7 +65,10 @@ def test_c5_model_matches_the_oracle(cuda):
     got = run(gpu, x0.float().to(cuda), h.to(cuda, torch.float32), probe)
     assert eager_ops.calls == before, "part of the model fell back to the eager path"
     out, dx = report(got[0], want[0]), report(got[1], want[1])
-    print(f"strict ratio: logits {out:.3f}, dx {dx:.3f}", flush=True)
+    print(f"scaled ratio: logits {out:.3f}, dx {dx:.3f}; unscaled (1e-5 |w| + 1e-6): logits "
+          f"{strict(got[0], want[0]):.3f}, dx {strict(got[1], want[1]):.3f}", flush=True)
+    # the north star's bound with its absolute term unscaled (measured 0.17 and 0.15 of it)
+    assert strict(got[0], want[0]) <= 1.0 and strict(got[1], want[1]) <= 1.0
     assert out <= 1.0 and dx <= 1.0
     assert set(got[2]) == set(want[2])
     worst = 0.0
