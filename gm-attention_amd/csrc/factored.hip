@@ -120,6 +120,9 @@ struct FactArgs {
   float trunk_c[8];
   float trunk_inv_width;
   int trunk_nb;
+  // lane-owned kernels with compiled-in slots: h, the rows and dh are
+  // bfloat16 (the pointers above then address 2-byte elements)
+  int b16;
 };
 
 template <typename T>
@@ -335,7 +338,9 @@ constexpr int kAggStep = 4;  // edges a step: 55 VGPRs, eight waves a SIMD (eigh
 // u Ha + h: edge u, column h) and reach the lanes that use them by lane
 // shuffles, so an edge costs its row pieces' vector load alone.
 
-template <int P>
+// B16: the rows are bfloat16 (four to an 8-byte piece, widened exactly), the
+// sums float32.
+template <int P, bool B16 = false>
 __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a) {
   const int64_t i = xcd_balanced_block(blockIdx.x, gridDim.x, a.row_ptr, a.n_targets, kWavesPerBlock) * kWavesPerBlock +
                     __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -344,15 +349,24 @@ __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a
   const int q4 = a.d_out / 4, W4 = a.H * q4, Ha = a.H / a.split;
   bool live[P];
   int ha[P];
-  const float* base[P];
+  int64_t base[P];  // element offsets of the lane's pieces in row 0
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int o = lane + 64 * p;
     live[p] = o < W4;
     const int hh = live[p] ? o / q4 : 0, c4 = live[p] ? o - hh * q4 : 0;
     ha[p] = hh / a.split;
-    base[p] = a.rows + (int64_t)hh * a.n_rows * a.d_out + 4 * c4;
+    base[p] = (int64_t)hh * a.n_rows * a.d_out + 4 * c4;
   }
+  auto piece = [&](int p, int64_t row) -> floatx4 {
+    if constexpr (B16) {
+      const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.rows) + base[p] +
+                                                      row * a.d_out);
+      return floatx4{bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y)};
+    } else {
+      return *reinterpret_cast<const floatx4*>(a.rows + base[p] + row * a.d_out);
+    }
+  };
   const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
   floatx4 s[P];
 #pragma unroll
@@ -384,7 +398,7 @@ __global__ __launch_bounds__(256) void aggregate_heads_vec_kernel(AggHeadsArgs a
         } else {
           w[u][p] = in ? a.alpha[(e + u) * Ha + ha[p]] : 0.f;
         }
-        v[u][p] = in ? *reinterpret_cast<const floatx4*>(base[p] + r[u] * a.d_out) : floatx4{0.f, 0.f, 0.f, 0.f};
+        v[u][p] = in ? piece(p, r[u]) : floatx4{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
     for (int u = 0; u < kAggStep; ++u) {
@@ -1354,6 +1368,86 @@ __device__ __forceinline__ void bstore4(floatx4 v, __amdgpu_buffer_rsrc_t r, int
 }
 constexpr int kDrop = 0x7FFFFFF0;  // a byte offset past every group's span: the access is dropped
 
+// Per-edge streams (trunk features h and their gradients dh, output rows) by
+// element index: float32, or with B16 bfloat16 (rounded to nearest even on
+// store, widened exactly on load) at half the bytes.  Arithmetic is float32
+// either way.
+template <bool B16>
+__device__ __forceinline__ int64_t stream_bytes(int64_t n) {
+  return n * (B16 ? 2 : 4);
+}
+template <bool B16>
+__device__ __forceinline__ void sstore1(float v, __amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (B16)
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)(pack_bf16(v, 0.f) & 0xFFFFu), r, 2 * i, 0, 0);
+  else
+    bstore1(v, r, 4 * i);
+}
+template <bool B16>
+__device__ __forceinline__ void sstore2(float x, float y, __amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (B16)
+    __builtin_amdgcn_raw_buffer_store_b32(pack_bf16(x, y), r, 2 * i, 0, 0);
+  else
+    bstore2(x, y, r, 4 * i);
+}
+template <bool B16>
+__device__ __forceinline__ void sstore4(floatx4 v, __amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (B16) {
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(u2{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])}, r, 2 * i, 0, 0);
+  } else {
+    bstore4(v, r, 4 * i);
+  }
+}
+template <bool B16>
+__device__ __forceinline__ float sload1(__amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (B16)
+    return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, 2 * i, 0, 0) << 16);
+  else
+    return bload1(r, 4 * i);
+}
+template <bool B16>
+__device__ __forceinline__ float2 sload2(__amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (B16) {
+    const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r, 2 * i, 0, 0);
+    return make_float2(bf16_lo(v), bf16_hi(v));
+  } else {
+    return bload2(r, 4 * i);
+  }
+}
+// A lane's four trunk features: with bfloat16 streams kept packed (the two
+// words as the bit patterns of h[0] and h[1]) until hwiden turns them into
+// floats where they are used, so two tiles in flight hold half the registers.
+template <bool B16>
+__device__ __forceinline__ floatx4 hload(__amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (B16) {
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(r, 2 * i, 0, 0);
+    return floatx4{__uint_as_float(v[0]), __uint_as_float(v[1]), 0.f, 0.f};
+  } else {
+    return bload4(r, 4 * i);
+  }
+}
+template <bool B16>
+__device__ __forceinline__ floatx4 hwiden(const floatx4& h) {
+  if constexpr (B16) {
+    const uint32_t a = __float_as_uint(h[0]), b = __float_as_uint(h[1]);
+    return floatx4{bf16_lo(a), bf16_hi(a), bf16_lo(b), bf16_hi(b)};
+  } else {
+    return h;
+  }
+}
+template <bool B16>
+__device__ __forceinline__ floatx4 sload4(__amdgpu_buffer_rsrc_t r, int i) {
+  if constexpr (B16) {
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    const u2 v = __builtin_amdgcn_raw_buffer_load_b64(r, 2 * i, 0, 0);
+    return floatx4{bf16_lo(v[0]), bf16_hi(v[0]), bf16_lo(v[1]), bf16_hi(v[1])};
+  } else {
+    return bload4(r, 4 * i);
+  }
+}
+
 // SlotsF2 by Horner's rule.  With z = r e^{i phi}, w = e^{i gamma} and
 // p = z conj(w), the thirteen factors are
 //   output 0 (real part): 1, p, p^2                      (slots 0, 1, 2)
@@ -1401,6 +1495,7 @@ __device__ __forceinline__ void cjmul(float xr, float xi, float yr, float yi, fl
 }
 
 // Forward: edge m's three outputs from u (slot s at acc[s / 2][2 (s % 2)], +1 imaginary), stored.
+template <bool B16>
 __device__ __forceinline__ void f2_forward_outputs(const floatx4 (&acc)[7], const floatx4& zw,
                                                    __amdgpu_buffer_rsrc_t out_r, int row, int q) {
   const F2Powers f = f2_powers(zw);
@@ -1408,7 +1503,7 @@ __device__ __forceinline__ void f2_forward_outputs(const floatx4 (&acc)[7], cons
   float tr, ti, vr, vi;
   // output 0: Re(u0) + Re(p (u1 + p u2))
   cmac(f.pr, f.pi, GM_U(2), GM_U(1), tr, ti);
-  bstore1(fmaf(f.pr, tr, fmaf(-f.pi, ti, acc[0][0])), out_r, (row + q) * 4);
+  sstore1<B16>(fmaf(f.pr, tr, fmaf(-f.pi, ti, acc[0][0])), out_r, row + q);
   // output 1: z (u3 + p (u5 + p u7)) + w u4 + conj(z) w^2 u6
   const float zr = zw[0], zi = zw[1], wr = zw[2], wi = zw[3];
   cmac(f.pr, f.pi, GM_U(7), GM_U(5), tr, ti);
@@ -1418,7 +1513,7 @@ __device__ __forceinline__ void f2_forward_outputs(const floatx4 (&acc)[7], cons
   cmac(f.cr, f.ci, GM_U(6), vr, vi, vr, vi);
   cmac(wr, wi, GM_U(4), vr, vi, vr, vi);
   cmac(zr, zi, tr, ti, vr, vi, vr, vi);
-  bstore2(vr, vi, out_r, (row + 4 + 2 * q) * 4);
+  sstore2<B16>(vr, vi, out_r, row + 4 + 2 * q);
   // output 2: z^2 (u8 + p (u10 + p u12)) + z w u9 + w^2 u11
   cmac(f.pr, f.pi, GM_U(12), GM_U(10), tr, ti);
   cmac(f.pr, f.pi, tr, ti, GM_U(8), tr, ti);
@@ -1427,7 +1522,7 @@ __device__ __forceinline__ void f2_forward_outputs(const floatx4 (&acc)[7], cons
   cmac(f.w2r, f.w2i, GM_U(11), vr, vi, vr, vi);
   cmac(f.zwr, f.zwi, GM_U(9), vr, vi, vr, vi);
   cmac(f.z2r, f.z2i, tr, ti, vr, vi, vr, vi);
-  bstore2(vr, vi, out_r, (row + 12 + 2 * q) * 4);
+  sstore2<B16>(vr, vi, out_r, row + 12 + 2 * q);
 #undef GM_U
 }
 
@@ -1703,7 +1798,7 @@ struct FwdTile {
 };
 
 // ph_r spans the zw rows (fixed slots) or the phase rows (runtime slots).
-template <class P>
+template <class P, bool B16 = false>
 __device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amdgpu_buffer_rsrc_t ph_r,
                                                __amdgpu_buffer_rsrc_t rho_r, int tb, int m, int q, bool fused) {
   FwdTile<P> t;
@@ -1711,7 +1806,7 @@ __device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amd
   if (fused) {
     t.h = floatx4{0.f, 0.f, 0.f, 0.f};
   } else {
-    t.h = bload4(h_r, (e * 16 + 4 * q) * 4);
+    t.h = hload<B16>(h_r, e * 16 + 4 * q);
   }
   if constexpr (P::kStatic) {
     t.ph.ph = bload4(ph_r, e * 16);
@@ -1725,12 +1820,12 @@ __device__ __forceinline__ FwdTile<P> load_fwd(__amdgpu_buffer_rsrc_t h_r, __amd
 
 // Edge m's outputs from u (slot s at acc[s / 2][2 (s % 2)], +1 imaginary):
 // V = F u per slot, summed over each output's slots and stored.
-template <int NT, class P>
+template <int NT, class P, bool B16 = false>
 __device__ __forceinline__ void forward_outputs(const FactArgs<float>& a, const FwdTile<P>& cur,
                                                 const floatx4 (&acc)[NT], float* Ph, __amdgpu_buffer_rsrc_t out_r,
                                                 int d_out, int tb, int m, int q) {
   if constexpr (kHorner<P>) {
-    f2_forward_outputs(acc, cur.ph.ph, out_r, (tb + m) * d_out, q);
+    f2_forward_outputs<B16>(acc, cur.ph.ph, out_r, (tb + m) * d_out, q);
     return;
   }
   Powers<P> pw;
@@ -1760,9 +1855,9 @@ __device__ __forceinline__ void forward_outputs(const FactArgs<float>& a, const 
     }
     if (w & kSlotFlush) {
       if (w & kSlotScalar)
-        bstore1(sr, out_r, (row + slot_ob(w) + q) * 4);
+        sstore1<B16>(sr, out_r, row + slot_ob(w) + q);
       else
-        bstore2(sr, si, out_r, (row + slot_ob(w) + 2 * q) * 4);
+        sstore2<B16>(sr, si, out_r, row + slot_ob(w) + 2 * q);
       sr = 0.f;
       si = 0.f;
     }
@@ -1771,13 +1866,13 @@ __device__ __forceinline__ void forward_outputs(const FactArgs<float>& a, const 
 }
 
 // One forward tile: 16 edges from tb, the rows stored through out_r.
-template <int NT, class P>
+template <int NT, class P, bool B16 = false>
 __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const FwdTile<P>& cur, const float (&za)[NT][4],
                                              const floatx4 (&z0)[NT], float* Ph, __amdgpu_buffer_rsrc_t out_r,
                                              int d_out, int tb, int m, int q, const TrunkLane& tl, bool fused) {
   // h(edge m)[4 q .. 4 q + 3]: read, or the trunk's features evaluated here
   floatx4 pre;
-  const floatx4 h = fused ? trunk_features(a, tl, q, cur.rho, pre) : cur.h;
+  const floatx4 h = fused ? trunk_features(a, tl, q, cur.rho, pre) : hwiden<B16>(cur.h);
   // u(e) = Z0 + sum_t h_t Z_t: lane (m, q) ends with edge m's slot columns 16 nt + 4 q + r
   floatx4 acc[NT];
 #pragma unroll
@@ -1786,31 +1881,46 @@ __device__ __forceinline__ void forward_tile(const FactArgs<float>& a, const Fwd
   for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[nt] = mfma16(za[nt][s], h[s], acc[nt]);
-  forward_outputs<NT, P>(a, cur, acc, Ph, out_r, d_out, tb, m, q);
+  forward_outputs<NT, P, B16>(a, cur, acc, Ph, out_r, d_out, tb, m, q);
 }
 
 // forward_tile with the product on the bf16 matrix cores (fixed slots, trunk
 // features read): Z's pieces for the lane's features 4 q .. 4 q + 3 at columns
 // 16 nt + m are held for the group, h's are split per tile.
 // Z's row 0 (the bias feature) is read from the LDS copy per tile.
-template <int NT, class P>
+// With B16 the features are bfloat16 values, their own single piece: the
+// three piece products of Z's pieces hi, mid and lo with h in two
+// instructions.
+template <int NT, class P, bool B16 = false>
 __device__ __forceinline__ void forward_tile_split(const FactArgs<float>& a, const FwdTile<P>& cur,
                                                    const SplitA (&zs)[NT], const float* Zs, float* Ph,
                                                    __amdgpu_buffer_rsrc_t out_r, int d_out, int tb, int m, int q) {
-  const SplitB hb = split_b(cur.h[0], cur.h[1], cur.h[2], cur.h[3]);
   floatx4 acc[NT];
+  if constexpr (B16) {
+    const uint32_t h01 = __float_as_uint(cur.h[0]), h23 = __float_as_uint(cur.h[1]);  // the packed features
+    const u32x4 hh{h01, h23, h01, h23}, zh{0u, 0u, h01, h23};
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    acc[nt] = mfma_split(zs[nt], hb, *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q));
-  forward_outputs<NT, P>(a, cur, acc, Ph, out_r, d_out, tb, m, q);
+    for (int nt = 0; nt < NT; ++nt) {
+      floatx4 c = mfma_bf16(zs[nt].hl, zh, *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q));  // lo h
+      acc[nt] = mfma_bf16(zs[nt].hm, hh, c);                                                          // hi h + mid h
+    }
+  } else {
+    const SplitB hb = split_b(cur.h[0], cur.h[1], cur.h[2], cur.h[3]);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      acc[nt] = mfma_split(zs[nt], hb, *reinterpret_cast<const floatx4*>(Zs + 16 * nt + 4 * q));
+  }
+  forward_outputs<NT, P, B16>(a, cur, acc, Ph, out_r, d_out, tb, m, q);
 }
 
 // SPLIT (fixed slots, trunk features read): the product on the bf16 matrix
-// cores in fp32 accuracy.
-template <int NT, class P, bool FUSED, bool SPLIT>
+// cores in fp32 accuracy.  B16 (fixed slots, trunk features read): h read and
+// the rows stored in bfloat16.
+template <int NT, class P, bool FUSED, bool SPLIT, bool B16 = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED || SPLIT ? 3 : 4) : 1))) void
 factored_forward_lanes(FactArgs<float> a) {
   static_assert(!SPLIT || (P::kStatic && !FUSED), "the split product serves fixed slots with trunk features read");
+  static_assert(!B16 || (P::kStatic && !FUSED), "bfloat16 streams serve fixed slots with trunk features read");
   constexpr int ZS = 16 * NT + 4;
   __shared__ __align__(16) float Zs[17 * ZS];
   __shared__ __align__(16) float Ph[P::kStatic ? 4 : kMT * kPhStride];
@@ -1823,16 +1933,19 @@ factored_forward_lanes(FactArgs<float> a) {
   const int64_t g0 = a.group_ptr[gi];
   const int ng = (int)(a.group_ptr[gi + 1] - g0);
   constexpr bool fused = FUSED;
-  const auto h_r = span(fused ? nullptr : a.h + g0 * 16, fused ? 0 : (int64_t)ng * 64);
+  // h and the rows: float32, or bfloat16 (B16) at half the bytes
+  const char* h_b = reinterpret_cast<const char*>(a.h);
+  char* out_b = reinterpret_cast<char*>(a.out);
+  const auto h_r = span(fused ? nullptr : h_b + stream_bytes<B16>(g0 * 16), fused ? 0 : stream_bytes<B16>((int64_t)ng * 16));
   const auto ph_r = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
                                : span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
   const auto rho_r = span(a.rho_g + g0, (int64_t)ng * 4);
-  const auto out_r = span(a.out + g0 * d_out, (int64_t)ng * d_out * 4);
+  const auto out_r = span(out_b + stream_bytes<B16>(g0 * d_out), stream_bytes<B16>((int64_t)ng * d_out));
   // two tiles in flight: each buffer is refilled right after its tile's
   // stores, so waiting for a tile never waits for the previous tile's stores.
   // The first two are requested with the node's mixes (one round trip).
-  FwdTile<P> ta = load_fwd<P>(h_r, ph_r, rho_r, 0, m, q, fused);
-  FwdTile<P> tbf = load_fwd<P>(h_r, ph_r, rho_r, kMT, m, q, fused);
+  FwdTile<P> ta = load_fwd<P, B16>(h_r, ph_r, rho_r, 0, m, q, fused);
+  FwdTile<P> tbf = load_fwd<P, B16>(h_r, ph_r, rho_r, kMT, m, q, fused);
   stage_colslot(a, colslot, lane);
   ZStage zst;
   z_issue<P::kStatic>(a, j, lane, zst);
@@ -1858,17 +1971,17 @@ factored_forward_lanes(FactArgs<float> a) {
   if (fused) tl = trunk_lane(a, m, q);
   for (int tb = 0;;) {
     if constexpr (SPLIT)
-      forward_tile_split<NT, P>(a, ta, zs, Zs, Ph, out_r, d_out, tb, m, q);
+      forward_tile_split<NT, P, B16>(a, ta, zs, Zs, Ph, out_r, d_out, tb, m, q);
     else
-      forward_tile<NT, P>(a, ta, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
-    ta = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
+      forward_tile<NT, P, B16>(a, ta, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
+    ta = load_fwd<P, B16>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
     tb += kMT;
     if (tb >= ng) break;
     if constexpr (SPLIT)
-      forward_tile_split<NT, P>(a, tbf, zs, Zs, Ph, out_r, d_out, tb, m, q);
+      forward_tile_split<NT, P, B16>(a, tbf, zs, Zs, Ph, out_r, d_out, tb, m, q);
     else
-      forward_tile<NT, P>(a, tbf, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
-    tbf = load_fwd<P>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
+      forward_tile<NT, P, B16>(a, tbf, za, z0, Ph, out_r, d_out, tb, m, q, tl, fused);
+    tbf = load_fwd<P, B16>(h_r, ph_r, rho_r, tb + 2 * kMT, m, q, fused);
     tb += kMT;
     if (tb >= ng) break;
   }
@@ -1884,14 +1997,14 @@ struct BwdTile {
   float dw_old;     // accumulating: dweights(edge m) already in the output
 };
 
-template <class P>
+template <class P, bool B16 = false>
 __device__ __forceinline__ BwdTile<P> load_bwd(__amdgpu_buffer_rsrc_t h_r, __amdgpu_buffer_rsrc_t ph_r,
                                                __amdgpu_buffer_rsrc_t rho_r, __amdgpu_buffer_rsrc_t w_r,
                                                __amdgpu_buffer_rsrc_t t_r, int tb, int m, int q, bool fused,
                                                __amdgpu_buffer_rsrc_t dh_r, __amdgpu_buffer_rsrc_t dw_r, bool acc) {
   BwdTile<P> t;
   const int e = tb + m;
-  t.h = fused ? floatx4{0.f, 0.f, 0.f, 0.f} : bload4(h_r, (e * 16 + 4 * q) * 4);
+  t.h = fused ? floatx4{0.f, 0.f, 0.f, 0.f} : hload<B16>(h_r, e * 16 + 4 * q);
   if constexpr (P::kStatic) {
     t.ph.ph = bload4(ph_r, e * 16);
     t.tgt = 0;
@@ -1903,7 +2016,7 @@ __device__ __forceinline__ BwdTile<P> load_bwd(__amdgpu_buffer_rsrc_t h_r, __amd
   }
   t.w = bload1(w_r, e * 4);
   if (acc) {
-    t.dh_old = bload4(dh_r, (e * 16 + 4 * q) * 4);
+    t.dh_old = sload4<B16>(dh_r, e * 16 + 4 * q);
     t.dw_old = bload1(dw_r, e * 4);
   } else {
     t.dh_old = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -1919,7 +2032,7 @@ struct OutVals {
   float gr[2 * NT], gi[2 * NT], rr[2 * NT], ri[2 * NT];
 };
 
-template <int NT, class P>
+template <int NT, class P, bool B16 = false>
 __device__ __forceinline__ void load_outs(OutVals<NT>& v, const float* grow, __amdgpu_buffer_rsrc_t rows_r, int row,
                                           int q) {
 #pragma unroll
@@ -1930,12 +2043,12 @@ __device__ __forceinline__ void load_outs(OutVals<NT>& v, const float* grow, __a
       const int o = slot_ob(w) + q;
       v.gr[s] = grow[o];
       v.gi[s] = 0.f;
-      v.rr[s] = bload1(rows_r, (row + o) * 4);
+      v.rr[s] = sload1<B16>(rows_r, row + o);
       v.ri[s] = 0.f;
     } else {
       const int o = slot_ob(w) + 2 * q;
       const float2 gv = *reinterpret_cast<const float2*>(grow + o);
-      const float2 rv = bload2(rows_r, (row + o) * 4);
+      const float2 rv = sload2<B16>(rows_r, row + o);
       v.gr[s] = gv.x;
       v.gi[s] = gv.y;
       v.rr[s] = rv.x;
@@ -1950,7 +2063,7 @@ struct BwdSpans {
 
 // One backward tile: 16 edges from tb; dh and dweights stored, dZ
 // accumulated in registers.
-template <int NT, class P, class O>
+template <int NT, class P, class O, bool B16 = false>
 __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const BwdTile<P>& cur, const O& outs,
                                               const floatx4 (&zb)[NT], floatx4 (&dz)[NT], float (&dz0)[NT], float* Sh,
                                               float* Ph, float* Gt, int64_t* Tg, float* Hs, const BwdSpans& sp,
@@ -1961,7 +2074,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
   // handed to the dZ operand's layout (feature m of edges 4 q + i) through Hs with the
   // W transpose below
   floatx4 pre;
-  const floatx4 hf = fused ? trunk_features(a, tl, q, cur.rho, pre) : cur.h;
+  const floatx4 hf = fused ? trunk_features(a, tl, q, cur.rho, pre) : hwiden<B16>(cur.h);
   *reinterpret_cast<floatx4*>(Hs + m * kHsStride + 4 * q) = hf;
   float wv[NT][4];
   float dwp = 0.f;  // this lane's share of dweights(edge m)
@@ -2018,7 +2131,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
       for (int o = m; o < GS; o += kMT) Gt[e * GS + o] = grow && o < d_out ? grow[o] : 0.f;
     }
     wave_sync();
-    for (int o = q; o < d_out; o += 4) dwp += Gt[m * GS + o] * bload1(sp.rows, (row + o) * 4);
+    for (int o = q; o < d_out; o += 4) dwp += Gt[m * GS + o] * sload1<B16>(sp.rows, row + o);
     const float* prow = Ph + m * kPhStride;
     const float* gq1 = Gt + m * GS + q;
     const float* gq2 = Gt + m * GS + 2 * q;
@@ -2044,7 +2157,7 @@ __device__ __forceinline__ void backward_tile(const FactArgs<float>& a, const Bw
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       if (kstep_live<P>(a, nt, r)) dh = mfma16(zb[nt][r], wv[nt][r], dh);
-  bstore4(dh + cur.dh_old, sp.dh, ((tb + m) * 16 + 4 * q) * 4);
+  sstore4<B16>(dh + cur.dh_old, sp.dh, (tb + m) * 16 + 4 * q);
   // W through LDS, column-major, for dZ's edge-major operand
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
@@ -2101,10 +2214,12 @@ __device__ __forceinline__ void z_stream(const FactArgs<float>& a, int64_t j, fl
 
 // ACC: dh and dweights added into the outputs (a later share of a head).
 // ZDMA (compiled-in slots, trunk read): the mixes by direct-to-LDS loads (z_stream).
-template <int NT, class P, bool FUSED, bool ACC, bool ZDMA = false>
+// B16 (compiled-in slots, trunk read): h, the rows and dh in bfloat16.
+template <int NT, class P, bool FUSED, bool ACC, bool ZDMA = false, bool B16 = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(P::kStatic ? (FUSED || P::kDout > 40 ? 2 : 3) : 1))) void
 factored_backward_lanes(FactArgs<float> a) {
   static_assert(!ZDMA || (P::kStatic && !FUSED), "the staged-mix form serves fixed slots with trunk features read");
+  static_assert(!B16 || (P::kStatic && !FUSED), "bfloat16 streams serve fixed slots with trunk features read");
   constexpr int ZS = 16 * NT + 4;
   constexpr int kZWords = 17 * ZS, kWWords = 16 * NT * kWtStride;
   __shared__ __align__(16) float Sh[kZWords > kWWords ? kZWords : kWWords];  // Z in, then W's transpose, then dZ out
@@ -2123,14 +2238,18 @@ factored_backward_lanes(FactArgs<float> a) {
   const int ng = (int)(a.group_ptr[gi + 1] - g0);
   constexpr bool fused = FUSED;
   BwdSpans sp;
-  sp.h = span(fused ? nullptr : a.h + g0 * 16, fused ? 0 : (int64_t)ng * 64);
+  // h, the rows and dh: float32, or bfloat16 (B16) at half the bytes
+  const char* h_b = reinterpret_cast<const char*>(a.h);
+  const char* rows_b = reinterpret_cast<const char*>(a.rows);
+  char* dh_b = reinterpret_cast<char*>(a.dh);
+  sp.h = span(fused ? nullptr : h_b + stream_bytes<B16>(g0 * 16), fused ? 0 : stream_bytes<B16>((int64_t)ng * 16));
   sp.ph = P::kStatic ? span(a.zw_g + g0 * 4, (int64_t)ng * 16)
                      : span(a.phase_g + g0 * kPhaseRow, (int64_t)ng * kPhaseRow * 4);
   sp.rho = span(a.rho_g + g0, (int64_t)ng * 4);
   sp.w = span(a.weights + g0, (int64_t)ng * 4);
   sp.t = span(a.target_g + g0, (int64_t)ng * 8);
-  sp.rows = span(a.rows + g0 * d_out, (int64_t)ng * d_out * 4);
-  sp.dh = span(a.dh + g0 * 16, (int64_t)ng * 64);
+  sp.rows = span(rows_b + stream_bytes<B16>(g0 * d_out), stream_bytes<B16>((int64_t)ng * d_out));
+  sp.dh = span(dh_b + stream_bytes<B16>(g0 * 16), stream_bytes<B16>((int64_t)ng * 16));
   sp.dw = span(a.dweights + g0, (int64_t)ng * 4);
   constexpr bool acc = ACC;
   // Two tiles in flight (buffers A and B, each refilled right after its
@@ -2139,8 +2258,8 @@ factored_backward_lanes(FactArgs<float> a) {
   // for within the tile after the one that issued it.
   // The first tiles' streams and targets are requested with the node's mixes
   // (one round trip), then the targets' gradient values.
-  BwdTile<P> ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, 0, m, q, fused, sp.dh, sp.dw, acc);
-  BwdTile<P> tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, kMT, m, q, fused, sp.dh, sp.dw, acc);
+  BwdTile<P> ta = load_bwd<P, B16>(sp.h, sp.ph, sp.rho, sp.w, sp.t, 0, m, q, fused, sp.dh, sp.dw, acc);
+  BwdTile<P> tbf = load_bwd<P, B16>(sp.h, sp.ph, sp.rho, sp.w, sp.t, kMT, m, q, fused, sp.dh, sp.dw, acc);
   int64_t t0 = 0, t1 = 0;
   if constexpr (P::kStatic) {
     t0 = bload_i64(sp.t, m * 8);
@@ -2158,8 +2277,8 @@ factored_backward_lanes(FactArgs<float> a) {
   OutVals<P::kStatic ? NT : 1> oa, ob;
   int64_t tn = 0;  // static slots: the targets of the tile two ahead of the current one
   if constexpr (P::kStatic) {
-    load_outs<NT, P>(oa, a.g + t0 * a.g_ld, sp.rows, m * d_out, q);
-    load_outs<NT, P>(ob, a.g + t1 * a.g_ld, sp.rows, (kMT + m) * d_out, q);
+    load_outs<NT, P, B16>(oa, a.g + t0 * a.g_ld, sp.rows, m * d_out, q);
+    load_outs<NT, P, B16>(ob, a.g + t1 * a.g_ld, sp.rows, (kMT + m) * d_out, q);
     tn = bload_i64(sp.t, (2 * kMT + m) * 8);
   }
   // Z_t(j) for t = 1 + m at the lane's slot columns 16 nt + 4 q + r
@@ -2191,20 +2310,22 @@ factored_backward_lanes(FactArgs<float> a) {
   TrunkLane tl{};
   if (fused) tl = trunk_lane(a, m, q);
   for (int tb = 0;;) {
-    backward_tile<NT, P>(a, ta, oa, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl, fused);
+    backward_tile<NT, P, decltype(oa), B16>(a, ta, oa, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl,
+                                            fused);
     if constexpr (P::kStatic) {
-      load_outs<NT, P>(oa, a.g + tn * a.g_ld, sp.rows, (tb + 2 * kMT + m) * d_out, q);
+      load_outs<NT, P, B16>(oa, a.g + tn * a.g_ld, sp.rows, (tb + 2 * kMT + m) * d_out, q);
       tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
     }
-    ta = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused, sp.dh, sp.dw, acc);
+    ta = load_bwd<P, B16>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused, sp.dh, sp.dw, acc);
     tb += kMT;
     if (tb >= ng) break;
-    backward_tile<NT, P>(a, tbf, ob, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl, fused);
+    backward_tile<NT, P, decltype(ob), B16>(a, tbf, ob, zb, dz, dz0, Sh, Ph, Gt, Tg, Hs, sp, d_out, ng, tb, m, q, tl,
+                                            fused);
     if constexpr (P::kStatic) {
-      load_outs<NT, P>(ob, a.g + tn * a.g_ld, sp.rows, (tb + 2 * kMT + m) * d_out, q);
+      load_outs<NT, P, B16>(ob, a.g + tn * a.g_ld, sp.rows, (tb + 2 * kMT + m) * d_out, q);
       tn = bload_i64(sp.t, (tb + 3 * kMT + m) * 8);
     }
-    tbf = load_bwd<P>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused, sp.dh, sp.dw, acc);
+    tbf = load_bwd<P, B16>(sp.h, sp.ph, sp.rho, sp.w, sp.t, tb + 2 * kMT, m, q, fused, sp.dh, sp.dw, acc);
     tb += kMT;
     if (tb >= ng) break;
   }
@@ -2626,10 +2747,38 @@ inline bool zdma_backward() {
   return v == nullptr || v[0] != '0';
 }
 
+// The lane-owned kernels over bfloat16 streams (compiled-in slots, trunk features read).
+template <int NT, class P>
+void launch_lanes_b16(bool forward, const FactArgs<float>& a, hipStream_t stream) {
+  const dim3 grid((unsigned)a.n_groups), block(64);
+  if (forward) {
+    if (split_products())
+      hipLaunchKernelGGL((factored_forward_lanes<NT, P, false, true, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((factored_forward_lanes<NT, P, false, false, true>), grid, block, 0, stream, a);
+    return;
+  }
+  constexpr int area = 17 * (16 * NT + 4) > 16 * NT * kWtStride ? 17 * (16 * NT + 4) : 16 * NT * kWtStride;
+  FactArgs<float> za = a;
+  if (zdma_backward() && prepare_zq(za, 1, area)) {
+    if (a.accumulate)
+      hipLaunchKernelGGL((factored_backward_lanes<NT, P, false, true, true, true>), grid, block, 0, stream, za);
+    else
+      hipLaunchKernelGGL((factored_backward_lanes<NT, P, false, false, true, true>), grid, block, 0, stream, za);
+  } else if (a.accumulate) {
+    hipLaunchKernelGGL((factored_backward_lanes<NT, P, false, true, false, true>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((factored_backward_lanes<NT, P, false, false, false, true>), grid, block, 0, stream, a);
+  }
+}
+
 template <int NT, class P = RuntimeSlots>
 void launch_lanes_nt(bool forward, const FactArgs<float>& a, hipStream_t stream) {
   const dim3 grid((unsigned)a.n_groups), block(64);
   const bool fused = a.trunk_w != nullptr;  // the trunk evaluated in the kernels: their own instantiation
+  if constexpr (P::kStatic) {
+    if (a.b16) return launch_lanes_b16<NT, P>(forward, a, stream);
+  }
   if (forward) {
     if (fused)
       hipLaunchKernelGGL((factored_forward_lanes<NT, P, true, false>), grid, block, 0, stream, a);
@@ -2667,6 +2816,17 @@ bool matches(const FactArgs<float>& a) {
     if (a.slot[s] != P::word(s)) return false;
   return true;
 }
+
+// Whether a plan's lane slots are one of the compiled-in tables
+// (GM_FACTORED_STATIC=0 declines them, read at every launch).
+bool fixed_table(const FactArgs<float>& a) {
+  const char* env = std::getenv("GM_FACTORED_STATIC");
+  return (env == nullptr || env[0] != '0') && a.n_slots > 0 &&
+         (matches<SlotsF2>(a) || matches<SlotsF1>(a) || matches<SlotsS16>(a));
+}
+
+// Whether the compiled-in slot kernels serve a prepared call (they read the zw rows).
+bool fixed_slots(const FactArgs<float>& a) { return a.zw_g != nullptr && fixed_table(a); }
 
 void launch_grouped(bool forward, const FactArgs<float>& a, hipStream_t stream) {
   if (a.n_slots > 0) {
@@ -2905,14 +3065,19 @@ struct TwoRuns {
 GM_FACT_EXPORTS(float, f32)
 GM_FACT_EXPORTS(double, f64)
 
-extern "C" int gm_factored_forward_grouped_f32(
-    const float* h_g, const float* const* z, const int64_t* node_stride, const int64_t* t_stride,
-    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
-    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
-    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
-    int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
-    int64_t trunk_nb, double trunk_width, float* rows_g, void* stream) {
+namespace gm {
+namespace {
+
+// The grouped forward; b16: h_g and rows_g hold bfloat16 (compiled-in lane slots only).
+int forward_grouped(bool b16, const float* h_g, const float* const* z, const int64_t* node_stride,
+                    const int64_t* t_stride, const int64_t* width, int64_t n_runs, const float* phase_g,
+                    const float* rho_g, const float* zw_g, const int32_t* desc, const int64_t* group_ptr,
+                    const int64_t* group_source, const int64_t* group_order, int64_t n_nodes, int64_t n_edges,
+                    int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
+                    int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
+                    int64_t trunk_nb, double trunk_width, float* rows_g, void* stream) {
   GM_REQUIRE(z && node_stride && t_stride && width, "the mix runs must be host arrays");
+  GM_REQUIRE(!(b16 && trunk_w), "bfloat16 streams read the trunk features (no fused trunk)");
   const gm::Runs<float> runs{z, nullptr, node_stride, t_stride, width, n_runs};
   gm::FactArgs<float> a;
   const gm::TrunkParams trunk{trunk_w, trunk_b, trunk_centers, trunk_nb, trunk_width};
@@ -2925,19 +3090,24 @@ extern "C" int gm_factored_forward_grouped_f32(
   a.group_order = group_order;
   GM_REQUIRE(zw_g == nullptr || gm::aligned(zw_g, 16), "zw_g must be a 16-byte aligned device pointer (or null)");
   a.zw_g = zw_g;
+  a.b16 = b16;
+  if (b16) GM_REQUIRE(fixed_slots(a), "bfloat16 streams take plans with compiled-in lane slots (gm_factored_lanes_fixed)");
   gm::launch_grouped(true, a, (hipStream_t)stream);
   return gm::check_launch("factored_forward_grouped");
 }
 
-extern "C" int gm_factored_backward_grouped_ld_f32(
-    const float* g, int64_t g_ld, const int64_t* target_g, const float* weights_g, const float* rows_g,
-    const float* h_g, const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
-    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
-    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
-    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
-    int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
-    int64_t trunk_nb, double trunk_width, int64_t accumulate, float* dh_g, float* dweights_g, void* stream) {
+// The grouped backward; b16: rows_g, h_g and dh_g hold bfloat16 (compiled-in lane slots only).
+int backward_grouped(bool b16, const float* g, int64_t g_ld, const int64_t* target_g, const float* weights_g,
+                     const float* rows_g, const float* h_g, const float* const* z, float* const* dz,
+                     const int64_t* node_stride, const int64_t* t_stride, const int64_t* width, int64_t n_runs,
+                     const float* phase_g, const float* rho_g, const float* zw_g, const int32_t* desc,
+                     const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order, int64_t n_nodes,
+                     int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+                     int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b,
+                     const float* trunk_centers, int64_t trunk_nb, double trunk_width, int64_t accumulate, float* dh_g,
+                     float* dweights_g, void* stream) {
   GM_REQUIRE(z && dz && node_stride && t_stride && width, "the mix runs must be host arrays");
+  GM_REQUIRE(!(b16 && trunk_w), "bfloat16 streams read the trunk features (no fused trunk)");
   GM_REQUIRE(g_ld >= d_out, "g_ld must be at least d_out");
   GM_REQUIRE(g_ld == d_out || (g_ld % 2 == 0 && gm::aligned(g, 8)),
              "strided gradient rows need an even row stride and 8-byte aligned rows");
@@ -2963,8 +3133,65 @@ extern "C" int gm_factored_backward_grouped_ld_f32(
   a.dweights = dweights_g;
   a.accumulate = accumulate != 0;
   GM_REQUIRE(!(a.accumulate && trunk_w), "the fused trunk's backward writes dh_g and dweights_g (no accumulate)");
+  a.b16 = b16;
+  if (b16) GM_REQUIRE(fixed_slots(a), "bfloat16 streams take plans with compiled-in lane slots (gm_factored_lanes_fixed)");
   gm::launch_grouped(false, a, (hipStream_t)stream);
   return gm::check_launch("factored_backward_grouped");
+}
+
+}  // namespace
+}  // namespace gm
+
+extern "C" int gm_factored_forward_grouped_f32(
+    const float* h_g, const float* const* z, const int64_t* node_stride, const int64_t* t_stride,
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
+    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
+    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+    int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
+    int64_t trunk_nb, double trunk_width, float* rows_g, void* stream) {
+  return gm::forward_grouped(false, h_g, z, node_stride, t_stride, width, n_runs, phase_g, rho_g, zw_g, desc,
+                             group_ptr, group_source, group_order, n_nodes, n_edges, n_groups, K, wc, wr, pa, pt,
+                             n_blocks, d_out, trunk_w, trunk_b, trunk_centers, trunk_nb, trunk_width, rows_g, stream);
+}
+
+extern "C" int gm_factored_forward_grouped_bf16(
+    const uint16_t* h_g, const float* const* z, const int64_t* node_stride, const int64_t* t_stride,
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
+    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
+    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+    int64_t n_blocks, int64_t d_out, uint16_t* rows_g, void* stream) {
+  return gm::forward_grouped(true, reinterpret_cast<const float*>(h_g), z, node_stride, t_stride, width, n_runs,
+                             phase_g, rho_g, zw_g, desc, group_ptr, group_source, group_order, n_nodes, n_edges,
+                             n_groups, K, wc, wr, pa, pt, n_blocks, d_out, nullptr, nullptr, nullptr, 0, 0.0,
+                             reinterpret_cast<float*>(rows_g), stream);
+}
+
+extern "C" int gm_factored_backward_grouped_ld_f32(
+    const float* g, int64_t g_ld, const int64_t* target_g, const float* weights_g, const float* rows_g,
+    const float* h_g, const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
+    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
+    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+    int64_t n_blocks, int64_t d_out, const float* trunk_w, const float* trunk_b, const float* trunk_centers,
+    int64_t trunk_nb, double trunk_width, int64_t accumulate, float* dh_g, float* dweights_g, void* stream) {
+  return gm::backward_grouped(false, g, g_ld, target_g, weights_g, rows_g, h_g, z, dz, node_stride, t_stride, width,
+                              n_runs, phase_g, rho_g, zw_g, desc, group_ptr, group_source, group_order, n_nodes,
+                              n_edges, n_groups, K, wc, wr, pa, pt, n_blocks, d_out, trunk_w, trunk_b, trunk_centers,
+                              trunk_nb, trunk_width, accumulate, dh_g, dweights_g, stream);
+}
+
+extern "C" int gm_factored_backward_grouped_ld_bf16(
+    const float* g, int64_t g_ld, const int64_t* target_g, const float* weights_g, const uint16_t* rows_g,
+    const uint16_t* h_g, const float* const* z, float* const* dz, const int64_t* node_stride, const int64_t* t_stride,
+    const int64_t* width, int64_t n_runs, const float* phase_g, const float* rho_g, const float* zw_g,
+    const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source, const int64_t* group_order,
+    int64_t n_nodes, int64_t n_edges, int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+    int64_t n_blocks, int64_t d_out, int64_t accumulate, uint16_t* dh_g, float* dweights_g, void* stream) {
+  return gm::backward_grouped(true, g, g_ld, target_g, weights_g, reinterpret_cast<const float*>(rows_g),
+                              reinterpret_cast<const float*>(h_g), z, dz, node_stride, t_stride, width, n_runs,
+                              phase_g, rho_g, zw_g, desc, group_ptr, group_source, group_order, n_nodes, n_edges,
+                              n_groups, K, wc, wr, pa, pt, n_blocks, d_out, nullptr, nullptr, nullptr, 0, 0.0,
+                              accumulate, reinterpret_cast<float*>(dh_g), dweights_g, stream);
 }
 
 extern "C" int gm_factored_backward_grouped_f32(
@@ -2990,8 +3217,12 @@ extern "C" int gm_factored_aggregate_gather_f32(const float* rows, const int64_t
                                        inv);
 }
 
-extern "C" int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out,
-                                       int64_t pa, int64_t pt, int32_t* n_slots, uint32_t* slot, uint8_t* slotcol) {
+namespace gm {
+namespace {
+
+// A plan's lane tables; fixed (optional): whether compiled-in slot kernels serve it.
+int lane_tables(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out, int64_t pa, int64_t pt,
+                int32_t* n_slots, uint32_t* slot, uint8_t* slotcol, int32_t* fixed) {
   GM_REQUIRE(n_slots != nullptr, "n_slots must be a host pointer");
   GM_REQUIRE(pa >= 1 && pt >= 1 && pa + pt <= gm::kPhaseRow / 2, "the grouped phase rows hold at most 8 pairs");
   gm::FactArgs<float> a;
@@ -3019,12 +3250,32 @@ extern "C" int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, in
     for (int i = 0; i < gm::kMaxSlots; ++i) slot[i] = a.n_slots ? a.slot[i] : 0u;
   if (slotcol)
     for (int i = 0; i < 128; ++i) slotcol[i] = a.n_slots ? a.slotcol[i] : (uint8_t)0xFF;
+  if (fixed) *fixed = gm::fixed_table(a) ? 1 : 0;
   return GM_OK;
 }
 
-extern "C" int gm_factored_aggregate_heads_f32(const float* rows, const int64_t* inv, const float* alpha,
-                                               const int64_t* row_ptr, int64_t n_targets, int64_t n_edges, int64_t H,
-                                               int64_t d_out, int64_t split, float* out, void* stream) {
+}  // namespace
+}  // namespace gm
+
+extern "C" int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out,
+                                       int64_t pa, int64_t pt, int32_t* n_slots, uint32_t* slot, uint8_t* slotcol) {
+  return gm::lane_tables(desc, n_blocks, wc, wr, d_out, pa, pt, n_slots, slot, slotcol, nullptr);
+}
+
+extern "C" int gm_factored_lanes_fixed(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out,
+                                       int64_t pa, int64_t pt, int32_t* fixed) {
+  GM_REQUIRE(fixed != nullptr, "fixed must be a host pointer");
+  int32_t n_slots = 0;
+  return gm::lane_tables(desc, n_blocks, wc, wr, d_out, pa, pt, &n_slots, nullptr, nullptr, fixed);
+}
+
+namespace gm {
+namespace {
+
+// rows float32, or bfloat16 (b16: the 16-byte-piece kernels only, as 8-byte pieces)
+int aggregate_heads(bool b16, const float* rows, const int64_t* inv, const float* alpha, const int64_t* row_ptr,
+                    int64_t n_targets, int64_t n_edges, int64_t H, int64_t d_out, int64_t split, float* out,
+                    void* stream) {
   GM_REQUIRE(n_targets >= 0 && n_edges >= 0, "sizes must be non-negative");
   GM_REQUIRE(H >= 1 && d_out >= 1 && H * d_out <= 64 * gm::kAggScalar, "H d_out must be in [1, 1024]");
   GM_REQUIRE(split >= 1 && H % split == 0, "split must divide H");
@@ -3035,7 +3286,19 @@ extern "C" int gm_factored_aggregate_heads_f32(const float* rows, const int64_t*
   const gm::AggHeadsArgs a{rows, alpha, inv, row_ptr, out, n_targets, n_edges, (int)H, (int)d_out, (int)split};
   const dim3 grid((unsigned)gm::blocks_for(n_targets)), block(256);
   const int64_t pieces = d_out % 4 == 0 ? H * d_out / 4 : 0;
-  const bool vec = pieces > 0 && pieces <= 64 * 4 && gm::aligned(rows, 16) && gm::aligned(out, 16);
+  const bool vec = pieces > 0 && pieces <= 64 * 4 && gm::aligned(rows, b16 ? 8 : 16) && gm::aligned(out, 16);
+  if (b16) {
+    GM_REQUIRE(vec, "bfloat16 rows take d_out a multiple of 4, H d_out <= 1024, 8-byte aligned rows and 16-byte aligned out");
+    if (pieces <= 64)
+      hipLaunchKernelGGL((gm::aggregate_heads_vec_kernel<1, true>), grid, block, 0, (hipStream_t)stream, a);
+    else if (pieces <= 128)
+      hipLaunchKernelGGL((gm::aggregate_heads_vec_kernel<2, true>), grid, block, 0, (hipStream_t)stream, a);
+    else if (pieces <= 192)
+      hipLaunchKernelGGL((gm::aggregate_heads_vec_kernel<3, true>), grid, block, 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL((gm::aggregate_heads_vec_kernel<4, true>), grid, block, 0, (hipStream_t)stream, a);
+    return gm::check_launch("factored_aggregate_heads");
+  }
   if (vec && pieces <= 64)
     hipLaunchKernelGGL(gm::aggregate_heads_vec_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
   else if (vec && pieces <= 128)
@@ -3047,6 +3310,22 @@ extern "C" int gm_factored_aggregate_heads_f32(const float* rows, const int64_t*
   else
     hipLaunchKernelGGL(gm::aggregate_heads_kernel, grid, block, 0, (hipStream_t)stream, a);
   return gm::check_launch("factored_aggregate_heads");
+}
+
+}  // namespace
+}  // namespace gm
+
+extern "C" int gm_factored_aggregate_heads_f32(const float* rows, const int64_t* inv, const float* alpha,
+                                               const int64_t* row_ptr, int64_t n_targets, int64_t n_edges, int64_t H,
+                                               int64_t d_out, int64_t split, float* out, void* stream) {
+  return gm::aggregate_heads(false, rows, inv, alpha, row_ptr, n_targets, n_edges, H, d_out, split, out, stream);
+}
+
+extern "C" int gm_factored_aggregate_heads_bf16(const uint16_t* rows, const int64_t* inv, const float* alpha,
+                                                const int64_t* row_ptr, int64_t n_targets, int64_t n_edges, int64_t H,
+                                                int64_t d_out, int64_t split, float* out, void* stream) {
+  return gm::aggregate_heads(true, reinterpret_cast<const float*>(rows), inv, alpha, row_ptr, n_targets, n_edges, H,
+                             d_out, split, out, stream);
 }
 
 extern "C" int gm_gather_transpose_f32(const float* src, const int64_t* perm, int64_t n, int64_t width, float* dst_t,

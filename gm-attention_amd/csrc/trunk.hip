@@ -18,9 +18,17 @@
 // the wave's tiles, one partial row per wavefront, and a second kernel sums
 // the partial rows in a fixed order.  No atomics:
 // the parameter gradients are deterministic.
+//
+// The features (and their gradients) may be kept in bfloat16 (the trunk of a
+// bfloat16 block): the forward rounds each feature to nearest even as it
+// stores it, the backward widens dh exactly as it loads it; the arithmetic
+// stays float32.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.hpp"
+#include "split.hpp"
 
 namespace gm {
 namespace {
@@ -34,6 +42,8 @@ struct TrunkArgs {
   const float* centers; // (B,)
   const float* dh;      // (H, E, T) backward
   float* h;             // (H, E, T) forward
+  const uint16_t* dhb;  // (H, E, T) backward, bfloat16 (in place of dh)
+  uint16_t* hb;         // (H, E, T) forward, bfloat16 (in place of h)
   float* partial;       // (n_blocks, H, T * B + T) backward
   int64_t n_edges;
   int H, T, B;
@@ -85,7 +95,7 @@ __device__ __forceinline__ void wave_sync() {
 //     A2_j[m = c][k = q] = b_c(edge 4q + j) (c < B), 1 at c = B, 0 above,
 //   so D2's rows m < B are dW^T and row B is db, accumulated over the wave's
 //   tiles in registers for every head.  Edges past the end read dh as zero and add nothing.
-template <int B>
+template <int B, bool B16 = false>
 __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a) {
   constexpr int T = 16, P = T * B + T, LDT = T + 4;
   __shared__ __align__(16) float stage[kTrunkWaves][T * LDT];  // per wave: dp as [feature][edge]
@@ -118,14 +128,29 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
     const float z = (r * r - mu) * iw;
     return fast_exp(-0.5f * z * z);
   };
-  // dh of head h for this lane's edge c of a tile, features 4q..4q+3 (zero past the end)
-  const int lane_off = c * T + 4 * q;  // the lane's 16 bytes within a tile's 1 KB of one head
-  auto load_dh = [&](int64_t e0, int h) {
-    const float* tile_dh = a.dh + ((int64_t)h * a.n_edges + e0) * T;  // uniform: a scalar base
-    if (e0 + 16 <= a.n_edges)  // every tile but the last: no per-lane test
-      return *reinterpret_cast<const float4*>(tile_dh + lane_off);
-    return e0 + c < a.n_edges ? *reinterpret_cast<const float4*>(tile_dh + lane_off)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
+  // dh of head h for this lane's edge c of a tile, features 4q..4q+3 (zero past the end),
+  // as loaded: four floats, or four bfloat16 in one 8-byte piece (widened where used, so
+  // the next tile's loads stay in flight)
+  using Raw = typename std::conditional<B16, uint2, float4>::type;
+  const int lane_off = c * T + 4 * q;  // the lane's piece within a tile's rows of one head
+  auto load_dh = [&](int64_t e0, int h) -> Raw {
+    if constexpr (B16) {
+      const uint16_t* tile_dh = a.dhb + ((int64_t)h * a.n_edges + e0) * T;  // uniform: a scalar base
+      if (e0 + 16 <= a.n_edges) return *reinterpret_cast<const uint2*>(tile_dh + lane_off);
+      return e0 + c < a.n_edges ? *reinterpret_cast<const uint2*>(tile_dh + lane_off) : make_uint2(0u, 0u);
+    } else {
+      const float* tile_dh = a.dh + ((int64_t)h * a.n_edges + e0) * T;  // uniform: a scalar base
+      if (e0 + 16 <= a.n_edges)  // every tile but the last: no per-lane test
+        return *reinterpret_cast<const float4*>(tile_dh + lane_off);
+      return e0 + c < a.n_edges ? *reinterpret_cast<const float4*>(tile_dh + lane_off)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto widen = [](const Raw& v) -> float4 {
+    if constexpr (B16)
+      return make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+    else
+      return v;
   };
   // rho of a tile: edge c (the B1 operand) and edges 4q..4q+3 (the A2 operands)
   auto load_rho = [&](int64_t e0, float& rc, float* r4) {
@@ -146,9 +171,9 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
   // than what the wave needs next.
   float rc, r4[4];
   load_rho(wave * 16, rc, r4);
-  float4 g[kTrunkMaxHeads];
+  Raw g[kTrunkMaxHeads];
 #pragma unroll
-  for (int h = 0; h < kTrunkMaxHeads; ++h) g[h] = h < a.H ? load_dh(wave * 16, h) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int h = 0; h < kTrunkMaxHeads; ++h) g[h] = h < a.H ? load_dh(wave * 16, h) : Raw{};
   for (int64_t tile = wave; tile < n_tiles; tile += n_waves) {
     const int64_t e_next = (tile + n_waves) * 16;
     float rc_next, r4_next[4];
@@ -165,7 +190,8 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
       floatx4 pre = mfma16(w0[h], b1_0, floatx4{0.f, 0.f, 0.f, 0.f});
       pre = mfma16(w1[h], b1_1, pre);
       if (B == 8) pre = mfma16(w2[h], b1_2, pre);
-      const float gv[4] = {g[h].x, g[h].y, g[h].z, g[h].w};
+      const float4 gw = widen(g[h]);
+      const float gv[4] = {gw.x, gw.y, gw.z, gw.w};
       g[h] = load_dh(e_next, h);
       wave_sync();  // the previous head's LDS reads are done
 #pragma unroll
@@ -204,7 +230,7 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
 // pre-activations (feature 4q + r, edge c) from the same two or three MFMAs
 // (the basis once per tile), SiLU in registers, and each lane's four features
 // of its edge stored as one 16-byte store (a head's tile is one contiguous 1 KB).
-template <int B>
+template <int B, bool B16 = false>
 __global__ __launch_bounds__(kTrunkThreads) void trunk_forward_mfma(TrunkArgs a) {
   constexpr int T = 16;
   const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15;
@@ -249,7 +275,12 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_forward_mfma(TrunkArgs a)
       out.y = pre[1] * sigmoid_of(pre[1]);
       out.z = pre[2] * sigmoid_of(pre[2]);
       out.w = pre[3] * sigmoid_of(pre[3]);
-      if (edge_in) *reinterpret_cast<float4*>(a.h + ((int64_t)h * a.n_edges + e0 + c) * T + 4 * q) = out;
+      const int64_t at = ((int64_t)h * a.n_edges + e0 + c) * T + 4 * q;
+      if constexpr (B16) {
+        if (edge_in) *reinterpret_cast<uint2*>(a.hb + at) = make_uint2(pack_bf16(out.x, out.y), pack_bf16(out.z, out.w));
+      } else {
+        if (edge_in) *reinterpret_cast<float4*>(a.h + at) = out;
+      }
     }
     rc = rn;
   }
@@ -296,24 +327,34 @@ constexpr int64_t kTrunkBlocks = 2048;  // about this many workgroups (waves str
 // The grid of a pass over n_edges: one tile per wave up to about kTrunkBlocks
 // workgroups, in whole rounds of the kernel's resident workgroups (the waves'
 // shares differ by at most a tile, so a partial last round would run on a
-// fraction of the chip).  The backward's grid (and so its partial rows)
-// follows the B = 8 instance's occupancy for every basis size.
-int64_t trunk_blocks(int64_t n_edges, bool forward) {
+// fraction of the chip).  The grid (and so the backward's partial rows)
+// follows the B = 8 instance's occupancy for every basis size, per storage
+// type of the features (the bfloat16 backward holds fewer registers).
+int64_t trunk_blocks(int64_t n_edges, bool forward, bool b16) {
   const int64_t need = (n_edges + 16 * kTrunkWaves - 1) / (16 * kTrunkWaves);  // one tile per wave
-  const void* kernel = forward ? (const void*)trunk_forward_mfma<8> : (const void*)trunk_backward_mfma<8>;
+  const void* kernel = forward ? (b16 ? (const void*)trunk_forward_mfma<8, true> : (const void*)trunk_forward_mfma<8>)
+                               : (b16 ? (const void*)trunk_backward_mfma<8, true> : (const void*)trunk_backward_mfma<8>);
   const int64_t full = whole_rounds(kTrunkBlocks, resident_blocks(kernel, kTrunkThreads));
   return need < full ? (need > 0 ? need : 1) : full;
 }
 
-int64_t backward_blocks(int64_t n_edges) { return trunk_blocks(n_edges, false); }
+int64_t backward_blocks(int64_t n_edges, bool b16) { return trunk_blocks(n_edges, false, b16); }
 
 template <int B>
 void launch(bool forward, const TrunkArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)trunk_blocks(a.n_edges, forward)), block(kTrunkThreads);
-  if (forward)
-    hipLaunchKernelGGL((trunk_forward_mfma<B>), grid, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL((trunk_backward_mfma<B>), grid, block, 0, stream, a);
+  const dim3 grid((unsigned)trunk_blocks(a.n_edges, forward, forward ? a.hb != nullptr : a.dhb != nullptr)),
+      block(kTrunkThreads);
+  if (forward) {
+    if (a.hb)
+      hipLaunchKernelGGL((trunk_forward_mfma<B, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((trunk_forward_mfma<B>), grid, block, 0, stream, a);
+  } else {
+    if (a.dhb)
+      hipLaunchKernelGGL((trunk_backward_mfma<B, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((trunk_backward_mfma<B>), grid, block, 0, stream, a);
+  }
 }
 
 void launch_any(bool forward, const TrunkArgs& a, hipStream_t stream) {
@@ -328,43 +369,90 @@ void launch_any(bool forward, const TrunkArgs& a, hipStream_t stream) {
 }  // namespace
 }  // namespace gm
 
-// Partial rows of the backward: one per wavefront of its grid.
-extern "C" int64_t gm_radial_trunk_partials(int64_t n_edges) { return gm::backward_blocks(n_edges) * gm::kTrunkWaves; }
+// Partial rows of the backward: one per wavefront of its grid (the larger of the
+// float32 and bfloat16 instances' grids).
+extern "C" int64_t gm_radial_trunk_partials(int64_t n_edges) {
+  const int64_t f = gm::backward_blocks(n_edges, false), b = gm::backward_blocks(n_edges, true);
+  return (f > b ? f : b) * gm::kTrunkWaves;
+}
+
+namespace gm {
+namespace {
+
+// h (float32) or hb (bfloat16): exactly one is given.
+int trunk_forward(const float* rho, const float* weight, const float* bias, const float* centers, int64_t n_edges,
+                  int64_t H, int64_t T, int64_t B, double width, float* h, uint16_t* hb, void* stream) {
+  TrunkArgs a;
+  const int status = prepare(a, rho, weight, bias, centers, n_edges, H, T, B, width);
+  if (status != GM_OK) return status;
+  if (n_edges == 0) return GM_OK;
+  if (hb)
+    GM_REQUIRE(aligned(hb, 8), "h must be an 8-byte aligned device pointer");
+  else
+    GM_REQUIRE(h && aligned(h, 16), "h must be a 16-byte aligned device pointer");
+  a.h = h;
+  a.hb = hb;
+  launch_any(true, a, (hipStream_t)stream);
+  return check_launch("radial_trunk_forward");
+}
+
+// dh (float32) or dhb (bfloat16): exactly one is given.
+int trunk_backward(const float* dh, const uint16_t* dhb, const float* rho, const float* weight, const float* bias,
+                   const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B, double width,
+                   float* partial, float* dparams, void* stream) {
+  TrunkArgs a;
+  const int status = prepare(a, rho, weight, bias, centers, n_edges, H, T, B, width);
+  if (status != GM_OK) return status;
+  GM_REQUIRE(dparams, "dparams must be a device pointer");
+  const int HP = (int)(H * (T * B + T));
+  if (n_edges == 0) {
+    hipLaunchKernelGGL(trunk_reduce_kernel, dim3(HP), dim3(256), 0, (hipStream_t)stream, partial, (int64_t)0, HP,
+                       dparams);
+    return check_launch("radial_trunk_backward (empty)");
+  }
+  if (dhb)
+    GM_REQUIRE(aligned(dhb, 8) && partial, "dh (8-byte aligned) and partial must be device pointers");
+  else
+    GM_REQUIRE(dh && aligned(dh, 16) && partial, "dh (16-byte aligned) and partial must be device pointers");
+  a.dh = dh;
+  a.dhb = dhb;
+  a.partial = partial;
+  a.rho_vec4 = aligned(rho, 16);
+  launch_any(false, a, (hipStream_t)stream);
+  int rc = check_launch("radial_trunk_backward");
+  if (rc != GM_OK) return rc;
+  hipLaunchKernelGGL(trunk_reduce_kernel, dim3(HP), dim3(256), 0, (hipStream_t)stream, partial,
+                     backward_blocks(n_edges, dhb != nullptr) * kTrunkWaves, HP, dparams);
+  return check_launch("radial_trunk_backward (reduce)");
+}
+
+}  // namespace
+}  // namespace gm
 
 extern "C" int gm_radial_trunk_forward_f32(const float* rho, const float* weight, const float* bias,
                                            const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B,
                                            double width, float* h, void* stream) {
-  gm::TrunkArgs a;
-  const int status = gm::prepare(a, rho, weight, bias, centers, n_edges, H, T, B, width);
-  if (status != GM_OK) return status;
-  if (n_edges == 0) return GM_OK;
-  GM_REQUIRE(h && gm::aligned(h, 16), "h must be a 16-byte aligned device pointer");
-  a.h = h;
-  gm::launch_any(true, a, (hipStream_t)stream);
-  return gm::check_launch("radial_trunk_forward");
+  return gm::trunk_forward(rho, weight, bias, centers, n_edges, H, T, B, width, h, nullptr, stream);
+}
+
+extern "C" int gm_radial_trunk_forward_bf16(const float* rho, const float* weight, const float* bias,
+                                            const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B,
+                                            double width, uint16_t* h, void* stream) {
+  GM_REQUIRE(h || n_edges == 0, "h must be a device pointer");
+  return gm::trunk_forward(rho, weight, bias, centers, n_edges, H, T, B, width, nullptr, h, stream);
 }
 
 extern "C" int gm_radial_trunk_backward_f32(const float* dh, const float* rho, const float* weight, const float* bias,
                                             const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B,
                                             double width, float* partial, float* dparams, void* stream) {
-  gm::TrunkArgs a;
-  const int status = gm::prepare(a, rho, weight, bias, centers, n_edges, H, T, B, width);
-  if (status != GM_OK) return status;
-  GM_REQUIRE(dparams, "dparams must be a device pointer");
-  const int HP = (int)(H * (T * B + T));
-  if (n_edges == 0) {
-    hipLaunchKernelGGL(gm::trunk_reduce_kernel, dim3(HP), dim3(256), 0, (hipStream_t)stream, partial, (int64_t)0, HP,
-                       dparams);
-    return gm::check_launch("radial_trunk_backward (empty)");
-  }
-  GM_REQUIRE(dh && gm::aligned(dh, 16) && partial, "dh (16-byte aligned) and partial must be device pointers");
-  a.dh = dh;
-  a.partial = partial;
-  a.rho_vec4 = gm::aligned(rho, 16);
-  gm::launch_any(false, a, (hipStream_t)stream);
-  int rc = gm::check_launch("radial_trunk_backward");
-  if (rc != GM_OK) return rc;
-  hipLaunchKernelGGL(gm::trunk_reduce_kernel, dim3(HP), dim3(256), 0, (hipStream_t)stream, partial,
-                     gm_radial_trunk_partials(n_edges), HP, dparams);
-  return gm::check_launch("radial_trunk_backward (reduce)");
+  return gm::trunk_backward(dh, nullptr, rho, weight, bias, centers, n_edges, H, T, B, width, partial, dparams, stream);
+}
+
+extern "C" int gm_radial_trunk_backward_bf16(const uint16_t* dh, const float* rho, const float* weight,
+                                             const float* bias, const float* centers, int64_t n_edges, int64_t H,
+                                             int64_t T, int64_t B, double width, float* partial, float* dparams,
+                                             void* stream) {
+  GM_REQUIRE(dh || n_edges == 0, "dh must be a device pointer");
+  return gm::trunk_backward(nullptr, dh, rho, weight, bias, centers, n_edges, H, T, B, width, partial, dparams,
+                            stream);
 }

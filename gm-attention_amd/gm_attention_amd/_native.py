@@ -55,6 +55,8 @@ SIGNATURES_F32 = {
     "gm_radial_trunk_forward_f32": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_D, _P, _P]),
     "gm_radial_trunk_backward_f32": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_D, _P, _P, _P]),
     "gm_radial_trunk_partials": (ctypes.c_int64, [_I]),
+    "gm_radial_trunk_forward_bf16": (ctypes.c_int, [_P] * 4 + [_I] * 4 + [_D, _P, _P]),
+    "gm_radial_trunk_backward_bf16": (ctypes.c_int, [_P] * 5 + [_I] * 4 + [_D, _P, _P, _P]),
     "gm_node_mix_forward_f32": (ctypes.c_int, [_P, _I, _P, _I, _I, _I, _P, _P]),
     "gm_node_mix_backward_input_f32": (ctypes.c_int, [_P, _P, _I, _I, _I, _P, _I, _P]),
     "gm_node_mix_weight_partials": (ctypes.c_int64, [_I, _I, _I]),
@@ -73,7 +75,12 @@ SIGNATURES_F32 = {
                                             + [_P] * 3 + [_I, _D] + [_I] + [_P] * 3),
     "gm_factored_aggregate_gather_f32": (ctypes.c_int, [_P] * 4 + [_I] * 3 + [_P, _P]),
     "gm_factored_lane_tables": (ctypes.c_int, [_P] + [_I] * 6 + [_P] * 3),
+    "gm_factored_lanes_fixed": (ctypes.c_int, [_P] + [_I] * 6 + [_P]),
     "gm_factored_aggregate_heads_f32": (ctypes.c_int, [_P] * 4 + [_I] * 5 + [_P, _P]),
+    "gm_factored_aggregate_heads_bf16": (ctypes.c_int, [_P] * 4 + [_I] * 5 + [_P, _P]),
+    "gm_factored_forward_grouped_bf16": (ctypes.c_int, [_P] * 5 + [_I] + [_P] * 7 + [_I] * 10 + [_P, _P]),
+    "gm_factored_backward_grouped_ld_bf16": (ctypes.c_int, [_P, _I] + [_P] * 9 + [_I] + [_P] * 7 + [_I] * 10 + [_I]
+                                             + [_P] * 3),
     "gm_gather_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
     "gm_scatter_transpose_f32": (ctypes.c_int, [_P, _P, _I, _I, _P, _P]),
     "gm_conv_radial_partial_row": (ctypes.c_int64, []),
@@ -621,27 +628,37 @@ def factored_backward_seg(g: Tensor, target: Tensor, weights: Tensor, rows: Tens
     return dweights
 
 
-def radial_trunk_forward(rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor, width: float) -> Tensor:
-    """``h (H, E, T)``: every head's SiLU(W b(rho) + c) over the Gaussian basis of rho^2."""
+def radial_trunk_forward(rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor, width: float,
+                         dtype: torch.dtype | None = None) -> Tensor:
+    """``h (H, E, T)``: every head's SiLU(W b(rho) + c) over the Gaussian basis
+    of rho^2, in rho's dtype or ``dtype`` (bfloat16: float32 arithmetic, each
+    feature rounded to nearest even as it is stored)."""
     H, T, B = weight.shape
-    h = torch.empty(H, rho.shape[0], T, dtype=rho.dtype, device=rho.device)
+    dtype = rho.dtype if dtype is None else dtype
+    _check(dtype in (torch.float32, torch.bfloat16), "the trunk features are float32 or bfloat16")
+    h = torch.empty(H, rho.shape[0], T, dtype=dtype, device=rho.device)
     if rho.shape[0] == 0:
         return h
-    _call("gm_radial_trunk_forward_f32", _ptr(rho), _ptr(weight), _ptr(bias) if bias is not None else None,
+    name = "gm_radial_trunk_forward_bf16" if dtype == torch.bfloat16 else "gm_radial_trunk_forward_f32"
+    _call(name, _ptr(rho), _ptr(weight), _ptr(bias) if bias is not None else None,
           _ptr(centers), rho.shape[0], H, T, B, float(width), _ptr(h), _stream(rho.device))
     return h
 
 
 def radial_trunk_backward(dh: Tensor, rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor,
                           width: float) -> tuple[Tensor, Tensor]:
-    """(dweight (H, T, B), dbias (H, T)) summed over the edges in a fixed order."""
+    """(dweight (H, T, B), dbias (H, T)) summed over the edges in a fixed order;
+    ``dh`` float32 or bfloat16."""
     H, T, B = weight.shape
+    _check(dh.dtype in (torch.float32, torch.bfloat16) and dh.is_contiguous(),
+           "dh must be contiguous float32 or bfloat16")
     P = T * B + T
     lib = library()
     blocks = int(lib.gm_radial_trunk_partials(rho.shape[0]))
     partial = torch.empty(max(blocks, 1) * H * P, dtype=torch.float32, device=rho.device)
     dparams = torch.empty(H, P, dtype=torch.float32, device=rho.device)
-    _call("gm_radial_trunk_backward_f32", _ptr(dh), _ptr(rho), _ptr(weight), _ptr(bias) if bias is not None else None,
+    name = "gm_radial_trunk_backward_bf16" if dh.dtype == torch.bfloat16 else "gm_radial_trunk_backward_f32"
+    _call(name, _ptr(dh), _ptr(rho), _ptr(weight), _ptr(bias) if bias is not None else None,
           _ptr(centers), rho.shape[0], H, T, B, float(width), _ptr(partial), _ptr(dparams), _stream(rho.device))
     return dparams[:, : T * B].reshape(H, T, B), dparams[:, T * B:]
 
@@ -733,18 +750,30 @@ def factored_forward_grouped(h_g: Tensor | None, runs: MixRuns, n_nodes: int, ph
                              d_out: int, out: Tensor | None = None, trunk: FusedTrunk | None = None) -> Tensor:
     """The rows in the grouping's order, every per-edge stream read in that order
     (into ``out`` (n_edges, d_out) when given).  With ``trunk`` the kernels
-    evaluate h from ``rho_g`` and ``h_g`` may be None."""
+    evaluate h from ``rho_g`` and ``h_g`` may be None.  A bfloat16 ``h_g``
+    gives bfloat16 rows (plans with compiled-in lane slots, :func:`lanes_fixed`;
+    float32 arithmetic)."""
     n_edges = rho_g.shape[0]
     if h_g is None and trunk is None:
         raise ValueError("h_g is required without a fused trunk")
+    b16 = h_g is not None and h_g.dtype == torch.bfloat16
+    row_dtype = torch.bfloat16 if b16 else rho_g.dtype
     if out is None:
-        out = torch.empty(n_edges, d_out, dtype=rho_g.dtype, device=rho_g.device)
-    elif out.shape != (n_edges, d_out) or not out.is_contiguous() or out.dtype != rho_g.dtype:
-        raise ValueError("out must be a contiguous (n_edges, d_out) tensor in rho's dtype")
+        out = torch.empty(n_edges, d_out, dtype=row_dtype, device=rho_g.device)
+    elif out.shape != (n_edges, d_out) or not out.is_contiguous() or out.dtype != row_dtype:
+        raise ValueError("out must be a contiguous (n_edges, d_out) tensor in h's dtype")
     if n_edges == 0:
         return out
     _check_order(group_order, group_source)
     hd = host_desc32(desc)
+    if b16:
+        _check(trunk is None, "bfloat16 trunk features are read, not evaluated in the kernels")
+        _call("gm_factored_forward_grouped_bf16", _ptr(h_g), ctypes.cast(runs.z, ctypes.c_void_p),
+              ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
+              ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),
+              _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, n_edges, group_source.shape[0], K, wc,
+              wr, pa, pt, hd.shape[0], d_out, _ptr(out), _stream(rho_g.device))
+        return out
     _call("gm_factored_forward_grouped_f32", _ptr(h_g), ctypes.cast(runs.z, ctypes.c_void_p),
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
           ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),
@@ -767,7 +796,8 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
     With ``trunk`` the kernels evaluate h from
     ``rho_g`` and ``h_g`` may be None.  ``accumulate``: dh and dweights are
     added to ``dh_g`` and ``dweights`` (which must then be given) instead of
-    written."""
+    written.  With bfloat16 ``h_g`` the rows and ``dh_g`` are bfloat16 too
+    (float32 arithmetic)."""
     if accumulate and dweights is None:
         raise ValueError("accumulate needs the dweights to add to")
     if h_g is None and trunk is None:
@@ -785,6 +815,17 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
     g_ld = g.stride(0) if g.dim() == 2 and g.stride(1) == 1 else -1
     if g_ld != g.shape[1] and not (g_ld >= g.shape[1] and g_ld % 2 == 0 and g.data_ptr() % 8 == 0):
         g, g_ld = g.contiguous(), g.shape[1]
+    if h_g is not None and h_g.dtype == torch.bfloat16:
+        _check(trunk is None and rows_g.dtype == torch.bfloat16 and dh_g.dtype == torch.bfloat16,
+               "bfloat16 trunk features go with bfloat16 rows and dh (no fused trunk)")
+        _call("gm_factored_backward_grouped_ld_bf16", _ptr(g), g_ld, _ptr(target_g), _ptr(weights_g), _ptr(rows_g),
+              _ptr(h_g), ctypes.cast(runs.z, ctypes.c_void_p), ctypes.cast(runs.dz, ctypes.c_void_p),
+              ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
+              ctypes.cast(runs.width, ctypes.c_void_p), runs.n, _ptr(phase_g), _ptr(rho_g), _ptr(zw_g), hd.data_ptr(),
+              _ptr(group_ptr), _ptr(group_source), _ptr(group_order), n_nodes, n_edges, group_source.shape[0], K,
+              wc, wr, pa, pt, hd.shape[0], g.shape[1], int(accumulate), _ptr(dh_g), _ptr(dweights),
+              _stream(rho_g.device))
+        return dweights
     _call("gm_factored_backward_grouped_ld_f32", _ptr(g), g_ld, _ptr(target_g), _ptr(weights_g), _ptr(rows_g), _ptr(h_g),
           ctypes.cast(runs.z, ctypes.c_void_p), ctypes.cast(runs.dz, ctypes.c_void_p),
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
@@ -807,21 +848,31 @@ def lane_tables(desc: Tensor, wc: int, wr: int, d_out: int, pa: int, pt: int) ->
     return n.value, list(slot), list(slotcol)
 
 
+def lanes_fixed(desc: Tensor, wc: int, wr: int, d_out: int, pa: int, pt: int) -> bool:
+    """Whether a plan's lane slots are one of the compiled-in tables (the
+    kernels that also take bfloat16 streams)."""
+    hd = host_desc32(desc)
+    fixed = ctypes.c_int32(0)
+    _call("gm_factored_lanes_fixed", hd.data_ptr(), hd.shape[0], wc, wr, d_out, pa, pt, ctypes.byref(fixed))
+    return bool(fixed.value)
+
+
 def aggregate_heads(rows: Tensor, inv: Tensor, alpha: Tensor, row_ptr: Tensor, split: int = 1) -> Tensor:
     """``out[i, h] = sum_e alpha[e, h // split] rows[h, inv[e]]`` over each
-    target's edges: rows ``(H, E, d_out)``, alpha ``(E, H / split)``;
-    ``(N, H, d_out)`` out."""
+    target's edges: rows ``(H, E, d_out)`` (float32, or bfloat16 widened as
+    read), alpha ``(E, H / split)``; ``(N, H, d_out)`` float32 out."""
     H, E, d_out = rows.shape
     n_targets = row_ptr.shape[0] - 1
-    out = torch.empty(n_targets, H, d_out, dtype=rows.dtype, device=rows.device)
-    if split < 1 or H % split or rows.dtype != torch.float32 or alpha.dtype != torch.float32 \
+    out = torch.empty(n_targets, H, d_out, dtype=torch.float32, device=rows.device)
+    if split < 1 or H % split or rows.dtype not in (torch.float32, torch.bfloat16) or alpha.dtype != torch.float32 \
             or alpha.shape != (E, H // split):
-        raise ValueError("rows (H, E, d_out) and alpha (E, H / split) must be float32, split dividing H")
+        raise ValueError("rows (H, E, d_out; float32 or bfloat16) and alpha (E, H / split; float32), split dividing H")
     if not (rows.is_contiguous() and alpha.is_contiguous() and inv.is_contiguous() and row_ptr.is_contiguous()):
         raise ValueError("rows, alpha, inv and row_ptr must be contiguous")
     if n_targets == 0:
         return out
-    _call("gm_factored_aggregate_heads_f32", _ptr(rows), _ptr(inv), _ptr(alpha), _ptr(row_ptr), n_targets, E, H,
+    name = "gm_factored_aggregate_heads_bf16" if rows.dtype == torch.bfloat16 else "gm_factored_aggregate_heads_f32"
+    _call(name, _ptr(rows), _ptr(inv), _ptr(alpha), _ptr(row_ptr), n_targets, E, H,
           d_out, split, _ptr(out), _stream(rows.device))
     return out
 

@@ -1073,6 +1073,13 @@ class FactoredHeadsTrunk(torch.autograd.Function):
 #: the recomputation costs more than the round trip it saves (168 vs 155 ms a step there).
 FUSED_TRUNK = os.environ.get("GM_FACTORED_TRUNK", "0") == "1"
 
+#: For bfloat16 node rows (a bfloat16 block), the grouped kernels keep their
+#: per-edge streams -- the trunk features, the value rows and the features'
+#: gradients -- in bfloat16, with float32 arithmetic, as the reference's block
+#: keeps them in the rows' dtype (``blocks.py:326-349``); ``GM_BF16_STREAMS=0``
+#: keeps them float32.  Plans with compiled-in lane slots only.
+BF16_STREAMS = os.environ.get("GM_BF16_STREAMS", "1") != "0"
+
 
 def _lanes_apply(kernel: Any, hp: HeadsPlan, pa: int, pt: int) -> bool:
     """Whether the grouped kernels take the lane-owned form for this plan."""
@@ -1083,6 +1090,19 @@ def _lanes_apply(kernel: Any, hp: HeadsPlan, pa: int, pt: int) -> bool:
         n_slots, _, _ = _native.lane_tables(torch.tensor([list(r) for r in hp.desc_rows], dtype=torch.int32), p.wc,
                                             p.wr, p.d_out, pa, pt)
         hit = n_slots > 0
+        kernel.__dict__[key] = hit
+    return hit
+
+
+def _lanes_fixed(kernel: Any, hp: HeadsPlan, pa: int, pt: int) -> bool:
+    """Whether the grouped kernels take compiled-in lane slots for this plan
+    (the kernels that also take bfloat16 streams)."""
+    key = ("_lanes_fixed", pa, pt, os.environ.get("GM_FACTORED_LANES", "1"), os.environ.get("GM_FACTORED_STATIC", "1"))
+    hit = kernel.__dict__.get(key)
+    if hit is None:
+        p = hp.plan
+        hit = _native.lanes_fixed(torch.tensor([list(r) for r in hp.desc_rows], dtype=torch.int32), p.wc, p.wr,
+                                  p.d_out, pa, pt)
         kernel.__dict__[key] = hit
     return hit
 
@@ -1114,10 +1134,12 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
     """Every head's ``forward_factored_aggregated`` at once: ``(N, H, d_out)``.
 
     ``h`` is every head's trunk features in edge order; alternatively
-    ``trunk(rho)`` computes them from ``rho = d / cutoff`` in whatever order
-    it is given, which lets the grouped kernels have them in the grouping's
-    order directly.  Heads too wide for the grouped kernels run there as
-    shares of their output copies (:func:`head_split`)."""
+    ``trunk(rho, dtype)`` computes them from ``rho = d / cutoff`` in whatever
+    order it is given (in ``dtype``, None for rho's), which lets the grouped
+    kernels have them in the grouping's order directly.  Heads too wide for
+    the grouped kernels run there as shares of their output copies
+    (:func:`head_split`).  Bfloat16 node rows keep the per-edge streams in
+    bfloat16 (:data:`BF16_STREAMS`)."""
     K = (h.shape[2] if h is not None else kernels[0].complex_head.in_features) + 1
     # bfloat16 rows: the node mixes read them as they are, everything after runs in float32
     dtype = h.dtype if h is not None else (torch.float32 if x.dtype == torch.bfloat16 else x.dtype)
@@ -1132,7 +1154,10 @@ def forward_aggregated_heads(kernels: list[Any], x: SO2FeatureField, edges: Any,
         st = grouped_streams(edges, order, kernels[0].radial_basis.cutoff, pa, pt, dtype)
         fused = (FUSED_TRUNK and split == 1 and len(kernels) <= 8 and trunk is not None
                  and _lanes_apply(kernels[0], hp, pa, pt))
-        h_g = None if fused else (trunk(st.rho_g) if trunk is not None else h.index_select(1, st.perm))
+        b16 = (BF16_STREAMS and not fused and trunk is not None and x.dtype == torch.bfloat16
+               and _lanes_fixed(kernels[0], hp, pa, pt))
+        h_g = None if fused else (trunk(st.rho_g, torch.bfloat16 if b16 else None) if trunk is not None
+                                  else h.index_select(1, st.perm))
         if st.group_order is None and os.environ.get("GM_FACTORED_LPT", "0") == "1":
             # the groups largest first: the long pole groups start early instead of trailing the launch
             st.group_order = torch.argsort(group_ptr[1:] - group_ptr[:-1], descending=True, stable=True).contiguous()
@@ -1178,7 +1203,7 @@ def forward_aggregated_shares(kernel: Any, x: SO2FeatureField, edges: Any, weigh
         groups = groups_for(edges, edges.source_index)
     values = [kernel]
     if radial.eligible(values, x.dtype, x.device):
-        h, trunk = None, lambda rho: radial.trunk_hidden_heads(values, rho)
+        h, trunk = None, lambda rho, dtype=None: radial.trunk_hidden_heads(values, rho, dtype)
     else:
         h, trunk = kernel._trunk_hidden(edges.distances).unsqueeze(0), None
     out = forward_aggregated_heads(values, x, edges, weights.unsqueeze(1), h, groups, trunk)

@@ -39,13 +39,16 @@ def eligible(kernels: list[Any], dtype: torch.dtype, device: torch.device) -> bo
 
 
 class RadialTrunk(torch.autograd.Function):
-    """``h (H, E, 16)`` from ``rho = d / cutoff`` and the heads' stacked trunk parameters."""
+    """``h (H, E, 16)`` from ``rho = d / cutoff`` and the heads' stacked trunk
+    parameters, in rho's dtype or ``dtype`` (bfloat16 features, float32
+    arithmetic; the gradient ``dh`` then comes in bfloat16 too)."""
 
     @staticmethod
-    def forward(ctx: Any, rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor, width: float) -> Tensor:
+    def forward(ctx: Any, rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor, width: float,
+                dtype: torch.dtype | None = None) -> Tensor:
         with torch.profiler.record_function("gm::kernel/radial"):
             h = _native.radial_trunk_forward(rho, weight.contiguous(), None if bias is None else bias.contiguous(),
-                                             centers, width)
+                                             centers, width, dtype)
         ctx.save_for_backward(rho, weight, bias if bias is not None else torch.empty(0, device=rho.device), centers)
         ctx.has_bias = bias is not None
         ctx.width = width
@@ -58,7 +61,7 @@ class RadialTrunk(torch.autograd.Function):
         with torch.profiler.record_function("gm::kernel/radial_backward"):
             dw, db = _native.radial_trunk_backward(dh.contiguous(), rho, weight.contiguous(),
                                                    bias.contiguous() if ctx.has_bias else None, centers, ctx.width)
-        return None, dw, db if ctx.has_bias else None, None, None
+        return None, dw, db if ctx.has_bias else None, None, None, None
 
 
 def stacked_trunk(kernels: list[Any]) -> tuple[Tensor, Tensor | None, Any]:
@@ -72,9 +75,10 @@ def stacked_trunk(kernels: list[Any]) -> tuple[Tensor, Tensor | None, Any]:
 HEADS_PER_LAUNCH = 8
 
 
-def trunk_hidden_heads(kernels: list[Any], rho: Tensor) -> Tensor:
+def trunk_hidden_heads(kernels: list[Any], rho: Tensor, dtype: torch.dtype | None = None) -> Tensor:
     """The stacked heads' trunk features ``(H, E, 16)`` on ``rho = d / cutoff``,
-    at most ``HEADS_PER_LAUNCH`` heads a launch."""
+    at most ``HEADS_PER_LAUNCH`` heads a launch, in rho's dtype or ``dtype``
+    (bfloat16: float32 arithmetic, the features rounded as stored)."""
     rb = kernels[0].radial_basis
     rho = rho.contiguous()
     parts = []
@@ -83,5 +87,5 @@ def trunk_hidden_heads(kernels: list[Any], rho: Tensor) -> Tensor:
         weight = torch.stack([list(k.radial_trunk)[0].weight for k in chunk])
         biases = [list(k.radial_trunk)[0].bias for k in chunk]
         bias = None if biases[0] is None else torch.stack(biases)
-        parts.append(RadialTrunk.apply(rho, weight, bias, rb.centers.contiguous(), float(rb.width)))
+        parts.append(RadialTrunk.apply(rho, weight, bias, rb.centers.contiguous(), float(rb.width), dtype))
     return parts[0] if len(parts) == 1 else torch.cat(parts, dim=0)

@@ -526,6 +526,32 @@ int gm_factored_backward_grouped_ld_f32(const float* g, int64_t g_ld, const int6
                                         const float* trunk_centers, int64_t trunk_nb, double trunk_width,
                                         int64_t accumulate, float* dh_g, float* dweights_g, void* stream);
 
+/* The grouped forward and backward with the per-edge streams h_g, rows_g and
+ * dh_g in bfloat16 (rounded to nearest even on store, widened exactly on
+ * load; every product and sum in float32, the gradients g and the weights
+ * float32): the value kernels of a bfloat16 transformer block, whose
+ * reference keeps these streams in the rows' dtype (nn/blocks.py:326-349
+ * over the factored path, fused_factored.py:247-299).  Plans whose lane
+ * slots are one of the compiled-in tables only (gm_factored_lanes_fixed), the
+ * trunk read (no fused trunk).  Arguments otherwise as the float32 entries. */
+int gm_factored_forward_grouped_bf16(const uint16_t* h_g, const float* const* z, const int64_t* node_stride,
+                                     const int64_t* t_stride, const int64_t* width, int64_t n_runs,
+                                     const float* phase_g, const float* rho_g, const float* zw_g,
+                                     const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source,
+                                     const int64_t* group_order, int64_t n_nodes, int64_t n_edges, int64_t n_groups,
+                                     int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt, int64_t n_blocks,
+                                     int64_t d_out, uint16_t* rows_g, void* stream);
+int gm_factored_backward_grouped_ld_bf16(const float* g, int64_t g_ld, const int64_t* target_g,
+                                         const float* weights_g, const uint16_t* rows_g, const uint16_t* h_g,
+                                         const float* const* z, float* const* dz, const int64_t* node_stride,
+                                         const int64_t* t_stride, const int64_t* width, int64_t n_runs,
+                                         const float* phase_g, const float* rho_g, const float* zw_g,
+                                         const int32_t* desc, const int64_t* group_ptr, const int64_t* group_source,
+                                         const int64_t* group_order, int64_t n_nodes, int64_t n_edges,
+                                         int64_t n_groups, int64_t K, int64_t wc, int64_t wr, int64_t pa, int64_t pt,
+                                         int64_t n_blocks, int64_t d_out, int64_t accumulate, uint16_t* dh_g,
+                                         float* dweights_g, void* stream);
+
 /* gm_factored_aggregate with edge e's row at rows[inv[e]] (rows kept in the
  * grouping's order; inv is the grouping's inverse permutation). */
 int gm_factored_aggregate_gather_f32(const float* rows, const int64_t* inv, const float* weights,
@@ -555,6 +581,18 @@ int64_t gm_radial_trunk_partials(int64_t n_edges);
 int gm_radial_trunk_backward_f32(const float* dh, const float* rho, const float* weight, const float* bias,
                                  const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B, double width,
                                  float* partial, float* dparams, void* stream);
+
+/* The same trunk with its features h, and in the backward their gradients dh,
+ * stored in bfloat16 (round to nearest even on store, widened exactly on
+ * load; float32 arithmetic): the trunk of a bfloat16 transformer block, whose
+ * per-edge streams the reference's block keeps in the rows' dtype
+ * (nn/blocks.py:326-349 over nn/kernels.py:605-607).  h and dh 8-byte aligned. */
+int gm_radial_trunk_forward_bf16(const float* rho, const float* weight, const float* bias, const float* centers,
+                                 int64_t n_edges, int64_t H, int64_t T, int64_t B, double width, uint16_t* h,
+                                 void* stream);
+int gm_radial_trunk_backward_bf16(const uint16_t* dh, const float* rho, const float* weight, const float* bias,
+                                  const float* centers, int64_t n_edges, int64_t H, int64_t T, int64_t B, double width,
+                                  float* partial, float* dparams, void* stream);
 
 /* ---------------- node mixes (the factored kernel's channel mixing) ----------------
  *
@@ -635,6 +673,13 @@ int gm_factored_aggregate_heads_f32(const float* rows, const int64_t* inv, const
                                     int64_t n_targets, int64_t n_edges, int64_t H, int64_t d_out, int64_t split,
                                     float* out, void* stream);
 
+/* The same aggregate over bfloat16 rows (widened exactly as read; float32
+ * sums and output): the rows of gm_factored_forward_grouped_bf16.  d_out a
+ * multiple of 4, rows 8-byte and out 16-byte aligned. */
+int gm_factored_aggregate_heads_bf16(const uint16_t* rows, const int64_t* inv, const float* alpha,
+                                     const int64_t* row_ptr, int64_t n_targets, int64_t n_edges, int64_t H,
+                                     int64_t d_out, int64_t split, float* out, void* stream);
+
 /* A row gather fused with a transpose, and its inverse:
  *   gm_gather_transpose_f32:  dst_t[h, g] = src[perm[g], h]   src (n, width), dst_t (width, n)
  *   gm_scatter_transpose_f32: dst[perm[g], h] = src_t[h, g]   src_t (width, n), dst (n, width)
@@ -661,6 +706,12 @@ int gm_scatter_transpose_f32(const float* src_t, const int64_t* perm, int64_t n,
  * tests and tools. */
 int gm_factored_lane_tables(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out, int64_t pa,
                             int64_t pt, int32_t* n_slots, uint32_t* slot, uint8_t* slotcol);
+
+/* *fixed = 1 when a plan's lane slots are one of the compiled-in tables (the
+ * kernels that also serve the bfloat16 streams; GM_FACTORED_STATIC=0 declines
+ * them), else 0.  Host only; no counterpart in the reference. */
+int gm_factored_lanes_fixed(const int32_t* desc, int64_t n_blocks, int64_t wc, int64_t wr, int64_t d_out, int64_t pa,
+                            int64_t pt, int32_t* fixed);
 
 /* ---------------- steerable kernel pair terms (per-edge readout) ----------------
  *
