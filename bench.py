@@ -142,8 +142,9 @@ def cost_factored_forward_grouped(a, kw, out):
     K, C, wc = _factored_shape(*a[12:15])
     d_out = a[15]
     E = rho_g.shape[0]
-    h_bytes = 4 * (K - 1) if h_g is not None else 4
-    return E * (h_bytes + 16 + 4 * d_out) + n_nodes * 4 * K * C, E * (2.0 * K * C + 8 * wc)
+    es = _es(h_g) if h_g is not None else 4  # bfloat16 streams: h and the rows at 2 bytes
+    h_bytes = es * (K - 1) if h_g is not None else 4
+    return E * (h_bytes + 16 + es * d_out) + n_nodes * 4 * K * C, E * (2.0 * K * C + 8 * wc)
 
 
 def cost_factored_backward_grouped(a, kw, out):
@@ -151,8 +152,9 @@ def cost_factored_backward_grouped(a, kw, out):
     K, C, wc = _factored_shape(*a[16:19])
     d_out = g.shape[1]
     E = rho_g.shape[0]
-    h_bytes = 4 * (K - 1) if h_g is not None else 4
-    per_edge = h_bytes + 16 + 4 + 8 + 2 * 4 * d_out + 4 * (K - 1) + 4
+    es = _es(h_g) if h_g is not None else 4  # bfloat16 streams: h, the rows and dh at 2 bytes
+    h_bytes = es * (K - 1) if h_g is not None else 4
+    per_edge = h_bytes + 16 + 4 + 8 + 4 * d_out + es * d_out + es * (K - 1) + 4
     return E * per_edge + 2 * n_nodes * 4 * K * C, E * (4.0 * K * C + 8 * wc)
 
 
@@ -181,21 +183,23 @@ def cost_aggregate_heads(a, kw, out):
     rows, inv, alpha, row_ptr = a[:4]
     H, E, d_out = rows.shape
     N = row_ptr.shape[0] - 1
-    return E * (8 + 4 * alpha.shape[1] + 4 * H * d_out) + N * (4 * H * d_out + 8), E * 2.0 * H * d_out
+    return E * (8 + 4 * alpha.shape[1] + _es(rows) * H * d_out) + N * (4 * H * d_out + 8), E * 2.0 * H * d_out
 
 
 def cost_trunk_forward(a, kw, out):
     rho, weight = a[:2]
     H, T, B = weight.shape
     E = rho.shape[0]
-    return E * (4 + 4 * H * T), E * H * (2.0 * T * B + 20 * T)
+    dtype = a[5] if len(a) > 5 else kw.get("dtype")  # the features' storage type (None: rho's, float32)
+    es = dtype.itemsize if dtype is not None else 4
+    return E * (4 + es * H * T), E * H * (2.0 * T * B + 20 * T)
 
 
 def cost_trunk_backward(a, kw, out):
     dh, rho, weight = a[:3]
     H, T, B = weight.shape
     E = rho.shape[0]
-    return E * (4 + 4 * H * T), E * H * (4.0 * T * B + 30 * T)
+    return E * (4 + _es(dh) * H * T), E * H * (4.0 * T * B + 30 * T)
 
 
 def cost_node_mix_forward(a, kw, out):

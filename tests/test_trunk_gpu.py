@@ -53,6 +53,7 @@ def test_trunk_matches_the_oracle(n_basis, bias, offset, cuda):
     (h * probe.float().to(cuda)).sum().backward()
     for head in range(5):
         w = want[head]
+        problems.report_strict(h[head].detach(), w, f"h[{head}]")
         torch.testing.assert_close(h[head].detach().double().cpu(), w, rtol=1e-5, atol=1e-6 * float(w.abs().max()))
         lin = list(gk[head].radial_trunk)[0]
         got = [lin.weight.grad] + ([lin.bias.grad] if bias else [])
