@@ -153,6 +153,10 @@ constexpr uint32_t kOrders012 = 0x22110u;
 // edges past that park their raw score in alpha and are read back for the sum
 // and for the quotient.
 constexpr int kSmRegs = 16;
+// Parked scores a lane reads back per batch (their loads in flight together).
+constexpr int kSmTail = 8;
+// Steps of the batched per-source pass whose rows are requested together.
+constexpr int kSrcPair = 2;
 constexpr bool kSmPrefetch = true;  // next step's source ids requested before this step's rows are used
 // Edges a lane of the per-target backward keeps alpha and dalpha of in registers (a multiple of 4).
 constexpr int kSmBwdRegs = 8;
@@ -359,14 +363,38 @@ __global__ __launch_bounds__(256) void softmax_forward_fast(SmArgs<T> a) {
       l += sc[r];
     }
   }
-  for (int64_t e = tail; e < e1; e += S) l += gm_exp(a.alpha[e * H + h] - m);
+  // the parked scores, kSmTail a batch with their loads in flight together, summed in edge order
+  constexpr int TU = kSmTail;
+  for (int64_t eb = tail; eb < e1; eb += (int64_t)TU * S) {
+    T v[TU];
+#pragma unroll
+    for (int u = 0; u < TU; ++u) {
+      const int64_t e = eb + (int64_t)u * S;
+      v[u] = e < e1 ? a.alpha[e * H + h] : T(0);
+    }
+#pragma unroll
+    for (int u = 0; u < TU; ++u)
+      if (eb + (int64_t)u * S < e1) l += gm_exp(v[u] - m);
+  }
   l = group_sum_pow2(l, H);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t e = e0 + s + (int64_t)r * S;
     if (e < e1) a.alpha[e * H + h] = sc[r] / l;
   }
-  for (int64_t e = tail; e < e1; e += S) a.alpha[e * H + h] = gm_exp(a.alpha[e * H + h] - m) / l;
+  for (int64_t eb = tail; eb < e1; eb += (int64_t)TU * S) {
+    T v[TU];
+#pragma unroll
+    for (int u = 0; u < TU; ++u) {
+      const int64_t e = eb + (int64_t)u * S;
+      v[u] = e < e1 ? a.alpha[e * H + h] : T(0);
+    }
+#pragma unroll
+    for (int u = 0; u < TU; ++u) {
+      const int64_t e = eb + (int64_t)u * S;
+      if (e < e1) a.alpha[e * H + h] = gm_exp(v[u] - m) / l;
+    }
+  }
 }
 
 // The forward for compiled-in chunk orders, with each edge's own entries
@@ -400,18 +428,20 @@ __global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
   if (i >= a.n_nodes) return;
   const int H = kWave / S;
   const int h = lane & (H - 1), s = lane / H;
-  const int64_t e0 = a.row_ptr[i], e1 = a.row_ptr[i + 1];
 
   int64_t off[NCH];
   float q[NCH * 4];
-  const auto qi = rows_of<T, B16, false>(a) + i * a.D;
+  int64_t e1 = 0;  // the current target's row end (the lambdas below read it)
+  auto load_q = [&](int64_t it) {
+    const auto qi = rows_of<T, B16, false>(a) + it * a.D;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    off[c] = a.C.base[c] + h * a.C.stride[c];
-    const Quad<float> x = row4<float>(qi + off[c]);
+    for (int c = 0; c < NCH; ++c) {
+      off[c] = a.C.base[c] + h * a.C.stride[c];
+      const Quad<float> x = row4<float>(qi + off[c]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) q[4 * c + u] = x.v[u];
-  }
+      for (int u = 0; u < 4; ++u) q[4 * c + u] = x.v[u];
+    }
+  };
   auto load_batch = [&](int64_t base, EdgeBatch<MO>& b) {
     const int64_t e = base + lane;
     if (e < e1) {
@@ -453,6 +483,68 @@ __global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
     const float acc = score_dot<float, NCH, ORD>(a.C, q, g, 0);
     return bm == neg_inf<float>() ? neg_inf<float>() : a.scale * acc + bm;
   };
+  // park the scores of the batches from `first` in alpha; the lane's maximum
+  auto park = [&](int64_t first, float m) {
+    EdgeBatch<MO> cur, nxt;
+    if (first < e1) load_batch(first, cur);
+    for (int64_t base = first; base < e1; base += kWave) {
+      if (base + kWave < e1) load_batch(base + kWave, nxt);
+#pragma unroll
+      for (int t = 0; t < SB; ++t) {
+        if (base + t * S >= e1) break;
+        const float lw = score(cur, t);
+        const int64_t e = base + t * S + s;
+        if (e < e1) a.alpha[e * H + h] = lw;
+        m = lw > m ? lw : m;
+      }
+      cur = nxt;
+    }
+    return m;
+  };
+  // the parked scores of those batches: the lane's sum of exp(s - m), in edge order, each batch's
+  // loads in flight together (one round trip a batch)
+  auto parked_sum = [&](int64_t first, float m) {
+    float l = 0.f;
+    for (int64_t eb = first + s; eb < e1; eb += kWave) {
+      float v[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int64_t e = eb + (int64_t)u * S;
+        v[u] = e < e1 ? a.alpha[e * H + h] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+        if (eb + (int64_t)u * S < e1) l += gm_exp(v[u] - m);
+    }
+    return l;
+  };
+  auto parked_quotients = [&](int64_t first, float m, float l) {
+    for (int64_t eb = first + s; eb < e1; eb += kWave) {
+      float v[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int64_t e = eb + (int64_t)u * S;
+        v[u] = e < e1 ? a.alpha[e * H + h] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int64_t e = eb + (int64_t)u * S;
+        if (e < e1) a.alpha[e * H + h] = gm_exp(v[u] - m) / l;
+      }
+    }
+  };
+  auto wave_max = [&](float m) {
+    for (int o = H; o < kWave; o <<= 1) {
+      const float mo = __shfl_xor(m, o, kWave);
+      m = mo > m ? mo : m;
+    }
+    return m;
+  };
+
+  const int64_t e0 = a.row_ptr[i];
+  e1 = a.row_ptr[i + 1];
+  load_q(i);
+  // a lane's first R scores stay in registers, later ones park in alpha
   EdgeBatch<MO> cur, nxt;
   load_batch(e0, cur);
   float sc[R];
@@ -471,22 +563,7 @@ __global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
     cur = nxt;
   }
   const int64_t tail = e0 + (int64_t)R * S;
-  for (int64_t base = tail; base < e1; base += kWave) {
-    if (base + kWave < e1) load_batch(base + kWave, nxt);
-#pragma unroll
-    for (int t = 0; t < SB; ++t) {
-      if (base + t * S >= e1) break;
-      const float lw = score(cur, t);
-      const int64_t e = base + t * S + s;
-      if (e < e1) a.alpha[e * H + h] = lw;
-      m = lw > m ? lw : m;
-    }
-    cur = nxt;
-  }
-  for (int o = H; o < kWave; o <<= 1) {
-    const float mo = __shfl_xor(m, o, kWave);
-    m = mo > m ? mo : m;
-  }
+  m = wave_max(park(tail, m));
   float l = 0.f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -495,14 +572,14 @@ __global__ __launch_bounds__(256) void softmax_forward_batched(SmArgs<T> a) {
       l += sc[r];
     }
   }
-  for (int64_t e = tail + s; e < e1; e += S) l += gm_exp(a.alpha[e * H + h] - m);
+  l += parked_sum(tail, m);
   l = group_sum_pow2(l, H);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t e = e0 + s + (int64_t)r * S;
     if (e < e1) a.alpha[e * H + h] = sc[r] / l;
   }
-  for (int64_t e = tail + s; e < e1; e += S) a.alpha[e * H + h] = gm_exp(a.alpha[e * H + h] - m) / l;
+  parked_quotients(tail, m, l);
 }
 
 // Backward per target: the adjoint's per-head total, ds, and dq.  ds goes to
@@ -533,14 +610,15 @@ __global__ __launch_bounds__(256) void softmax_backward_target_fast(SmArgs<T> a)
 #pragma unroll
   for (int r = 0; r < RB; r += 4)
     total += (ar[r] * dr[r] + ar[r + 1] * dr[r + 1]) + (ar[r + 2] * dr[r + 2] + ar[r + 3] * dr[r + 3]);
-  for (int64_t e = e0 + s + (int64_t)RB * S; e < e1; e += 4 * S) {
-    T p[4];
+  for (int64_t e = e0 + s + (int64_t)RB * S; e < e1; e += 8 * S) {
+    T p[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 8; ++u) {
       const int64_t f = e + (int64_t)u * S;
       p[u] = f < e1 ? a.alpha_in[f * H + h] * a.dalpha[f * H + h] : T(0);
     }
     total += (p[0] + p[1]) + (p[2] + p[3]);
+    total += (p[4] + p[5]) + (p[6] + p[7]);
   }
   total = group_sum_pow2(total, H);
 
@@ -745,33 +823,40 @@ __global__ __launch_bounds__(256) void softmax_backward_source_batched(SmArgs<T>
   for (int64_t base = g0; base < g1; base += kWave) {
     if (base + kWave < g1)
       load_ids<MO>(nxt, base + kWave + lane, g1, a.target_s, a.transport_s, a.orders);
+    // two steps' rows and ds requested before either is used: two round trips in flight a wave
 #pragma unroll
-    for (int t = 0; t < SB; ++t) {
+    for (int t = 0; t < SB; t += kSrcPair) {
       if (base + t * S >= g1) break;
-      const int from = t * S + s;
-      const int64_t g = base + from;
-      const bool live = g < g1;
-      float cs[MO + 1], sn[MO + 1];
-      const int ti = take_ids<MO>(cur, from, cs, sn);
-      const float ds = live ? a.ds[g * H + h] : 0.f;
-      Quad<float> qq[NCH];
-      const auto r = qrows + (int64_t)ti * a.D;
+      Quad<float> qq[kSrcPair][NCH];
+      float cs[kSrcPair][MO + 1], sn[kSrcPair][MO + 1], ds[kSrcPair];
+      bool live[kSrcPair];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) qq[c] = row4<float>(r + off[c]);
-      if (live) {
+      for (int u = 0; u < kSrcPair; ++u) {
+        const int from = (t + u) * S + s;
+        const int64_t g = base + from;
+        live[u] = t + u < SB && g < g1;
+        const int ti = take_ids<MO>(cur, t + u < SB ? from : s, cs[u], sn[u]);
+        ds[u] = live[u] ? a.ds[g * H + h] : 0.f;
+        const auto r = qrows + (int64_t)ti * a.D;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) qq[u][c] = row4<float>(r + off[c]);
+      }
+#pragma unroll
+      for (int u = 0; u < kSrcPair; ++u) {
+        if (!live[u]) continue;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
           const int o = chunk_order<ORD>(a.C, c);
           if (o == 0) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds * qq[c].v[v];
+            for (int v = 0; v < 4; ++v) acc[4 * c + v] += ds[u] * qq[u][c].v[v];
           } else {
-            const float cr = cs[o], ci = sn[o];
+            const float cr = cs[u][o], ci = sn[u][o];
             // conj(tau) q = (c q0 + s q1, c q1 - s q0)
-            acc[4 * c + 0] += ds * (cr * qq[c].v[0] + ci * qq[c].v[1]);
-            acc[4 * c + 1] += ds * (cr * qq[c].v[1] - ci * qq[c].v[0]);
-            acc[4 * c + 2] += ds * (cr * qq[c].v[2] + ci * qq[c].v[3]);
-            acc[4 * c + 3] += ds * (cr * qq[c].v[3] - ci * qq[c].v[2]);
+            acc[4 * c + 0] += ds[u] * (cr * qq[u][c].v[0] + ci * qq[u][c].v[1]);
+            acc[4 * c + 1] += ds[u] * (cr * qq[u][c].v[1] - ci * qq[u][c].v[0]);
+            acc[4 * c + 2] += ds[u] * (cr * qq[u][c].v[2] + ci * qq[u][c].v[3]);
+            acc[4 * c + 3] += ds[u] * (cr * qq[u][c].v[3] - ci * qq[u][c].v[2]);
           }
         }
       }

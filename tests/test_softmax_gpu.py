@@ -29,6 +29,12 @@ CASES = [
     # S = 4 (sixteen heads) and S = 32 (two heads) here
     (12, 24, 1, {0: 64, 1: 64, 2: 64}, 16, "hard"),
     (12, 24, 2, {0: 8, 1: 8, 2: 8}, 2, "quartic"),
+    # rows of more than 256 edges (the polar caps of these grids: up to 4 nlon edges), which the
+    # batched forward shares among a workgroup's waves, at every slot count
+    (48, 96, 1, {0: 32, 1: 32, 2: 32}, 8, "hard"),
+    (40, 80, 1, {0: 16, 1: 16, 2: 16}, 4, "quartic"),
+    (40, 80, 1, {0: 64, 1: 64, 2: 64}, 16, "hard"),
+    (40, 80, 1, {0: 8, 1: 8, 2: 8}, 2, "quartic"),
     # ... and the generic path (odd segments, three heads; sixteen heads of 20 chunks)
     (12, 24, 1, {0: 6, 1: 4, 2: 2}, 2, "quartic"),
     (10, 20, 1, {0: 3, 1: 3, 2: 3}, 3, "hard"),
