@@ -313,21 +313,45 @@ __device__ __forceinline__ bool tile_live(const RadialConvArgs& a, int m) {
   return m < kRNS ? m < a.ns : m - kRNS < a.nc;
 }
 
+// A coefficient tile's source values and target gradient pieces for the lane
+// (a scalar tile's four, a complex tile's pair in x and y), requested a tile
+// ahead of their use so the walk does not wait a round trip per tile.
+struct TileIn {
+  float4 x, g;
+};
+
+__device__ __forceinline__ TileIn tile_in(const RadialConvArgs& a, int m, int q, const float* vj, const float* gt) {
+  TileIn t{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  if (m < kRNS) {
+    const int col = 16 * m + 4 * q;
+    if (m < a.ns && col < a.a0) {
+      t.x = *reinterpret_cast<const float4*>(vj + col);
+      t.g = *reinterpret_cast<const float4*>(gt + col);
+    }
+  } else if (m - kRNS < a.nc) {
+    const int col = a.tile_col[m - kRNS] + 2 * q;
+    const float2 x = ld2(vj + col), g = ld2(gt + col);
+    t.x = make_float4(x.x, x.y, 0.f, 0.f);
+    t.g = make_float4(g.x, g.y, 0.f, 0.f);
+  }
+  return t;
+}
+
 // The backward of one coefficient tile for the lane's edge: the coefficients
 // again (times w), the copy's value gradient into dv, and the coefficients'
-// gradient dC (rows 4q..4q+3, D layout).
+// gradient dC (rows 4q..4q+3, D layout), from the tile's pieces `in`.
 template <bool SPLIT>
 __device__ __forceinline__ void tile_dc(const RadialConvArgs& a, const float* rf_s, const SplitTile* rs_s,
                                         const float* bias_s, int m, int lane, int q, const EdgeView& ev,
-                                        const float (&bv)[4], const SplitB& hb, const float* vj, const float* gt,
+                                        const float (&bv)[4], const SplitB& hb, const TileIn& in,
                                         float (&dv)[4], float (&dc)[4]) {
   const floatx4 d = coefficients_of<SPLIT>(rf_s, rs_s, bias_s, m, lane, q, ev.w, bv, hb);
   if (m < kRNS) {
     const int col = 16 * m + 4 * q;
     dc[0] = dc[1] = dc[2] = dc[3] = 0.f;
     if (col < a.a0) {
-      const float4 x = *reinterpret_cast<const float4*>(vj + col);
-      const float4 gv = *reinterpret_cast<const float4*>(gt + col);
+      const float4 x = in.x;
+      const float4 gv = in.g;
       dv[0] = fmaf(d[0], gv.x, dv[0]);
       dv[1] = fmaf(d[1], gv.y, dv[1]);
       dv[2] = fmaf(d[2], gv.z, dv[2]);
@@ -341,8 +365,7 @@ __device__ __forceinline__ void tile_dc(const RadialConvArgs& a, const float* rf
   }
   const int mc = m - kRNS;
   const bool one = a.tile_n[mc] == 1;
-  const int col = a.tile_col[mc] + 2 * q;
-  const float2 x = ld2(vj + col), gv = ld2(gt + col);
+  const float2 x = make_float2(in.x.x, in.x.y), gv = make_float2(in.g.x, in.g.y);
   const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
   const float pr = one ? ev.p1.x : ev.p2.x, pi = one ? ev.p1.y : ev.p2.y;
   const float zr = tc * x.x - ts * x.y, zi = tc * x.y + ts * x.x;
@@ -419,17 +442,21 @@ __device__ __forceinline__ void backward_walk(const RadialConvArgs& a, float* pa
       for (int s = 0; s < 4; ++s) ht[s] = T[(4 * s + q) * 16 + c];
       const float* gt = a.g + ev.node * a.D;
       floatx4 dh[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+      static_assert(kRChunk == 1, "the tiles' pieces are requested one tile ahead");
+      TileIn in_next = tile_in(a, T0, q, vj, gt);
       // kRChunk tiles at a time: dC and dh~ += R^T dC from the D layout, then dC through the
       // wave's LDS into the A-operand layout dC[row c][edge 4s + q] (one hand-over per
       // chunk), the bias column sums and dR += dC h~^T
 #pragma unroll
       for (int i0 = 0; i0 < G; i0 += kRChunk) {
         float dcs[kRChunk][4];
+        const TileIn in = in_next;
+        if (i0 + 1 < G) in_next = tile_in(a, T0 + i0 + 1, q, vj, gt);
 #pragma unroll
         for (int p = 0; p < kRChunk; ++p) {
           const int i = i0 + p, m = T0 + i;
           if (i < G && tile_live(a, m)) {
-            tile_dc<SPLIT>(a, rf_s, rs_s, bias_s, m, lane, q, ev, bv, hb, vj, gt, dvx[i], dcs[p]);
+            tile_dc<SPLIT>(a, rf_s, rs_s, bias_s, m, lane, q, ev, bv, hb, in, dvx[i], dcs[p]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) dh[i & 1] = mfma16(rb_s[(m * 4 + r) * 64 + lane], dcs[p][r], dh[i & 1]);
           }
