@@ -103,7 +103,8 @@ __device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x)
 __device__ __forceinline__ float2 ld2(const float* p) { return *reinterpret_cast<const float2*>(p); }
 
 // One edge as a lane sees it: the source (or target), weight, transport
-// phases of orders 1 and 2 and the angular factors r^{2n} e^{2 i n phi}.
+// phases of orders 1 and 2 and the angular factors r^{2n} e^{2 i n phi}
+// (e^{2 i n phi} as loaded; with_radius applies r^{2n}).
 struct EdgeView {
   int64_t node;
   float w, r;
@@ -119,10 +120,18 @@ __device__ __forceinline__ EdgeView edge_view(const RadialConvArgs& a, int64_t e
   const float* an = a.angular + e * a.orders * 2;
   v.t1 = ld2(tr + 2);
   v.t2 = ld2(tr + 4);
+  v.p1 = ld2(an + 4);
+  v.p2 = ld2(an + 8);
+  return v;
+}
+
+// The view with its angular factors scaled by r^2 and r^4.  Kept apart from
+// edge_view so that a view requested a tile ahead leaves its loads in flight
+// until the tile that uses it.
+__device__ __forceinline__ EdgeView with_radius(EdgeView v) {
   const float r2 = v.r * v.r, r4 = r2 * r2;
-  const float2 a2 = ld2(an + 4), a4 = ld2(an + 8);
-  v.p1 = make_float2(r2 * a2.x, r2 * a2.y);
-  v.p2 = make_float2(r4 * a4.x, r4 * a4.y);
+  v.p1 = make_float2(r2 * v.p1.x, r2 * v.p1.y);
+  v.p2 = make_float2(r4 * v.p2.x, r4 * v.p2.y);
   return v;
 }
 
@@ -209,6 +218,24 @@ __device__ __forceinline__ floatx4 coefficients_of(const float* rf_s, const Spli
     return coefficients(rf_s, bias_s, m, lane, q, w, bv);
 }
 
+// Whether coefficient tile slot m holds copies (uniform).
+__device__ __forceinline__ bool tile_live(const RadialConvArgs& a, int m) {
+  return m < kRNS ? m < a.ns : m - kRNS < a.nc;
+}
+
+// Coefficient tile m's source values for the lane: a scalar tile's four, a
+// complex tile's pair in x and y (zeros for a dead tile or absent copies).
+__device__ __forceinline__ float4 tile_x(const RadialConvArgs& a, int m, int q, const float* vj) {
+  if (m < kRNS) {
+    const int col = 16 * m + 4 * q;
+    if (m < a.ns && col < a.a0) return *reinterpret_cast<const float4*>(vj + col);
+  } else if (m - kRNS < a.nc) {
+    const float2 x = ld2(vj + a.tile_col[m - kRNS] + 2 * q);
+    return make_float4(x.x, x.y, 0.f, 0.f);
+  }
+  return make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 template <int NB, bool SPLIT>
 __global__ __launch_bounds__(kRThreads) __attribute__((amdgpu_waves_per_eu(SPLIT ? 4 : 1))) void
 conv_radial_forward_kernel(RadialConvArgs a) {
@@ -239,7 +266,7 @@ conv_radial_forward_kernel(RadialConvArgs a) {
     nxt = edge_view(a, e, a.source[e], e0 + c < e1);
   }
   for (int64_t base = e0; base < e1; base += 16) {
-    const EdgeView ev = nxt;
+    const EdgeView ev = with_radius(nxt);
     if (base + 16 < e1) {
       const bool live = base + 16 + c < e1;
       const int64_t e = live ? base + 16 + c : e0;
@@ -255,11 +282,11 @@ conv_radial_forward_kernel(RadialConvArgs a) {
     const float* vj = a.v + ev.node * a.D;
 #pragma unroll
     for (int m = 0; m < kRNS; ++m) {
+      const float4 x = tile_x(a, m, q, vj);
       if (m < a.ns) {
       const floatx4 d = coefficients_of<SPLIT>(rf_s, rs_s, bias_s, m, lane, q, ev.w, bv, hb);
       const int col = 16 * m + 4 * q;
       if (col < a.a0) {
-        const float4 x = *reinterpret_cast<const float4*>(vj + col);
         accs[m][0] = fmaf(d[0], x.x, accs[m][0]);
         accs[m][1] = fmaf(d[1], x.y, accs[m][1]);
         accs[m][2] = fmaf(d[2], x.z, accs[m][2]);
@@ -269,10 +296,10 @@ conv_radial_forward_kernel(RadialConvArgs a) {
     }
 #pragma unroll
     for (int m = 0; m < kRNC; ++m) {
+      const float4 x = tile_x(a, kRNS + m, q, vj);
       if (m < a.nc) {
       const floatx4 d = coefficients_of<SPLIT>(rf_s, rs_s, bias_s, kRNS + m, lane, q, ev.w, bv, hb);
       const bool one = a.tile_n[m] == 1;
-      const float2 x = ld2(vj + a.tile_col[m] + 2 * q);
       const float tc = one ? ev.t1.x : ev.t2.x, ts = one ? ev.t1.y : ev.t2.y;
       const float pr = one ? ev.p1.x : ev.p2.x, pi = one ? ev.p1.y : ev.p2.y;
       const float zr = tc * x.x - ts * x.y, zi = tc * x.y + ts * x.x;
@@ -306,11 +333,6 @@ conv_radial_forward_kernel(RadialConvArgs a) {
 #pragma unroll
   for (int m = 0; m < kRNC; ++m)
     if (m < a.nc) *reinterpret_cast<float2*>(oi + a.tile_col[m] + 2 * q) = make_float2(accc[m][0], accc[m][1]);
-}
-
-// Whether coefficient tile slot m holds copies (uniform).
-__device__ __forceinline__ bool tile_live(const RadialConvArgs& a, int m) {
-  return m < kRNS ? m < a.ns : m - kRNS < a.nc;
 }
 
 // A coefficient tile's source values and target gradient pieces for the lane
@@ -425,7 +447,7 @@ __device__ __forceinline__ void backward_walk(const RadialConvArgs& a, float* pa
     for (int64_t base = g0; base < g1; base += 16) {
       const bool live = base + c < g1;
       const int64_t e = a.src_order[live ? base + c : g0];
-      const EdgeView ev = edge_view(a, e, a.target[e], live);
+      const EdgeView ev = with_radius(edge_view(a, e, a.target[e], live));
       float bas[NB], pre[4], h[4];
       trunk_of<NB>(a, w1s, ev.r, q, bas, pre, h);
       float bv[4];
