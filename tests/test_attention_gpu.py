@@ -297,5 +297,12 @@ def test_staged_mixes_backward_equals_the_register_staged_one(case, cuda, monkey
     near(results[0][0], results[1][0], "out")
     near(results[0][1]["x"], results[1][1]["x"], "x")
     assert set(results[0][2]) == set(results[1][2])
-    for n in results[1][2]:  # sums over every edge or node (a vanishing key bias is rounding noise in both)
+    scale = max(float(g.abs().max()) for g in results[1][2].values())
+    for n in results[1][2]:  # sums over every edge or node
+        if n.endswith("key.bias"):
+            # the softmax is invariant to a key bias: its gradient vanishes in exact arithmetic and holds
+            # float32 rounding noise in both forms (up to about 1e-6 with the fp32 matrix products)
+            for r in results:
+                assert float(r[2][n].abs().max()) <= 1e-5 * scale, f"{n}: {float(r[2][n].abs().max()):.3e}"
+            continue
         close(results[0][2][n], results[1][2][n], torch.float32, n, reduction=True)
