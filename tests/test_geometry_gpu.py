@@ -35,6 +35,12 @@ from oracle import sphere
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def gpu_builder_on(monkeypatch):
+    """These tests check the GPU builder itself, whatever GM_GPU_GEOMETRY says."""
+    monkeypatch.setattr(hip_builder, "ENABLED", True)
+
+
 def gpu_edges(nlat, nlon, radius, cuda):
     grid = build_equiangular_grid(nlat, nlon, device=cuda)
     assert hip_builder.applies(grid)
