@@ -95,11 +95,32 @@ __device__ __forceinline__ void wave_sync() {
 //     A2_j[m = c][k = q] = b_c(edge 4q + j) (c < B), 1 at c = B, 0 above,
 //   so D2's rows m < B are dW^T and row B is db, accumulated over the wave's
 //   tiles in registers for every head.  Edges past the end read dh as zero and add nothing.
-template <int B, bool B16 = false>
+// SPLIT: D1 as split-bf16 products (split.hpp), off the fp32 datapath that the
+// rest of the tile's arithmetic shares with fp32 MFMA: a lane's contraction
+// slots s are basis entries k = 4q + s (the bias at k = B); the heads' A1
+// pieces split once per workgroup into LDS, the basis pieces once per tile.
+template <int B, bool B16 = false, bool SPLIT = false>
 __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a) {
   constexpr int T = 16, P = T * B + T, LDT = T + 4;
   __shared__ __align__(16) float stage[kTrunkWaves][T * LDT];  // per wave: dp as [feature][edge]
+  __shared__ __align__(16) u32x4 a1p[SPLIT ? 2 * kTrunkMaxHeads * 64 : 1];  // [head][lane]: hm, hl
   const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15, wv = threadIdx.x >> 6;
+  if constexpr (SPLIT) {
+    for (int i = threadIdx.x; i < kTrunkMaxHeads * 64; i += kTrunkThreads) {
+      const int h = i >> 6, l = i & 63, f = l & 15, k0 = 4 * (l >> 4);
+      float x[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int k = k0 + s;
+        x[s] = h >= a.H ? 0.f
+                        : (k < B ? a.weight[(h * T + f) * B + k] : ((k == B && a.bias) ? a.bias[h * T + f] : 0.f));
+      }
+      const SplitA sa = split_a(x[0], x[1], x[2], x[3]);
+      a1p[2 * i] = sa.hm;
+      a1p[2 * i + 1] = sa.hl;
+    }
+    __syncthreads();
+  }
   float* tile_lds = stage[wv];
   const int64_t wave = (int64_t)blockIdx.x * kTrunkWaves + wv;
   const int64_t n_waves = (int64_t)gridDim.x * kTrunkWaves;
@@ -116,13 +137,18 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
   };
 #pragma unroll
   for (int h = 0; h < kTrunkMaxHeads; ++h) {
-    w0[h] = a1_weight(h, q);
-    w1[h] = a1_weight(h, q + 4);
-    w2[h] = q == 0 ? a1_weight(h, 8) : 0.f;
+    if constexpr (!SPLIT) {
+      w0[h] = a1_weight(h, q);
+      w1[h] = a1_weight(h, q + 4);
+      w2[h] = q == 0 ? a1_weight(h, 8) : 0.f;
+    }
     acc[h] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
   const float mu0 = q < B ? centers[q] : 0.f, mu1 = q + 4 < B ? centers[q + 4] : 0.f;
   const float mu2 = c < B ? centers[c] : 0.f;
+  float mus[4];  // SPLIT: the centres of the lane's basis slots 4q + s
+#pragma unroll
+  for (int s = 0; s < 4; ++s) mus[s] = 4 * q + s < B ? centers[4 * q + s] : 0.f;
   const float iw = a.inv_width;
   auto gauss = [iw](float r, float mu) {
     const float z = (r * r - mu) * iw;
@@ -184,12 +210,25 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
     float a2[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) a2[j] = c < B ? gauss(r4[j], mu2) : (c == B ? 1.f : 0.f);
+    SplitB b1p{};
+    if constexpr (SPLIT) {
+      float x[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) x[s] = 4 * q + s < B ? gauss(rc, mus[s]) : (4 * q + s == B ? 1.f : 0.f);
+      b1p = split_b(x[0], x[1], x[2], x[3]);
+    }
 #pragma unroll
     for (int h = 0; h < kTrunkMaxHeads; ++h) {
       if (h >= a.H) break;
-      floatx4 pre = mfma16(w0[h], b1_0, floatx4{0.f, 0.f, 0.f, 0.f});
-      pre = mfma16(w1[h], b1_1, pre);
-      if (B == 8) pre = mfma16(w2[h], b1_2, pre);
+      floatx4 pre;
+      if constexpr (SPLIT) {
+        pre = mfma_split(SplitA{a1p[2 * (h * 64 + lane)], a1p[2 * (h * 64 + lane) + 1]}, b1p,
+                         floatx4{0.f, 0.f, 0.f, 0.f});
+      } else {
+        pre = mfma16(w0[h], b1_0, floatx4{0.f, 0.f, 0.f, 0.f});
+        pre = mfma16(w1[h], b1_1, pre);
+        if (B == 8) pre = mfma16(w2[h], b1_2, pre);
+      }
       const float4 gw = widen(g[h]);
       const float gv[4] = {gw.x, gw.y, gw.z, gw.w};
       g[h] = load_dh(e_next, h);
@@ -330,10 +369,19 @@ constexpr int64_t kTrunkBlocks = 2048;  // about this many workgroups (waves str
 // fraction of the chip).  The grid (and so the backward's partial rows)
 // follows the B = 8 instance's occupancy for every basis size, per storage
 // type of the features (the bfloat16 backward holds fewer registers).
+// The backward's instance for features of this storage type: the split
+// pre-activations unless GM_SPLIT_PRODUCTS=0.
+template <int B>
+const void* backward_kernel(bool b16) {
+  if (split_products())
+    return b16 ? (const void*)trunk_backward_mfma<B, true, true> : (const void*)trunk_backward_mfma<B, false, true>;
+  return b16 ? (const void*)trunk_backward_mfma<B, true> : (const void*)trunk_backward_mfma<B>;
+}
+
 int64_t trunk_blocks(int64_t n_edges, bool forward, bool b16) {
   const int64_t need = (n_edges + 16 * kTrunkWaves - 1) / (16 * kTrunkWaves);  // one tile per wave
   const void* kernel = forward ? (b16 ? (const void*)trunk_forward_mfma<8, true> : (const void*)trunk_forward_mfma<8>)
-                               : (b16 ? (const void*)trunk_backward_mfma<8, true> : (const void*)trunk_backward_mfma<8>);
+                               : backward_kernel<8>(b16);
   const int64_t full = whole_rounds(kTrunkBlocks, resident_blocks(kernel, kTrunkThreads));
   return need < full ? (need > 0 ? need : 1) : full;
 }
@@ -349,6 +397,11 @@ void launch(bool forward, const TrunkArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL((trunk_forward_mfma<B, true>), grid, block, 0, stream, a);
     else
       hipLaunchKernelGGL((trunk_forward_mfma<B>), grid, block, 0, stream, a);
+  } else if (split_products()) {
+    if (a.dhb)
+      hipLaunchKernelGGL((trunk_backward_mfma<B, true, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((trunk_backward_mfma<B, false, true>), grid, block, 0, stream, a);
   } else {
     if (a.dhb)
       hipLaunchKernelGGL((trunk_backward_mfma<B, true>), grid, block, 0, stream, a);
