@@ -103,7 +103,7 @@ template <int B, bool B16 = false, bool SPLIT = false>
 __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a) {
   constexpr int T = 16, P = T * B + T, LDT = T + 4;
   __shared__ __align__(16) float stage[kTrunkWaves][T * LDT];  // per wave: dp as [feature][edge]
-  __shared__ __align__(16) u32x4 a1p[SPLIT ? 2 * kTrunkMaxHeads * 64 : 1];  // [head][lane]: hm, hl
+  __shared__ __align__(16) u32x4 a1p[SPLIT ? 2 * kTrunkMaxHeads * 64 : 1];  // [head][hm, hl][lane]
   const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15, wv = threadIdx.x >> 6;
   if constexpr (SPLIT) {
     for (int i = threadIdx.x; i < kTrunkMaxHeads * 64; i += kTrunkThreads) {
@@ -116,8 +116,8 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
                         : (k < B ? a.weight[(h * T + f) * B + k] : ((k == B && a.bias) ? a.bias[h * T + f] : 0.f));
       }
       const SplitA sa = split_a(x[0], x[1], x[2], x[3]);
-      a1p[2 * i] = sa.hm;
-      a1p[2 * i + 1] = sa.hl;
+      a1p[128 * h + l] = sa.hm;  // consecutive lanes read consecutive 16-byte pieces
+      a1p[128 * h + 64 + l] = sa.hl;
     }
     __syncthreads();
   }
@@ -222,8 +222,7 @@ __global__ __launch_bounds__(kTrunkThreads) void trunk_backward_mfma(TrunkArgs a
       if (h >= a.H) break;
       floatx4 pre;
       if constexpr (SPLIT) {
-        pre = mfma_split(SplitA{a1p[2 * (h * 64 + lane)], a1p[2 * (h * 64 + lane) + 1]}, b1p,
-                         floatx4{0.f, 0.f, 0.f, 0.f});
+        pre = mfma_split(SplitA{a1p[128 * h + lane], a1p[128 * h + 64 + lane]}, b1p, floatx4{0.f, 0.f, 0.f, 0.f});
       } else {
         pre = mfma16(w0[h], b1_0, floatx4{0.f, 0.f, 0.f, 0.f});
         pre = mfma16(w1[h], b1_1, pre);
