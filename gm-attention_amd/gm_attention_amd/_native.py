@@ -869,6 +869,8 @@ def aggregate_heads(rows: Tensor, inv: Tensor, alpha: Tensor, row_ptr: Tensor, s
         raise ValueError("rows (H, E, d_out; float32 or bfloat16) and alpha (E, H / split; float32), split dividing H")
     if not (rows.is_contiguous() and alpha.is_contiguous() and inv.is_contiguous() and row_ptr.is_contiguous()):
         raise ValueError("rows, alpha, inv and row_ptr must be contiguous")
+    if inv.dtype != torch.int64 or row_ptr.dtype != torch.int64 or inv.shape != (E,):
+        raise ValueError("inv must be int64 (E,) and row_ptr int64")
     if n_targets == 0:
         return out
     name = "gm_factored_aggregate_heads_bf16" if rows.dtype == torch.bfloat16 else "gm_factored_aggregate_heads_f32"
