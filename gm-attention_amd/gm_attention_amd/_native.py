@@ -714,6 +714,29 @@ def node_mix_backward_weight(v: Tensor, dmix: Tensor) -> Tensor:
     return dm
 
 
+def _index_vector(t: Tensor, n: int | None, name: str, dtype: torch.dtype = torch.int64) -> None:
+    """An index tensor the kernels read as contiguous entries of ``dtype`` (``n`` of them when given):
+    a wider or shorter one would send them past its end."""
+    if t.dtype != dtype or t.dim() != 1 or not t.is_contiguous() or (n is not None and t.shape[0] != n):
+        raise ValueError(f"{name} must be a contiguous {str(dtype).replace('torch.', '')} vector"
+                         + (f" of {n} entries" if n is not None else ""))
+
+
+def _edge_stream(t: Tensor | None, n_edges: int, width: int, name: str) -> None:
+    """A per-edge stream in the grouping's order: contiguous (n_edges, width) (or (n_edges,) for width 1)."""
+    if t is None:
+        return
+    shape = (n_edges,) if width == 1 else (n_edges, width)
+    if tuple(t.shape) != shape or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous {shape} tensor")
+
+
+def _grouping(group_ptr: Tensor, group_source: Tensor, group_order: Tensor | None) -> None:
+    _index_vector(group_source, None, "group_source")
+    _index_vector(group_ptr, group_source.shape[0] + 1, "group_ptr")
+    _check_order(group_order, group_source)
+
+
 def _check_order(group_order: Tensor | None, group_source: Tensor) -> None:
     if group_order is None:
         return
@@ -764,7 +787,9 @@ def factored_forward_grouped(h_g: Tensor | None, runs: MixRuns, n_nodes: int, ph
         raise ValueError("out must be a contiguous (n_edges, d_out) tensor in h's dtype")
     if n_edges == 0:
         return out
-    _check_order(group_order, group_source)
+    _grouping(group_ptr, group_source, group_order)
+    _edge_stream(h_g, n_edges, 16, "h_g")
+    _edge_stream(rho_g, n_edges, 1, "rho_g")
     hd = host_desc32(desc)
     if b16:
         _check(trunk is None, "bfloat16 trunk features are read, not evaluated in the kernels")
@@ -809,7 +834,13 @@ def factored_backward_grouped(g: Tensor, target_g: Tensor, weights_g: Tensor, ro
     n_edges = rho_g.shape[0]
     if n_edges == 0:
         return dweights
-    _check_order(group_order, group_source)
+    _grouping(group_ptr, group_source, group_order)
+    _index_vector(target_g, n_edges, "target_g")
+    _edge_stream(weights_g, n_edges, 1, "weights_g")
+    _edge_stream(rows_g, n_edges, g.shape[1], "rows_g")
+    _edge_stream(h_g, n_edges, 16, "h_g")
+    _edge_stream(dh_g, n_edges, 16, "dh_g")
+    _edge_stream(rho_g, n_edges, 1, "rho_g")
     hd = host_desc32(desc)
     # g may be one head's columns of a wider gradient array, read in place (rows g_ld floats apart)
     g_ld = g.stride(0) if g.dim() == 2 and g.stride(1) == 1 else -1
@@ -884,6 +915,7 @@ def gather_transpose(src: Tensor, perm: Tensor) -> Tensor:
     n, width = src.shape
     if src.dtype != torch.float32 or not src.is_contiguous() or perm.shape != (n,) or not perm.is_contiguous():
         raise ValueError("src must be a contiguous float32 (n, width) tensor and perm a contiguous (n,) index")
+    _index_vector(perm, n, "perm")
     out = torch.empty(width, n, dtype=src.dtype, device=src.device)
     _call("gm_gather_transpose_f32", _ptr(src), _ptr(perm), n, width, _ptr(out), _stream(src.device))
     return out
@@ -894,6 +926,7 @@ def scatter_transpose(src_t: Tensor, perm: Tensor) -> Tensor:
     width, n = src_t.shape
     if src_t.dtype != torch.float32 or not src_t.is_contiguous() or perm.shape != (n,) or not perm.is_contiguous():
         raise ValueError("src_t must be a contiguous float32 (width, n) tensor and perm a contiguous (n,) index")
+    _index_vector(perm, n, "perm")
     out = torch.empty(n, width, dtype=src_t.dtype, device=src_t.device)
     _call("gm_scatter_transpose_f32", _ptr(src_t), _ptr(perm), n, width, _ptr(out), _stream(src_t.device))
     return out
@@ -905,6 +938,9 @@ def aggregate_gather(rows_g: Tensor, inv: Tensor, weights: Tensor, row_ptr: Tens
     out = torch.empty(n_targets, rows_g.shape[1], dtype=rows_g.dtype, device=rows_g.device)
     if n_targets == 0:
         return out
+    _index_vector(row_ptr, n_targets + 1, "row_ptr")
+    _index_vector(inv, None, "inv")
+    _edge_stream(weights, inv.shape[0], 1, "weights")
     _call("gm_factored_aggregate_gather_f32", _ptr(rows_g), _ptr(inv), _ptr(weights), _ptr(row_ptr), n_targets,
           rows_g.shape[0], rows_g.shape[1], _ptr(out), _stream(rows_g.device))
     return out

@@ -69,3 +69,12 @@ def test_aggregate_refuses_32_bit_indices(cuda):
     with pytest.raises(ValueError):
         _native.aggregate_heads(torch.zeros(8, 3, 20, device=cuda), torch.zeros(3, dtype=torch.int32, device=cuda),
                                 torch.zeros(3, 8, device=cuda), torch.tensor([0, 3], device=cuda))
+
+
+def test_transposes_refuse_32_bit_permutations(cuda):
+    """The grouping's permutation is read as int64 entries."""
+    perm = torch.arange(5, dtype=torch.int32, device=cuda)
+    with pytest.raises(ValueError):
+        _native.gather_transpose(torch.zeros(5, 8, device=cuda), perm)
+    with pytest.raises(ValueError):
+        _native.scatter_transpose(torch.zeros(8, 5, device=cuda), perm)
