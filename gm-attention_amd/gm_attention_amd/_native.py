@@ -628,11 +628,23 @@ def factored_backward_seg(g: Tensor, target: Tensor, weights: Tensor, rows: Tens
     return dweights
 
 
+def _trunk_checks(rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor) -> None:
+    _check(rho.dtype == torch.float32 and rho.dim() == 1 and rho.is_contiguous(), "rho must be a contiguous float32 vector")
+    _check(weight.dtype == torch.float32 and weight.dim() == 3 and weight.is_contiguous(),
+           "weight must be a contiguous float32 (H, T, B) tensor")
+    H, T, B = weight.shape
+    _check(bias is None or (bias.dtype == torch.float32 and bias.is_contiguous() and tuple(bias.shape) == (H, T)),
+           "bias must be a contiguous float32 (H, T) tensor")
+    _check(centers.dtype == torch.float32 and centers.is_contiguous() and tuple(centers.shape) == (B,),
+           "centers must be a contiguous float32 (B,) tensor")
+
+
 def radial_trunk_forward(rho: Tensor, weight: Tensor, bias: Tensor | None, centers: Tensor, width: float,
                          dtype: torch.dtype | None = None) -> Tensor:
     """``h (H, E, T)``: every head's SiLU(W b(rho) + c) over the Gaussian basis
     of rho^2, in rho's dtype or ``dtype`` (bfloat16: float32 arithmetic, each
     feature rounded to nearest even as it is stored)."""
+    _trunk_checks(rho, weight, bias, centers)
     H, T, B = weight.shape
     dtype = rho.dtype if dtype is None else dtype
     _check(dtype in (torch.float32, torch.bfloat16), "the trunk features are float32 or bfloat16")
@@ -649,9 +661,10 @@ def radial_trunk_backward(dh: Tensor, rho: Tensor, weight: Tensor, bias: Tensor 
                           width: float) -> tuple[Tensor, Tensor]:
     """(dweight (H, T, B), dbias (H, T)) summed over the edges in a fixed order;
     ``dh`` float32 or bfloat16."""
+    _trunk_checks(rho, weight, bias, centers)
     H, T, B = weight.shape
-    _check(dh.dtype in (torch.float32, torch.bfloat16) and dh.is_contiguous(),
-           "dh must be contiguous float32 or bfloat16")
+    _check(dh.dtype in (torch.float32, torch.bfloat16) and dh.is_contiguous() and tuple(dh.shape) == (H, rho.shape[0], T),
+           "dh must be contiguous float32 or bfloat16 (H, E, T)")
     P = T * B + T
     lib = library()
     blocks = int(lib.gm_radial_trunk_partials(rho.shape[0]))
@@ -1041,6 +1054,37 @@ def pairs() -> PairsExtension:
 RADIAL_TILES_SCALAR, RADIAL_TILES_COMPLEX = 2, 16
 
 
+def _conv_radial_checks(v: Tensor, rf: Tensor, rbias: Tensor, rb: Tensor | None, w1: Tensor, b1: Tensor | None,
+                        centers: list[float], transport: Tensor, angular: Tensor, rho: Tensor, weights: Tensor,
+                        row_ptr: Tensor, source: Tensor, tiles: Tensor) -> None:
+    """The walk's arguments as the kernels read them: the readout's operand tables
+    of the compiled tile count, the per-edge streams of the CSR's edges, the host tile table."""
+    _check(v.dim() == 2 and v.is_contiguous(), "v must be a contiguous (N, D) tensor")
+    row = int(library().gm_conv_radial_partial_row())
+    nt = (row - 16 * 8 - 16) // (256 + 16)  # coefficient tiles: the partial row holds dR, its bias column, W1, b1
+    for t, numel, name in ((rf, nt * 256, "rf"), (rbias, nt * 16, "rbias"), (rb, nt * 256, "rb")):
+        if t is not None:
+            _check(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == numel,
+                   f"{name} must be a contiguous float32 table of {numel} entries")
+    nb = len(centers)
+    _check(w1.dtype == torch.float32 and w1.is_contiguous() and tuple(w1.shape) == (16, nb),
+           f"w1 must be a contiguous float32 (16, {nb}) tensor")
+    _check(b1 is None or (b1.dtype == torch.float32 and b1.is_contiguous() and tuple(b1.shape) == (16,)),
+           "b1 must be a contiguous float32 (16,) tensor")
+    n, E = v.shape[0], source.shape[0]
+    _index_vector(row_ptr, n + 1, "row_ptr")
+    _index_vector(source, E, "source")
+    for t, name in ((rho, "rho"), (weights, "weights")):
+        _check(t.dtype == torch.float32 and t.is_contiguous() and tuple(t.shape) == (E,),
+               f"{name} must be a contiguous float32 ({E},) tensor")
+    for t, name in ((transport, "transport"), (angular, "angular")):
+        _check(t.dtype == torch.float32 and t.is_contiguous() and t.dim() == 3 and t.shape[0] == E
+               and t.shape[2] == 2 and tuple(t.shape) == tuple(transport.shape),
+               f"{name} must be a contiguous float32 (E, orders, 2) tensor shaped like transport")
+    _check(tiles.device.type == "cpu" and tiles.dtype == torch.int32 and tiles.is_contiguous() and tiles.dim() == 2
+           and tiles.shape[0] == 2, "tiles must be a contiguous host int32 (2, nc) table")
+
+
 def conv_radial_forward(v: Tensor, rf: Tensor, rbias: Tensor, w1: Tensor, b1: Tensor | None, centers: list[float], width: float,
                         transport: Tensor, angular: Tensor, rho: Tensor, weights: Tensor, row_ptr: Tensor,
                         source: Tensor, a0: int, ns: int, tiles: Tensor) -> Tensor:
@@ -1050,6 +1094,7 @@ def conv_radial_forward(v: Tensor, rf: Tensor, rbias: Tensor, w1: Tensor, b1: Te
     table of the complex tiles' frequencies and first columns."""
     _require_device(v, rf, rbias, w1, transport, angular, rho, weights, row_ptr, source)
     _check(v.dtype == torch.float32 and v.data_ptr() % 16 == 0, "v must be 16-byte aligned float32")
+    _conv_radial_checks(v, rf, rbias, None, w1, b1, centers, transport, angular, rho, weights, row_ptr, source, tiles)
     out = torch.empty_like(v)
     if v.shape[0] == 0:
         return out
@@ -1071,6 +1116,8 @@ def conv_radial_backward(g: Tensor, v: Tensor, rf: Tensor, rbias: Tensor, rb: Te
     _require_device(g, v, rf, rbias, rb, w1, transport, angular, rho, weights, row_ptr, source)
     _check(g.shape == v.shape and g.dtype == v.dtype and g.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0,
            "g must be shaped and typed as v, both 16-byte aligned")
+    _check(g.is_contiguous(), "g must be contiguous")
+    _conv_radial_checks(v, rf, rbias, rb, w1, b1, centers, transport, angular, rho, weights, row_ptr, source, tiles)
     src_ptr, src_order, target = source_major(source, row_ptr)
     n = v.shape[0]
     dv = torch.empty_like(v)
