@@ -599,6 +599,11 @@ def factored_forward_seg(h: Tensor, runs: MixRuns, n_nodes: int, angular: Tensor
     out = torch.empty(h.shape[0], d_out, dtype=h.dtype, device=h.device)
     if h.shape[0] == 0:
         return out
+    E = h.shape[0]
+    _edge_stream(h, E, 16, "h")
+    _index_vector(order, E, "order")
+    _grouping(group_ptr, group_source, None)
+    _edge_stream(rho, E, 1, "rho")
     hd = host_desc32(desc)
     _call("gm_factored_forward_seg" + _suffix(h.dtype), _ptr(h), ctypes.cast(runs.z, ctypes.c_void_p),
           ctypes.cast(runs.node_stride, ctypes.c_void_p), ctypes.cast(runs.t_stride, ctypes.c_void_p),
@@ -617,6 +622,14 @@ def factored_backward_seg(g: Tensor, target: Tensor, weights: Tensor, rows: Tens
     dweights = torch.empty_like(weights)
     if h.shape[0] == 0:
         return dweights
+    E = h.shape[0]
+    for t, width, name in ((h, 16, "h"), (dh, 16, "dh"), (rho, 1, "rho"), (weights, 1, "weights"),
+                           (rows, g.shape[1], "rows")):
+        _edge_stream(t, E, width, name)
+    _index_vector(target, E, "target")
+    _index_vector(order, E, "order")
+    _grouping(group_ptr, group_source, None)
+    _check(g.dim() == 2 and g.is_contiguous(), "g must be a contiguous (n_targets, d_out) tensor")
     hd = host_desc32(desc)
     _call("gm_factored_backward_seg" + _suffix(h.dtype), _ptr(g), _ptr(target), _ptr(weights), _ptr(rows), _ptr(h),
           ctypes.cast(runs.z, ctypes.c_void_p), ctypes.cast(runs.dz, ctypes.c_void_p),
@@ -1321,7 +1334,7 @@ def param_dtype(dtype: torch.dtype) -> torch.dtype:
 def _pw_check(x: Tensor, layout: PointwiseLayout) -> str:
     _require_device(x)
     _check(x.dtype in _PW_SUFFIX, f"the pointwise operators take float32, float64 or bfloat16 rows, got {x.dtype}")
-    _check(x.dim() == 2 and x.shape[1] == layout.D, f"rows must be (n_nodes, {layout.D})")
+    _check(x.dim() == 2 and x.shape[1] == layout.D and x.is_contiguous(), f"rows must be contiguous (n_nodes, {layout.D})")
     return _PW_SUFFIX[x.dtype]
 
 
@@ -1331,8 +1344,9 @@ def layer_norm_forward(x: Tensor, gamma: Tensor, beta: Tensor | None, layout: Po
     sfx = _pw_check(x, layout)
     pd = param_dtype(x.dtype)
     _require_device(x, gamma, *(() if beta is None else (beta,)))
-    _check(gamma.dtype == pd and gamma.shape == (layout.D,), f"gamma must be ({layout.D},) {pd}")
-    _check(beta is None or (beta.dtype == pd and beta.shape == (layout.a0,)), f"beta must be ({layout.a0},) {pd}")
+    _check(gamma.dtype == pd and gamma.shape == (layout.D,) and gamma.is_contiguous(), f"gamma must be ({layout.D},) {pd}")
+    _check(beta is None or (beta.dtype == pd and beta.shape == (layout.a0,) and beta.is_contiguous()),
+           f"beta must be ({layout.a0},) {pd}")
     n = x.shape[0]
     y = torch.empty_like(x)
     mean = torch.empty(n, dtype=pd, device=x.device)
@@ -1347,9 +1361,12 @@ def layer_norm_backward(gy: Tensor, x: Tensor, gamma: Tensor, mean: Tensor, inv_
     """``(dx, dparams)`` with ``dparams = (dgamma (D), dbeta (a0))`` summed over the nodes in a fixed order."""
     sfx = _pw_check(x, layout)
     _require_device(gy, x, gamma, mean, inv_d)
-    _check(gy.dtype == x.dtype and gy.shape == x.shape, "gy must match x")
+    _check(gy.dtype == x.dtype and gy.shape == x.shape and gy.is_contiguous(), "gy must match x (contiguous)")
     pd = param_dtype(x.dtype)
     n = x.shape[0]
+    _check(gamma.dtype == pd and gamma.shape == (layout.D,) and gamma.is_contiguous(), f"gamma must be ({layout.D},) {pd}")
+    for t, name in ((mean, "mean"), (inv_d, "inv_d")):
+        _check(t.dtype == pd and t.shape == (n,) and t.is_contiguous(), f"{name} must be ({n},) {pd}")
     rows = int(library().gm_layer_norm_partial_rows(n))
     partial = torch.empty(rows, layout.D + layout.a0, dtype=pd, device=x.device)
     dparams = torch.empty(layout.D + layout.a0, dtype=pd, device=x.device)
@@ -1363,7 +1380,8 @@ def gate_forward(h: Tensor, pre: Tensor, layout: PointwiseLayout, double_sigmoid
     """SiLU on the scalar entries, every copy scaled by its gate ``act(pre)``."""
     sfx = _pw_check(h, layout)
     _require_device(h, pre)
-    _check(pre.dtype == h.dtype and tuple(pre.shape) == (h.shape[0], layout.G), f"pre must be (n_nodes, {layout.G})")
+    _check(pre.dtype == h.dtype and tuple(pre.shape) == (h.shape[0], layout.G) and pre.is_contiguous(),
+           f"pre must be contiguous (n_nodes, {layout.G})")
     y = torch.empty_like(h)
     _call(f"gm_gate_forward_{sfx}", _ptr(h), _ptr(pre), h.shape[0], *layout.args(), int(double_sigmoid), _ptr(y),
           _stream(h.device))
@@ -1375,7 +1393,9 @@ def gate_backward(gy: Tensor, h: Tensor, pre: Tensor, layout: PointwiseLayout,
     """``(dh, dpre)``: the gate's direct gradient and the pre-activations' gradient."""
     sfx = _pw_check(h, layout)
     _require_device(gy, h, pre)
-    _check(gy.dtype == h.dtype and gy.shape == h.shape, "gy must match h")
+    _check(gy.dtype == h.dtype and gy.shape == h.shape and gy.is_contiguous(), "gy must match h (contiguous)")
+    _check(pre.dtype == h.dtype and tuple(pre.shape) == (h.shape[0], layout.G) and pre.is_contiguous(),
+           f"pre must be contiguous (n_nodes, {layout.G})")
     dh = torch.empty_like(h)
     dpre = torch.empty_like(pre)
     _call(f"gm_gate_backward_{sfx}", _ptr(gy), _ptr(h), _ptr(pre), h.shape[0], *layout.args(), int(double_sigmoid),
