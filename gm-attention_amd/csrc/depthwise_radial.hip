@@ -187,25 +187,29 @@ __device__ __forceinline__ floatx4 coefficients(const float* rf_s, const float* 
 // workgroup into the A operand pieces (hm, hl), held in LDS; w h~'s features
 // 4q..4q+3 of the lane's edge split once per edge tile into the B pieces,
 // shared by every tile.  Three bf16 instructions a tile instead of four fp32
-// ones, in fp32 accuracy.
+// ones, in fp32 accuracy.  A tile's pieces are stored as its 64 lanes' hm,
+// then their hl, so consecutive lanes read consecutive 16-byte pieces (no
+// bank conflicts).
 struct SplitTile {
   u32x4 hm, hl;
 };
 
 __device__ __forceinline__ void load_split(const RadialConvArgs& a, SplitTile* rs_s) {
+  u32x4* pieces = reinterpret_cast<u32x4*>(rs_s);
   for (int i = threadIdx.x; i < kRNT * kWave; i += kRThreads) {
     const int m = i / kWave, l = i % kWave;
     const SplitA sa = split_a(a.rf[(m * 4 + 0) * 64 + l], a.rf[(m * 4 + 1) * 64 + l], a.rf[(m * 4 + 2) * 64 + l],
                               a.rf[(m * 4 + 3) * 64 + l]);
-    rs_s[i] = SplitTile{sa.hm, sa.hl};
+    pieces[2 * kWave * m + l] = sa.hm;
+    pieces[2 * kWave * m + kWave + l] = sa.hl;
   }
 }
 
 __device__ __forceinline__ floatx4 coefficients_split(const SplitTile* rs_s, const float* bias_s, int m, int lane,
                                                       int q, float w, const SplitB& hb) {
   const float4 b = *reinterpret_cast<const float4*>(bias_s + m * 16 + 4 * q);
-  const SplitTile t = rs_s[m * kWave + lane];
-  return mfma_split(SplitA{t.hm, t.hl}, hb, floatx4{w * b.x, w * b.y, w * b.z, w * b.w});
+  const u32x4* pieces = reinterpret_cast<const u32x4*>(rs_s) + 2 * kWave * m;
+  return mfma_split(SplitA{pieces[lane], pieces[kWave + lane]}, hb, floatx4{w * b.x, w * b.y, w * b.z, w * b.w});
 }
 
 // The tile's coefficients for the lane's edge: fp32 MFMA from rf_s, or the split products from rs_s.
