@@ -813,8 +813,7 @@ def run_stage(args) -> None:
         "roofline": timer.line_roofline(ops, dominant, "c5"),
         "ops": {name: {k: (round(x, 4) if isinstance(x, float) else x) for k, x in v.items()}
                 for name, v in ops.items()},
-        "ops_coverage": ops_coverage(ops, ms_per_step) if not graphed else {
-            "note": "the ops are timed on eager steps; the step time is of graph replays, without launch gaps"},
+        "ops_coverage": ops_coverage(ops, ms_per_step),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_stage(model),
     }
     print(json.dumps(line))
@@ -973,8 +972,7 @@ def run_encoder(args) -> None:
         "roofline": roof,
         "ops": {name: {k: (round(x, 4) if isinstance(x, float) else x) for k, x in v.items()}
                 for name, v in ops.items()},
-        "ops_coverage": ops_coverage(ops, ms_per_step) if not graphed else {
-            "note": "the ops are timed on eager steps; the step time is of graph replays, without launch gaps"},
+        "ops_coverage": ops_coverage(ops, ms_per_step),
         "cpu_baseline": baseline,
     }
     print(json.dumps(line))
