@@ -650,7 +650,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   constexpr int RT = SplitRT<W>, ROWS = 64 * RT;
   // chunks of KC columns (32 for the widest vectors: fewer staged registers); LDM: a 16-lane 8-byte read
   // covers 32 banks once
-  constexpr int KC = W == 128 ? 32 : 64, LDD = KC + 4, LDM = KC + 4, JW = W / 16, KS = KC / 16;
+  constexpr int KC = W == 128 ? 32 : 64, LDM = KC + 4, JW = W / 16, KS = KC / 16;
+  // 64-column chunks of dmix unpadded, 16-byte unit u of row r at u ^ (r mod 16): a 16-byte read's set of
+  // 16 lanes (c < 8 of one lane row, c >= 8 of another) then meets 16 distinct bank quads
+  constexpr bool SWZ = KC == 64;
+  constexpr int LDD = SWZ ? KC : KC + 4;
   constexpr int TOTAL_EVERY = 256 / KC;  // chunks a running sum spans before it joins the total
   constexpr int DQ = ROWS * KC / 4 / kThreads;
   constexpr int MQ = W * KC / 4 / kThreads;
@@ -689,7 +693,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int p = 0; p < DQ; ++p) {
       const int idx = threadIdx.x + p * kThreads;
-      *reinterpret_cast<float4*>(&dt[(idx / CQ) * LDD + 4 * (idx % CQ)]) = pd[p];
+      const int u = SWZ ? (idx % CQ) ^ ((idx / CQ) & 15) : idx % CQ;
+      *reinterpret_cast<float4*>(&dt[(idx / CQ) * LDD + 4 * u]) = pd[p];
     }
 #pragma unroll
     for (int p = 0; p < MQ; ++p) {
@@ -703,7 +708,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       SplitA a[RT];
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        const float4 x = *reinterpret_cast<const float4*>(&dt[(16 * RT * wv + 16 * rt + c) * LDD + 16 * kc + 4 * q]);
+        const int u = SWZ ? (4 * kc + q) ^ c : 4 * kc + q;
+        const float4 x = *reinterpret_cast<const float4*>(&dt[(16 * RT * wv + 16 * rt + c) * LDD + 4 * u]);
         a[rt] = split_a(x.x, x.y, x.z, x.w);
       }
 #pragma unroll
