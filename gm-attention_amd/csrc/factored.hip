@@ -469,10 +469,14 @@ __global__ __launch_bounds__(256) void aggregate_heads_kernel(AggHeadsArgs a) {
 // dst_t[h, g] = src[perm[g], h] (a row gather and a transpose), and its
 // inverse dst[perm[g], h] = src_t[h, g]: one thread per row g, whole rows
 // moved as 16-byte pieces where the width allows (W4 = width / 4 pieces).
+// Each XCD runs a contiguous range of the blocks: the rows of neighbouring
+// sources share the cache lines they gather from (or scatter into), and those
+// lines then meet in one L2 instead of being fetched (or written back in
+// pieces) by several.
 template <int W4>
 __global__ __launch_bounds__(256) void gather_transpose_kernel(const float* src, const int64_t* perm, int64_t n,
                                                                int width, float* dst_t) {
-  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t g = xcd_block(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
   if (g >= n) return;
   const float* row = src + perm[g] * width;
   if constexpr (W4 > 0) {
@@ -490,7 +494,7 @@ __global__ __launch_bounds__(256) void gather_transpose_kernel(const float* src,
 template <int W4>
 __global__ __launch_bounds__(256) void scatter_transpose_kernel(const float* src_t, const int64_t* perm, int64_t n,
                                                                 int width, float* dst) {
-  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t g = xcd_block(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
   if (g >= n) return;
   float* row = dst + perm[g] * width;
   if constexpr (W4 > 0) {
