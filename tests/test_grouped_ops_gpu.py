@@ -42,10 +42,13 @@ def test_aggregate_heads_matches_a_csr_sum(H, d_out, split, cuda):
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5 * float(want.abs().max()))
 
 
+@pytest.mark.parametrize("n", [1000, 9483, 100003])
 @pytest.mark.parametrize("width", [1, 4, 8, 13])
-def test_gather_and_scatter_transposes_are_exact(width, cuda):
-    g = torch.Generator().manual_seed(width)
-    n = 1000
+def test_gather_and_scatter_transposes_are_exact(width, n, cuda):
+    """Rows 0 .. n-1 in 256-row blocks that each XCD takes as a contiguous range:
+    fewer blocks than XCDs, a block count that does not divide among them and a
+    ragged last block all move every row exactly once."""
+    g = torch.Generator().manual_seed(width + n)
     src = torch.randn(n, width, generator=g)
     perm = torch.randperm(n, generator=g)
     t = _native.gather_transpose(src.to(cuda), perm.to(cuda)).cpu()
