@@ -13,6 +13,7 @@ as the timed CPU path); the product in ``gm-attention_amd/`` never imports it.
   header-only CPU arithmetic (``nn/fused/attention.h``, ``factored.h``)
   compiled by ``oracle/Makefile`` from ``oracle/ref_driver.cpp``.
 
-How each function is pinned (golden vectors, the compiled reference, closed
-forms, finite differences, gauge equivariance) is listed in DESIGN.md.
+Each function is pinned by the CPU tests ``tests/test_oracle_*.py``: the
+reference's own known answers, the compiled reference, closed forms, finite
+differences or gauge equivariance.
 """
