@@ -36,13 +36,14 @@ FLAGS = [
 ]
 
 
-#: Per-source extra flags.  The factored and trunk kernels keep their MFMA
-#: accumulators in VGPRs: the VALU reads every accumulator (the factored slots,
-#: the trunk's SiLU and partial rows), so AGPRs would only add copies and
-#: registers (the trunk backward: 184 -> 151 VGPRs, three waves a SIMD).  The
-#: depthwise walk is left to the default, which measured faster there.
+#: Per-source extra flags.  The factored, trunk and depthwise-walk kernels keep
+#: their MFMA accumulators in VGPRs: the VALU reads every accumulator (the
+#: factored slots, the trunk's SiLU and partial rows, the walk's dC and dh~), so
+#: AGPRs would only add copies and registers (the trunk backward: 184 -> 151
+#: VGPRs, three waves a SIMD; the paired depthwise backward: 88 AGPR copies an
+#: edge tile gone, 28.0 -> 27.0 ms at 256x512, B = 4).
 _VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-EXTRA = {"factored.hip": _VGPR_MFMA, "trunk.hip": _VGPR_MFMA}
+EXTRA = {"factored.hip": _VGPR_MFMA, "trunk.hip": _VGPR_MFMA, "depthwise_radial.hip": _VGPR_MFMA}
 
 
 def _compile(source: Path, verbose: bool) -> Path:
