@@ -418,6 +418,12 @@ __device__ __forceinline__ void tile_dc(const RadialConvArgs& a, const float* rf
 // 0..kRNS-1, then the complex tiles), for one wave: sources j_lo + lw, + nwx,
 // ... of its XCD's eighth, its dR, bias column and dv accumulated for those
 // tiles only, its partial row at `part_row`.
+// Rows of the wave's 16 x 16 hand-over tile in LDS, padded to 20 floats: a
+// 16-byte write's set of 8 lanes (c = 0..7 or 8..15 of one lane row) then meets
+// 8 distinct bank quads (at 16 floats lanes c and c + 4 share one), and the
+// 4-byte reads of a half-wave (rows 4 s + q, q = 0, 1) stay in distinct banks.
+constexpr int kTRow = 20;
+
 template <int NB, int T0, int T1, bool SPLIT>
 __device__ __forceinline__ void backward_walk(const RadialConvArgs& a, float* partial, const float* rf_s,
                                               const SplitTile* rs_s, const float* rb_s, const float* bias_s,
@@ -461,11 +467,11 @@ __device__ __forceinline__ void backward_walk(const RadialConvArgs& a, float* pa
       if constexpr (SPLIT) hb = split_b(bv[0], bv[1], bv[2], bv[3]);
       // h~^T for dR's B operand: ht[s] = h_c(edge 4s + q)
       wave_sync();
-      *reinterpret_cast<float4*>(T + c * 16 + 4 * q) = make_float4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<float4*>(T + c * kTRow + 4 * q) = make_float4(h[0], h[1], h[2], h[3]);
       wave_sync();
       float ht[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ht[s] = T[(4 * s + q) * 16 + c];
+      for (int s = 0; s < 4; ++s) ht[s] = T[(4 * s + q) * kTRow + c];
       const float* gt = a.g + ev.node * a.D;
       floatx4 dh[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
       static_assert(kRChunk == 1, "the tiles' pieces are requested one tile ahead");
@@ -492,7 +498,7 @@ __device__ __forceinline__ void backward_walk(const RadialConvArgs& a, float* pa
         for (int p = 0; p < kRChunk; ++p) {
           const int i = i0 + p;
           if (i < G && tile_live(a, T0 + i))
-            *reinterpret_cast<float4*>(T + p * 256 + c * 16 + 4 * q) =
+            *reinterpret_cast<float4*>(T + p * 16 * kTRow + c * kTRow + 4 * q) =
                 make_float4(dcs[p][0], dcs[p][1], dcs[p][2], dcs[p][3]);
         }
         wave_sync();
@@ -502,7 +508,7 @@ __device__ __forceinline__ void backward_walk(const RadialConvArgs& a, float* pa
           if (i < G && tile_live(a, T0 + i)) {
             float at[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) at[s] = T[p * 256 + (4 * s + q) * 16 + c];
+            for (int s = 0; s < 4; ++s) at[s] = T[p * 16 * kTRow + (4 * s + q) * kTRow + c];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
               db[i] += at[s];
@@ -587,7 +593,7 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_kernel(RadialC
   __shared__ float rb_s[kRNT * 4 * 64];
   __shared__ __attribute__((aligned(16))) float bias_s[kRNT * 16];
   __shared__ float w1s[16 * kRMaxBasis + 16];
-  __shared__ __attribute__((aligned(16))) float tr_s[kRWaves][kRChunk * 256];
+  __shared__ __attribute__((aligned(16))) float tr_s[kRWaves][kRChunk * 16 * kTRow];
   if constexpr (SPLIT) {
     load_split(a, rs_s);
     load_tables(a, nullptr, rb_s, bias_s, w1s, NB);
@@ -612,7 +618,7 @@ __global__ __launch_bounds__(kRThreads) void conv_radial_backward_paired(RadialC
   __shared__ float rb_s[kRNT * 4 * 64];
   __shared__ __attribute__((aligned(16))) float bias_s[kRNT * 16];
   __shared__ float w1s[16 * kRMaxBasis + 16];
-  __shared__ __attribute__((aligned(16))) float tr_s[kRWaves][kRChunk * 256];
+  __shared__ __attribute__((aligned(16))) float tr_s[kRWaves][kRChunk * 16 * kTRow];
   if constexpr (SPLIT) {
     load_split(a, rs_s);
     load_tables(a, nullptr, rb_s, bias_s, w1s, NB);
