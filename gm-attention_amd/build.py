@@ -41,9 +41,12 @@ FLAGS = [
 #: factored slots, the trunk's SiLU and partial rows, the walk's dC and dh~), so
 #: AGPRs would only add copies and registers (the trunk backward: 184 -> 151
 #: VGPRs, three waves a SIMD; the paired depthwise backward: 88 AGPR copies an
-#: edge tile gone, 28.0 -> 27.0 ms at 256x512, B = 4).
+#: edge tile gone, 28.0 -> 27.0 ms at 256x512, B = 4; the fused feed-forward's
+#: backward: 222 + 40 AGPRs -> 254 registers, two waves a SIMD instead of one,
+#: 1.41 -> 1.08 ms at the C4 block).
 _VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-EXTRA = {"factored.hip": _VGPR_MFMA, "trunk.hip": _VGPR_MFMA, "depthwise_radial.hip": _VGPR_MFMA}
+EXTRA = {"factored.hip": _VGPR_MFMA, "trunk.hip": _VGPR_MFMA, "depthwise_radial.hip": _VGPR_MFMA,
+         "ffn.hip": _VGPR_MFMA}
 
 
 def _compile(source: Path, verbose: bool) -> Path:
